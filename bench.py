@@ -1,0 +1,301 @@
+#!/usr/bin/env python3
+"""Headline benchmark: single-token Qwen3-MoE layer decode on one MI355X.
+
+Workload: hidden 2048, 128 experts, top-8 softmax
+routing renormalised; F32 router 2048x128 N(0, 0.02); experts gate/up
+2048->768 Q4_K and down 768->2048 Q6_K; SwiGLU; weighted combine; x ~ N(0, 1).
+
+A step is one MoE-layer pass for one token: router + top-k, gate/up SwiGLU,
+down + combine (three kernels).  Weights are resident in HBM; every step
+reads a different one of --layers distinct layers (24 x 392 MB) with a
+different token, so the routed 25.5 MB never comes from the 256 MB MALL.
+The timed steps run as HIP-graph replays on one stream (the launch cost of
+three ~microsecond kernels would otherwise dominate); eager timing is
+reported beside it.
+
+value = algorithmic bytes of the timed steps / wall time, where one step's
+algorithmic bytes are the router (1,048,576 B) plus the 8 selected experts'
+gate, up and down slices (8 x 3,059,712 B): 25,526,272 B.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+METRIC = "MoE-layer decode achieved HBM GB/s (% of peak); model decode tokens/sec"
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=1000)
+    ap.add_argument("--warmup", type=int, default=50)
+    ap.add_argument("--layers", type=int, default=24)
+    ap.add_argument("--tokens", type=int, default=64)
+    ap.add_argument("--graph-chunk", type=int, default=250)
+    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--eager", action="store_true", help="time eager launches instead of graphs")
+    return ap.parse_args()
+
+
+def device_quant(torch, gtype, rows, inn, gen, dev):
+    """GGUF-encoded random weights made on the GPU: uniform quant bytes,
+    fp16 scales |N(0, 0.02)| (the same recipe as pokitlms_amd.synth)."""
+    from pokitlms_amd import synth as S
+    bb = S.BLOCK_BYTES[gtype]
+    nb = rows * inn // S.BLOCK_ELEMENTS[gtype]
+    blocks = torch.randint(0, 256, (nb, bb), dtype=torch.uint8, device=dev, generator=gen)
+    for off in S.SCALE_OFFSETS[gtype]:
+        h = (torch.randn(nb, device=dev, generator=gen) * 0.02).abs().to(torch.float16)
+        blocks[:, off:off + 2] = h.view(torch.uint8).view(nb, 2)
+    return blocks.view(-1)
+
+
+def build_layers(torch, hip, n_layers, dev, hidden=2048, experts=128, ffn=768):
+    from pokitlms_amd import synth as S
+    from pokitlms_amd.backend import MoeLayerHandles
+    layers = []
+    for li in range(n_layers):
+        gen = torch.Generator(device=dev)
+        gen.manual_seed(1000 + li)
+        router = (torch.randn(experts * hidden, device=dev, generator=gen) * 0.02).contiguous()
+        r = hip.upload_device(S.F32, hidden, experts, router.data_ptr(), router.numel() * 4)
+        del router
+        parts = []
+        for gtype, inn, out in ((S.Q4_K, hidden, ffn), (S.Q4_K, hidden, ffn), (S.Q6_K, ffn, hidden)):
+            buf = device_quant(torch, gtype, experts * out, inn, gen, dev)
+            parts.append(hip.upload_device(gtype, inn, out, buf.data_ptr(), buf.numel(), experts))
+            del buf
+        layers.append(MoeLayerHandles(r, *parts, top_k=8, normalize=True))
+        torch.cuda.synchronize()
+    return layers
+
+
+def cpu_baseline(seconds: float):
+    """The reference CPU MoE block (oracle/_ref, compiled from the reference's
+    own sources) on one layer of the same shape; falls back to the C port."""
+    import numpy as np
+
+    import oracle
+    from pokitlms_amd import synth as S
+    kind = "reference" if oracle.available("reference") else "port"
+    cpu = oracle.Oracle(kind)
+    layer = S.moe_layer(seed=3)
+    blk = cpu.moe(layer)
+    g = S.rng(33)
+    xs = S.normal_f32(g, 64 * 2048).reshape(64, 2048)
+    blk.forward(xs[0])  # warm-up
+    n, t0 = 0, time.perf_counter()
+    times = []
+    while True:
+        t1 = time.perf_counter()
+        blk.forward(xs[n % 64])
+        times.append(time.perf_counter() - t1)
+        n += 1
+        if time.perf_counter() - t0 >= seconds and n >= 5:
+            break
+    med = float(np.median(times))
+    cores = cpu.lib.pkref_row_workers() if kind == "reference" else 1
+    return {
+        "value": round(layer.routed_bytes() / med / 1e9, 3),
+        "unit": "GB/s",
+        "cores": int(cores),
+        "kind": kind,
+        "ms_per_token": round(med * 1e3, 3),
+        "sample": f"{n} single-token MoE-layer passes (config-3 shape, seed 3), median "
+                  f"wall time; reference row pool of {cores} workers, router single-threaded; "
+                  f"host nproc {os.cpu_count()}",
+    }
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build runs on one GPU only; --gpus must be 1",
+                          "n_gpus": args.gpus}))
+        sys.exit(2)
+
+    import numpy as np
+    import torch
+
+    from pokitlms_amd.backend import HipBackend
+
+    dev = torch.device("cuda:0")
+    hip = HipBackend(0)
+    log(f"building {args.layers} resident layers ...")
+    layers = build_layers(torch, hip, args.layers, dev)
+    step_bytes = layers[0].routed_bytes()
+    assert step_bytes == 25_526_272, step_bytes
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(77)
+    X = torch.randn(args.tokens, 2048, device=dev, generator=gen)
+    Y = torch.empty(args.tokens, 2048, device=dev)
+    IDS = torch.empty(args.tokens, 8, dtype=torch.int32, device=dev)
+    P = torch.empty(args.tokens, 8, dtype=torch.float32, device=dev)
+
+    stream = torch.cuda.Stream()
+    torch.cuda.synchronize()
+
+    def step(i, s):
+        t = i % args.tokens
+        hip.moe_decode_async(layers[i % args.layers], X[t].data_ptr(), Y[t].data_ptr(),
+                             IDS[t].data_ptr(), P[t].data_ptr(), s)
+
+    with torch.cuda.stream(stream):
+        s = stream.cuda_stream
+        for i in range(args.warmup):
+            step(i, s)
+        hip.sync(s)
+        # eager reference outputs for the graph check
+        for i in range(args.tokens):
+            step(i, s)
+        hip.sync(s)
+        y_eager, ids_eager = Y.clone(), IDS.clone()
+
+        # eager timing (host launch bound; reported beside the graph figure)
+        ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        n_eager = min(args.steps, 500)
+        ev0.record(stream)
+        for i in range(n_eager):
+            step(i, s)
+        ev1.record(stream)
+        ev1.synchronize()
+        eager_ms = ev0.elapsed_time(ev1) / n_eager
+
+    chunk = min(args.graph_chunk, args.steps)
+    if args.steps % chunk:
+        chunk = args.steps
+    graphs = []
+    if not args.eager:
+        for c in range(args.steps // chunk):
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g, stream=stream):
+                cs = torch.cuda.current_stream().cuda_stream
+                for i in range(c * chunk, (c + 1) * chunk):
+                    step(i, cs)
+            graphs.append(g)
+        with torch.cuda.stream(stream):
+            for g in graphs:  # untimed first replay: graph upload
+                g.replay()
+            hip.sync(stream.cuda_stream)
+        # every replay must reproduce the eager result (first --tokens steps)
+        ok_graph = bool(torch.equal(Y, y_eager) and torch.equal(IDS, ids_eager))
+
+    with torch.cuda.stream(stream):
+        torch.cuda.synchronize()
+        ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        t0 = time.perf_counter()
+        ev0.record(stream)
+        if args.eager:
+            for i in range(args.steps):
+                step(i, stream.cuda_stream)
+        else:
+            for g in graphs:
+                g.replay()
+        ev1.record(stream)
+        ev1.synchronize()
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t0
+        gpu_ms = ev0.elapsed_time(ev1)
+        hip.sync(stream.cuda_stream)
+    if not args.eager:
+        ok_graph = ok_graph and bool(torch.equal(Y, y_eager) and torch.equal(IDS, ids_eager))
+    ms_per_step = gpu_ms / args.steps
+    value = step_bytes * args.steps / (gpu_ms / 1e3) / 1e9
+
+    # per-kernel device time with HIP events on the launch stream
+    hip.reset_stats()
+    hip.set_kernel_timing(True)
+    n_timed = 200
+    with torch.cuda.stream(stream):
+        for i in range(n_timed):
+            step(i, stream.cuda_stream)
+    hip.set_kernel_timing(False)
+    st = hip.stats()
+    kbytes = {
+        # algorithmic bytes per launch: weights + activations in/out
+        "k_router": 1_048_576 + 2048 * 4 + 8 * 8,
+        "k_gate_up": 8 * 2 * 884_736 + 2048 * 4 + 8 * 768 * 4,
+        "k_down": 8 * 1_290_240 + 8 * 768 * 4 + 2048 * 4,
+    }
+    kns = {"k_router": st["router_ns"] / n_timed, "k_gate_up": st["gate_up_ns"] / n_timed,
+           "k_down": st["down_ns"] / n_timed}
+    kernels = {k: {"avg_us": round(kns[k] / 1e3, 3), "bytes": kbytes[k],
+                   "gbs": round(kbytes[k] / kns[k], 1) if kns[k] else None} for k in kns}
+    dominant = max(kns, key=lambda k: kns[k])
+    achieved = kbytes[dominant] / kns[dominant]  # B/ns == GB/s
+    roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
+                "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                "kernel": dominant}
+
+    # a spot parity check of the timed path against the CPU oracle
+    parity = None
+    try:
+        import oracle
+        from pokitlms_amd import synth as S
+        layer = S.moe_layer(seed=3)
+        h = hip.upload_moe_layer(layer)
+        x = S.normal_f32(S.rng(33), 2048)
+        y, ids, _ = hip.moe_decode(h, x)
+        cy, cids, _ = oracle.Oracle("port").moe(layer).forward(x)
+        parity = {"ids_equal": bool(np.array_equal(ids, cids)),
+                  "normwise_rel": float(np.max(np.abs(y - cy)) / np.max(np.abs(cy)))}
+        h.release()
+    except Exception as e:  # reported, never fatal for the timing
+        parity = {"error": str(e)}
+
+    cpu = None if args.no_cpu else cpu_baseline(args.cpu_seconds)
+
+    out = {
+        "metric": METRIC,
+        "value": round(value, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (random-init weights generated on the GPU, x ~ N(0,1))",
+        "config": {
+            "workload": "single-token Qwen3-MoE layer (BASELINE configs[2]): hidden 2048, "
+                        "128 experts, top-8 renormalised, F32 router, gate/up Q4_K 768x2048, "
+                        "down Q6_K 2048x768",
+            "layers_rotated": args.layers, "tokens_rotated": args.tokens,
+            "bytes_per_step": step_bytes,
+            "timing": "eager" if args.eager else f"HIP graph replay, {chunk} steps per graph",
+        },
+        "pct_of_peak": round(100.0 * value / HBM_PEAK_GBS, 2),
+        "eager_ms_per_step": round(eager_ms, 5),
+        "wall_s": round(wall, 4),
+        "roofline": roofline,
+        "kernels": kernels,
+        "router_fallbacks_per_1k": round(1000.0 * st["router_fallbacks"] / n_timed, 2),
+        "graph_matches_eager": None if args.eager else ok_graph,
+        "parity": parity,
+        "cpu_baseline": cpu,
+    }
+    if cpu:
+        out["speedup_vs_cpu"] = round(value / cpu["value"], 1)
+    print(json.dumps(out), flush=True)
+    for l in layers:
+        l.release()
+    hip.close()
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,177 @@
+/*
+ * pokit_hip.h -- C ABI of the PokitLMs MI355X (gfx950) HIP backend for the
+ * routed-MoE K-quant path.
+ *
+ * Conventions follow the reference C API (include/pokitlms/pokitlms.h of
+ * RemydreScarlet/PokitLMs v0.4.0): opaque handles, a status enum whose values
+ * 0-4 match pokitlms_status (pokitlms.h:18-24), error text truncated and
+ * NUL-terminated into a caller buffer (src/c_api.cpp:22-27), no exceptions
+ * across the ABI.  Host buffers are caller-owned; device memory is owned by
+ * the context.  Calls on one context must be serialized (the reference
+ * backends serialize with a mutex, src/vulkan_linear.cpp:635; C handles
+ * require serialized calls, pokitlms.h:81).
+ *
+ * GGUF type ids: F32 0, F16 1, Q4_0 2, Q8_0 8, Q4_K 12, Q5_K 13, Q6_K 14,
+ * BF16 30 (src/gguf_reader.cpp:21-57).  Matrices are GGUF [in, out] tensors:
+ * `out` rows of `in` elements, each row a run of encoded blocks.  Expert
+ * tensors are [in, out, n_experts] with the expert index slowest, so expert e
+ * is the contiguous slice e * (out * row_bytes) (src/expert_store.cpp:17-36).
+ */
+#ifndef POKIT_HIP_H
+#define POKIT_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define PK_HIP_VERSION_MAJOR 0
+#define PK_HIP_VERSION_MINOR 1
+#define PK_HIP_VERSION_PATCH 0
+
+typedef enum pk_hip_status {
+    PK_HIP_STATUS_OK = 0,
+    PK_HIP_STATUS_INVALID_ARGUMENT = 1,
+    PK_HIP_STATUS_RUNTIME_ERROR = 2,
+    PK_HIP_STATUS_BUFFER_TOO_SMALL = 3,
+    PK_HIP_STATUS_INTERNAL_ERROR = 4,
+    /* The backend does not cover this type/shape: the caller runs its CPU
+     * kernel, exactly as TensorLinearBackend::try_linear returning false
+     * (include/pokitlms/model/tensor_linear.hpp:14-15). */
+    PK_HIP_STATUS_UNSUPPORTED = 5
+} pk_hip_status;
+
+typedef struct pk_hip_ctx pk_hip_ctx;
+typedef struct pk_hip_weight pk_hip_weight;
+
+/* Options of pk_hip_create; zero-initialise, then set struct_size. */
+typedef struct pk_hip_options {
+    uint32_t struct_size;  /* sizeof(pk_hip_options) */
+    /* Non-zero: time every launch with HIP events and accumulate per-kernel
+     * device time into pk_hip_stats (synchronises after each call). */
+    uint32_t time_kernels;
+} pk_hip_options;
+
+/* Counters in the spirit of VulkanLinearStats (include/pokitlms/gpu/
+ * vulkan_linear.hpp:41-67) and ExpertCacheStats (qwen3_moe_runner.hpp:44-52). */
+typedef struct pk_hip_stats {
+    uint64_t matvec_calls;
+    uint64_t moe_decode_calls;
+    uint64_t dispatches;                /* kernel launches */
+    uint64_t q4_0_dispatches, q8_0_dispatches, q4_k_dispatches, q5_k_dispatches,
+        q6_k_dispatches, float_dispatches;
+    uint64_t weight_bytes;              /* algorithmic weight bytes streamed */
+    uint64_t resident_bytes;            /* device bytes held by weight handles */
+    uint64_t uploaded_bytes;            /* host->device weight bytes */
+    uint64_t router_fallbacks;          /* tokens whose routing needed exact serial logits */
+    uint64_t router_candidates;         /* rows recomputed serially, summed */
+    uint64_t expert_hits;               /* routed expert accesses (all resident) */
+    uint64_t expert_misses;             /* always 0: experts never leave HBM */
+    /* Device time in ns; filled when pk_hip_options.time_kernels != 0. */
+    uint64_t matvec_ns, router_ns, gate_up_ns, down_ns;
+    uint64_t router_launches, gate_up_launches, down_launches, matvec_launches;
+} pk_hip_stats;
+
+const char* pk_hip_version(void);
+
+/* Non-zero when `ggml_type` has a matvec kernel: F32/F16/BF16/Q4_0/Q8_0/
+ * Q4_K/Q5_K/Q6_K, i.e. the Vulkan backend's type list
+ * (src/vulkan_linear.cpp:78-83) without Q4_1. */
+int pk_hip_type_supported(uint32_t ggml_type);
+
+/* Backend construction / destruction: VulkanLinearBackend ctor and dtor
+ * (src/vulkan_linear.cpp:88-95, 738-758).  device < 0 selects device 0. */
+pk_hip_status pk_hip_create(int device, const pk_hip_options* options, pk_hip_ctx** out_ctx,
+                            char* error_buffer, size_t error_capacity);
+void pk_hip_destroy(pk_hip_ctx* ctx);
+
+/* Uploads one GGUF tensor [in, out(, n_experts)] to HBM, where it stays
+ * resident: the whole-model device cache of the Vulkan backend
+ * (src/vulkan_linear.cpp:516-563) and, for expert tensors, the ExpertStore
+ * with every expert resident (src/expert_store.cpp:17-36, 81-141).
+ * n_experts == 0 means a plain matrix.  nbytes must equal the encoded size. */
+pk_hip_status pk_hip_upload(pk_hip_ctx* ctx, uint32_t ggml_type, uint64_t in, uint64_t out,
+                            uint32_t n_experts, const void* host_bytes, uint64_t nbytes,
+                            pk_hip_weight** out_weight, char* error_buffer,
+                            size_t error_capacity);
+
+/* As pk_hip_upload, from device memory the caller owns (device-to-device copy). */
+pk_hip_status pk_hip_upload_device(pk_hip_ctx* ctx, uint32_t ggml_type, uint64_t in,
+                                   uint64_t out, uint32_t n_experts, const void* device_bytes,
+                                   uint64_t nbytes, pk_hip_weight** out_weight,
+                                   char* error_buffer, size_t error_capacity);
+
+void pk_hip_weight_release(pk_hip_weight* weight);
+uint64_t pk_hip_weight_bytes(const pk_hip_weight* weight);
+/* Device address of the encoded payload (read-only use by the caller). */
+const void* pk_hip_weight_device_ptr(const pk_hip_weight* weight);
+
+/* y[b] = W . x[b] for b < batch (1..8): TensorLinearBackend::try_linear
+ * (tensor_linear.hpp:16-17; Vulkan: src/vulkan_linear.cpp:612-736), with
+ * caller-owned host buffers x [batch][in] and y [batch][out].  expert selects
+ * one slice of an expert tensor (UINT32_MAX for a plain matrix).  Returns
+ * PK_HIP_STATUS_UNSUPPORTED (CPU fallback) for types or widths without a
+ * kernel; shape errors return INVALID_ARGUMENT; device failures return
+ * RUNTIME_ERROR and mark the context failed (src/vulkan_linear.cpp:636,731-735). */
+pk_hip_status pk_hip_matvec(pk_hip_ctx* ctx, const pk_hip_weight* weight, uint32_t expert,
+                            const float* x, uint32_t batch, float* y, char* error_buffer,
+                            size_t error_capacity);
+
+/* As pk_hip_matvec with device buffers, enqueued on `stream` (a hipStream_t;
+ * NULL = the context stream) without synchronising. */
+pk_hip_status pk_hip_matvec_async(pk_hip_ctx* ctx, const pk_hip_weight* weight,
+                                  uint32_t expert, const float* device_x, uint32_t batch,
+                                  float* device_y, void* stream, char* error_buffer,
+                                  size_t error_capacity);
+
+/* One Qwen3-MoE routed layer. router: F32 [hidden, n_experts]; gate/up:
+ * [hidden, ffn, n_experts]; down: [ffn, hidden, n_experts].  top_k routes by
+ * route_experts (src/qwen3_moe_runner.cpp:267-305): expert ids and their
+ * order bit-exact; normalize = qwen3moe.expert_weights_norm; scale multiplies
+ * every route weight (Qwen3.5 expert_weights_scale,
+ * src/qwen35_runner.cpp:738; 1 for Qwen3-MoE). */
+typedef struct pk_hip_moe_layer {
+    const pk_hip_weight* router;
+    const pk_hip_weight* gate;
+    const pk_hip_weight* up;
+    const pk_hip_weight* down;
+    uint32_t top_k;
+    uint32_t normalize;
+    float scale;
+} pk_hip_moe_layer;
+
+/* MoE block for one token (src/qwen3_moe_runner.cpp:644-691): x is the
+ * normalised hidden state [hidden]; y receives moe_result [hidden] (the
+ * residual add stays with the caller); ids/probs receive the routes in
+ * order [top_k].  Non-finite router logits return RUNTIME_ERROR, as
+ * route_experts throws (:270-276).  Host buffers; synchronous. */
+pk_hip_status pk_hip_moe_decode(pk_hip_ctx* ctx, const pk_hip_moe_layer* layer, const float* x,
+                                float* y, uint32_t* ids, float* probs, char* error_buffer,
+                                size_t error_capacity);
+
+/* Device-buffer variant, enqueued on `stream` without synchronising.  A
+ * router error is reported by the next pk_hip_sync. */
+pk_hip_status pk_hip_moe_decode_async(pk_hip_ctx* ctx, const pk_hip_moe_layer* layer,
+                                      const float* device_x, float* device_y,
+                                      uint32_t* device_ids, float* device_probs, void* stream,
+                                      char* error_buffer, size_t error_capacity);
+
+/* Waits for the context's work (and `stream`, if not NULL) and reports any
+ * deferred router error. */
+pk_hip_status pk_hip_sync(pk_hip_ctx* ctx, void* stream, char* error_buffer,
+                          size_t error_capacity);
+
+pk_hip_status pk_hip_get_stats(const pk_hip_ctx* ctx, pk_hip_stats* out_stats);
+void pk_hip_reset_stats(pk_hip_ctx* ctx);
+
+/* Switches per-launch HIP-event timing (pk_hip_options.time_kernels) on or
+ * off for later calls.  While on, every call synchronises its stream. */
+pk_hip_status pk_hip_set_kernel_timing(pk_hip_ctx* ctx, int enabled);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* POKIT_HIP_H */

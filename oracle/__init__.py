@@ -1,0 +1,200 @@
+"""ctypes bindings to the parity oracle -- TEST INFRASTRUCTURE ONLY.
+
+Two interchangeable back ends with one API:
+
+* ``Oracle("port")``      -- oracle/libpk_oracle.so, the C restatement of the
+  reference CPU path (oracle/pk_oracle.c).
+* ``Oracle("reference")`` -- oracle/_ref/libpkref.so, the reference's own CPU
+  sources compiled in place by ``make -C oracle ref`` (present only where the
+  reference checkout was available at build time, or carried as a built file).
+
+Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg use this
+module; the product package never imports it.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+PORT_PATH = os.path.join(HERE, "libpk_oracle.so")
+REF_PATH = os.path.join(HERE, "_ref", "libpkref.so")
+REFERENCE_ROOT = "/root/reference"
+
+_f32p = ctypes.POINTER(ctypes.c_float)
+_u32p = ctypes.POINTER(ctypes.c_uint32)
+_u8p = ctypes.c_void_p
+
+
+def build(reference: bool = True) -> None:
+    """Compile the C restatement, and the reference library when its sources exist."""
+    targets = ["all"]
+    if reference and os.path.isdir(os.path.join(REFERENCE_ROOT, "src")):
+        targets.append("ref")
+    subprocess.run(["make", "-s", "-C", HERE, "-j8", *targets], check=True)
+
+
+def available(kind: str) -> bool:
+    return os.path.exists(PORT_PATH if kind == "port" else REF_PATH)
+
+
+class OracleError(RuntimeError):
+    def __init__(self, status: int, what: str):
+        super().__init__(f"{what} failed with status {status}")
+        self.status = status
+
+
+def _fp(a: np.ndarray):
+    return a.ctypes.data_as(_f32p)
+
+
+class Oracle:
+    def __init__(self, kind: str = "port"):
+        if kind not in ("port", "reference"):
+            raise ValueError(kind)
+        self.kind = kind
+        path = PORT_PATH if kind == "port" else REF_PATH
+        if not os.path.exists(path):
+            raise FileNotFoundError(f"{path} is not built (run make -C oracle)")
+        self.lib = ctypes.CDLL(path)
+        L = self.lib
+        if kind == "port":
+            L.pko_half_to_float.restype = ctypes.c_float
+            L.pko_half_to_float.argtypes = [ctypes.c_uint16]
+            L.pko_linear.argtypes = [ctypes.c_uint32, _u8p, ctypes.c_uint64, ctypes.c_uint64,
+                                     ctypes.c_uint64, _f32p, _f32p]
+            L.pko_dequantize_row.argtypes = [ctypes.c_uint32, _u8p, ctypes.c_uint64, _f32p,
+                                             ctypes.c_uint64]
+            L.pko_route_experts.argtypes = [_f32p, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_int,
+                                            _u32p, _f32p, _f32p]
+            L.pko_moe_block.argtypes = [_f32p, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32,
+                                        ctypes.c_uint32, _u8p, ctypes.c_uint32, _u8p,
+                                        ctypes.c_uint32, _u8p, ctypes.c_uint32, ctypes.c_int,
+                                        _f32p, _f32p, _u32p, _f32p]
+        else:
+            L.pkref_row_workers.restype = ctypes.c_uint
+            L.pkref_tensor_linear.argtypes = [ctypes.c_uint32, ctypes.c_uint64, ctypes.c_uint64,
+                                              _u8p, ctypes.c_uint64, _f32p, _f32p]
+            L.pkref_tensor_linear_repeat.argtypes = [ctypes.c_uint32, ctypes.c_uint64,
+                                                     ctypes.c_uint64, _u8p, ctypes.c_uint64,
+                                                     _f32p, _f32p, ctypes.c_uint32]
+            L.pkref_dequantize_row.argtypes = [ctypes.c_uint32, _u8p, ctypes.c_uint64, _f32p,
+                                               ctypes.c_uint64]
+            L.pkref_route_experts.argtypes = [_f32p, ctypes.c_uint32, ctypes.c_uint32,
+                                              ctypes.c_int, _u32p, _f32p, _f32p]
+            L.pkref_moe_create.restype = ctypes.c_void_p
+            L.pkref_moe_create.argtypes = [_f32p, ctypes.c_uint32, ctypes.c_uint32,
+                                           ctypes.c_uint32, ctypes.c_uint32, _u8p,
+                                           ctypes.c_uint32, _u8p, ctypes.c_uint32, _u8p,
+                                           ctypes.c_uint32, ctypes.c_int]
+            L.pkref_moe_forward.argtypes = [ctypes.c_void_p, _f32p, _f32p, _u32p, _f32p]
+            L.pkref_moe_destroy.argtypes = [ctypes.c_void_p]
+
+    # ---- single ops -------------------------------------------------------
+    def half_to_float(self, bits: int) -> float:
+        if self.kind != "port":
+            raise NotImplementedError("half_to_float is exported by the port only")
+        return self.lib.pko_half_to_float(bits)
+
+    def linear(self, gtype: int, weights: np.ndarray, in_features: int, rows: int,
+               x: np.ndarray) -> np.ndarray:
+        w = np.ascontiguousarray(weights, dtype=np.uint8)
+        xx = np.ascontiguousarray(x, dtype=np.float32)
+        y = np.empty(rows, dtype=np.float32)
+        if self.kind == "port":
+            rc = self.lib.pko_linear(gtype, w.ctypes.data, w.nbytes, in_features, rows,
+                                     _fp(xx), _fp(y))
+        else:
+            rc = self.lib.pkref_tensor_linear(gtype, in_features, rows, w.ctypes.data, w.nbytes,
+                                              _fp(xx), _fp(y))
+        if rc:
+            raise OracleError(rc, "linear")
+        return y
+
+    def linear_repeat(self, gtype, weights, in_features, rows, x, calls) -> np.ndarray:
+        """Reference only: ``calls`` tensor_linear calls on one reader (timing)."""
+        w = np.ascontiguousarray(weights, dtype=np.uint8)
+        xx = np.ascontiguousarray(x, dtype=np.float32)
+        y = np.empty(rows, dtype=np.float32)
+        rc = self.lib.pkref_tensor_linear_repeat(gtype, in_features, rows, w.ctypes.data,
+                                                 w.nbytes, _fp(xx), _fp(y), calls)
+        if rc:
+            raise OracleError(rc, "linear_repeat")
+        return y
+
+    def dequantize_row(self, gtype: int, encoded: np.ndarray, count: int) -> np.ndarray:
+        e = np.ascontiguousarray(encoded, dtype=np.uint8)
+        out = np.empty(count, dtype=np.float32)
+        fn = self.lib.pko_dequantize_row if self.kind == "port" else self.lib.pkref_dequantize_row
+        rc = fn(gtype, e.ctypes.data, e.nbytes, _fp(out), count)
+        if rc:
+            raise OracleError(rc, "dequantize_row")
+        return out
+
+    def route_experts(self, logits: np.ndarray, top_k: int, normalize: bool):
+        lg = np.ascontiguousarray(logits, dtype=np.float32)
+        ids = np.zeros(max(top_k, 1), dtype=np.uint32)
+        sel = np.zeros(max(top_k, 1), dtype=np.float32)
+        probs = np.zeros(max(top_k, 1), dtype=np.float32)
+        fn = self.lib.pko_route_experts if self.kind == "port" else self.lib.pkref_route_experts
+        rc = fn(_fp(lg), lg.size, top_k, int(normalize), ids.ctypes.data_as(_u32p), _fp(sel),
+                _fp(probs))
+        if rc:
+            raise OracleError(rc, "route_experts")
+        return ids[:top_k], sel[:top_k], probs[:top_k]
+
+    # ---- MoE block -----------------------------------------------------------
+    def moe(self, layer) -> "MoeBlock":
+        return MoeBlock(self, layer)
+
+
+class MoeBlock:
+    """A prepared MoE layer; ``forward(x)`` returns (moe_result, ids, probs)."""
+
+    def __init__(self, oracle: Oracle, layer):
+        self.o, self.layer = oracle, layer
+        self._keep = (np.ascontiguousarray(layer.router, dtype=np.float32),
+                      np.ascontiguousarray(layer.gate), np.ascontiguousarray(layer.up),
+                      np.ascontiguousarray(layer.down))
+        self.handle = None
+        if oracle.kind == "reference":
+            r, g, u, d = self._keep
+            self.handle = oracle.lib.pkref_moe_create(
+                _fp(r), layer.hidden, layer.experts, layer.ffn, layer.gate_type, g.ctypes.data,
+                layer.up_type, u.ctypes.data, layer.down_type, d.ctypes.data, layer.top_k,
+                int(layer.normalize))
+            if not self.handle:
+                raise OracleError(1, "pkref_moe_create")
+
+    def forward(self, x: np.ndarray):
+        L = self.layer
+        xx = np.ascontiguousarray(x, dtype=np.float32)
+        y = np.empty(L.hidden, dtype=np.float32)
+        ids = np.zeros(L.top_k, dtype=np.uint32)
+        probs = np.zeros(L.top_k, dtype=np.float32)
+        if self.o.kind == "port":
+            r, g, u, d = self._keep
+            rc = self.o.lib.pko_moe_block(_fp(r), L.hidden, L.experts, L.ffn, L.gate_type,
+                                          g.ctypes.data, L.up_type, u.ctypes.data, L.down_type,
+                                          d.ctypes.data, L.top_k, int(L.normalize), _fp(xx),
+                                          _fp(y), ids.ctypes.data_as(_u32p), _fp(probs))
+        else:
+            rc = self.o.lib.pkref_moe_forward(self.handle, _fp(xx), _fp(y),
+                                              ids.ctypes.data_as(_u32p), _fp(probs))
+        if rc:
+            raise OracleError(rc, "moe_block")
+        return y, ids, probs
+
+    def close(self):
+        if self.handle:
+            self.o.lib.pkref_moe_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass

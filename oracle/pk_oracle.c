@@ -1,0 +1,347 @@
+/*
+ * pk_oracle.c -- CPU restatement of the PokitLMs routed-MoE K-quant path.
+ *
+ * TEST INFRASTRUCTURE ONLY (parity checker and CPU-baseline port); the HIP
+ * product path never calls it.  Build: oracle/Makefile (gcc -O3, no -march,
+ * -ffp-contract=off), i.e. the same no-FMA scalar arithmetic as the reference
+ * x86-64 build.  Each function names the reference lines it restates.
+ *
+ * Pinned by: tests/test_oracle.py (golden vectors written by the compiled
+ * reference, tests/golden/make_golden.py; exhaustive binary16 check against
+ * numpy; known-answer Q5_K blocks of tests/regression_test.cpp:86-112;
+ * dyadic-exact closed forms for every decoder; brute-force routing order).
+ */
+#include "pk_oracle.h"
+
+#include <math.h>
+#include <stdlib.h>
+#include <string.h>
+
+uint32_t pko_block_elements(uint32_t type) {
+    switch (type) {
+        case PKO_F32: case PKO_F16: case PKO_BF16: return 1;
+        case PKO_Q4_0: case PKO_Q8_0: return 32;
+        case PKO_Q4_K: case PKO_Q5_K: case PKO_Q6_K: return 256;
+        default: return 0;
+    }
+}
+
+uint32_t pko_block_bytes(uint32_t type) {
+    switch (type) {
+        case PKO_F32: return 4;
+        case PKO_F16: case PKO_BF16: return 2;
+        case PKO_Q4_0: return 18;
+        case PKO_Q8_0: return 34;
+        case PKO_Q4_K: return 144;
+        case PKO_Q5_K: return 176;
+        case PKO_Q6_K: return 210;
+        default: return 0;
+    }
+}
+
+static uint16_t rd16(const uint8_t* p) { return (uint16_t)(p[0] | (p[1] << 8)); }
+
+static float bits_to_float(uint32_t u) {
+    float f;
+    memcpy(&f, &u, sizeof f);
+    return f;
+}
+
+/* src/quantized_linear.cpp:18-39 */
+float pko_half_to_float(uint16_t bits) {
+    const uint32_t sign = (uint32_t)(bits & 0x8000u) << 16;
+    const uint32_t exponent = (bits >> 10) & 0x1fu;
+    uint32_t mantissa = bits & 0x03ffu;
+    if (exponent == 0) {
+        if (mantissa == 0) return bits_to_float(sign);
+        int e = -14;
+        while ((mantissa & 0x0400u) == 0) {
+            mantissa <<= 1;
+            --e;
+        }
+        mantissa &= 0x03ffu;
+        return bits_to_float(sign | ((uint32_t)(e + 127) << 23) | (mantissa << 13));
+    }
+    if (exponent == 0x1fu) return bits_to_float(sign | 0x7f800000u | (mantissa << 13));
+    return bits_to_float(sign | ((exponent + 112u) << 23) | (mantissa << 13));
+}
+
+/* 6-bit (scale, min) pair j of a Q4_K/Q5_K block, from the 12 packed bytes
+ * (the scale_min lambda, src/quantized_linear.cpp:176-188). */
+static void kq_scale_min(const uint8_t* sc, unsigned j, unsigned* s, unsigned* m) {
+    if (j < 4) {
+        *s = sc[j] & 63u;
+        *m = sc[j + 4] & 63u;
+    } else {
+        *s = (sc[j + 4] & 0x0fu) | ((sc[j - 4] >> 6) << 4);
+        *m = (sc[j + 4] >> 4) | ((sc[j] >> 6) << 4);
+    }
+}
+
+/* src/quantized_linear.cpp:166-205: value = fl(fl(d*sc)*q) - fl(dmin*m). */
+void pko_decode_q4_k(const uint8_t* block, float* out) {
+    const float d = pko_half_to_float(rd16(block));
+    const float dmin = pko_half_to_float(rd16(block + 2));
+    const uint8_t* sc = block + 4;
+    const uint8_t* qs = block + 16;
+    unsigned o = 0;
+    for (unsigned chunk = 0; chunk < 4; ++chunk) {
+        unsigned s0, m0, s1, m1;
+        kq_scale_min(sc, 2 * chunk, &s0, &m0);
+        kq_scale_min(sc, 2 * chunk + 1, &s1, &m1);
+        const float ds0 = d * (float)s0, dm0 = dmin * (float)m0;
+        const float ds1 = d * (float)s1, dm1 = dmin * (float)m1;
+        for (unsigned i = 0; i < 32; ++i) out[o++] = ds0 * (float)(qs[i] & 0x0fu) - dm0;
+        for (unsigned i = 0; i < 32; ++i) out[o++] = ds1 * (float)(qs[i] >> 4) - dm1;
+        qs += 32;
+    }
+}
+
+/* src/quantized_linear.cpp:286-328: as Q4_K with a fifth bit from qh[32]. */
+void pko_decode_q5_k(const uint8_t* block, float* out) {
+    const float d = pko_half_to_float(rd16(block));
+    const float dmin = pko_half_to_float(rd16(block + 2));
+    const uint8_t* sc = block + 4;
+    const uint8_t* qh = block + 16;
+    const uint8_t* qs = block + 48;
+    unsigned o = 0;
+    unsigned mask1 = 1, mask2 = 2;
+    for (unsigned chunk = 0; chunk < 4; ++chunk) {
+        unsigned s0, m0, s1, m1;
+        kq_scale_min(sc, 2 * chunk, &s0, &m0);
+        kq_scale_min(sc, 2 * chunk + 1, &s1, &m1);
+        const float ds0 = d * (float)s0, dm0 = dmin * (float)m0;
+        const float ds1 = d * (float)s1, dm1 = dmin * (float)m1;
+        for (unsigned i = 0; i < 32; ++i)
+            out[o++] = ds0 * (float)((qs[i] & 0x0fu) + ((qh[i] & mask1) ? 16u : 0u)) - dm0;
+        for (unsigned i = 0; i < 32; ++i)
+            out[o++] = ds1 * (float)((qs[i] >> 4) + ((qh[i] & mask2) ? 16u : 0u)) - dm1;
+        qs += 32;
+        mask1 = (mask1 << 2) & 0xffu;
+        mask2 = (mask2 << 2) & 0xffu;
+        /* mask1 never reaches zero inside four chunks (the reference's
+         * wrap at :326 is dead for one block), so qh is not advanced. */
+    }
+}
+
+/* src/quantized_linear.cpp:330-358: value = fl(fl(d*s)*q), s int8, q in [-32,31]. */
+void pko_decode_q6_k(const uint8_t* block, float* out) {
+    const uint8_t* ql = block;
+    const uint8_t* qh = block + 128;
+    const int8_t* sc = (const int8_t*)(block + 192);
+    const float d = pko_half_to_float(rd16(block + 208));
+    for (unsigned half = 0; half < 2; ++half) {
+        const unsigned base = half * 128;
+        for (unsigned l = 0; l < 32; ++l) {
+            const unsigned is = l / 16;
+            const int q0 = (int)((ql[l] & 0x0fu) | ((qh[l] & 0x03u) << 4)) - 32;
+            const int q1 = (int)((ql[l + 32] & 0x0fu) | (((qh[l] >> 2) & 0x03u) << 4)) - 32;
+            const int q2 = (int)((ql[l] >> 4) | (((qh[l] >> 4) & 0x03u) << 4)) - 32;
+            const int q3 = (int)((ql[l + 32] >> 4) | (((qh[l] >> 6) & 0x03u) << 4)) - 32;
+            const int8_t* s = sc + half * 8 + is;
+            out[base + l] = d * (float)s[0] * (float)q0;
+            out[base + l + 32] = d * (float)s[2] * (float)q1;
+            out[base + l + 64] = d * (float)s[4] * (float)q2;
+            out[base + l + 96] = d * (float)s[6] * (float)q3;
+        }
+        ql += 64;
+        qh += 32;
+    }
+}
+
+/* x86 scalar dot_f32 (src/simd_kernels.hpp:12-24): serial, no FMA. */
+static float dot_f32(const float* a, const float* b, size_t n) {
+    float s = 0.0f;
+    for (size_t i = 0; i < n; ++i) s += a[i] * b[i];
+    return s;
+}
+
+/* x86 scalar dot_i8_f32 (src/simd_kernels.hpp:26-48). */
+static float dot_i8_f32(const float* x, const int8_t* q, size_t n) {
+    float s = 0.0f;
+    for (size_t i = 0; i < n; ++i) s += (float)q[i] * x[i];
+    return s;
+}
+
+/* unpack_q4_0 scalar branch (src/simd_kernels.hpp:50-65). */
+static void unpack_q4_0(const uint8_t* packed, int8_t* out) {
+    for (unsigned i = 0; i < 16; ++i) {
+        out[i] = (int8_t)((int)(packed[i] & 0x0fu) - 8);
+        out[i + 16] = (int8_t)((int)(packed[i] >> 4) - 8);
+    }
+}
+
+int pko_dequantize_row(uint32_t type, const uint8_t* enc, uint64_t enc_bytes, float* out,
+                       uint64_t count) {
+    const uint32_t be = pko_block_elements(type), bb = pko_block_bytes(type);
+    if (be < 32 || count == 0 || count % be != 0 || enc_bytes != count / be * bb) return 1;
+    const uint64_t blocks = count / be;
+    for (uint64_t b = 0; b < blocks; ++b) {
+        const uint8_t* blk = enc + b * bb;
+        float* row = out + b * be;
+        switch (type) {
+            case PKO_Q4_0: case PKO_Q8_0: {
+                /* src/quantized_linear.cpp:437-449 via scale_i8_f32 (simd_kernels.hpp:85) */
+                const float scale = pko_half_to_float(rd16(blk));
+                int8_t q[32];
+                if (type == PKO_Q4_0) unpack_q4_0(blk + 2, q);
+                else memcpy(q, blk + 2, 32);
+                for (unsigned i = 0; i < 32; ++i) row[i] = scale * (float)q[i];
+                break;
+            }
+            case PKO_Q4_K: pko_decode_q4_k(blk, row); break;
+            case PKO_Q5_K: pko_decode_q5_k(blk, row); break;
+            case PKO_Q6_K: pko_decode_q6_k(blk, row); break;
+            default: return 1;
+        }
+    }
+    return 0;
+}
+
+/* Floating rows are converted exactly as TensorReader::read_float_rows_into
+ * (src/tensor_reader.cpp:164-198) and fed to linear() (src/linear.cpp:10-31),
+ * whose empty bias contributes 0.0F + dot. */
+static float float_element(uint32_t type, const uint8_t* row, uint64_t i) {
+    if (type == PKO_F32) {
+        float f;
+        memcpy(&f, row + 4 * i, 4);
+        return f;
+    }
+    if (type == PKO_BF16) return bits_to_float((uint32_t)rd16(row + 2 * i) << 16);
+    return pko_half_to_float(rd16(row + 2 * i));
+}
+
+int pko_linear(uint32_t type, const uint8_t* w, uint64_t w_bytes, uint64_t in, uint64_t rows,
+               const float* x, float* y) {
+    const uint32_t be = pko_block_elements(type), bb = pko_block_bytes(type);
+    if (be == 0 || in == 0 || rows == 0 || in % be != 0) return 1;
+    const uint64_t row_bytes = in / be * bb;
+    if (w_bytes != row_bytes * rows) return 1;
+    if (be == 1) {
+        float* tmp = (float*)malloc(in * sizeof(float));
+        if (!tmp) return 2;
+        for (uint64_t r = 0; r < rows; ++r) {
+            const uint8_t* row = w + r * row_bytes;
+            for (uint64_t i = 0; i < in; ++i) tmp[i] = float_element(type, row, i);
+            y[r] = 0.0f + dot_f32(tmp, x, in);
+        }
+        free(tmp);
+        return 0;
+    }
+    const uint64_t blocks = in / be;
+    for (uint64_t r = 0; r < rows; ++r) {
+        float sum = 0.0f;
+        for (uint64_t b = 0; b < blocks; ++b) {
+            const uint8_t* blk = w + r * row_bytes + b * bb;
+            const float* xb = x + b * be;
+            if (type == PKO_Q4_0 || type == PKO_Q8_0) {
+                /* linear_quantized (src/quantized_linear.cpp:405-422) */
+                const float scale = pko_half_to_float(rd16(blk));
+                int8_t q[32];
+                if (type == PKO_Q4_0) unpack_q4_0(blk + 2, q);
+                else memcpy(q, blk + 2, 32);
+                sum += scale * dot_i8_f32(xb, q, 32);
+            } else {
+                /* linear_k (src/quantized_linear.cpp:374-384); on x86 Q4_K takes
+                 * this decode-then-dot branch (:541-549). */
+                float dec[256];
+                if (type == PKO_Q4_K) pko_decode_q4_k(blk, dec);
+                else if (type == PKO_Q5_K) pko_decode_q5_k(blk, dec);
+                else pko_decode_q6_k(blk, dec);
+                sum += dot_f32(dec, xb, 256);
+            }
+        }
+        y[r] = sum;
+    }
+    return 0;
+}
+
+/* src/qwen3_moe_runner.cpp:267-305 */
+int pko_route_experts(const float* logits, uint32_t n, uint32_t top_k, int normalize,
+                      uint32_t* ids, float* sel_logits, float* probs) {
+    if (top_k == 0 || top_k > n) return 1;
+    /* std::max_element: first maximum under operator< */
+    uint32_t mi = 0;
+    for (uint32_t i = 1; i < n; ++i)
+        if (logits[mi] < logits[i]) mi = i;
+    const float mx = logits[mi];
+    if (!isfinite(mx)) return 2;
+    for (uint32_t i = 0; i < n; ++i)
+        if (!isfinite(logits[i])) return 2;
+    double denominator = 0.0;
+    for (uint32_t i = 0; i < n; ++i) denominator += exp((double)(logits[i] - mx));
+    /* sorted insertion by (logit desc, id asc); keep the first top_k */
+    uint32_t count = 0;
+    for (uint32_t id = 0; id < n; ++id) {
+        const float v = logits[id];
+        uint32_t where = 0;
+        while (where < count && (logits[ids[where]] > v ||
+                                 (logits[ids[where]] == v && ids[where] < id)))
+            ++where;
+        if (count < top_k) {
+            for (uint32_t j = count; j > where; --j) ids[j] = ids[j - 1];
+            ids[where] = id;
+            ++count;
+        } else if (where < count) {
+            for (uint32_t j = count - 1; j > where; --j) ids[j] = ids[j - 1];
+            ids[where] = id;
+        }
+    }
+    float selected_sum = 0.0f;
+    for (uint32_t i = 0; i < top_k; ++i) {
+        const uint32_t id = ids[i];
+        probs[i] = (float)(exp((double)(logits[id] - mx)) / denominator);
+        selected_sum += probs[i];
+        if (sel_logits) sel_logits[i] = logits[id];
+    }
+    if (normalize)
+        for (uint32_t i = 0; i < top_k; ++i) probs[i] /= selected_sum;
+    return 0;
+}
+
+/* src/qwen3_moe_runner.cpp:643-692 (rms_norm at :643 and the residual add at
+ * :692 are the caller's). */
+int pko_moe_block(const float* router, uint32_t hidden, uint32_t n_experts, uint32_t ffn,
+                  uint32_t gate_type, const uint8_t* gate, uint32_t up_type, const uint8_t* up,
+                  uint32_t down_type, const uint8_t* down, uint32_t top_k, int normalize,
+                  const float* x, float* y, uint32_t* ids, float* probs) {
+    if (hidden == 0 || n_experts == 0 || ffn == 0 || top_k == 0 || top_k > n_experts) return 1;
+    const uint64_t gate_be = pko_block_elements(gate_type), up_be = pko_block_elements(up_type),
+                   down_be = pko_block_elements(down_type);
+    if (!gate_be || !up_be || !down_be || hidden % gate_be || hidden % up_be || ffn % down_be)
+        return 1;
+    const uint64_t gate_slice = (uint64_t)ffn * (hidden / gate_be) * pko_block_bytes(gate_type);
+    const uint64_t up_slice = (uint64_t)ffn * (hidden / up_be) * pko_block_bytes(up_type);
+    const uint64_t down_slice = (uint64_t)hidden * (ffn / down_be) * pko_block_bytes(down_type);
+    float* logits = (float*)malloc(sizeof(float) * n_experts);
+    float* g = (float*)malloc(sizeof(float) * ffn);
+    float* u = (float*)malloc(sizeof(float) * ffn);
+    float* act = (float*)malloc(sizeof(float) * ffn);
+    float* out = (float*)malloc(sizeof(float) * hidden);
+    int rc = 2;
+    if (!logits || !g || !u || !act || !out) goto done;
+    rc = pko_linear(PKO_F32, (const uint8_t*)router, (uint64_t)hidden * n_experts * 4, hidden,
+                    n_experts, x, logits);
+    if (rc) goto done;
+    rc = pko_route_experts(logits, n_experts, top_k, normalize, ids, NULL, probs);
+    if (rc) goto done;
+    for (uint32_t i = 0; i < hidden; ++i) y[i] = 0.0f;
+    for (uint32_t r = 0; r < top_k; ++r) {
+        const uint64_t e = ids[r];
+        rc = pko_linear(gate_type, gate + e * gate_slice, gate_slice, hidden, ffn, x, g);
+        if (!rc) rc = pko_linear(up_type, up + e * up_slice, up_slice, hidden, ffn, x, u);
+        if (rc) goto done;
+        for (uint32_t i = 0; i < ffn; ++i) act[i] = (g[i] / (1.0f + expf(-g[i]))) * u[i];
+        rc = pko_linear(down_type, down + e * down_slice, down_slice, ffn, hidden, act, out);
+        if (rc) goto done;
+        for (uint32_t i = 0; i < hidden; ++i) y[i] += probs[r] * out[i];
+    }
+    rc = 0;
+done:
+    free(logits);
+    free(g);
+    free(u);
+    free(act);
+    free(out);
+    return rc;
+}

@@ -1,0 +1,80 @@
+/*
+ * pk_oracle.h -- CPU restatement of the PokitLMs routed-MoE K-quant path.
+ *
+ * TEST INFRASTRUCTURE ONLY.  This library is the parity checker for the HIP
+ * backend: only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline
+ * leg may load it.  The product path (pokitlms_amd) never links or calls it.
+ *
+ * Every function restates the reference's x86-64 CPU arithmetic order
+ * (reference built with -O3 and no -march, so no FMA contraction and the
+ * scalar branches of src/simd_kernels.hpp).  Citations are to the reference
+ * checkout (RemydreScarlet/PokitLMs v0.4.0).
+ *
+ * Return codes follow pokitlms_status (include/pokitlms/pokitlms.h:18-24):
+ * 0 ok, 1 invalid argument, 2 runtime error.
+ */
+#ifndef PK_ORACLE_H
+#define PK_ORACLE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* GGUF tensor type ids (reference src/gguf_reader.cpp:21-57). */
+enum {
+    PKO_F32 = 0, PKO_F16 = 1, PKO_Q4_0 = 2, PKO_Q8_0 = 8,
+    PKO_Q4_K = 12, PKO_Q5_K = 13, PKO_Q6_K = 14, PKO_BF16 = 30
+};
+
+/* Elements and bytes of one encoded block; 0 when the type is not on the path. */
+uint32_t pko_block_elements(uint32_t type);
+uint32_t pko_block_bytes(uint32_t type);
+
+/* IEEE binary16 -> binary32, subnormals/Inf/NaN included
+ * (src/quantized_linear.cpp:18-39). */
+float pko_half_to_float(uint16_t bits);
+
+/* One 256-element K-quant block to F32 (src/quantized_linear.cpp:166-205,
+ * 286-328, 330-358). */
+void pko_decode_q4_k(const uint8_t* block, float* out256);
+void pko_decode_q5_k(const uint8_t* block, float* out256);
+void pko_decode_q6_k(const uint8_t* block, float* out256);
+
+/* dequantize_quantized_row for Q4_0/Q8_0/Q4_K/Q5_K/Q6_K
+ * (src/quantized_linear.cpp:427-493). */
+int pko_dequantize_row(uint32_t type, const uint8_t* encoded, uint64_t encoded_bytes,
+                       float* out, uint64_t count);
+
+/* out[r] = W[r] . x for a row-major GGUF matrix [in, rows] of the given type:
+ * the tensor_linear CPU branch (src/tensor_linear.cpp:232-263) over
+ * linear_k / linear_quantized / linear (src/quantized_linear.cpp:360-423,
+ * src/linear.cpp:10-31).  Single-threaded; rows are independent, so the
+ * reference's row thread pool does not change any bit. */
+int pko_linear(uint32_t type, const uint8_t* weights, uint64_t weight_bytes,
+               uint64_t in, uint64_t rows, const float* x, float* y);
+
+/* route_experts (src/qwen3_moe_runner.cpp:267-305): double softmax
+ * denominator over all logits, top-k ordered by (logit desc, id asc),
+ * float probabilities, optional float renormalisation.  Returns 2 on
+ * non-finite logits, 1 on a bad top_k. */
+int pko_route_experts(const float* logits, uint32_t count, uint32_t top_k, int normalize,
+                      uint32_t* ids, float* selected_logits, float* probabilities);
+
+/* One Qwen3-MoE MoE block for a single token (src/qwen3_moe_runner.cpp:643-692):
+ * router logits (F32 [hidden, n_experts]) -> route_experts -> for each route in
+ * order: gate/up matvec, SwiGLU g/(1+expf(-g))*u, down matvec, moe += p*y.
+ * Expert tensors are the GGUF [in, out, E] layout, expert e at byte e*slice.
+ * y receives moe_result (the residual add is the caller's). */
+int pko_moe_block(const float* router, uint32_t hidden, uint32_t n_experts, uint32_t ffn,
+                  uint32_t gate_type, const uint8_t* gate, uint32_t up_type, const uint8_t* up,
+                  uint32_t down_type, const uint8_t* down, uint32_t top_k, int normalize,
+                  const float* x, float* y, uint32_t* ids, float* probabilities);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

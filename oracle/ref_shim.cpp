@@ -1,0 +1,200 @@
+// ref_shim.cpp -- C entry points into the compiled reference CPU path.
+//
+// TEST INFRASTRUCTURE ONLY.  oracle/Makefile compiles this file together with
+// the reference's own sources, read in place from /root/reference/src (nothing
+// is copied into this repository), into oracle/_ref/libpkref.so.  The library
+// writes the golden vectors under tests/golden/ and serves as the timed CPU
+// baseline ("kind": "reference").  route_experts lives in an anonymous
+// namespace of src/qwen3_moe_runner.cpp, so that translation unit is included
+// here to make it reachable.
+#include "qwen3_moe_runner.cpp"  // resolved through -I/root/reference/src
+
+#include "pokitlms/model/tensor_linear.hpp"
+#include "pokitlms/model/tensor_reader.hpp"
+#include "pokitlms/ops/quantized_linear.hpp"
+
+#include <cmath>
+#include <cstdint>
+#include <cstring>
+#include <memory>
+#include <stdexcept>
+#include <thread>
+#include <vector>
+
+namespace {
+
+int status_of_current_exception() {
+    try {
+        throw;
+    } catch (const std::invalid_argument&) {
+        return 1;
+    } catch (const std::exception&) {
+        return 2;
+    } catch (...) {
+        return 4;
+    }
+}
+
+pokitlms::model::TensorReader make_reader(std::uint32_t type, std::uint64_t in,
+                                          std::uint64_t rows, const void* bytes,
+                                          std::uint64_t nbytes) {
+    pokitlms::model::TensorInfo tensor;
+    tensor.name = "pkref";
+    tensor.dimensions = {in, rows};
+    tensor.type = type;
+    tensor.payload_size = nbytes;
+    auto payload = std::make_shared<std::vector<std::byte>>(nbytes);
+    std::memcpy(payload->data(), bytes, nbytes);
+    return pokitlms::model::TensorReader(tensor, payload);
+}
+
+}  // namespace
+
+extern "C" {
+
+// Worker count of the reference row pool (src/tensor_linear.cpp:56-64).
+unsigned pkref_row_workers(void) {
+    const auto hardware = std::thread::hardware_concurrency();
+    return std::min(6U, std::max(2U, hardware > 1 ? hardware - 1 : 2U));
+}
+
+// tensor_linear over an in-memory GGUF matrix [in, rows] (src/tensor_linear.cpp:232-263).
+int pkref_tensor_linear(std::uint32_t type, std::uint64_t in, std::uint64_t rows,
+                        const void* bytes, std::uint64_t nbytes, const float* x, float* y) {
+    try {
+        const auto reader = make_reader(type, in, rows, bytes, nbytes);
+        pokitlms::model::tensor_linear(reader, std::span<const float>(x, in),
+                                       std::span<float>(y, rows));
+        return 0;
+    } catch (...) {
+        return status_of_current_exception();
+    }
+}
+
+// Same, repeated `calls` times on one prepared reader (CPU baseline timing).
+int pkref_tensor_linear_repeat(std::uint32_t type, std::uint64_t in, std::uint64_t rows,
+                               const void* bytes, std::uint64_t nbytes, const float* x,
+                               float* y, std::uint32_t calls) {
+    try {
+        const auto reader = make_reader(type, in, rows, bytes, nbytes);
+        for (std::uint32_t c = 0; c < calls; ++c) {
+            pokitlms::model::tensor_linear(reader, std::span<const float>(x, in),
+                                           std::span<float>(y, rows));
+        }
+        return 0;
+    } catch (...) {
+        return status_of_current_exception();
+    }
+}
+
+int pkref_dequantize_row(std::uint32_t type, const void* encoded, std::uint64_t nbytes,
+                         float* out, std::uint64_t count) {
+    try {
+        pokitlms::dequantize_quantized_row(
+            type, std::span<const std::byte>(static_cast<const std::byte*>(encoded), nbytes),
+            std::span<float>(out, count));
+        return 0;
+    } catch (...) {
+        return status_of_current_exception();
+    }
+}
+
+int pkref_route_experts(const float* logits, std::uint32_t count, std::uint32_t top_k,
+                        int normalize, std::uint32_t* ids, float* selected_logits,
+                        float* probabilities) {
+    try {
+        const auto routes = pokitlms::model::route_experts(
+            std::span<const float>(logits, count), top_k, normalize != 0);
+        for (std::size_t i = 0; i < routes.size(); ++i) {
+            ids[i] = static_cast<std::uint32_t>(routes[i].id);
+            if (selected_logits) selected_logits[i] = routes[i].logit;
+            probabilities[i] = routes[i].probability;
+        }
+        return 0;
+    } catch (...) {
+        return status_of_current_exception();
+    }
+}
+
+// A prepared MoE layer: readers over the router and every expert slice.
+struct pkref_moe {
+    std::uint32_t hidden{}, experts{}, ffn{}, top_k{};
+    bool normalize{};
+    std::unique_ptr<pokitlms::model::TensorReader> router;
+    std::vector<pokitlms::model::TensorReader> gate, up, down;
+};
+
+void pkref_moe_destroy(pkref_moe* moe) { delete moe; }
+
+pkref_moe* pkref_moe_create(const float* router, std::uint32_t hidden, std::uint32_t experts,
+                            std::uint32_t ffn, std::uint32_t gate_type, const void* gate,
+                            std::uint32_t up_type, const void* up, std::uint32_t down_type,
+                            const void* down, std::uint32_t top_k, int normalize) {
+    try {
+        auto moe = std::make_unique<pkref_moe>();
+        moe->hidden = hidden;
+        moe->experts = experts;
+        moe->ffn = ffn;
+        moe->top_k = top_k;
+        moe->normalize = normalize != 0;
+        moe->router = std::make_unique<pokitlms::model::TensorReader>(
+            make_reader(0, hidden, experts, router, std::uint64_t{hidden} * experts * 4));
+        const auto slice_bytes = [](std::uint32_t type, std::uint64_t in, std::uint64_t out) {
+            const std::uint64_t block = type >= 12 ? 256 : 32;
+            const std::uint64_t bytes = type == 2 ? 18 : type == 8 ? 34 : type == 12 ? 144
+                                        : type == 13 ? 176 : 210;
+            return out * (in / block) * bytes;
+        };
+        const auto gs = slice_bytes(gate_type, hidden, ffn);
+        const auto us = slice_bytes(up_type, hidden, ffn);
+        const auto ds = slice_bytes(down_type, ffn, hidden);
+        for (std::uint32_t e = 0; e < experts; ++e) {
+            moe->gate.push_back(make_reader(gate_type, hidden, ffn,
+                                            static_cast<const std::byte*>(gate) + e * gs, gs));
+            moe->up.push_back(make_reader(up_type, hidden, ffn,
+                                          static_cast<const std::byte*>(up) + e * us, us));
+            moe->down.push_back(make_reader(down_type, ffn, hidden,
+                                            static_cast<const std::byte*>(down) + e * ds, ds));
+        }
+        return moe.release();
+    } catch (...) {
+        return nullptr;
+    }
+}
+
+// The MoE block of src/qwen3_moe_runner.cpp:644-691, statement for statement,
+// over the reference's own tensor_linear and route_experts.  y = moe_result.
+int pkref_moe_forward(pkref_moe* moe, const float* x, float* y, std::uint32_t* ids,
+                      float* probabilities) {
+    try {
+        using pokitlms::model::tensor_linear;
+        const std::span<const float> normalized(x, moe->hidden);
+        std::vector<float> router_logits(moe->experts), gate(moe->ffn), up(moe->ffn),
+            activated(moe->ffn), expert_output(moe->hidden);
+        pokitlms::model::TensorLinearScratch scratch;
+        tensor_linear(*moe->router, normalized, router_logits, 0, &scratch);
+        const auto routes = pokitlms::model::route_experts(router_logits, moe->top_k,
+                                                           moe->normalize);
+        std::span<float> moe_result(y, moe->hidden);
+        std::fill(moe_result.begin(), moe_result.end(), 0.0F);
+        for (std::size_t r = 0; r < routes.size(); ++r) {
+            const auto& route = routes[r];
+            ids[r] = static_cast<std::uint32_t>(route.id);
+            probabilities[r] = route.probability;
+            tensor_linear(moe->gate[route.id], normalized, gate, 0, &scratch);
+            tensor_linear(moe->up[route.id], normalized, up, 0, &scratch);
+            for (std::size_t i = 0; i < activated.size(); ++i) {
+                activated[i] = (gate[i] / (1.0F + std::exp(-gate[i]))) * up[i];
+            }
+            tensor_linear(moe->down[route.id], activated, expert_output, 0, &scratch);
+            for (std::size_t i = 0; i < moe_result.size(); ++i) {
+                moe_result[i] += route.probability * expert_output[i];
+            }
+        }
+        return 0;
+    } catch (...) {
+        return status_of_current_exception();
+    }
+}
+
+}  // extern "C"

@@ -1,0 +1,233 @@
+"""Python host API over libpokit_hip.so.
+
+Mirrors the reference plugin surface for the routed-MoE path:
+
+* ``HipBackend.try_linear(tensor, x, y) -> bool`` is
+  ``TensorLinearBackend::try_linear`` (include/pokitlms/model/tensor_linear.hpp:
+  11-18 of the reference): False means "not covered, use the CPU kernel";
+  shape errors raise ``ValueError``; device failures raise ``HipError`` and
+  leave the backend failed (src/vulkan_linear.cpp:636, 731-735).
+* ``HipBackend.upload(..., n_experts=E)`` keeps every expert resident in HBM,
+  replacing ExpertStore's LRU (src/expert_store.cpp:81-141).
+* ``HipBackend.moe_decode(layer, x)`` is the MoE block of
+  src/qwen3_moe_runner.cpp:643-692 for one token.
+
+Everything here is plumbing around the C ABI; the arithmetic runs in the HIP
+kernels of ``csrc/``.
+"""
+from __future__ import annotations
+
+import ctypes
+from dataclasses import dataclass
+
+import numpy as np
+
+from . import _abi
+from . import synth as S
+
+_ERRBUF = 512
+
+
+class HipError(RuntimeError):
+    def __init__(self, status: int, message: str):
+        super().__init__(f"[status {status}] {message}")
+        self.status = status
+
+
+class Unsupported(HipError):
+    pass
+
+
+def _raise(status: int, err: ctypes.Array) -> None:
+    if status == _abi.STATUS_OK:
+        return
+    msg = err.value.decode(errors="replace")
+    if status == _abi.STATUS_UNSUPPORTED:
+        raise Unsupported(status, msg)
+    if status == _abi.STATUS_INVALID_ARGUMENT:
+        raise ValueError(msg)
+    raise HipError(status, msg)
+
+
+def _f32p(a: np.ndarray):
+    return a.ctypes.data_as(ctypes.POINTER(ctypes.c_float))
+
+
+@dataclass
+class TensorView:
+    """A GGUF tensor as the reference's TensorReader presents it: type,
+    dims = [in, out], and the encoded payload (host bytes)."""
+    gtype: int
+    dims: tuple
+    payload: np.ndarray
+
+
+class Weight:
+    def __init__(self, backend: "HipBackend", handle: int, gtype: int, in_features: int,
+                 out_features: int, n_experts: int, nbytes: int):
+        self.backend, self.handle = backend, handle
+        self.gtype, self.in_features, self.out_features = gtype, in_features, out_features
+        self.n_experts, self.nbytes = n_experts, nbytes
+
+    @property
+    def device_ptr(self) -> int:
+        return _abi.lib().pk_hip_weight_device_ptr(self.handle) or 0
+
+    @property
+    def slice_bytes(self) -> int:
+        return self.nbytes // max(self.n_experts, 1)
+
+    def release(self) -> None:
+        if self.handle:
+            _abi.lib().pk_hip_weight_release(self.handle)
+            self.handle = None
+
+
+class MoeLayerHandles:
+    """A routed MoE layer resident in HBM (router, gate, up, down)."""
+
+    def __init__(self, router: Weight, gate: Weight, up: Weight, down: Weight, top_k: int,
+                 normalize: bool, scale: float = 1.0):
+        self.router, self.gate, self.up, self.down = router, gate, up, down
+        self.top_k, self.normalize, self.scale = top_k, normalize, scale
+        self.desc = _abi.MoeLayerDesc(router.handle, gate.handle, up.handle, down.handle, top_k,
+                                      1 if normalize else 0, scale)
+        self.hidden, self.ffn, self.experts = router.in_features, gate.out_features, router.out_features
+
+    def routed_bytes(self) -> int:
+        return self.router.nbytes + self.top_k * (self.gate.slice_bytes + self.up.slice_bytes +
+                                                  self.down.slice_bytes)
+
+    def release(self) -> None:
+        for w in (self.router, self.gate, self.up, self.down):
+            w.release()
+
+
+class HipBackend:
+    def __init__(self, device: int = 0, time_kernels: bool = False):
+        L = _abi.lib()
+        opts = _abi.Options(ctypes.sizeof(_abi.Options), 1 if time_kernels else 0)
+        h = ctypes.c_void_p()
+        err = ctypes.create_string_buffer(_ERRBUF)
+        _raise(L.pk_hip_create(device, ctypes.byref(opts), ctypes.byref(h), err, _ERRBUF), err)
+        self.handle = h.value
+        self._cache = {}
+
+    # ---- lifetime ---------------------------------------------------------------
+    def close(self) -> None:
+        for w in self._cache.values():
+            w.release()
+        self._cache.clear()
+        if self.handle:
+            _abi.lib().pk_hip_destroy(self.handle)
+            self.handle = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    # ---- weights ----------------------------------------------------------------
+    def upload(self, gtype: int, in_features: int, out_features: int, data: np.ndarray,
+               n_experts: int = 0) -> Weight:
+        buf = np.ascontiguousarray(data).view(np.uint8)
+        h = ctypes.c_void_p()
+        err = ctypes.create_string_buffer(_ERRBUF)
+        _raise(_abi.lib().pk_hip_upload(self.handle, gtype, in_features, out_features, n_experts,
+                                        buf.ctypes.data, buf.nbytes, ctypes.byref(h), err,
+                                        _ERRBUF), err)
+        return Weight(self, h.value, gtype, in_features, out_features, n_experts, buf.nbytes)
+
+    def upload_device(self, gtype: int, in_features: int, out_features: int, device_ptr: int,
+                      nbytes: int, n_experts: int = 0) -> Weight:
+        h = ctypes.c_void_p()
+        err = ctypes.create_string_buffer(_ERRBUF)
+        _raise(_abi.lib().pk_hip_upload_device(self.handle, gtype, in_features, out_features,
+                                               n_experts, device_ptr, nbytes, ctypes.byref(h),
+                                               err, _ERRBUF), err)
+        return Weight(self, h.value, gtype, in_features, out_features, n_experts, nbytes)
+
+    def upload_moe_layer(self, layer: "S.MoeLayer") -> MoeLayerHandles:
+        r = self.upload(S.F32, layer.hidden, layer.experts, layer.router)
+        g = self.upload(layer.gate_type, layer.hidden, layer.ffn, layer.gate, layer.experts)
+        u = self.upload(layer.up_type, layer.hidden, layer.ffn, layer.up, layer.experts)
+        d = self.upload(layer.down_type, layer.ffn, layer.hidden, layer.down, layer.experts)
+        return MoeLayerHandles(r, g, u, d, layer.top_k, layer.normalize)
+
+    # ---- matvec -----------------------------------------------------------------
+    def matvec(self, w: Weight, x: np.ndarray, expert: int | None = None) -> np.ndarray:
+        xx = np.ascontiguousarray(x, dtype=np.float32)
+        batch = 1 if xx.ndim == 1 else xx.shape[0]
+        if xx.size != batch * w.in_features:
+            raise ValueError("input width does not match the matrix")
+        y = np.empty((batch, w.out_features), dtype=np.float32)
+        err = ctypes.create_string_buffer(_ERRBUF)
+        _raise(_abi.lib().pk_hip_matvec(self.handle, w.handle,
+                                        _abi.NO_EXPERT if expert is None else expert, _f32p(xx),
+                                        batch, _f32p(y), err, _ERRBUF), err)
+        return y[0] if xx.ndim == 1 else y
+
+    def matvec_async(self, w: Weight, device_x: int, batch: int, device_y: int, stream: int = 0,
+                     expert: int | None = None) -> None:
+        err = ctypes.create_string_buffer(_ERRBUF)
+        _raise(_abi.lib().pk_hip_matvec_async(self.handle, w.handle,
+                                              _abi.NO_EXPERT if expert is None else expert,
+                                              device_x, batch, device_y, stream or None, err,
+                                              _ERRBUF), err)
+
+    def try_linear(self, tensor: TensorView, x: np.ndarray, y: np.ndarray) -> bool:
+        """TensorLinearBackend::try_linear over a host GGUF tensor (uploaded
+        once per payload object and kept resident)."""
+        if not _abi.lib().pk_hip_type_supported(tensor.gtype):
+            return False
+        in_features, out_features = int(tensor.dims[0]), int(tensor.dims[1])
+        if x.size != in_features or y.size != out_features:
+            raise ValueError("GGUF matrix dimensions do not match linear input/output")
+        key = id(tensor.payload)
+        w = self._cache.get(key)
+        if w is None or w.gtype != tensor.gtype:
+            try:
+                w = self.upload(tensor.gtype, in_features, out_features, tensor.payload)
+            except Unsupported:
+                return False
+            self._cache[key] = w
+        try:
+            y[...] = self.matvec(w, x)
+        except Unsupported:
+            return False
+        return True
+
+    # ---- MoE --------------------------------------------------------------------
+    def moe_decode(self, layer: MoeLayerHandles, x: np.ndarray):
+        xx = np.ascontiguousarray(x, dtype=np.float32)
+        y = np.empty(layer.hidden, dtype=np.float32)
+        ids = np.zeros(layer.top_k, dtype=np.uint32)
+        probs = np.zeros(layer.top_k, dtype=np.float32)
+        err = ctypes.create_string_buffer(_ERRBUF)
+        _raise(_abi.lib().pk_hip_moe_decode(self.handle, ctypes.byref(layer.desc), _f32p(xx),
+                                            _f32p(y), ids.ctypes.data_as(ctypes.POINTER(ctypes.c_uint32)),
+                                            _f32p(probs), err, _ERRBUF), err)
+        return y, ids, probs
+
+    def moe_decode_async(self, layer: MoeLayerHandles, device_x: int, device_y: int,
+                         device_ids: int, device_probs: int, stream: int = 0) -> None:
+        err = ctypes.create_string_buffer(_ERRBUF)
+        _raise(_abi.lib().pk_hip_moe_decode_async(self.handle, ctypes.byref(layer.desc),
+                                                  device_x, device_y, device_ids, device_probs,
+                                                  stream or None, err, _ERRBUF), err)
+
+    def sync(self, stream: int = 0) -> None:
+        err = ctypes.create_string_buffer(_ERRBUF)
+        _raise(_abi.lib().pk_hip_sync(self.handle, stream or None, err, _ERRBUF), err)
+
+    def stats(self) -> dict:
+        st = _abi.Stats()
+        _abi.lib().pk_hip_get_stats(self.handle, ctypes.byref(st))
+        return st.as_dict()
+
+    def reset_stats(self) -> None:
+        _abi.lib().pk_hip_reset_stats(self.handle)
+
+    def set_kernel_timing(self, enabled: bool) -> None:
+        _abi.lib().pk_hip_set_kernel_timing(self.handle, 1 if enabled else 0)

@@ -1,0 +1,588 @@
+// api.hip -- the extern "C" boundary of libpokit_hip.so (include/pokit_hip.h).
+//
+// Error model of the reference backends: invalid shapes -> INVALID_ARGUMENT,
+// uncovered types/widths -> UNSUPPORTED (the caller's CPU fallback, like
+// try_linear returning false), device failures -> RUNTIME_ERROR and a sticky
+// failed state (src/vulkan_linear.cpp:636, 731-735 of the reference).  No C++
+// exception crosses the ABI (src/c_api.cpp:87-101).
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstring>
+#include <mutex>
+#include <new>
+#include <stdexcept>
+#include <string>
+
+#include "../../include/pokit_hip.h"
+#include "launch.hpp"
+
+namespace {
+
+struct ArgError : std::invalid_argument {
+    using std::invalid_argument::invalid_argument;
+};
+struct Unsupported : std::runtime_error {
+    using std::runtime_error::runtime_error;
+};
+struct DeviceError : std::runtime_error {
+    using std::runtime_error::runtime_error;
+};
+
+void set_error(char* dst, size_t cap, const char* msg) noexcept {
+    if (!dst || cap == 0) return;
+    const size_t n = std::min(cap - 1, std::strlen(msg));
+    std::memcpy(dst, msg, n);
+    dst[n] = '\0';
+}
+
+void check(hipError_t e, const char* what) {
+    if (e != hipSuccess) throw DeviceError(std::string(what) + ": " + hipGetErrorString(e));
+}
+
+uint32_t block_elements(uint32_t t) {
+    switch (t) {
+        case 0: case 1: case 30: return 1;
+        case 2: case 8: return 32;
+        case 12: case 13: case 14: return 256;
+        default: return 0;
+    }
+}
+
+uint32_t block_bytes(uint32_t t) {
+    switch (t) {
+        case 0: return 4;
+        case 1: case 30: return 2;
+        case 2: return 18;
+        case 8: return 34;
+        case 12: return 144;
+        case 13: return 176;
+        case 14: return 210;
+        default: return 0;
+    }
+}
+
+template <typename T>
+struct DeviceBuffer {
+    T* ptr = nullptr;
+    size_t count = 0;
+    void ensure(size_t n) {
+        if (n <= count) return;
+        if (ptr) (void)hipFree(ptr);
+        ptr = nullptr;
+        count = 0;
+        check(hipMalloc(&ptr, n * sizeof(T)), "hipMalloc scratch");
+        count = n;
+    }
+    void release() noexcept {
+        if (ptr) (void)hipFree(ptr);
+        ptr = nullptr;
+        count = 0;
+    }
+};
+
+}  // namespace
+
+struct pk_hip_ctx {
+    int device = 0;
+    hipStream_t stream = nullptr;
+    bool failed = false;
+    bool time_kernels = false;
+    mutable std::mutex mutex;
+    pk_hip_stats stats{};
+    uint64_t live_weights = 0;
+    // scratch
+    DeviceBuffer<float> x, y, act, probs;
+    DeviceBuffer<uint32_t> ids, words;  // words: [0] counter, [1..4] status
+    DeviceBuffer<double> row_sum, row_bound;
+    hipEvent_t ev[8] = {};
+
+    void set_device() const { check(hipSetDevice(device), "hipSetDevice"); }
+};
+
+struct pk_hip_weight {
+    pk_hip_ctx* ctx = nullptr;
+    uint32_t type = 0;
+    uint64_t in = 0, out = 0;
+    uint32_t n_experts = 0;
+    uint64_t row_bytes = 0, slice_bytes = 0, nbytes = 0;
+    uint8_t* dptr = nullptr;
+};
+
+namespace {
+
+constexpr uint32_t kStatusCounter = 0, kStatusError = 1;
+
+uint32_t* status_words(pk_hip_ctx* c) { return c->words.ptr + 1; }
+
+template <typename F>
+pk_hip_status guarded(pk_hip_ctx* ctx, char* err, size_t cap, F&& body) {
+    try {
+        body();
+        set_error(err, cap, "");
+        return PK_HIP_STATUS_OK;
+    } catch (const Unsupported& e) {
+        set_error(err, cap, e.what());
+        return PK_HIP_STATUS_UNSUPPORTED;
+    } catch (const ArgError& e) {
+        set_error(err, cap, e.what());
+        return PK_HIP_STATUS_INVALID_ARGUMENT;
+    } catch (const DeviceError& e) {
+        if (ctx) ctx->failed = true;
+        set_error(err, cap, e.what());
+        return PK_HIP_STATUS_RUNTIME_ERROR;
+    } catch (const std::bad_alloc&) {
+        set_error(err, cap, "out of host memory");
+        return PK_HIP_STATUS_RUNTIME_ERROR;
+    } catch (const std::exception& e) {
+        set_error(err, cap, e.what());
+        return PK_HIP_STATUS_RUNTIME_ERROR;
+    } catch (...) {
+        set_error(err, cap, "unknown HIP backend failure");
+        return PK_HIP_STATUS_INTERNAL_ERROR;
+    }
+}
+
+void require_usable(const pk_hip_ctx* ctx) {
+    if (!ctx) throw ArgError("HIP backend context is required");
+    if (ctx->failed) throw DeviceError("HIP backend failed during an earlier operation");
+}
+
+void count_dispatch(pk_hip_ctx* c, uint32_t type) {
+    ++c->stats.dispatches;
+    switch (type) {
+        case 2: ++c->stats.q4_0_dispatches; break;
+        case 8: ++c->stats.q8_0_dispatches; break;
+        case 12: ++c->stats.q4_k_dispatches; break;
+        case 13: ++c->stats.q5_k_dispatches; break;
+        case 14: ++c->stats.q6_k_dispatches; break;
+        default: ++c->stats.float_dispatches; break;
+    }
+}
+
+pk_hip_weight* make_weight(pk_hip_ctx* ctx, uint32_t type, uint64_t in, uint64_t out,
+                           uint32_t n_experts, uint64_t nbytes) {
+    require_usable(ctx);
+    const uint32_t be = block_elements(type), bb = block_bytes(type);
+    if (be == 0) throw Unsupported("GGUF type has no HIP kernel");
+    if (in == 0 || out == 0) throw ArgError("GGUF matrix dimensions must be non-zero");
+    if (in % be) throw ArgError("GGUF row is not a whole number of blocks");
+    if (in > 0xffffffffull || out > 0xffffffffull) throw Unsupported("matrix too large");
+    const uint64_t row = in / be * bb;
+    const uint64_t slice = row * out;
+    const uint64_t experts = n_experts ? n_experts : 1;
+    if (slice > UINT64_MAX / experts || slice * experts != nbytes)
+        throw ArgError("GGUF payload size does not match its dimensions");
+    auto w = new pk_hip_weight;
+    w->ctx = ctx;
+    w->type = type;
+    w->in = in;
+    w->out = out;
+    w->n_experts = n_experts;
+    w->row_bytes = row;
+    w->slice_bytes = slice;
+    w->nbytes = nbytes;
+    ctx->set_device();
+    const hipError_t e = hipMalloc(&w->dptr, nbytes + pk::kWeightTailPad);
+    if (e != hipSuccess) {
+        delete w;
+        throw DeviceError(std::string("hipMalloc weights: ") + hipGetErrorString(e));
+    }
+    check(hipMemsetAsync(w->dptr + nbytes, 0, pk::kWeightTailPad, ctx->stream), "pad weights");
+    return w;
+}
+
+void begin_timing(pk_hip_ctx* c, hipStream_t s, int slot) {
+    if (c->time_kernels) check(hipEventRecord(c->ev[slot], s), "hipEventRecord");
+}
+
+uint64_t elapsed_ns(pk_hip_ctx* c, int a, int b) {
+    float ms = 0.0f;
+    check(hipEventElapsedTime(&ms, c->ev[a], c->ev[b]), "hipEventElapsedTime");
+    return static_cast<uint64_t>(static_cast<double>(ms) * 1.0e6);
+}
+
+void launch_checked(hipError_t e, const char* what) {
+    if (e == hipErrorInvalidValue) throw Unsupported(std::string(what) + ": shape not covered");
+    check(e, what);
+}
+
+void enqueue_matvec(pk_hip_ctx* c, const pk_hip_weight* w, uint32_t expert, const float* dx,
+                    uint32_t batch, float* dy, hipStream_t s) {
+    if (!w || w->ctx != c) throw ArgError("weight handle does not belong to this context");
+    if (batch == 0 || batch > 8) throw ArgError("batch must be between 1 and 8");
+    if (!dx || !dy) throw ArgError("input and output buffers are required");
+    uint64_t offset = 0;
+    if (expert != UINT32_MAX) {
+        if (w->n_experts == 0 || expert >= w->n_experts)
+            throw ArgError("expert index out of range");
+        offset = static_cast<uint64_t>(expert) * w->slice_bytes;
+    }
+    if (!pk::matvec_supported(w->type, static_cast<uint32_t>(w->in), batch))
+        throw Unsupported("matrix width/batch not covered by the HIP matvec kernels");
+    begin_timing(c, s, 0);
+    launch_checked(pk::launch_matvec(w->type, w->dptr + offset, w->row_bytes,
+                                     static_cast<uint32_t>(w->out), static_cast<uint32_t>(w->in),
+                                     dx, dy, batch, s),
+                   "matvec launch");
+    begin_timing(c, s, 1);
+    ++c->stats.matvec_calls;
+    ++c->stats.matvec_launches;
+    count_dispatch(c, w->type);
+    c->stats.weight_bytes += w->slice_bytes;
+}
+
+struct MoeShape {
+    uint32_t hidden, ffn, experts;
+};
+
+MoeShape check_layer(pk_hip_ctx* c, const pk_hip_moe_layer* L) {
+    if (!L || !L->router || !L->gate || !L->up || !L->down)
+        throw ArgError("MoE layer needs router, gate, up and down weights");
+    for (const pk_hip_weight* w : {L->router, L->gate, L->up, L->down})
+        if (w->ctx != c) throw ArgError("weight handle does not belong to this context");
+    if (L->router->type != 0 || L->router->n_experts != 0)
+        throw Unsupported("router must be a plain F32 matrix");
+    MoeShape m{static_cast<uint32_t>(L->router->in), static_cast<uint32_t>(L->gate->out),
+               static_cast<uint32_t>(L->router->out)};
+    if (L->gate->n_experts != m.experts || L->up->n_experts != m.experts ||
+        L->down->n_experts != m.experts)
+        throw ArgError("expert tensors must have one slice per router output");
+    if (L->gate->in != m.hidden || L->up->in != m.hidden || L->up->out != m.ffn ||
+        L->down->in != m.ffn || L->down->out != m.hidden)
+        throw ArgError("MoE tensor dimensions do not match");
+    if (L->top_k == 0 || L->top_k > m.experts) throw ArgError("invalid expert top-k");
+    if (!(L->scale > 0.0f) || !(L->scale < 1.0e30f)) throw ArgError("invalid route scale");
+    if (!pk::moe_decode_supported(L->gate->type, L->up->type, L->down->type, m.hidden, m.ffn,
+                                  m.experts, L->top_k))
+        throw Unsupported("MoE shape not covered by the HIP kernels");
+    return m;
+}
+
+void ensure_moe_scratch(pk_hip_ctx* c, const MoeShape& m, uint32_t top_k) {
+    c->act.ensure(static_cast<size_t>(top_k) * m.ffn);
+    c->row_sum.ensure(m.experts);
+    c->row_bound.ensure(m.experts);
+    c->ids.ensure(16);
+    c->probs.ensure(16);
+}
+
+void enqueue_moe(pk_hip_ctx* c, const pk_hip_moe_layer* L, const MoeShape& m, const float* dx,
+                 float* dy, uint32_t* dids, float* dprobs, hipStream_t s) {
+    ensure_moe_scratch(c, m, L->top_k);
+    pk::MoeDecodeArgs a{};
+    a.router = reinterpret_cast<const float*>(L->router->dptr);
+    a.gate = L->gate->dptr;
+    a.up = L->up->dptr;
+    a.down = L->down->dptr;
+    a.gate_type = L->gate->type;
+    a.up_type = L->up->type;
+    a.down_type = L->down->type;
+    a.gate_slice = L->gate->slice_bytes;
+    a.up_slice = L->up->slice_bytes;
+    a.down_slice = L->down->slice_bytes;
+    a.gate_row = L->gate->row_bytes;
+    a.up_row = L->up->row_bytes;
+    a.down_row = L->down->row_bytes;
+    a.hidden = m.hidden;
+    a.ffn = m.ffn;
+    a.n_experts = m.experts;
+    a.top_k = L->top_k;
+    a.normalize = L->normalize ? 1u : 0u;
+    a.scale = L->scale;
+    a.x = dx;
+    a.y = dy;
+    a.ids = dids;
+    a.probs = dprobs;
+    a.row_sum = c->row_sum.ptr;
+    a.row_bound = c->row_bound.ptr;
+    a.act = c->act.ptr;
+    a.counter = c->words.ptr + kStatusCounter;
+    a.status = status_words(c);
+    begin_timing(c, s, 2);
+    launch_checked(pk::launch_moe_router(a, s), "router launch");
+    begin_timing(c, s, 3);
+    launch_checked(pk::launch_moe_gate_up(a, s), "gate/up launch");
+    begin_timing(c, s, 4);
+    launch_checked(pk::launch_moe_down(a, s), "down launch");
+    begin_timing(c, s, 5);
+    ++c->stats.moe_decode_calls;
+    ++c->stats.router_launches;
+    ++c->stats.gate_up_launches;
+    ++c->stats.down_launches;
+    c->stats.dispatches += 3;
+    count_dispatch(c, L->gate->type);
+    count_dispatch(c, L->down->type);
+    c->stats.dispatches -= 2;  // the two per-format counts above are the same launches
+    c->stats.weight_bytes += L->router->nbytes +
+                             static_cast<uint64_t>(L->top_k) *
+                                 (L->gate->slice_bytes + L->up->slice_bytes + L->down->slice_bytes);
+    c->stats.expert_hits += L->top_k;
+}
+
+void collect_timing_matvec(pk_hip_ctx* c) {
+    if (c->time_kernels) c->stats.matvec_ns += elapsed_ns(c, 0, 1);
+}
+
+void collect_timing_moe(pk_hip_ctx* c) {
+    if (!c->time_kernels) return;
+    c->stats.router_ns += elapsed_ns(c, 2, 3);
+    c->stats.gate_up_ns += elapsed_ns(c, 3, 4);
+    c->stats.down_ns += elapsed_ns(c, 4, 5);
+}
+
+void sync_and_check(pk_hip_ctx* c, hipStream_t s) {
+    uint32_t err_word = 0;
+    check(hipMemcpyAsync(&err_word, status_words(c) + (kStatusError - 1), sizeof(err_word),
+                         hipMemcpyDeviceToHost, s),
+          "read router status");
+    check(hipStreamSynchronize(s), "hipStreamSynchronize");
+    if (err_word) {
+        check(hipMemsetAsync(status_words(c) + (kStatusError - 1), 0, sizeof(uint32_t), s),
+              "clear router status");
+        check(hipStreamSynchronize(s), "hipStreamSynchronize");
+        throw std::runtime_error("expert router produced non-finite logits");
+    }
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* pk_hip_version(void) { return "0.1.0"; }
+
+int pk_hip_type_supported(uint32_t t) {
+    switch (t) {
+        case 0: case 1: case 2: case 8: case 12: case 13: case 14: case 30: return 1;
+        default: return 0;
+    }
+}
+
+pk_hip_status pk_hip_create(int device, const pk_hip_options* options, pk_hip_ctx** out_ctx,
+                            char* err, size_t cap) {
+    if (out_ctx) *out_ctx = nullptr;
+    pk_hip_ctx* c = nullptr;
+    const pk_hip_status st = guarded(nullptr, err, cap, [&] {
+        if (!out_ctx) throw ArgError("output handle is required");
+        if (options && options->struct_size != sizeof(pk_hip_options))
+            throw ArgError("pk_hip_options.struct_size mismatch");
+        int count = 0;
+        check(hipGetDeviceCount(&count), "hipGetDeviceCount");
+        const int dev = device < 0 ? 0 : device;
+        if (dev >= count) throw ArgError("HIP device index out of range");
+        c = new pk_hip_ctx;
+        c->device = dev;
+        c->time_kernels = options && options->time_kernels;
+        c->set_device();
+        check(hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking), "hipStreamCreate");
+        for (auto& e : c->ev) check(hipEventCreate(&e), "hipEventCreate");
+        c->words.ensure(8);
+        check(hipMemsetAsync(c->words.ptr, 0, 8 * sizeof(uint32_t), c->stream), "init status");
+        check(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+        *out_ctx = c;
+    });
+    if (st != PK_HIP_STATUS_OK && c) pk_hip_destroy(c);
+    return st;
+}
+
+void pk_hip_destroy(pk_hip_ctx* c) {
+    if (!c) return;
+    (void)hipSetDevice(c->device);
+    if (c->stream) (void)hipStreamSynchronize(c->stream);
+    c->x.release();
+    c->y.release();
+    c->act.release();
+    c->probs.release();
+    c->ids.release();
+    c->words.release();
+    c->row_sum.release();
+    c->row_bound.release();
+    for (auto& e : c->ev)
+        if (e) (void)hipEventDestroy(e);
+    if (c->stream) (void)hipStreamDestroy(c->stream);
+    delete c;
+}
+
+static pk_hip_status upload_impl(pk_hip_ctx* ctx, uint32_t type, uint64_t in, uint64_t out,
+                                 uint32_t n_experts, const void* src, uint64_t nbytes,
+                                 hipMemcpyKind kind, pk_hip_weight** out_w, char* err,
+                                 size_t cap) {
+    if (out_w) *out_w = nullptr;
+    return guarded(ctx, err, cap, [&] {
+        if (!out_w || !src) throw ArgError("source bytes and output handle are required");
+        require_usable(ctx);
+        std::lock_guard lock(ctx->mutex);
+        pk_hip_weight* w = make_weight(ctx, type, in, out, n_experts, nbytes);
+        const hipError_t e = hipMemcpyAsync(w->dptr, src, nbytes, kind, ctx->stream);
+        const hipError_t s = e == hipSuccess ? hipStreamSynchronize(ctx->stream) : e;
+        if (s != hipSuccess) {
+            (void)hipFree(w->dptr);
+            delete w;
+            check(s, "weight upload");
+        }
+        ctx->stats.resident_bytes += nbytes;
+        ctx->stats.uploaded_bytes += nbytes;
+        ++ctx->live_weights;
+        *out_w = w;
+    });
+}
+
+pk_hip_status pk_hip_upload(pk_hip_ctx* ctx, uint32_t type, uint64_t in, uint64_t out,
+                            uint32_t n_experts, const void* host_bytes, uint64_t nbytes,
+                            pk_hip_weight** out_w, char* err, size_t cap) {
+    return upload_impl(ctx, type, in, out, n_experts, host_bytes, nbytes, hipMemcpyHostToDevice,
+                       out_w, err, cap);
+}
+
+pk_hip_status pk_hip_upload_device(pk_hip_ctx* ctx, uint32_t type, uint64_t in, uint64_t out,
+                                   uint32_t n_experts, const void* device_bytes, uint64_t nbytes,
+                                   pk_hip_weight** out_w, char* err, size_t cap) {
+    return upload_impl(ctx, type, in, out, n_experts, device_bytes, nbytes,
+                       hipMemcpyDeviceToDevice, out_w, err, cap);
+}
+
+void pk_hip_weight_release(pk_hip_weight* w) {
+    if (!w) return;
+    if (w->ctx) {
+        std::lock_guard lock(w->ctx->mutex);
+        (void)hipSetDevice(w->ctx->device);
+        (void)hipStreamSynchronize(w->ctx->stream);
+        (void)hipFree(w->dptr);
+        w->ctx->stats.resident_bytes -= w->nbytes;
+        --w->ctx->live_weights;
+    }
+    delete w;
+}
+
+uint64_t pk_hip_weight_bytes(const pk_hip_weight* w) { return w ? w->nbytes : 0; }
+const void* pk_hip_weight_device_ptr(const pk_hip_weight* w) { return w ? w->dptr : nullptr; }
+
+pk_hip_status pk_hip_matvec(pk_hip_ctx* ctx, const pk_hip_weight* w, uint32_t expert,
+                            const float* x, uint32_t batch, float* y, char* err, size_t cap) {
+    return guarded(ctx, err, cap, [&] {
+        require_usable(ctx);
+        if (!w || !x || !y) throw ArgError("weight, input and output are required");
+        if (batch == 0 || batch > 8) throw ArgError("batch must be between 1 and 8");
+        std::lock_guard lock(ctx->mutex);
+        if (!pk::matvec_supported(w->type, static_cast<uint32_t>(w->in), batch))
+            throw Unsupported("matrix width/batch not covered by the HIP matvec kernels");
+        ctx->set_device();
+        ctx->x.ensure(static_cast<size_t>(batch) * w->in);
+        ctx->y.ensure(static_cast<size_t>(batch) * w->out);
+        check(hipMemcpyAsync(ctx->x.ptr, x, batch * w->in * sizeof(float), hipMemcpyHostToDevice,
+                             ctx->stream),
+              "copy input");
+        enqueue_matvec(ctx, w, expert, ctx->x.ptr, batch, ctx->y.ptr, ctx->stream);
+        check(hipMemcpyAsync(y, ctx->y.ptr, batch * w->out * sizeof(float),
+                             hipMemcpyDeviceToHost, ctx->stream),
+              "copy output");
+        check(hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
+        collect_timing_matvec(ctx);
+    });
+}
+
+pk_hip_status pk_hip_matvec_async(pk_hip_ctx* ctx, const pk_hip_weight* w, uint32_t expert,
+                                  const float* dx, uint32_t batch, float* dy, void* stream,
+                                  char* err, size_t cap) {
+    return guarded(ctx, err, cap, [&] {
+        require_usable(ctx);
+        std::lock_guard lock(ctx->mutex);
+        ctx->set_device();
+        hipStream_t s = stream ? static_cast<hipStream_t>(stream) : ctx->stream;
+        enqueue_matvec(ctx, w, expert, dx, batch, dy, s);
+        if (ctx->time_kernels) {
+            check(hipStreamSynchronize(s), "hipStreamSynchronize");
+            collect_timing_matvec(ctx);
+        }
+    });
+}
+
+pk_hip_status pk_hip_moe_decode(pk_hip_ctx* ctx, const pk_hip_moe_layer* layer, const float* x,
+                                float* y, uint32_t* ids, float* probs, char* err, size_t cap) {
+    return guarded(ctx, err, cap, [&] {
+        require_usable(ctx);
+        if (!x || !y || !ids || !probs) throw ArgError("input and output buffers are required");
+        std::lock_guard lock(ctx->mutex);
+        const MoeShape m = check_layer(ctx, layer);
+        ctx->set_device();
+        ctx->x.ensure(m.hidden);
+        ctx->y.ensure(m.hidden);
+        ensure_moe_scratch(ctx, m, layer->top_k);
+        check(hipMemcpyAsync(ctx->x.ptr, x, m.hidden * sizeof(float), hipMemcpyHostToDevice,
+                             ctx->stream),
+              "copy input");
+        enqueue_moe(ctx, layer, m, ctx->x.ptr, ctx->y.ptr, ctx->ids.ptr, ctx->probs.ptr,
+                    ctx->stream);
+        check(hipMemcpyAsync(y, ctx->y.ptr, m.hidden * sizeof(float), hipMemcpyDeviceToHost,
+                             ctx->stream),
+              "copy output");
+        check(hipMemcpyAsync(ids, ctx->ids.ptr, layer->top_k * sizeof(uint32_t),
+                             hipMemcpyDeviceToHost, ctx->stream),
+              "copy ids");
+        check(hipMemcpyAsync(probs, ctx->probs.ptr, layer->top_k * sizeof(float),
+                             hipMemcpyDeviceToHost, ctx->stream),
+              "copy probabilities");
+        sync_and_check(ctx, ctx->stream);
+        collect_timing_moe(ctx);
+    });
+}
+
+pk_hip_status pk_hip_moe_decode_async(pk_hip_ctx* ctx, const pk_hip_moe_layer* layer,
+                                      const float* dx, float* dy, uint32_t* dids, float* dprobs,
+                                      void* stream, char* err, size_t cap) {
+    return guarded(ctx, err, cap, [&] {
+        require_usable(ctx);
+        if (!dx || !dy || !dids || !dprobs) throw ArgError("device buffers are required");
+        std::lock_guard lock(ctx->mutex);
+        const MoeShape m = check_layer(ctx, layer);
+        ctx->set_device();
+        hipStream_t s = stream ? static_cast<hipStream_t>(stream) : ctx->stream;
+        enqueue_moe(ctx, layer, m, dx, dy, dids, dprobs, s);
+        if (ctx->time_kernels) {
+            check(hipStreamSynchronize(s), "hipStreamSynchronize");
+            collect_timing_moe(ctx);
+        }
+    });
+}
+
+pk_hip_status pk_hip_sync(pk_hip_ctx* ctx, void* stream, char* err, size_t cap) {
+    return guarded(ctx, err, cap, [&] {
+        require_usable(ctx);
+        std::lock_guard lock(ctx->mutex);
+        ctx->set_device();
+        if (stream) check(hipStreamSynchronize(static_cast<hipStream_t>(stream)), "sync stream");
+        sync_and_check(ctx, ctx->stream);
+    });
+}
+
+pk_hip_status pk_hip_get_stats(const pk_hip_ctx* ctx, pk_hip_stats* out) {
+    if (!ctx || !out) return PK_HIP_STATUS_INVALID_ARGUMENT;
+    std::lock_guard lock(ctx->mutex);
+    *out = ctx->stats;
+    uint32_t words[4] = {};
+    if (hipSetDevice(ctx->device) == hipSuccess &&
+        hipStreamSynchronize(ctx->stream) == hipSuccess &&
+        hipMemcpy(words, ctx->words.ptr + 1, sizeof(words), hipMemcpyDeviceToHost) == hipSuccess) {
+        out->router_fallbacks = words[1];
+        out->router_candidates = words[2];
+    }
+    return PK_HIP_STATUS_OK;
+}
+
+pk_hip_status pk_hip_set_kernel_timing(pk_hip_ctx* ctx, int enabled) {
+    if (!ctx) return PK_HIP_STATUS_INVALID_ARGUMENT;
+    std::lock_guard lock(ctx->mutex);
+    ctx->time_kernels = enabled != 0;
+    return PK_HIP_STATUS_OK;
+}
+
+void pk_hip_reset_stats(pk_hip_ctx* ctx) {
+    if (!ctx) return;
+    std::lock_guard lock(ctx->mutex);
+    const uint64_t resident = ctx->stats.resident_bytes, uploaded = ctx->stats.uploaded_bytes;
+    ctx->stats = pk_hip_stats{};
+    ctx->stats.resident_bytes = resident;
+    ctx->stats.uploaded_bytes = uploaded;
+}
+
+}  // extern "C"

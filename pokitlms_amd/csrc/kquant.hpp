@@ -1,0 +1,287 @@
+// kquant.hpp -- device-side GGUF block decoding for gfx950 matrix-vector work.
+//
+// A row of a GGUF matrix is a run of encoded blocks.  Each block is split into
+// "units": UB consecutive bytes of the block's primary quant stream, the
+// natural 4/8/16-byte load of one lane.  Decoding a unit yields RUNS runs of
+// UB elements whose activation columns are fixed for a given unit index, so a
+// lane keeps the activations of its units in registers and streams rows past
+// them.  Per-run sums use the factored form
+//     sum_i w_i x_i = (d*sc) * sum_i q_i x_i  -  (dmin*m) * sum_i x_i
+// (with a bias folded into sum_i x_i for the signed formats), which is
+// algebraically the reference decode-then-dot of src/quantized_linear.cpp
+// (:166-205, :286-358, :387-423) with a different FP32 rounding order.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace pk {
+
+enum : uint32_t {
+    T_F32 = 0, T_F16 = 1, T_Q4_0 = 2, T_Q8_0 = 8, T_Q4_K = 12, T_Q5_K = 13, T_Q6_K = 14,
+    T_BF16 = 30
+};
+
+template <int T> struct Fmt;
+// BE: elements per block, BB: bytes per block, PRIM: bytes of the primary
+// quant stream per block, RUNS: element runs per unit.
+template <> struct Fmt<T_Q4_K> { static constexpr int BE = 256, BB = 144, PRIM = 128, RUNS = 2, MAXUB = 32; };
+template <> struct Fmt<T_Q5_K> { static constexpr int BE = 256, BB = 176, PRIM = 128, RUNS = 2, MAXUB = 32; };
+template <> struct Fmt<T_Q6_K> { static constexpr int BE = 256, BB = 210, PRIM = 128, RUNS = 2, MAXUB = 16; };
+template <> struct Fmt<T_Q8_0> { static constexpr int BE = 32, BB = 34, PRIM = 32, RUNS = 1, MAXUB = 16; };
+template <> struct Fmt<T_Q4_0> { static constexpr int BE = 32, BB = 18, PRIM = 16, RUNS = 2, MAXUB = 16; };
+
+// ---------------------------------------------------------------------------
+// Loads.  Q4_K/Q5_K blocks (144/176 B) keep 16-byte alignment; Q6_K (210 B),
+// Q8_0 (34 B) and Q4_0 (18 B) only keep 2-byte alignment, so their fields are
+// fetched as dword-aligned words and re-aligned with v_alignbyte.  Buffers
+// handed to the kernels carry at least 16 readable bytes past the payload.
+
+template <int N>
+__device__ __forceinline__ void ld_words(const uint8_t* p, uint32_t (&w)[N]) {
+    __builtin_memcpy(w, __builtin_assume_aligned(p, 4), 4 * N);
+}
+
+template <int N>
+__device__ __forceinline__ void ld_words_2a(const uint8_t* p, uint32_t (&w)[N]) {
+    const uintptr_t a = reinterpret_cast<uintptr_t>(p);
+    const uint32_t shift = static_cast<uint32_t>(a & 3u);
+    uint32_t raw[N + 1];
+    ld_words<N + 1>(reinterpret_cast<const uint8_t*>(a & ~uintptr_t{3}), raw);
+#pragma unroll
+    for (int i = 0; i < N; ++i) w[i] = __builtin_amdgcn_alignbyte(raw[i + 1], raw[i], shift);
+}
+
+__device__ __forceinline__ float half_bits_to_float(uint32_t bits16) {
+    return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(bits16)));
+}
+
+__device__ __forceinline__ uint16_t ld_u16(const uint8_t* p) {
+    return *reinterpret_cast<const uint16_t*>(__builtin_assume_aligned(p, 2));
+}
+
+// v_cvt_f32_ubyteN: byte N of a word as float in one instruction (the
+// compiler otherwise emits bfe + cvt for pre-masked words).
+template <int N>
+__device__ __forceinline__ float ub(uint32_t v) {
+    float r;
+    if constexpr (N == 0) asm("v_cvt_f32_ubyte0 %0, %1" : "=v"(r) : "v"(v));
+    else if constexpr (N == 1) asm("v_cvt_f32_ubyte1 %0, %1" : "=v"(r) : "v"(v));
+    else if constexpr (N == 2) asm("v_cvt_f32_ubyte2 %0, %1" : "=v"(r) : "v"(v));
+    else asm("v_cvt_f32_ubyte3 %0, %1" : "=v"(r) : "v"(v));
+    return r;
+}
+
+// dot += bytes(v) . x[0..3]
+__device__ __forceinline__ float dot4(uint32_t v, const float* x, float acc) {
+    acc = __builtin_fmaf(ub<0>(v), x[0], acc);
+    acc = __builtin_fmaf(ub<1>(v), x[1], acc);
+    acc = __builtin_fmaf(ub<2>(v), x[2], acc);
+    acc = __builtin_fmaf(ub<3>(v), x[3], acc);
+    return acc;
+}
+
+// 6-bit (scale, min) pair j of a Q4_K/Q5_K block from header words h[1..3]
+// (the 12 packed bytes at block+4; scale_min, src/quantized_linear.cpp:176-188).
+__device__ __forceinline__ void kq_scale_min(const uint32_t (&h)[4], uint32_t j, float& s,
+                                             float& m) {
+    const uint32_t sh = 8u * (j & 3u);
+    const uint32_t by = (h[1] >> sh) & 0xffu, bz = (h[2] >> sh) & 0xffu, bw = (h[3] >> sh) & 0xffu;
+    const uint32_t s_lo = by & 63u, m_lo = bz & 63u;
+    const uint32_t s_hi = (bw & 15u) | ((by >> 6) << 4), m_hi = (bw >> 4) | ((bz >> 6) << 4);
+    s = static_cast<float>(j < 4 ? s_lo : s_hi);
+    m = static_cast<float>(j < 4 ? m_lo : m_hi);
+}
+
+// ---------------------------------------------------------------------------
+// Unit geometry.  Unit u of a row: block b = u / UPB, unit j = u % UPB inside
+// the block, primary byte offset k0 = j * UB.  col[r] is the activation column
+// of the first element of run r.  All of it is row-independent.
+
+struct UnitPos {
+    uint32_t boff;    // byte offset of the block inside the row
+    uint32_t k0;      // primary-stream byte offset inside the block
+    uint32_t col[2];  // activation column of run 0 / run 1
+};
+
+template <int T, int UB>
+__device__ __forceinline__ UnitPos unit_pos(uint32_t u) {
+    using F = Fmt<T>;
+    constexpr uint32_t UPB = F::PRIM / UB;
+    const uint32_t b = u / UPB, j = u % UPB, k0 = j * UB;
+    UnitPos p;
+    p.boff = b * F::BB;
+    p.k0 = k0;
+    const uint32_t base = b * F::BE;
+    if constexpr (T == T_Q4_K || T == T_Q5_K) {
+        p.col[0] = base + 64u * (k0 / 32u) + (k0 % 32u);
+        p.col[1] = p.col[0] + 32u;
+    } else if constexpr (T == T_Q6_K) {
+        const uint32_t kk = k0 % 64u;
+        p.col[0] = base + 128u * (k0 / 64u) + (kk >= 32u ? 32u : 0u) + (kk % 32u);
+        p.col[1] = p.col[0] + 64u;
+    } else if constexpr (T == T_Q8_0) {
+        p.col[0] = base + k0;
+        p.col[1] = p.col[0];
+    } else {  // Q4_0
+        p.col[0] = base + k0;
+        p.col[1] = p.col[0] + 16u;
+    }
+    return p;
+}
+
+// Activations of one unit for B vectors: xv[b][r*UB + i] = x[b][col[r] + i],
+// xs[b][r] = sum_i xv[b][r*UB + i].
+template <int T, int UB, int B>
+struct UnitX {
+    static constexpr int R = Fmt<T>::RUNS;
+    float v[B][R * UB];
+    float s[B][R];
+};
+
+template <int T, int UB, int B>
+__device__ __forceinline__ void load_unit_x(const float* x, uint32_t x_stride, const UnitPos& p,
+                                            bool valid, UnitX<T, UB, B>& ux) {
+    constexpr int R = Fmt<T>::RUNS;
+#pragma unroll
+    for (int b = 0; b < B; ++b) {
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            float sum = 0.0f;
+#pragma unroll
+            for (int i = 0; i < UB; i += 4) {
+                float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+                if (valid) v = *reinterpret_cast<const float4*>(x + b * x_stride + p.col[r] + i);
+                ux.v[b][r * UB + i + 0] = v.x;
+                ux.v[b][r * UB + i + 1] = v.y;
+                ux.v[b][r * UB + i + 2] = v.z;
+                ux.v[b][r * UB + i + 3] = v.w;
+                sum += (v.x + v.y) + (v.z + v.w);
+            }
+            ux.s[b][r] = sum;
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// acc[b] += (this unit of the row starting at `row`) . x[b]
+
+template <int T, int UB, int B>
+__device__ __forceinline__ void unit_fma(const uint8_t* __restrict__ row, const UnitPos& p,
+                                         const UnitX<T, UB, B>& ux, float (&acc)[B]) {
+    constexpr int NW = UB / 4;
+    const uint8_t* blk = row + p.boff;
+    float dot0[B], dot1[B];
+#pragma unroll
+    for (int b = 0; b < B; ++b) dot0[b] = dot1[b] = 0.0f;
+
+    if constexpr (T == T_Q4_K || T == T_Q5_K) {
+        uint32_t h[4];
+        ld_words<4>(blk, h);
+        uint32_t q[NW];
+        ld_words<NW>(blk + (T == T_Q4_K ? 16 : 48) + p.k0, q);
+        uint32_t qh[NW];
+        const uint32_t c = p.k0 / 32u;
+        if constexpr (T == T_Q5_K) ld_words<NW>(blk + 16 + (p.k0 % 32u), qh);
+#pragma unroll
+        for (int t = 0; t < NW; ++t) {
+            uint32_t lo = q[t] & 0x0f0f0f0fu;
+            uint32_t hi = (q[t] >> 4) & 0x0f0f0f0fu;
+            if constexpr (T == T_Q5_K) {
+                lo |= ((qh[t] >> (2u * c)) & 0x01010101u) << 4;
+                hi |= ((qh[t] >> (2u * c + 1u)) & 0x01010101u) << 4;
+            }
+#pragma unroll
+            for (int b = 0; b < B; ++b) {
+                dot0[b] = dot4(lo, &ux.v[b][4 * t], dot0[b]);
+                dot1[b] = dot4(hi, &ux.v[b][UB + 4 * t], dot1[b]);
+            }
+        }
+        const float d = half_bits_to_float(h[0] & 0xffffu);
+        const float dmin = half_bits_to_float(h[0] >> 16);
+        float s0, m0, s1, m1;
+        kq_scale_min(h, 2u * c, s0, m0);
+        kq_scale_min(h, 2u * c + 1u, s1, m1);
+        const float ds0 = d * s0, dm0 = dmin * m0, ds1 = d * s1, dm1 = dmin * m1;
+#pragma unroll
+        for (int b = 0; b < B; ++b) {
+            float t0 = __builtin_fmaf(ds0, dot0[b], -dm0 * ux.s[b][0]);
+            float t1 = __builtin_fmaf(ds1, dot1[b], -dm1 * ux.s[b][1]);
+            acc[b] += t0 + t1;
+        }
+    } else if constexpr (T == T_Q6_K) {
+        const uint32_t kk = p.k0 % 64u;
+        const uint32_t sl = kk >= 32u ? 2u : 0u;
+        uint32_t ql[NW], qh[NW];
+        ld_words_2a<NW>(blk + p.k0, ql);
+        ld_words_2a<NW>(blk + 128u + 32u * (p.k0 / 64u) + (kk % 32u), qh);
+        const uint32_t sidx = (p.col[0] % 256u) / 16u;
+        const float sc0 = static_cast<float>(static_cast<int8_t>(blk[192u + sidx]));
+        const float sc1 = static_cast<float>(static_cast<int8_t>(blk[192u + sidx + 4u]));
+        const float d = half_bits_to_float(ld_u16(blk + 208));
+#pragma unroll
+        for (int t = 0; t < NW; ++t) {
+            const uint32_t lo = (ql[t] & 0x0f0f0f0fu) | ((qh[t] << (4u - sl)) & 0x30303030u);
+            const uint32_t hi = ((ql[t] >> 4) & 0x0f0f0f0fu) | ((qh[t] >> sl) & 0x30303030u);
+#pragma unroll
+            for (int b = 0; b < B; ++b) {
+                dot0[b] = dot4(lo, &ux.v[b][4 * t], dot0[b]);
+                dot1[b] = dot4(hi, &ux.v[b][UB + 4 * t], dot1[b]);
+            }
+        }
+        const float ds0 = d * sc0, ds1 = d * sc1;
+#pragma unroll
+        for (int b = 0; b < B; ++b) {
+            const float t0 = __builtin_fmaf(-32.0f, ux.s[b][0], dot0[b]);
+            const float t1 = __builtin_fmaf(-32.0f, ux.s[b][1], dot1[b]);
+            acc[b] += __builtin_fmaf(ds0, t0, ds1 * t1);
+        }
+    } else if constexpr (T == T_Q8_0) {
+        uint32_t q[NW];
+        ld_words_2a<NW>(blk + 2 + p.k0, q);
+        const float d = half_bits_to_float(ld_u16(blk));
+#pragma unroll
+        for (int t = 0; t < NW; ++t) {
+            const uint32_t biased = q[t] ^ 0x80808080u;  // int8 q -> q + 128
+#pragma unroll
+            for (int b = 0; b < B; ++b) dot0[b] = dot4(biased, &ux.v[b][4 * t], dot0[b]);
+        }
+#pragma unroll
+        for (int b = 0; b < B; ++b) acc[b] += d * __builtin_fmaf(-128.0f, ux.s[b][0], dot0[b]);
+    } else {  // Q4_0
+        uint32_t q[NW];
+        ld_words_2a<NW>(blk + 2 + p.k0, q);
+        const float d = half_bits_to_float(ld_u16(blk));
+#pragma unroll
+        for (int t = 0; t < NW; ++t) {
+            const uint32_t lo = q[t] & 0x0f0f0f0fu;
+            const uint32_t hi = (q[t] >> 4) & 0x0f0f0f0fu;
+#pragma unroll
+            for (int b = 0; b < B; ++b) {
+                dot0[b] = dot4(lo, &ux.v[b][4 * t], dot0[b]);
+                dot1[b] = dot4(hi, &ux.v[b][UB + 4 * t], dot1[b]);
+            }
+        }
+#pragma unroll
+        for (int b = 0; b < B; ++b) {
+            const float t0 = __builtin_fmaf(-8.0f, ux.s[b][0], dot0[b]);
+            const float t1 = __builtin_fmaf(-8.0f, ux.s[b][1], dot1[b]);
+            acc[b] += d * (t0 + t1);
+        }
+    }
+}
+
+// Sum over aligned groups of G lanes (G a power of two <= 64).
+template <int G>
+__device__ __forceinline__ float group_sum(float v) {
+#pragma unroll
+    for (int off = G / 2; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+    return v;
+}
+
+__device__ __forceinline__ float group_sum_dyn(float v, uint32_t g) {
+    for (uint32_t off = g >> 1; off >= 1; off >>= 1) v += __shfl_xor(v, static_cast<int>(off), 64);
+    return v;
+}
+
+}  // namespace pk

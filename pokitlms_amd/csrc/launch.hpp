@@ -1,0 +1,57 @@
+// launch.hpp -- host-side entry points of the HIP kernels (no torch types).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace pk {
+
+// Bytes each kernel may read past the end of a weight payload (2-byte-aligned
+// formats fetch one extra dword); every device weight buffer is padded by it.
+constexpr uint64_t kWeightTailPad = 64;
+
+// Largest hidden (input) width the register-resident matvec supports, per
+// batch size; wider rows are reported unsupported.
+bool matvec_supported(uint32_t type, uint32_t in, uint32_t batch);
+
+// y[b][r] = W[r] . x[b] for b < batch.  W: rows x row_bytes encoded GGUF rows
+// (device), x: batch x in floats (device, rows 16-byte aligned), y: batch x rows.
+hipError_t launch_matvec(uint32_t type, const uint8_t* W, uint64_t row_bytes, uint32_t rows,
+                         uint32_t in, const float* x, float* y, uint32_t batch,
+                         hipStream_t stream);
+
+// One single-token routed-MoE layer (router -> top-k -> gate/up SwiGLU ->
+// down -> weighted combine).  Device pointers throughout.
+struct MoeDecodeArgs {
+    const float* router;    // F32 [n_experts][hidden]
+    const uint8_t* gate;    // expert-major slices
+    const uint8_t* up;
+    const uint8_t* down;
+    uint32_t gate_type, up_type, down_type;
+    uint64_t gate_slice, up_slice, down_slice;     // bytes per expert
+    uint64_t gate_row, up_row, down_row;           // bytes per row
+    uint32_t hidden, ffn, n_experts, top_k;
+    uint32_t normalize;
+    float scale;
+    const float* x;          // [hidden]
+    float* y;                // [hidden] moe_result
+    uint32_t* ids;           // [top_k] route order
+    float* probs;            // [top_k]
+    // context scratch (device)
+    double* row_sum;         // [n_experts]
+    double* row_bound;       // [n_experts]
+    float* act;              // [top_k][ffn]
+    uint32_t* counter;       // 1 word, zero between calls
+    uint32_t* status;        // [4]: error flag, serial-fallback count, candidates, spare
+};
+
+bool moe_decode_supported(uint32_t gate_type, uint32_t up_type, uint32_t down_type,
+                          uint32_t hidden, uint32_t ffn, uint32_t n_experts, uint32_t top_k);
+hipError_t launch_moe_decode(const MoeDecodeArgs& a, hipStream_t stream);
+
+// Individual stages (timing and tests).
+hipError_t launch_moe_router(const MoeDecodeArgs& a, hipStream_t stream);
+hipError_t launch_moe_gate_up(const MoeDecodeArgs& a, hipStream_t stream);
+hipError_t launch_moe_down(const MoeDecodeArgs& a, hipStream_t stream);
+
+}  // namespace pk

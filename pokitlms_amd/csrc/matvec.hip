@@ -1,0 +1,282 @@
+// matvec.hip -- decode-time GGUF matrix-vector products on gfx950.
+//
+// Replaces the CPU row loop of tensor_linear (src/tensor_linear.cpp:232-263 of
+// the reference) and its per-format kernels linear_k / linear_quantized /
+// linear (src/quantized_linear.cpp:360-423, src/linear.cpp:10-31).
+//
+// Work layout: a lane owns a fixed set of units (see kquant.hpp) of every
+// row and keeps their activations in registers; a wave streams whole rows
+// (or 64/G rows at once when a row has G < 64 units) with coalesced 4..16-byte
+// loads, reduces with cross-lane shuffles, and lane 0 of the row writes y.
+// When one wave cannot hold a row's activations (large batch or wide rows),
+// S waves of the workgroup split the row's units (K-split) and combine their
+// partial sums through LDS in a fixed order.
+#include "kquant.hpp"
+#include "launch.hpp"
+
+namespace pk {
+namespace {
+
+constexpr int kMaxS = 8;  // waves per K-split group
+
+template <int T, int B, int UB, int NU>
+__global__ __launch_bounds__(64 * kMaxS) void k_matvec_q(
+    const uint8_t* __restrict__ W, uint64_t row_bytes, const float* __restrict__ x,
+    uint32_t x_stride, float* __restrict__ y, uint32_t y_stride, uint32_t rows, uint32_t units,
+    uint32_t slice_units, uint32_t S, uint32_t glog2) {
+    extern __shared__ float partial[];  // [waves][RPP][B] when S > 1
+    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+    const uint32_t waves = blockDim.x >> 6;
+    const uint32_t groups = waves / S;               // independent row streams per block
+    const uint32_t group = wave / S, slice = wave % S;
+    const uint32_t G = 1u << glog2, RPP = 64u >> glog2;
+    const uint32_t sub = lane >> glog2, ul = lane & (G - 1u);
+
+    UnitPos pos[NU];
+    bool valid[NU];
+    UnitX<T, UB, B> ux[NU];
+#pragma unroll
+    for (int k = 0; k < NU; ++k) {
+        const uint32_t local = ul + G * k;
+        const uint32_t u = slice * slice_units + local;
+        valid[k] = local < slice_units && u < units;
+        pos[k] = unit_pos<T, UB>(valid[k] ? u : 0u);
+        load_unit_x<T, UB, B>(x, x_stride, pos[k], valid[k], ux[k]);
+    }
+
+    const uint32_t passes = (rows + RPP - 1u) / RPP;
+    for (uint32_t p0 = blockIdx.x * groups; p0 < passes; p0 += gridDim.x * groups) {
+        const uint32_t p = p0 + group;
+        const uint32_t row = p * RPP + sub;
+        const bool live = p < passes && row < rows;
+        float acc[B];
+#pragma unroll
+        for (int b = 0; b < B; ++b) acc[b] = 0.0f;
+        if (live) {
+            const uint8_t* rp = W + static_cast<uint64_t>(row) * row_bytes;
+#pragma unroll
+            for (int k = 0; k < NU; ++k)
+                if (valid[k]) unit_fma<T, UB, B>(rp, pos[k], ux[k], acc);
+        }
+#pragma unroll
+        for (int b = 0; b < B; ++b) acc[b] = group_sum_dyn(acc[b], G);
+        if (S == 1) {
+            if (ul == 0 && live) {
+#pragma unroll
+                for (int b = 0; b < B; ++b) y[b * y_stride + row] = acc[b];
+            }
+        } else {
+            if (ul == 0) {
+#pragma unroll
+                for (int b = 0; b < B; ++b) partial[(wave * RPP + sub) * B + b] = acc[b];
+            }
+            __syncthreads();
+            // the group's first wave finalises (row sub, batch b) = (t / B, t % B)
+            if (slice == 0) {
+                for (uint32_t t = lane; t < RPP * B; t += 64u) {
+                    const uint32_t s_row = p * RPP + t / B;
+                    if (p < passes && s_row < rows) {
+                        float v = 0.0f;
+                        for (uint32_t s = 0; s < S; ++s)
+                            v += partial[((group * S + s) * RPP + t / B) * B + t % B];
+                        y[(t % B) * y_stride + s_row] = v;
+                    }
+                }
+            }
+            __syncthreads();
+        }
+    }
+}
+
+// F32 / F16 / BF16 rows (router-style matrices): one wave per row, lanes
+// stride the row; activations are read from memory each row.
+template <int T, int B>
+__global__ __launch_bounds__(256) void k_matvec_float(
+    const uint8_t* __restrict__ W, uint64_t row_bytes, const float* __restrict__ x,
+    uint32_t x_stride, float* __restrict__ y, uint32_t y_stride, uint32_t rows, uint32_t in) {
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t wave = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+    const uint32_t nwaves = gridDim.x * (blockDim.x >> 6);
+    for (uint32_t row = wave; row < rows; row += nwaves) {
+        const uint8_t* rp = W + static_cast<uint64_t>(row) * row_bytes;
+        float acc[B];
+#pragma unroll
+        for (int b = 0; b < B; ++b) acc[b] = 0.0f;
+        for (uint32_t i = lane; i < in; i += 64u) {
+            float w;
+            if constexpr (T == T_F32) {
+                w = reinterpret_cast<const float*>(rp)[i];
+            } else if constexpr (T == T_F16) {
+                w = half_bits_to_float(reinterpret_cast<const uint16_t*>(rp)[i]);
+            } else {
+                w = __builtin_bit_cast(float,
+                                       static_cast<uint32_t>(reinterpret_cast<const uint16_t*>(rp)[i]) << 16);
+            }
+#pragma unroll
+            for (int b = 0; b < B; ++b) acc[b] = __builtin_fmaf(w, x[b * x_stride + i], acc[b]);
+        }
+#pragma unroll
+        for (int b = 0; b < B; ++b) {
+            const float v = group_sum<64>(acc[b]);
+            if (lane == 0) y[b * y_stride + row] = v;
+        }
+    }
+}
+
+template <int T>
+constexpr int block_elems() { return Fmt<T>::BE; }
+
+// Unit bytes per lane by batch: activations held per unit are RUNS*UB*B
+// floats, kept at <= 64 by narrowing the unit as the batch grows.
+constexpr int unit_bytes_for(uint32_t batch, int maxub) {
+    return batch <= 2 ? (maxub < 16 ? maxub : 16) : (batch <= 4 ? 8 : 4);
+}
+
+constexpr uint32_t kMaxUnitsPerLane = 4;
+
+struct Plan {
+    uint32_t units, S, slice_units, glog2, nu, waves_per_block;
+};
+
+uint32_t ceil_div(uint32_t a, uint32_t b) { return (a + b - 1u) / b; }
+uint32_t log2_ceil(uint32_t v) {
+    uint32_t l = 0;
+    while ((1u << l) < v) ++l;
+    return l;
+}
+
+template <int T>
+bool plan_for(uint32_t in, uint32_t batch, int ub, Plan& p) {
+    using F = Fmt<T>;
+    if (in == 0 || in % F::BE) return false;
+    p.units = in / F::BE * (F::PRIM / ub);
+    // units one lane may hold: activation floats per unit = RUNS*ub*batch
+    const uint32_t per_unit = F::RUNS * ub * batch;
+    uint32_t nu_cap = 128u / per_unit;
+    if (nu_cap == 0) nu_cap = 1;
+    if (nu_cap > kMaxUnitsPerLane) nu_cap = kMaxUnitsPerLane;
+    p.S = ceil_div(p.units, 64u * nu_cap);
+    if (p.S > kMaxS) return false;
+    p.slice_units = ceil_div(p.units, p.S);
+    if (p.slice_units >= 64u) {
+        p.glog2 = 6;
+        p.nu = ceil_div(p.slice_units, 64u);
+    } else {
+        p.glog2 = log2_ceil(p.slice_units);
+        p.nu = 1;
+    }
+    p.waves_per_block = p.S >= 4 ? p.S : (4u / p.S) * p.S;
+    return p.nu <= kMaxUnitsPerLane;
+}
+
+template <int T, int B, int UB, int NU>
+hipError_t run_q(const Plan& pl, const uint8_t* W, uint64_t row_bytes, uint32_t rows,
+                 const float* x, uint32_t in, float* y, hipStream_t stream) {
+    const uint32_t RPP = 64u >> pl.glog2;
+    const uint32_t groups = pl.waves_per_block / pl.S;
+    const uint32_t passes = ceil_div(rows, RPP);
+    uint32_t blocks = ceil_div(passes, groups);
+    // ~8 waves per CU: enough loads in flight, and each wave reuses its
+    // register-resident activations over several rows.
+    const uint32_t max_blocks = 256u * 8u / pl.waves_per_block;
+    if (blocks > max_blocks) blocks = max_blocks;
+    const size_t lds = pl.S > 1 ? static_cast<size_t>(pl.waves_per_block) * RPP * B * sizeof(float) : 0;
+    hipLaunchKernelGGL((k_matvec_q<T, B, UB, NU>), dim3(blocks), dim3(64u * pl.waves_per_block),
+                       lds, stream, W, row_bytes, x, in, y, rows, rows, pl.units, pl.slice_units,
+                       pl.S, pl.glog2);
+    return hipGetLastError();
+}
+
+template <int T, int B, int UB>
+hipError_t dispatch_nu(const Plan& pl, const uint8_t* W, uint64_t rb, uint32_t rows,
+                       const float* x, uint32_t in, float* y, hipStream_t s) {
+    switch (pl.nu) {
+        case 1: return run_q<T, B, UB, 1>(pl, W, rb, rows, x, in, y, s);
+        case 2: return run_q<T, B, UB, 2>(pl, W, rb, rows, x, in, y, s);
+        case 3: return run_q<T, B, UB, 3>(pl, W, rb, rows, x, in, y, s);
+        default: return run_q<T, B, UB, 4>(pl, W, rb, rows, x, in, y, s);
+    }
+}
+
+template <int T, int B>
+hipError_t dispatch_q(const uint8_t* W, uint64_t rb, uint32_t rows, const float* x,
+                      uint32_t in, float* y, hipStream_t s) {
+    constexpr int UB = unit_bytes_for(B, Fmt<T>::MAXUB);
+    Plan pl;
+    if (!plan_for<T>(in, B, UB, pl)) return hipErrorInvalidValue;
+    return dispatch_nu<T, B, UB>(pl, W, rb, rows, x, in, y, s);
+}
+
+template <int T>
+hipError_t dispatch_batch_q(uint32_t batch, const uint8_t* W, uint64_t rb, uint32_t rows,
+                            const float* x, uint32_t in, float* y, hipStream_t s) {
+    switch (batch) {
+        case 1: return dispatch_q<T, 1>(W, rb, rows, x, in, y, s);
+        case 2: return dispatch_q<T, 2>(W, rb, rows, x, in, y, s);
+        case 3: return dispatch_q<T, 3>(W, rb, rows, x, in, y, s);
+        case 4: return dispatch_q<T, 4>(W, rb, rows, x, in, y, s);
+        case 5: return dispatch_q<T, 5>(W, rb, rows, x, in, y, s);
+        case 6: return dispatch_q<T, 6>(W, rb, rows, x, in, y, s);
+        case 7: return dispatch_q<T, 7>(W, rb, rows, x, in, y, s);
+        case 8: return dispatch_q<T, 8>(W, rb, rows, x, in, y, s);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+template <int T>
+hipError_t dispatch_batch_f(uint32_t batch, const uint8_t* W, uint64_t rb, uint32_t rows,
+                            const float* x, uint32_t in, float* y, hipStream_t s) {
+    uint32_t blocks = ceil_div(rows, 4u);
+    if (blocks > 2048u) blocks = 2048u;
+#define PK_F(BB)                                                                              \
+    case BB:                                                                                  \
+        hipLaunchKernelGGL((k_matvec_float<T, BB>), dim3(blocks), dim3(256), 0, s, W, rb, x, \
+                           in, y, rows, rows, in);                                            \
+        return hipGetLastError();
+    switch (batch) {
+        PK_F(1) PK_F(2) PK_F(3) PK_F(4) PK_F(5) PK_F(6) PK_F(7) PK_F(8)
+        default: return hipErrorInvalidValue;
+    }
+#undef PK_F
+}
+
+template <int T>
+bool supported_q(uint32_t in, uint32_t batch) {
+    Plan pl;
+    const int ub = batch <= 2 ? (Fmt<T>::MAXUB < 16 ? Fmt<T>::MAXUB : 16) : (batch <= 4 ? 8 : 4);
+    return plan_for<T>(in, batch, ub, pl);
+}
+
+}  // namespace
+
+bool matvec_supported(uint32_t type, uint32_t in, uint32_t batch) {
+    if (batch == 0 || batch > 8 || in == 0) return false;
+    switch (type) {
+        case T_F32: case T_F16: case T_BF16: return true;
+        case T_Q4_0: return supported_q<T_Q4_0>(in, batch);
+        case T_Q8_0: return supported_q<T_Q8_0>(in, batch);
+        case T_Q4_K: return supported_q<T_Q4_K>(in, batch);
+        case T_Q5_K: return supported_q<T_Q5_K>(in, batch);
+        case T_Q6_K: return supported_q<T_Q6_K>(in, batch);
+        default: return false;
+    }
+}
+
+hipError_t launch_matvec(uint32_t type, const uint8_t* W, uint64_t row_bytes, uint32_t rows,
+                         uint32_t in, const float* x, float* y, uint32_t batch,
+                         hipStream_t stream) {
+    if (rows == 0) return hipSuccess;
+    switch (type) {
+        case T_F32: return dispatch_batch_f<T_F32>(batch, W, row_bytes, rows, x, in, y, stream);
+        case T_F16: return dispatch_batch_f<T_F16>(batch, W, row_bytes, rows, x, in, y, stream);
+        case T_BF16: return dispatch_batch_f<T_BF16>(batch, W, row_bytes, rows, x, in, y, stream);
+        case T_Q4_0: return dispatch_batch_q<T_Q4_0>(batch, W, row_bytes, rows, x, in, y, stream);
+        case T_Q8_0: return dispatch_batch_q<T_Q8_0>(batch, W, row_bytes, rows, x, in, y, stream);
+        case T_Q4_K: return dispatch_batch_q<T_Q4_K>(batch, W, row_bytes, rows, x, in, y, stream);
+        case T_Q5_K: return dispatch_batch_q<T_Q5_K>(batch, W, row_bytes, rows, x, in, y, stream);
+        case T_Q6_K: return dispatch_batch_q<T_Q6_K>(batch, W, row_bytes, rows, x, in, y, stream);
+        default: return hipErrorInvalidValue;
+    }
+}
+
+}  // namespace pk

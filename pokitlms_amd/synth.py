@@ -1,0 +1,146 @@
+"""Seeded synthetic GGUF-compatible inputs for the routed-MoE K-quant path.
+
+Every generator returns the exact bytes a GGUF file would hold for the tensor
+(row-major ``[out, in]`` rows of encoded blocks; expert tensors ``[in, out, E]``
+with the expert index slowest), so the same buffers feed the HIP backend and
+the CPU checkers.
+
+Randomness: NumPy ``Generator(PCG64(seed))``.  Quant fields are uniform random
+bytes; every fp16 scale (``d``, ``dmin``) is ``|N(0, std)|`` rounded to
+binary16; activations are ``N(0, 1)`` float32; the F32 router is
+``N(0, 0.02)``.  Block layouts follow the reference decoders
+(src/quantized_linear.cpp:166-205, 286-358, 387-423 of the reference).
+"""
+from __future__ import annotations
+
+import hashlib
+
+import numpy as np
+
+F32, F16, Q4_0, Q8_0, Q4_K, Q5_K, Q6_K, BF16 = 0, 1, 2, 8, 12, 13, 14, 30
+
+TYPE_NAMES = {F32: "F32", F16: "F16", Q4_0: "Q4_0", Q8_0: "Q8_0", Q4_K: "Q4_K",
+              Q5_K: "Q5_K", Q6_K: "Q6_K", BF16: "BF16"}
+BLOCK_ELEMENTS = {F32: 1, F16: 1, BF16: 1, Q4_0: 32, Q8_0: 32, Q4_K: 256, Q5_K: 256, Q6_K: 256}
+BLOCK_BYTES = {F32: 4, F16: 2, BF16: 2, Q4_0: 18, Q8_0: 34, Q4_K: 144, Q5_K: 176, Q6_K: 210}
+# Byte offsets of the fp16 scale fields inside one block.
+SCALE_OFFSETS = {Q4_0: (0,), Q8_0: (0,), Q4_K: (0, 2), Q5_K: (0, 2), Q6_K: (208,)}
+
+
+def rng(seed: int) -> np.random.Generator:
+    return np.random.Generator(np.random.PCG64(seed))
+
+
+def row_bytes(gtype: int, in_features: int) -> int:
+    be = BLOCK_ELEMENTS[gtype]
+    if in_features % be:
+        raise ValueError(f"{TYPE_NAMES[gtype]} rows need a multiple of {be} elements")
+    return in_features // be * BLOCK_BYTES[gtype]
+
+
+def matrix_bytes(gtype: int, in_features: int, rows: int) -> int:
+    return rows * row_bytes(gtype, in_features)
+
+
+def half_abs_normal(gen: np.random.Generator, n: int, std: float) -> np.ndarray:
+    """``n`` binary16 bit patterns of |N(0, std)| (round to nearest even)."""
+    return np.abs(gen.standard_normal(n) * std).astype(np.float16).view(np.uint16)
+
+
+def normal_f32(gen: np.random.Generator, n: int, std: float = 1.0) -> np.ndarray:
+    return (gen.standard_normal(n) * std).astype(np.float32)
+
+
+def quant_matrix(gtype: int, rows: int, in_features: int, gen: np.random.Generator,
+                 scale_std: float = 0.02) -> np.ndarray:
+    """Encoded weights, uint8 of shape ``(rows, row_bytes)``.
+
+    Float types are N(0, scale_std) values in that storage type.
+    """
+    if gtype == F32:
+        return normal_f32(gen, rows * in_features, scale_std).view(np.uint8).reshape(rows, -1)
+    if gtype == F16:
+        vals = (gen.standard_normal(rows * in_features) * scale_std).astype(np.float16)
+        return vals.view(np.uint8).reshape(rows, -1)
+    if gtype == BF16:
+        vals = normal_f32(gen, rows * in_features, scale_std).view(np.uint32)
+        return (vals >> 16).astype(np.uint16).view(np.uint8).reshape(rows, -1)
+    bb = BLOCK_BYTES[gtype]
+    nblocks = rows * (in_features // BLOCK_ELEMENTS[gtype])
+    row_bytes(gtype, in_features)  # validates divisibility
+    blocks = gen.integers(0, 256, size=(nblocks, bb), dtype=np.uint8)
+    for off in SCALE_OFFSETS[gtype]:
+        blocks[:, off:off + 2] = half_abs_normal(gen, nblocks, scale_std).view(np.uint8).reshape(-1, 2)
+    return blocks.reshape(rows, -1)
+
+
+def digest(*arrays: np.ndarray) -> str:
+    h = hashlib.sha256()
+    for a in arrays:
+        h.update(np.ascontiguousarray(a).view(np.uint8).tobytes())
+    return h.hexdigest()
+
+
+class MoeLayer:
+    """One Qwen3-MoE MoE layer's routed weights (host copies).
+
+    router: float32 ``(experts, hidden)``; gate/up: ``experts`` slices of a
+    ``hidden -> ffn`` matrix; down: ``experts`` slices of ``ffn -> hidden``.
+    The expert tensors are uint8 ``(experts, slice_bytes)``, i.e. the GGUF
+    ``[in, out, E]`` payload with expert ``e`` at byte ``e * slice_bytes``.
+    """
+
+    def __init__(self, router, gate, up, down, hidden, experts, ffn,
+                 gate_type=Q4_K, up_type=Q4_K, down_type=Q6_K, top_k=8, normalize=True):
+        self.router = router
+        self.gate, self.up, self.down = gate, up, down
+        self.hidden, self.experts, self.ffn = hidden, experts, ffn
+        self.gate_type, self.up_type, self.down_type = gate_type, up_type, down_type
+        self.top_k, self.normalize = top_k, normalize
+
+    def routed_bytes(self) -> int:
+        """Algorithmic bytes of one single-token pass: router + top_k experts."""
+        per_expert = self.gate.shape[1] + self.up.shape[1] + self.down.shape[1]
+        return self.router.nbytes + self.top_k * per_expert
+
+
+def moe_layer(seed: int, hidden: int = 2048, experts: int = 128, ffn: int = 768,
+              gate_type: int = Q4_K, up_type: int = Q4_K, down_type: int = Q6_K,
+              top_k: int = 8, normalize: bool = True, router_std: float = 0.02) -> MoeLayer:
+    gen = rng(seed)
+    router = normal_f32(gen, experts * hidden, router_std).reshape(experts, hidden)
+    gate = quant_matrix(gate_type, experts * ffn, hidden, gen).reshape(experts, -1)
+    up = quant_matrix(up_type, experts * ffn, hidden, gen).reshape(experts, -1)
+    down = quant_matrix(down_type, experts * hidden, ffn, gen).reshape(experts, -1)
+    return MoeLayer(router, gate, up, down, hidden, experts, ffn, gate_type, up_type,
+                    down_type, top_k, normalize)
+
+
+def dyadic_matrix(gtype: int, rows: int, in_features: int, gen: np.random.Generator) -> np.ndarray:
+    """Random quant fields with power-of-two scales (2^-4 or 2^-3).
+
+    Sub-block scales are kept small (K-quant 6-bit fields <= 15, Q6_K int8
+    scales in [-8, 7]).  With dyadic activations (``dyadic_vector``) every
+    decoded weight, product and partial sum is then a multiple of 2^-8; as
+    long as sum |w*x| of a row stays below 2^16 (checked by the tests) every
+    partial sum is exact in FP32, so every summation order gives the same
+    bits and GPU and CPU results can be compared bit for bit.
+    """
+    m = quant_matrix(gtype, rows, in_features, gen)
+    if gtype in (F32, F16, BF16):
+        return m
+    blocks = m.reshape(-1, BLOCK_BYTES[gtype])
+    for off in SCALE_OFFSETS[gtype]:
+        exps = gen.integers(-4, -2, size=blocks.shape[0])
+        blocks[:, off:off + 2] = np.ldexp(1.0, exps).astype(np.float16).view(np.uint8).reshape(-1, 2)
+    if gtype == Q6_K:
+        blocks[:, 192:208] = (gen.integers(-8, 8, size=(blocks.shape[0], 16))
+                              .astype(np.int8).view(np.uint8))
+    if gtype in (Q4_K, Q5_K):
+        blocks[:, 4:16] &= 0x0F
+    return m
+
+
+def dyadic_vector(gen: np.random.Generator, n: int) -> np.ndarray:
+    """Activations k/16 with k in [-16, 16]."""
+    return (gen.integers(-16, 17, size=n).astype(np.float32) / 16.0).astype(np.float32)

@@ -1,0 +1,292 @@
+"""GPU parity: libpokit_hip.so (through its C ABI) against the CPU oracle.
+
+Bars: expert ids and routing order bit-exact; FP32
+outputs within normwise relative error max|gpu-cpu| / max|cpu| <= 1e-4; on
+dyadic-exact inputs every output bit-exact.  The reference's own Vulkan
+harness tolerance |cpu-gpu| <= 1e-3 + 2e-5|cpu| (tests/vulkan_linear_cases.hpp:81)
+is checked as well on its 37 x 512 shapes.
+"""
+import numpy as np
+import pytest
+
+from pokitlms_amd import synth as S
+from tests.conftest import normwise_rel
+from tests.golden import make_golden as G
+
+pytestmark = pytest.mark.gpu
+
+QUANT = (S.Q4_0, S.Q8_0, S.Q4_K, S.Q5_K, S.Q6_K)
+FLOAT = (S.F32, S.F16, S.BF16)
+TOL = 1e-4
+
+
+def bits(a):
+    return np.asarray(a, np.float32).view(np.uint32)
+
+
+def say(*a):
+    print(*a, flush=True)
+
+
+# ---- matvec -------------------------------------------------------------------------
+
+@pytest.mark.parametrize("gtype", FLOAT + QUANT)
+def test_reference_harness_shapes(hip, port, gtype):
+    """37 rows x 512 (257 for floats) of xorshift-style random bytes with the
+    harness's fixed scales, three rounds with x *= -0.75
+    (tests/vulkan_linear_cases.hpp:31-88)."""
+    say("harness", S.TYPE_NAMES[gtype])
+    w, x, inn = G.small_inputs(gtype, seed=123)
+    if gtype in QUANT:
+        blocks = w.reshape(-1, S.BLOCK_BYTES[gtype])
+        for off in S.SCALE_OFFSETS[gtype]:
+            val = 0x2800 if off in (0, 208) else 0x2400
+            blocks[:, off] = val & 0xFF
+            blocks[:, off + 1] = val >> 8
+    wt = hip.upload(gtype, inn, 37, w)
+    for _ in range(3):
+        cpu = port.linear(gtype, w, inn, 37, x)
+        gpu = hip.matvec(wt, x)
+        assert np.all(np.isfinite(gpu))
+        assert np.all(np.abs(cpu - gpu) <= 1e-3 + 2e-5 * np.abs(cpu))
+        assert normwise_rel(gpu, cpu) <= TOL
+        x = (x * np.float32(-0.75)).astype(np.float32)
+    wt.release()
+
+
+@pytest.mark.parametrize("gtype", QUANT)
+@pytest.mark.parametrize("batch", (1, 4, 8))
+def test_dyadic_bit_exact(hip, port, gtype, batch):
+    say("dyadic", S.TYPE_NAMES[gtype], batch)
+    g = S.rng(500 + gtype * 10 + batch)
+    rows, inn = 96, 2048
+    w = S.dyadic_matrix(gtype, rows, inn, g)
+    xs = np.stack([S.dyadic_vector(g, inn) for _ in range(batch)])
+    wt = hip.upload(gtype, inn, rows, w)
+    gpu = hip.matvec(wt, xs)
+    for b in range(batch):
+        cpu = port.linear(gtype, w, inn, rows, xs[b])
+        assert np.array_equal(bits(gpu[b]), bits(cpu)), (S.TYPE_NAMES[gtype], batch, b)
+    wt.release()
+
+
+def test_c1_q4k_4096(hip, golden):
+    say("c1")
+    w, x = G.c1_inputs()
+    wt = hip.upload(S.Q4_K, 4096, 4096, w)
+    gpu = hip.matvec(wt, x)
+    err = normwise_rel(gpu, golden["c1_y"])
+    say("c1 normwise", err)
+    assert err <= TOL
+    wt.release()
+
+
+@pytest.mark.parametrize("gtype", QUANT)
+@pytest.mark.parametrize("shape", G.C2_SHAPES)
+def test_c2_sweep(hip, port, golden, gtype, shape):
+    rows, inn = shape
+    say("c2", S.TYPE_NAMES[gtype], rows, inn)
+    w, xs = G.c2_inputs(gtype, rows, inn)
+    key = f"c2_{S.TYPE_NAMES[gtype]}_{rows}x{inn}"
+    wt = hip.upload(gtype, inn, rows, w)
+    cpu = np.stack([port.linear(gtype, w, inn, rows, xs[b]) for b in range(8)])
+    assert np.array_equal(bits(cpu[0]), bits(golden[key + "_y0"]))
+    for batch in (1, 4, 8):
+        gpu = hip.matvec(wt, xs[:batch])
+        for b in range(batch):
+            err = normwise_rel(gpu[b], cpu[b])
+            assert err <= TOL, (batch, b, err)
+    wt.release()
+
+
+@pytest.mark.parametrize("batch", (2, 3, 5, 6, 7))
+def test_odd_batches(hip, port, batch):
+    g = S.rng(40 + batch)
+    w = S.quant_matrix(S.Q6_K, 300, 1536, g)
+    xs = S.normal_f32(g, batch * 1536).reshape(batch, 1536)
+    wt = hip.upload(S.Q6_K, 1536, 300, w)
+    gpu = hip.matvec(wt, xs)
+    for b in range(batch):
+        assert normwise_rel(gpu[b], port.linear(S.Q6_K, w, 1536, 300, xs[b])) <= TOL
+    wt.release()
+
+
+def test_expert_slice_matvec(hip, port):
+    layer = S.moe_layer(seed=21, hidden=512, experts=4, ffn=256)
+    g = hip.upload(layer.gate_type, 512, 256, layer.gate, n_experts=4)
+    d = hip.upload(layer.down_type, 256, 512, layer.down, n_experts=4)
+    x = S.normal_f32(S.rng(22), 512)
+    a = S.normal_f32(S.rng(23), 256)
+    for e in range(4):
+        assert normwise_rel(hip.matvec(g, x, expert=e),
+                            port.linear(layer.gate_type, layer.gate[e], 512, 256, x)) <= TOL
+        assert normwise_rel(hip.matvec(d, a, expert=e),
+                            port.linear(layer.down_type, layer.down[e], 256, 512, a)) <= TOL
+    with pytest.raises(ValueError):
+        hip.matvec(g, x, expert=4)
+    g.release()
+    d.release()
+
+
+def test_try_linear_contract(hip, port):
+    from pokitlms_amd.backend import TensorView
+    g = S.rng(31)
+    w = S.quant_matrix(S.Q4_K, 64, 512, g)
+    x = S.normal_f32(g, 512)
+    y = np.zeros(64, np.float32)
+    assert hip.try_linear(TensorView(S.Q4_K, (512, 64), w), x, y)
+    assert normwise_rel(y, port.linear(S.Q4_K, w, 512, 64, x)) <= TOL
+    # Q2_K (10) has no kernel: False, so the caller runs its CPU path
+    assert not hip.try_linear(TensorView(10, (512, 64), np.zeros(64 * 168, np.uint8)), x, y)
+    with pytest.raises(ValueError):
+        hip.try_linear(TensorView(S.Q4_K, (512, 64), w), x[:256], y)
+
+
+# ---- MoE layer ------------------------------------------------------------------------
+
+@pytest.fixture(scope="module")
+def c3(hip):
+    layer = G.c3_layer()
+    handles = hip.upload_moe_layer(layer)
+    yield layer, handles
+    handles.release()
+
+
+def test_c3_moe_decode_golden(hip, port, golden, c3):
+    layer, h = c3
+    toks = G.c3_tokens()
+    blk = port.moe(layer)
+    worst = 0.0
+    for t in range(toks.shape[0]):
+        y, ids, probs = hip.moe_decode(h, toks[t])
+        assert np.array_equal(ids, golden["c3_ids"][t]), (t, ids, golden["c3_ids"][t])
+        assert np.max(np.abs(probs - golden["c3_probs"][t])) <= TOL * np.max(golden["c3_probs"][t])
+        cpu = golden["c3_y"][t] if t < 4 else blk.forward(toks[t])[0]
+        worst = max(worst, normwise_rel(y, cpu))
+    say("c3 worst normwise", worst)
+    assert worst <= TOL
+
+
+def test_moe_decode_deterministic(hip, c3):
+    _, h = c3
+    x = G.c3_tokens(2)[1]
+    y0, i0, p0 = hip.moe_decode(h, x)
+    for _ in range(3):
+        y1, i1, p1 = hip.moe_decode(h, x)
+        assert np.array_equal(bits(y0), bits(y1)) and np.array_equal(i0, i1)
+        assert np.array_equal(bits(p0), bits(p1))
+
+
+def _small_layer(seed, router=None, experts=32, hidden=512, ffn=256, top_k=4, normalize=True):
+    layer = S.moe_layer(seed=seed, hidden=hidden, experts=experts, ffn=ffn, top_k=top_k,
+                        normalize=normalize)
+    if router is not None:
+        layer.router = np.ascontiguousarray(router, np.float32)
+    return layer
+
+
+def test_router_ties_break_by_id(hip, port):
+    """All-zero router (the reference's smoke models): every logit ties, so
+    the routes are experts 0..k-1 with equal weights."""
+    layer = _small_layer(50, router=np.zeros((32, 512), np.float32))
+    h = hip.upload_moe_layer(layer)
+    x = S.normal_f32(S.rng(51), 512)
+    y, ids, probs = hip.moe_decode(h, x)
+    cy, cids, cprobs = port.moe(layer).forward(x)
+    assert np.array_equal(ids, np.arange(4)) and np.array_equal(ids, cids)
+    assert np.array_equal(bits(probs), bits(cprobs))
+    assert normwise_rel(y, cy) <= TOL
+    h.release()
+
+
+def test_router_near_ties_take_the_exact_path(hip, port):
+    """Rows that differ by one ulp in one weight, and exact duplicates: the
+    certified ranking cannot separate them, so the exact serial logits decide.
+    The ids must still equal the CPU's on every token."""
+    g = S.rng(60)
+    router = S.normal_f32(g, 32 * 512, 0.02).reshape(32, 512)
+    for j in range(0, 32, 2):
+        router[j + 1] = router[j]
+        k = int(g.integers(0, 512))
+        router[j + 1, k] = np.nextafter(router[j, k], np.float32(1))
+    layer = _small_layer(61, router=router, top_k=8)
+    h = hip.upload_moe_layer(layer)
+    blk = port.moe(layer)
+    hip.reset_stats()
+    for t in range(24):
+        x = S.normal_f32(g, 512)
+        y, ids, probs = hip.moe_decode(h, x)
+        cy, cids, cprobs = blk.forward(x)
+        assert np.array_equal(ids, cids), (t, ids, cids)
+        assert np.max(np.abs(probs - cprobs)) <= TOL * np.max(cprobs)
+        assert normwise_rel(y, cy) <= TOL
+    st = hip.stats()
+    say("near-tie fallbacks", st["router_fallbacks"], "candidates", st["router_candidates"])
+    assert st["router_fallbacks"] > 0
+    h.release()
+
+
+@pytest.mark.parametrize("normalize", (True, False))
+def test_moe_shapes_and_normalisation(hip, port, normalize):
+    for (hidden, experts, ffn, k, gt, dt) in ((512, 16, 256, 2, S.Q4_K, S.Q6_K),
+                                             (1024, 64, 512, 8, S.Q5_K, S.Q8_0),
+                                             (2048, 128, 768, 8, S.Q4_0, S.Q4_K)):
+        layer = S.moe_layer(seed=70 + hidden, hidden=hidden, experts=experts, ffn=ffn,
+                            gate_type=gt, up_type=gt, down_type=dt, top_k=k,
+                            normalize=normalize)
+        h = hip.upload_moe_layer(layer)
+        blk = port.moe(layer)
+        for t in range(4):
+            x = S.normal_f32(S.rng(700 + t), hidden)
+            y, ids, probs = hip.moe_decode(h, x)
+            cy, cids, cprobs = blk.forward(x)
+            assert np.array_equal(ids, cids)
+            assert np.max(np.abs(probs - cprobs)) <= TOL * np.max(cprobs)
+            assert normwise_rel(y, cy) <= TOL
+        h.release()
+
+
+def test_non_finite_router_is_a_runtime_error(hip, port):
+    from pokitlms_amd.backend import HipError
+    router = S.normal_f32(S.rng(80), 32 * 512, 0.02).reshape(32, 512)
+    router[5, 7] = np.inf
+    layer = _small_layer(81, router=router)
+    h = hip.upload_moe_layer(layer)
+    with pytest.raises(HipError) as ex:
+        hip.moe_decode(h, S.normal_f32(S.rng(82), 512))
+    assert ex.value.status == 2 and "non-finite" in str(ex.value)
+    h.release()
+    # the context stays usable: routing errors are data errors, not device failures
+    good = hip.upload_moe_layer(_small_layer(83))
+    x = S.normal_f32(S.rng(84), 512)
+    y, ids, _ = hip.moe_decode(good, x)
+    assert np.array_equal(ids, port.moe(_small_layer(83)).forward(x)[1])
+    good.release()
+
+
+def test_async_device_buffers_match_sync(hip, c3):
+    import torch
+    _, h = c3
+    x = G.c3_tokens(3)[2]
+    y_ref, ids_ref, p_ref = hip.moe_decode(h, x)
+    dev = torch.device("cuda:0")
+    dx = torch.from_numpy(x).to(dev)
+    dy = torch.empty(2048, dtype=torch.float32, device=dev)
+    di = torch.empty(8, dtype=torch.int32, device=dev)
+    dp = torch.empty(8, dtype=torch.float32, device=dev)
+    stream = torch.cuda.current_stream().cuda_stream
+    hip.moe_decode_async(h, dx.data_ptr(), dy.data_ptr(), di.data_ptr(), dp.data_ptr(), stream)
+    hip.sync(stream)
+    assert np.array_equal(bits(dy.cpu().numpy()), bits(y_ref))
+    assert np.array_equal(di.cpu().numpy().astype(np.uint32), ids_ref)
+    assert np.array_equal(bits(dp.cpu().numpy()), bits(p_ref))
+
+
+def test_stats_track_resident_experts(hip, c3):
+    _, h = c3
+    hip.reset_stats()
+    hip.moe_decode(h, G.c3_tokens(1)[0])
+    st = hip.stats()
+    assert st["moe_decode_calls"] == 1 and st["expert_hits"] == 8 and st["expert_misses"] == 0
+    assert st["weight_bytes"] == h.routed_bytes() == 25_526_272
+    assert st["resident_bytes"] >= h.router.nbytes + h.gate.nbytes + h.up.nbytes + h.down.nbytes
