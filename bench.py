@@ -158,8 +158,11 @@ def main():
         for i in range(args.warmup):
             step(i, s)
         hip.sync(s)
-        # eager reference outputs for the graph check
-        for i in range(args.tokens):
+        if not bool(torch.isfinite(Y).all()):
+            raise RuntimeError("non-finite MoE output in warm-up")
+        # eager reference for the graph check: the same `steps` steps, so every
+        # output slot holds the result of the same final step
+        for i in range(args.steps):
             step(i, s)
         hip.sync(s)
         y_eager, ids_eager = Y.clone(), IDS.clone()
@@ -210,8 +213,13 @@ def main():
         wall = time.perf_counter() - t0
         gpu_ms = ev0.elapsed_time(ev1)
         hip.sync(stream.cuda_stream)
+    graph_diag = None
     if not args.eager:
         ok_graph = ok_graph and bool(torch.equal(Y, y_eager) and torch.equal(IDS, ids_eager))
+        bad_y = (Y != y_eager).any(dim=1)
+        bad_i = (IDS != ids_eager).any(dim=1)
+        graph_diag = {"slots_y_differ": int(bad_y.sum()), "slots_ids_differ": int(bad_i.sum()),
+                      "max_abs_diff": float((Y - y_eager).abs().max())}
     ms_per_step = gpu_ms / args.steps
     value = step_bytes * args.steps / (gpu_ms / 1e3) / 1e9
 
@@ -286,6 +294,7 @@ def main():
         "kernels": kernels,
         "router_fallbacks_per_1k": round(1000.0 * st["router_fallbacks"] / n_timed, 2),
         "graph_matches_eager": None if args.eager else ok_graph,
+        "graph_check": graph_diag,
         "parity": parity,
         "cpu_baseline": cpu,
     }

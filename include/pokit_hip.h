@@ -97,7 +97,9 @@ pk_hip_status pk_hip_upload(pk_hip_ctx* ctx, uint32_t ggml_type, uint64_t in, ui
                             pk_hip_weight** out_weight, char* error_buffer,
                             size_t error_capacity);
 
-/* As pk_hip_upload, from device memory the caller owns (device-to-device copy). */
+/* As pk_hip_upload, from device memory the caller owns (device-to-device
+ * copy).  The copy starts after all earlier work on the device has finished,
+ * so a source still being written on another stream is complete. */
 pk_hip_status pk_hip_upload_device(pk_hip_ctx* ctx, uint32_t ggml_type, uint64_t in,
                                    uint64_t out, uint32_t n_experts, const void* device_bytes,
                                    uint64_t nbytes, pk_hip_weight** out_weight,

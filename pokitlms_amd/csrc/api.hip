@@ -413,6 +413,10 @@ static pk_hip_status upload_impl(pk_hip_ctx* ctx, uint32_t type, uint64_t in, ui
         require_usable(ctx);
         std::lock_guard lock(ctx->mutex);
         pk_hip_weight* w = make_weight(ctx, type, in, out, n_experts, nbytes);
+        // Device sources may still be in production on another stream (the
+        // caller's generator or loader): uploads are rare, so wait for all
+        // earlier work on the device before copying.
+        if (kind == hipMemcpyDeviceToDevice) check(hipDeviceSynchronize(), "hipDeviceSynchronize");
         const hipError_t e = hipMemcpyAsync(w->dptr, src, nbytes, kind, ctx->stream);
         const hipError_t s = e == hipSuccess ? hipStreamSynchronize(ctx->stream) : e;
         if (s != hipSuccess) {

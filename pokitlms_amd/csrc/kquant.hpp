@@ -164,32 +164,78 @@ __device__ __forceinline__ void load_unit_x(const float* x, uint32_t x_stride, c
 }
 
 // ---------------------------------------------------------------------------
-// acc[b] += (this unit of the row starting at `row`) . x[b]
+// Unit decode in two phases, so a wave can issue the loads of several rows
+// before it consumes any of them.
 
-template <int T, int UB, int B>
-__device__ __forceinline__ void unit_fma(const uint8_t* __restrict__ row, const UnitPos& p,
-                                         const UnitX<T, UB, B>& ux, float (&acc)[B]) {
+template <int T, int UB>
+struct UnitRaw {
+    static constexpr int NW = UB / 4;
+    // Q4_K/Q5_K: h = 16-byte block header; q = quants; qh = Q5_K fifth bits.
+    // Q6_K/Q8_0/Q4_0: q/qh hold NW+1 dword-aligned words re-aligned at use.
+    uint32_t h[(T == T_Q4_K || T == T_Q5_K) ? 4 : 1];
+    uint32_t q[NW + 1];
+    uint32_t qh[(T == T_Q5_K || T == T_Q6_K) ? NW + 1 : 1];
+    uint32_t shift;  // byte misalignment (0 or 2) of the 2-byte-aligned formats
+    int32_t s0, s1;  // Q6_K int8 sub-block scales
+    uint32_t d;      // fp16 bits of d (Q6_K, Q8_0, Q4_0)
+};
+
+template <int T, int UB>
+__device__ __forceinline__ void unit_load(const uint8_t* __restrict__ row, const UnitPos& p,
+                                          UnitRaw<T, UB>& r) {
     constexpr int NW = UB / 4;
     const uint8_t* blk = row + p.boff;
+    if constexpr (T == T_Q4_K || T == T_Q5_K) {
+        ld_words<4>(blk, r.h);
+        uint32_t q[NW];
+        ld_words<NW>(blk + (T == T_Q4_K ? 16 : 48) + p.k0, q);
+#pragma unroll
+        for (int i = 0; i < NW; ++i) r.q[i] = q[i];
+        if constexpr (T == T_Q5_K) {
+            uint32_t qh[NW];
+            ld_words<NW>(blk + 16 + (p.k0 % 32u), qh);
+#pragma unroll
+            for (int i = 0; i < NW; ++i) r.qh[i] = qh[i];
+        }
+    } else {
+        const uint8_t* qp = T == T_Q6_K ? blk + p.k0 : blk + 2 + p.k0;
+        const uintptr_t a = reinterpret_cast<uintptr_t>(qp);
+        r.shift = static_cast<uint32_t>(a & 3u);
+        ld_words<NW + 1>(reinterpret_cast<const uint8_t*>(a & ~uintptr_t{3}), r.q);
+        if constexpr (T == T_Q6_K) {
+            const uint32_t kk = p.k0 % 64u;
+            const uint8_t* hp = blk + 128u + 32u * (p.k0 / 64u) + (kk % 32u);
+            // qh and ql share the block's alignment (both offsets are even)
+            ld_words<NW + 1>(reinterpret_cast<const uint8_t*>(
+                                 reinterpret_cast<uintptr_t>(hp) & ~uintptr_t{3}),
+                             r.qh);
+            const uint32_t sidx = (p.col[0] % 256u) / 16u;
+            r.s0 = static_cast<int8_t>(blk[192u + sidx]);
+            r.s1 = static_cast<int8_t>(blk[192u + sidx + 4u]);
+            r.d = ld_u16(blk + 208);
+        } else {
+            r.d = ld_u16(blk);
+        }
+    }
+}
+
+template <int T, int UB, int B>
+__device__ __forceinline__ void unit_compute(const UnitRaw<T, UB>& r, const UnitPos& p,
+                                             const UnitX<T, UB, B>& ux, float (&acc)[B]) {
+    constexpr int NW = UB / 4;
     float dot0[B], dot1[B];
 #pragma unroll
     for (int b = 0; b < B; ++b) dot0[b] = dot1[b] = 0.0f;
 
     if constexpr (T == T_Q4_K || T == T_Q5_K) {
-        uint32_t h[4];
-        ld_words<4>(blk, h);
-        uint32_t q[NW];
-        ld_words<NW>(blk + (T == T_Q4_K ? 16 : 48) + p.k0, q);
-        uint32_t qh[NW];
         const uint32_t c = p.k0 / 32u;
-        if constexpr (T == T_Q5_K) ld_words<NW>(blk + 16 + (p.k0 % 32u), qh);
 #pragma unroll
         for (int t = 0; t < NW; ++t) {
-            uint32_t lo = q[t] & 0x0f0f0f0fu;
-            uint32_t hi = (q[t] >> 4) & 0x0f0f0f0fu;
+            uint32_t lo = r.q[t] & 0x0f0f0f0fu;
+            uint32_t hi = (r.q[t] >> 4) & 0x0f0f0f0fu;
             if constexpr (T == T_Q5_K) {
-                lo |= ((qh[t] >> (2u * c)) & 0x01010101u) << 4;
-                hi |= ((qh[t] >> (2u * c + 1u)) & 0x01010101u) << 4;
+                lo |= ((r.qh[t] >> (2u * c)) & 0x01010101u) << 4;
+                hi |= ((r.qh[t] >> (2u * c + 1u)) & 0x01010101u) << 4;
             }
 #pragma unroll
             for (int b = 0; b < B; ++b) {
@@ -197,39 +243,34 @@ __device__ __forceinline__ void unit_fma(const uint8_t* __restrict__ row, const 
                 dot1[b] = dot4(hi, &ux.v[b][UB + 4 * t], dot1[b]);
             }
         }
-        const float d = half_bits_to_float(h[0] & 0xffffu);
-        const float dmin = half_bits_to_float(h[0] >> 16);
+        const float d = half_bits_to_float(r.h[0] & 0xffffu);
+        const float dmin = half_bits_to_float(r.h[0] >> 16);
         float s0, m0, s1, m1;
-        kq_scale_min(h, 2u * c, s0, m0);
-        kq_scale_min(h, 2u * c + 1u, s1, m1);
+        kq_scale_min(r.h, 2u * c, s0, m0);
+        kq_scale_min(r.h, 2u * c + 1u, s1, m1);
         const float ds0 = d * s0, dm0 = dmin * m0, ds1 = d * s1, dm1 = dmin * m1;
 #pragma unroll
         for (int b = 0; b < B; ++b) {
-            float t0 = __builtin_fmaf(ds0, dot0[b], -dm0 * ux.s[b][0]);
-            float t1 = __builtin_fmaf(ds1, dot1[b], -dm1 * ux.s[b][1]);
+            const float t0 = __builtin_fmaf(ds0, dot0[b], -dm0 * ux.s[b][0]);
+            const float t1 = __builtin_fmaf(ds1, dot1[b], -dm1 * ux.s[b][1]);
             acc[b] += t0 + t1;
         }
     } else if constexpr (T == T_Q6_K) {
-        const uint32_t kk = p.k0 % 64u;
-        const uint32_t sl = kk >= 32u ? 2u : 0u;
-        uint32_t ql[NW], qh[NW];
-        ld_words_2a<NW>(blk + p.k0, ql);
-        ld_words_2a<NW>(blk + 128u + 32u * (p.k0 / 64u) + (kk % 32u), qh);
-        const uint32_t sidx = (p.col[0] % 256u) / 16u;
-        const float sc0 = static_cast<float>(static_cast<int8_t>(blk[192u + sidx]));
-        const float sc1 = static_cast<float>(static_cast<int8_t>(blk[192u + sidx + 4u]));
-        const float d = half_bits_to_float(ld_u16(blk + 208));
+        const uint32_t sl = (p.k0 % 64u) >= 32u ? 2u : 0u;
 #pragma unroll
         for (int t = 0; t < NW; ++t) {
-            const uint32_t lo = (ql[t] & 0x0f0f0f0fu) | ((qh[t] << (4u - sl)) & 0x30303030u);
-            const uint32_t hi = ((ql[t] >> 4) & 0x0f0f0f0fu) | ((qh[t] >> sl) & 0x30303030u);
+            const uint32_t ql = __builtin_amdgcn_alignbyte(r.q[t + 1], r.q[t], r.shift);
+            const uint32_t qh = __builtin_amdgcn_alignbyte(r.qh[t + 1], r.qh[t], r.shift);
+            const uint32_t lo = (ql & 0x0f0f0f0fu) | ((qh << (4u - sl)) & 0x30303030u);
+            const uint32_t hi = ((ql >> 4) & 0x0f0f0f0fu) | ((qh >> sl) & 0x30303030u);
 #pragma unroll
             for (int b = 0; b < B; ++b) {
                 dot0[b] = dot4(lo, &ux.v[b][4 * t], dot0[b]);
                 dot1[b] = dot4(hi, &ux.v[b][UB + 4 * t], dot1[b]);
             }
         }
-        const float ds0 = d * sc0, ds1 = d * sc1;
+        const float d = half_bits_to_float(r.d);
+        const float ds0 = d * static_cast<float>(r.s0), ds1 = d * static_cast<float>(r.s1);
 #pragma unroll
         for (int b = 0; b < B; ++b) {
             const float t0 = __builtin_fmaf(-32.0f, ux.s[b][0], dot0[b]);
@@ -237,31 +278,29 @@ __device__ __forceinline__ void unit_fma(const uint8_t* __restrict__ row, const 
             acc[b] += __builtin_fmaf(ds0, t0, ds1 * t1);
         }
     } else if constexpr (T == T_Q8_0) {
-        uint32_t q[NW];
-        ld_words_2a<NW>(blk + 2 + p.k0, q);
-        const float d = half_bits_to_float(ld_u16(blk));
 #pragma unroll
         for (int t = 0; t < NW; ++t) {
-            const uint32_t biased = q[t] ^ 0x80808080u;  // int8 q -> q + 128
+            const uint32_t q = __builtin_amdgcn_alignbyte(r.q[t + 1], r.q[t], r.shift);
+            const uint32_t biased = q ^ 0x80808080u;  // int8 q -> q + 128
 #pragma unroll
             for (int b = 0; b < B; ++b) dot0[b] = dot4(biased, &ux.v[b][4 * t], dot0[b]);
         }
+        const float d = half_bits_to_float(r.d);
 #pragma unroll
         for (int b = 0; b < B; ++b) acc[b] += d * __builtin_fmaf(-128.0f, ux.s[b][0], dot0[b]);
     } else {  // Q4_0
-        uint32_t q[NW];
-        ld_words_2a<NW>(blk + 2 + p.k0, q);
-        const float d = half_bits_to_float(ld_u16(blk));
 #pragma unroll
         for (int t = 0; t < NW; ++t) {
-            const uint32_t lo = q[t] & 0x0f0f0f0fu;
-            const uint32_t hi = (q[t] >> 4) & 0x0f0f0f0fu;
+            const uint32_t q = __builtin_amdgcn_alignbyte(r.q[t + 1], r.q[t], r.shift);
+            const uint32_t lo = q & 0x0f0f0f0fu;
+            const uint32_t hi = (q >> 4) & 0x0f0f0f0fu;
 #pragma unroll
             for (int b = 0; b < B; ++b) {
                 dot0[b] = dot4(lo, &ux.v[b][4 * t], dot0[b]);
                 dot1[b] = dot4(hi, &ux.v[b][UB + 4 * t], dot1[b]);
             }
         }
+        const float d = half_bits_to_float(r.d);
 #pragma unroll
         for (int b = 0; b < B; ++b) {
             const float t0 = __builtin_fmaf(-8.0f, ux.s[b][0], dot0[b]);
@@ -271,17 +310,105 @@ __device__ __forceinline__ void unit_fma(const uint8_t* __restrict__ row, const 
     }
 }
 
-// Sum over aligned groups of G lanes (G a power of two <= 64).
+template <int T, int UB, int B>
+__device__ __forceinline__ void unit_fma(const uint8_t* __restrict__ row, const UnitPos& p,
+                                         const UnitX<T, UB, B>& ux, float (&acc)[B]) {
+    UnitRaw<T, UB> r;
+    unit_load<T, UB>(row, p, r);
+    unit_compute<T, UB, B>(r, p, ux, acc);
+}
+
+// ---------------------------------------------------------------------------
+// Cross-lane sums with DPP (row_shr / quad_perm / mirrors / row_bcast): VALU
+// latency instead of the LDS round trip of a bpermute shuffle.
+
+template <int CTRL, int ROW_MASK = 0xf, int BANK_MASK = 0xf>
+__device__ __forceinline__ float dpp(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v),
+                                                                 CTRL, ROW_MASK, BANK_MASK,
+                                                                 false));
+}
+
+template <int CTRL, int ROW_MASK = 0xf, int BANK_MASK = 0xf>
+__device__ __forceinline__ double dpp(double v) {
+    const int2 p = __builtin_bit_cast(int2, v);
+    int2 r;
+    r.x = __builtin_amdgcn_update_dpp(0, p.x, CTRL, ROW_MASK, BANK_MASK, false);
+    r.y = __builtin_amdgcn_update_dpp(0, p.y, CTRL, ROW_MASK, BANK_MASK, false);
+    return __builtin_bit_cast(double, r);
+}
+
+// As dpp(), but lanes outside ROW_MASK keep their own value (for max).
+template <int CTRL, int ROW_MASK = 0xf, int BANK_MASK = 0xf>
+__device__ __forceinline__ double dpp_keep(double v) {
+    const int2 p = __builtin_bit_cast(int2, v);
+    int2 r;
+    r.x = __builtin_amdgcn_update_dpp(p.x, p.x, CTRL, ROW_MASK, BANK_MASK, false);
+    r.y = __builtin_amdgcn_update_dpp(p.y, p.y, CTRL, ROW_MASK, BANK_MASK, false);
+    return __builtin_bit_cast(double, r);
+}
+
+// Maximum over aligned groups of G lanes, exact in the group's last lane.
 template <int G>
-__device__ __forceinline__ float group_sum(float v) {
-#pragma unroll
-    for (int off = G / 2; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+__device__ __forceinline__ double group_max(double v) {
+    if constexpr (G >= 2) v = fmax(v, dpp_keep<0xb1>(v));
+    if constexpr (G >= 4) v = fmax(v, dpp_keep<0x4e>(v));
+    if constexpr (G >= 8) v = fmax(v, dpp_keep<0x141>(v));
+    if constexpr (G >= 16) v = fmax(v, dpp_keep<0x140>(v));
+    if constexpr (G >= 32) v = fmax(v, dpp_keep<0x142, 0xa>(v));
+    if constexpr (G >= 64) v = fmax(v, dpp_keep<0x143, 0xc>(v));
     return v;
 }
 
-__device__ __forceinline__ float group_sum_dyn(float v, uint32_t g) {
-    for (uint32_t off = g >> 1; off >= 1; off >>= 1) v += __shfl_xor(v, static_cast<int>(off), 64);
+// Sum over aligned groups of G lanes (G a power of two <= 64).  The group
+// total is exact in the group's last lane (all lanes when G <= 16).
+template <int G, typename V>
+__device__ __forceinline__ V group_sum(V v) {
+    if constexpr (G >= 2) v += dpp<0xb1>(v);         // quad_perm [1,0,3,2]
+    if constexpr (G >= 4) v += dpp<0x4e>(v);         // quad_perm [2,3,0,1]
+    if constexpr (G >= 8) v += dpp<0x141>(v);        // row_half_mirror
+    if constexpr (G >= 16) v += dpp<0x140>(v);       // row_mirror
+    if constexpr (G >= 32) v += dpp<0x142, 0xa>(v);  // row_bcast:15 into rows 1, 3
+    if constexpr (G >= 64) v += dpp<0x143, 0xc>(v);  // row_bcast:31 into rows 2, 3
     return v;
+}
+
+template <typename V>
+__device__ __forceinline__ V group_sum_dyn(V v, uint32_t g) {
+    switch (g) {
+        case 1: return v;
+        case 2: return group_sum<2>(v);
+        case 4: return group_sum<4>(v);
+        case 8: return group_sum<8>(v);
+        case 16: return group_sum<16>(v);
+        case 32: return group_sum<32>(v);
+        default: return group_sum<64>(v);
+    }
+}
+
+// Inclusive prefix sum over the 64 lanes of a wave.
+template <typename V>
+__device__ __forceinline__ V wave_inclusive_scan(V v) {
+    v += dpp<0x111>(v);        // row_shr:1
+    v += dpp<0x112>(v);        // row_shr:2
+    v += dpp<0x114>(v);        // row_shr:4
+    v += dpp<0x118>(v);        // row_shr:8
+    v += dpp<0x142, 0xa>(v);   // row_bcast:15
+    v += dpp<0x143, 0xc>(v);   // row_bcast:31
+    return v;
+}
+
+template <typename V>
+__device__ __forceinline__ V lane63(V v) {
+    if constexpr (sizeof(V) == 4) {
+        return __builtin_bit_cast(V, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
+    } else {
+        const int2 p = __builtin_bit_cast(int2, v);
+        int2 r;
+        r.x = __builtin_amdgcn_readlane(p.x, 63);
+        r.y = __builtin_amdgcn_readlane(p.y, 63);
+        return __builtin_bit_cast(V, r);
+    }
 }
 
 }  // namespace pk

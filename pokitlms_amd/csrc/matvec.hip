@@ -17,14 +17,21 @@
 namespace pk {
 namespace {
 
-constexpr int kMaxS = 8;  // waves per K-split group
+constexpr int kMaxS = 12;  // waves per K-split group
+
+// Row passes whose loads a wave keeps in flight, and the workgroup bound: a
+// batch above 4 holds 64 activation floats per lane, so it keeps one pass in
+// flight and may split a row over up to 12 waves.
+template <int B> constexpr int passes_for() { return B > 4 ? 1 : 2; }
+template <int B> constexpr int max_threads_for() { return B > 4 ? 768 : 512; }
 
 template <int T, int B, int UB, int NU>
-__global__ __launch_bounds__(64 * kMaxS) void k_matvec_q(
+__global__ __launch_bounds__(max_threads_for<B>()) void k_matvec_q(
     const uint8_t* __restrict__ W, uint64_t row_bytes, const float* __restrict__ x,
     uint32_t x_stride, float* __restrict__ y, uint32_t y_stride, uint32_t rows, uint32_t units,
     uint32_t slice_units, uint32_t S, uint32_t glog2) {
-    extern __shared__ float partial[];  // [waves][RPP][B] when S > 1
+    extern __shared__ float partial[];  // [waves][kPasses][RPP][B] when S > 1
+    constexpr int kPasses = passes_for<B>();
     const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
     const uint32_t waves = blockDim.x >> 6;
     const uint32_t groups = waves / S;               // independent row streams per block
@@ -34,52 +41,78 @@ __global__ __launch_bounds__(64 * kMaxS) void k_matvec_q(
 
     UnitPos pos[NU];
     bool valid[NU];
-    UnitX<T, UB, B> ux[NU];
 #pragma unroll
     for (int k = 0; k < NU; ++k) {
         const uint32_t local = ul + G * k;
         const uint32_t u = slice * slice_units + local;
         valid[k] = local < slice_units && u < units;
         pos[k] = unit_pos<T, UB>(valid[k] ? u : 0u);
-        load_unit_x<T, UB, B>(x, x_stride, pos[k], valid[k], ux[k]);
     }
+    UnitX<T, UB, B> ux[NU];
+    bool have_x = false;
 
     const uint32_t passes = (rows + RPP - 1u) / RPP;
-    for (uint32_t p0 = blockIdx.x * groups; p0 < passes; p0 += gridDim.x * groups) {
-        const uint32_t p = p0 + group;
-        const uint32_t row = p * RPP + sub;
-        const bool live = p < passes && row < rows;
-        float acc[B];
+    const uint32_t stride = gridDim.x * groups * kPasses;
+    for (uint32_t p0 = blockIdx.x * groups * kPasses; p0 < passes; p0 += stride) {
+        // passes p0 + group*kPasses + q, q < kPasses: loads first
+        UnitRaw<T, UB> raw[kPasses][NU];
+        uint32_t row[kPasses];
+        bool live[kPasses];
 #pragma unroll
-        for (int b = 0; b < B; ++b) acc[b] = 0.0f;
-        if (live) {
-            const uint8_t* rp = W + static_cast<uint64_t>(row) * row_bytes;
+        for (int q = 0; q < kPasses; ++q) {
+            const uint32_t p = p0 + group * kPasses + q;
+            row[q] = p * RPP + sub;
+            live[q] = p < passes && row[q] < rows;
+            if (live[q]) {
+                const uint8_t* rp = W + static_cast<uint64_t>(row[q]) * row_bytes;
 #pragma unroll
-            for (int k = 0; k < NU; ++k)
-                if (valid[k]) unit_fma<T, UB, B>(rp, pos[k], ux[k], acc);
+                for (int k = 0; k < NU; ++k)
+                    if (valid[k]) unit_load<T, UB>(rp, pos[k], raw[q][k]);
+            }
+        }
+        if (!have_x) {  // activations arrive while the first weights are in flight
+#pragma unroll
+            for (int k = 0; k < NU; ++k) load_unit_x<T, UB, B>(x, x_stride, pos[k], valid[k], ux[k]);
+            have_x = true;
         }
 #pragma unroll
-        for (int b = 0; b < B; ++b) acc[b] = group_sum_dyn(acc[b], G);
-        if (S == 1) {
-            if (ul == 0 && live) {
+        for (int q = 0; q < kPasses; ++q) {
+            float acc[B];
 #pragma unroll
-                for (int b = 0; b < B; ++b) y[b * y_stride + row] = acc[b];
-            }
-        } else {
-            if (ul == 0) {
+            for (int b = 0; b < B; ++b) acc[b] = 0.0f;
+            if (live[q]) {
 #pragma unroll
-                for (int b = 0; b < B; ++b) partial[(wave * RPP + sub) * B + b] = acc[b];
+                for (int k = 0; k < NU; ++k)
+                    if (valid[k]) unit_compute<T, UB, B>(raw[q][k], pos[k], ux[k], acc);
             }
+#pragma unroll
+            for (int b = 0; b < B; ++b) acc[b] = group_sum_dyn(acc[b], G);
+            if (ul == G - 1u) {
+                if (S == 1) {
+                    if (live[q]) {
+#pragma unroll
+                        for (int b = 0; b < B; ++b) y[b * y_stride + row[q]] = acc[b];
+                    }
+                } else {
+#pragma unroll
+                    for (int b = 0; b < B; ++b)
+                        partial[((wave * kPasses + q) * RPP + sub) * B + b] = acc[b];
+                }
+            }
+        }
+        if (S > 1) {
             __syncthreads();
-            // the group's first wave finalises (row sub, batch b) = (t / B, t % B)
+            // the group's first wave finalises (pass q, row sub, batch b)
             if (slice == 0) {
-                for (uint32_t t = lane; t < RPP * B; t += 64u) {
-                    const uint32_t s_row = p * RPP + t / B;
+                for (uint32_t t = lane; t < kPasses * RPP * B; t += 64u) {
+                    const uint32_t q = t / (RPP * B), rs = (t / B) % RPP, b = t % B;
+                    const uint32_t p = p0 + group * kPasses + q;
+                    const uint32_t s_row = p * RPP + rs;
                     if (p < passes && s_row < rows) {
                         float v = 0.0f;
                         for (uint32_t s = 0; s < S; ++s)
-                            v += partial[((group * S + s) * RPP + t / B) * B + t % B];
-                        y[(t % B) * y_stride + s_row] = v;
+                            v += partial[(((group * S + s) * kPasses + q) * RPP + rs) * B + b];
+                        y[b * y_stride + s_row] = v;
                     }
                 }
             }
@@ -118,7 +151,7 @@ __global__ __launch_bounds__(256) void k_matvec_float(
 #pragma unroll
         for (int b = 0; b < B; ++b) {
             const float v = group_sum<64>(acc[b]);
-            if (lane == 0) y[b * y_stride + row] = v;
+            if (lane == 63) y[b * y_stride + row] = v;
         }
     }
 }
@@ -132,7 +165,7 @@ constexpr int unit_bytes_for(uint32_t batch, int maxub) {
     return batch <= 2 ? (maxub < 16 ? maxub : 16) : (batch <= 4 ? 8 : 4);
 }
 
-constexpr uint32_t kMaxUnitsPerLane = 4;
+constexpr uint32_t kMaxUnitsPerLane = 2;
 
 struct Plan {
     uint32_t units, S, slice_units, glog2, nu, waves_per_block;
@@ -147,16 +180,17 @@ uint32_t log2_ceil(uint32_t v) {
 
 template <int T>
 bool plan_for(uint32_t in, uint32_t batch, int ub, Plan& p) {
+    const uint32_t max_s = batch > 4 ? 12u : 8u;
     using F = Fmt<T>;
     if (in == 0 || in % F::BE) return false;
     p.units = in / F::BE * (F::PRIM / ub);
     // units one lane may hold: activation floats per unit = RUNS*ub*batch
     const uint32_t per_unit = F::RUNS * ub * batch;
-    uint32_t nu_cap = 128u / per_unit;
+    uint32_t nu_cap = 64u / per_unit;
     if (nu_cap == 0) nu_cap = 1;
     if (nu_cap > kMaxUnitsPerLane) nu_cap = kMaxUnitsPerLane;
     p.S = ceil_div(p.units, 64u * nu_cap);
-    if (p.S > kMaxS) return false;
+    if (p.S > max_s) return false;
     p.slice_units = ceil_div(p.units, p.S);
     if (p.slice_units >= 64u) {
         p.glog2 = 6;
@@ -173,14 +207,16 @@ template <int T, int B, int UB, int NU>
 hipError_t run_q(const Plan& pl, const uint8_t* W, uint64_t row_bytes, uint32_t rows,
                  const float* x, uint32_t in, float* y, hipStream_t stream) {
     const uint32_t RPP = 64u >> pl.glog2;
+    constexpr int kPasses = passes_for<B>();
     const uint32_t groups = pl.waves_per_block / pl.S;
     const uint32_t passes = ceil_div(rows, RPP);
-    uint32_t blocks = ceil_div(passes, groups);
+    uint32_t blocks = ceil_div(passes, groups * kPasses);
     // ~8 waves per CU: enough loads in flight, and each wave reuses its
     // register-resident activations over several rows.
     const uint32_t max_blocks = 256u * 8u / pl.waves_per_block;
     if (blocks > max_blocks) blocks = max_blocks;
-    const size_t lds = pl.S > 1 ? static_cast<size_t>(pl.waves_per_block) * RPP * B * sizeof(float) : 0;
+    const size_t lds =
+        pl.S > 1 ? static_cast<size_t>(pl.waves_per_block) * kPasses * RPP * B * sizeof(float) : 0;
     hipLaunchKernelGGL((k_matvec_q<T, B, UB, NU>), dim3(blocks), dim3(64u * pl.waves_per_block),
                        lds, stream, W, row_bytes, x, in, y, rows, rows, pl.units, pl.slice_units,
                        pl.S, pl.glog2);
@@ -190,11 +226,11 @@ hipError_t run_q(const Plan& pl, const uint8_t* W, uint64_t row_bytes, uint32_t 
 template <int T, int B, int UB>
 hipError_t dispatch_nu(const Plan& pl, const uint8_t* W, uint64_t rb, uint32_t rows,
                        const float* x, uint32_t in, float* y, hipStream_t s) {
-    switch (pl.nu) {
-        case 1: return run_q<T, B, UB, 1>(pl, W, rb, rows, x, in, y, s);
-        case 2: return run_q<T, B, UB, 2>(pl, W, rb, rows, x, in, y, s);
-        case 3: return run_q<T, B, UB, 3>(pl, W, rb, rows, x, in, y, s);
-        default: return run_q<T, B, UB, 4>(pl, W, rb, rows, x, in, y, s);
+    if constexpr (Fmt<T>::RUNS * UB * B > 32) {
+        return run_q<T, B, UB, 1>(pl, W, rb, rows, x, in, y, s);  // plan_for caps nu at 1
+    } else {
+        if (pl.nu == 1) return run_q<T, B, UB, 1>(pl, W, rb, rows, x, in, y, s);
+        return run_q<T, B, UB, 2>(pl, W, rb, rows, x, in, y, s);
     }
 }
 

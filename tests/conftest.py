@@ -4,6 +4,15 @@ import sys
 import numpy as np
 import pytest
 
+# PyTorch-ROCm ships its own HIP runtime and loads it as "libamdhip64.so";
+# libpokit_hip.so asks for soname "libamdhip64.so.7", which that copy also
+# carries.  Importing torch first makes both share one runtime (one HSA
+# instance per process); loading our library first would bring up a second.
+try:
+    import torch  # noqa: F401
+except ImportError:
+    torch = None
+
 ROOT = os.path.abspath(os.path.join(os.path.dirname(__file__), ".."))
 if ROOT not in sys.path:
     sys.path.insert(0, ROOT)
