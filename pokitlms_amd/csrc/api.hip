@@ -587,6 +587,11 @@ void pk_hip_reset_stats(pk_hip_ctx* ctx) {
     ctx->stats = pk_hip_stats{};
     ctx->stats.resident_bytes = resident;
     ctx->stats.uploaded_bytes = uploaded;
+    // device-side router counters (status words 1 and 2); the error word stays
+    if (hipSetDevice(ctx->device) == hipSuccess &&
+        hipStreamSynchronize(ctx->stream) == hipSuccess) {
+        (void)hipMemset(status_words(ctx) + 1, 0, 2 * sizeof(uint32_t));
+    }
 }
 
 }  // extern "C"

@@ -42,6 +42,36 @@ __device__ __forceinline__ void ld_words(const uint8_t* p, uint32_t (&w)[N]) {
     __builtin_memcpy(w, __builtin_assume_aligned(p, 4), 4 * N);
 }
 
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+
+// Streaming variant for weights read once: nontemporal loads (16-byte
+// pieces, then single dwords), so they do not displace reused data in L2.
+template <int N>
+__device__ __forceinline__ void ld_words_nt(const uint8_t* p, uint32_t (&w)[N]) {
+#pragma unroll
+    for (int i = 0; i < N / 4; ++i) {
+        const u32x4_t v = __builtin_nontemporal_load(
+            reinterpret_cast<const u32x4_t*>(__builtin_assume_aligned(p + 16 * i, 4)));
+        w[4 * i + 0] = v.x;
+        w[4 * i + 1] = v.y;
+        w[4 * i + 2] = v.z;
+        w[4 * i + 3] = v.w;
+    }
+#pragma unroll
+    for (int i = 4 * (N / 4); i < N; ++i)
+        w[i] = __builtin_nontemporal_load(
+            reinterpret_cast<const uint32_t*>(__builtin_assume_aligned(p + 4 * i, 4)));
+}
+
+#ifndef PK_WEIGHT_NT
+#define PK_WEIGHT_NT 1
+#endif
+template <int N>
+__device__ __forceinline__ void ld_weights(const uint8_t* p, uint32_t (&w)[N]) {
+    if constexpr (PK_WEIGHT_NT) ld_words_nt<N>(p, w);
+    else ld_words<N>(p, w);
+}
+
 template <int N>
 __device__ __forceinline__ void ld_words_2a(const uint8_t* p, uint32_t (&w)[N]) {
     const uintptr_t a = reinterpret_cast<uintptr_t>(p);
@@ -186,14 +216,14 @@ __device__ __forceinline__ void unit_load(const uint8_t* __restrict__ row, const
     constexpr int NW = UB / 4;
     const uint8_t* blk = row + p.boff;
     if constexpr (T == T_Q4_K || T == T_Q5_K) {
-        ld_words<4>(blk, r.h);
+        ld_weights<4>(blk, r.h);
         uint32_t q[NW];
-        ld_words<NW>(blk + (T == T_Q4_K ? 16 : 48) + p.k0, q);
+        ld_weights<NW>(blk + (T == T_Q4_K ? 16 : 48) + p.k0, q);
 #pragma unroll
         for (int i = 0; i < NW; ++i) r.q[i] = q[i];
         if constexpr (T == T_Q5_K) {
             uint32_t qh[NW];
-            ld_words<NW>(blk + 16 + (p.k0 % 32u), qh);
+            ld_weights<NW>(blk + 16 + (p.k0 % 32u), qh);
 #pragma unroll
             for (int i = 0; i < NW; ++i) r.qh[i] = qh[i];
         }
@@ -201,14 +231,14 @@ __device__ __forceinline__ void unit_load(const uint8_t* __restrict__ row, const
         const uint8_t* qp = T == T_Q6_K ? blk + p.k0 : blk + 2 + p.k0;
         const uintptr_t a = reinterpret_cast<uintptr_t>(qp);
         r.shift = static_cast<uint32_t>(a & 3u);
-        ld_words<NW + 1>(reinterpret_cast<const uint8_t*>(a & ~uintptr_t{3}), r.q);
+        ld_weights<NW + 1>(reinterpret_cast<const uint8_t*>(a & ~uintptr_t{3}), r.q);
         if constexpr (T == T_Q6_K) {
             const uint32_t kk = p.k0 % 64u;
             const uint8_t* hp = blk + 128u + 32u * (p.k0 / 64u) + (kk % 32u);
             // qh and ql share the block's alignment (both offsets are even)
-            ld_words<NW + 1>(reinterpret_cast<const uint8_t*>(
-                                 reinterpret_cast<uintptr_t>(hp) & ~uintptr_t{3}),
-                             r.qh);
+            ld_weights<NW + 1>(reinterpret_cast<const uint8_t*>(
+                                   reinterpret_cast<uintptr_t>(hp) & ~uintptr_t{3}),
+                               r.qh);
             const uint32_t sidx = (p.col[0] % 256u) / 16u;
             r.s0 = static_cast<int8_t>(blk[192u + sidx]);
             r.s1 = static_cast<int8_t>(blk[192u + sidx + 4u]);

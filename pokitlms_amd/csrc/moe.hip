@@ -8,16 +8,19 @@
 //     rigorous bound B on how far the CPU's serial, unfused FP32 sum
 //     (src/linear.cpp:26-30, src/simd_kernels.hpp:22) can be from S:
 //         |serial - S| <= u * sum_i |T_i| / (1 - n u),  T_i = exact prefix sums.
-//  2. k_gate_up: every workgroup first ranks the experts by S.  When the
-//     intervals [S-B, S+B] prove the top-k set and order, that ranking is the
-//     CPU's; otherwise every expert that could still enter the top-k is
-//     recomputed with the CPU's exact serial FP32 recurrence and the ranking
-//     is redone on those bit-exact logits.  (All workgroups reach the same
-//     routes; workgroup 0 also writes ids and route weights: FP64 exp, FP32
-//     probabilities, FP32 renormalisation, as route_experts.)  Then every
-//     (route, ffn row) pair dots the gate and up rows of the selected expert
-//     with the register-resident input and stores the SwiGLU activation
-//     g / (1 + expf(-g)) * u (:682-684).
+//  2. k_gate_up: every wave first ranks the experts by S (no LDS, no
+//     barrier).  When the intervals [S-B, S+B] prove the top-k set and
+//     order, that ranking is the CPU's; otherwise the workgroup recomputes
+//     every expert that could still enter the top-k with the CPU's exact
+//     serial FP32 recurrence and ranks those bit-exact logits.  (Ranking in
+//     a separate launch costs a dependent round trip per step; ranking at
+//     the end of k_router needs a device-wide fence per workgroup, which on
+//     this GPU writes back the whole L2.)  Workgroup 0 writes ids and route
+//     weights (FP64 exp, FP32 probabilities, FP32 renormalisation, as
+//     route_experts).  Every (route, ffn row) pair then dots the gate and up
+//     rows of the selected expert with the register-resident input and
+//     stores the SwiGLU activation g / (1 + expf(-g)) * u (:682-684), while
+//     the selected down slices are pulled toward the device-side cache.
 //  3. k_down: a workgroup of top_k waves computes one down-row dot per route
 //     and combines them in route order, y = ((0 + p0*o0) + p1*o1) + ...
 //     (:688-690), deterministically and without atomics.
@@ -34,7 +37,7 @@ constexpr uint32_t kMaxExperts = 256;
 constexpr uint32_t kRouterThreads = 256;
 constexpr uint32_t kMaxTopK = 8;      // routes per token: waves of the down/combine workgroup
 constexpr uint32_t kGateUpPasses = 2;  // row passes whose loads a gate/up wave keeps in flight
-constexpr uint32_t kDownPasses = 4;    // row passes per down workgroup
+constexpr uint32_t kDownPasses = 2;    // row passes per down workgroup
 
 // Status words (MoeDecodeArgs::status).
 enum : uint32_t { ST_ERROR = 0, ST_FALLBACKS = 1, ST_CANDIDATES = 2 };
@@ -54,59 +57,6 @@ __device__ __forceinline__ double block_reduce_d(double v, double* red) {
     for (uint32_t w = 1; w < (blockDim.x >> 6); ++w) r = MAX ? fmax(r, red[w]) : r + red[w];
     __syncthreads();
     return r;
-}
-
-// ---------------------------------------------------------------------------
-// 1. Router: exact sum and serial-error bound of one expert row per workgroup.
-
-template <int C>  // consecutive products per thread: hidden = 256 * C
-__global__ __launch_bounds__(kRouterThreads) void k_router(MoeDecodeArgs a) {
-    __shared__ double wtot[kRouterThreads / 64];
-    __shared__ double red[kRouterThreads / 64];
-    const uint32_t t = threadIdx.x, lane = t & 63u, wave = t >> 6;
-    const uint32_t e = blockIdx.x;
-    const float* w = a.router + static_cast<uint64_t>(e) * a.hidden + t * C;
-    const float* xx = a.x + t * C;
-    float p[C];
-#pragma unroll
-    for (int i = 0; i < C; i += 4) {
-        const float4 wv = *reinterpret_cast<const float4*>(w + i);
-        const float4 xv = *reinterpret_cast<const float4*>(xx + i);
-        p[i + 0] = __fmul_rn(wv.x, xv.x);  // the CPU's rounded products, exactly
-        p[i + 1] = __fmul_rn(wv.y, xv.y);
-        p[i + 2] = __fmul_rn(wv.z, xv.z);
-        p[i + 3] = __fmul_rn(wv.w, xv.w);
-    }
-    double local = 0.0, abs_p = 0.0;
-#pragma unroll
-    for (int i = 0; i < C; ++i) {
-        local += static_cast<double>(p[i]);
-        abs_p += fabs(static_cast<double>(p[i]));
-    }
-    // exclusive prefix of the thread totals: wave scan + wave offsets
-    const double incl = wave_inclusive_scan(local);
-    if (lane == 63) wtot[wave] = incl;
-    __syncthreads();
-    double off = incl - local;
-    for (uint32_t v = 0; v < wave; ++v) off += wtot[v];
-    double prefix_abs = 0.0;
-#pragma unroll
-    for (int i = 0; i < C; ++i) {
-        off += static_cast<double>(p[i]);
-        prefix_abs += fabs(off);
-    }
-    double total = 0.0;
-    for (uint32_t v = 0; v < (kRouterThreads >> 6); ++v) total += wtot[v];
-    prefix_abs = block_reduce_d<false>(prefix_abs, red);
-    abs_p = block_reduce_d<false>(abs_p, red);
-    if (t == 0) {
-        // u = 2^-24.  (1 + 2^-10) >= 1/(1 - n u) for n <= 2^13 and also covers
-        // the FP64 rounding of the prefix sums; abs_p * 2^-40 covers S itself.
-        double bound = prefix_abs * 0x1p-24 * (1.0 + 0x1p-10) + abs_p * 0x1p-40;
-        if (!(abs_p < 1.0e36)) bound = INFINITY;  // near FP32 overflow: always recompute
-        a.row_sum[e] = total;
-        a.row_bound[e] = bound;
-    }
 }
 
 // The CPU's router logit, bit for bit: s = fl(s + fl(w_i * x_i)), i ascending,
@@ -165,121 +115,307 @@ __device__ __forceinline__ void rank_select(const double* __restrict__ v, uint32
     __syncthreads();
 }
 
-struct RouteShared {
-    double logit[kMaxExperts];
-    double lo[kMaxExperts];
-    double hi[kMaxExperts];
-    double red[4];
-    uint32_t rank[kMaxExperts];
+// Order-preserving 32-bit key of an FP32 value.
+__device__ __forceinline__ uint32_t order_key(float f) {
+    const uint32_t b = __builtin_bit_cast(uint32_t, f);
+    return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+}
+
+template <int CTRL, int ROW_MASK = 0xf>
+__device__ __forceinline__ uint32_t dpp_keep_u(uint32_t v) {
+    return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(
+        static_cast<int>(v), static_cast<int>(v), CTRL, ROW_MASK, 0xf, false));
+}
+
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+    v = max(v, dpp_keep_u<0xb1>(v));
+    v = max(v, dpp_keep_u<0x4e>(v));
+    v = max(v, dpp_keep_u<0x141>(v));
+    v = max(v, dpp_keep_u<0x140>(v));
+    v = max(v, dpp_keep_u<0x142, 0xa>(v));
+    v = max(v, dpp_keep_u<0x143, 0xc>(v));
+    return static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(v), 63));
+}
+
+__device__ __forceinline__ double readlane_d(double v, uint32_t lane) {
+    const int2 p = __builtin_bit_cast(int2, v);
+    int2 r;
+    r.x = __builtin_amdgcn_readlane(p.x, static_cast<int>(lane));
+    r.y = __builtin_amdgcn_readlane(p.y, static_cast<int>(lane));
+    return __builtin_bit_cast(double, r);
+}
+
+constexpr uint32_t kSlots = kMaxExperts / 64;  // candidates per lane
+
+// Expert e's value from the lane/slot layout e = lane + 64 * slot (e uniform).
+__device__ __forceinline__ double slot_value(const double (&v)[kSlots], uint32_t e) {
+    const uint32_t slot = e >> 6;
+    const double x = slot == 0 ? v[0] : slot == 1 ? v[1] : slot == 2 ? v[2] : v[3];
+    return readlane_d(x, e & 63u);
+}
+
+// Routes as every wave computes them, without LDS or barriers.
+struct WaveRoutes {
     uint32_t sel[kMaxTopK];
-    float probs[kMaxTopK];
-    uint32_t need_serial;
-    uint32_t bad;
+    float logit[kSlots];  // FP32 of S for experts lane + 64 * m (-inf past n_experts)
+    bool certified;
+    bool finite;
     double lo_min_sel;
 };
 
-// The routes of this token, identical in every workgroup.  Returns false
-// (and workgroup 0 flags the error) on non-finite logits.  xs: x in LDS.
-__device__ bool route(const MoeDecodeArgs& a, RouteShared& sh, const float* xs) {
-    const uint32_t t = threadIdx.x;
+// Top-k by (S desc, id asc) using 32-bit keys (FP32 value with its low byte
+// replaced by 255 - id).  The key only proposes an order: certification
+// below checks it against the exact intervals, so an ordering the truncated
+// key gets wrong is never certified and goes to the exact path.
+__device__ __forceinline__ WaveRoutes wave_route(const MoeDecodeArgs& a) {
+    const uint32_t lane = threadIdx.x & 63u;
     const uint32_t E = a.n_experts, K = a.top_k;
+    double S[kSlots], B[kSlots];
+    uint32_t key[kSlots];
+    bool fin = true;
+#pragma unroll
+    for (uint32_t m = 0; m < kSlots; ++m) {
+        const uint32_t e = lane + 64u * m;
+        S[m] = 0.0;
+        B[m] = 0.0;
+        key[m] = 0u;
+        if (e < E) {
+            S[m] = a.row_sum[e];
+            B[m] = a.row_bound[e];
+            const float f = static_cast<float>(S[m]);
+            fin = fin && isfinite(f);
+            key[m] = (order_key(f) & ~0xffu) | (255u - e);
+        }
+    }
+    WaveRoutes w;
+    w.finite = __all(fin);
+#pragma unroll
+    for (uint32_t m = 0; m < kSlots; ++m)
+        w.logit[m] = lane + 64u * m < E ? static_cast<float>(S[m]) : -INFINITY;
+#pragma unroll
+    for (uint32_t r = 0; r < kMaxTopK; ++r) {
+        if (r >= K) {
+            w.sel[r] = 0u;
+            continue;
+        }
+        uint32_t mk = key[0];
+#pragma unroll
+        for (uint32_t m = 1; m < kSlots; ++m) mk = max(mk, key[m]);
+        const uint32_t best = wave_max_u32(mk);
+        w.sel[r] = 255u - (best & 0xffu);
+#pragma unroll
+        for (uint32_t m = 0; m < kSlots; ++m)
+            if (key[m] == best) key[m] = 0u;
+    }
+    // certified when lo(sel[r]) > max hi over everything ranked after r
+    double hi_rest = -INFINITY;
+#pragma unroll
+    for (uint32_t m = 0; m < kSlots; ++m)
+        if (key[m] != 0u) hi_rest = fmax(hi_rest, S[m] + B[m]);
+    double after = lane63(group_max<64>(hi_rest));
+    bool ok = true;
+    double lmin = INFINITY;
+#pragma unroll
+    for (int r = kMaxTopK - 1; r >= 0; --r) {  // constant indices keep sel in registers
+        if (static_cast<uint32_t>(r) < K) {
+            const double s = slot_value(S, w.sel[r]), b = slot_value(B, w.sel[r]);
+            ok = ok && (s - b > after);
+            after = fmax(after, s + b);
+            lmin = fmin(lmin, s - b);
+        }
+    }
+    w.certified = ok;
+    w.lo_min_sel = lmin;
+    return w;
+}
+
+// Exact routing of an uncertified token, by the whole workgroup (rare).
+struct FallbackShared {
+    double logit[kMaxExperts];
+    uint32_t rank[kMaxExperts];
+    uint32_t sel[kMaxTopK];
+    uint32_t bad;  // a non-finite exact logit
+};
+
+__device__ __forceinline__ void exact_routes(const MoeDecodeArgs& a, double lo_min_sel,
+                                             const float* xs, FallbackShared& fb) {
+    const uint32_t t = threadIdx.x, E = a.n_experts;
     if (t < E) {
         const double s = a.row_sum[t], b = a.row_bound[t];
-        sh.logit[t] = s;
-        sh.lo[t] = s - b;
-        sh.hi[t] = s + b;
-    }
-    __syncthreads();
-    rank_select(sh.logit, E, K, sh.rank, sh.sel);
-
-    // Certified when lo(sel[r]) > max hi over everything ranked after r.
-    const double mx_rest =
-        block_reduce_d<true>(t < E && sh.rank[t] >= K ? sh.hi[t] : -INFINITY, sh.red);
-    if (t == 0) {
-        double after = mx_rest, lmin = INFINITY;
-        uint32_t ok = 1u;
-        for (int r = static_cast<int>(K) - 1; r >= 0; --r) {
-            const uint32_t id = sh.sel[r];
-            if (!(sh.lo[id] > after)) ok = 0u;
-            after = fmax(after, sh.hi[id]);
-            lmin = fmin(lmin, sh.lo[id]);
-        }
-        sh.need_serial = ok ? 0u : 1u;
-        sh.lo_min_sel = lmin;
-    }
-    __syncthreads();
-    if (sh.need_serial) {
         // An expert with hi < lo_min_sel is below k certain experts; every other
         // expert gets its exact CPU logit.  FP32 rounding of S keeps the rest
         // below lo_min_sel (|fl(S) - S| <= u|S| <= bound).
-        if (t < E) {
-            if (!(sh.hi[t] < sh.lo_min_sel)) {
-                sh.logit[t] = static_cast<double>(
-                    serial_logit(a.router + static_cast<uint64_t>(t) * a.hidden, xs, a.hidden));
-                if (blockIdx.x == 0) atomicAdd(a.status + ST_CANDIDATES, 1u);
-            } else {
-                sh.logit[t] = static_cast<double>(static_cast<float>(sh.logit[t]));
+        if (!(s + b < lo_min_sel)) {
+            fb.logit[t] = static_cast<double>(
+                serial_logit(a.router + static_cast<uint64_t>(t) * a.hidden, xs, a.hidden));
+            if (blockIdx.x == 0) atomicAdd(a.status + ST_CANDIDATES, 1u);
+        } else {
+            fb.logit[t] = static_cast<double>(static_cast<float>(s));
+        }
+    }
+    if (t == 0 && blockIdx.x == 0) atomicAdd(a.status + ST_FALLBACKS, 1u);
+    if (t == 0) fb.bad = 0u;
+    __syncthreads();
+    // route_experts throws on any non-finite logit (src/qwen3_moe_runner.cpp:270-276)
+    if (t < E && !isfinite(fb.logit[t])) fb.bad = 1u;
+    __syncthreads();
+    rank_select(fb.logit, E, a.top_k, fb.rank, fb.sel);
+}
+
+// Workgroup 0, wave 0: route weights as route_experts (FP64 softmax over all
+// experts, FP32 probabilities, FP32 renormalisation, optional scale), written
+// with the ids.  l[m] is the FP32 logit the ranking used for expert
+// lane + 64 * m (unused slots: -inf).
+__device__ __forceinline__ void write_routes(const MoeDecodeArgs& a, const uint32_t (&sel)[kMaxTopK],
+                                             const float (&l)[kSlots]) {
+    const uint32_t lane = threadIdx.x & 63u, K = a.top_k;
+    double ld[kSlots];
+#pragma unroll
+    for (uint32_t m = 0; m < kSlots; ++m) ld[m] = static_cast<double>(l[m]);
+    const float mxf = static_cast<float>(slot_value(ld, sel[0]));
+    double ex = 0.0;
+#pragma unroll
+    for (uint32_t m = 0; m < kSlots; ++m)
+        if (lane + 64u * m < a.n_experts) ex += exp(static_cast<double>(l[m] - mxf));
+    const double denom = lane63(group_sum<64>(ex));
+    float mine = mxf;  // logit of route `lane`
+    uint32_t my_id = 0u;
+#pragma unroll
+    for (uint32_t r = 0; r < kMaxTopK; ++r) {
+        if (r < K) {
+            const float v = static_cast<float>(slot_value(ld, sel[r]));
+            if (lane == r) {
+                mine = v;
+                my_id = sel[r];
             }
         }
-        if (t == 0 && blockIdx.x == 0) atomicAdd(a.status + ST_FALLBACKS, 1u);
-        __syncthreads();
-        rank_select(sh.logit, E, K, sh.rank, sh.sel);
+    }
+    float p = 0.0f;
+    if (lane < K) p = static_cast<float>(exp(static_cast<double>(mine - mxf)) / denom);
+    float selected_sum = 0.0f;
+    for (uint32_t r = 0; r < K; ++r)
+        selected_sum = __fadd_rn(selected_sum, __builtin_bit_cast(float, __builtin_amdgcn_readlane(
+                                                                        __builtin_bit_cast(int, p),
+                                                                        static_cast<int>(r))));
+    if (lane < K) {
+        float q = a.normalize ? p / selected_sum : p;
+        if (a.scale != 1.0f) q = __fmul_rn(q, a.scale);
+        a.ids[lane] = my_id;
+        a.probs[lane] = q;
+    }
+    if (lane == 0) a.status[ST_ERROR] = 0u;
+}
+
+// ---------------------------------------------------------------------------
+// 1. Router: exact sum and serial-error bound of one expert row per workgroup.
+
+template <int C>  // consecutive products per thread: hidden = 256 * C
+__global__ __launch_bounds__(kRouterThreads) void k_router(MoeDecodeArgs a) {
+    __shared__ double wtot[kRouterThreads / 64];
+    __shared__ double red[kRouterThreads / 64];
+    const uint32_t t = threadIdx.x, lane = t & 63u, wave = t >> 6;
+    const uint32_t e = blockIdx.x;
+    const float* w = a.router + static_cast<uint64_t>(e) * a.hidden + t * C;
+    const float* xx = a.x + t * C;
+    static_assert(C % 2 == 0, "router rows split into pairs of products per thread");
+    float p[C];
+    if constexpr (C % 4 == 0) {
+#pragma unroll
+        for (int i = 0; i < C; i += 4) {
+            const float4 wv = *reinterpret_cast<const float4*>(w + i);
+            const float4 xv = *reinterpret_cast<const float4*>(xx + i);
+            p[i + 0] = __fmul_rn(wv.x, xv.x);  // the CPU's rounded products, exactly
+            p[i + 1] = __fmul_rn(wv.y, xv.y);
+            p[i + 2] = __fmul_rn(wv.z, xv.z);
+            p[i + 3] = __fmul_rn(wv.w, xv.w);
+        }
     } else {
-        if (t < E) sh.logit[t] = static_cast<double>(static_cast<float>(sh.logit[t]));
-        __syncthreads();
+#pragma unroll
+        for (int i = 0; i < C; i += 2) {
+            const float2 wv = *reinterpret_cast<const float2*>(w + i);
+            const float2 xv = *reinterpret_cast<const float2*>(xx + i);
+            p[i + 0] = __fmul_rn(wv.x, xv.x);
+            p[i + 1] = __fmul_rn(wv.y, xv.y);
+        }
     }
-    // route_experts throws on non-finite logits (src/qwen3_moe_runner.cpp:270-276)
-    if (t == 0) sh.bad = 0u;
+    double local = 0.0, abs_p = 0.0;
+#pragma unroll
+    for (int i = 0; i < C; ++i) {
+        local += static_cast<double>(p[i]);
+        abs_p += fabs(static_cast<double>(p[i]));
+    }
+    // exclusive prefix of the thread totals: wave scan + wave offsets
+    const double incl = wave_inclusive_scan(local);
+    if (lane == 63) wtot[wave] = incl;
     __syncthreads();
-    if (t < E && !isfinite(sh.logit[t])) sh.bad = 1u;
-    __syncthreads();
-    if (sh.bad) {
-        if (blockIdx.x == 0) {
-            if (t == 0) a.status[ST_ERROR] = 1u;
-            if (t < K) {
-                a.ids[t] = 0xffffffffu;
-                a.probs[t] = 0.0f;
-            }
-        }
-        return false;
+    double off = incl - local;
+    for (uint32_t v = 0; v < wave; ++v) off += wtot[v];
+    double prefix_abs = 0.0;
+#pragma unroll
+    for (int i = 0; i < C; ++i) {
+        off += static_cast<double>(p[i]);
+        prefix_abs += fabs(off);
     }
-    if (blockIdx.x == 0) {
-        // softmax over all experts: FP64 exp of the FP32 difference to the max
-        const float mxf = static_cast<float>(sh.logit[sh.sel[0]]);
-        const double denom = block_reduce_d<false>(
-            t < E ? exp(static_cast<double>(static_cast<float>(sh.logit[t]) - mxf)) : 0.0,
-            sh.red);
-        if (t < K) {
-            const float l = static_cast<float>(sh.logit[sh.sel[t]]);
-            sh.probs[t] = static_cast<float>(exp(static_cast<double>(l - mxf)) / denom);
-        }
-        __syncthreads();
-        if (t < K) {
-            float selected_sum = 0.0f;
-            for (uint32_t r = 0; r < K; ++r) selected_sum = __fadd_rn(selected_sum, sh.probs[r]);
-            float q = a.normalize ? sh.probs[t] / selected_sum : sh.probs[t];
-            if (a.scale != 1.0f) q = __fmul_rn(q, a.scale);
-            a.ids[t] = sh.sel[t];
-            a.probs[t] = q;
-        }
-        if (t == 0) a.status[ST_ERROR] = 0u;
+    double total = 0.0;
+    for (uint32_t v = 0; v < (kRouterThreads >> 6); ++v) total += wtot[v];
+    prefix_abs = block_reduce_d<false>(prefix_abs, red);
+    abs_p = block_reduce_d<false>(abs_p, red);
+    if (t == 0) {
+        // u = 2^-24.  (1 + 2^-10) >= 1/(1 - n u) for n <= 2^13 and also covers
+        // the FP64 rounding of the prefix sums; abs_p * 2^-40 covers S itself.
+        double bound = prefix_abs * 0x1p-24 * (1.0 + 0x1p-10) + abs_p * 0x1p-40;
+        if (!(abs_p < 1.0e36)) bound = INFINITY;  // near FP32 overflow: always recompute
+        a.row_sum[e] = total;
+        a.row_bound[e] = bound;
     }
-    return true;
+
 }
 
 // ---------------------------------------------------------------------------
 // 2. Routing + gate/up + SwiGLU.  All (route, row) items share the input x,
 // so one unit mapping (and one register copy of x per lane) serves them all.
 
-template <int T, int UB, int NU>
+template <int T, int UB, int NU, int NP>
 __global__ __launch_bounds__(256) void k_gate_up(MoeDecodeArgs a, uint32_t units, uint32_t glog2) {
     extern __shared__ float xs[];  // [hidden]
-    __shared__ RouteShared sh;
-    for (uint32_t i = threadIdx.x; i < a.hidden; i += blockDim.x) xs[i] = a.x[i];
-    __syncthreads();
-    if (!route(a, sh, xs)) return;
-
+    __shared__ FallbackShared fb;
     const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+    WaveRoutes w = wave_route(a);
+    if (!w.finite) {
+        // route_experts throws on non-finite logits (src/qwen3_moe_runner.cpp:270-276)
+        if (blockIdx.x == 0 && wave == 0) {
+            if (lane == 0) a.status[ST_ERROR] = 1u;
+            if (lane < a.top_k) {
+                a.ids[lane] = 0xffffffffu;
+                a.probs[lane] = 0.0f;
+            }
+        }
+        return;
+    }
+    bool staged = false;
+    if (!w.certified) {  // uniform over the workgroup: every wave saw the same data
+        for (uint32_t i = threadIdx.x; i < a.hidden; i += blockDim.x) xs[i] = a.x[i];
+        __syncthreads();
+        staged = true;
+        exact_routes(a, w.lo_min_sel, xs, fb);
+        if (fb.bad) {  // uniform: every wave reads the same flag
+            if (blockIdx.x == 0 && wave == 0) {
+                if (lane == 0) a.status[ST_ERROR] = 1u;
+                if (lane < a.top_k) {
+                    a.ids[lane] = 0xffffffffu;
+                    a.probs[lane] = 0.0f;
+                }
+            }
+            return;
+        }
+#pragma unroll
+        for (uint32_t r = 0; r < kMaxTopK; ++r) w.sel[r] = r < a.top_k ? fb.sel[r] : 0u;
+#pragma unroll
+        for (uint32_t m = 0; m < kSlots; ++m)
+            w.logit[m] = lane + 64u * m < a.n_experts ? static_cast<float>(fb.logit[lane + 64u * m])
+                                                      : -INFINITY;
+    }
+
     const uint32_t G = 1u << glog2, RPP = 64u >> glog2;
     const uint32_t sub = lane >> glog2, ul = lane & (G - 1u);
     UnitPos pos[NU];
@@ -292,21 +428,23 @@ __global__ __launch_bounds__(256) void k_gate_up(MoeDecodeArgs a, uint32_t units
     }
     const uint32_t items = a.top_k * a.ffn;
     const uint32_t passes = (items + RPP - 1u) / RPP;
-    const uint32_t wave_id = blockIdx.x * (blockDim.x >> 6) + wave;
-    const uint32_t first = wave_id * kGateUpPasses;  // this wave's passes: consecutive rows
+    const uint32_t first = (blockIdx.x * (blockDim.x >> 6) + wave) * NP;
 
-    // issue every load of this wave's rows first
-    UnitRaw<T, UB> rg[kGateUpPasses][NU], ru[kGateUpPasses][NU];
-    uint32_t item[kGateUpPasses];
+    // weights first: every load of this wave's rows is in flight before x arrives
+    UnitRaw<T, UB> rg[NP][NU], ru[NP][NU];
+    uint32_t item[NP];
 #pragma unroll
-    for (int q = 0; q < kGateUpPasses; ++q) {
+    for (int q = 0; q < NP; ++q) {
         const uint32_t p = first + q;
         item[q] = p * RPP + sub;
         if (p < passes && item[q] < items) {
             const uint32_t route_i = item[q] / a.ffn, row = item[q] % a.ffn;
-            const uint64_t e = sh.sel[route_i];
-            const uint8_t* gr = a.gate + e * a.gate_slice + row * a.gate_row;
-            const uint8_t* ur = a.up + e * a.up_slice + row * a.up_row;
+            uint32_t e = 0u;
+#pragma unroll
+            for (uint32_t r = 0; r < kMaxTopK; ++r)
+                if (route_i == r) e = w.sel[r];
+            const uint8_t* gr = a.gate + static_cast<uint64_t>(e) * a.gate_slice + row * a.gate_row;
+            const uint8_t* ur = a.up + static_cast<uint64_t>(e) * a.up_slice + row * a.up_row;
 #pragma unroll
             for (int k = 0; k < NU; ++k) {
                 if (valid[k]) {
@@ -316,12 +454,36 @@ __global__ __launch_bounds__(256) void k_gate_up(MoeDecodeArgs a, uint32_t units
             }
         }
     }
+    // Pull this workgroup's share of the selected down slices toward the
+    // device-side cache while the gate/up stream is in flight; k_down then
+    // reads them without waiting on HBM.
+    uint32_t touch = 0u;
+    {
+        const uint32_t span = static_cast<uint32_t>(a.down_slice / 64u);  // 64-byte lines per slice
+        const uint32_t lines = span * a.top_k;
+        const uint32_t per_block = (lines + gridDim.x - 1u) / gridDim.x;
+        const uint32_t l0 = blockIdx.x * per_block;
+        for (uint32_t l = l0 + threadIdx.x; l < l0 + per_block && l < lines; l += blockDim.x) {
+            const uint32_t route_i = l / span, off = l % span;
+            uint32_t e = 0u;
+#pragma unroll
+            for (uint32_t r = 0; r < kMaxTopK; ++r)
+                if (route_i == r) e = w.sel[r];
+            touch ^= *reinterpret_cast<const uint32_t*>(a.down + static_cast<uint64_t>(e) * a.down_slice +
+                                                        64ull * off);
+        }
+    }
+    if (!staged) {
+        for (uint32_t i = threadIdx.x; i < a.hidden; i += blockDim.x) xs[i] = a.x[i];
+        __syncthreads();
+    }
+    if (blockIdx.x == 0 && wave == 0) write_routes(a, w.sel, w.logit);
     UnitX<T, UB, 1> ux[NU];
 #pragma unroll
     for (int k = 0; k < NU; ++k) load_unit_x<T, UB, 1>(xs, 0, pos[k], valid[k], ux[k]);
 
 #pragma unroll
-    for (int q = 0; q < kGateUpPasses; ++q) {
+    for (int q = 0; q < NP; ++q) {
         const bool live = first + q < passes && item[q] < items;
         float g[1] = {0.0f}, u[1] = {0.0f};
         if (live) {
@@ -337,13 +499,14 @@ __global__ __launch_bounds__(256) void k_gate_up(MoeDecodeArgs a, uint32_t units
         const float us = group_sum_dyn(u[0], G);
         if (live && ul == G - 1u) a.act[item[q]] = (gs / (1.0f + expf(-gs))) * us;
     }
+    if (touch == 0x9e3779b9u && a.hidden == 0u) a.act[0] = 0.0f;  // keeps the touches alive
 }
 
 // ---------------------------------------------------------------------------
 // 3. down + combine.  blockDim = 64 * top_k: wave k owns route k; the
 // workgroup covers kDownPasses * RPP output rows.
 
-template <int T, int UB, int NU>
+template <int T, int UB, int NU, int kDownPasses>
 __global__ __launch_bounds__(64 * kMaxTopK) void k_down(MoeDecodeArgs a, uint32_t units,
                                                          uint32_t glog2) {
     extern __shared__ float part[];  // [top_k][kDownPasses * RPP]
@@ -441,7 +604,7 @@ hipError_t gate_up_t(const MoeDecodeArgs& a, hipStream_t s) {
     const size_t lds = a.hidden * sizeof(float);
 #define PK_GU(N)                                                                              \
     case N:                                                                                   \
-        hipLaunchKernelGGL((k_gate_up<T, UB, N>), dim3(blocks), dim3(256), lds, s, a, units, \
+        hipLaunchKernelGGL((k_gate_up<T, UB, N, kGateUpPasses>), dim3(blocks), dim3(256), lds, s, a, units, \
                            glog2);                                                            \
         break;
     switch (nu) { PK_GU(1) PK_GU(2) default: return hipErrorInvalidValue; }
@@ -459,7 +622,7 @@ hipError_t down_t(const MoeDecodeArgs& a, hipStream_t s) {
     const size_t lds = static_cast<size_t>(a.top_k) * kDownPasses * RPP * sizeof(float);
 #define PK_DN(N)                                                                              \
     case N:                                                                                   \
-        hipLaunchKernelGGL((k_down<T, UB, N>), dim3(blocks), dim3(64u * a.top_k), lds, s, a,  \
+        hipLaunchKernelGGL((k_down<T, UB, N, kDownPasses>), dim3(blocks), dim3(64u * a.top_k), lds, s, a,  \
                            units, glog2);                                                     \
         break;
     switch (nu) { PK_DN(1) PK_DN(2) default: return hipErrorInvalidValue; }

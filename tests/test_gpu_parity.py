@@ -156,6 +156,7 @@ def test_c3_moe_decode_golden(hip, port, golden, c3):
     layer, h = c3
     toks = G.c3_tokens()
     blk = port.moe(layer)
+    hip.reset_stats()
     worst = 0.0
     for t in range(toks.shape[0]):
         y, ids, probs = hip.moe_decode(h, toks[t])
@@ -165,6 +166,11 @@ def test_c3_moe_decode_golden(hip, port, golden, c3):
         worst = max(worst, normwise_rel(y, cpu))
     say("c3 worst normwise", worst)
     assert worst <= TOL
+    # the certified (parallel) routing must carry most tokens; the exact serial
+    # path is the exception (it also hid a broken fast path once)
+    st = hip.stats()
+    say("c3 router fallbacks", st["router_fallbacks"], "of", toks.shape[0])
+    assert st["router_fallbacks"] <= toks.shape[0] // 8
 
 
 def test_moe_decode_deterministic(hip, c3):
@@ -244,6 +250,27 @@ def test_moe_shapes_and_normalisation(hip, port, normalize):
             assert np.max(np.abs(probs - cprobs)) <= TOL * np.max(cprobs)
             assert normwise_rel(y, cy) <= TOL
         h.release()
+
+
+@pytest.mark.parametrize("hidden", (512, 1024, 3072))
+def test_router_fast_path_widths(hip, port, hidden):
+    """Every router width the kernel supports certifies most random tokens
+    itself (no exact fallback) and still matches the CPU's routes."""
+    layer = S.moe_layer(seed=90 + hidden, hidden=hidden, experts=64, ffn=256, top_k=8)
+    h = hip.upload_moe_layer(layer)
+    blk = port.moe(layer)
+    hip.reset_stats()
+    n = 16
+    for t in range(n):
+        x = S.normal_f32(S.rng(900 + t), hidden)
+        y, ids, _ = hip.moe_decode(h, x)
+        cy, cids, _ = blk.forward(x)
+        assert np.array_equal(ids, cids)
+        assert normwise_rel(y, cy) <= TOL
+    st = hip.stats()
+    say("width", hidden, "fallbacks", st["router_fallbacks"])
+    assert st["router_fallbacks"] <= n // 4
+    h.release()
 
 
 def test_non_finite_router_is_a_runtime_error(hip, port):
