@@ -47,7 +47,25 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--eager", action="store_true", help="time eager launches instead of graphs")
+    ap.add_argument("--calibrate-copy-mib", type=int, default=0,
+                    help="first run a plain device copy of this many MiB three times "
+                         "(the known-size kernel that scales rocprofv3 FETCH/WRITE_SIZE)")
     return ap.parse_args()
+
+
+def profiled_traffic(kernel: str):
+    """HBM bytes per launch of `kernel` from the committed rocprofv3 --pmc
+    summary (FETCH_SIZE + WRITE_SIZE, copy-kernel scaled), or None."""
+    path = os.path.join(ROOT, "profiles", "moe_layer_decode_traffic.txt")
+    try:
+        with open(path) as f:
+            for line in f:
+                parts = line.split()
+                if len(parts) == 3 and parts[0] == kernel and parts[1] == "traffic_bytes":
+                    return int(parts[2])
+    except OSError:
+        pass
+    return None
 
 
 def device_quant(torch, gtype, rows, inn, gen, dev):
@@ -133,6 +151,15 @@ def main():
     from pokitlms_amd.backend import HipBackend
 
     dev = torch.device("cuda:0")
+    if args.calibrate_copy_mib > 0:
+        n = args.calibrate_copy_mib << 18  # float32 elements
+        src = torch.ones(n, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        log(f"copy calibration: 3 x {args.calibrate_copy_mib} MiB device copies")
+        del src, dst
     hip = HipBackend(0)
     log(f"building {args.layers} resident layers ...")
     layers = build_layers(torch, hip, args.layers, dev)
@@ -245,8 +272,9 @@ def main():
     dominant = max(kns, key=lambda k: kns[k])
     achieved = kbytes[dominant] / kns[dominant]  # B/ns == GB/s
     roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
-                "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-                "kernel": dominant}
+                "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                "traffic": profiled_traffic(dominant), "kernel": dominant,
+                "avg_us": round(kns[dominant] / 1e3, 3), "algorithmic_bytes": kbytes[dominant]}
 
     # a spot parity check of the timed path against the CPU oracle
     parity = None

@@ -96,6 +96,7 @@ struct pk_hip_ctx {
     DeviceBuffer<uint32_t> ids, words;  // words: [0] counter, [1..4] status
     DeviceBuffer<double> row_sum, row_bound;
     hipEvent_t ev[8] = {};
+    int wall_rate_khz = 100000;  // wall_clock64() rate
 
     void set_device() const { check(hipSetDevice(device), "hipSetDevice"); }
 };
@@ -192,6 +193,23 @@ pk_hip_weight* make_weight(pk_hip_ctx* ctx, uint32_t type, uint64_t in, uint64_t
     return w;
 }
 
+// Holds the stream for `ticks` of the constant-rate wall clock so that the
+// launches and events of one timed call are all queued before the GPU reaches
+// them; event intervals then cover dispatch + execution, not host latency.
+// The wait is bounded by the clock alone.
+__global__ void k_hold(uint64_t ticks) {
+    const uint64_t t0 = wall_clock64();
+    while (wall_clock64() - t0 < ticks) __builtin_amdgcn_s_sleep(16);
+}
+
+constexpr uint64_t kHoldMicroseconds = 100;
+
+void hold_stream(pk_hip_ctx* c, hipStream_t s) {
+    const uint64_t ticks = kHoldMicroseconds * static_cast<uint64_t>(c->wall_rate_khz) / 1000u;
+    hipLaunchKernelGGL(k_hold, dim3(1), dim3(64), 0, s, ticks);
+    check(hipGetLastError(), "hold launch");
+}
+
 void begin_timing(pk_hip_ctx* c, hipStream_t s, int slot) {
     if (c->time_kernels) check(hipEventRecord(c->ev[slot], s), "hipEventRecord");
 }
@@ -220,6 +238,7 @@ void enqueue_matvec(pk_hip_ctx* c, const pk_hip_weight* w, uint32_t expert, cons
     }
     if (!pk::matvec_supported(w->type, static_cast<uint32_t>(w->in), batch))
         throw Unsupported("matrix width/batch not covered by the HIP matvec kernels");
+    if (c->time_kernels) hold_stream(c, s);
     begin_timing(c, s, 0);
     launch_checked(pk::launch_matvec(w->type, w->dptr + offset, w->row_bytes,
                                      static_cast<uint32_t>(w->out), static_cast<uint32_t>(w->in),
@@ -299,6 +318,7 @@ void enqueue_moe(pk_hip_ctx* c, const pk_hip_moe_layer* L, const MoeShape& m, co
     a.act = c->act.ptr;
     a.counter = c->words.ptr + kStatusCounter;
     a.status = status_words(c);
+    if (c->time_kernels) hold_stream(c, s);
     begin_timing(c, s, 2);
     launch_checked(pk::launch_moe_router(a, s), "router launch");
     begin_timing(c, s, 3);
@@ -374,8 +394,14 @@ pk_hip_status pk_hip_create(int device, const pk_hip_options* options, pk_hip_ct
         c->device = dev;
         c->time_kernels = options && options->time_kernels;
         c->set_device();
+        int rate = 0;
+        if (hipDeviceGetAttribute(&rate, hipDeviceAttributeWallClockRate, dev) == hipSuccess &&
+            rate > 0)
+            c->wall_rate_khz = rate;
         check(hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking), "hipStreamCreate");
-        for (auto& e : c->ev) check(hipEventCreate(&e), "hipEventCreate");
+        // timing-only events: no system-scope fence (cache writeback) on record
+        for (auto& e : c->ev)
+            check(hipEventCreateWithFlags(&e, hipEventDisableSystemFence), "hipEventCreate");
         c->words.ensure(8);
         check(hipMemsetAsync(c->words.ptr, 0, 8 * sizeof(uint32_t), c->stream), "init status");
         check(hipStreamSynchronize(c->stream), "hipStreamSynchronize");

@@ -19,8 +19,7 @@
 //     weights (FP64 exp, FP32 probabilities, FP32 renormalisation, as
 //     route_experts).  Every (route, ffn row) pair then dots the gate and up
 //     rows of the selected expert with the register-resident input and
-//     stores the SwiGLU activation g / (1 + expf(-g)) * u (:682-684), while
-//     the selected down slices are pulled toward the device-side cache.
+//     stores the SwiGLU activation g / (1 + expf(-g)) * u (:682-684).
 //  3. k_down: a workgroup of top_k waves computes one down-row dot per route
 //     and combines them in route order, y = ((0 + p0*o0) + p1*o1) + ...
 //     (:688-690), deterministically and without atomics.
@@ -454,25 +453,6 @@ __global__ __launch_bounds__(256) void k_gate_up(MoeDecodeArgs a, uint32_t units
             }
         }
     }
-    // Pull this workgroup's share of the selected down slices toward the
-    // device-side cache while the gate/up stream is in flight; k_down then
-    // reads them without waiting on HBM.
-    uint32_t touch = 0u;
-    {
-        const uint32_t span = static_cast<uint32_t>(a.down_slice / 64u);  // 64-byte lines per slice
-        const uint32_t lines = span * a.top_k;
-        const uint32_t per_block = (lines + gridDim.x - 1u) / gridDim.x;
-        const uint32_t l0 = blockIdx.x * per_block;
-        for (uint32_t l = l0 + threadIdx.x; l < l0 + per_block && l < lines; l += blockDim.x) {
-            const uint32_t route_i = l / span, off = l % span;
-            uint32_t e = 0u;
-#pragma unroll
-            for (uint32_t r = 0; r < kMaxTopK; ++r)
-                if (route_i == r) e = w.sel[r];
-            touch ^= *reinterpret_cast<const uint32_t*>(a.down + static_cast<uint64_t>(e) * a.down_slice +
-                                                        64ull * off);
-        }
-    }
     if (!staged) {
         for (uint32_t i = threadIdx.x; i < a.hidden; i += blockDim.x) xs[i] = a.x[i];
         __syncthreads();
@@ -499,7 +479,6 @@ __global__ __launch_bounds__(256) void k_gate_up(MoeDecodeArgs a, uint32_t units
         const float us = group_sum_dyn(u[0], G);
         if (live && ul == G - 1u) a.act[item[q]] = (gs / (1.0f + expf(-gs))) * us;
     }
-    if (touch == 0x9e3779b9u && a.hidden == 0u) a.act[0] = 0.0f;  // keeps the touches alive
 }
 
 // ---------------------------------------------------------------------------
