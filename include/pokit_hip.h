@@ -87,6 +87,11 @@ pk_hip_status pk_hip_create(int device, const pk_hip_options* options, pk_hip_ct
                             char* error_buffer, size_t error_capacity);
 void pk_hip_destroy(pk_hip_ctx* ctx);
 
+/* Writes "<device name> (<gfx arch>, <CUs> CUs, <GiB> GiB)" of the context's
+ * device, truncated and NUL-terminated: VulkanLinearBackend::device_name
+ * (include/pokitlms/gpu/vulkan_linear.hpp:80). */
+pk_hip_status pk_hip_device_name(const pk_hip_ctx* ctx, char* buffer, size_t capacity);
+
 /* Uploads one GGUF tensor [in, out(, n_experts)] to HBM, where it stays
  * resident: the whole-model device cache of the Vulkan backend
  * (src/vulkan_linear.cpp:516-563) and, for expert tensors, the ExpertStore

@@ -34,6 +34,10 @@ def build(reference: bool = True) -> None:
     targets = ["all"]
     if reference and os.path.isdir(os.path.join(REFERENCE_ROOT, "src")):
         targets.append("ref")
+        # the C++ backend parity program links the product library
+        hiplib = os.path.join(os.path.dirname(HERE), "pokitlms_amd", "libpokit_hip.so")
+        if os.path.exists(hiplib):
+            targets.append("cases")
     subprocess.run(["make", "-s", "-C", HERE, "-j8", *targets], check=True)
 
 

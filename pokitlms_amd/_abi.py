@@ -26,7 +26,7 @@ EXPORTS = (
     "pk_hip_upload", "pk_hip_upload_device", "pk_hip_weight_release", "pk_hip_weight_bytes",
     "pk_hip_weight_device_ptr", "pk_hip_matvec", "pk_hip_matvec_async", "pk_hip_moe_decode",
     "pk_hip_moe_decode_async", "pk_hip_sync", "pk_hip_get_stats", "pk_hip_reset_stats",
-    "pk_hip_set_kernel_timing",
+    "pk_hip_set_kernel_timing", "pk_hip_device_name",
 )
 
 
@@ -103,5 +103,7 @@ def lib() -> ctypes.CDLL:
     L.pk_hip_reset_stats.argtypes = [vp]
     L.pk_hip_set_kernel_timing.restype = ctypes.c_int
     L.pk_hip_set_kernel_timing.argtypes = [vp, ctypes.c_int]
+    L.pk_hip_device_name.restype = ctypes.c_int
+    L.pk_hip_device_name.argtypes = [vp, cp, sz]
     _lib = L
     return L

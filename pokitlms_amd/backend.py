@@ -229,5 +229,12 @@ class HipBackend:
     def reset_stats(self) -> None:
         _abi.lib().pk_hip_reset_stats(self.handle)
 
+    def device_name(self) -> str:
+        buf = ctypes.create_string_buffer(256)
+        st = _abi.lib().pk_hip_device_name(self.handle, buf, len(buf))
+        if st not in (0, 3):
+            _raise(st, buf)
+        return buf.value.decode(errors="replace")
+
     def set_kernel_timing(self, enabled: bool) -> None:
         _abi.lib().pk_hip_set_kernel_timing(self.handle, 1 if enabled else 0)

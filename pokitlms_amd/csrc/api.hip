@@ -599,6 +599,22 @@ pk_hip_status pk_hip_get_stats(const pk_hip_ctx* ctx, pk_hip_stats* out) {
     return PK_HIP_STATUS_OK;
 }
 
+pk_hip_status pk_hip_device_name(const pk_hip_ctx* ctx, char* buf, size_t cap) {
+    if (!ctx || !buf || cap == 0) return PK_HIP_STATUS_INVALID_ARGUMENT;
+    hipDeviceProp_t prop{};
+    if (hipGetDeviceProperties(&prop, ctx->device) != hipSuccess) {
+        set_error(buf, cap, "hipGetDeviceProperties failed");
+        return PK_HIP_STATUS_RUNTIME_ERROR;
+    }
+    const std::string name = prop.name[0] ? std::string(prop.name)
+                                          : "HIP device " + std::to_string(ctx->device);
+    const std::string text = name + " (" + prop.gcnArchName + ", " +
+                             std::to_string(prop.multiProcessorCount) + " CUs, " +
+                             std::to_string(prop.totalGlobalMem >> 30) + " GiB)";
+    set_error(buf, cap, text.c_str());
+    return text.size() < cap ? PK_HIP_STATUS_OK : PK_HIP_STATUS_BUFFER_TOO_SMALL;
+}
+
 pk_hip_status pk_hip_set_kernel_timing(pk_hip_ctx* ctx, int enabled) {
     if (!ctx) return PK_HIP_STATUS_INVALID_ARGUMENT;
     std::lock_guard lock(ctx->mutex);

@@ -1,0 +1,298 @@
+// hip_linear_backend.cpp -- HipLinearBackend over the libpokit_hip C ABI.
+//
+// Mirrors the behaviour of VulkanLinearBackend::try_linear
+// (src/vulkan_linear.cpp:612-736): the same type gate, the same shape and
+// row-size checks with std::invalid_argument, one internal mutex, and a
+// permanent failed state after any device error.  Weights differ by design:
+// file-backed tensors are uploaded once and stay resident in HBM (keyed by
+// model file and offset); in-memory tensors are uploaded for the call.
+#include "hip_linear_backend.hpp"
+
+#include "pokit_hip.h"
+
+#include <array>
+#include <cstring>
+#include <limits>
+#include <map>
+#include <mutex>
+#include <stdexcept>
+#include <utility>
+#include <vector>
+
+namespace pokitlms::gpu {
+namespace {
+
+constexpr std::size_t kErrorCapacity = 512;
+
+struct ErrorBuffer {
+    std::array<char, kErrorCapacity> text{};
+    char* data() noexcept { return text.data(); }
+    [[nodiscard]] std::string str() const { return std::string(text.data()); }
+};
+
+// Encoded bytes of one row of `in` elements; 0 for types without a kernel.
+std::size_t encoded_row_bytes(std::uint32_t type, std::uint64_t in) {
+    switch (type) {
+        case 0: return in * 4;
+        case 1: case 30: return in * 2;
+        case 2: return in % 32 ? 0 : in / 32 * 18;
+        case 8: return in % 32 ? 0 : in / 32 * 34;
+        case 12: return in % 256 ? 0 : in / 256 * 144;
+        case 13: return in % 256 ? 0 : in / 256 * 176;
+        case 14: return in % 256 ? 0 : in / 256 * 210;
+        default: return 0;
+    }
+}
+
+bool block_aligned(std::uint32_t type, std::uint64_t in) {
+    switch (type) {
+        case 2: case 8: return in % 32 == 0;
+        case 12: case 13: case 14: return in % 256 == 0;
+        default: return true;
+    }
+}
+
+struct WeightDeleter {
+    void operator()(pk_hip_weight* w) const noexcept { pk_hip_weight_release(w); }
+};
+using WeightPtr = std::unique_ptr<pk_hip_weight, WeightDeleter>;
+
+}  // namespace
+
+class HipLinearBackend::Impl {
+public:
+    explicit Impl(const HipLinearOptions& options) : cache_file_tensors(options.cache_file_tensors) {
+        pk_hip_options opts{};
+        opts.struct_size = sizeof(opts);
+        opts.time_kernels = options.time_kernels ? 1U : 0U;
+        ErrorBuffer err;
+        const auto st = pk_hip_create(options.device_index, &opts, &ctx, err.data(), kErrorCapacity);
+        if (st == PK_HIP_STATUS_INVALID_ARGUMENT) throw std::invalid_argument(err.str());
+        if (st != PK_HIP_STATUS_OK) throw std::runtime_error("HIP backend: " + err.str());
+    }
+    ~Impl() {
+        resident.clear();  // weights before the context that owns them
+        if (ctx) pk_hip_destroy(ctx);
+    }
+    Impl(const Impl&) = delete;
+    Impl& operator=(const Impl&) = delete;
+
+    // Throws for a non-OK status: invalid_argument for argument errors,
+    // runtime_error for everything else.  A device error leaves the C context
+    // failed (every later call on it fails), and then this backend is failed
+    // for good too; a data error such as non-finite router logits does not.
+    void raise(pk_hip_status st, const ErrorBuffer& err) {
+        if (st == PK_HIP_STATUS_INVALID_ARGUMENT) throw std::invalid_argument(err.str());
+        ErrorBuffer probe;
+        if (pk_hip_sync(ctx, nullptr, probe.data(), kErrorCapacity) != PK_HIP_STATUS_OK)
+            failed = true;
+        throw std::runtime_error("HIP backend: " + err.str());
+    }
+
+    void require_usable() const {
+        if (failed) throw std::runtime_error("HIP backend failed during an earlier operation");
+    }
+
+    WeightPtr upload(const model::TensorReader& reader, std::uint64_t in, std::uint64_t out,
+                     std::uint32_t experts) {
+        const auto bytes = reader.read_all();
+        pk_hip_weight* w = nullptr;
+        ErrorBuffer err;
+        const auto st = pk_hip_upload(ctx, reader.tensor().type, in, out, experts, bytes.data(),
+                                      bytes.size(), &w, err.data(), kErrorCapacity);
+        if (st != PK_HIP_STATUS_OK) raise(st, err);
+        return WeightPtr(w);
+    }
+
+    // The resident copy of a file-backed matrix, uploading it on first use;
+    // nullptr for an in-memory reader (the caller uploads it for the call).
+    pk_hip_weight* resident_matrix(const model::TensorReader& reader, std::uint64_t in,
+                                   std::uint64_t out) {
+        const auto& file = reader.model_file();
+        if (!file || !cache_file_tensors) return nullptr;
+        const Key key{file.get(), reader.tensor().file_offset};
+        if (const auto it = resident.find(key); it != resident.end()) return it->second.get();
+        auto w = upload(reader, in, out, 0);
+        auto* raw = w.get();
+        resident.emplace(key, std::move(w));
+        ++counters.resident_tensors;
+        return raw;
+    }
+
+    using Key = std::pair<const void*, std::uint64_t>;
+
+    pk_hip_ctx* ctx = nullptr;
+    bool cache_file_tensors = true;
+    bool failed = false;
+    std::mutex mutex;
+    std::map<Key, WeightPtr> resident;
+    HipLinearStats counters{};  // fields the C ABI does not keep
+};
+
+class HipMoeLayer {
+public:
+    std::shared_ptr<HipLinearBackend::Impl> owner;
+    WeightPtr router, gate, up, down;
+    std::uint32_t hidden = 0, ffn = 0, experts = 0, top_k = 0;
+    bool normalize = false;
+    float scale = 1.0F;
+
+    ~HipMoeLayer() {
+        std::lock_guard lock(owner->mutex);
+        router.reset();
+        gate.reset();
+        up.reset();
+        down.reset();
+    }
+};
+
+HipLinearBackend::HipLinearBackend(const HipLinearOptions& options)
+    : impl_(std::make_shared<Impl>(options)) {}
+
+HipLinearBackend::~HipLinearBackend() = default;
+
+bool HipLinearBackend::try_linear(const model::TensorReader& weights,
+                                  std::span<const float> input, std::span<float> output) {
+    const auto& tensor = weights.tensor();
+    if (!pk_hip_type_supported(tensor.type)) {
+        std::lock_guard lock(impl_->mutex);
+        ++impl_->counters.unsupported_calls;
+        return false;
+    }
+    if (input.empty() || output.empty() || tensor.dimensions.empty() ||
+        tensor.dimensions.front() != input.size() || weights.row_count() != output.size()) {
+        throw std::invalid_argument("HIP matrix dimensions do not match input/output");
+    }
+    if (!block_aligned(tensor.type, input.size()))
+        throw std::invalid_argument("HIP quantized row is not block-aligned");
+    if (weights.row_bytes() != encoded_row_bytes(tensor.type, input.size()))
+        throw std::invalid_argument("HIP encoded row size mismatch");
+    if (input.size() > std::numeric_limits<std::uint32_t>::max() ||
+        output.size() > std::numeric_limits<std::uint32_t>::max()) {
+        std::lock_guard lock(impl_->mutex);
+        ++impl_->counters.unsupported_calls;
+        return false;
+    }
+    std::lock_guard lock(impl_->mutex);
+    impl_->require_usable();
+    pk_hip_weight* w = impl_->resident_matrix(weights, input.size(), output.size());
+    WeightPtr transient;
+    if (!w) {
+        transient = impl_->upload(weights, input.size(), output.size(), 0);
+        w = transient.get();
+        ++impl_->counters.transient_uploads;
+    }
+    ErrorBuffer err;
+    const auto st = pk_hip_matvec(impl_->ctx, w, UINT32_MAX, input.data(), 1, output.data(),
+                                  err.data(), kErrorCapacity);
+    if (st == PK_HIP_STATUS_UNSUPPORTED) {
+        ++impl_->counters.unsupported_calls;
+        return false;
+    }
+    if (st != PK_HIP_STATUS_OK) impl_->raise(st, err);
+    ++impl_->counters.linear_calls;
+    return true;
+}
+
+std::shared_ptr<HipMoeLayer> HipLinearBackend::upload_moe_layer(
+    const model::TensorReader& router, const model::TensorReader& gate_exps,
+    const model::TensorReader& up_exps, const model::TensorReader& down_exps,
+    std::size_t experts_per_token, bool expert_weights_norm, float expert_weights_scale) {
+    const auto& rd = router.tensor().dimensions;
+    const auto& gd = gate_exps.tensor().dimensions;
+    const auto& ud = up_exps.tensor().dimensions;
+    const auto& dd = down_exps.tensor().dimensions;
+    if (rd.size() != 2 || gd.size() != 3 || ud.size() != 3 || dd.size() != 3)
+        throw std::invalid_argument("HIP MoE layer: router must be 2-D and experts 3-D");
+    const std::uint64_t hidden = rd[0], experts = rd[1], ffn = gd[1];
+    if (gd != ud || gd[0] != hidden || gd[2] != experts || dd[0] != ffn || dd[1] != hidden ||
+        dd[2] != experts)
+        throw std::invalid_argument("HIP MoE layer: expert tensor dimensions disagree");
+    if (experts_per_token == 0 || experts_per_token > experts)
+        throw std::invalid_argument("HIP MoE layer: experts_per_token out of range");
+    if (hidden > UINT32_MAX || ffn > UINT32_MAX || experts > UINT32_MAX)
+        throw std::invalid_argument("HIP MoE layer: dimensions exceed 32 bits");
+    // The layer exists before the lock is taken, so if an upload throws it is
+    // destroyed (and takes the lock itself) only after the lock is released.
+    auto layer = std::make_shared<HipMoeLayer>();
+    layer->owner = impl_;
+    std::lock_guard lock(impl_->mutex);
+    impl_->require_usable();
+    const auto n = static_cast<std::uint32_t>(experts);
+    layer->router = impl_->upload(router, hidden, experts, 0);
+    layer->gate = impl_->upload(gate_exps, hidden, ffn, n);
+    layer->up = impl_->upload(up_exps, hidden, ffn, n);
+    layer->down = impl_->upload(down_exps, ffn, hidden, n);
+    layer->hidden = static_cast<std::uint32_t>(hidden);
+    layer->ffn = static_cast<std::uint32_t>(ffn);
+    layer->experts = static_cast<std::uint32_t>(experts);
+    layer->top_k = static_cast<std::uint32_t>(experts_per_token);
+    layer->normalize = expert_weights_norm;
+    layer->scale = expert_weights_scale;
+    return layer;
+}
+
+bool HipLinearBackend::try_moe_block(const HipMoeLayer& layer, std::span<const float> normalized,
+                                     std::span<float> moe_result,
+                                     std::span<std::uint32_t> route_ids,
+                                     std::span<float> route_probabilities) {
+    if (layer.owner != impl_)
+        throw std::invalid_argument("HIP MoE layer belongs to another backend");
+    if (normalized.size() != layer.hidden || moe_result.size() != layer.hidden)
+        throw std::invalid_argument("HIP MoE block: hidden size mismatch");
+    if ((!route_ids.empty() && route_ids.size() != layer.top_k) ||
+        (!route_probabilities.empty() && route_probabilities.size() != layer.top_k))
+        throw std::invalid_argument("HIP MoE block: route outputs must hold experts_per_token");
+    std::vector<std::uint32_t> ids(layer.top_k);
+    std::vector<float> probs(layer.top_k);
+    pk_hip_moe_layer desc{};
+    desc.router = layer.router.get();
+    desc.gate = layer.gate.get();
+    desc.up = layer.up.get();
+    desc.down = layer.down.get();
+    desc.top_k = layer.top_k;
+    desc.normalize = layer.normalize ? 1U : 0U;
+    desc.scale = layer.scale;
+    std::lock_guard lock(impl_->mutex);
+    impl_->require_usable();
+    ErrorBuffer err;
+    const auto st = pk_hip_moe_decode(impl_->ctx, &desc, normalized.data(), moe_result.data(),
+                                      ids.data(), probs.data(), err.data(), kErrorCapacity);
+    if (st == PK_HIP_STATUS_UNSUPPORTED) return false;
+    if (st != PK_HIP_STATUS_OK) impl_->raise(st, err);
+    if (!route_ids.empty()) std::copy(ids.begin(), ids.end(), route_ids.begin());
+    if (!route_probabilities.empty())
+        std::copy(probs.begin(), probs.end(), route_probabilities.begin());
+    ++impl_->counters.moe_calls;
+    return true;
+}
+
+HipLinearStats HipLinearBackend::stats() const {
+    std::lock_guard lock(impl_->mutex);
+    HipLinearStats out = impl_->counters;
+    pk_hip_stats s{};
+    if (pk_hip_get_stats(impl_->ctx, &s) == PK_HIP_STATUS_OK) {
+        out.dispatches = s.dispatches;
+        out.q4_0_dispatches = s.q4_0_dispatches;
+        out.q8_0_dispatches = s.q8_0_dispatches;
+        out.q4_k_dispatches = s.q4_k_dispatches;
+        out.q5_k_dispatches = s.q5_k_dispatches;
+        out.q6_k_dispatches = s.q6_k_dispatches;
+        out.other_dispatches = s.float_dispatches;
+        out.weight_bytes = s.weight_bytes;
+        out.gpu_time_ns = s.matvec_ns + s.router_ns + s.gate_up_ns + s.down_ns;
+        out.resident_bytes = s.resident_bytes;
+        out.uploaded_bytes = s.uploaded_bytes;
+        out.router_fallbacks = s.router_fallbacks;
+    }
+    return out;
+}
+
+std::string HipLinearBackend::device_name() const {
+    std::array<char, 256> text{};
+    std::lock_guard lock(impl_->mutex);
+    (void)pk_hip_device_name(impl_->ctx, text.data(), text.size());
+    return std::string(text.data());
+}
+
+}  // namespace pokitlms::gpu

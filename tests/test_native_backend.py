@@ -1,0 +1,48 @@
+"""The C++ HipLinearBackend (pokitlms_amd/host) inside the reference's own
+call sites: tests/native/hip_backend_cases.cpp, built by ``make -C oracle
+cases`` against the reference headers and CPU library in place.
+
+On the GPU it runs every case: try_linear through tensor_linear's backend hook
+(src/tensor_linear.cpp:213) for F32/F16/BF16/Q4_0/Q8_0/Q4_K/Q5_K/Q6_K against
+the CPU kernels; false for the formats without a kernel; shape errors;
+file-backed tensors kept resident; the MoE block hook against the reference
+MoE block (ids exact, outputs normwise <= 1e-4); a non-finite router as a
+data error that leaves the backend usable.
+"""
+import os
+import subprocess
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+CASES = os.path.join(ROOT, "oracle", "_ref", "hip_backend_cases")
+MISSING = ("oracle/_ref/hip_backend_cases is built only where the reference checkout "
+           "is present (make -C oracle cases)")
+
+
+def _run(*args, timeout):
+    r = subprocess.run([CASES, *args], capture_output=True, text=True, timeout=timeout)
+    print(r.stdout)
+    print(r.stderr[-4000:])
+    return r
+
+
+@pytest.mark.skipif(not os.path.exists(CASES), reason=MISSING)
+def test_native_backend_without_a_device_fails_cleanly():
+    import torch
+    if torch.cuda.device_count() > 0:
+        pytest.skip("a GPU is visible; the GPU test covers this host")
+    r = _run("--expect-no-device", timeout=60)
+    assert r.returncode == 0
+    assert r.stdout.startswith("PASS no_device HIP backend:")
+
+
+@pytest.mark.gpu
+@pytest.mark.skipif(not os.path.exists(CASES), reason=MISSING)
+def test_native_backend_cases():
+    r = _run(timeout=300)
+    assert r.returncode == 0, r.stdout[-3000:]
+    lines = r.stdout.splitlines()
+    assert not [l for l in lines if l.startswith("FAIL")]
+    assert sum(l.startswith("PASS try_linear_parity") for l in lines) == 8
+    assert sum(l.startswith("PASS moe_block_parity") for l in lines) == 2
