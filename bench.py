@@ -314,6 +314,7 @@ def main():
             "layers_rotated": args.layers, "tokens_rotated": args.tokens,
             "bytes_per_step": step_bytes,
             "timing": "eager" if args.eager else f"HIP graph replay, {chunk} steps per graph",
+            "launches_per_step": 3,
         },
         "pct_of_peak": round(100.0 * value / HBM_PEAK_GBS, 2),
         "eager_ms_per_step": round(eager_ms, 5),

@@ -93,7 +93,7 @@ struct pk_hip_ctx {
     uint64_t live_weights = 0;
     // scratch
     DeviceBuffer<float> x, y, act, probs;
-    DeviceBuffer<uint32_t> ids, words;  // words: [0] counter, [1..4] status
+    DeviceBuffer<uint32_t> ids, words;  // words: [1..4] status
     DeviceBuffer<double> row_sum, row_bound;
     hipEvent_t ev[8] = {};
     int wall_rate_khz = 100000;  // wall_clock64() rate
@@ -112,7 +112,7 @@ struct pk_hip_weight {
 
 namespace {
 
-constexpr uint32_t kStatusCounter = 0, kStatusError = 1;
+constexpr uint32_t kStatusError = 1;
 
 uint32_t* status_words(pk_hip_ctx* c) { return c->words.ptr + 1; }
 
@@ -316,7 +316,6 @@ void enqueue_moe(pk_hip_ctx* c, const pk_hip_moe_layer* L, const MoeShape& m, co
     a.row_sum = c->row_sum.ptr;
     a.row_bound = c->row_bound.ptr;
     a.act = c->act.ptr;
-    a.counter = c->words.ptr + kStatusCounter;
     a.status = status_words(c);
     if (c->time_kernels) hold_stream(c, s);
     begin_timing(c, s, 2);
@@ -326,11 +325,11 @@ void enqueue_moe(pk_hip_ctx* c, const pk_hip_moe_layer* L, const MoeShape& m, co
     begin_timing(c, s, 4);
     launch_checked(pk::launch_moe_down(a, s), "down launch");
     begin_timing(c, s, 5);
-    ++c->stats.moe_decode_calls;
     ++c->stats.router_launches;
     ++c->stats.gate_up_launches;
     ++c->stats.down_launches;
     c->stats.dispatches += 3;
+    ++c->stats.moe_decode_calls;
     count_dispatch(c, L->gate->type);
     count_dispatch(c, L->down->type);
     c->stats.dispatches -= 2;  // the two per-format counts above are the same launches

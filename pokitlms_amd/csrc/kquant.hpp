@@ -72,12 +72,14 @@ __device__ __forceinline__ void ld_weights(const uint8_t* p, uint32_t (&w)[N]) {
     else ld_words<N>(p, w);
 }
 
+// The dword-aligned address below p is formed by pointer subtraction (not by
+// masking an integer), so the compiler keeps the global address space and
+// emits global loads.
 template <int N>
 __device__ __forceinline__ void ld_words_2a(const uint8_t* p, uint32_t (&w)[N]) {
-    const uintptr_t a = reinterpret_cast<uintptr_t>(p);
-    const uint32_t shift = static_cast<uint32_t>(a & 3u);
+    const uint32_t shift = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(p) & 3u);
     uint32_t raw[N + 1];
-    ld_words<N + 1>(reinterpret_cast<const uint8_t*>(a & ~uintptr_t{3}), raw);
+    ld_words<N + 1>(p - shift, raw);
 #pragma unroll
     for (int i = 0; i < N; ++i) w[i] = __builtin_amdgcn_alignbyte(raw[i + 1], raw[i], shift);
 }
@@ -229,16 +231,13 @@ __device__ __forceinline__ void unit_load(const uint8_t* __restrict__ row, const
         }
     } else {
         const uint8_t* qp = T == T_Q6_K ? blk + p.k0 : blk + 2 + p.k0;
-        const uintptr_t a = reinterpret_cast<uintptr_t>(qp);
-        r.shift = static_cast<uint32_t>(a & 3u);
-        ld_weights<NW + 1>(reinterpret_cast<const uint8_t*>(a & ~uintptr_t{3}), r.q);
+        r.shift = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(qp) & 3u);
+        ld_weights<NW + 1>(qp - r.shift, r.q);  // pointer arithmetic keeps global loads
         if constexpr (T == T_Q6_K) {
             const uint32_t kk = p.k0 % 64u;
             const uint8_t* hp = blk + 128u + 32u * (p.k0 / 64u) + (kk % 32u);
             // qh and ql share the block's alignment (both offsets are even)
-            ld_weights<NW + 1>(reinterpret_cast<const uint8_t*>(
-                                   reinterpret_cast<uintptr_t>(hp) & ~uintptr_t{3}),
-                               r.qh);
+            ld_weights<NW + 1>(hp - r.shift, r.qh);
             const uint32_t sidx = (p.col[0] % 256u) / 16u;
             r.s0 = static_cast<int8_t>(blk[192u + sidx]);
             r.s1 = static_cast<int8_t>(blk[192u + sidx + 4u]);

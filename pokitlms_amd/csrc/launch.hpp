@@ -41,7 +41,6 @@ struct MoeDecodeArgs {
     double* row_sum;         // [n_experts]
     double* row_bound;       // [n_experts]
     float* act;              // [top_k][ffn]
-    uint32_t* counter;       // 1 word, zero between calls
     uint32_t* status;        // [4]: error flag, serial-fallback count, candidates, spare
 };
 

@@ -8,22 +8,27 @@
 //     rigorous bound B on how far the CPU's serial, unfused FP32 sum
 //     (src/linear.cpp:26-30, src/simd_kernels.hpp:22) can be from S:
 //         |serial - S| <= u * sum_i |T_i| / (1 - n u),  T_i = exact prefix sums.
-//  2. k_gate_up: every wave first ranks the experts by S (no LDS, no
-//     barrier).  When the intervals [S-B, S+B] prove the top-k set and
-//     order, that ranking is the CPU's; otherwise the workgroup recomputes
-//     every expert that could still enter the top-k with the CPU's exact
-//     serial FP32 recurrence and ranks those bit-exact logits.  (Ranking in
-//     a separate launch costs a dependent round trip per step; ranking at
-//     the end of k_router needs a device-wide fence per workgroup, which on
-//     this GPU writes back the whole L2.)  Workgroup 0 writes ids and route
-//     weights (FP64 exp, FP32 probabilities, FP32 renormalisation, as
-//     route_experts).  Every (route, ffn row) pair then dots the gate and up
-//     rows of the selected expert with the register-resident input and
-//     stores the SwiGLU activation g / (1 + expf(-g)) * u (:682-684).
+//  2. k_gate_up: wave 0 of every workgroup ranks the experts by S and shares
+//     the result through LDS.  When the intervals [S-B, S+B] prove the
+//     top-k set and order, that ranking is the CPU's; otherwise the
+//     workgroup recomputes every expert that could still enter the top-k
+//     with the CPU's exact serial FP32 recurrence and ranks those bit-exact
+//     logits.  Workgroup 0 writes ids and route weights (FP64 exp, FP32
+//     probabilities, FP32 renormalisation, as route_experts).  Every (route,
+//     ffn row) pair then dots the gate and up rows of the selected expert
+//     with the register-resident input and stores the SwiGLU activation
+//     g / (1 + expf(-g)) * u (:682-684).
 //  3. k_down: a workgroup of top_k waves computes one down-row dot per route
 //     and combines them in route order, y = ((0 + p0*o0) + p1*o1) + ...
 //     (:688-690), deterministically and without atomics.
-// Every wave issues the loads of all its rows before it consumes any.
+//
+// Ranking lives in every gate/up workgroup because on this GPU any handoff
+// between workgroups of one launch costs several dependent memory round
+// trips (a release fence writes back the whole L2; coherent stores, counter
+// atomics and polls each cost about a microsecond), more than the kernel
+// boundary it would save.  Every wave issues all its loads before it consumes
+// any: a load inside a branch, or behind a use, waits for every load issued
+// before it.
 #include <math.h>
 
 #include "kquant.hpp"
@@ -38,7 +43,8 @@ constexpr uint32_t kMaxTopK = 8;      // routes per token: waves of the down/com
 constexpr uint32_t kGateUpPasses = 2;  // row passes whose loads a gate/up wave keeps in flight
 constexpr uint32_t kDownPasses = 2;    // row passes per down workgroup
 
-// Status words (MoeDecodeArgs::status).
+// Status words (MoeDecodeArgs::status).  ST_ERROR: 1 = non-finite router
+// logits; it stays set until the host reads and clears it.
 enum : uint32_t { ST_ERROR = 0, ST_FALLBACKS = 1, ST_CANDIDATES = 2 };
 
 // route_experts' sorted-insertion order: larger logit first, then smaller id.
@@ -153,7 +159,7 @@ __device__ __forceinline__ double slot_value(const double (&v)[kSlots], uint32_t
     return readlane_d(x, e & 63u);
 }
 
-// Routes as every wave computes them, without LDS or barriers.
+// Routes as one wave computes them, without LDS or barriers.
 struct WaveRoutes {
     uint32_t sel[kMaxTopK];
     float logit[kSlots];  // FP32 of S for experts lane + 64 * m (-inf past n_experts)
@@ -166,7 +172,26 @@ struct WaveRoutes {
 // replaced by 255 - id).  The key only proposes an order: certification
 // below checks it against the exact intervals, so an ordering the truncated
 // key gets wrong is never certified and goes to the exact path.
-__device__ __forceinline__ WaveRoutes wave_route(const MoeDecodeArgs& a) {
+// The routing data of the experts lane + 64 * m, loaded before anything
+// uses it (absent experts re-read expert 0): a load inside a branch would
+// wait for every load issued before it.
+struct RouteData {
+    double S[kSlots], B[kSlots];
+};
+
+__device__ __forceinline__ RouteData load_route_data(const MoeDecodeArgs& a) {
+    const uint32_t lane = threadIdx.x & 63u, E = a.n_experts;
+    RouteData d;
+#pragma unroll
+    for (uint32_t m = 0; m < kSlots; ++m) {
+        const uint32_t e = lane + 64u * m;
+        d.S[m] = a.row_sum[e < E ? e : 0u];
+        d.B[m] = a.row_bound[e < E ? e : 0u];
+    }
+    return d;
+}
+
+__device__ __forceinline__ WaveRoutes wave_route(const MoeDecodeArgs& a, const RouteData& d) {
     const uint32_t lane = threadIdx.x & 63u;
     const uint32_t E = a.n_experts, K = a.top_k;
     double S[kSlots], B[kSlots];
@@ -174,16 +199,20 @@ __device__ __forceinline__ WaveRoutes wave_route(const MoeDecodeArgs& a) {
     bool fin = true;
 #pragma unroll
     for (uint32_t m = 0; m < kSlots; ++m) {
+        S[m] = d.S[m];
+        B[m] = d.B[m];
+    }
+#pragma unroll
+    for (uint32_t m = 0; m < kSlots; ++m) {
         const uint32_t e = lane + 64u * m;
-        S[m] = 0.0;
-        B[m] = 0.0;
         key[m] = 0u;
         if (e < E) {
-            S[m] = a.row_sum[e];
-            B[m] = a.row_bound[e];
             const float f = static_cast<float>(S[m]);
             fin = fin && isfinite(f);
             key[m] = (order_key(f) & ~0xffu) | (255u - e);
+        } else {
+            S[m] = 0.0;
+            B[m] = 0.0;
         }
     }
     WaveRoutes w;
@@ -237,7 +266,7 @@ struct FallbackShared {
 };
 
 __device__ __forceinline__ void exact_routes(const MoeDecodeArgs& a, double lo_min_sel,
-                                             const float* xs, FallbackShared& fb) {
+                                             const float* xs, FallbackShared& fb, bool count) {
     const uint32_t t = threadIdx.x, E = a.n_experts;
     if (t < E) {
         const double s = a.row_sum[t], b = a.row_bound[t];
@@ -247,12 +276,12 @@ __device__ __forceinline__ void exact_routes(const MoeDecodeArgs& a, double lo_m
         if (!(s + b < lo_min_sel)) {
             fb.logit[t] = static_cast<double>(
                 serial_logit(a.router + static_cast<uint64_t>(t) * a.hidden, xs, a.hidden));
-            if (blockIdx.x == 0) atomicAdd(a.status + ST_CANDIDATES, 1u);
+            if (count) atomicAdd(a.status + ST_CANDIDATES, 1u);
         } else {
             fb.logit[t] = static_cast<double>(static_cast<float>(s));
         }
     }
-    if (t == 0 && blockIdx.x == 0) atomicAdd(a.status + ST_FALLBACKS, 1u);
+    if (t == 0 && count) atomicAdd(a.status + ST_FALLBACKS, 1u);
     if (t == 0) fb.bad = 0u;
     __syncthreads();
     // route_experts throws on any non-finite logit (src/qwen3_moe_runner.cpp:270-276)
@@ -261,10 +290,10 @@ __device__ __forceinline__ void exact_routes(const MoeDecodeArgs& a, double lo_m
     rank_select(fb.logit, E, a.top_k, fb.rank, fb.sel);
 }
 
-// Workgroup 0, wave 0: route weights as route_experts (FP64 softmax over all
-// experts, FP32 probabilities, FP32 renormalisation, optional scale), written
-// with the ids.  l[m] is the FP32 logit the ranking used for expert
-// lane + 64 * m (unused slots: -inf).
+// Wave 0 of gate/up workgroup 0: route weights as route_experts (FP64
+// softmax over all experts, FP32 probabilities, FP32 renormalisation,
+// optional scale), written with the ids.  l[m] is the FP32 logit the ranking
+// used for expert lane + 64 * m (unused slots: -inf).
 __device__ __forceinline__ void write_routes(const MoeDecodeArgs& a, const uint32_t (&sel)[kMaxTopK],
                                              const float (&l)[kSlots]) {
     const uint32_t lane = threadIdx.x & 63u, K = a.top_k;
@@ -302,7 +331,6 @@ __device__ __forceinline__ void write_routes(const MoeDecodeArgs& a, const uint3
         a.ids[lane] = my_id;
         a.probs[lane] = q;
     }
-    if (lane == 0) a.status[ST_ERROR] = 0u;
 }
 
 // ---------------------------------------------------------------------------
@@ -367,53 +395,108 @@ __global__ __launch_bounds__(kRouterThreads) void k_router(MoeDecodeArgs a) {
         a.row_sum[e] = total;
         a.row_bound[e] = bound;
     }
-
 }
 
 // ---------------------------------------------------------------------------
 // 2. Routing + gate/up + SwiGLU.  All (route, row) items share the input x,
 // so one unit mapping (and one register copy of x per lane) serves them all.
 
+// Marks a router error (wave 0 of gate/up workgroup 0): route_experts throws
+// on non-finite logits (src/qwen3_moe_runner.cpp:270-276).
+__device__ __forceinline__ void flag_router_error(const MoeDecodeArgs& a) {
+    const uint32_t lane = threadIdx.x & 63u;
+    if (lane == 0) atomicOr(a.status + ST_ERROR, 1u);
+    if (lane < a.top_k) {
+        a.ids[lane] = 0xffffffffu;
+        a.probs[lane] = 0.0f;
+    }
+}
+
+// A workgroup's share of a float vector held in registers: float4 pieces
+// i * blockDim + threadIdx, i < kXPieces (hidden <= 4 * 256 * kXPieces).  All
+// loads are issued before any is used.
+constexpr uint32_t kXPieces = 8;  // hidden <= 8192, the widest router (32 * 256)
+struct XRegs {
+    float4 v[kXPieces];
+};
+
+// Pieces past the end load and store the last piece again (the same values
+// as its own thread writes), so neither the loads nor the stores sit in a
+// branch: a load sunk into a branch next to its use would wait for every
+// load issued before it.
+__device__ __forceinline__ uint32_t x_piece(uint32_t i, uint32_t n) {
+    const uint32_t k = (i * blockDim.x + threadIdx.x) * 4u;
+    return k < n ? k : n - 4u;
+}
+
+__device__ __forceinline__ XRegs load_x_regs(const float* x, uint32_t n) {
+    XRegs r;
+#pragma unroll
+    for (uint32_t i = 0; i < kXPieces; ++i)
+        r.v[i] = *reinterpret_cast<const float4*>(x + x_piece(i, n));
+    return r;
+}
+
+__device__ __forceinline__ void store_x_regs(float* xs, const XRegs& r, uint32_t n) {
+#pragma unroll
+    for (uint32_t i = 0; i < kXPieces; ++i) *reinterpret_cast<float4*>(xs + x_piece(i, n)) = r.v[i];
+}
+
+// The ranking wave 0 hands to the workgroup.
+struct SharedRoutes {
+    uint32_t sel[kMaxTopK];
+    uint32_t state;  // 0 certified, 1 needs the exact path, 2 a logit is not finite
+    double lo_min_sel;
+};
+
 template <int T, int UB, int NU, int NP>
 __global__ __launch_bounds__(256) void k_gate_up(MoeDecodeArgs a, uint32_t units, uint32_t glog2) {
-    extern __shared__ float xs[];  // [hidden]
+    extern __shared__ __attribute__((aligned(16))) float xs[];  // [hidden]
     __shared__ FallbackShared fb;
+    __shared__ SharedRoutes sr;
     const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
-    WaveRoutes w = wave_route(a);
-    if (!w.finite) {
-        // route_experts throws on non-finite logits (src/qwen3_moe_runner.cpp:270-276)
-        if (blockIdx.x == 0 && wave == 0) {
-            if (lane == 0) a.status[ST_ERROR] = 1u;
-            if (lane < a.top_k) {
-                a.ids[lane] = 0xffffffffu;
-                a.probs[lane] = 0.0f;
-            }
+    const bool first_wave = blockIdx.x == 0 && wave == 0;
+    // x and (wave 0) the routing data go out together; x is stored first
+    const XRegs xr = load_x_regs(a.x, a.hidden);
+    RouteData rd;
+    if (wave == 0) rd = load_route_data(a);
+    store_x_regs(xs, xr, a.hidden);
+    WaveRoutes w;
+    if (wave == 0) {
+        w = wave_route(a, rd);
+        if (lane == 0) {
+#pragma unroll
+            for (uint32_t r = 0; r < kMaxTopK; ++r) sr.sel[r] = w.sel[r];
+            sr.state = !w.finite ? 2u : w.certified ? 0u : 1u;
+            sr.lo_min_sel = w.lo_min_sel;
         }
+    }
+    __syncthreads();
+    const uint32_t state = sr.state;  // uniform
+    if (state == 2u) {
+        if (first_wave) flag_router_error(a);
         return;
     }
-    bool staged = false;
-    if (!w.certified) {  // uniform over the workgroup: every wave saw the same data
-        for (uint32_t i = threadIdx.x; i < a.hidden; i += blockDim.x) xs[i] = a.x[i];
-        __syncthreads();
-        staged = true;
-        exact_routes(a, w.lo_min_sel, xs, fb);
-        if (fb.bad) {  // uniform: every wave reads the same flag
-            if (blockIdx.x == 0 && wave == 0) {
-                if (lane == 0) a.status[ST_ERROR] = 1u;
-                if (lane < a.top_k) {
-                    a.ids[lane] = 0xffffffffu;
-                    a.probs[lane] = 0.0f;
-                }
-            }
+    uint32_t sel[kMaxTopK];
+    if (state == 1u) {  // rare: exact serial logits of the candidates
+        exact_routes(a, sr.lo_min_sel, xs, fb, blockIdx.x == 0);
+        if (fb.bad) {  // uniform
+            if (first_wave) flag_router_error(a);
             return;
         }
 #pragma unroll
-        for (uint32_t r = 0; r < kMaxTopK; ++r) w.sel[r] = r < a.top_k ? fb.sel[r] : 0u;
+        for (uint32_t r = 0; r < kMaxTopK; ++r) sel[r] = r < a.top_k ? fb.sel[r] : 0u;
+        if (first_wave) {
 #pragma unroll
-        for (uint32_t m = 0; m < kSlots; ++m)
-            w.logit[m] = lane + 64u * m < a.n_experts ? static_cast<float>(fb.logit[lane + 64u * m])
-                                                      : -INFINITY;
+            for (uint32_t m = 0; m < kSlots; ++m)
+                w.logit[m] = lane + 64u * m < a.n_experts ? static_cast<float>(fb.logit[lane + 64u * m])
+                                                          : -INFINITY;
+        }
+    } else {
+#pragma unroll
+        for (uint32_t r = 0; r < kMaxTopK; ++r) sel[r] = sr.sel[r];
     }
+    if (first_wave) write_routes(a, sel, w.logit);
 
     const uint32_t G = 1u << glog2, RPP = 64u >> glog2;
     const uint32_t sub = lane >> glog2, ul = lane & (G - 1u);
@@ -429,35 +512,28 @@ __global__ __launch_bounds__(256) void k_gate_up(MoeDecodeArgs a, uint32_t units
     const uint32_t passes = (items + RPP - 1u) / RPP;
     const uint32_t first = (blockIdx.x * (blockDim.x >> 6) + wave) * NP;
 
-    // weights first: every load of this wave's rows is in flight before x arrives
+    // Loads are unconditional (items past the end re-read the last item,
+    // absent units re-read unit 0, results unused), so no branch splits
+    // them and none waits on another.
     UnitRaw<T, UB> rg[NP][NU], ru[NP][NU];
     uint32_t item[NP];
 #pragma unroll
     for (int q = 0; q < NP; ++q) {
-        const uint32_t p = first + q;
-        item[q] = p * RPP + sub;
-        if (p < passes && item[q] < items) {
-            const uint32_t route_i = item[q] / a.ffn, row = item[q] % a.ffn;
-            uint32_t e = 0u;
+        item[q] = (first + q) * RPP + sub;
+        const uint32_t it = item[q] < items ? item[q] : items - 1u;
+        const uint32_t route_i = it / a.ffn, row = it % a.ffn;
+        uint32_t e = 0u;
 #pragma unroll
-            for (uint32_t r = 0; r < kMaxTopK; ++r)
-                if (route_i == r) e = w.sel[r];
-            const uint8_t* gr = a.gate + static_cast<uint64_t>(e) * a.gate_slice + row * a.gate_row;
-            const uint8_t* ur = a.up + static_cast<uint64_t>(e) * a.up_slice + row * a.up_row;
+        for (uint32_t r = 0; r < kMaxTopK; ++r)
+            if (route_i == r) e = sel[r];
+        const uint8_t* gr = a.gate + static_cast<uint64_t>(e) * a.gate_slice + row * a.gate_row;
+        const uint8_t* ur = a.up + static_cast<uint64_t>(e) * a.up_slice + row * a.up_row;
 #pragma unroll
-            for (int k = 0; k < NU; ++k) {
-                if (valid[k]) {
-                    unit_load<T, UB>(gr, pos[k], rg[q][k]);
-                    unit_load<T, UB>(ur, pos[k], ru[q][k]);
-                }
-            }
+        for (int k = 0; k < NU; ++k) {
+            unit_load<T, UB>(gr, pos[k], rg[q][k]);
+            unit_load<T, UB>(ur, pos[k], ru[q][k]);
         }
     }
-    if (!staged) {
-        for (uint32_t i = threadIdx.x; i < a.hidden; i += blockDim.x) xs[i] = a.x[i];
-        __syncthreads();
-    }
-    if (blockIdx.x == 0 && wave == 0) write_routes(a, w.sel, w.logit);
     UnitX<T, UB, 1> ux[NU];
 #pragma unroll
     for (int k = 0; k < NU; ++k) load_unit_x<T, UB, 1>(xs, 0, pos[k], valid[k], ux[k]);
@@ -480,6 +556,7 @@ __global__ __launch_bounds__(256) void k_gate_up(MoeDecodeArgs a, uint32_t units
         if (live && ul == G - 1u) a.act[item[q]] = (gs / (1.0f + expf(-gs))) * us;
     }
 }
+
 
 // ---------------------------------------------------------------------------
 // 3. down + combine.  blockDim = 64 * top_k: wave k owns route k; the
@@ -506,16 +583,14 @@ __global__ __launch_bounds__(64 * kMaxTopK) void k_down(MoeDecodeArgs a, uint32_
     const uint8_t* base = a.down + e * a.down_slice;
     const uint32_t rows = a.hidden;
     const uint32_t row0 = blockIdx.x * kDownPasses * RPP;
+    // unconditional loads (rows past the end re-read the last row, unused)
     UnitRaw<T, UB> raw[kDownPasses][NU];
 #pragma unroll
     for (int p = 0; p < kDownPasses; ++p) {
         const uint32_t row = row0 + p * RPP + sub;
-        if (ok && row < rows) {
-            const uint8_t* rp = base + static_cast<uint64_t>(row) * a.down_row;
+        const uint8_t* rp = base + static_cast<uint64_t>(row < rows ? row : rows - 1u) * a.down_row;
 #pragma unroll
-            for (int q = 0; q < NU; ++q)
-                if (valid[q]) unit_load<T, UB>(rp, pos[q], raw[p][q]);
-        }
+        for (int q = 0; q < NU; ++q) unit_load<T, UB>(rp, pos[q], raw[p][q]);
     }
     UnitX<T, UB, 1> ux[NU];
     const float* act = a.act + k * a.ffn;
@@ -647,7 +722,7 @@ hipError_t launch_moe_router(const MoeDecodeArgs& a, hipStream_t s) {
     switch (a.hidden / kRouterThreads) {
 #define PK_RT(C)                                                                                \
     case C:                                                                                     \
-        hipLaunchKernelGGL(k_router<C>, dim3(a.n_experts), dim3(kRouterThreads), 0, s, a); \
+        hipLaunchKernelGGL(k_router<C>, dim3(a.n_experts), dim3(kRouterThreads), a.hidden * sizeof(float), s, a); \
         break;
         PK_RT(2) PK_RT(4) PK_RT(8) PK_RT(12) PK_RT(16) PK_RT(24) PK_RT(32)
 #undef PK_RT

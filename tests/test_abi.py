@@ -37,11 +37,26 @@ def test_version_and_type_table():
         assert lib.pk_hip_type_supported(t) == 0
 
 
+def header_stats_fields():
+    text = open(os.path.join(ROOT, "include", "pokit_hip.h")).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    body = re.search(r"typedef struct pk_hip_stats \{(.*?)\} pk_hip_stats;", text, re.S).group(1)
+    names = []
+    for decl in body.split(";"):
+        decl = decl.strip()
+        if decl:
+            assert decl.startswith("uint64_t "), decl
+            names += [n.strip() for n in decl[len("uint64_t "):].split(",")]
+    return names
+
+
 def test_struct_layouts_match_header():
     # pk_hip_moe_layer: 4 pointers, two uint32, one float (+ tail padding)
     assert ctypes.sizeof(_abi.MoeLayerDesc) == 4 * 8 + 4 + 4 + 4 + 4
     assert ctypes.sizeof(_abi.Options) == 8
-    assert ctypes.sizeof(_abi.Stats) == 24 * 8
+    # pk_hip_stats: every field uint64_t, same names in the same order
+    assert [n for n, _ in _abi.Stats._fields_] == header_stats_fields()
+    assert ctypes.sizeof(_abi.Stats) == 8 * len(header_stats_fields())
 
 
 def test_null_arguments_are_rejected_without_a_device():

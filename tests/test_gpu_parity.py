@@ -317,3 +317,92 @@ def test_stats_track_resident_experts(hip, c3):
     assert st["moe_decode_calls"] == 1 and st["expert_hits"] == 8 and st["expert_misses"] == 0
     assert st["weight_bytes"] == h.routed_bytes() == 25_526_272
     assert st["resident_bytes"] >= h.router.nbytes + h.gate.nbytes + h.up.nbytes + h.down.nbytes
+
+
+# ---- more layer shapes, near ties at another width, graph replays ------------------------
+# (hidden, experts, ffn, top_k, gate/up type, down type)
+LAYER_SHAPES = (
+    (1024, 64, 512, 8, S.Q4_K, S.Q6_K),
+    (2048, 128, 768, 8, S.Q4_K, S.Q4_K),
+    (2048, 64, 768, 6, S.Q5_K, S.Q6_K),
+    (1024, 32, 256, 4, S.Q8_0, S.Q8_0),
+    (4096, 64, 1536, 8, S.Q4_K, S.Q6_K),
+)
+
+
+@pytest.mark.parametrize("shape", LAYER_SHAPES, ids=lambda s: f"{s[0]}x{s[1]}x{s[2]}k{s[3]}t{s[4]}-{s[5]}")
+def test_moe_layer_shapes_against_cpu(hip, port, shape):
+    hidden, experts, ffn, k, gt, dt = shape
+    say("layer shape", shape)
+    layer = S.moe_layer(seed=110 + hidden + ffn, hidden=hidden, experts=experts, ffn=ffn,
+                        gate_type=gt, up_type=gt, down_type=dt, top_k=k)
+    h = hip.upload_moe_layer(layer)
+    blk = port.moe(layer)
+    for t in range(6):
+        x = S.normal_f32(S.rng(1100 + t), hidden)
+        y, ids, probs = hip.moe_decode(h, x)
+        cy, cids, cprobs = blk.forward(x)
+        assert np.array_equal(ids, cids)
+        assert np.max(np.abs(probs - cprobs)) <= TOL * np.max(cprobs)
+        assert normwise_rel(y, cy) <= TOL
+    h.release()
+
+
+def test_near_ties_at_width_1024(hip, port):
+    """Near-tied router rows at a second width: the exact serial ranking
+    decides, and the ids equal the CPU's on every token."""
+    g = S.rng(130)
+    router = S.normal_f32(g, 64 * 1024, 0.02).reshape(64, 1024)
+    for j in range(0, 64, 2):
+        router[j + 1] = router[j]
+        kk = int(g.integers(0, 1024))
+        router[j + 1, kk] = np.nextafter(router[j, kk], np.float32(1))
+    layer = S.moe_layer(seed=131, hidden=1024, experts=64, ffn=512, top_k=8)
+    layer.router = router
+    h = hip.upload_moe_layer(layer)
+    blk = port.moe(layer)
+    hip.reset_stats()
+    for t in range(12):
+        x = S.normal_f32(g, 1024)
+        y, ids, _ = hip.moe_decode(h, x)
+        cy, cids, _ = blk.forward(x)
+        assert np.array_equal(ids, cids), (t, ids, cids)
+        assert normwise_rel(y, cy) <= TOL
+    st = hip.stats()
+    say("width-1024 near-tie fallbacks", st["router_fallbacks"])
+    assert st["router_fallbacks"] > 0
+    h.release()
+
+
+def test_graph_replays_match_eager(hip, c3):
+    """A HIP graph of several layers, replayed repeatedly with eager work and
+    synchronisation between replays, reproduces the eager results every time
+    (no memset node is recorded)."""
+    import torch
+    _, h = c3
+    dev = torch.device("cuda:0")
+    xs = torch.from_numpy(G.c3_tokens(4)).to(dev)
+    ys = torch.empty(4, 2048, device=dev)
+    ids = torch.empty(4, 8, dtype=torch.int32, device=dev)
+    ps = torch.empty(4, 8, device=dev)
+    stream = torch.cuda.Stream()
+
+    def run(s):
+        for t in range(4):
+            hip.moe_decode_async(h, xs[t].data_ptr(), ys[t].data_ptr(), ids[t].data_ptr(),
+                                 ps[t].data_ptr(), s)
+    with torch.cuda.stream(stream):
+        run(stream.cuda_stream)
+    hip.sync(stream.cuda_stream)
+    y_ref, i_ref = ys.clone(), ids.clone()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=stream):
+        run(torch.cuda.current_stream().cuda_stream)
+    for rep in range(4):
+        ys.zero_()
+        ids.zero_()
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        hip.sync(0)
+        assert torch.equal(ys, y_ref) and torch.equal(ids, i_ref), rep
