@@ -150,40 +150,51 @@ __device__ __forceinline__ double readlane_d(double v, uint32_t lane) {
     return __builtin_bit_cast(double, r);
 }
 
-constexpr uint32_t kSlots = kMaxExperts / 64;  // candidates per lane
+// Experts sit in the lane/slot layout e = lane + 64 * slot: NS slots per lane
+// cover up to 64 * NS experts.
+constexpr int slots_for(uint32_t experts) { return experts <= 64 ? 1 : experts <= 128 ? 2 : 4; }
 
-// Expert e's value from the lane/slot layout e = lane + 64 * slot (e uniform).
-__device__ __forceinline__ double slot_value(const double (&v)[kSlots], uint32_t e) {
-    const uint32_t slot = e >> 6;
-    const double x = slot == 0 ? v[0] : slot == 1 ? v[1] : slot == 2 ? v[2] : v[3];
+// Expert e's entry (e uniform) of a per-lane slot array.
+template <int NS>
+__device__ __forceinline__ double slot_at(const double (&v)[NS], uint32_t e) {
+    double x = v[0];
+#pragma unroll
+    for (int m = 1; m < NS; ++m) x = (e >> 6) == static_cast<uint32_t>(m) ? v[m] : x;
     return readlane_d(x, e & 63u);
+}
+template <int NS>
+__device__ __forceinline__ float slot_at(const float (&v)[NS], uint32_t e) {
+    float x = v[0];
+#pragma unroll
+    for (int m = 1; m < NS; ++m) x = (e >> 6) == static_cast<uint32_t>(m) ? v[m] : x;
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x),
+                                                               static_cast<int>(e & 63u)));
 }
 
 // Routes as one wave computes them, without LDS or barriers.
+template <int NS>
 struct WaveRoutes {
     uint32_t sel[kMaxTopK];
-    float logit[kSlots];  // FP32 of S for experts lane + 64 * m (-inf past n_experts)
+    float logit[NS];  // FP32 of S for experts lane + 64 * m (-inf past n_experts)
     bool certified;
     bool finite;
     double lo_min_sel;
 };
 
-// Top-k by (S desc, id asc) using 32-bit keys (FP32 value with its low byte
-// replaced by 255 - id).  The key only proposes an order: certification
-// below checks it against the exact intervals, so an ordering the truncated
-// key gets wrong is never certified and goes to the exact path.
 // The routing data of the experts lane + 64 * m, loaded before anything
 // uses it (absent experts re-read expert 0): a load inside a branch would
 // wait for every load issued before it.
+template <int NS>
 struct RouteData {
-    double S[kSlots], B[kSlots];
+    double S[NS], B[NS];
 };
 
-__device__ __forceinline__ RouteData load_route_data(const MoeDecodeArgs& a) {
+template <int NS>
+__device__ __forceinline__ RouteData<NS> load_route_data(const MoeDecodeArgs& a) {
     const uint32_t lane = threadIdx.x & 63u, E = a.n_experts;
-    RouteData d;
+    RouteData<NS> d;
 #pragma unroll
-    for (uint32_t m = 0; m < kSlots; ++m) {
+    for (int m = 0; m < NS; ++m) {
         const uint32_t e = lane + 64u * m;
         d.S[m] = a.row_sum[e < E ? e : 0u];
         d.B[m] = a.row_bound[e < E ? e : 0u];
@@ -191,68 +202,63 @@ __device__ __forceinline__ RouteData load_route_data(const MoeDecodeArgs& a) {
     return d;
 }
 
-__device__ __forceinline__ WaveRoutes wave_route(const MoeDecodeArgs& a, const RouteData& d) {
+// Top-k by (S desc, id asc) using 32-bit keys (FP32 value with its low byte
+// replaced by 255 - id).  The key only proposes an order: certification
+// below checks it against the exact intervals [S - B, S + B], so an ordering
+// the truncated key gets wrong is never certified and goes to the exact
+// path.  Branch-free: always kMaxTopK selection rounds (ranks past top_k
+// only tighten the check), each taking the winner's interval by readlane.
+template <int NS>
+__device__ __forceinline__ WaveRoutes<NS> wave_route(const MoeDecodeArgs& a, const RouteData<NS>& d) {
     const uint32_t lane = threadIdx.x & 63u;
     const uint32_t E = a.n_experts, K = a.top_k;
-    double S[kSlots], B[kSlots];
-    uint32_t key[kSlots];
+    uint32_t key[NS];
+    double lo[NS], hi[NS];
     bool fin = true;
+    WaveRoutes<NS> w;
 #pragma unroll
-    for (uint32_t m = 0; m < kSlots; ++m) {
-        S[m] = d.S[m];
-        B[m] = d.B[m];
-    }
-#pragma unroll
-    for (uint32_t m = 0; m < kSlots; ++m) {
+    for (int m = 0; m < NS; ++m) {
         const uint32_t e = lane + 64u * m;
-        key[m] = 0u;
-        if (e < E) {
-            const float f = static_cast<float>(S[m]);
-            fin = fin && isfinite(f);
-            key[m] = (order_key(f) & ~0xffu) | (255u - e);
-        } else {
-            S[m] = 0.0;
-            B[m] = 0.0;
-        }
+        const bool present = e < E;
+        const float f = static_cast<float>(d.S[m]);
+        fin = fin && (!present || isfinite(f));
+        key[m] = present ? (order_key(f) & ~0xffu) | (255u - e) : 0u;
+        lo[m] = d.S[m] - d.B[m];
+        hi[m] = d.S[m] + d.B[m];
+        w.logit[m] = present ? f : -INFINITY;
     }
-    WaveRoutes w;
     w.finite = __all(fin);
-#pragma unroll
-    for (uint32_t m = 0; m < kSlots; ++m)
-        w.logit[m] = lane + 64u * m < E ? static_cast<float>(S[m]) : -INFINITY;
+    double lo_r[kMaxTopK], hi_r[kMaxTopK];
 #pragma unroll
     for (uint32_t r = 0; r < kMaxTopK; ++r) {
-        if (r >= K) {
-            w.sel[r] = 0u;
-            continue;
-        }
         uint32_t mk = key[0];
 #pragma unroll
-        for (uint32_t m = 1; m < kSlots; ++m) mk = max(mk, key[m]);
+        for (int m = 1; m < NS; ++m) mk = max(mk, key[m]);
         const uint32_t best = wave_max_u32(mk);
-        w.sel[r] = 255u - (best & 0xffu);
+        const uint32_t e = 255u - (best & 0xffu);
+        w.sel[r] = e;
+        const bool present = best != 0u;  // fewer than kMaxTopK experts
+        lo_r[r] = present ? slot_at<NS>(lo, e) : -INFINITY;
+        hi_r[r] = present ? slot_at<NS>(hi, e) : -INFINITY;
 #pragma unroll
-        for (uint32_t m = 0; m < kSlots; ++m)
-            if (key[m] == best) key[m] = 0u;
+        for (int m = 0; m < NS; ++m) key[m] = key[m] == best ? 0u : key[m];
     }
-    // certified when lo(sel[r]) > max hi over everything ranked after r
-    double hi_rest = -INFINITY;
-#pragma unroll
-    for (uint32_t m = 0; m < kSlots; ++m)
-        if (key[m] != 0u) hi_rest = fmax(hi_rest, S[m] + B[m]);
-    double after = lane63(group_max<64>(hi_rest));
+    // route r < top_k is certain when its lower bound clears the upper bound
+    // of everything ranked after it
+    double after = -INFINITY, lmin = INFINITY;
     bool ok = true;
-    double lmin = INFINITY;
 #pragma unroll
-    for (int r = kMaxTopK - 1; r >= 0; --r) {  // constant indices keep sel in registers
-        if (static_cast<uint32_t>(r) < K) {
-            const double s = slot_value(S, w.sel[r]), b = slot_value(B, w.sel[r]);
-            ok = ok && (s - b > after);
-            after = fmax(after, s + b);
-            lmin = fmin(lmin, s - b);
-        }
+    for (int r = kMaxTopK - 1; r >= 0; --r) {
+        const bool routed = static_cast<uint32_t>(r) < K;
+        ok = ok && (!routed || lo_r[r] > after);
+        lmin = routed ? fmin(lmin, lo_r[r]) : lmin;
+        after = fmax(after, hi_r[r]);
     }
-    w.certified = ok;
+    // ... including every expert outside the first kMaxTopK ranks
+    bool reach = false;
+#pragma unroll
+    for (int m = 0; m < NS; ++m) reach = reach || (key[m] != 0u && hi[m] >= lmin);
+    w.certified = ok && !__any(reach);
     w.lo_min_sel = lmin;
     return w;
 }
@@ -294,16 +300,14 @@ __device__ __forceinline__ void exact_routes(const MoeDecodeArgs& a, double lo_m
 // softmax over all experts, FP32 probabilities, FP32 renormalisation,
 // optional scale), written with the ids.  l[m] is the FP32 logit the ranking
 // used for expert lane + 64 * m (unused slots: -inf).
+template <int NS>
 __device__ __forceinline__ void write_routes(const MoeDecodeArgs& a, const uint32_t (&sel)[kMaxTopK],
-                                             const float (&l)[kSlots]) {
+                                             const float (&l)[NS]) {
     const uint32_t lane = threadIdx.x & 63u, K = a.top_k;
-    double ld[kSlots];
-#pragma unroll
-    for (uint32_t m = 0; m < kSlots; ++m) ld[m] = static_cast<double>(l[m]);
-    const float mxf = static_cast<float>(slot_value(ld, sel[0]));
+    const float mxf = slot_at<NS>(l, sel[0]);
     double ex = 0.0;
 #pragma unroll
-    for (uint32_t m = 0; m < kSlots; ++m)
+    for (int m = 0; m < NS; ++m)
         if (lane + 64u * m < a.n_experts) ex += exp(static_cast<double>(l[m] - mxf));
     const double denom = lane63(group_sum<64>(ex));
     float mine = mxf;  // logit of route `lane`
@@ -311,7 +315,7 @@ __device__ __forceinline__ void write_routes(const MoeDecodeArgs& a, const uint3
 #pragma unroll
     for (uint32_t r = 0; r < kMaxTopK; ++r) {
         if (r < K) {
-            const float v = static_cast<float>(slot_value(ld, sel[r]));
+            const float v = slot_at<NS>(l, sel[r]);
             if (lane == r) {
                 mine = v;
                 my_id = sel[r];
@@ -449,7 +453,7 @@ struct SharedRoutes {
     double lo_min_sel;
 };
 
-template <int T, int UB, int NU, int NP>
+template <int T, int UB, int NU, int NP, int NS>
 __global__ __launch_bounds__(256) void k_gate_up(MoeDecodeArgs a, uint32_t units, uint32_t glog2) {
     extern __shared__ __attribute__((aligned(16))) float xs[];  // [hidden]
     __shared__ FallbackShared fb;
@@ -458,12 +462,12 @@ __global__ __launch_bounds__(256) void k_gate_up(MoeDecodeArgs a, uint32_t units
     const bool first_wave = blockIdx.x == 0 && wave == 0;
     // x and (wave 0) the routing data go out together; x is stored first
     const XRegs xr = load_x_regs(a.x, a.hidden);
-    RouteData rd;
-    if (wave == 0) rd = load_route_data(a);
+    RouteData<NS> rd;
+    if (wave == 0) rd = load_route_data<NS>(a);
     store_x_regs(xs, xr, a.hidden);
-    WaveRoutes w;
+    WaveRoutes<NS> w;
     if (wave == 0) {
-        w = wave_route(a, rd);
+        w = wave_route<NS>(a, rd);
         if (lane == 0) {
 #pragma unroll
             for (uint32_t r = 0; r < kMaxTopK; ++r) sr.sel[r] = w.sel[r];
@@ -488,7 +492,7 @@ __global__ __launch_bounds__(256) void k_gate_up(MoeDecodeArgs a, uint32_t units
         for (uint32_t r = 0; r < kMaxTopK; ++r) sel[r] = r < a.top_k ? fb.sel[r] : 0u;
         if (first_wave) {
 #pragma unroll
-            for (uint32_t m = 0; m < kSlots; ++m)
+            for (int m = 0; m < NS; ++m)
                 w.logit[m] = lane + 64u * m < a.n_experts ? static_cast<float>(fb.logit[lane + 64u * m])
                                                           : -INFINITY;
         }
@@ -496,7 +500,7 @@ __global__ __launch_bounds__(256) void k_gate_up(MoeDecodeArgs a, uint32_t units
 #pragma unroll
         for (uint32_t r = 0; r < kMaxTopK; ++r) sel[r] = sr.sel[r];
     }
-    if (first_wave) write_routes(a, sel, w.logit);
+    if (first_wave) write_routes<NS>(a, sel, w.logit);
 
     const uint32_t G = 1u << glog2, RPP = 64u >> glog2;
     const uint32_t sub = lane >> glog2, ul = lane & (G - 1u);
@@ -656,12 +660,17 @@ hipError_t gate_up_t(const MoeDecodeArgs& a, hipStream_t s) {
     const uint32_t passes = ceil_div(a.top_k * a.ffn, RPP);
     const uint32_t blocks = ceil_div(passes, 4u * kGateUpPasses);
     const size_t lds = a.hidden * sizeof(float);
-#define PK_GU(N)                                                                              \
-    case N:                                                                                   \
-        hipLaunchKernelGGL((k_gate_up<T, UB, N, kGateUpPasses>), dim3(blocks), dim3(256), lds, s, a, units, \
-                           glog2);                                                            \
-        break;
-    switch (nu) { PK_GU(1) PK_GU(2) default: return hipErrorInvalidValue; }
+#define PK_GU(N, NS)                                                                            \
+    hipLaunchKernelGGL((k_gate_up<T, UB, N, kGateUpPasses, NS>), dim3(blocks), dim3(256), lds, s, a, \
+                       units, glog2)
+    const int ns = slots_for(a.n_experts);
+    if (nu == 1 && ns == 1) PK_GU(1, 1);
+    else if (nu == 1 && ns == 2) PK_GU(1, 2);
+    else if (nu == 1 && ns == 4) PK_GU(1, 4);
+    else if (nu == 2 && ns == 1) PK_GU(2, 1);
+    else if (nu == 2 && ns == 2) PK_GU(2, 2);
+    else if (nu == 2 && ns == 4) PK_GU(2, 4);
+    else return hipErrorInvalidValue;
 #undef PK_GU
     return hipGetLastError();
 }
