@@ -72,6 +72,7 @@ typedef struct pk_hip_stats {
     /* Device time in ns; filled when pk_hip_options.time_kernels != 0. */
     uint64_t matvec_ns, router_ns, gate_up_ns, down_ns;
     uint64_t router_launches, gate_up_launches, down_launches, matvec_launches;
+    uint64_t prefill_calls, prefill_tokens, prefill_ns;
 } pk_hip_stats;
 
 const char* pk_hip_version(void);
@@ -164,6 +165,28 @@ pk_hip_status pk_hip_moe_decode_async(pk_hip_ctx* ctx, const pk_hip_moe_layer* l
                                       const float* device_x, float* device_y,
                                       uint32_t* device_ids, float* device_probs, void* stream,
                                       char* error_buffer, size_t error_capacity);
+
+/* A batch of tokens through one MoE layer: the prompt loop of the reference
+ * (src/qwen3_moe_runner.cpp:785-790), whose tokens each take the MoE block
+ * (:644-691) independently.  x [tokens][hidden] holds the normalised hidden
+ * states; y [tokens][hidden], ids and probs [tokens][top_k] receive each
+ * token's moe_result and routes, equal to pk_hip_moe_decode's for that token
+ * (ids bit-exact, outputs within FP32 reassociation).  Tokens are grouped per
+ * expert and the expert products run as FP32 MFMA GEMMs.  1 <= tokens <=
+ * 4096; gate/up and down of any K-quant/Q8_0/Q4_0 type, ffn a multiple of
+ * 256.  Host buffers; synchronous.  Non-finite router logits return
+ * RUNTIME_ERROR. */
+pk_hip_status pk_hip_moe_prefill(pk_hip_ctx* ctx, const pk_hip_moe_layer* layer, const float* x,
+                                 uint32_t tokens, float* y, uint32_t* ids, float* probs,
+                                 char* error_buffer, size_t error_capacity);
+
+/* Device-buffer variant, enqueued on `stream` without synchronising.  The
+ * first call for a given batch shape allocates scratch; capture it into a
+ * HIP graph only after one such call. */
+pk_hip_status pk_hip_moe_prefill_async(pk_hip_ctx* ctx, const pk_hip_moe_layer* layer,
+                                       const float* device_x, uint32_t tokens, float* device_y,
+                                       uint32_t* device_ids, float* device_probs, void* stream,
+                                       char* error_buffer, size_t error_capacity);
 
 /* Waits for the context's work (and `stream`, if not NULL) and reports any
  * deferred router error. */

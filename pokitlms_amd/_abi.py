@@ -26,7 +26,8 @@ EXPORTS = (
     "pk_hip_upload", "pk_hip_upload_device", "pk_hip_weight_release", "pk_hip_weight_bytes",
     "pk_hip_weight_device_ptr", "pk_hip_matvec", "pk_hip_matvec_async", "pk_hip_moe_decode",
     "pk_hip_moe_decode_async", "pk_hip_sync", "pk_hip_get_stats", "pk_hip_reset_stats",
-    "pk_hip_set_kernel_timing", "pk_hip_device_name",
+    "pk_hip_set_kernel_timing", "pk_hip_device_name", "pk_hip_moe_prefill",
+    "pk_hip_moe_prefill_async",
 )
 
 
@@ -41,7 +42,7 @@ class Stats(ctypes.Structure):
         "weight_bytes", "resident_bytes", "uploaded_bytes", "router_fallbacks",
         "router_candidates", "expert_hits", "expert_misses", "matvec_ns", "router_ns",
         "gate_up_ns", "down_ns", "router_launches", "gate_up_launches", "down_launches",
-        "matvec_launches")]
+        "matvec_launches", "prefill_calls", "prefill_tokens", "prefill_ns")]
 
     def as_dict(self) -> dict:
         return {n: getattr(self, n) for n, _ in self._fields_}
@@ -104,6 +105,11 @@ def lib() -> ctypes.CDLL:
     L.pk_hip_set_kernel_timing.restype = ctypes.c_int
     L.pk_hip_set_kernel_timing.argtypes = [vp, ctypes.c_int]
     L.pk_hip_device_name.restype = ctypes.c_int
+    L.pk_hip_moe_prefill.restype = ctypes.c_int
+    L.pk_hip_moe_prefill.argtypes = [vp, ctypes.POINTER(MoeLayerDesc), fp, u32, fp, up, fp, cp, sz]
+    L.pk_hip_moe_prefill_async.restype = ctypes.c_int
+    L.pk_hip_moe_prefill_async.argtypes = [vp, ctypes.POINTER(MoeLayerDesc), vp, u32, vp, vp, vp,
+                                           vp, cp, sz]
     L.pk_hip_device_name.argtypes = [vp, cp, sz]
     _lib = L
     return L

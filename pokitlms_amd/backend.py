@@ -217,6 +217,32 @@ class HipBackend:
                                                   device_x, device_y, device_ids, device_probs,
                                                   stream or None, err, _ERRBUF), err)
 
+    def moe_prefill(self, layer: MoeLayerHandles, x: np.ndarray):
+        """A batch of tokens x [tokens, hidden] through the layer; per token the
+        result of moe_decode (the reference's prompt loop, one token at a time:
+        src/qwen3_moe_runner.cpp:785-790)."""
+        xx = np.ascontiguousarray(x, dtype=np.float32)
+        if xx.ndim != 2 or xx.shape[1] != layer.hidden:
+            raise ValueError(f"x must be [tokens, {layer.hidden}], got {xx.shape}")
+        tokens = xx.shape[0]
+        y = np.empty((tokens, layer.hidden), dtype=np.float32)
+        ids = np.zeros((tokens, layer.top_k), dtype=np.uint32)
+        probs = np.zeros((tokens, layer.top_k), dtype=np.float32)
+        err = ctypes.create_string_buffer(_ERRBUF)
+        _raise(_abi.lib().pk_hip_moe_prefill(self.handle, ctypes.byref(layer.desc), _f32p(xx),
+                                             tokens, _f32p(y),
+                                             ids.ctypes.data_as(ctypes.POINTER(ctypes.c_uint32)),
+                                             _f32p(probs), err, _ERRBUF), err)
+        return y, ids, probs
+
+    def moe_prefill_async(self, layer: MoeLayerHandles, device_x: int, tokens: int, device_y: int,
+                          device_ids: int, device_probs: int, stream: int = 0) -> None:
+        err = ctypes.create_string_buffer(_ERRBUF)
+        _raise(_abi.lib().pk_hip_moe_prefill_async(self.handle, ctypes.byref(layer.desc),
+                                                   device_x, tokens, device_y, device_ids,
+                                                   device_probs, stream or None, err, _ERRBUF),
+               err)
+
     def sync(self, stream: int = 0) -> None:
         err = ctypes.create_string_buffer(_ERRBUF)
         _raise(_abi.lib().pk_hip_sync(self.handle, stream or None, err, _ERRBUF), err)

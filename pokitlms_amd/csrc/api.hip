@@ -95,6 +95,10 @@ struct pk_hip_ctx {
     DeviceBuffer<float> x, y, act, probs;
     DeviceBuffer<uint32_t> ids, words;  // words: [1..4] status
     DeviceBuffer<double> row_sum, row_bound;
+    // prefill scratch (grown on demand; counts stay zero between calls)
+    DeviceBuffer<float> px, py, pprobs, pact, pout;
+    DeviceBuffer<uint32_t> pids, pcounts, poffsets, ptiles, pperm;
+    DeviceBuffer<double> prow_sum, prow_bound;
     hipEvent_t ev[8] = {};
     int wall_rate_khz = 100000;  // wall_clock64() rate
 
@@ -272,6 +276,11 @@ MoeShape check_layer(pk_hip_ctx* c, const pk_hip_moe_layer* L) {
         throw ArgError("MoE tensor dimensions do not match");
     if (L->top_k == 0 || L->top_k > m.experts) throw ArgError("invalid expert top-k");
     if (!(L->scale > 0.0f) || !(L->scale < 1.0e30f)) throw ArgError("invalid route scale");
+    return m;
+}
+
+MoeShape check_decode_layer(pk_hip_ctx* c, const pk_hip_moe_layer* L) {
+    const MoeShape m = check_layer(c, L);
     if (!pk::moe_decode_supported(L->gate->type, L->up->type, L->down->type, m.hidden, m.ffn,
                                   m.experts, L->top_k))
         throw Unsupported("MoE shape not covered by the HIP kernels");
@@ -422,6 +431,10 @@ void pk_hip_destroy(pk_hip_ctx* c) {
     c->words.release();
     c->row_sum.release();
     c->row_bound.release();
+    for (auto* b : {&c->px, &c->py, &c->pprobs, &c->pact, &c->pout}) b->release();
+    for (auto* b : {&c->pids, &c->pcounts, &c->poffsets, &c->ptiles, &c->pperm}) b->release();
+    c->prow_sum.release();
+    c->prow_bound.release();
     for (auto& e : c->ev)
         if (e) (void)hipEventDestroy(e);
     if (c->stream) (void)hipStreamDestroy(c->stream);
@@ -532,7 +545,7 @@ pk_hip_status pk_hip_moe_decode(pk_hip_ctx* ctx, const pk_hip_moe_layer* layer, 
         require_usable(ctx);
         if (!x || !y || !ids || !probs) throw ArgError("input and output buffers are required");
         std::lock_guard lock(ctx->mutex);
-        const MoeShape m = check_layer(ctx, layer);
+        const MoeShape m = check_decode_layer(ctx, layer);
         ctx->set_device();
         ctx->x.ensure(m.hidden);
         ctx->y.ensure(m.hidden);
@@ -563,13 +576,149 @@ pk_hip_status pk_hip_moe_decode_async(pk_hip_ctx* ctx, const pk_hip_moe_layer* l
         require_usable(ctx);
         if (!dx || !dy || !dids || !dprobs) throw ArgError("device buffers are required");
         std::lock_guard lock(ctx->mutex);
-        const MoeShape m = check_layer(ctx, layer);
+        const MoeShape m = check_decode_layer(ctx, layer);
         ctx->set_device();
         hipStream_t s = stream ? static_cast<hipStream_t>(stream) : ctx->stream;
         enqueue_moe(ctx, layer, m, dx, dy, dids, dprobs, s);
         if (ctx->time_kernels) {
             check(hipStreamSynchronize(s), "hipStreamSynchronize");
             collect_timing_moe(ctx);
+        }
+    });
+}
+
+namespace {
+
+MoeShape check_prefill(pk_hip_ctx* c, const pk_hip_moe_layer* L, uint32_t tokens) {
+    const MoeShape m = check_layer(c, L);
+    if (tokens == 0 || tokens > pk::kMaxPrefillTokens)
+        throw ArgError("prefill token count must be between 1 and " +
+                       std::to_string(pk::kMaxPrefillTokens));
+    if (!pk::moe_prefill_supported(L->gate->type, L->up->type, L->down->type, m.hidden, m.ffn,
+                                   m.experts, L->top_k, tokens))
+        throw Unsupported("MoE prefill shape not covered by the HIP kernels");
+    return m;
+}
+
+void enqueue_prefill(pk_hip_ctx* c, const pk_hip_moe_layer* L, const MoeShape& m, uint32_t tokens,
+                     const float* dx, float* dy, uint32_t* dids, float* dprobs, hipStream_t s) {
+    const uint64_t T = tokens, K = L->top_k, E = m.experts;
+    const uint32_t max_tiles = pk::moe_prefill_max_tiles(tokens, L->top_k, m.experts);
+    if (c->pcounts.count < E) {  // counts must start at zero; later calls leave them zero
+        c->pcounts.ensure(E);
+        check(hipMemsetAsync(c->pcounts.ptr, 0, E * sizeof(uint32_t), s), "clear counts");
+    }
+    c->prow_sum.ensure(T * E);
+    c->prow_bound.ensure(T * E);
+    c->poffsets.ensure(E + 1);
+    c->ptiles.ensure(static_cast<size_t>(max_tiles) + 1);
+    c->pperm.ensure(T * K);
+    c->pact.ensure(T * K * m.ffn);
+    c->pout.ensure(T * K * m.hidden);
+    pk::MoePrefillArgs a{};
+    pk::MoeDecodeArgs& l = a.layer;
+    l.router = reinterpret_cast<const float*>(L->router->dptr);
+    l.gate = L->gate->dptr;
+    l.up = L->up->dptr;
+    l.down = L->down->dptr;
+    l.gate_type = L->gate->type;
+    l.up_type = L->up->type;
+    l.down_type = L->down->type;
+    l.gate_slice = L->gate->slice_bytes;
+    l.up_slice = L->up->slice_bytes;
+    l.down_slice = L->down->slice_bytes;
+    l.gate_row = L->gate->row_bytes;
+    l.up_row = L->up->row_bytes;
+    l.down_row = L->down->row_bytes;
+    l.hidden = m.hidden;
+    l.ffn = m.ffn;
+    l.n_experts = m.experts;
+    l.top_k = L->top_k;
+    l.normalize = L->normalize ? 1u : 0u;
+    l.scale = L->scale;
+    l.status = status_words(c);
+    a.tokens = tokens;
+    a.max_tiles = max_tiles;
+    a.x = dx;
+    a.y = dy;
+    a.ids = dids;
+    a.probs = dprobs;
+    a.row_sum = c->prow_sum.ptr;
+    a.row_bound = c->prow_bound.ptr;
+    a.counts = c->pcounts.ptr;
+    a.offsets = c->poffsets.ptr;
+    a.tiles = c->ptiles.ptr;
+    a.n_tiles = c->ptiles.ptr + max_tiles;
+    a.perm = c->pperm.ptr;
+    a.act = c->pact.ptr;
+    a.out = c->pout.ptr;
+    a.status = status_words(c);
+    if (c->time_kernels) hold_stream(c, s);
+    begin_timing(c, s, 6);
+    launch_checked(pk::launch_moe_prefill(a, s), "prefill launch");
+    begin_timing(c, s, 7);
+    ++c->stats.prefill_calls;
+    c->stats.prefill_tokens += tokens;
+    c->stats.dispatches += 6;
+    count_dispatch(c, L->gate->type);
+    count_dispatch(c, L->down->type);
+    c->stats.dispatches -= 2;
+}
+
+void collect_timing_prefill(pk_hip_ctx* c) {
+    if (c->time_kernels) c->stats.prefill_ns += elapsed_ns(c, 6, 7);
+}
+
+}  // namespace
+
+pk_hip_status pk_hip_moe_prefill(pk_hip_ctx* ctx, const pk_hip_moe_layer* layer, const float* x,
+                                 uint32_t tokens, float* y, uint32_t* ids, float* probs,
+                                 char* err, size_t cap) {
+    return guarded(ctx, err, cap, [&] {
+        require_usable(ctx);
+        if (!x || !y || !ids || !probs) throw ArgError("input and output buffers are required");
+        std::lock_guard lock(ctx->mutex);
+        const MoeShape m = check_prefill(ctx, layer, tokens);
+        ctx->set_device();
+        const uint64_t T = tokens, K = layer->top_k;
+        ctx->px.ensure(T * m.hidden);
+        ctx->py.ensure(T * m.hidden);
+        ctx->pids.ensure(T * K);
+        ctx->pprobs.ensure(T * K);
+        check(hipMemcpyAsync(ctx->px.ptr, x, T * m.hidden * sizeof(float), hipMemcpyHostToDevice,
+                             ctx->stream),
+              "copy input");
+        enqueue_prefill(ctx, layer, m, tokens, ctx->px.ptr, ctx->py.ptr, ctx->pids.ptr,
+                        ctx->pprobs.ptr, ctx->stream);
+        check(hipMemcpyAsync(y, ctx->py.ptr, T * m.hidden * sizeof(float), hipMemcpyDeviceToHost,
+                             ctx->stream),
+              "copy output");
+        check(hipMemcpyAsync(ids, ctx->pids.ptr, T * K * sizeof(uint32_t), hipMemcpyDeviceToHost,
+                             ctx->stream),
+              "copy ids");
+        check(hipMemcpyAsync(probs, ctx->pprobs.ptr, T * K * sizeof(float),
+                             hipMemcpyDeviceToHost, ctx->stream),
+              "copy probabilities");
+        sync_and_check(ctx, ctx->stream);
+        collect_timing_prefill(ctx);
+    });
+}
+
+pk_hip_status pk_hip_moe_prefill_async(pk_hip_ctx* ctx, const pk_hip_moe_layer* layer,
+                                       const float* dx, uint32_t tokens, float* dy,
+                                       uint32_t* dids, float* dprobs, void* stream, char* err,
+                                       size_t cap) {
+    return guarded(ctx, err, cap, [&] {
+        require_usable(ctx);
+        if (!dx || !dy || !dids || !dprobs) throw ArgError("device buffers are required");
+        std::lock_guard lock(ctx->mutex);
+        const MoeShape m = check_prefill(ctx, layer, tokens);
+        ctx->set_device();
+        hipStream_t s = stream ? static_cast<hipStream_t>(stream) : ctx->stream;
+        enqueue_prefill(ctx, layer, m, tokens, dx, dy, dids, dprobs, s);
+        if (ctx->time_kernels) {
+            check(hipStreamSynchronize(s), "hipStreamSynchronize");
+            collect_timing_prefill(ctx);
         }
     });
 }

@@ -144,3 +144,93 @@ def dyadic_matrix(gtype: int, rows: int, in_features: int, gen: np.random.Genera
 def dyadic_vector(gen: np.random.Generator, n: int) -> np.ndarray:
     """Activations k/16 with k in [-16, 16]."""
     return (gen.integers(-16, 17, size=n).astype(np.float32) / 16.0).astype(np.float32)
+
+
+# ---- skewed expert load for batched prefill ------------------------------------------
+
+def zipf_targets(tokens: int, experts: int, top_k: int, s: float = 1.1) -> np.ndarray:
+    """Expected tokens per expert, by load rank, under Zipf(s): shares
+    proportional to rank**-s of the tokens * top_k (token, route) pairs.  A
+    token picks distinct experts, so no expert can take more than ``tokens``;
+    capped ranks hold exactly ``tokens`` and the rest share what is left in
+    the same proportions."""
+    w = np.arange(1, experts + 1, dtype=np.float64) ** -s
+    total = float(tokens * top_k)
+    capped = np.zeros(experts, bool)
+    while True:
+        t = np.where(capped, float(tokens), 0.0)
+        free = ~capped
+        t[free] = (total - tokens * capped.sum()) * w[free] / w[free].sum()
+        over = free & (t > tokens)
+        if not over.any():
+            return t
+        capped |= over
+
+
+def zipf_direction(seed: int, hidden: int) -> np.ndarray:
+    g = rng(seed)
+    u = g.standard_normal(hidden)
+    return u / np.linalg.norm(u)
+
+
+def pin_direction(z: np.ndarray, u: np.ndarray, a: float = 1.0) -> np.ndarray:
+    """Tokens N(0, 1) with their component along the unit vector ``u`` set to
+    ``a``: every token then shares the term a * (W_e . u) of its router logits,
+    while each coordinate stays within |u_i| (about hidden**-0.5) of N(0, 1)."""
+    z = np.asarray(z, np.float64)
+    return (z - np.outer(z @ u, u) + a * u).astype(np.float32)
+
+
+def zipf_router(layer: "MoeLayer", seed: int, s: float = 1.1, calib_tokens: int = 4096,
+                iters: int = 200) -> tuple[np.ndarray, np.ndarray]:
+    """Router rows (float32 [experts, hidden]) that realise a Zipf(s) expert
+    load on tokens drawn by ``zipf_tokens(seed, ...)``.
+
+    The reference router is a bias-free matvec (src/qwen3_moe_runner.cpp:
+    645-646), so the skew is carried by the rows: W_e = G_e + beta_e * u with
+    G_e ~ N(0, 1/hidden) (logit noise of unit variance) and u the tokens'
+    pinned direction.  The offsets beta_e are fitted on ``calib_tokens``
+    tokens drawn independently of the measured ones, so that expert e's
+    share of the top-k selections matches the Zipf target of its load rank;
+    ranks are assigned to expert ids in a seeded random order.  Returns the
+    router and each expert's target share: its expected picks per token
+    (the shares sum to top_k; multiply by a token count for counts)."""
+    E, H, K = layer.experts, layer.hidden, layer.top_k
+    g = rng(seed + 1)
+    u = zipf_direction(seed, H)
+    G = g.standard_normal((E, H)) / np.sqrt(H)
+    share = zipf_targets(1, E, K, s)               # per token, sums to K
+    share = share[g.permutation(E)]                # rank -> expert id
+    zc = pin_direction(rng(seed + 2).standard_normal((calib_tokens, H)), u, 0.0)
+    noise = zc.astype(np.float64) @ G.T           # [calib, E]
+    target = np.clip(share, 1.0 / calib_tokens, 1.0 - 0.5 / calib_tokens)
+    bias = np.log(target) * 2.0
+    for _ in range(iters):
+        logits = noise + bias
+        kth = np.partition(logits, E - K, axis=1)[:, E - K][:, None]
+        freq = (logits >= kth).mean(axis=0)
+        step = np.log(target) - np.log(np.maximum(freq, 0.25 / calib_tokens))
+        bias += 0.5 * step
+    beta = bias - G @ u                           # a = 1: logit bias = (G_e . u + beta_e)
+    W = G + np.outer(beta, u)
+    return W.astype(np.float32), share
+
+
+def zipf_tokens(seed: int, tokens: int, hidden: int) -> np.ndarray:
+    """Prefill tokens for ``zipf_router(seed)``: N(0, 1) with the pinned
+    direction set to 1."""
+    z = rng(seed + 3).standard_normal((tokens, hidden))
+    return pin_direction(z, zipf_direction(seed, hidden), 1.0)
+
+
+def zipf_fit(counts: np.ndarray) -> float:
+    """Least-squares Zipf exponent of per-expert counts: minus the slope of
+    log(count) against log(rank) over the ranks whose count is nonzero and
+    below the largest (capped) count."""
+    c = np.sort(np.asarray(counts, np.float64))[::-1]
+    r = np.arange(1, c.size + 1, dtype=np.float64)
+    keep = (c > 0) & (c < c[0])
+    if keep.sum() < 3:
+        return float("nan")
+    slope = np.polyfit(np.log(r[keep]), np.log(c[keep]), 1)[0]
+    return float(-slope)
