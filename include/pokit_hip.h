@@ -73,6 +73,7 @@ typedef struct pk_hip_stats {
     uint64_t matvec_ns, router_ns, gate_up_ns, down_ns;
     uint64_t router_launches, gate_up_launches, down_launches, matvec_launches;
     uint64_t prefill_calls, prefill_tokens, prefill_ns;
+    uint64_t prefill_route_ns, prefill_gate_up_ns, prefill_down_ns;
 } pk_hip_stats;
 
 const char* pk_hip_version(void);

@@ -95,11 +95,12 @@ struct pk_hip_ctx {
     DeviceBuffer<float> x, y, act, probs;
     DeviceBuffer<uint32_t> ids, words;  // words: [1..4] status
     DeviceBuffer<double> row_sum, row_bound;
-    // prefill scratch (grown on demand; counts stay zero between calls)
-    DeviceBuffer<float> px, py, pprobs, pact, pout;
-    DeviceBuffer<uint32_t> pids, pcounts, poffsets, ptiles, pperm;
+    // prefill scratch (grown on demand)
+    DeviceBuffer<float> px, py, pprobs, pact, pout, pxsum, pasum;
+    DeviceBuffer<uint32_t> pids, poffsets, ptiles, pperm;
+    DeviceBuffer<uint16_t> pxparts, paparts;
     DeviceBuffer<double> prow_sum, prow_bound;
-    hipEvent_t ev[8] = {};
+    hipEvent_t ev[10] = {};
     int wall_rate_khz = 100000;  // wall_clock64() rate
 
     void set_device() const { check(hipSetDevice(device), "hipSetDevice"); }
@@ -431,8 +432,11 @@ void pk_hip_destroy(pk_hip_ctx* c) {
     c->words.release();
     c->row_sum.release();
     c->row_bound.release();
-    for (auto* b : {&c->px, &c->py, &c->pprobs, &c->pact, &c->pout}) b->release();
-    for (auto* b : {&c->pids, &c->pcounts, &c->poffsets, &c->ptiles, &c->pperm}) b->release();
+    for (auto* b : {&c->px, &c->py, &c->pprobs, &c->pact, &c->pout, &c->pxsum, &c->pasum})
+        b->release();
+    for (auto* b : {&c->pids, &c->poffsets, &c->ptiles, &c->pperm}) b->release();
+    c->pxparts.release();
+    c->paparts.release();
     c->prow_sum.release();
     c->prow_bound.release();
     for (auto& e : c->ev)
@@ -604,16 +608,16 @@ void enqueue_prefill(pk_hip_ctx* c, const pk_hip_moe_layer* L, const MoeShape& m
                      const float* dx, float* dy, uint32_t* dids, float* dprobs, hipStream_t s) {
     const uint64_t T = tokens, K = L->top_k, E = m.experts;
     const uint32_t max_tiles = pk::moe_prefill_max_tiles(tokens, L->top_k, m.experts);
-    if (c->pcounts.count < E) {  // counts must start at zero; later calls leave them zero
-        c->pcounts.ensure(E);
-        check(hipMemsetAsync(c->pcounts.ptr, 0, E * sizeof(uint32_t), s), "clear counts");
-    }
     c->prow_sum.ensure(T * E);
     c->prow_bound.ensure(T * E);
     c->poffsets.ensure(E + 1);
     c->ptiles.ensure(static_cast<size_t>(max_tiles) + 1);
     c->pperm.ensure(T * K);
     c->pact.ensure(T * K * m.ffn);
+    c->pxparts.ensure(3 * T * m.hidden);
+    c->pxsum.ensure(T * m.hidden / 16);
+    c->paparts.ensure(3 * T * K * m.ffn);
+    c->pasum.ensure(T * K * m.ffn / 16);
     c->pout.ensure(T * K * m.hidden);
     pk::MoePrefillArgs a{};
     pk::MoeDecodeArgs& l = a.layer;
@@ -645,28 +649,39 @@ void enqueue_prefill(pk_hip_ctx* c, const pk_hip_moe_layer* L, const MoeShape& m
     a.probs = dprobs;
     a.row_sum = c->prow_sum.ptr;
     a.row_bound = c->prow_bound.ptr;
-    a.counts = c->pcounts.ptr;
     a.offsets = c->poffsets.ptr;
     a.tiles = c->ptiles.ptr;
     a.n_tiles = c->ptiles.ptr + max_tiles;
     a.perm = c->pperm.ptr;
+    a.x_parts = c->pxparts.ptr;
+    a.x_sums = c->pxsum.ptr;
     a.act = c->pact.ptr;
+    a.act_parts = c->paparts.ptr;
+    a.act_sums = c->pasum.ptr;
     a.out = c->pout.ptr;
     a.status = status_words(c);
     if (c->time_kernels) hold_stream(c, s);
     begin_timing(c, s, 6);
-    launch_checked(pk::launch_moe_prefill(a, s), "prefill launch");
+    launch_checked(pk::launch_prefill_routing(a, s), "prefill routing launch");
     begin_timing(c, s, 7);
+    launch_checked(pk::launch_prefill_gate_up(a, s), "prefill gate/up launch");
+    begin_timing(c, s, 8);
+    launch_checked(pk::launch_prefill_down(a, s), "prefill down launch");
+    begin_timing(c, s, 9);
     ++c->stats.prefill_calls;
     c->stats.prefill_tokens += tokens;
-    c->stats.dispatches += 6;
+    c->stats.dispatches += 8;
     count_dispatch(c, L->gate->type);
     count_dispatch(c, L->down->type);
     c->stats.dispatches -= 2;
 }
 
 void collect_timing_prefill(pk_hip_ctx* c) {
-    if (c->time_kernels) c->stats.prefill_ns += elapsed_ns(c, 6, 7);
+    if (!c->time_kernels) return;
+    c->stats.prefill_ns += elapsed_ns(c, 6, 9);
+    c->stats.prefill_route_ns += elapsed_ns(c, 6, 7);
+    c->stats.prefill_gate_up_ns += elapsed_ns(c, 7, 8);
+    c->stats.prefill_down_ns += elapsed_ns(c, 8, 9);
 }
 
 }  // namespace

@@ -50,9 +50,10 @@ hipError_t launch_moe_decode(const MoeDecodeArgs& a, hipStream_t stream);
 
 // Batched prefill: tokens independent single-token MoE blocks, grouped per
 // expert for MFMA GEMMs.  Scratch sizes for `tokens` tokens (T), top_k (K),
-// n_experts (E): row_sum/row_bound T*E, counts E (zero between calls),
-// offsets E+1, tiles and n_tiles moe_prefill_max_tiles(T, K, E) + 1, perm T*K,
-// act T*K*ffn, out T*K*hidden.
+// n_experts (E), pairs P = T*K: row_sum/row_bound T*E, offsets E+1, tiles and
+// n_tiles moe_prefill_max_tiles(T, K, E) + 1, perm P, x_parts 3*T*hidden,
+// x_sums T*hidden/16, act P*ffn, act_parts 3*P*ffn, act_sums P*ffn/16,
+// out P*hidden.
 constexpr uint32_t kMaxPrefillTokens = 4096;
 struct MoePrefillArgs {
     MoeDecodeArgs layer;     // weights, shapes, top_k, normalize, scale
@@ -63,20 +64,27 @@ struct MoePrefillArgs {
     float* probs;            // [tokens][top_k]
     double* row_sum;         // [tokens][n_experts]
     double* row_bound;
-    uint32_t* counts;        // [n_experts]
     uint32_t* offsets;       // [n_experts + 1]
     uint32_t* tiles;         // [max_tiles]
     uint32_t* n_tiles;       // [1]
-    uint32_t* perm;          // [tokens * top_k]
-    float* act;              // [tokens * top_k][ffn]
-    float* out;              // [tokens * top_k][hidden]
+    uint32_t* perm;          // [P]: grouped row -> token * top_k + route
+    uint16_t* x_parts;       // 3 bf16 planes [tokens][hidden]: x = hi + mid + lo
+    float* x_sums;           // [tokens][hidden / G]: sums over gate/up scale groups
+    float* act;              // [P][ffn], grouped rows
+    uint16_t* act_parts;     // 3 bf16 planes [P][ffn]
+    float* act_sums;         // [P][ffn / G]: sums over down scale groups
+    float* out;              // [P][hidden], slot token * top_k + route
     uint32_t* status;        // as MoeDecodeArgs::status
 };
 uint32_t moe_prefill_max_tiles(uint32_t tokens, uint32_t top_k, uint32_t n_experts);
 bool moe_prefill_supported(uint32_t gate_type, uint32_t up_type, uint32_t down_type,
                            uint32_t hidden, uint32_t ffn, uint32_t n_experts, uint32_t top_k,
                            uint32_t tokens);
-hipError_t launch_moe_prefill(const MoePrefillArgs& a, hipStream_t stream);
+// The prefill's launches in three phases (timed separately): routing and
+// grouping (router, ranking, grouping), the gate/up GEMMs, and down + combine.
+hipError_t launch_prefill_routing(const MoePrefillArgs& a, hipStream_t stream);
+hipError_t launch_prefill_gate_up(const MoePrefillArgs& a, hipStream_t stream);
+hipError_t launch_prefill_down(const MoePrefillArgs& a, hipStream_t stream);
 
 // Individual stages (timing and tests).
 hipError_t launch_moe_router(const MoeDecodeArgs& a, hipStream_t stream);

@@ -3,22 +3,23 @@
 // The reference prefills a prompt one token at a time through the MoE block
 // of src/qwen3_moe_runner.cpp:643-692 (the loop at :785-790), so every
 // token's routes and output are those of a single-token pass.  Here the
-// whole batch goes through six launches:
+// whole batch goes through eight launches:
 //
 //  1. k_router_batch: the exact logit value S and rounding bound B of every
 //     (token, expert) pair (the decode router's arithmetic, one expert row
 //     held in registers across a tile of tokens).
 //  2. k_route_batch: one workgroup per token ranks the experts exactly as the
-//     decode path does (certified wave ranking, exact serial fallback),
-//     writes ids and route weights, and counts each expert's tokens.
-//  3. k_group: one workgroup turns the counts into per-expert row ranges,
-//     a list of 32-row tiles and the assignments (token * top_k + route)
-//     grouped by expert; it leaves the counts at zero for the next call.
-//  4. k_gate_up_mfma: per tile and 128 ffn rows, gate and up GEMMs on
-//     v_mfma_f32_32x32x2f32 with the weights dequantised into LDS exactly as
-//     the reference decodes them (FP32 values), and the SwiGLU epilogue.
-//  5. k_down_mfma: per tile and 128 hidden rows, the down GEMM; each
-//     output row goes to its (token, route) slot.
+//     decode path does (certified wave ranking, exact serial fallback) and
+//     writes ids and route weights.
+//  3. k_group: one workgroup counts each expert's tokens and lays out
+//     per-expert row ranges, a list of 32-row tiles and the assignments
+//     (token * top_k + route) grouped by expert.
+//  4. k_split (x), then k_expert_gemm<gate/up>: per tile and 128 ffn rows,
+//     gate and up GEMMs on bf16 MFMA with exact products (x split into three
+//     bf16 planes, the quantised weights as bf16 integers, the scales applied
+//     per group outside the MFMA), and the SwiGLU epilogue.
+//  5. k_split (act), then k_expert_gemm<down>: per tile and 128 hidden rows;
+//     each output row goes to its (token, route) slot.
 //  6. k_combine: y = ((0 + p0*o0) + p1*o1) + ... per token in route order
 //     (:688-690).
 //
@@ -37,21 +38,40 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 constexpr uint32_t kTileM = 32;      // tokens per GEMM tile (MFMA M)
 constexpr uint32_t kTileN = 128;     // output rows per workgroup: 4 waves x 32
-constexpr uint32_t kChunk = 32;      // K elements staged per step
 constexpr uint32_t kRouterTokens = 8;  // tokens per batched-router workgroup
 
 // ---------------------------------------------------------------------------
-// Dequantisation of 32 consecutive elements k0 .. k0 + 31 (k0 % 32 == 0) of
-// one GGUF row to the reference's FP32 values (src/quantized_linear.cpp:
-// 166-205, 286-358, 387-423): loads first (Raw32), values later.
+// The quant fields of 32 consecutive elements k0 .. k0 + 31 (k0 % 32 == 0)
+// of one GGUF row (block layouts of src/quantized_linear.cpp:166-205,
+// 286-358, 387-423): loads first (Raw32), values later.
 
 template <int T>
 struct Raw32;
 template <> struct Raw32<T_Q4_K> { uint32_t h[4]; uint32_t q[8]; };
 template <> struct Raw32<T_Q5_K> { uint32_t h[4]; uint32_t q[8]; uint32_t qh[8]; };
-template <> struct Raw32<T_Q6_K> { uint32_t ql[8]; uint32_t qh[8]; int32_t s0, s1; uint32_t d; };
-template <> struct Raw32<T_Q8_0> { uint32_t q[8]; uint32_t d; };
-template <> struct Raw32<T_Q4_0> { uint32_t q[4]; uint32_t d; };
+// Q6_K, Q8_0 and Q4_0 blocks keep only 2-byte alignment: their fields are
+// loaded as the dwords that cover them (one extra) and realigned by `shift`
+// bytes when decoded, so no load result is needed before its use.
+// (Each field keeps a power-of-two word array plus one trailing word: such
+// arrays stay in registers.)
+template <> struct Raw32<T_Q6_K> { uint32_t ql[8], qh[8]; uint32_t ql8, qh8, sc, d, shift; };
+template <> struct Raw32<T_Q8_0> { uint32_t q[8]; uint32_t q8, d, shift; };
+template <> struct Raw32<T_Q4_0> { uint32_t q[4]; uint32_t q4, d, shift; };
+
+// Word i of a field loaded `shift` bytes early.
+template <int N>
+__device__ __forceinline__ uint32_t word_at(const uint32_t (&raw)[N], uint32_t tail, uint32_t shift,
+                                            uint32_t i) {
+    return __builtin_amdgcn_alignbyte(i + 1u < N ? raw[i + 1u] : tail, raw[i], shift);
+}
+
+__device__ __forceinline__ uint32_t ld_word(const uint8_t* p) {
+    return *reinterpret_cast<const uint32_t*>(__builtin_assume_aligned(p, 4));
+}
+
+__device__ __forceinline__ uint32_t align_shift(const uint8_t* p) {
+    return static_cast<uint32_t>(reinterpret_cast<uintptr_t>(p) & 3u);
+}
 
 template <int T>
 __device__ __forceinline__ void raw32_load(const uint8_t* row, uint32_t k0, Raw32<T>& r) {
@@ -64,18 +84,26 @@ __device__ __forceinline__ void raw32_load(const uint8_t* row, uint32_t k0, Raw3
     } else if constexpr (T == T_Q6_K) {
         const uint8_t* blk = row + (k0 / 256u) * 210u;
         const uint32_t c = (k0 % 256u) / 32u, half = c / 4u, g = c % 4u;
-        ld_words_2a<8>(blk + 64u * half + 32u * (g & 1u), r.ql);
-        ld_words_2a<8>(blk + 128u + 32u * half, r.qh);
-        r.s0 = static_cast<int8_t>(blk[192u + 8u * half + 2u * g]);
-        r.s1 = static_cast<int8_t>(blk[192u + 8u * half + 2u * g + 1u]);
+        r.shift = align_shift(blk);  // field offsets below are multiples of 4
+        const uint8_t* pl = blk - r.shift + 64u * half + 32u * (g & 1u);
+        const uint8_t* ph = blk - r.shift + 128u + 32u * half;
+        ld_words<8>(pl, r.ql);
+        r.ql8 = ld_word(pl + 32u);
+        ld_words<8>(ph, r.qh);
+        r.qh8 = ld_word(ph + 32u);
+        r.sc = ld_u16(blk + 192u + 8u * half + 2u * g);  // int8 scales of both 16-halves
         r.d = ld_u16(blk + 208u);
     } else if constexpr (T == T_Q8_0) {
         const uint8_t* blk = row + (k0 / 32u) * 34u;
-        ld_words_2a<8>(blk + 2u, r.q);
+        r.shift = align_shift(blk + 2u);
+        ld_words<8>(blk + 2u - r.shift, r.q);
+        r.q8 = ld_word(blk + 34u - r.shift);
         r.d = ld_u16(blk);
     } else {  // Q4_0
         const uint8_t* blk = row + (k0 / 32u) * 18u;
-        ld_words_2a<4>(blk + 2u, r.q);
+        r.shift = align_shift(blk + 2u);
+        ld_words<4>(blk + 2u - r.shift, r.q);
+        r.q4 = ld_word(blk + 18u - r.shift);
         r.d = ld_u16(blk);
     }
 }
@@ -84,47 +112,73 @@ __device__ __forceinline__ uint32_t byte_of(const uint32_t* w, uint32_t i) {
     return (w[i >> 2] >> (8u * (i & 3u))) & 0xffu;
 }
 
+// The same 32 elements as bf16 bit patterns of their integer fields, two per
+// dword (element 2i in the low half of bw[i]): each field is converted to
+// float exactly (v_cvt_f32_ubyteN) and its upper half kept, which is exact
+// for integers below 256.  Per scale group of the 32 (one group; two of 16
+// for Q6_K) the reference's weight is w = ds * (f - o) - dm with f the
+// unsigned field and o its offset, so the group's dot product with x is
+// ds * sum(x * f) + cn * sum(x) with cn = -(dm + o * ds): K-quants o = 0
+// (cn = -dm), Q6_K o = 32, Q4_0 o = 8, Q8_0 o = 128 (its int8 read as
+// q + 128).
+__device__ __forceinline__ uint32_t bf16_pair(float lo, float hi) {  // exact for small integers
+    return __builtin_amdgcn_perm(__float_as_uint(hi), __float_as_uint(lo), 0x07060302u);
+}
+
+// Four unsigned byte fields (each < 256) to two dwords of bf16.
+__device__ __forceinline__ void bf16_bytes(uint32_t w, uint32_t& lo, uint32_t& hi) {
+    lo = bf16_pair(static_cast<float>(w & 0xffu), static_cast<float>((w >> 8) & 0xffu));
+    hi = bf16_pair(static_cast<float>((w >> 16) & 0xffu), static_cast<float>(w >> 24));
+}
+
 template <int T>
-__device__ __forceinline__ void raw32_decode(const Raw32<T>& r, uint32_t k0, float (&v)[32]) {
+__device__ __forceinline__ void raw32_bf16(const Raw32<T>& r, uint32_t k0, uint32_t (&bw)[16],
+                                           float (&ds)[2], float (&cn)[2]) {
     if constexpr (T == T_Q4_K || T == T_Q5_K) {
-        const uint32_t j = (k0 % 256u) / 32u, chunk = j / 2u, hi = j & 1u;
+        const uint32_t j = (k0 % 256u) / 32u, hi = j & 1u;
         const float d = half_bits_to_float(r.h[0] & 0xffffu);
         const float dmin = half_bits_to_float(r.h[0] >> 16);
         float sc, mn;
         kq_scale_min(r.h, j, sc, mn);
-        const float ds = __fmul_rn(d, sc), dm = __fmul_rn(dmin, mn);
 #pragma unroll
-        for (uint32_t i = 0; i < 32; ++i) {
-            uint32_t q = byte_of(r.q, i);
-            q = hi ? q >> 4 : q & 15u;
-            if constexpr (T == T_Q5_K) q += ((byte_of(r.qh, i) >> (2u * chunk + hi)) & 1u) << 4;
-            v[i] = __fsub_rn(__fmul_rn(ds, static_cast<float>(q)), dm);  // fl(fl(d*s)*q) - fl(dmin*m)
+        for (uint32_t i = 0; i < 8; ++i) {
+            uint32_t q = (hi ? r.q[i] >> 4 : r.q[i]) & 0x0f0f0f0fu;
+            if constexpr (T == T_Q5_K) q |= ((r.qh[i] >> j) & 0x01010101u) << 4;
+            bf16_bytes(q, bw[2 * i], bw[2 * i + 1]);
         }
+        ds[0] = ds[1] = __fmul_rn(d, sc);
+        cn[0] = cn[1] = -__fmul_rn(dmin, mn);
     } else if constexpr (T == T_Q6_K) {
         const uint32_t c = (k0 % 256u) / 32u, g = c % 4u;
         const float d = half_bits_to_float(r.d);
-        const float ds0 = __fmul_rn(d, static_cast<float>(r.s0));
-        const float ds1 = __fmul_rn(d, static_cast<float>(r.s1));
 #pragma unroll
-        for (uint32_t i = 0; i < 32; ++i) {
-            const uint32_t lb = byte_of(r.ql, i), hb = byte_of(r.qh, i);
-            const uint32_t nib = g >= 2u ? lb >> 4 : lb & 15u;
-            const int q = static_cast<int>(nib | (((hb >> (2u * g)) & 3u) << 4)) - 32;
-            v[i] = __fmul_rn(i < 16u ? ds0 : ds1, static_cast<float>(q));  // fl(fl(d*s)*q)
+        for (uint32_t i = 0; i < 8; ++i) {
+            const uint32_t ql = word_at(r.ql, r.ql8, r.shift, i);
+            const uint32_t qh = word_at(r.qh, r.qh8, r.shift, i);
+            const uint32_t nib = (g >= 2u ? ql >> 4 : ql) & 0x0f0f0f0fu;
+            bf16_bytes(nib | (((qh >> (2u * g)) & 0x03030303u) << 4), bw[2 * i], bw[2 * i + 1]);
         }
+        ds[0] = __fmul_rn(d, static_cast<float>(static_cast<int8_t>(r.sc & 0xffu)));
+        ds[1] = __fmul_rn(d, static_cast<float>(static_cast<int8_t>(r.sc >> 8)));
+        cn[0] = __fmul_rn(-32.0f, ds[0]);
+        cn[1] = __fmul_rn(-32.0f, ds[1]);
     } else if constexpr (T == T_Q8_0) {
         const float d = half_bits_to_float(r.d);
 #pragma unroll
-        for (uint32_t i = 0; i < 32; ++i)
-            v[i] = __fmul_rn(d, static_cast<float>(static_cast<int8_t>(byte_of(r.q, i))));
+        for (uint32_t i = 0; i < 8; ++i)
+            bf16_bytes(word_at(r.q, r.q8, r.shift, i) ^ 0x80808080u, bw[2 * i], bw[2 * i + 1]);
+        ds[0] = ds[1] = d;
+        cn[0] = cn[1] = __fmul_rn(-128.0f, d);
     } else {  // Q4_0: low nibbles are elements 0..15, high nibbles 16..31
         const float d = half_bits_to_float(r.d);
 #pragma unroll
-        for (uint32_t i = 0; i < 16; ++i) {
-            const uint32_t b = byte_of(r.q, i);
-            v[i] = __fmul_rn(d, static_cast<float>(static_cast<int>(b & 15u) - 8));
-            v[i + 16] = __fmul_rn(d, static_cast<float>(static_cast<int>(b >> 4) - 8));
+        for (uint32_t i = 0; i < 4; ++i) {
+            const uint32_t q = word_at(r.q, r.q4, r.shift, i);
+            bf16_bytes(q & 0x0f0f0f0fu, bw[2 * i], bw[2 * i + 1]);
+            bf16_bytes((q >> 4) & 0x0f0f0f0fu, bw[8 + 2 * i], bw[9 + 2 * i]);
         }
+        ds[0] = ds[1] = d;
+        cn[0] = cn[1] = __fmul_rn(-8.0f, d);
     }
 }
 
@@ -222,18 +276,14 @@ __global__ __launch_bounds__(256) void k_route_batch(MoePrefillArgs A) {
 #pragma unroll
         for (uint32_t r = 0; r < kMaxTopK; ++r) sel[r] = s_sel[r];
     }
-    if (wave == 0) {
-        write_routes<NS>(a, sel, w.logit);
-        uint32_t mine = 0u;
-#pragma unroll
-        for (uint32_t r = 0; r < kMaxTopK; ++r)
-            if (lane == r) mine = sel[r];
-        if (lane < K) atomicAdd(A.counts + mine, 1u);
-    }
+    if (wave == 0) write_routes<NS>(a, sel, w.logit);
 }
 
 // ---------------------------------------------------------------------------
-// 3. Grouping (one workgroup of 1024 threads).
+// 3. Grouping (one workgroup of 1024 threads): per-expert counts from the
+// ids (LDS atomics), row ranges, the 32-row tile list and the assignments
+// (token * top_k + route) grouped by expert.  Tokens the router flagged
+// (ids 0xffffffff) take no rows.
 
 constexpr uint32_t kGroupThreads = 1024;
 
@@ -241,10 +291,15 @@ __global__ __launch_bounds__(kGroupThreads) void k_group(MoePrefillArgs a) {
     __shared__ uint32_t cnt[kMaxExperts], off[kMaxExperts + 1], tb[kMaxExperts + 1],
         fill[kMaxExperts];
     const uint32_t E = a.layer.n_experts, K = a.layer.top_k, tid = threadIdx.x;
+    const uint32_t n = a.tokens * K;
     if (tid < E) {
-        cnt[tid] = a.counts[tid];
-        a.counts[tid] = 0u;  // zero for the next call
+        cnt[tid] = 0u;
         fill[tid] = 0u;
+    }
+    __syncthreads();
+    for (uint32_t i = tid; i < n; i += kGroupThreads) {
+        const uint32_t e = a.ids[i];
+        if (e < E) atomicAdd(&cnt[e], 1u);
     }
     __syncthreads();
     if (tid == 0) {
@@ -264,9 +319,7 @@ __global__ __launch_bounds__(kGroupThreads) void k_group(MoePrefillArgs a) {
     if (tid < E)
         for (uint32_t j = 0; j < (cnt[tid] + kTileM - 1u) / kTileM; ++j)
             a.tiles[tb[tid] + j] = (tid << 16) | j;
-    // assignments t * top_k + r grouped by expert (order inside a group is
-    // free: every row's result is independent of its neighbours)
-    const uint32_t n = a.tokens * K;
+    // the order inside a group is free: every row's result is independent
     for (uint32_t i = tid; i < n; i += kGroupThreads) {
         const uint32_t e = a.ids[i];
         if (e < E) a.perm[off[e] + atomicAdd(&fill[e], 1u)] = i;
@@ -274,18 +327,90 @@ __global__ __launch_bounds__(kGroupThreads) void k_group(MoePrefillArgs a) {
 }
 
 // ---------------------------------------------------------------------------
-// 4-5. Grouped GEMMs on MFMA.  A workgroup of 4 waves owns one 32-row tile
-// of one expert and 128 output rows (32 per wave); K advances kChunk
-// elements at a time: activations and dequantised weights are staged in LDS
-// (the next chunk's loads are in flight while the MFMAs run on this one).
+// 4. Split-bf16 operands.  Every FP32 value x is exactly hi + mid + lo with
+// three bf16 values (8 significant bits each and FP32's exponent range:
+// hi = RNE(x), mid = RNE(x - hi), lo = x - hi - mid, each difference exact).
+// With the weights' integer fields as bf16 (raw32_bf16), every product of the
+// expert GEMMs is exact in the FP32 accumulators of the bf16 MFMA; the
+// per-group scales are applied outside it.  k_split writes the three planes
+// of `rows` x `cols` FP32 values and, per G consecutive values of a row,
+// their sum (accumulated in FP64, rounded once).
+
+__device__ __forceinline__ uint32_t bf16_rne_bits(float x) {  // finite x
+    const uint32_t u = __float_as_uint(x);
+    return (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+}
+
+template <uint32_t G>
+__global__ __launch_bounds__(256) void k_split(const float* __restrict__ src, uint32_t pieces,
+                                               uint16_t* __restrict__ parts, uint64_t plane,
+                                               float* __restrict__ sums) {
+    const uint32_t i = blockIdx.x * 256u + threadIdx.x;  // 16-value piece
+    const uint32_t ic = i < pieces ? i : pieces - 1u;    // every lane loads (and shuffles)
+    const float4* sp = reinterpret_cast<const float4*>(src + static_cast<uint64_t>(ic) * 16u);
+    float v[16];
+#pragma unroll
+    for (uint32_t j = 0; j < 4; ++j) {
+        const float4 f = sp[j];
+        v[4 * j] = f.x;
+        v[4 * j + 1] = f.y;
+        v[4 * j + 2] = f.z;
+        v[4 * j + 3] = f.w;
+    }
+    uint32_t ph[8], pm[8], pl[8];
+    double sum = 0.0;
+#pragma unroll
+    for (uint32_t e = 0; e < 16; e += 2) {
+        uint32_t h2[2], m2[2], l2[2];
+#pragma unroll
+        for (uint32_t t = 0; t < 2; ++t) {
+            const float x = v[e + t];
+            sum += static_cast<double>(x);
+            h2[t] = bf16_rne_bits(x);
+            const float r1 = x - __uint_as_float(h2[t] << 16);
+            m2[t] = bf16_rne_bits(r1);
+            const float r2 = r1 - __uint_as_float(m2[t] << 16);
+            l2[t] = __float_as_uint(r2) >> 16;  // r2 has at most 8 significant bits
+        }
+        ph[e / 2] = h2[0] | (h2[1] << 16);
+        pm[e / 2] = m2[0] | (m2[1] << 16);
+        pl[e / 2] = l2[0] | (l2[1] << 16);
+    }
+    if constexpr (G == 32) sum += __shfl_xor(sum, 1);
+    if (i >= pieces) return;
+    uint4* d0 = reinterpret_cast<uint4*>(parts + static_cast<uint64_t>(i) * 16u);
+    uint4* d1 = reinterpret_cast<uint4*>(parts + plane + static_cast<uint64_t>(i) * 16u);
+    uint4* d2 = reinterpret_cast<uint4*>(parts + 2u * plane + static_cast<uint64_t>(i) * 16u);
+    d0[0] = make_uint4(ph[0], ph[1], ph[2], ph[3]);
+    d0[1] = make_uint4(ph[4], ph[5], ph[6], ph[7]);
+    d1[0] = make_uint4(pm[0], pm[1], pm[2], pm[3]);
+    d1[1] = make_uint4(pm[4], pm[5], pm[6], pm[7]);
+    d2[0] = make_uint4(pl[0], pl[1], pl[2], pl[3]);
+    d2[1] = make_uint4(pl[4], pl[5], pl[6], pl[7]);
+    if (G == 16 || (i & 1u) == 0u) sums[i * 16u / G] = static_cast<float>(sum);
+}
+
+// ---------------------------------------------------------------------------
+// 5. Grouped GEMMs on bf16 MFMA (v_mfma_f32_32x32x16_bf16).  A workgroup of
+// 4 waves owns one 32-row tile of one expert and 256 staged weight rows, two
+// 32-row blocks per wave: 128 gate rows and the same 128 up rows, or 256
+// down rows.  K advances one
+// stage at a time through two LDS buffers: the three activation planes, the
+// weights' integer fields as bf16, and per scale group the row scales ds, the bias
+// coefficients cn and the activations' group sums.  Per group g and tile,
+// P = sum over the three planes of A_part x q on MFMA, then acc += ds_g * P;
+// the bias term sum_g xs_g * cn_g (two groups at a time) goes through a
+// v_mfma_f32_32x32x2f32 into the same accumulator.
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 
 struct TileRef {
     uint32_t e, base, rows;  // expert, first grouped row, valid rows (<= kTileM)
 };
 
-__device__ __forceinline__ bool tile_ref(const MoePrefillArgs& a, TileRef& r) {
-    if (blockIdx.x >= a.n_tiles[0]) return false;
-    const uint32_t code = a.tiles[blockIdx.x];
+__device__ __forceinline__ bool tile_ref(const MoePrefillArgs& a, uint32_t tile, TileRef& r) {
+    if (tile >= a.n_tiles[0]) return false;
+    const uint32_t code = a.tiles[tile];
     r.e = code >> 16;
     const uint32_t m0 = (code & 0xffffu) * kTileM;
     const uint32_t lo = a.offsets[r.e], hi = a.offsets[r.e + 1];
@@ -294,133 +419,253 @@ __device__ __forceinline__ bool tile_ref(const MoePrefillArgs& a, TileRef& r) {
     return true;
 }
 
-constexpr uint32_t kLdsA = kChunk + 1;     // padded A row (tokens x K)
-constexpr uint32_t kLdsB = kTileN + 4;     // padded B row (K x N)
+// Workgroups go to the 8 XCDs round robin by linear id.  Block L runs on XCD
+// L % 8; on each XCD, the blocks walk its tiles (tile % 8 == XCD) with all
+// `nb` row blocks of one tile next to each other, so a tile's activations
+// are fetched into that XCD's L2 once and the tiles that share an expert run
+// there side by side.
+__device__ __forceinline__ void xcd_tile(uint32_t nb, uint32_t& tile, uint32_t& yb) {
+    const uint32_t L = blockIdx.x, xcd = L % 8u, slot = L / 8u;
+    tile = 8u * (slot / nb) + xcd;
+    yb = slot % nb;
+}
 
-template <int TG>
-__global__ __launch_bounds__(256) void k_gate_up_mfma(MoePrefillArgs a) {
-    __shared__ float As[kTileM * kLdsA];
-    __shared__ float Bg[kChunk * kLdsB], Bu[kChunk * kLdsB];
-    __shared__ const float* s_xrow[kTileM];
-    TileRef tr;
-    if (!tile_ref(a, tr)) return;  // uniform
-    const MoeDecodeArgs& L = a.layer;
-    const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
-    const uint32_t H = L.hidden, K = L.top_k, n0 = blockIdx.y * kTileN;
-    if (tid < kTileM) {
-        const uint32_t i = tid < tr.rows ? tid : 0u;  // absent rows reuse row 0
-        s_xrow[tid] = a.x + static_cast<uint64_t>(a.perm[tr.base + i] / K) * H;
-    }
-    __syncthreads();
-    // this thread's staging jobs: A row tid / 8, 4 columns; B matrix tid / 128, row tid % 128
-    const float* xrow = s_xrow[tid / 8u] + (tid % 8u) * 4u;
-    const bool up_row = tid >= 128u;
-    const uint8_t* wrow = (up_row ? L.up : L.gate) + static_cast<uint64_t>(tr.e) *
-                                                       (up_row ? L.up_slice : L.gate_slice) +
-                          static_cast<uint64_t>(n0 + (tid % 128u)) * (up_row ? L.up_row : L.gate_row);
-    float* bdst = (up_row ? Bu : Bg) + (tid % 128u);
+template <int TW, bool DUAL>
+struct GemmCfg {
+    static constexpr uint32_t G = TW == T_Q6_K ? 16u : 32u;  // scale group
+    static constexpr uint32_t NRW = 256u;                    // weight rows staged (2 x 128)
+    static constexpr uint32_t PARTS = 256u / NRW;            // 32-value parts per row and stage
+    static constexpr uint32_t KC = 32u * PARTS;              // K per stage
+    static constexpr uint32_t NG = KC / G;                   // scale groups per stage
+    static constexpr uint32_t GP = 32u / G;                  // groups per part
+    static constexpr uint32_t SR = KC * 2u + 16u;            // LDS row stride (bytes)
+    static constexpr uint32_t NQ = 3u * kTileM * KC / 8u;    // 16-byte activation pieces
+};
 
-    f32x16 accg = {}, accu = {};
-    float4 xa = *reinterpret_cast<const float4*>(xrow);
-    Raw32<TG> raw;
-    raw32_load<TG>(wrow, 0, raw);
-    for (uint32_t k0 = 0; k0 < H; k0 += kChunk) {
-        // stage chunk k0
-        float* adst = As + (tid / 8u) * kLdsA + (tid % 8u) * 4u;
-        adst[0] = xa.x;
-        adst[1] = xa.y;
-        adst[2] = xa.z;
-        adst[3] = xa.w;
-        float v[32];
-        raw32_decode<TG>(raw, k0, v);
+template <int TW, bool DUAL>
+struct alignas(16) GemmStage {
+    using C = GemmCfg<TW, DUAL>;
+    uint8_t a[3 * kTileM * C::SR];  // planes hi, mid, lo: [m][k]
+    uint8_t b[C::NRW * C::SR];      // weights: [n][k]
+    float xs[C::NG * kTileM];       // [g][m]
+    float ds[C::NG * C::NRW];       // [g][n]
+    float cn[C::NG * C::NRW];       // [g][n]
+};
+
+template <int TW, bool DUAL>
+struct GemmPrefetch {
+    Raw32<TW> raw;
+    u32x4_t ap0, ap1;  // two 16-byte activation pieces (native vectors: they stay in registers)
+    float xs;
+};
+
+// A thread's global sources (at k = 0) and LDS destinations, fixed for the
+// whole K loop: activation pieces tid and tid + 256 of a stage's 384 (three
+// planes x 32 rows x 4), and group sum tid.  Pieces and sums past the
+// stage's count repeat the last one, so every thread loads and stores
+// unconditionally (the duplicate stores write the same values to the same
+// places).
+template <int TW, bool DUAL>
+struct GemmSrc {
+    const uint8_t* wrow;
+    const uint16_t *ap0, *ap1;
+    uint32_t adst0, adst1;
+    const float* xs;
+    uint32_t xdst;
+};
+
+template <int TW, bool DUAL>
+__device__ __forceinline__ void gemm_piece(const uint16_t* parts, uint64_t plane, uint32_t kdim,
+                                           const uint32_t* arow, uint32_t q, const uint16_t*& src,
+                                           uint32_t& dst) {
+    using C = GemmCfg<TW, DUAL>;
+    q = q < C::NQ ? q : C::NQ - 1u;
+    const uint32_t p = q / (kTileM * C::KC / 8u), rem = q % (kTileM * C::KC / 8u);
+    const uint32_t m = rem / (C::KC / 8u), kk = (rem % (C::KC / 8u)) * 8u;
+    src = parts + p * plane + static_cast<uint64_t>(arow[m]) * kdim + kk;
+    dst = (p * kTileM + m) * C::SR + kk * 2u;
+}
+
+template <int TW, bool DUAL>
+__device__ __forceinline__ void gemm_src(GemmSrc<TW, DUAL>& g, const uint8_t* wrow,
+                                         const uint16_t* parts, uint64_t plane, uint32_t kdim,
+                                         const float* sums, const uint32_t* arow) {
+    using C = GemmCfg<TW, DUAL>;
+    static_assert(C::NQ > 256u && C::NQ <= 512u, "two activation pieces per thread");
+    const uint32_t tid = threadIdx.x;
+    g.wrow = wrow;
+    gemm_piece<TW, DUAL>(parts, plane, kdim, arow, tid, g.ap0, g.adst0);
+    gemm_piece<TW, DUAL>(parts, plane, kdim, arow, tid + 256u, g.ap1, g.adst1);
+    const uint32_t t = tid < C::NG * kTileM ? tid : C::NG * kTileM - 1u;
+    g.xs = sums + static_cast<uint64_t>(arow[t % kTileM]) * (kdim / C::G) + t / kTileM;
+    g.xdst = t;
+}
+
+template <int TW, bool DUAL>
+__device__ __forceinline__ void gemm_load(GemmPrefetch<TW, DUAL>& f, const GemmSrc<TW, DUAL>& g,
+                                          uint32_t k0) {
+    using C = GemmCfg<TW, DUAL>;
+    raw32_load<TW>(g.wrow, k0 + 32u * (threadIdx.x / C::NRW), f.raw);
+    f.ap0 = *reinterpret_cast<const u32x4_t*>(g.ap0 + k0);
+    f.ap1 = *reinterpret_cast<const u32x4_t*>(g.ap1 + k0);
+    f.xs = g.xs[k0 / C::G];
+}
+
+template <int TW, bool DUAL>
+__device__ __forceinline__ void gemm_store(GemmStage<TW, DUAL>& st, const GemmPrefetch<TW, DUAL>& f,
+                                           const GemmSrc<TW, DUAL>& g, uint32_t k0) {
+    using C = GemmCfg<TW, DUAL>;
+    const uint32_t tid = threadIdx.x, wr = tid % C::NRW, part = tid / C::NRW;
+    uint32_t bw[16];
+    float ds[2], cn[2];
+    raw32_bf16<TW>(f.raw, k0 + 32u * part, bw, ds, cn);
+    uint4* bd = reinterpret_cast<uint4*>(st.b + wr * C::SR + part * 64u);
 #pragma unroll
-        for (uint32_t i = 0; i < 32; ++i) bdst[i * kLdsB] = v[i];
-        __syncthreads();
-        // next chunk's loads in flight during the MFMAs
-        if (k0 + kChunk < H) {
-            xa = *reinterpret_cast<const float4*>(xrow + k0 + kChunk);
-            raw32_load<TG>(wrow, k0 + kChunk, raw);
-        }
-        const float* ap = As + (lane % 32u) * kLdsA + lane / 32u;
-        const float* bgp = Bg + (lane / 32u) * kLdsB + wave * 32u + (lane % 32u);
-        const float* bup = Bu + (lane / 32u) * kLdsB + wave * 32u + (lane % 32u);
+    for (uint32_t j = 0; j < 4; ++j)
+        bd[j] = make_uint4(bw[4 * j], bw[4 * j + 1], bw[4 * j + 2], bw[4 * j + 3]);
 #pragma unroll
-        for (uint32_t kk = 0; kk < kChunk; kk += 2) {
-            const float av = ap[kk];
-            accg = __builtin_amdgcn_mfma_f32_32x32x2f32(av, bgp[kk * kLdsB], accg, 0, 0, 0);
-            accu = __builtin_amdgcn_mfma_f32_32x32x2f32(av, bup[kk * kLdsB], accu, 0, 0, 0);
-        }
-        __syncthreads();
+    for (uint32_t q = 0; q < C::GP; ++q) {
+        st.ds[(part * C::GP + q) * C::NRW + wr] = ds[q];
+        st.cn[(part * C::GP + q) * C::NRW + wr] = cn[q];
     }
-    // epilogue: SwiGLU g / (1 + expf(-g)) * u (src/qwen3_moe_runner.cpp:682-684)
-    const uint32_t col = n0 + wave * 32u + (lane % 32u);
+    *reinterpret_cast<u32x4_t*>(st.a + g.adst0) = f.ap0;
+    *reinterpret_cast<u32x4_t*>(st.a + g.adst1) = f.ap1;
+    st.xs[g.xdst] = f.xs;
+}
+
+__device__ __forceinline__ bf16x8 lds_bf16x8(const uint8_t* p) {
+    return __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(p));
+}
+
+// One stage of one wave: tile rows m, staged weight rows n and n + 128 (gate
+// and up rows, or two down row blocks).  Each scale group's MFMA sum is
+// scaled into the accumulator as soon as it is complete.
+template <int TW, bool DUAL>
+__device__ __forceinline__ void gemm_compute(const GemmStage<TW, DUAL>& st, f32x16& acc,
+                                             f32x16& acc2) {
+    using C = GemmCfg<TW, DUAL>;
+    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+    const uint32_t m = lane % 32u, kq = lane / 32u, n = wave * 32u + m;
+    // bias term first: its MFMA result is long complete when the scaled
+    // group sums are added below
 #pragma unroll
-    for (uint32_t r = 0; r < 16; ++r) {
-        const uint32_t row = (r / 4u) * 8u + (lane / 32u) * 4u + (r % 4u);
-        if (row < tr.rows) {
-            const float g = accg[r], u = accu[r];
-            a.act[static_cast<uint64_t>(tr.base + row) * L.ffn + col] = (g / (1.0f + expf(-g))) * u;
+    for (uint32_t gp = 0; gp < (C::NG + 1u) / 2u; ++gp) {
+        const uint32_t gi = 2u * gp + kq;
+        const bool ok = gi < C::NG;  // an odd group count pads with a zero group
+        const uint32_t gc = ok ? gi : 0u;
+        const float av = ok ? st.xs[gc * kTileM + m] : 0.0f;
+        const float bv = st.cn[gc * C::NRW + n], bv2 = st.cn[gc * C::NRW + n + 128u];
+        acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av, bv, acc, 0, 0, 0);
+        acc2 = __builtin_amdgcn_mfma_f32_32x32x2f32(av, bv2, acc2, 0, 0, 0);
+    }
+    f32x16 P, Q;
+#pragma unroll
+    for (uint32_t h = 0; h < C::KC / 16u; ++h) {
+        const uint32_t koff = (16u * h + 8u * kq) * 2u;
+        const bf16x8 a0 = lds_bf16x8(st.a + (0u * kTileM + m) * C::SR + koff);
+        const bf16x8 a1 = lds_bf16x8(st.a + (1u * kTileM + m) * C::SR + koff);
+        const bf16x8 a2 = lds_bf16x8(st.a + (2u * kTileM + m) * C::SR + koff);
+        const bf16x8 b = lds_bf16x8(st.b + n * C::SR + koff);
+        const bf16x8 bu = lds_bf16x8(st.b + (n + 128u) * C::SR + koff);
+        const bool first = (16u * h) % C::G == 0u, closes = (16u * h + 16u) % C::G == 0u;
+        P = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a2, b, first ? f32x16{} : P, 0, 0, 0);
+        Q = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a2, bu, first ? f32x16{} : Q, 0, 0, 0);
+        P = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1, b, P, 0, 0, 0);
+        Q = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1, bu, Q, 0, 0, 0);
+        P = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, b, P, 0, 0, 0);
+        Q = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, bu, Q, 0, 0, 0);
+        if (closes) {
+            const uint32_t g = 16u * h / C::G;
+            const float d = st.ds[g * C::NRW + n], du = st.ds[g * C::NRW + n + 128u];
+#pragma unroll
+            for (uint32_t r = 0; r < 16; ++r) acc[r] = __builtin_fmaf(d, P[r], acc[r]);
+#pragma unroll
+            for (uint32_t r = 0; r < 16; ++r) acc2[r] = __builtin_fmaf(du, Q[r], acc2[r]);
         }
     }
 }
 
-template <int TD>
-__global__ __launch_bounds__(256) void k_down_mfma(MoePrefillArgs a) {
-    __shared__ float As[kTileM * (2 * kChunk + 1)];
-    __shared__ float Bd[2 * kChunk * kLdsB];
-    TileRef tr;
-    if (!tile_ref(a, tr)) return;  // uniform
+// DUAL: gate/up over x (token rows), SwiGLU into act (grouped rows).
+// Otherwise: down over act, each row to its (token, route) slot of out.
+// Global loads run two stages ahead of the MFMAs (two register sets), LDS
+// holds two stages.
+template <int TW, bool DUAL>
+__global__ __launch_bounds__(256, 2) void k_expert_gemm(MoePrefillArgs a) {
+    using C = GemmCfg<TW, DUAL>;
+    __shared__ GemmStage<TW, DUAL> st[2];
+    __shared__ uint32_t arow[kTileM], oslot[kTileM];
     const MoeDecodeArgs& L = a.layer;
+    const uint32_t kdim = DUAL ? L.hidden : L.ffn, ndim = DUAL ? L.ffn : L.hidden;
+    const uint32_t nblk = DUAL ? kTileN : 2u * kTileN;  // output rows per workgroup
+    uint32_t tile, yb;
+    xcd_tile(ndim / nblk, tile, yb);
+    TileRef tr;
+    if (!tile_ref(a, tile, tr)) return;  // uniform
     const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
-    const uint32_t F = L.ffn, H = L.hidden, n0 = blockIdx.y * kTileN;
-    constexpr uint32_t KC = 2 * kChunk, LA = KC + 1;
-    // staging jobs: A row tid / 8, 8 columns; B row tid % 128, half tid / 128
-    const uint32_t arow = tid / 8u < tr.rows ? tid / 8u : 0u;
-    const float* xrow = a.act + static_cast<uint64_t>(tr.base + arow) * F + (tid % 8u) * 8u;
-    const uint32_t half = tid / 128u;
-    const uint8_t* wrow = L.down + static_cast<uint64_t>(tr.e) * L.down_slice +
-                          static_cast<uint64_t>(n0 + (tid % 128u)) * L.down_row;
-    float* bdst = Bd + half * kChunk * kLdsB + (tid % 128u);
-
-    f32x16 acc = {};
-    float4 xa0 = *reinterpret_cast<const float4*>(xrow);
-    float4 xa1 = *reinterpret_cast<const float4*>(xrow + 4);
-    Raw32<TD> raw;
-    raw32_load<TD>(wrow, half * kChunk, raw);
-    for (uint32_t k0 = 0; k0 < F; k0 += KC) {
-        float* adst = As + (tid / 8u) * LA + (tid % 8u) * 8u;
-        adst[0] = xa0.x;
-        adst[1] = xa0.y;
-        adst[2] = xa0.z;
-        adst[3] = xa0.w;
-        adst[4] = xa1.x;
-        adst[5] = xa1.y;
-        adst[6] = xa1.z;
-        adst[7] = xa1.w;
-        float v[32];
-        raw32_decode<TD>(raw, k0 + half * kChunk, v);
-#pragma unroll
-        for (uint32_t i = 0; i < 32; ++i) bdst[i * kLdsB] = v[i];
-        __syncthreads();
-        if (k0 + KC < F) {
-            xa0 = *reinterpret_cast<const float4*>(xrow + k0 + KC);
-            xa1 = *reinterpret_cast<const float4*>(xrow + k0 + KC + 4);
-            raw32_load<TD>(wrow, k0 + KC + half * kChunk, raw);
-        }
-        const float* ap = As + (lane % 32u) * LA + lane / 32u;
-        const float* bp = Bd + (lane / 32u) * kLdsB + wave * 32u + (lane % 32u);
-#pragma unroll
-        for (uint32_t kk = 0; kk < KC; kk += 2)
-            acc = __builtin_amdgcn_mfma_f32_32x32x2f32(ap[kk], bp[kk * kLdsB], acc, 0, 0, 0);
-        __syncthreads();
+    const uint32_t n0 = yb * nblk;
+    if (tid < kTileM) {
+        const uint32_t i = tid < tr.rows ? tid : tr.rows - 1u;  // absent rows repeat a real one
+        const uint32_t slot = a.perm[tr.base + i];  // token * top_k + route
+        arow[tid] = DUAL ? slot / L.top_k : tr.base + i;
+        oslot[tid] = slot;
     }
+    const uint32_t wr = tid % C::NRW;
+    const uint8_t* wrow;
+    if constexpr (DUAL)
+        wrow = (wr < 128u ? L.gate + static_cast<uint64_t>(tr.e) * L.gate_slice +
+                                static_cast<uint64_t>(n0 + wr) * L.gate_row
+                          : L.up + static_cast<uint64_t>(tr.e) * L.up_slice +
+                                static_cast<uint64_t>(n0 + wr - 128u) * L.up_row);
+    else  // rows n0 .. n0 + 255
+        wrow = L.down + static_cast<uint64_t>(tr.e) * L.down_slice +
+               static_cast<uint64_t>(n0 + wr) * L.down_row;
+    const uint16_t* parts = DUAL ? a.x_parts : a.act_parts;
+    const uint64_t plane = DUAL ? static_cast<uint64_t>(a.tokens) * L.hidden
+                                : static_cast<uint64_t>(a.tokens) * L.top_k * L.ffn;
+    const float* sums = DUAL ? a.x_sums : a.act_sums;
+    __syncthreads();
+    GemmSrc<TW, DUAL> src;
+    gemm_src<TW, DUAL>(src, wrow, parts, plane, kdim, sums, arow);
+
+    const uint32_t nst = kdim / C::KC, last = nst - 1u;
+    auto stage_k = [&](uint32_t s) { return (s < last ? s : last) * C::KC; };  // tail: harmless reloads
+    GemmPrefetch<TW, DUAL> f0, f1;
+    gemm_load<TW, DUAL>(f0, src, 0u);
+    gemm_load<TW, DUAL>(f1, src, stage_k(1u));
+    gemm_store<TW, DUAL>(st[0], f0, src, 0u);
+    gemm_load<TW, DUAL>(f0, src, stage_k(2u));
+    __syncthreads();
+    f32x16 acc = {}, acc2 = {};
+    // Stage j's loads live in f(j % 2); step s computes stage s, stages s + 1
+    // and loads s + 3.  The steps carry no conditions, so the load counters
+    // the compiler tracks stay exact across the loop (two sets in flight).
+    auto step = [&](uint32_t s, GemmPrefetch<TW, DUAL>& f) {
+        gemm_compute<TW, DUAL>(st[s & 1u], acc, acc2);
+        gemm_store<TW, DUAL>(st[(s + 1u) & 1u], f, src, (s + 1u) * C::KC);
+        gemm_load<TW, DUAL>(f, src, stage_k(s + 3u));
+        __syncthreads();
+    };
+    uint32_t s = 0;
+    for (; s + 2u < nst; s += 2u) {
+        step(s, f1);
+        step(s + 1u, f0);
+    }
+    if (s + 1u < nst) step(s++, f1);
+    gemm_compute<TW, DUAL>(st[s & 1u], acc, acc2);
     const uint32_t col = n0 + wave * 32u + (lane % 32u);
 #pragma unroll
     for (uint32_t r = 0; r < 16; ++r) {
         const uint32_t row = (r / 4u) * 8u + (lane / 32u) * 4u + (r % 4u);
         if (row < tr.rows) {
-            const uint32_t slot = a.perm[tr.base + row];  // token * top_k + route
-            a.out[static_cast<uint64_t>(slot) * H + col] = acc[r];
+            if constexpr (DUAL) {
+                // SwiGLU g / (1 + expf(-g)) * u (src/qwen3_moe_runner.cpp:682-684)
+                const float g = acc[r], u = acc2[r];
+                a.act[static_cast<uint64_t>(tr.base + row) * ndim + col] = (g / (1.0f + expf(-g))) * u;
+            } else {
+                float* o = a.out + static_cast<uint64_t>(oslot[row]) * ndim + col;
+                o[0] = acc[r];
+                o[kTileN] = acc2[r];
+            }
         }
     }
 }
@@ -445,27 +690,45 @@ __global__ __launch_bounds__(256) void k_combine(MoePrefillArgs a) {
 // ---------------------------------------------------------------------------
 // Host side.
 
-template <int T>
-constexpr bool prefill_type() {
-    return T == T_Q4_K || T == T_Q5_K || T == T_Q6_K || T == T_Q8_0 || T == T_Q4_0;
-}
-
 bool prefill_type_ok(uint32_t t) {
     return t == T_Q4_K || t == T_Q5_K || t == T_Q6_K || t == T_Q8_0 || t == T_Q4_0;
 }
 
 uint32_t ceil_div_u(uint32_t a, uint32_t b) { return (a + b - 1u) / b; }
 
-template <int TG>
-hipError_t gate_up_mfma_t(const MoePrefillArgs& a, hipStream_t s) {
-    hipLaunchKernelGGL((k_gate_up_mfma<TG>), dim3(a.max_tiles, a.layer.ffn / kTileN), dim3(256), 0, s, a);
+template <uint32_t G>
+void split_t(const float* src, uint64_t rows, uint32_t cols, uint16_t* parts, float* sums,
+             hipStream_t s) {
+    const uint32_t pieces = static_cast<uint32_t>(rows * cols / 16u);
+    hipLaunchKernelGGL(k_split<G>, dim3(ceil_div_u(pieces, 256u)), dim3(256), 0, s, src, pieces,
+                       parts, rows * cols, sums);
+}
+
+template <int TW, bool DUAL>
+hipError_t expert_gemm_t(const MoePrefillArgs& a, hipStream_t s) {
+    const MoeDecodeArgs& L = a.layer;
+    constexpr uint32_t G = GemmCfg<TW, DUAL>::G;
+    if constexpr (DUAL)
+        split_t<G>(a.x, a.tokens, L.hidden, a.x_parts, a.x_sums, s);
+    else
+        split_t<G>(a.act, static_cast<uint64_t>(a.tokens) * L.top_k, L.ffn, a.act_parts,
+                   a.act_sums, s);
+    const uint32_t nb = DUAL ? L.ffn / kTileN : L.hidden / (2u * kTileN);
+    const uint32_t blocks = 8u * ceil_div_u(a.max_tiles, 8u) * nb;  // xcd_tile's layout
+    hipLaunchKernelGGL((k_expert_gemm<TW, DUAL>), dim3(blocks), dim3(256), 0, s, a);
     return hipGetLastError();
 }
 
-template <int TD>
-hipError_t down_mfma_t(const MoePrefillArgs& a, hipStream_t s) {
-    hipLaunchKernelGGL((k_down_mfma<TD>), dim3(a.max_tiles, a.layer.hidden / kTileN), dim3(256), 0, s, a);
-    return hipGetLastError();
+template <bool DUAL>
+hipError_t expert_gemm(uint32_t type, const MoePrefillArgs& a, hipStream_t s) {
+    switch (type) {
+        case T_Q4_K: return expert_gemm_t<T_Q4_K, DUAL>(a, s);
+        case T_Q5_K: return expert_gemm_t<T_Q5_K, DUAL>(a, s);
+        case T_Q6_K: return expert_gemm_t<T_Q6_K, DUAL>(a, s);
+        case T_Q8_0: return expert_gemm_t<T_Q8_0, DUAL>(a, s);
+        case T_Q4_0: return expert_gemm_t<T_Q4_0, DUAL>(a, s);
+        default: return hipErrorInvalidValue;
+    }
 }
 
 }  // namespace
@@ -486,12 +749,13 @@ bool moe_prefill_supported(uint32_t gate_type, uint32_t up_type, uint32_t down_t
         case 2: case 4: case 8: case 12: case 16: case 24: case 32: break;
         default: return false;
     }
-    if (ffn % kTileN || hidden % kTileN || ffn % (2 * kChunk)) return false;
+    // hidden and ffn are multiples of 256: whole 128-row blocks, 32- and 64-value stages
+
     return n_experts >= 1 && n_experts <= kMaxExperts && top_k >= 1 && top_k <= kMaxTopK &&
            top_k <= n_experts;
 }
 
-hipError_t launch_moe_prefill(const MoePrefillArgs& a, hipStream_t s) {
+hipError_t launch_prefill_routing(const MoePrefillArgs& a, hipStream_t s) {
     const MoeDecodeArgs& L = a.layer;
     // 1. router
     const dim3 rgrid(L.n_experts, ceil_div_u(a.tokens, kRouterTokens));
@@ -513,28 +777,17 @@ hipError_t launch_moe_prefill(const MoePrefillArgs& a, hipStream_t s) {
     }
     // 3. grouping
     hipLaunchKernelGGL(k_group, dim3(1), dim3(kGroupThreads), 0, s, a);
-    // 4. gate/up
-    hipError_t err = hipSuccess;
-    switch (L.gate_type) {
-        case T_Q4_K: err = gate_up_mfma_t<T_Q4_K>(a, s); break;
-        case T_Q5_K: err = gate_up_mfma_t<T_Q5_K>(a, s); break;
-        case T_Q6_K: err = gate_up_mfma_t<T_Q6_K>(a, s); break;
-        case T_Q8_0: err = gate_up_mfma_t<T_Q8_0>(a, s); break;
-        case T_Q4_0: err = gate_up_mfma_t<T_Q4_0>(a, s); break;
-        default: return hipErrorInvalidValue;
-    }
+    return hipGetLastError();
+}
+
+hipError_t launch_prefill_gate_up(const MoePrefillArgs& a, hipStream_t s) {
+    return expert_gemm<true>(a.layer.gate_type, a, s);
+}
+
+hipError_t launch_prefill_down(const MoePrefillArgs& a, hipStream_t s) {
+    const MoeDecodeArgs& L = a.layer;
+    const hipError_t err = expert_gemm<false>(L.down_type, a, s);
     if (err != hipSuccess) return err;
-    // 5. down
-    switch (L.down_type) {
-        case T_Q4_K: err = down_mfma_t<T_Q4_K>(a, s); break;
-        case T_Q5_K: err = down_mfma_t<T_Q5_K>(a, s); break;
-        case T_Q6_K: err = down_mfma_t<T_Q6_K>(a, s); break;
-        case T_Q8_0: err = down_mfma_t<T_Q8_0>(a, s); break;
-        case T_Q4_0: err = down_mfma_t<T_Q4_0>(a, s); break;
-        default: return hipErrorInvalidValue;
-    }
-    if (err != hipSuccess) return err;
-    // 6. combine
     hipLaunchKernelGGL(k_combine, dim3(a.tokens, ceil_div_u(L.hidden, 256u)), dim3(256), 0, s, a);
     return hipGetLastError();
 }

@@ -181,8 +181,8 @@ def pin_direction(z: np.ndarray, u: np.ndarray, a: float = 1.0) -> np.ndarray:
     return (z - np.outer(z @ u, u) + a * u).astype(np.float32)
 
 
-def zipf_router(layer: "MoeLayer", seed: int, s: float = 1.1, calib_tokens: int = 4096,
-                iters: int = 200) -> tuple[np.ndarray, np.ndarray]:
+def zipf_router(experts: int, hidden: int, top_k: int, seed: int, s: float = 1.1,
+                calib_tokens: int = 4096, iters: int = 200) -> tuple[np.ndarray, np.ndarray]:
     """Router rows (float32 [experts, hidden]) that realise a Zipf(s) expert
     load on tokens drawn by ``zipf_tokens(seed, ...)``.
 
@@ -195,7 +195,7 @@ def zipf_router(layer: "MoeLayer", seed: int, s: float = 1.1, calib_tokens: int 
     ranks are assigned to expert ids in a seeded random order.  Returns the
     router and each expert's target share: its expected picks per token
     (the shares sum to top_k; multiply by a token count for counts)."""
-    E, H, K = layer.experts, layer.hidden, layer.top_k
+    E, H, K = experts, hidden, top_k
     g = rng(seed + 1)
     u = zipf_direction(seed, H)
     G = g.standard_normal((E, H)) / np.sqrt(H)

@@ -99,7 +99,7 @@ def c4(hip):
     """The C3 layer (2048 -> 768, 128 experts, top-8, Q4_K gate/up, Q6_K down)
     with a router that realises a Zipf(1.1) expert load over 512 tokens."""
     layer = G.c3_layer()
-    layer.router, share = S.zipf_router(layer, seed=404)
+    layer.router, _ = S.zipf_router(layer.experts, layer.hidden, layer.top_k, seed=404)
     x = S.zipf_tokens(404, 512, layer.hidden)
     h = hip.upload_moe_layer(layer)
     yield layer, h, x

@@ -30,8 +30,7 @@ def test_zipf_router_realises_the_skew():
     """The fitted router, applied to fresh tokens (top-k of exact float64
     logits), gives a load whose exponent is near 1.1 with the top expert
     taken by nearly every token."""
-    layer = S.moe_layer(seed=3, hidden=512, experts=64, ffn=256, top_k=8)
-    router, share = S.zipf_router(layer, seed=5, calib_tokens=2048, iters=120)
+    router, share = S.zipf_router(64, 512, 8, seed=5, calib_tokens=2048, iters=120)
     assert router.shape == (64, 512) and router.dtype == np.float32
     assert abs(share.sum() - 8) < 1e-9
     x = S.zipf_tokens(5, 1024, 512)
