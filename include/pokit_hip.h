@@ -173,7 +173,9 @@ pk_hip_status pk_hip_moe_decode_async(pk_hip_ctx* ctx, const pk_hip_moe_layer* l
  * states; y [tokens][hidden], ids and probs [tokens][top_k] receive each
  * token's moe_result and routes, equal to pk_hip_moe_decode's for that token
  * (ids bit-exact, outputs within FP32 reassociation).  Tokens are grouped per
- * expert and the expert products run as FP32 MFMA GEMMs.  1 <= tokens <=
+ * expert; the expert products run on bf16 MFMA with exact products (FP32
+ * activations split into three bf16 parts, the quantised weights as exact
+ * bf16 integers, scales applied per group in FP32).  1 <= tokens <=
  * 4096; gate/up and down of any K-quant/Q8_0/Q4_0 type, ffn a multiple of
  * 256.  Host buffers; synchronous.  Non-finite router logits return
  * RUNTIME_ERROR. */
@@ -188,6 +190,68 @@ pk_hip_status pk_hip_moe_prefill_async(pk_hip_ctx* ctx, const pk_hip_moe_layer* 
                                        const float* device_x, uint32_t tokens, float* device_y,
                                        uint32_t* device_ids, float* device_probs, void* stream,
                                        char* error_buffer, size_t error_capacity);
+
+/* ---- Whole-model greedy decode (Qwen3-MoE) ------------------------------------
+ * Qwen3MoeRunner (include/pokitlms/model/qwen3_moe_runner.hpp:57-110) with
+ * every layer of a token step on the GPU: forward_into
+ * (src/qwen3_moe_runner.cpp:580-704) per token, greedy first-max argmax
+ * (sample_token at temperature 0, :320-333), FP16 KV ring of kv_capacity
+ * positions (the runner's context window, :372-376; kv_cache.cpp:131-294).
+ * All weights are pk_hip_weight handles already resident on the context's
+ * device; norm vectors are F32 [n, 1] uploads. */
+typedef struct pk_hip_qwen3moe pk_hip_qwen3moe;
+
+typedef struct pk_hip_qwen3moe_config {
+    uint32_t layers, hidden, heads, kv_heads, head_dim; /* qwen3moe.* GGUF keys */
+    uint32_t experts, top_k, ffn, vocab;
+    uint32_t kv_capacity;                               /* <= 8192 positions */
+    uint32_t normalize;                                 /* expert_weights_norm */
+    float rms_eps, rope_theta;
+} pk_hip_qwen3moe_config;
+
+typedef struct pk_hip_qwen3moe_layer {
+    const pk_hip_weight *attn_norm, *q, *q_norm, *k, *k_norm, *v, *o, *ffn_norm;
+    const pk_hip_weight *router, *gate, *up, *down; /* as pk_hip_moe_layer */
+} pk_hip_qwen3moe_layer;
+
+typedef struct pk_hip_qwen3moe_weights {
+    const pk_hip_weight *token_embd, *output_norm, *output;
+    const pk_hip_qwen3moe_layer* layers; /* [config.layers] */
+} pk_hip_qwen3moe_weights;
+
+typedef struct pk_hip_generation_stats {
+    uint64_t prefill_ns;      /* host wall time of the prompt forwards */
+    uint64_t decode_ns;       /* device time of the decode forwards (HIP events) */
+    uint32_t prompt_tokens;
+    uint32_t decode_forwards; /* n_new - 1: the first token comes from the prompt's logits */
+} pk_hip_generation_stats;
+
+/* Validates shapes against the reference index (src/qwen3_moe_index.cpp:37-85)
+ * and builds the device state; the weights must outlive the model. */
+pk_hip_status pk_hip_qwen3moe_create(pk_hip_ctx* ctx, const pk_hip_qwen3moe_config* config,
+                                     const pk_hip_qwen3moe_weights* weights,
+                                     pk_hip_qwen3moe** out_model, char* error_buffer,
+                                     size_t error_capacity);
+void pk_hip_qwen3moe_destroy(pk_hip_qwen3moe* model);
+
+/* generate_tokens (qwen3_moe_runner.hpp:74-78) at temperature 0 without an EOS
+ * stop: resets the state, feeds the prompt at positions 0.., then writes n_new
+ * greedy tokens to out_tokens.  last_logits (optional, vocab floats) receives
+ * the logits after the last prompt token.  Non-finite router logits or
+ * logits return RUNTIME_ERROR (route_experts and sample_token throw). */
+pk_hip_status pk_hip_qwen3moe_generate(pk_hip_qwen3moe* model, const uint32_t* prompt,
+                                       uint32_t n_prompt, uint32_t n_new, uint32_t* out_tokens,
+                                       float* last_logits, pk_hip_generation_stats* stats,
+                                       char* error_buffer, size_t error_capacity);
+
+/* Seeded synthetic weights made in HBM (no counterpart in the reference: the
+ * benchmark and test models, byte-identical to pokitlms_amd/synth_model.py):
+ * word i = splitmix64(key + i), then the scale fix-up `kind` (0 none, 1
+ * K-quant, 2 Q6_K, 3 F32 norm, 4 F32 router). */
+pk_hip_status pk_hip_synth_weight(pk_hip_ctx* ctx, uint32_t ggml_type, uint64_t in, uint64_t out,
+                                  uint32_t n_experts, uint64_t key, uint32_t kind,
+                                  pk_hip_weight** out_weight, char* error_buffer,
+                                  size_t error_capacity);
 
 /* Waits for the context's work (and `stream`, if not NULL) and reports any
  * deferred router error. */

@@ -96,6 +96,9 @@ class Oracle:
                                            ctypes.c_uint32, ctypes.c_int]
             L.pkref_moe_forward.argtypes = [ctypes.c_void_p, _f32p, _f32p, _u32p, _f32p]
             L.pkref_moe_destroy.argtypes = [ctypes.c_void_p]
+            L.pkref_qwen3moe_greedy.argtypes = [ctypes.c_char_p, _u32p, ctypes.c_uint32,
+                                                ctypes.c_uint32, ctypes.c_uint64, _u32p, _f32p,
+                                                ctypes.POINTER(ctypes.c_double)]
 
     # ---- single ops -------------------------------------------------------
     def half_to_float(self, bits: int) -> float:
@@ -151,6 +154,26 @@ class Oracle:
         return ids[:top_k], sel[:top_k], probs[:top_k]
 
     # ---- MoE block -----------------------------------------------------------
+    def qwen3moe_greedy(self, path: str, prompt: np.ndarray, n_new: int,
+                        expert_cache_bytes: int = 1 << 40, want_logits: bool = False,
+                        vocab: int = 0):
+        """The reference Qwen3MoeRunner on a GGUF file (reference library
+        only): greedy tokens [n_new], logits after the prompt (or None) and
+        the decode forwards' wall seconds."""
+        if self.kind != "reference":
+            raise OracleError(1, "qwen3moe_greedy needs the compiled reference")
+        p = np.ascontiguousarray(prompt, np.uint32)
+        out = np.zeros(max(n_new, 1), np.uint32)
+        logits = np.zeros(vocab, np.float32) if want_logits else None
+        secs = ctypes.c_double()
+        rc = self.lib.pkref_qwen3moe_greedy(path.encode(), p.ctypes.data_as(_u32p), p.size, n_new,
+                                            expert_cache_bytes, out.ctypes.data_as(_u32p),
+                                            _fp(logits) if want_logits else None,
+                                            ctypes.byref(secs))
+        if rc:
+            raise OracleError(rc, "pkref_qwen3moe_greedy")
+        return out[:n_new], logits, secs.value
+
     def moe(self, layer) -> "MoeBlock":
         return MoeBlock(self, layer)
 

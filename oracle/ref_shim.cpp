@@ -197,4 +197,44 @@ int pkref_moe_forward(pkref_moe* moe, const float* x, float* y, std::uint32_t* i
     }
 }
 
+// Greedy generation with the reference Qwen3MoeRunner on a GGUF file: every
+// prompt token through forward_token (:785-790), then n_new tokens by
+// first-max argmax (sample_token at temperature 0, :320-333) without an EOS
+// stop.  out_tokens[n_new]; last_logits (optional, vocab floats) receives the
+// logits after the final prompt token.  decode_seconds (optional) receives
+// the wall time of the n_new - 1 decode forwards.
+int pkref_qwen3moe_greedy(const char* path, const std::uint32_t* prompt, std::uint32_t n_prompt,
+                          std::uint32_t n_new, std::uint64_t expert_cache_bytes,
+                          std::uint32_t* out_tokens, float* last_logits, double* decode_seconds) {
+    try {
+        if (!path || !prompt || n_prompt == 0 || !out_tokens) {
+            throw std::invalid_argument("path, prompt and output are required");
+        }
+        pokitlms::model::Qwen3MoeRunner runner(path, static_cast<std::size_t>(expert_cache_bytes));
+        std::vector<float> logits;
+        for (std::uint32_t i = 0; i < n_prompt; ++i) logits = runner.forward_token(prompt[i], i);
+        if (last_logits) std::copy(logits.begin(), logits.end(), last_logits);
+        const auto argmax = [](const std::vector<float>& l) {
+            std::size_t best = 0;
+            for (std::size_t i = 0; i < l.size(); ++i) {
+                if (!std::isfinite(l[i])) throw std::runtime_error("model produced non-finite logits");
+                if (l[i] > l[best]) best = i;
+            }
+            return static_cast<std::uint32_t>(best);
+        };
+        const auto start = std::chrono::steady_clock::now();
+        for (std::uint32_t j = 0; j < n_new; ++j) {
+            out_tokens[j] = argmax(logits);
+            if (j + 1 < n_new) logits = runner.forward_token(out_tokens[j], n_prompt + j);
+        }
+        if (decode_seconds) {
+            *decode_seconds = std::chrono::duration<double>(std::chrono::steady_clock::now() - start)
+                                  .count();
+        }
+        return 0;
+    } catch (...) {
+        return status_of_current_exception();
+    }
+}
+
 }  // extern "C"

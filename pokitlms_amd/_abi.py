@@ -27,7 +27,8 @@ EXPORTS = (
     "pk_hip_weight_device_ptr", "pk_hip_matvec", "pk_hip_matvec_async", "pk_hip_moe_decode",
     "pk_hip_moe_decode_async", "pk_hip_sync", "pk_hip_get_stats", "pk_hip_reset_stats",
     "pk_hip_set_kernel_timing", "pk_hip_device_name", "pk_hip_moe_prefill",
-    "pk_hip_moe_prefill_async",
+    "pk_hip_moe_prefill_async", "pk_hip_qwen3moe_create", "pk_hip_qwen3moe_destroy",
+    "pk_hip_qwen3moe_generate", "pk_hip_synth_weight",
 )
 
 
@@ -53,6 +54,28 @@ class MoeLayerDesc(ctypes.Structure):
     _fields_ = [("router", ctypes.c_void_p), ("gate", ctypes.c_void_p), ("up", ctypes.c_void_p),
                 ("down", ctypes.c_void_p), ("top_k", ctypes.c_uint32),
                 ("normalize", ctypes.c_uint32), ("scale", ctypes.c_float)]
+
+
+class Qwen3MoeConfig(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_uint32) for n in (
+        "layers", "hidden", "heads", "kv_heads", "head_dim", "experts", "top_k", "ffn", "vocab",
+        "kv_capacity", "normalize")] + [("rms_eps", ctypes.c_float), ("rope_theta", ctypes.c_float)]
+
+
+class Qwen3MoeLayer(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_void_p) for n in (
+        "attn_norm", "q", "q_norm", "k", "k_norm", "v", "o", "ffn_norm", "router", "gate", "up",
+        "down")]
+
+
+class Qwen3MoeWeights(ctypes.Structure):
+    _fields_ = [("token_embd", ctypes.c_void_p), ("output_norm", ctypes.c_void_p),
+                ("output", ctypes.c_void_p), ("layers", ctypes.POINTER(Qwen3MoeLayer))]
+
+
+class GenerationStats(ctypes.Structure):
+    _fields_ = [("prefill_ns", ctypes.c_uint64), ("decode_ns", ctypes.c_uint64),
+                ("prompt_tokens", ctypes.c_uint32), ("decode_forwards", ctypes.c_uint32)]
 
 
 _lib = None
@@ -112,5 +135,15 @@ def lib() -> ctypes.CDLL:
     L.pk_hip_moe_prefill_async.argtypes = [vp, ctypes.POINTER(MoeLayerDesc), vp, u32, vp, vp, vp,
                                            vp, cp, sz]
     L.pk_hip_device_name.argtypes = [vp, cp, sz]
+    L.pk_hip_qwen3moe_create.restype = ctypes.c_int
+    L.pk_hip_qwen3moe_create.argtypes = [vp, ctypes.POINTER(Qwen3MoeConfig),
+                                         ctypes.POINTER(Qwen3MoeWeights), ctypes.POINTER(vp), cp, sz]
+    L.pk_hip_qwen3moe_destroy.restype = None
+    L.pk_hip_qwen3moe_destroy.argtypes = [vp]
+    L.pk_hip_qwen3moe_generate.restype = ctypes.c_int
+    L.pk_hip_qwen3moe_generate.argtypes = [vp, up, u32, u32, up, fp,
+                                           ctypes.POINTER(GenerationStats), cp, sz]
+    L.pk_hip_synth_weight.restype = ctypes.c_int
+    L.pk_hip_synth_weight.argtypes = [vp, u32, u64, u64, u32, u64, u32, ctypes.POINTER(vp), cp, sz]
     _lib = L
     return L

@@ -9,10 +9,14 @@
 
 #include <algorithm>
 #include <cstring>
+#include <chrono>
+#include <cmath>
+#include <memory>
 #include <mutex>
 #include <new>
 #include <stdexcept>
 #include <string>
+#include <vector>
 
 #include "../../include/pokit_hip.h"
 #include "launch.hpp"
@@ -745,6 +749,328 @@ pk_hip_status pk_hip_sync(pk_hip_ctx* ctx, void* stream, char* err, size_t cap) 
         ctx->set_device();
         if (stream) check(hipStreamSynchronize(static_cast<hipStream_t>(stream)), "sync stream");
         sync_and_check(ctx, ctx->stream);
+    });
+}
+
+// ---------------------------------------------------------------------------
+// Whole-model greedy decode (Qwen3MoeRunner on the device).
+
+struct pk_hip_qwen3moe {
+    pk_hip_ctx* ctx = nullptr;
+    pk_hip_qwen3moe_config cfg{};
+    pk::ModelArgs args{};
+    std::vector<pk::ModelLayer> layers;
+    DeviceBuffer<uint32_t> state, tokens, ids, moe_status;
+    DeviceBuffer<float> work, probs, act, moe_out;
+    DeviceBuffer<double> row_sum, row_bound;
+    DeviceBuffer<uint16_t> kv;
+    hipGraphExec_t step_logits = nullptr, step_plain = nullptr;
+    hipEvent_t ev[2] = {};
+};
+
+namespace {
+
+const uint8_t* weight_bytes(const pk_hip_weight* w) { return w->dptr; }
+
+void require_weight(const pk_hip_weight* w, const char* what, uint64_t in, uint64_t out) {
+    if (!w) throw ArgError(std::string("missing weight: ") + what);
+    if (w->in != in || w->out != out || w->n_experts != 0)
+        throw ArgError(std::string("unexpected dimensions for weight: ") + what);
+}
+
+void require_vector(const pk_hip_weight* w, const char* what, uint64_t n) {
+    require_weight(w, what, n, 1);
+    if (w->type != 0) throw ArgError(std::string("norm weight must be F32: ") + what);
+}
+
+void require_matvec(const pk_hip_weight* w, const char* what, uint64_t in, uint64_t out) {
+    require_weight(w, what, in, out);
+    if (!pk::matvec_supported(w->type, static_cast<uint32_t>(in), 1))
+        throw Unsupported(std::string("no matvec kernel for weight: ") + what);
+}
+
+hipGraphExec_t capture_step(pk_hip_qwen3moe* m, bool logits) {
+    hipStream_t s = m->ctx->stream;
+    check(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal), "hipStreamBeginCapture");
+    const hipError_t launched = pk::launch_model_step(m->args, m->layers.data(), logits, s);
+    hipGraph_t graph = nullptr;
+    const hipError_t ended = hipStreamEndCapture(s, &graph);
+    check(launched, "model step launch");
+    check(ended, "hipStreamEndCapture");
+    hipGraphExec_t exec = nullptr;
+    const hipError_t inst = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(graph);
+    check(inst, "hipGraphInstantiate");
+    return exec;
+}
+
+void release_model(pk_hip_qwen3moe* m) {
+    if (m->step_logits) (void)hipGraphExecDestroy(m->step_logits);
+    if (m->step_plain) (void)hipGraphExecDestroy(m->step_plain);
+    for (auto& e : m->ev)
+        if (e) (void)hipEventDestroy(e);
+    m->state.release();
+    m->tokens.release();
+    m->ids.release();
+    m->moe_status.release();
+    m->work.release();
+    m->probs.release();
+    m->act.release();
+    m->moe_out.release();
+    m->row_sum.release();
+    m->row_bound.release();
+    m->kv.release();
+}
+
+}  // namespace
+
+pk_hip_status pk_hip_qwen3moe_create(pk_hip_ctx* ctx, const pk_hip_qwen3moe_config* cfg,
+                                     const pk_hip_qwen3moe_weights* w, pk_hip_qwen3moe** out,
+                                     char* err, size_t cap) {
+    return guarded(ctx, err, cap, [&] {
+        require_usable(ctx);
+        if (!cfg || !w || !out || !w->layers) throw ArgError("config, weights and output are required");
+        const pk_hip_qwen3moe_config& c = *cfg;
+        if (c.layers == 0 || c.hidden == 0 || c.heads == 0 || c.kv_heads == 0 || c.head_dim == 0 ||
+            c.vocab == 0 || c.kv_capacity == 0)
+            throw ArgError("model dimensions must be non-zero");
+        if (c.heads % c.kv_heads) throw ArgError("query heads must be evenly grouped over KV heads");
+        if (!(c.rms_eps > 0.0f) || !(c.rope_theta > 0.0f)) throw ArgError("invalid norm epsilon or RoPE base");
+        const uint64_t qd = uint64_t(c.heads) * c.head_dim, kd = uint64_t(c.kv_heads) * c.head_dim;
+        require_weight(w->token_embd, "token_embd", c.hidden, c.vocab);
+        require_vector(w->output_norm, "output_norm", c.hidden);
+        require_matvec(w->output, "output", c.hidden, c.vocab);
+        std::lock_guard lock(ctx->mutex);
+        ctx->set_device();
+        auto m = std::make_unique<pk_hip_qwen3moe>();
+        m->ctx = ctx;
+        m->cfg = c;
+        pk::ModelArgs& a = m->args;
+        a.layers = c.layers;
+        a.hidden = c.hidden;
+        a.heads = c.heads;
+        a.kv_heads = c.kv_heads;
+        a.head_dim = c.head_dim;
+        a.vocab = c.vocab;
+        a.capacity = c.kv_capacity;
+        a.embd_type = w->token_embd->type;
+        a.out_type = w->output->type;
+        a.embd_row = w->token_embd->row_bytes;
+        a.out_row = w->output->row_bytes;
+        a.rms_eps = c.rms_eps;
+        a.rope_theta = c.rope_theta;
+        a.attn_scale = 1.0f / std::sqrt(static_cast<float>(c.head_dim));  // KvCache::attend default
+        a.embd = weight_bytes(w->token_embd);
+        a.out_norm = reinterpret_cast<const float*>(weight_bytes(w->output_norm));
+        a.out = weight_bytes(w->output);
+        if (!pk::model_supported(a)) throw Unsupported("model shape not covered by the HIP kernels");
+        // device state and activations
+        m->state.ensure(4);
+        m->tokens.ensure(1);
+        const uint64_t wf = 3ull * c.hidden + 2 * qd + 2 * kd + c.head_dim + c.vocab;
+        m->work.ensure(wf);
+        float* p = m->work.ptr;
+        a.hidden_state = p; p += c.hidden;
+        a.normed = p; p += c.hidden;
+        a.attn_out = p; p += c.hidden;
+        a.q = p; p += qd;
+        a.att = p; p += qd;
+        a.k = p; p += kd;
+        a.v = p; p += kd;
+        a.rope = p; p += c.head_dim;
+        a.logits = p;
+        a.state = m->state.ptr;
+        m->kv.ensure(2ull * c.layers * c.kv_capacity * kd);
+        uint32_t max_experts = 1, max_k = 1, max_ffn = 1;
+        for (uint32_t l = 0; l < c.layers; ++l) {
+            const pk_hip_qwen3moe_layer& L = w->layers[l];
+            if (!L.router || !L.gate || !L.up || !L.down) throw ArgError("missing MoE weight");
+            max_experts = std::max<uint32_t>(max_experts, static_cast<uint32_t>(L.router->out));
+            max_ffn = std::max<uint32_t>(max_ffn, static_cast<uint32_t>(L.gate->out));
+        }
+        max_k = c.top_k;
+        m->ids.ensure(16);
+        m->probs.ensure(16);
+        m->moe_status.ensure(4);
+        m->act.ensure(uint64_t(max_k) * max_ffn);
+        m->row_sum.ensure(max_experts);
+        m->row_bound.ensure(max_experts);
+        m->moe_out.ensure(c.hidden);
+        check(hipMemsetAsync(m->moe_status.ptr, 0, 4 * sizeof(uint32_t), ctx->stream), "clear status");
+        m->layers.resize(c.layers);
+        for (uint32_t l = 0; l < c.layers; ++l) {
+            const pk_hip_qwen3moe_layer& L = w->layers[l];
+            pk::ModelLayer& D = m->layers[l];
+            require_vector(L.attn_norm, "attn_norm", c.hidden);
+            require_vector(L.q_norm, "attn_q_norm", c.head_dim);
+            require_vector(L.k_norm, "attn_k_norm", c.head_dim);
+            require_vector(L.ffn_norm, "ffn_norm", c.hidden);
+            require_matvec(L.q, "attn_q", c.hidden, qd);
+            require_matvec(L.k, "attn_k", c.hidden, kd);
+            require_matvec(L.v, "attn_v", c.hidden, kd);
+            require_matvec(L.o, "attn_output", qd, c.hidden);
+            if (L.k->type != L.q->type || L.v->type != L.q->type || L.o->type != L.q->type)
+                throw Unsupported("attention weights must share one format");
+            const pk_hip_moe_layer ml{L.router, L.gate, L.up, L.down, c.top_k, c.normalize, 1.0f};
+            const MoeShape ms = check_decode_layer(ctx, &ml);
+            if (ms.hidden != c.hidden) throw ArgError("MoE layer width does not match the model");
+            D.attn_norm = reinterpret_cast<const float*>(weight_bytes(L.attn_norm));
+            D.q_norm = reinterpret_cast<const float*>(weight_bytes(L.q_norm));
+            D.k_norm = reinterpret_cast<const float*>(weight_bytes(L.k_norm));
+            D.ffn_norm = reinterpret_cast<const float*>(weight_bytes(L.ffn_norm));
+            D.q = weight_bytes(L.q);
+            D.k = weight_bytes(L.k);
+            D.v = weight_bytes(L.v);
+            D.o = weight_bytes(L.o);
+            D.attn_type = L.q->type;
+            D.q_row = L.q->row_bytes;
+            D.k_row = L.k->row_bytes;
+            D.v_row = L.v->row_bytes;
+            D.o_row = L.o->row_bytes;
+            D.kcache = m->kv.ptr + 2ull * l * c.kv_capacity * kd;
+            D.vcache = D.kcache + uint64_t(c.kv_capacity) * kd;
+            pk::MoeDecodeArgs& g = D.moe;
+            g = pk::MoeDecodeArgs{};
+            g.router = reinterpret_cast<const float*>(L.router->dptr);
+            g.gate = L.gate->dptr;
+            g.up = L.up->dptr;
+            g.down = L.down->dptr;
+            g.gate_type = L.gate->type;
+            g.up_type = L.up->type;
+            g.down_type = L.down->type;
+            g.gate_slice = L.gate->slice_bytes;
+            g.up_slice = L.up->slice_bytes;
+            g.down_slice = L.down->slice_bytes;
+            g.gate_row = L.gate->row_bytes;
+            g.up_row = L.up->row_bytes;
+            g.down_row = L.down->row_bytes;
+            g.hidden = ms.hidden;
+            g.ffn = ms.ffn;
+            g.n_experts = ms.experts;
+            g.top_k = c.top_k;
+            g.normalize = c.normalize ? 1u : 0u;
+            g.scale = 1.0f;
+            g.x = a.normed;
+            g.y = m->moe_out.ptr;
+            g.ids = m->ids.ptr;
+            g.probs = m->probs.ptr;
+            g.row_sum = m->row_sum.ptr;
+            g.row_bound = m->row_bound.ptr;
+            g.act = m->act.ptr;
+            g.status = m->moe_status.ptr;
+        }
+        for (auto& e : m->ev) check(hipEventCreate(&e), "hipEventCreate");
+        *out = m.release();
+    });
+}
+
+void pk_hip_qwen3moe_destroy(pk_hip_qwen3moe* m) {
+    if (!m) return;
+    if (m->ctx) {
+        std::lock_guard lock(m->ctx->mutex);
+        (void)hipSetDevice(m->ctx->device);
+        (void)hipStreamSynchronize(m->ctx->stream);
+        release_model(m);
+    }
+    delete m;
+}
+
+pk_hip_status pk_hip_qwen3moe_generate(pk_hip_qwen3moe* m, const uint32_t* prompt,
+                                       uint32_t n_prompt, uint32_t n_new, uint32_t* out_tokens,
+                                       float* last_logits, pk_hip_generation_stats* stats,
+                                       char* err, size_t cap) {
+    pk_hip_ctx* ctx = m ? m->ctx : nullptr;
+    return guarded(ctx, err, cap, [&] {
+        require_usable(ctx);
+        if (!prompt || n_prompt == 0 || (n_new && !out_tokens))
+            throw ArgError("a prompt and an output buffer are required");
+        const pk::ModelArgs& a = m->args;
+        for (uint32_t i = 0; i < n_prompt; ++i)
+            if (prompt[i] >= a.vocab) throw ArgError("token id exceeds model vocabulary");
+        std::lock_guard lock(ctx->mutex);
+        ctx->set_device();
+        hipStream_t s = ctx->stream;
+        const uint64_t total = uint64_t(n_prompt) + n_new + 1;
+        if (m->tokens.count < total) {
+            m->tokens.ensure(total);
+            // the graphs hold the old token buffer: capture again
+            if (m->step_logits) (void)hipGraphExecDestroy(m->step_logits);
+            if (m->step_plain) (void)hipGraphExecDestroy(m->step_plain);
+            m->step_logits = m->step_plain = nullptr;
+        }
+        m->args.tokens = m->tokens.ptr;
+        check(hipMemcpyAsync(m->tokens.ptr, prompt, n_prompt * sizeof(uint32_t),
+                             hipMemcpyHostToDevice, s),
+              "copy prompt");
+        const uint32_t init[4] = {0, n_prompt, 0, 0};
+        check(hipMemcpyAsync(m->state.ptr, init, sizeof(init), hipMemcpyHostToDevice, s), "reset state");
+        check(hipStreamSynchronize(s), "hipStreamSynchronize");
+        if (!m->step_logits) m->step_logits = capture_step(m, true);
+        if (!m->step_plain) m->step_plain = capture_step(m, false);
+        const auto t0 = std::chrono::steady_clock::now();
+        for (uint32_t i = 0; i + 1 < n_prompt; ++i) check(hipGraphLaunch(m->step_plain, s), "prefill step");
+        check(hipGraphLaunch(m->step_logits, s), "prefill logits step");
+        if (last_logits)
+            check(hipMemcpyAsync(last_logits, a.logits, uint64_t(a.vocab) * sizeof(float),
+                                 hipMemcpyDeviceToHost, s),
+                  "copy logits");
+        check(hipStreamSynchronize(s), "hipStreamSynchronize");
+        const auto t1 = std::chrono::steady_clock::now();
+        check(hipEventRecord(m->ev[0], s), "hipEventRecord");
+        for (uint32_t j = 0; j + 1 < n_new; ++j) check(hipGraphLaunch(m->step_logits, s), "decode step");
+        check(hipEventRecord(m->ev[1], s), "hipEventRecord");
+        check(hipEventSynchronize(m->ev[1]), "hipEventSynchronize");
+        float ms = 0.0f;
+        check(hipEventElapsedTime(&ms, m->ev[0], m->ev[1]), "hipEventElapsedTime");
+        uint32_t flags[4] = {}, moe_flags[4] = {};
+        check(hipMemcpy(flags, m->state.ptr, sizeof(flags), hipMemcpyDeviceToHost), "read state");
+        check(hipMemcpy(moe_flags, m->moe_status.ptr, sizeof(moe_flags), hipMemcpyDeviceToHost),
+              "read router status");
+        if (moe_flags[0] || flags[2]) {
+            const uint32_t zero[4] = {};
+            (void)hipMemcpy(m->moe_status.ptr, zero, sizeof(zero), hipMemcpyHostToDevice);
+            throw std::runtime_error(moe_flags[0] ? "expert router produced non-finite logits"
+                                                  : "model produced non-finite logits");
+        }
+        if (n_new)
+            check(hipMemcpy(out_tokens, m->tokens.ptr + n_prompt, n_new * sizeof(uint32_t),
+                            hipMemcpyDeviceToHost),
+                  "copy tokens");
+        if (stats) {
+            stats->prefill_ns = static_cast<uint64_t>(
+                std::chrono::duration_cast<std::chrono::nanoseconds>(t1 - t0).count());
+            stats->decode_ns = static_cast<uint64_t>(static_cast<double>(ms) * 1.0e6);
+            stats->prompt_tokens = n_prompt;
+            stats->decode_forwards = n_new ? n_new - 1 : 0;
+        }
+    });
+}
+
+pk_hip_status pk_hip_synth_weight(pk_hip_ctx* ctx, uint32_t type, uint64_t in, uint64_t out,
+                                  uint32_t n_experts, uint64_t key, uint32_t kind,
+                                  pk_hip_weight** out_w, char* err, size_t cap) {
+    return guarded(ctx, err, cap, [&] {
+        require_usable(ctx);
+        if (!out_w) throw ArgError("output handle is required");
+        const uint32_t be = block_elements(type), bb = block_bytes(type);
+        if (be == 0) throw Unsupported("GGUF type has no HIP kernel");
+        if (in == 0 || out == 0 || in % be) throw ArgError("invalid GGUF matrix dimensions");
+        const bool kq = kind == 1 && (type == 12 || type == 13), q6 = kind == 2 && type == 14;
+        const bool f32 = (kind == 3 || kind == 4) && type == 0;
+        if (!(kind == 0 || kq || q6 || f32)) throw ArgError("synthetic recipe does not match the type");
+        const uint64_t nbytes = in / be * bb * out * (n_experts ? n_experts : 1);
+        std::lock_guard lock(ctx->mutex);
+        pk_hip_weight* w = make_weight(ctx, type, in, out, n_experts, nbytes);
+        const hipError_t e = pk::launch_synth_fill(w->dptr, nbytes, key, kind, bb, ctx->stream);
+        const hipError_t s = e == hipSuccess ? hipStreamSynchronize(ctx->stream) : e;
+        if (s != hipSuccess) {
+            (void)hipFree(w->dptr);
+            delete w;
+            check(s, "synthetic weights");
+        }
+        ctx->stats.resident_bytes += nbytes;
+        ++ctx->live_weights;
+        *out_w = w;
     });
 }
 

@@ -86,6 +86,55 @@ hipError_t launch_prefill_routing(const MoePrefillArgs& a, hipStream_t stream);
 hipError_t launch_prefill_gate_up(const MoePrefillArgs& a, hipStream_t stream);
 hipError_t launch_prefill_down(const MoePrefillArgs& a, hipStream_t stream);
 
+// Whole-model greedy decode (Qwen3-MoE).  One step = one token through every
+// layer; the step's position and token are read from `state` and `tokens` in
+// device memory, so a captured step graph replays for every token.
+constexpr uint32_t kMaxModelContext = 8192;  // KV ring positions (attention scores in LDS)
+struct ModelLayer {
+    const float* attn_norm;   // [hidden]
+    const float* q_norm;      // [head_dim]
+    const float* k_norm;
+    const float* ffn_norm;    // [hidden]
+    const uint8_t* q;         // [heads * head_dim] rows of [hidden]
+    const uint8_t* k;         // [kv_heads * head_dim] rows
+    const uint8_t* v;
+    const uint8_t* o;         // [hidden] rows of [heads * head_dim]
+    uint32_t attn_type;
+    uint64_t q_row, k_row, v_row, o_row;
+    uint16_t* kcache;         // FP16 [capacity][kv_heads][head_dim]
+    uint16_t* vcache;
+    MoeDecodeArgs moe;        // x = the normed state, y = this layer's MoE output
+};
+struct ModelArgs {
+    uint32_t layers, hidden, heads, kv_heads, head_dim, vocab, capacity;
+    uint32_t embd_type, out_type;
+    uint64_t embd_row, out_row;
+    float rms_eps, rope_theta, attn_scale;
+    const uint8_t* embd;      // token_embd rows [vocab] of [hidden]
+    const float* out_norm;
+    const uint8_t* out;       // output head rows [vocab]
+    uint32_t* state;          // [0] position, [1] prompt length, [2] non-finite logits flag
+    uint32_t* tokens;         // prompt, then generated ids
+    float* hidden_state;      // residual stream [hidden]
+    float* normed;            // [hidden]
+    float* q;                 // [heads * head_dim]
+    float* k;                 // [kv_heads * head_dim]
+    float* v;
+    float* att;               // attention output [heads * head_dim]
+    float* attn_out;          // [hidden]
+    float* rope;              // cos [head_dim / 2], then sin
+    float* logits;            // [vocab]
+};
+bool model_supported(const ModelArgs& a);
+// logits: run the final norm, head and argmax (else only advance the position).
+hipError_t launch_model_step(const ModelArgs& a, const ModelLayer* layers, bool logits,
+                             hipStream_t stream);
+
+// Seeded synthetic weight bytes (see pokitlms_amd/synth_model.py): kind 0 raw,
+// 1 K-quant scale fix-up (block_bytes 144/176), 2 Q6_K, 3 F32 norm, 4 F32 router.
+hipError_t launch_synth_fill(uint8_t* dst, uint64_t nbytes, uint64_t key, uint32_t kind,
+                             uint32_t block_bytes, hipStream_t stream);
+
 // Individual stages (timing and tests).
 hipError_t launch_moe_router(const MoeDecodeArgs& a, hipStream_t stream);
 hipError_t launch_moe_gate_up(const MoeDecodeArgs& a, hipStream_t stream);

@@ -1,0 +1,128 @@
+"""Whole-model Qwen3-MoE greedy decode on the GPU against the reference runner.
+
+The golden tokens (tests/golden/model_golden.npz, written by
+tests/golden/make_model_golden.py) come from the reference's own
+Qwen3MoeRunner reading a GGUF file of the seeded synthetic model; here the
+same model is generated directly in HBM (pk_hip_synth_weight, byte-identical)
+and decoded by pk_hip_qwen3moe_generate.  Bar: greedy token ids identical.
+"""
+import os
+
+import numpy as np
+import pytest
+
+from pokitlms_amd import synth as S
+from pokitlms_amd import synth_model as SM
+from tests.conftest import normwise_rel
+
+pytestmark = pytest.mark.gpu
+
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden", "model_golden.npz")
+
+
+def say(*a):
+    print(*a, flush=True)
+
+
+@pytest.fixture(scope="module")
+def mg():
+    with np.load(GOLDEN, allow_pickle=False) as z:
+        return {k: z[k] for k in z.files}
+
+
+def _device_bytes(w, nbytes):
+    import torch
+    import ctypes
+    t = torch.empty(nbytes, dtype=torch.uint8, device="cuda:0")
+    torch.cuda.synchronize()
+    from pokitlms_amd.backend import HipBackend  # noqa: F401  (library loaded after torch)
+    hip_memcpy = ctypes.CDLL("libamdhip64.so.7").hipMemcpy  # torch's runtime (loaded first)
+    hip_memcpy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int]
+    assert hip_memcpy(t.data_ptr(), w.device_ptr, nbytes, 3) == 0  # device to device
+    return t.cpu().numpy()
+
+
+def test_device_generator_matches_numpy(hip):
+    """pk_hip_synth_weight writes the bytes synth_model.tensor_payload computes,
+    for every fix-up recipe."""
+    import ctypes
+    from pokitlms_amd import _abi
+    from pokitlms_amd.backend import Weight, _ERRBUF, _raise
+    cases = ((S.Q4_K, 512, 24, 0, SM.KIND_KQUANT), (S.Q6_K, 768, 16, 3, SM.KIND_Q6K),
+             (S.F32, 2048, 1, 0, SM.KIND_NORM), (S.F32, 512, 40, 0, SM.KIND_ROUTER),
+             (S.Q4_K, 256, 7, 0, SM.KIND_RAW))
+    for i, (gtype, inn, out, ne, kind) in enumerate(cases):
+        key = SM.tensor_key(99, i)
+        h = ctypes.c_void_p()
+        err = ctypes.create_string_buffer(_ERRBUF)
+        _raise(_abi.lib().pk_hip_synth_weight(hip.handle, gtype, inn, out, ne, key, kind,
+                                              ctypes.byref(h), err, _ERRBUF), err)
+        nbytes = S.row_bytes(gtype, inn) * out * max(ne, 1)
+        w = Weight(hip, h.value, gtype, inn, out, ne, nbytes)
+        got = _device_bytes(w, nbytes)
+        want = SM.tensor_payload(99, i, gtype, kind, nbytes)
+        assert np.array_equal(got, want), (gtype, kind)
+        w.release()
+
+
+def test_small_model_matches_reference(hip, mg):
+    from pokitlms_amd.model import Qwen3MoeModel
+    m = SM.Qwen3MoeShape(layers=int(mg["small_layers"]))
+    with Qwen3MoeModel.synthetic(hip, m, int(mg["small_seed"])) as model:
+        tokens, logits, stats = model.generate(mg["small_prompt"], len(mg["small_tokens"]),
+                                               want_logits=True)
+    err = normwise_rel(logits, mg["small_logits"])
+    say("small model: logits normwise", err, "tokens", tokens[:8], "stats", stats)
+    assert err <= 1e-4
+    assert np.argmax(logits) == np.argmax(mg["small_logits"])
+    assert np.array_equal(tokens, mg["small_tokens"])
+
+
+def test_full_model_greedy_tokens_match_reference(hip, mg):
+    """The 48-layer 30B-A3B-shape model: 128 prompt tokens, 256 greedy tokens."""
+    if "full_tokens" not in mg:
+        pytest.skip("full-model golden not generated (make_model_golden.py without --skip-full)")
+    from pokitlms_amd.model import Qwen3MoeModel
+    m = SM.Qwen3MoeShape(layers=int(mg["full_layers"]))
+    with Qwen3MoeModel.synthetic(hip, m, int(mg["full_seed"])) as model:
+        tokens, _, stats = model.generate(mg["full_prompt"], len(mg["full_tokens"]))
+    same = tokens == mg["full_tokens"]
+    first_diff = int(np.argmin(same)) if not same.all() else -1
+    say("full model: decode", stats["decode_ns"] / 1e6, "ms for", stats["decode_forwards"],
+        "forwards; first mismatch", first_diff)
+    assert same.all(), (first_diff, tokens[max(first_diff - 2, 0):first_diff + 3],
+                        mg["full_tokens"][max(first_diff - 2, 0):first_diff + 3])
+
+
+def test_gguf_file_loads_like_the_generator(hip, tmp_path):
+    """A GGUF file written by synth_model and loaded through the GGUF reader
+    decodes to the same tokens and logits, bit for bit, as the model generated
+    in HBM (same bytes, same kernels)."""
+    from pokitlms_amd.model import Qwen3MoeModel
+    m = SM.Qwen3MoeShape(layers=1, vocab=4096, experts=16, top_k=4, context=1024)
+    path = str(tmp_path / "tiny.gguf")
+    SM.write_gguf(path, m, 5)
+    prompt = SM.prompt_tokens(5, 20, m.vocab)
+    with Qwen3MoeModel.synthetic(hip, m, 5) as a:
+        ta, la, _ = a.generate(prompt, 12, want_logits=True)
+    with Qwen3MoeModel.from_gguf(hip, path) as b:
+        assert (b.shape.layers, b.shape.vocab, b.shape.experts, b.shape.top_k) == (1, 4096, 16, 4)
+        tb, lb, _ = b.generate(prompt, 12, want_logits=True)
+    assert np.array_equal(ta, tb)
+    assert np.array_equal(la.view(np.uint32), lb.view(np.uint32))
+
+
+def test_generation_is_repeatable_and_validated(hip):
+    from pokitlms_amd.model import Qwen3MoeModel
+    m = SM.Qwen3MoeShape(layers=2, vocab=4096, experts=16, top_k=4, context=1024)
+    prompt = SM.prompt_tokens(11, 40, m.vocab)
+    with Qwen3MoeModel.synthetic(hip, m, 11) as model:
+        t0, l0, _ = model.generate(prompt, 30, want_logits=True)
+        t1, l1, _ = model.generate(prompt, 30, want_logits=True)
+        assert np.array_equal(t0, t1) and np.array_equal(l0.view(np.uint32), l1.view(np.uint32))
+        # a shorter prompt after a longer run starts from a clean state
+        t2, _, _ = model.generate(prompt[:10], 5)
+        t3, _, _ = model.generate(prompt[:10], 5)
+        assert np.array_equal(t2, t3)
+        with pytest.raises(ValueError, match="vocabulary"):
+            model.generate(np.array([m.vocab], np.uint32), 2)
