@@ -135,6 +135,17 @@ pk_hip_status pk_hip_matvec_async(pk_hip_ctx* ctx, const pk_hip_weight* weight,
                                   float* device_y, void* stream, char* error_buffer,
                                   size_t error_capacity);
 
+/* y = W . x in the CPU's own summation order: per row ((0 + dot_0) + dot_1)
+ * + ... over blocks, each block dot a left-to-right FP32 chain (linear_k,
+ * linear_quantized, linear: src/quantized_linear.cpp:360-423,
+ * src/linear.cpp:10-31), so outputs equal the reference's bit for bit.
+ * Slower than pk_hip_matvec (one serial chain per row and block); used by the
+ * reference-order model decode.  F32 and Q4_0/Q8_0/Q4_K/Q5_K/Q6_K, width up
+ * to 8192.  Host buffers, batch 1. */
+pk_hip_status pk_hip_matvec_reference_order(pk_hip_ctx* ctx, const pk_hip_weight* weight,
+                                           uint32_t expert, const float* x, float* y,
+                                           char* error_buffer, size_t error_capacity);
+
 /* One Qwen3-MoE routed layer. router: F32 [hidden, n_experts]; gate/up:
  * [hidden, ffn, n_experts]; down: [ffn, hidden, n_experts].  top_k routes by
  * route_experts (src/qwen3_moe_runner.cpp:267-305): expert ids and their
@@ -205,8 +216,23 @@ typedef struct pk_hip_qwen3moe_config {
     uint32_t layers, hidden, heads, kv_heads, head_dim; /* qwen3moe.* GGUF keys */
     uint32_t experts, top_k, ffn, vocab;
     uint32_t kv_capacity;                               /* <= 8192 positions */
+    uint32_t context;                                   /* qwen3moe.context_length */
     uint32_t normalize;                                 /* expert_weights_norm */
+    /* Non-zero: every kernel repeats the CPU's operation order (serial FP32
+     * sums as linear_k/rms_norm/KvCache::attend, route_experts over serial
+     * logits, RoPE table from the host libm), so greedy tokens track the
+     * reference through router and logit near-ties.  Zero: the bandwidth-
+     * optimised kernels (outputs within FP32 reassociation error). */
+    uint32_t reference_order;
     float rms_eps, rope_theta;
+    /* reference_order only: the host libm's expf results that differ from the
+     * correctly rounded exponential, as (input bits, result bits) pairs in
+     * increasing input-bit order (pokitlms_amd/host/expf_table.c writes them;
+     * glibc: 170,648 pairs).  The softmax and SwiGLU exponentials then return
+     * the CPU's bits (kv_cache.cpp:249, qwen3_moe_runner.cpp:683).  Count 0:
+     * the correctly rounded value everywhere. */
+    const uint32_t* libm_expf_pairs;
+    uint64_t libm_expf_count;
 } pk_hip_qwen3moe_config;
 
 typedef struct pk_hip_qwen3moe_layer {

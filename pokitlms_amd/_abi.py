@@ -28,7 +28,7 @@ EXPORTS = (
     "pk_hip_moe_decode_async", "pk_hip_sync", "pk_hip_get_stats", "pk_hip_reset_stats",
     "pk_hip_set_kernel_timing", "pk_hip_device_name", "pk_hip_moe_prefill",
     "pk_hip_moe_prefill_async", "pk_hip_qwen3moe_create", "pk_hip_qwen3moe_destroy",
-    "pk_hip_qwen3moe_generate", "pk_hip_synth_weight",
+    "pk_hip_qwen3moe_generate", "pk_hip_synth_weight", "pk_hip_matvec_reference_order",
 )
 
 
@@ -59,7 +59,9 @@ class MoeLayerDesc(ctypes.Structure):
 class Qwen3MoeConfig(ctypes.Structure):
     _fields_ = [(n, ctypes.c_uint32) for n in (
         "layers", "hidden", "heads", "kv_heads", "head_dim", "experts", "top_k", "ffn", "vocab",
-        "kv_capacity", "normalize")] + [("rms_eps", ctypes.c_float), ("rope_theta", ctypes.c_float)]
+        "kv_capacity", "context", "normalize", "reference_order")] + [
+        ("rms_eps", ctypes.c_float), ("rope_theta", ctypes.c_float),
+        ("libm_expf_pairs", ctypes.c_void_p), ("libm_expf_count", ctypes.c_uint64)]
 
 
 class Qwen3MoeLayer(ctypes.Structure):
@@ -113,6 +115,8 @@ def lib() -> ctypes.CDLL:
     L.pk_hip_weight_device_ptr.argtypes = [vp]
     L.pk_hip_matvec.restype = ctypes.c_int
     L.pk_hip_matvec.argtypes = [vp, vp, u32, fp, u32, fp, cp, sz]
+    L.pk_hip_matvec_reference_order.restype = ctypes.c_int
+    L.pk_hip_matvec_reference_order.argtypes = [vp, vp, u32, fp, fp, cp, sz]
     L.pk_hip_matvec_async.restype = ctypes.c_int
     L.pk_hip_matvec_async.argtypes = [vp, vp, u32, vp, u32, vp, vp, cp, sz]
     L.pk_hip_moe_decode.restype = ctypes.c_int

@@ -168,6 +168,17 @@ class HipBackend:
                                         batch, _f32p(y), err, _ERRBUF), err)
         return y[0] if xx.ndim == 1 else y
 
+    def matvec_reference_order(self, w: Weight, x: np.ndarray,
+                               expert: int | None = None) -> np.ndarray:
+        """W . x summed in the CPU's order (bit-equal to the reference)."""
+        xx = np.ascontiguousarray(x, dtype=np.float32).reshape(-1)
+        y = np.empty(w.out_features, dtype=np.float32)
+        err = ctypes.create_string_buffer(_ERRBUF)
+        _raise(_abi.lib().pk_hip_matvec_reference_order(
+            self.handle, w.handle, _abi.NO_EXPERT if expert is None else expert, _f32p(xx),
+            _f32p(y), err, _ERRBUF), err)
+        return y
+
     def matvec_async(self, w: Weight, device_x: int, batch: int, device_y: int, stream: int = 0,
                      expert: int | None = None) -> None:
         err = ctypes.create_string_buffer(_ERRBUF)

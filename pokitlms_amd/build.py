@@ -2,7 +2,11 @@
 
 ``python -m pokitlms_amd.build`` compiles every ``csrc/*.hip`` translation unit
 with hipcc for gfx950 and links them into ``pokitlms_amd/libpokit_hip.so``,
-in-tree, so the library travels with the source tree to the GPU host.
+in-tree, so the library travels with the source tree to the GPU host.  It
+also compiles and runs ``host/expf_table.c``, which writes ``libm_expf.bin``:
+the float inputs on which this host's libm ``expf`` differs from the correctly
+rounded exponential, with libm's results (the reference-order decode uses them
+to return the CPU's bits).
 """
 from __future__ import annotations
 
@@ -16,6 +20,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 LIB = os.path.join(HERE, "libpokit_hip.so")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+EXPF_TABLE = os.path.join(HERE, "libm_expf.bin")
 
 # -ffp-contract=off: every fused multiply-add is written out (fmaf), so the
 # bit-exact router recurrence and the reference's unfused orders stay intact.
@@ -40,9 +45,27 @@ def _compile(src: str, obj_dir: str) -> str:
     return obj
 
 
+def build_expf_table(obj_dir: str) -> str:
+    """Compile the libm expf scan with gcc and write EXPF_TABLE (about 8 s on
+    8 cores: every finite float is evaluated once)."""
+    exe = os.path.join(obj_dir, "expf_table")
+    src = os.path.join(HERE, "host", "expf_table.c")
+    r = subprocess.run(["gcc", "-O2", "-pthread", src, "-o", exe, "-lm"], capture_output=True,
+                       text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"gcc failed for {src}:\n{r.stderr[-4000:]}")
+    tmp = EXPF_TABLE + ".tmp"
+    r = subprocess.run([exe, tmp], capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"expf_table failed:\n{r.stderr[-4000:]}")
+    os.replace(tmp, EXPF_TABLE)
+    return EXPF_TABLE
+
+
 def build(verbose: bool = False) -> str:
     obj_dir = os.path.join(HERE, "_build")
     os.makedirs(obj_dir, exist_ok=True)
+    build_expf_table(obj_dir)
     srcs = sources()
     with cf.ThreadPoolExecutor(max_workers=min(8, len(srcs))) as ex:
         objs = list(ex.map(lambda s: _compile(s, obj_dir), srcs))

@@ -531,6 +531,39 @@ pk_hip_status pk_hip_matvec(pk_hip_ctx* ctx, const pk_hip_weight* w, uint32_t ex
     });
 }
 
+pk_hip_status pk_hip_matvec_reference_order(pk_hip_ctx* ctx, const pk_hip_weight* w,
+                                           uint32_t expert, const float* x, float* y, char* err,
+                                           size_t cap) {
+    return guarded(ctx, err, cap, [&] {
+        require_usable(ctx);
+        if (!w || !x || !y) throw ArgError("weight, input and output are required");
+        std::lock_guard lock(ctx->mutex);
+        if (!pk::ref_matvec_supported(w->type, static_cast<uint32_t>(w->in)))
+            throw Unsupported("matrix type/width not covered by the reference-order kernels");
+        if (w->n_experts && expert >= w->n_experts) throw ArgError("expert index out of range");
+        if (!w->n_experts && expert != UINT32_MAX) throw ArgError("not an expert tensor");
+        ctx->set_device();
+        ctx->x.ensure(w->in);
+        ctx->y.ensure(w->out);
+        check(hipMemcpyAsync(ctx->x.ptr, x, w->in * sizeof(float), hipMemcpyHostToDevice,
+                             ctx->stream),
+              "copy input");
+        pk::RefMatvecArgs a{};
+        a.W = w->dptr + (w->n_experts ? uint64_t(expert) * w->slice_bytes : 0u);
+        a.row_bytes = w->row_bytes;
+        a.rows = static_cast<uint32_t>(w->out);
+        a.in = static_cast<uint32_t>(w->in);
+        a.x = ctx->x.ptr;
+        a.y = ctx->y.ptr;
+        launch_checked(pk::launch_ref_matvec(w->type, a, 1, ctx->stream), "reference matvec");
+        check(hipMemcpyAsync(y, ctx->y.ptr, w->out * sizeof(float), hipMemcpyDeviceToHost,
+                             ctx->stream),
+              "copy output");
+        check(hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
+        ++ctx->stats.matvec_calls;
+    });
+}
+
 pk_hip_status pk_hip_matvec_async(pk_hip_ctx* ctx, const pk_hip_weight* w, uint32_t expert,
                                   const float* dx, uint32_t batch, float* dy, void* stream,
                                   char* err, size_t cap) {
@@ -761,7 +794,8 @@ struct pk_hip_qwen3moe {
     pk::ModelArgs args{};
     std::vector<pk::ModelLayer> layers;
     DeviceBuffer<uint32_t> state, tokens, ids, moe_status;
-    DeviceBuffer<float> work, probs, act, moe_out;
+    DeviceBuffer<float> work, probs, act, moe_out, rope_table, ref_scratch;
+    DeviceBuffer<uint32_t> expf_bucket, expf_pairs;
     DeviceBuffer<double> row_sum, row_bound;
     DeviceBuffer<uint16_t> kv;
     hipGraphExec_t step_logits = nullptr, step_plain = nullptr;
@@ -783,10 +817,12 @@ void require_vector(const pk_hip_weight* w, const char* what, uint64_t n) {
     if (w->type != 0) throw ArgError(std::string("norm weight must be F32: ") + what);
 }
 
-void require_matvec(const pk_hip_weight* w, const char* what, uint64_t in, uint64_t out) {
+void require_matvec(const pk_hip_weight* w, const char* what, uint64_t in, uint64_t out,
+                    bool exact) {
     require_weight(w, what, in, out);
-    if (!pk::matvec_supported(w->type, static_cast<uint32_t>(in), 1))
-        throw Unsupported(std::string("no matvec kernel for weight: ") + what);
+    const bool ok = exact ? pk::ref_matvec_supported(w->type, static_cast<uint32_t>(in))
+                          : pk::matvec_supported(w->type, static_cast<uint32_t>(in), 1);
+    if (!ok) throw Unsupported(std::string("no matvec kernel for weight: ") + what);
 }
 
 hipGraphExec_t capture_step(pk_hip_qwen3moe* m, bool logits) {
@@ -817,6 +853,10 @@ void release_model(pk_hip_qwen3moe* m) {
     m->probs.release();
     m->act.release();
     m->moe_out.release();
+    m->rope_table.release();
+    m->ref_scratch.release();
+    m->expf_bucket.release();
+    m->expf_pairs.release();
     m->row_sum.release();
     m->row_bound.release();
     m->kv.release();
@@ -832,14 +872,16 @@ pk_hip_status pk_hip_qwen3moe_create(pk_hip_ctx* ctx, const pk_hip_qwen3moe_conf
         if (!cfg || !w || !out || !w->layers) throw ArgError("config, weights and output are required");
         const pk_hip_qwen3moe_config& c = *cfg;
         if (c.layers == 0 || c.hidden == 0 || c.heads == 0 || c.kv_heads == 0 || c.head_dim == 0 ||
-            c.vocab == 0 || c.kv_capacity == 0)
+            c.vocab == 0 || c.kv_capacity == 0 || c.context == 0)
             throw ArgError("model dimensions must be non-zero");
+        if (c.kv_capacity > c.context) throw ArgError("KV window exceeds the model context");
         if (c.heads % c.kv_heads) throw ArgError("query heads must be evenly grouped over KV heads");
         if (!(c.rms_eps > 0.0f) || !(c.rope_theta > 0.0f)) throw ArgError("invalid norm epsilon or RoPE base");
         const uint64_t qd = uint64_t(c.heads) * c.head_dim, kd = uint64_t(c.kv_heads) * c.head_dim;
         require_weight(w->token_embd, "token_embd", c.hidden, c.vocab);
         require_vector(w->output_norm, "output_norm", c.hidden);
-        require_matvec(w->output, "output", c.hidden, c.vocab);
+        const bool exact = c.reference_order != 0;
+        require_matvec(w->output, "output", c.hidden, c.vocab, exact);
         std::lock_guard lock(ctx->mutex);
         ctx->set_device();
         auto m = std::make_unique<pk_hip_qwen3moe>();
@@ -859,6 +901,7 @@ pk_hip_status pk_hip_qwen3moe_create(pk_hip_ctx* ctx, const pk_hip_qwen3moe_conf
         a.out_row = w->output->row_bytes;
         a.rms_eps = c.rms_eps;
         a.rope_theta = c.rope_theta;
+        a.exact = exact ? 1u : 0u;
         a.attn_scale = 1.0f / std::sqrt(static_cast<float>(c.head_dim));  // KvCache::attend default
         a.embd = weight_bytes(w->token_embd);
         a.out_norm = reinterpret_cast<const float*>(weight_bytes(w->output_norm));
@@ -896,6 +939,51 @@ pk_hip_status pk_hip_qwen3moe_create(pk_hip_ctx* ctx, const pk_hip_qwen3moe_conf
         m->row_sum.ensure(max_experts);
         m->row_bound.ensure(max_experts);
         m->moe_out.ensure(c.hidden);
+        if (exact) {
+            if (max_experts > pk::kMaxExperts256 || c.top_k > pk::kMaxRefTopK)
+                throw Unsupported("reference-order MoE covers up to 256 experts and top-16");
+            m->ref_scratch.ensure(pk::ref_scratch_floats(c.top_k, max_ffn, c.hidden));
+            a.ref_scratch = m->ref_scratch.ptr;
+            // prepare_qwen_rope (src/qwen3_moe_runner.cpp:141-155) with this host's libm,
+            // for every position of the model context
+            const uint32_t half = c.head_dim / 2;
+            std::vector<float> table(uint64_t(c.context) * c.head_dim);
+            for (uint32_t pos = 0; pos < c.context; ++pos) {
+                float* row = table.data() + uint64_t(pos) * c.head_dim;
+                for (uint32_t p = 0; p < half; ++p) {
+                    const float angle = static_cast<float>(pos) *
+                        std::pow(c.rope_theta, -static_cast<float>(p) / static_cast<float>(half));
+                    row[p] = std::cos(angle);
+                    row[half + p] = std::sin(angle);
+                }
+            }
+            m->rope_table.ensure(table.size());
+            check(hipMemcpy(m->rope_table.ptr, table.data(), table.size() * sizeof(float),
+                            hipMemcpyHostToDevice),
+                  "copy RoPE table");
+            a.rope_table = m->rope_table.ptr;
+            if (c.libm_expf_count) {
+                if (!c.libm_expf_pairs || c.libm_expf_count > (1ull << 31))
+                    throw ArgError("libm_expf_pairs: missing or oversized table");
+                const uint32_t* p = c.libm_expf_pairs;
+                std::vector<uint32_t> bucket(65537, 0);
+                for (uint64_t i = 0; i < c.libm_expf_count; ++i) {
+                    if (i && p[2 * i] <= p[2 * i - 2])
+                        throw ArgError("libm_expf_pairs: inputs not increasing");
+                    ++bucket[(p[2 * i] >> 16) + 1];
+                }
+                for (uint32_t t = 0; t < 65536; ++t) bucket[t + 1] += bucket[t];
+                m->expf_bucket.ensure(bucket.size());
+                m->expf_pairs.ensure(2 * c.libm_expf_count);
+                check(hipMemcpy(m->expf_bucket.ptr, bucket.data(), bucket.size() * 4,
+                                hipMemcpyHostToDevice),
+                      "copy expf buckets");
+                check(hipMemcpy(m->expf_pairs.ptr, p, 8 * c.libm_expf_count, hipMemcpyHostToDevice),
+                      "copy expf pairs");
+                a.expf_bucket = m->expf_bucket.ptr;
+                a.expf_pairs = m->expf_pairs.ptr;
+            }
+        }
         check(hipMemsetAsync(m->moe_status.ptr, 0, 4 * sizeof(uint32_t), ctx->stream), "clear status");
         m->layers.resize(c.layers);
         for (uint32_t l = 0; l < c.layers; ++l) {
@@ -905,10 +993,10 @@ pk_hip_status pk_hip_qwen3moe_create(pk_hip_ctx* ctx, const pk_hip_qwen3moe_conf
             require_vector(L.q_norm, "attn_q_norm", c.head_dim);
             require_vector(L.k_norm, "attn_k_norm", c.head_dim);
             require_vector(L.ffn_norm, "ffn_norm", c.hidden);
-            require_matvec(L.q, "attn_q", c.hidden, qd);
-            require_matvec(L.k, "attn_k", c.hidden, kd);
-            require_matvec(L.v, "attn_v", c.hidden, kd);
-            require_matvec(L.o, "attn_output", qd, c.hidden);
+            require_matvec(L.q, "attn_q", c.hidden, qd, exact);
+            require_matvec(L.k, "attn_k", c.hidden, kd, exact);
+            require_matvec(L.v, "attn_v", c.hidden, kd, exact);
+            require_matvec(L.o, "attn_output", qd, c.hidden, exact);
             if (L.k->type != L.q->type || L.v->type != L.q->type || L.o->type != L.q->type)
                 throw Unsupported("attention weights must share one format");
             const pk_hip_moe_layer ml{L.router, L.gate, L.up, L.down, c.top_k, c.normalize, 1.0f};
@@ -987,6 +1075,8 @@ pk_hip_status pk_hip_qwen3moe_generate(pk_hip_qwen3moe* m, const uint32_t* promp
         const pk::ModelArgs& a = m->args;
         for (uint32_t i = 0; i < n_prompt; ++i)
             if (prompt[i] >= a.vocab) throw ArgError("token id exceeds model vocabulary");
+        if (uint64_t(n_prompt) + n_new > m->cfg.context)
+            throw ArgError("prompt and new tokens exceed the model context");
         std::lock_guard lock(ctx->mutex);
         ctx->set_device();
         hipStream_t s = ctx->stream;

@@ -124,6 +124,14 @@ struct ModelArgs {
     float* attn_out;          // [hidden]
     float* rope;              // cos [head_dim / 2], then sin
     float* logits;            // [vocab]
+    // reference-order mode: every kernel repeats the CPU's operation order
+    uint32_t exact;
+    const float* rope_table;  // [positions][head_dim]: cos, then sin (host libm)
+    float* ref_scratch;       // router logits, gate, up, act, expert outputs
+    // libm expf exceptions: pairs [n][2] (input bits, result bits) sorted by
+    // input; bucket[t] .. bucket[t + 1] the pairs whose input's top 16 bits are t
+    const uint32_t* expf_bucket;  // [65537], or null
+    const uint32_t* expf_pairs;
 };
 bool model_supported(const ModelArgs& a);
 // logits: run the final norm, head and argmax (else only advance the position).
@@ -134,6 +142,33 @@ hipError_t launch_model_step(const ModelArgs& a, const ModelLayer* layers, bool 
 // 1 K-quant scale fix-up (block_bytes 144/176), 2 Q6_K, 3 F32 norm, 4 F32 router.
 hipError_t launch_synth_fill(uint8_t* dst, uint64_t nbytes, uint64_t key, uint32_t kind,
                              uint32_t block_bytes, hipStream_t stream);
+
+// Reference-order matvec: y[route][row] = row . x[route] summed as the CPU
+// does (see exact.hip).  ids (optional) selects each route's expert slice.
+constexpr uint32_t kMaxRefWidth = 8192;
+constexpr uint32_t kMaxRefTopK = 16;
+constexpr uint32_t kMaxExperts256 = 256;
+struct RefMatvecArgs {
+    const uint8_t* W;
+    uint64_t row_bytes, slice_bytes;
+    const uint32_t* ids;
+    uint32_t rows, in;
+    const float* x;
+    uint64_t x_stride;
+    float* y;
+    uint64_t y_stride;
+};
+bool ref_matvec_supported(uint32_t type, uint32_t in);
+hipError_t launch_ref_matvec(uint32_t type, const RefMatvecArgs& a, uint32_t routes,
+                             hipStream_t stream);
+hipError_t launch_ref_rmsnorm(float* x, const float* delta, const float* w, float* out, uint32_t n,
+                              uint32_t rows, float eps, hipStream_t stream);
+hipError_t launch_ref_layer_attention(const ModelArgs& a, const ModelLayer& L, hipStream_t stream);
+hipError_t launch_ref_moe(const ModelArgs& a, const ModelLayer& L, hipStream_t stream);
+// floats of ModelArgs::ref_scratch for one layer shape
+inline uint64_t ref_scratch_floats(uint32_t top_k, uint32_t ffn, uint32_t hidden) {
+    return kMaxExperts256 + 3ull * top_k * ffn + static_cast<uint64_t>(top_k) * hidden;
+}
 
 // Individual stages (timing and tests).
 hipError_t launch_moe_router(const MoeDecodeArgs& a, hipStream_t stream);

@@ -4,6 +4,11 @@
 qwen3_moe_runner.hpp:57-110) for the greedy path: every tensor resident in
 HBM (no expert cache), every layer of a token step on the GPU, one captured
 HIP graph replayed per token (pk_hip_qwen3moe_* in include/pokit_hip.h).
+``reference_order`` (default) runs the kernels that repeat the CPU's
+operation order, so greedy tokens follow the reference through near-ties;
+False selects the bandwidth-optimised kernels.  Reference order also needs
+the host libm's expf exceptions (``libm_expf.bin``, written at build time by
+host/expf_table.c), so the device's float exponentials return glibc's bits.
 
 Two ways to build one:
 * ``from_gguf(backend, path)``: a GGUF v3 qwen3moe file, tensor names and
@@ -17,6 +22,7 @@ Two ways to build one:
 from __future__ import annotations
 
 import ctypes
+import os
 
 import numpy as np
 
@@ -33,6 +39,27 @@ _LAYER_TENSORS = ("attn_norm", "attn_q", "attn_q_norm", "attn_k", "attn_k_norm",
                   "ffn_down_exps")
 
 
+_EXPF_TABLE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libm_expf.bin")
+_expf_pairs: np.ndarray | None = None
+
+
+def libm_expf_pairs() -> np.ndarray:
+    """uint32 [n, 2] (input bits, libm expf bits), increasing inputs: the
+    floats on which the host libm's expf is not the correctly rounded value."""
+    global _expf_pairs
+    if _expf_pairs is None:
+        if not os.path.exists(_EXPF_TABLE):
+            raise ImportError(f"{_EXPF_TABLE} missing: run pokitlms_amd.build first")
+        raw = np.fromfile(_EXPF_TABLE, dtype=np.uint8)
+        if raw.size < 12 or bytes(raw[:8]) != b"PKEXPF01":
+            raise ValueError(f"{_EXPF_TABLE}: not an expf exception table")
+        n = int(raw[8:12].view(np.uint32)[0])
+        if raw.size != 12 + 8 * n:
+            raise ValueError(f"{_EXPF_TABLE}: truncated")
+        _expf_pairs = raw[12:].view(np.uint32).reshape(n, 2)
+    return _expf_pairs
+
+
 def _upload_args(dims: list[int]) -> tuple[int, int, int]:
     """(in, out, n_experts) of a GGUF tensor for pk_hip_upload."""
     if len(dims) == 1:
@@ -43,12 +70,20 @@ def _upload_args(dims: list[int]) -> tuple[int, int, int]:
 
 
 class Qwen3MoeModel:
-    def __init__(self, backend: HipBackend, shape: SM.Qwen3MoeShape, weights: dict[str, Weight]):
+    def __init__(self, backend: HipBackend, shape: SM.Qwen3MoeShape, weights: dict[str, Weight],
+                 reference_order: bool = True):
         self.backend, self.shape, self.weights = backend, shape, weights
+        self.reference_order = reference_order
         m = shape
+        # the runner's default KV window: min(context, 512) (src/qwen3_moe_runner.cpp:372-376)
         cfg = _abi.Qwen3MoeConfig(m.layers, m.hidden, m.heads, m.kv_heads, m.head_dim, m.experts,
-                                  m.top_k, m.ffn, m.vocab, min(m.context, 512),
-                                  1 if m.normalize else 0, m.rms_eps, m.rope_theta)
+                                  m.top_k, m.ffn, m.vocab, min(m.context, 512), m.context,
+                                  1 if m.normalize else 0, 1 if reference_order else 0,
+                                  m.rms_eps, m.rope_theta)
+        if reference_order:
+            pairs = libm_expf_pairs()
+            cfg.libm_expf_pairs = pairs.ctypes.data
+            cfg.libm_expf_count = pairs.shape[0]
         layers = (_abi.Qwen3MoeLayer * m.layers)()
         for l in range(m.layers):
             for field, name in zip(_LAYER_FIELDS, _LAYER_TENSORS):
@@ -65,7 +100,8 @@ class Qwen3MoeModel:
 
     # ---- construction ---------------------------------------------------------------
     @classmethod
-    def synthetic(cls, backend: HipBackend, shape: SM.Qwen3MoeShape, seed: int) -> "Qwen3MoeModel":
+    def synthetic(cls, backend: HipBackend, shape: SM.Qwen3MoeShape, seed: int,
+                  reference_order: bool = True) -> "Qwen3MoeModel":
         weights = {}
         L = _abi.lib()
         try:
@@ -78,14 +114,15 @@ class Qwen3MoeModel:
                                              _ERRBUF), err)
                 weights[name] = Weight(backend, h.value, gtype, inn, out, ne,
                                        gguf.payload_bytes(gtype, dims))
-            return cls(backend, shape, weights)
+            return cls(backend, shape, weights, reference_order)
         except BaseException:
             for w in weights.values():
                 w.release()
             raise
 
     @classmethod
-    def from_gguf(cls, backend: HipBackend, path: str) -> "Qwen3MoeModel":
+    def from_gguf(cls, backend: HipBackend, path: str,
+                  reference_order: bool = True) -> "Qwen3MoeModel":
         with gguf.GgufFile(path) as f:
             md = f.metadata
             if md.get("general.architecture") != "qwen3moe":
@@ -117,7 +154,7 @@ class Qwen3MoeModel:
                     t = f.tensors["token_embd.weight"]
                     weights["output.weight"] = backend.upload(t.gtype, t.dims[0], t.dims[1],
                                                               f.payload("token_embd.weight"))
-                return cls(backend, shape, weights)
+                return cls(backend, shape, weights, reference_order)
             except BaseException:
                 for w in weights.values():
                     w.release()

@@ -66,16 +66,34 @@ def test_device_generator_matches_numpy(hip):
 
 
 def test_small_model_matches_reference(hip, mg):
+    """Reference order: every greedy token matches, and the logits after the
+    prompt are the CPU's bits (serial sums in the reference's order, the host
+    libm's expf and RoPE tables)."""
     from pokitlms_amd.model import Qwen3MoeModel
     m = SM.Qwen3MoeShape(layers=int(mg["small_layers"]))
     with Qwen3MoeModel.synthetic(hip, m, int(mg["small_seed"])) as model:
         tokens, logits, stats = model.generate(mg["small_prompt"], len(mg["small_tokens"]),
                                                want_logits=True)
     err = normwise_rel(logits, mg["small_logits"])
-    say("small model: logits normwise", err, "tokens", tokens[:8], "stats", stats)
-    assert err <= 1e-4
-    assert np.argmax(logits) == np.argmax(mg["small_logits"])
+    same_bits = int(np.sum(logits.view(np.uint32) == mg["small_logits"].view(np.uint32)))
+    say("small model: logits normwise", err, "bit-equal", same_bits, "of", logits.size,
+        "tokens", tokens[:8], "stats", stats)
+    assert same_bits == logits.size, err
     assert np.array_equal(tokens, mg["small_tokens"])
+
+
+def test_small_model_fast_kernels_within_tolerance(hip, mg):
+    """The bandwidth-optimised kernels: the prompt's logits within 1e-3
+    normwise of the CPU's (reassociation noise, amplified by FP16 KV
+    rounding) and the first greedy token equal."""
+    from pokitlms_amd.model import Qwen3MoeModel
+    m = SM.Qwen3MoeShape(layers=int(mg["small_layers"]))
+    with Qwen3MoeModel.synthetic(hip, m, int(mg["small_seed"]), reference_order=False) as model:
+        tokens, logits, _ = model.generate(mg["small_prompt"], 4, want_logits=True)
+    err = normwise_rel(logits, mg["small_logits"])
+    say("small model, fast kernels: logits normwise", err)
+    assert err <= 1e-3
+    assert tokens[0] == mg["small_tokens"][0]
 
 
 def test_full_model_greedy_tokens_match_reference(hip, mg):

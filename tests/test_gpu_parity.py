@@ -99,6 +99,36 @@ def test_c2_sweep(hip, port, golden, gtype, shape):
     wt.release()
 
 
+@pytest.mark.parametrize("gtype", QUANT)
+@pytest.mark.parametrize("shape", G.C2_SHAPES)
+def test_reference_order_matvec_bit_exact(hip, golden, gtype, shape):
+    """pk_hip_matvec_reference_order returns the reference's bits (the golden
+    vectors come from the compiled reference itself)."""
+    rows, inn = shape
+    w, xs = G.c2_inputs(gtype, rows, inn)
+    key = f"c2_{S.TYPE_NAMES[gtype]}_{rows}x{inn}"
+    wt = hip.upload(gtype, inn, rows, w)
+    y = hip.matvec_reference_order(wt, xs[0])
+    same = int(np.sum(bits(y) == bits(golden[key + "_y0"])))
+    say("reference order", S.TYPE_NAMES[gtype], shape, "bit-equal", same, "of", rows)
+    assert same == rows
+    wt.release()
+
+
+def test_reference_order_router_and_c1(hip, port, golden):
+    w, x = G.c1_inputs()
+    wt = hip.upload(S.Q4_K, 4096, 4096, w)
+    assert np.array_equal(bits(hip.matvec_reference_order(wt, x)), bits(golden["c1_y"]))
+    wt.release()
+    g = S.rng(71)
+    router = S.normal_f32(g, 128 * 2048, 0.02).reshape(128, 2048)
+    xr = S.normal_f32(g, 2048)
+    rt = hip.upload(S.F32, 2048, 128, router)
+    cpu = port.linear(S.F32, router.view(np.uint8), 2048, 128, xr)
+    assert np.array_equal(bits(hip.matvec_reference_order(rt, xr)), bits(cpu))
+    rt.release()
+
+
 @pytest.mark.parametrize("batch", (2, 3, 5, 6, 7))
 def test_odd_batches(hip, port, batch):
     g = S.rng(40 + batch)
