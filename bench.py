@@ -49,6 +49,7 @@ def parse():
     ap.add_argument("--eager", action="store_true", help="time eager launches instead of graphs")
     ap.add_argument("--no-prefill", action="store_true", help="skip the batched-prefill leg")
     ap.add_argument("--prefill-reps", type=int, default=40)
+    ap.add_argument("--no-decode", action="store_true", help="skip the whole-model decode leg")
     ap.add_argument("--calibrate-copy-mib", type=int, default=0,
                     help="first run a plain device copy of this many MiB three times "
                          "(the known-size kernel that scales rocprofv3 FETCH/WRITE_SIZE)")
@@ -202,6 +203,108 @@ def prefill_leg(torch, hip, layers, stream, reps: int, cpu_ms_per_token):
                                          "single-token pass time of the decode baseline"}
         out["speedup_vs_cpu"] = round(out["tokens_per_s"] / cpu_tps, 1)
     r.release()
+    return out
+
+
+def decode_weight_bytes(shape) -> int:
+    """Algorithmic weight bytes of one decode forward: every dense tensor,
+    top_k of the n_experts slices of each expert tensor, one embedding row."""
+    from pokitlms_amd import gguf
+    from pokitlms_amd import synth_model as SM
+    total = 0
+    for name, dims, gtype, _ in SM.tensor_list(shape):
+        nbytes = gguf.payload_bytes(gtype, dims)
+        if name == "token_embd.weight":
+            total += nbytes // dims[1]
+        elif "_exps." in name:
+            total += nbytes // shape.experts * shape.top_k
+        else:
+            total += nbytes
+    return total
+
+
+def decode_cpu_baseline(prompt_len: int = 32, forwards: int = 20):
+    """The reference Qwen3MoeRunner (oracle/_ref) on models of the config-5
+    shape with 1 and 4 layers (GGUF files in /dev/shm, all experts cached after
+    the prompt), steady-state seconds per forward extrapolated linearly to 48
+    layers: t(L) = head + L * layer."""
+    import numpy as np
+
+    import oracle
+    from pokitlms_amd import synth_model as SM
+    if not oracle.available("reference"):
+        return None
+    cpu = oracle.Oracle("reference")
+    d = "/dev/shm" if os.path.isdir("/dev/shm") else "/tmp"
+    med = {}
+    for L in (1, 4):
+        m = SM.Qwen3MoeShape(layers=L)
+        path = os.path.join(d, f"pk_bench_decode_{os.getpid()}_{L}.gguf")
+        try:
+            SM.write_gguf(path, m, 1234)
+            secs = cpu.qwen3moe_forward_times(path, SM.prompt_tokens(1234, prompt_len, m.vocab),
+                                              forwards)
+        finally:
+            if os.path.exists(path):
+                os.remove(path)
+        med[L] = float(np.median(secs[forwards // 3:]))
+    layer = (med[4] - med[1]) / 3.0
+    head = med[1] - layer
+    per_forward = head + 48 * layer
+    workers = cpu.lib.pkref_row_workers()
+    return {"value": round(1.0 / per_forward, 4), "unit": "tokens/s", "cores": int(workers),
+            "kind": "reference", "s_per_forward": round(per_forward, 4),
+            "s_per_layer": round(layer, 5), "s_head": round(head, 5),
+            "sample": f"reference runner on 1- and 4-layer models of the config-5 shape "
+                      f"({prompt_len}-token prompt, median of the last {forwards - forwards // 3} "
+                      f"of {forwards} greedy forwards each), extrapolated to 48 layers; "
+                      f"row pool of {workers} workers; host nproc {os.cpu_count()}"}
+
+
+def decode_leg(torch, hip, with_cpu: bool):
+    """Whole-model greedy decode: the seeded 48-layer
+    30B-A3B-shape model generated in HBM, the golden 128-token prompt, 256
+    greedy tokens.  Reference-order kernels (token parity with the CPU
+    runner's golden tokens) and the bandwidth-optimised kernels."""
+    import numpy as np
+
+    from pokitlms_amd import synth_model as SM
+    from pokitlms_amd.model import Qwen3MoeModel
+    with np.load(os.path.join(ROOT, "tests", "golden", "model_golden.npz"),
+                 allow_pickle=False) as z:
+        seed, prompt, golden = int(z["full_seed"]), z["full_prompt"], z["full_tokens"]
+        ref_decode_s = float(z["full_decode_seconds"]) if "full_decode_seconds" in z.files else None
+    shape = SM.Qwen3MoeShape()
+    n_new = len(golden)
+    out = {"workload": "seeded 48-layer Qwen3-MoE 30B-A3B-shape model in HBM (Q4_K attention "
+                       "and experts, Q6_K down and output head, F32 router/norms), 128-token "
+                       "prompt, 256 greedy tokens",
+           "weight_bytes_per_forward": decode_weight_bytes(shape)}
+    for mode, ref in (("reference_order", True), ("fast", False)):
+        with Qwen3MoeModel.synthetic(hip, shape, seed, reference_order=ref) as model:
+            model.generate(prompt[:8], 4)  # warm-up: graph capture, first-touch
+            tokens, _, st = model.generate(prompt, n_new)
+        dec_s = st["decode_ns"] / 1e9
+        same = tokens == golden
+        first_diff = -1 if same.all() else int(np.argmin(same))
+        fwd_s = dec_s / st["decode_forwards"]
+        out[mode] = {"forwards_per_s": round(st["decode_forwards"] / dec_s, 2),
+                     "generated_tokens_per_s": round(n_new / dec_s, 2),
+                     "ms_per_forward": round(fwd_s * 1e3, 3),
+                     "prefill_ms": round(st["prefill_ns"] / 1e6, 1),
+                     "weight_gbs": round(out["weight_bytes_per_forward"] / fwd_s / 1e9, 1),
+                     "tokens_equal_golden": bool(same.all()), "first_mismatch": first_diff}
+        log(f"decode {mode}: {fwd_s * 1e3:.3f} ms/forward, first mismatch {first_diff}")
+    out["token_parity"] = out["reference_order"]["tokens_equal_golden"]
+    if ref_decode_s:
+        out["golden_cpu_s_per_forward"] = round(ref_decode_s / (n_new - 1), 4)
+    if with_cpu:
+        log("decode cpu baseline ...")
+        cpu = decode_cpu_baseline()
+        out["cpu_baseline"] = cpu
+        if cpu:
+            for mode in ("reference_order", "fast"):
+                out[mode]["speedup_vs_cpu"] = round(out[mode]["forwards_per_s"] / cpu["value"], 1)
     return out
 
 
@@ -403,6 +506,14 @@ def main():
         prefill = prefill_leg(torch, hip, layers[:4], stream, args.prefill_reps,
                               cpu["ms_per_token"] if cpu else None)
 
+    decode = None
+    if not args.no_decode:
+        log("whole-model decode leg ...")
+        for l in layers:
+            l.release()
+        layers = []
+        decode = decode_leg(torch, hip, not args.no_cpu)
+
     out = {
         "metric": METRIC,
         "value": round(value, 1),
@@ -436,6 +547,7 @@ def main():
         "parity": parity,
         "cpu_baseline": cpu,
         "prefill": prefill,
+        "decode": decode,
     }
     if cpu:
         out["speedup_vs_cpu"] = round(value / cpu["value"], 1)

@@ -99,6 +99,9 @@ class Oracle:
             L.pkref_qwen3moe_greedy.argtypes = [ctypes.c_char_p, _u32p, ctypes.c_uint32,
                                                 ctypes.c_uint32, ctypes.c_uint64, _u32p, _f32p,
                                                 ctypes.POINTER(ctypes.c_double)]
+            L.pkref_qwen3moe_forward_times.argtypes = [
+                ctypes.c_char_p, _u32p, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint64,
+                ctypes.POINTER(ctypes.c_double)]
 
     # ---- single ops -------------------------------------------------------
     def half_to_float(self, bits: int) -> float:
@@ -173,6 +176,21 @@ class Oracle:
         if rc:
             raise OracleError(rc, "pkref_qwen3moe_greedy")
         return out[:n_new], logits, secs.value
+
+    def qwen3moe_forward_times(self, path: str, prompt: np.ndarray, n_forwards: int,
+                               expert_cache_bytes: int = 1 << 40) -> np.ndarray:
+        """Wall seconds of each of n_forwards greedy decode forwards of the
+        reference runner after the prompt (reference library only)."""
+        if self.kind != "reference":
+            raise OracleError(1, "qwen3moe_forward_times needs the compiled reference")
+        p = np.ascontiguousarray(prompt, np.uint32)
+        secs = np.zeros(n_forwards, np.float64)
+        rc = self.lib.pkref_qwen3moe_forward_times(
+            path.encode(), p.ctypes.data_as(_u32p), p.size, n_forwards, expert_cache_bytes,
+            secs.ctypes.data_as(ctypes.POINTER(ctypes.c_double)))
+        if rc:
+            raise OracleError(rc, "pkref_qwen3moe_forward_times")
+        return secs
 
     def moe(self, layer) -> "MoeBlock":
         return MoeBlock(self, layer)

@@ -13,6 +13,8 @@
 #include "pokitlms/model/tensor_reader.hpp"
 #include "pokitlms/ops/quantized_linear.hpp"
 
+#include <algorithm>
+#include <chrono>
 #include <cmath>
 #include <cstdint>
 #include <cstring>
@@ -230,6 +232,33 @@ int pkref_qwen3moe_greedy(const char* path, const std::uint32_t* prompt, std::ui
         if (decode_seconds) {
             *decode_seconds = std::chrono::duration<double>(std::chrono::steady_clock::now() - start)
                                   .count();
+        }
+        return 0;
+    } catch (...) {
+        return status_of_current_exception();
+    }
+}
+
+// Steady-state decode cost of the reference runner: feeds the prompt, then
+// n_forwards greedy forwards, writing each forward's wall seconds (argmax
+// included, as the runner's generate loop pays it).
+int pkref_qwen3moe_forward_times(const char* path, const std::uint32_t* prompt,
+                                 std::uint32_t n_prompt, std::uint32_t n_forwards,
+                                 std::uint64_t expert_cache_bytes, double* seconds) {
+    try {
+        if (!path || !prompt || n_prompt == 0 || !seconds) {
+            throw std::invalid_argument("path, prompt and output are required");
+        }
+        pokitlms::model::Qwen3MoeRunner runner(path, static_cast<std::size_t>(expert_cache_bytes));
+        std::vector<float> logits;
+        for (std::uint32_t i = 0; i < n_prompt; ++i) logits = runner.forward_token(prompt[i], i);
+        for (std::uint32_t j = 0; j < n_forwards; ++j) {
+            const auto start = std::chrono::steady_clock::now();
+            const auto best = static_cast<std::uint32_t>(
+                std::max_element(logits.begin(), logits.end()) - logits.begin());
+            logits = runner.forward_token(best, n_prompt + j);
+            seconds[j] = std::chrono::duration<double>(std::chrono::steady_clock::now() - start)
+                             .count();
         }
         return 0;
     } catch (...) {

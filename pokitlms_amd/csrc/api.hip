@@ -788,6 +788,43 @@ pk_hip_status pk_hip_sync(pk_hip_ctx* ctx, void* stream, char* err, size_t cap) 
 // ---------------------------------------------------------------------------
 // Whole-model greedy decode (Qwen3MoeRunner on the device).
 
+// Two-choice cuckoo table of (input bits, libm result bits) for the device's
+// expf_libm: each half holds 1 << bits slots, at most a third of all slots
+// used; the hash multipliers are the first pair from a fixed list with which
+// every insertion settles (deterministic for a given table).
+pk::LibmExpf build_expf_cuckoo(const uint32_t* pairs, uint64_t n, std::vector<uint32_t>& slots) {
+    static const uint32_t kMul[] = {0x9E3779B1u, 0x85EBCA77u, 0xC2B2AE3Du, 0x27D4EB2Fu,
+                                    0x165667B1u, 0xD3A2646Du, 0xFD7046C5u, 0xB55A4F09u};
+    uint32_t bits = 4;
+    while ((2ull << bits) < 3 * n) ++bits;
+    const uint64_t half = 1ull << bits;
+    for (uint32_t t0 = 0; t0 < 8; ++t0) {
+        for (uint32_t t1 = 0; t1 < 8; ++t1) {
+            if (t0 == t1) continue;
+            const uint32_t mul[2] = {kMul[t0], kMul[t1]};
+            slots.assign(4 * half, pk::kExpfEmpty);
+            bool ok = true;
+            for (uint64_t i = 0; i < n && ok; ++i) {
+                uint32_t key = pairs[2 * i], val = pairs[2 * i + 1];
+                uint32_t side = 0;
+                ok = false;
+                for (int step = 0; step < 512; ++step) {
+                    const uint64_t at = 2 * (side * half + ((key * mul[side]) >> (32 - bits)));
+                    std::swap(key, slots[at]);
+                    std::swap(val, slots[at + 1]);
+                    if (key == pk::kExpfEmpty) {
+                        ok = true;
+                        break;
+                    }
+                    side ^= 1u;
+                }
+            }
+            if (ok) return pk::LibmExpf{nullptr, bits, mul[0], mul[1]};
+        }
+    }
+    throw Unsupported("libm_expf_pairs: no cuckoo placement found");
+}
+
 struct pk_hip_qwen3moe {
     pk_hip_ctx* ctx = nullptr;
     pk_hip_qwen3moe_config cfg{};
@@ -795,7 +832,7 @@ struct pk_hip_qwen3moe {
     std::vector<pk::ModelLayer> layers;
     DeviceBuffer<uint32_t> state, tokens, ids, moe_status;
     DeviceBuffer<float> work, probs, act, moe_out, rope_table, ref_scratch;
-    DeviceBuffer<uint32_t> expf_bucket, expf_pairs;
+    DeviceBuffer<uint32_t> expf_slots;
     DeviceBuffer<double> row_sum, row_bound;
     DeviceBuffer<uint16_t> kv;
     hipGraphExec_t step_logits = nullptr, step_plain = nullptr;
@@ -855,8 +892,7 @@ void release_model(pk_hip_qwen3moe* m) {
     m->moe_out.release();
     m->rope_table.release();
     m->ref_scratch.release();
-    m->expf_bucket.release();
-    m->expf_pairs.release();
+    m->expf_slots.release();
     m->row_sum.release();
     m->row_bound.release();
     m->kv.release();
@@ -942,6 +978,8 @@ pk_hip_status pk_hip_qwen3moe_create(pk_hip_ctx* ctx, const pk_hip_qwen3moe_conf
         if (exact) {
             if (max_experts > pk::kMaxExperts256 || c.top_k > pk::kMaxRefTopK)
                 throw Unsupported("reference-order MoE covers up to 256 experts and top-16");
+            if (!pk::ref_attention_supported(c.head_dim, c.kv_capacity) || c.hidden > pk::kMaxRefWidth)
+                throw Unsupported("reference-order attention covers head_dim 64/128/256");
             m->ref_scratch.ensure(pk::ref_scratch_floats(c.top_k, max_ffn, c.hidden));
             a.ref_scratch = m->ref_scratch.ptr;
             // prepare_qwen_rope (src/qwen3_moe_runner.cpp:141-155) with this host's libm,
@@ -963,25 +1001,20 @@ pk_hip_status pk_hip_qwen3moe_create(pk_hip_ctx* ctx, const pk_hip_qwen3moe_conf
                   "copy RoPE table");
             a.rope_table = m->rope_table.ptr;
             if (c.libm_expf_count) {
-                if (!c.libm_expf_pairs || c.libm_expf_count > (1ull << 31))
+                if (!c.libm_expf_pairs || c.libm_expf_count > (1ull << 24))
                     throw ArgError("libm_expf_pairs: missing or oversized table");
                 const uint32_t* p = c.libm_expf_pairs;
-                std::vector<uint32_t> bucket(65537, 0);
                 for (uint64_t i = 0; i < c.libm_expf_count; ++i) {
-                    if (i && p[2 * i] <= p[2 * i - 2])
+                    if (p[2 * i] == pk::kExpfEmpty || (i && p[2 * i] <= p[2 * i - 2]))
                         throw ArgError("libm_expf_pairs: inputs not increasing");
-                    ++bucket[(p[2 * i] >> 16) + 1];
                 }
-                for (uint32_t t = 0; t < 65536; ++t) bucket[t + 1] += bucket[t];
-                m->expf_bucket.ensure(bucket.size());
-                m->expf_pairs.ensure(2 * c.libm_expf_count);
-                check(hipMemcpy(m->expf_bucket.ptr, bucket.data(), bucket.size() * 4,
+                std::vector<uint32_t> slots;
+                a.expf = build_expf_cuckoo(p, c.libm_expf_count, slots);
+                m->expf_slots.ensure(slots.size());
+                check(hipMemcpy(m->expf_slots.ptr, slots.data(), slots.size() * 4,
                                 hipMemcpyHostToDevice),
-                      "copy expf buckets");
-                check(hipMemcpy(m->expf_pairs.ptr, p, 8 * c.libm_expf_count, hipMemcpyHostToDevice),
-                      "copy expf pairs");
-                a.expf_bucket = m->expf_bucket.ptr;
-                a.expf_pairs = m->expf_pairs.ptr;
+                      "copy expf table");
+                a.expf.slots = m->expf_slots.ptr;
             }
         }
         check(hipMemsetAsync(m->moe_status.ptr, 0, 4 * sizeof(uint32_t), ctx->stream), "clear status");

@@ -27,24 +27,20 @@
 namespace pk {
 namespace {
 
-// bucket[t] .. bucket[t + 1]: the pairs whose input's top 16 bits are t
-// (at most a few hundred per bucket for glibc), binary-searched.
-__device__ float expf_libm(float x, const uint32_t* bucket, const uint32_t* pairs) {
+// Two independent loads (one slot in each half of the cuckoo table), so the
+// exception costs one memory round trip whether or not the input has one.
+__device__ float expf_libm(float x, const LibmExpf& t) {
     float r = static_cast<float>(exp(static_cast<double>(x)));
-    if (bucket) {
+    if (t.slots) {
         const uint32_t b = __float_as_uint(x);
-        uint32_t lo = bucket[b >> 16], hi = bucket[(b >> 16) + 1u];
-        while (lo < hi) {
-            const uint32_t mid = (lo + hi) >> 1;
-            if (pairs[2u * mid] < b) lo = mid + 1u;
-            else hi = mid;
-        }
-        if (lo < bucket[(b >> 16) + 1u] && pairs[2u * lo] == b) r = __uint_as_float(pairs[2u * lo + 1u]);
+        const uint32_t i0 = (b * t.mul0) >> (32u - t.bits), i1 = (b * t.mul1) >> (32u - t.bits);
+        const uint2 e0 = reinterpret_cast<const uint2*>(t.slots)[i0];
+        const uint2 e1 = reinterpret_cast<const uint2*>(t.slots)[(1u << t.bits) + i1];
+        if (e0.x == b) r = __uint_as_float(e0.y);
+        if (e1.x == b) r = __uint_as_float(e1.y);
     }
     return r;
 }
-
-__device__ __forceinline__ uint32_t u16_at(const uint8_t* p) { return p[0] | (p[1] << 8); }
 
 // Reference-decoded weight i (0..255) of one K-quant block, or of a 32-block.
 template <int T>
@@ -71,125 +67,329 @@ struct RefBlock<T_Q4_0> {
     static constexpr uint32_t BE = 32, BB = 18;
 };
 
-// dot of one block with x (x in LDS), in element order.  K-quants: the
-// decoded FP32 weight times x; Q8_0/Q4_0: d * dot_i8_f32 (the int8 value
-// times x, then the scale once).
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ float add16(float s, const f32x16 v) {
+    s = __fadd_rn(s, v[0]); s = __fadd_rn(s, v[1]); s = __fadd_rn(s, v[2]); s = __fadd_rn(s, v[3]);
+    s = __fadd_rn(s, v[4]); s = __fadd_rn(s, v[5]); s = __fadd_rn(s, v[6]); s = __fadd_rn(s, v[7]);
+    s = __fadd_rn(s, v[8]); s = __fadd_rn(s, v[9]); s = __fadd_rn(s, v[10]); s = __fadd_rn(s, v[11]);
+    s = __fadd_rn(s, v[12]); s = __fadd_rn(s, v[13]); s = __fadd_rn(s, v[14]);
+    return __fadd_rn(s, v[15]);
+}
+
+// LDS floats an array summed by serial_sum needs beyond n rounded up to 16.
+constexpr uint32_t kChainPad = 32;
+__host__ __device__ constexpr uint32_t chain_floats(uint32_t n) { return (n + 15u) / 16u * 16u + kChainPad; }
+
+// s = ((s + p[0]) + p[1]) + ... + p[n - 1], by the calling lane.  p is in LDS,
+// 64-byte aligned, readable for chain_floats(n) floats: the next 32 values
+// are read while the current 32 are added, so the chain of dependent adds
+// does not wait on LDS latency.
+__device__ float serial_sum(const float* p, uint32_t n, float s) {
+    const f32x16* v = reinterpret_cast<const f32x16*>(p);
+    const uint32_t nb = n / 16u;
+    f32x16 a = v[0], b = v[1];
+    uint32_t k = 0;
+    for (; k + 2u <= nb; k += 2u) {
+        const f32x16 na = v[k + 2u], nb2 = v[k + 3u];
+        s = add16(s, a);
+        s = add16(s, b);
+        a = na;
+        b = nb2;
+    }
+    if (k < nb) s = add16(s, a);
+    for (uint32_t i = 16u * nb; i < n; ++i) s = __fadd_rn(s, p[i]);
+    return s;
+}
+
+// s + ((ds * q) - dm) * x: one element of a K-quant block dot (decode_q4_k /
+// decode_q5_k weight, then dot_f32's rounded product and add).
+__device__ __forceinline__ float kq_step(float s, float ds, float dm, float q, float x) {
+    return __fadd_rn(s, __fmul_rn(__fsub_rn(__fmul_rn(ds, q), dm), x));
+}
+
+// Four elements whose quants are the bytes of v, x the matching float4.
+__device__ __forceinline__ float kq_step4(float s, float ds, float dm, uint32_t v, float4 x) {
+    s = kq_step(s, ds, dm, ub<0>(v), x.x);
+    s = kq_step(s, ds, dm, ub<1>(v), x.y);
+    s = kq_step(s, ds, dm, ub<2>(v), x.z);
+    return kq_step(s, ds, dm, ub<3>(v), x.w);
+}
+
+// Q6_K: s + (dsc * (q - 32)) * x for the four 6-bit quants in the bytes of v.
+__device__ __forceinline__ float q6_step4(float s, float dsc, uint32_t v, float4 x) {
+    s = __fadd_rn(s, __fmul_rn(__fmul_rn(dsc, ub<0>(v) - 32.0f), x.x));
+    s = __fadd_rn(s, __fmul_rn(__fmul_rn(dsc, ub<1>(v) - 32.0f), x.y));
+    s = __fadd_rn(s, __fmul_rn(__fmul_rn(dsc, ub<2>(v) - 32.0f), x.z));
+    return __fadd_rn(s, __fmul_rn(__fmul_rn(dsc, ub<3>(v) - 32.0f), x.w));
+}
+
+// dot of one block with x (x in LDS, 16-byte aligned), in element order.
+// The whole block is loaded into registers first (whole words; the 2-byte
+// aligned formats through v_alignbyte).  K-quants: the decoded FP32 weight
+// times x; Q8_0/Q4_0: d * dot_i8_f32 (the int8 value times x, then the scale
+// once).
 template <int T>
 __device__ float block_dot(const uint8_t* blk, const float* x) {
+    const float4* x4 = reinterpret_cast<const float4*>(x);
     float s = 0.0f;
     if constexpr (T == T_Q4_K || T == T_Q5_K) {
-        uint32_t h[4];
-        for (int i = 0; i < 4; ++i) h[i] = u16_at(blk + 4 * i) | (u16_at(blk + 4 * i + 2) << 16);
-        const float d = half_bits_to_float(h[0] & 0xffffu), dmin = half_bits_to_float(h[0] >> 16);
+        constexpr int NW = T == T_Q4_K ? 36 : 44, QS = T == T_Q4_K ? 4 : 12;
+        uint32_t w[NW];
+        ld_words<NW>(blk, w);
+        const uint32_t h[4] = {w[0], w[1], w[2], w[3]};
+        const float d = half_bits_to_float(w[0] & 0xffffu), dmin = half_bits_to_float(w[0] >> 16);
+#pragma unroll
         for (uint32_t j = 0; j < 8; ++j) {
             float sc, mn;
             kq_scale_min(h, j, sc, mn);
             const float ds = __fmul_rn(d, sc), dm = __fmul_rn(dmin, mn);
-            const uint8_t* qs = blk + (T == T_Q4_K ? 16u : 48u) + 32u * (j / 2u);
-            for (uint32_t i = 0; i < 32; ++i) {
-                uint32_t q = (j & 1u) ? qs[i] >> 4 : qs[i] & 15u;
-                if constexpr (T == T_Q5_K) q += ((blk[16u + i] >> j) & 1u) << 4;
-                const float w = __fsub_rn(__fmul_rn(ds, static_cast<float>(q)), dm);
-                s = __fadd_rn(s, __fmul_rn(w, x[32u * j + i]));
+#pragma unroll
+            for (uint32_t k = 0; k < 8; ++k) {
+                const uint32_t raw = w[QS + 8u * (j / 2u) + k];
+                uint32_t v = (j & 1u) ? (raw >> 4) & 0x0f0f0f0fu : raw & 0x0f0f0f0fu;
+                if constexpr (T == T_Q5_K) v |= ((w[4u + k] >> j) & 0x01010101u) << 4;
+                s = kq_step4(s, ds, dm, v, x4[8u * j + k]);
             }
         }
     } else if constexpr (T == T_Q6_K) {
-        const float d = half_bits_to_float(u16_at(blk + 208));
+        uint32_t w[53];  // ql words 0..31, qh 32..47, scales 48..51, d in 52
+        ld_words_2a<53>(blk, w);
+        const float d = half_bits_to_float(w[52] & 0xffffu);
+#pragma unroll
         for (uint32_t c = 0; c < 8; ++c) {
             const uint32_t half = c / 4u, g = c % 4u;
-            const uint8_t* ql = blk + 64u * half + 32u * (g & 1u);
-            const uint8_t* qh = blk + 128u + 32u * half;
-            for (uint32_t i = 0; i < 32; ++i) {
-                const int sc = static_cast<int8_t>(blk[192u + 8u * half + 2u * g + (i >= 16u ? 1u : 0u)]);
-                const uint32_t nib = g >= 2u ? ql[i] >> 4 : ql[i] & 15u;
-                const int q = static_cast<int>(nib | (((qh[i] >> (2u * g)) & 3u) << 4)) - 32;
-                const float w = __fmul_rn(__fmul_rn(d, static_cast<float>(sc)), static_cast<float>(q));
-                s = __fadd_rn(s, __fmul_rn(w, x[32u * c + i]));
+#pragma unroll
+            for (uint32_t k = 0; k < 8; ++k) {
+                const uint32_t sb = 8u * half + 2u * g + (k >= 4u ? 1u : 0u);
+                const int sc = static_cast<int8_t>(w[48u + sb / 4u] >> (8u * (sb % 4u)));
+                const float dsc = __fmul_rn(d, static_cast<float>(sc));
+                const uint32_t ql = w[16u * half + 8u * (g & 1u) + k];
+                const uint32_t qh = w[32u + 8u * half + k];
+                const uint32_t v = (g >= 2u ? (ql >> 4) & 0x0f0f0f0fu : ql & 0x0f0f0f0fu) |
+                                   (((qh >> (2u * g)) & 0x03030303u) << 4);
+                s = q6_step4(s, dsc, v, x4[8u * c + k]);
             }
         }
     } else if constexpr (T == T_Q8_0) {
-        for (uint32_t i = 0; i < 32; ++i)
-            s = __fadd_rn(s, __fmul_rn(x[i], static_cast<float>(static_cast<int8_t>(blk[2 + i]))));
-        s = __fmul_rn(half_bits_to_float(u16_at(blk)), s);
-    } else {  // Q4_0: low nibbles are elements 0..15, high 16..31
-        for (uint32_t i = 0; i < 32; ++i) {
-            const uint32_t b = blk[2 + (i & 15u)];
-            const int q = static_cast<int>(i < 16u ? (b & 15u) : (b >> 4)) - 8;
-            s = __fadd_rn(s, __fmul_rn(x[i], static_cast<float>(q)));
+        uint32_t w[9];  // d in the low half of word 0, quant i in byte 2 + i
+        ld_words_2a<9>(blk, w);
+#pragma unroll
+        for (uint32_t k = 0; k < 8; ++k) {
+            const float4 xv = x4[k];
+            const float xs[4] = {xv.x, xv.y, xv.z, xv.w};
+#pragma unroll
+            for (uint32_t m = 0; m < 4; ++m) {
+                const uint32_t byte = 2u + 4u * k + m;
+                const int q = static_cast<int8_t>(w[byte / 4u] >> (8u * (byte % 4u)));
+                s = __fadd_rn(s, __fmul_rn(xs[m], static_cast<float>(q)));
+            }
         }
-        s = __fmul_rn(half_bits_to_float(u16_at(blk)), s);
+        s = __fmul_rn(half_bits_to_float(w[0] & 0xffffu), s);
+    } else {  // Q4_0: low nibbles are elements 0..15, high 16..31
+        uint32_t w[5];
+        ld_words_2a<5>(blk, w);
+#pragma unroll
+        for (uint32_t k = 0; k < 8; ++k) {
+            const float4 xv = x4[k];
+            const float xs[4] = {xv.x, xv.y, xv.z, xv.w};
+#pragma unroll
+            for (uint32_t m = 0; m < 4; ++m) {
+                const uint32_t i = 4u * k + m, byte = 2u + (i & 15u);
+                const uint32_t b = (w[byte / 4u] >> (8u * (byte % 4u))) & 0xffu;
+                const int q = static_cast<int>(i < 16u ? (b & 15u) : (b >> 4)) - 8;
+                s = __fadd_rn(s, __fmul_rn(xs[m], static_cast<float>(q)));
+            }
+        }
+        s = __fmul_rn(half_bits_to_float(w[0] & 0xffffu), s);
     }
     return s;
 }
 
 // y[route][row] for rows of W (route: the expert ids[route] slice when ids
-// is set), x[route] staged in LDS.  Lanes (row, block); one lane per row then
-// sums the block dots in block order starting from 0.
+// is set), x[route] staged in LDS -- or, with x_up, the SwiGLU activation
+// g / (1 + expf(-g)) * u of x[route] and x_up[route] (src/qwen3_moe_runner.cpp:
+// 682-684).  Lanes (row, block); one lane per row then sums the block dots in
+// block order starting from 0.  With segments, workgroups along x are split
+// between up to three matrices that share the input.
 template <int T>
 __global__ __launch_bounds__(256) void k_ref_matvec(RefMatvecArgs a) {
-    extern __shared__ float lds[];  // x [in], then partial dots [256]
+    extern __shared__ __attribute__((aligned(64))) float lds[];  // x [in], then block dots [256]
     constexpr uint32_t BE = RefBlock<T>::BE, BB = RefBlock<T>::BB;
     const uint32_t r = blockIdx.y, tid = threadIdx.x;
     const uint32_t nb = a.in / BE, rpw = 256u / nb;
+    const uint8_t* W = a.W;
+    uint64_t row_bytes = a.row_bytes, slice_bytes = a.slice_bytes;
+    uint32_t rows = a.rows, bx = blockIdx.x;
+    float* y = a.y;
+    if (a.nseg) {
+#pragma unroll
+        for (uint32_t j = 0; j < kMaxRefSegs; ++j) {
+            if (j < a.nseg && blockIdx.x >= a.seg[j].block0) {
+                W = a.seg[j].W;
+                row_bytes = a.seg[j].row_bytes;
+                slice_bytes = a.seg[j].slice_bytes;
+                rows = a.seg[j].rows;
+                y = a.seg[j].y;
+                bx = blockIdx.x - a.seg[j].block0;
+            }
+        }
+    }
     const float* x = a.x + static_cast<uint64_t>(r) * a.x_stride;
     float* xs = lds;
     float* part = lds + a.in;
-    for (uint32_t i = tid; i < a.in; i += 256u) xs[i] = x[i];
+    // staging: every load of a batch is issued before any is used
+    const uint32_t n4 = a.in / 4u;  // in is a multiple of 32
+    if (a.x_up) {
+        const f32x4* g4 = reinterpret_cast<const f32x4*>(x);
+        const f32x4* u4 = reinterpret_cast<const f32x4*>(a.x_up + static_cast<uint64_t>(r) * a.x_stride);
+        for (uint32_t base = 0; base < n4; base += 256u) {
+            const uint32_t i = base + tid, ic = i < n4 ? i : 0u;
+            const f32x4 gv = g4[ic], uv = u4[ic];
+            f32x4 act;
+            act.x = __fmul_rn(__fdiv_rn(gv.x, __fadd_rn(1.0f, expf_libm(-gv.x, a.expf))), uv.x);
+            act.y = __fmul_rn(__fdiv_rn(gv.y, __fadd_rn(1.0f, expf_libm(-gv.y, a.expf))), uv.y);
+            act.z = __fmul_rn(__fdiv_rn(gv.z, __fadd_rn(1.0f, expf_libm(-gv.z, a.expf))), uv.z);
+            act.w = __fmul_rn(__fdiv_rn(gv.w, __fadd_rn(1.0f, expf_libm(-gv.w, a.expf))), uv.w);
+            if (i < n4) reinterpret_cast<f32x4*>(xs)[i] = act;
+        }
+    } else {
+        const f32x4* x4 = reinterpret_cast<const f32x4*>(x);
+        for (uint32_t base = 0; base < n4; base += 512u) {
+            const uint32_t i0 = base + tid, i1 = i0 + 256u;
+            const f32x4 v0 = x4[i0 < n4 ? i0 : 0u], v1 = x4[i1 < n4 ? i1 : 0u];
+            if (i0 < n4) reinterpret_cast<f32x4*>(xs)[i0] = v0;
+            if (i1 < n4) reinterpret_cast<f32x4*>(xs)[i1] = v1;
+        }
+    }
     __syncthreads();
-    const uint8_t* W = a.W + (a.ids ? static_cast<uint64_t>(a.ids[r]) * a.slice_bytes : 0u);
-    const uint32_t row0 = blockIdx.x * rpw, lr = tid / nb, b = tid % nb, row = row0 + lr;
-    if (lr < rpw && row < a.rows)
-        part[tid] = block_dot<T>(W + static_cast<uint64_t>(row) * a.row_bytes + b * BB, xs + b * BE);
+    if (a.ids) W += static_cast<uint64_t>(a.ids[r]) * slice_bytes;
+    const uint32_t row0 = bx * rpw, lr = tid / nb, b = tid % nb, row = row0 + lr;
+    if (lr < rpw && row < rows)
+        part[tid] = block_dot<T>(W + static_cast<uint64_t>(row) * row_bytes + b * BB, xs + b * BE);
     __syncthreads();
-    if (tid < rpw && row0 + tid < a.rows) {
-        float s = 0.0f;
-        for (uint32_t k = 0; k < nb; ++k) s = __fadd_rn(s, part[tid * nb + k]);
-        a.y[static_cast<uint64_t>(r) * a.y_stride + row0 + tid] = s;
+    if (tid < rpw && row0 + tid < rows) {
+        float acc = 0.0f;
+        for (uint32_t k = 0; k < nb; ++k) acc = __fadd_rn(acc, part[tid * nb + k]);
+        y[static_cast<uint64_t>(r) * a.y_stride + row0 + tid] = acc;
     }
 }
 
-// F32 linear: 0 + dot_f32(w_row, x), one lane per row over the whole width.
-__global__ __launch_bounds__(256) void k_ref_linear_f32(RefMatvecArgs a) {
-    extern __shared__ float xs[];
-    const uint32_t r = blockIdx.y, tid = threadIdx.x;
+// F32 linear: 0 + dot_f32(w_row, x).  One wave per row: the products are
+// formed in parallel from coalesced loads (eight 16-byte loads per lane in
+// flight), then lane 0 adds them in order.
+__global__ __launch_bounds__(64) void k_ref_linear_f32(RefMatvecArgs a) {
+    extern __shared__ __attribute__((aligned(64))) float prod[];  // [chain_floats(in)]
+    const uint32_t row = blockIdx.x, r = blockIdx.y, lane = threadIdx.x;
     const float* x = a.x + static_cast<uint64_t>(r) * a.x_stride;
-    for (uint32_t i = tid; i < a.in; i += 256u) xs[i] = x[i];
-    __syncthreads();
-    const uint32_t row = blockIdx.x * 256u + tid;
-    if (row >= a.rows) return;
     const float* w = reinterpret_cast<const float*>(a.W + static_cast<uint64_t>(row) * a.row_bytes);
-    float s = 0.0f;
-    for (uint32_t i = 0; i < a.in; ++i) s = __fadd_rn(s, __fmul_rn(w[i], xs[i]));
-    a.y[static_cast<uint64_t>(r) * a.y_stride + row] = __fadd_rn(0.0f, s);
+    if ((a.in & 3u) == 0u) {
+        const uint32_t n4 = a.in / 4u;
+        const f32x4* w4 = reinterpret_cast<const f32x4*>(w);
+        const f32x4* x4 = reinterpret_cast<const f32x4*>(x);
+        f32x4* p4 = reinterpret_cast<f32x4*>(prod);
+        for (uint32_t base = 0; base < n4; base += 512u) {
+            f32x4 wv[8], xv[8];
+#pragma unroll
+            for (uint32_t k = 0; k < 8; ++k) {
+                const uint32_t i = base + lane + 64u * k, ic = i < n4 ? i : 0u;
+                wv[k] = w4[ic];
+                xv[k] = x4[ic];
+            }
+#pragma unroll
+            for (uint32_t k = 0; k < 8; ++k) {
+                const uint32_t i = base + lane + 64u * k;
+                if (i < n4) {
+                    f32x4 pv;
+                    pv.x = __fmul_rn(wv[k].x, xv[k].x);
+                    pv.y = __fmul_rn(wv[k].y, xv[k].y);
+                    pv.z = __fmul_rn(wv[k].z, xv[k].z);
+                    pv.w = __fmul_rn(wv[k].w, xv[k].w);
+                    p4[i] = pv;
+                }
+            }
+        }
+    } else {
+        for (uint32_t i = lane; i < a.in; i += 64u) prod[i] = __fmul_rn(w[i], x[i]);
+    }
+    __syncthreads();
+    if (lane == 0)
+        a.y[static_cast<uint64_t>(r) * a.y_stride + row] = __fadd_rn(0.0f, serial_sum(prod, a.in, 0.0f));
 }
 
-// x += delta (if any); out = (x * scale) * w, scale = 1 / sqrt(sum_sq / n + eps)
-// with sum_sq the serial FP32 sum of the rounded squares.  One workgroup per
-// row of `n` values (rows: the per-head q/k norms).
-__global__ __launch_bounds__(256) void k_ref_rmsnorm(float* x, const float* delta, const float* w,
-                                                     float* out, uint32_t n, float eps) {
-    extern __shared__ float sq[];
+// x += the residual (delta, or sum_r p_r * parts_r added in route order from
+// 0, as the MoE block's moe_result, src/qwen3_moe_runner.cpp:688-692); then
+// out = (x * scale) * w with scale = 1 / sqrt(sum_sq / n + eps) and sum_sq the
+// serial FP32 sum of the rounded squares (rms_norm, src/rms_norm.cpp:9-27).
+// One 1024-thread workgroup per row of n <= 1024 * PER values; every load is
+// issued before any is used, and the values stay in registers across the sum.
+template <int PER>
+__global__ __launch_bounds__(1024) void k_ref_rmsnorm(float* x, RefResidual res, const float* w,
+                                                      float* out, uint32_t n, float eps) {
+    extern __shared__ __attribute__((aligned(64))) float sq[];  // [chain_floats(n)]
     __shared__ float s_scale;
+    const uint32_t tid = threadIdx.x;
     float* xr = x + static_cast<uint64_t>(blockIdx.x) * n;
     float* orow = out + static_cast<uint64_t>(blockIdx.x) * n;
-    for (uint32_t i = threadIdx.x; i < n; i += blockDim.x) {
-        float v = xr[i];
-        if (delta) {
-            v = __fadd_rn(v, delta[i]);
-            xr[i] = v;
-        }
-        sq[i] = __fmul_rn(v, v);
+    uint32_t ic[PER];
+    float v[PER], wv[PER];
+#pragma unroll
+    for (int k = 0; k < PER; ++k) {
+        const uint32_t i = tid + 1024u * k;
+        ic[k] = i < n ? i : 0u;
+        v[k] = xr[ic[k]];
+        wv[k] = w[ic[k]];
     }
+    if (res.parts) {
+        // routes in batches of RB whose loads are all in flight together
+        constexpr uint32_t RB = PER <= 2 ? kMaxRefTopK : 32u / PER;
+        float yv[PER];
+#pragma unroll
+        for (int k = 0; k < PER; ++k) yv[k] = 0.0f;
+        for (uint32_t r0 = 0; r0 < res.K; r0 += RB) {
+            float pr[RB], pv[RB][PER];
+#pragma unroll
+            for (uint32_t j = 0; j < RB; ++j) {
+                const uint32_t rc = r0 + j < res.K ? r0 + j : 0u;
+                pr[j] = res.probs[rc];
+#pragma unroll
+                for (int k = 0; k < PER; ++k) pv[j][k] = res.parts[static_cast<uint64_t>(rc) * n + ic[k]];
+            }
+#pragma unroll
+            for (uint32_t j = 0; j < RB; ++j)
+                if (r0 + j < res.K) {
+#pragma unroll
+                    for (int k = 0; k < PER; ++k) yv[k] = __fadd_rn(yv[k], __fmul_rn(pr[j], pv[j][k]));
+                }
+        }
+#pragma unroll
+        for (int k = 0; k < PER; ++k) v[k] = __fadd_rn(v[k], yv[k]);
+    } else if (res.delta) {
+        float dv[PER];
+#pragma unroll
+        for (int k = 0; k < PER; ++k) dv[k] = res.delta[ic[k]];
+#pragma unroll
+        for (int k = 0; k < PER; ++k) v[k] = __fadd_rn(v[k], dv[k]);
+    }
+#pragma unroll
+    for (int k = 0; k < PER; ++k)
+        if (tid + 1024u * k < n) sq[tid + 1024u * k] = __fmul_rn(v[k], v[k]);
     __syncthreads();
-    if (threadIdx.x == 0) {
-        float s = 0.0f;
-        for (uint32_t i = 0; i < n; ++i) s = __fadd_rn(s, sq[i]);
-        s_scale = 1.0f / sqrtf(s / static_cast<float>(n) + eps);
+    if (tid == 0) {
+        const float sum = serial_sum(sq, n, 0.0f);
+        s_scale = 1.0f / sqrtf(sum / static_cast<float>(n) + eps);
     }
     __syncthreads();
     const float scale = s_scale;
-    for (uint32_t i = threadIdx.x; i < n; i += blockDim.x)
-        orow[i] = __fmul_rn(__fmul_rn(xr[i], scale), w[i]);
+#pragma unroll
+    for (int k = 0; k < PER; ++k) {
+        const uint32_t i = tid + 1024u * k;
+        if (i < n) {
+            if (res.parts || res.delta) xr[i] = v[k];
+            orow[i] = __fmul_rn(__fmul_rn(v[k], scale), wv[k]);
+        }
+    }
 }
 
 // Per-head q/k RMSNorm (serial) and RoPE from the host-computed table, k and
@@ -237,138 +437,180 @@ __global__ __launch_bounds__(128) void k_ref_qk_rope_kv(ModelArgs a, ModelLayer 
     }
 }
 
-// Attention of one q head: serial scores, max, exp, serial denominator,
-// out[d] = ((0 + p0 v0[d]) + p1 v1[d]) + ... in position order.
+// Attention of one q head over its KV window, in position order
+// (KvCache::attend, src/kv_cache.cpp:185-293): score_i = (serial dot of q
+// and k_i) * scale; the maximum; p_i = expf(score_i - max); the serial
+// denominator; out[d] = ((0 + (p_0 / den) v_0[d]) + (p_1 / den) v_1[d]) + ...
+// Each position's FP16 K row is loaded whole (HD / 8 16-byte loads), V rows
+// are staged through LDS a tile of positions at a time.
+constexpr uint32_t kAttnTileBytes = 64u * 1024u;
+template <int HD>
 __global__ __launch_bounds__(256) void k_ref_attention(ModelArgs a, ModelLayer L) {
-    extern __shared__ float sc[];  // [capacity]
-    __shared__ float qv[256];
-    __shared__ float s_max, s_den;
-    const uint32_t h = blockIdx.x, tid = threadIdx.x, hd = a.head_dim;
+    extern __shared__ __attribute__((aligned(64))) float lds[];  // sc [chain_floats(capacity)], V tile
+    __shared__ float qv[HD];
+    __shared__ float red[4];
+    __shared__ float s_den;
+    constexpr uint32_t TILE = kAttnTileBytes / (2u * HD);
+    const uint32_t h = blockIdx.x, tid = threadIdx.x;
     const uint32_t kvh = h / (a.heads / a.kv_heads);
     const uint32_t pos = a.state[0];
     const uint32_t n = pos + 1u < a.capacity ? pos + 1u : a.capacity;
     const uint32_t first = pos + 1u - n;
-    for (uint32_t d = tid; d < hd; d += blockDim.x) qv[d] = a.q[h * hd + d];
+    float* sc = lds;
+    uint16_t* vt = reinterpret_cast<uint16_t*>(lds + chain_floats(a.capacity));
+    for (uint32_t d = tid; d < HD; d += 256u) qv[d] = a.q[h * HD + d];
     __syncthreads();
-    for (uint32_t i = tid; i < n; i += blockDim.x) {
+    const uint64_t row_halves = static_cast<uint64_t>(a.kv_heads) * HD;
+    float m = -INFINITY;
+    for (uint32_t i = tid; i < n; i += 256u) {
         const uint32_t slot = (first + i) % a.capacity;
-        const uint16_t* kr = L.kcache + (static_cast<uint64_t>(slot) * a.kv_heads + kvh) * hd;
+        const u32x4_t* kr = reinterpret_cast<const u32x4_t*>(L.kcache + slot * row_halves + kvh * HD);
+        u32x4_t kw[HD / 8];
+#pragma unroll
+        for (int j = 0; j < HD / 8; ++j) kw[j] = kr[j];
         float s = 0.0f;
-        for (uint32_t d = 0; d < hd; ++d)
-            s = __fadd_rn(s, __fmul_rn(qv[d], __half2float(__ushort_as_half(kr[d]))));
-        sc[i] = __fmul_rn(s, a.attn_scale);
+#pragma unroll
+        for (int j = 0; j < HD / 8; ++j) {
+            const uint32_t w4[4] = {kw[j].x, kw[j].y, kw[j].z, kw[j].w};
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const uint16_t bits = static_cast<uint16_t>(w4[e / 2] >> (16 * (e % 2)));
+                s = __fadd_rn(s, __fmul_rn(qv[8 * j + e], __half2float(__ushort_as_half(bits))));
+            }
+        }
+        s = __fmul_rn(s, a.attn_scale);
+        sc[i] = s;
+        m = fmaxf(m, s);
+    }
+    // the maximum (its value does not depend on the order it is found in)
+    for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+    if ((tid & 63u) == 0u) red[tid >> 6] = m;
+    __syncthreads();
+    const float mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    for (uint32_t i = tid; i < n; i += 256u) sc[i] = expf_libm(__fsub_rn(sc[i], mx), a.expf);
+    __syncthreads();
+    if (tid == 0) s_den = serial_sum(sc, n, 0.0f);
+    __syncthreads();
+    const float den = s_den;
+    for (uint32_t i = tid; i < n; i += 256u) sc[i] = __fdiv_rn(sc[i], den);
+    float o = 0.0f;
+    for (uint32_t t0 = 0; t0 < n; t0 += TILE) {
+        const uint32_t tn = n - t0 < TILE ? n - t0 : TILE;
+        __syncthreads();  // previous tile consumed (and, first time, the weights written)
+        // stage V rows t0 .. t0 + tn: HD / 8 16-byte pieces per row
+        constexpr uint32_t PPR = HD / 8;
+        for (uint32_t base = 0; base < tn * PPR; base += 256u * 4u) {
+            u32x4_t pv[4];
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const uint32_t q = base + tid + 256u * k, qc = q < tn * PPR ? q : 0u;
+                const uint32_t slot = (first + t0 + qc / PPR) % a.capacity;
+                pv[k] = reinterpret_cast<const u32x4_t*>(L.vcache + slot * row_halves + kvh * HD)[qc % PPR];
+            }
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const uint32_t q = base + tid + 256u * k;
+                if (q < tn * PPR) reinterpret_cast<u32x4_t*>(vt)[q] = pv[k];
+            }
+        }
+        __syncthreads();
+        if (tid < HD) {
+            for (uint32_t i = 0; i < tn; ++i) {
+                const float v = __half2float(__ushort_as_half(vt[i * HD + tid]));
+                o = __fadd_rn(o, __fmul_rn(sc[t0 + i], v));
+            }
+        }
+    }
+    if (tid < HD) a.att[h * HD + tid] = o;
+}
+
+// route_experts over the serial FP32 logits, one thread per expert: the
+// FP64 exponentials in parallel, their sum in expert order by one lane, the
+// route order as each expert's rank under (logit desc, id asc) -- the order
+// the reference's stable insertion produces -- then FP32 probabilities and
+// the FP32 renormalisation.  Non-finite logits flag the status word.
+__global__ __launch_bounds__(256) void k_ref_routes(const float* logits, uint32_t E, uint32_t K,
+                                                    uint32_t normalize, uint32_t* ids,
+                                                    float* probs, uint32_t* status) {
+    __shared__ __attribute__((aligned(16))) float lg[kMaxExperts256];
+    __shared__ __attribute__((aligned(16))) double ex[kMaxExperts256];
+    __shared__ float wmax[4];
+    __shared__ uint32_t sel[kMaxRefTopK];
+    __shared__ float pr[kMaxRefTopK];
+    __shared__ double s_den;
+    const uint32_t t = threadIdx.x;
+    const bool on = t < E;
+    const float l = on ? logits[t] : -INFINITY;
+    lg[t] = l;  // -inf past E: never ranks before a finite logit
+    if (__syncthreads_or(on && !isfinite(l))) {
+        if (t < K) {
+            ids[t] = 0u;  // keep the expert reads in bounds; the error is reported
+            probs[t] = 0.0f;
+        }
+        if (t == 0) atomicOr(status, 1u);
+        return;
+    }
+    // the maximum (its value does not depend on the order it is found in)
+    float m = l;
+    for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+    if ((t & 63u) == 0u) wmax[t >> 6] = m;
+    __syncthreads();
+    const float mx = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
+    const double e = on ? exp(static_cast<double>(__fsub_rn(l, mx))) : 0.0;
+    if (on) ex[t] = e;
+    uint32_t rank = 0;
+    if (on) {
+        const uint32_t E4 = (E + 3u) / 4u;  // lg is padded with -inf to a multiple of 4
+        for (uint32_t j4 = 0; j4 < E4; ++j4) {
+            const f32x4 q = reinterpret_cast<const f32x4*>(lg)[j4];
+            const uint32_t j = 4u * j4;
+            rank += (q.x > l || (q.x == l && j < t)) ? 1u : 0u;
+            rank += (q.y > l || (q.y == l && j + 1u < t)) ? 1u : 0u;
+            rank += (q.z > l || (q.z == l && j + 2u < t)) ? 1u : 0u;
+            rank += (q.w > l || (q.w == l && j + 3u < t)) ? 1u : 0u;
+        }
+        if (rank < K) sel[rank] = t;
     }
     __syncthreads();
-    if (tid == 0) {
-        float m = -INFINITY;
-        for (uint32_t i = 0; i < n; ++i) m = fmaxf(m, sc[i]);
-        s_max = m;
-    }
-    __syncthreads();
-    for (uint32_t i = tid; i < n; i += blockDim.x) sc[i] = expf_libm(__fsub_rn(sc[i], s_max), a.expf_bucket, a.expf_pairs);
-    __syncthreads();
-    if (tid == 0) {
-        float den = 0.0f;
-        for (uint32_t i = 0; i < n; ++i) den = __fadd_rn(den, sc[i]);
+    if (t == 0) {
+        double den = 0.0;
+        for (uint32_t i = 0; i < E; ++i) den += ex[i];
         s_den = den;
     }
     __syncthreads();
-    const float den = s_den;
-    for (uint32_t d = tid; d < hd; d += blockDim.x) {
-        float o = 0.0f;
-        for (uint32_t i = 0; i < n; ++i) {
-            const uint32_t slot = (first + i) % a.capacity;
-            const float v = __half2float(__ushort_as_half(
-                L.vcache[(static_cast<uint64_t>(slot) * a.kv_heads + kvh) * hd + d]));
-            o = __fadd_rn(o, __fmul_rn(__fdiv_rn(sc[i], den), v));
-        }
-        a.att[h * hd + d] = o;
-    }
-}
-
-// route_experts over the serial FP32 logits: FP64 denominator in expert
-// order, stable top-k by (logit desc, id asc), FP32 probabilities, FP32
-// renormalisation.  One thread.  Non-finite logits flag the status word.
-__global__ void k_ref_routes(const float* logits, uint32_t E, uint32_t K, uint32_t normalize,
-                             uint32_t* ids, float* probs, uint32_t* status) {
-    if (threadIdx.x != 0) return;
-    float mx = logits[0];
-    bool bad = false;
-    for (uint32_t e = 0; e < E; ++e) {
-        bad = bad || !isfinite(logits[e]);
-        if (logits[e] > mx) mx = logits[e];
-    }
-    if (bad || !isfinite(mx)) {
-        atomicOr(status, 1u);
+    if (on && rank < K) pr[rank] = static_cast<float>(e / s_den);
+    __syncthreads();
+    if (t == 0) {
+        float sum = 0.0f;
+        for (uint32_t r = 0; r < K; ++r) sum = __fadd_rn(sum, pr[r]);
         for (uint32_t r = 0; r < K; ++r) {
-            ids[r] = 0u;  // keep the expert reads in bounds; the error is reported
-            probs[r] = 0.0f;
+            ids[r] = sel[r];
+            probs[r] = normalize ? __fdiv_rn(pr[r], sum) : pr[r];
         }
-        return;
-    }
-    double den = 0.0;
-    for (uint32_t e = 0; e < E; ++e) den += exp(static_cast<double>(__fsub_rn(logits[e], mx)));
-    uint32_t sel[kMaxRefTopK];
-    uint32_t n = 0;
-    for (uint32_t e = 0; e < E; ++e) {
-        const float l = logits[e];
-        uint32_t at = n;  // lower_bound: first place whose entry is not before e
-        for (uint32_t j = 0; j < n; ++j) {
-            const float lj = logits[sel[j]];
-            if (!(lj > l || (lj == l && sel[j] < e))) {
-                at = j;
-                break;
-            }
-        }
-        if (n < K) {
-            for (uint32_t j = n; j > at; --j) sel[j] = sel[j - 1];
-            sel[at] = e;
-            ++n;
-        } else if (at < n) {
-            for (uint32_t j = n - 1; j > at; --j) sel[j] = sel[j - 1];
-            sel[at] = e;
-        }
-    }
-    float p[kMaxRefTopK];
-    float sum = 0.0f;
-    for (uint32_t r = 0; r < K; ++r) {
-        p[r] = static_cast<float>(exp(static_cast<double>(__fsub_rn(logits[sel[r]], mx))) / den);
-        sum = __fadd_rn(sum, p[r]);
-    }
-    for (uint32_t r = 0; r < K; ++r) {
-        ids[r] = sel[r];
-        probs[r] = normalize ? __fdiv_rn(p[r], sum) : p[r];
     }
 }
 
-// act = (g / (1 + expf(-g))) * u for every route (src/qwen3_moe_runner.cpp:682-684).
-__global__ __launch_bounds__(256) void k_ref_swiglu(const float* g, const float* u, float* act,
-                                                    uint32_t n, const uint32_t* expf_bucket,
-                                                    const uint32_t* expf_pairs) {
-    const uint32_t i = blockIdx.x * 256u + threadIdx.x;
-    if (i >= n) return;
-    const float e = expf_libm(-g[i], expf_bucket, expf_pairs);
-    act[i] = __fmul_rn(__fdiv_rn(g[i], __fadd_rn(1.0f, e)), u[i]);
-}
-
-// moe[i] = ((0 + p0 o0[i]) + p1 o1[i]) + ... in route order.
-__global__ __launch_bounds__(256) void k_ref_combine(const float* out, const float* probs,
-                                                     uint32_t K, uint32_t H, float* moe) {
-    const uint32_t i = blockIdx.x * 256u + threadIdx.x;
-    if (i >= H) return;
-    float y = 0.0f;
-    for (uint32_t r = 0; r < K; ++r)
-        y = __fadd_rn(y, __fmul_rn(probs[r], out[static_cast<uint64_t>(r) * H + i]));
-    moe[i] = y;
+uint32_t ref_block_elems(uint32_t type) {
+    return type == T_Q8_0 || type == T_Q4_0 ? 32u : 256u;
 }
 
 template <int T>
-hipError_t ref_matvec_t(const RefMatvecArgs& a, uint32_t routes, hipStream_t s) {
-    constexpr uint32_t BE = RefBlock<T>::BE;
-    const uint32_t nb = a.in / BE, rpw = 256u / nb;
+hipError_t ref_matvec_t(const RefMatvecArgs& a, uint32_t blocks, uint32_t routes, hipStream_t s) {
     const size_t lds = (a.in + 256u) * sizeof(float);
-    hipLaunchKernelGGL(k_ref_matvec<T>, dim3((a.rows + rpw - 1u) / rpw, routes), dim3(256), lds, s, a);
+    hipLaunchKernelGGL(k_ref_matvec<T>, dim3(blocks, routes), dim3(256), lds, s, a);
     return hipGetLastError();
+}
+
+hipError_t ref_matvec_launch(uint32_t type, const RefMatvecArgs& a, uint32_t blocks,
+                             uint32_t routes, hipStream_t s) {
+    switch (type) {
+        case T_Q4_K: return ref_matvec_t<T_Q4_K>(a, blocks, routes, s);
+        case T_Q5_K: return ref_matvec_t<T_Q5_K>(a, blocks, routes, s);
+        case T_Q6_K: return ref_matvec_t<T_Q6_K>(a, blocks, routes, s);
+        case T_Q8_0: return ref_matvec_t<T_Q8_0>(a, blocks, routes, s);
+        case T_Q4_0: return ref_matvec_t<T_Q4_0>(a, blocks, routes, s);
+        default: return hipErrorInvalidValue;
+    }
 }
 
 }  // namespace
@@ -384,90 +626,142 @@ bool ref_matvec_supported(uint32_t type, uint32_t in) {
 }
 
 hipError_t launch_ref_matvec(uint32_t type, const RefMatvecArgs& a, uint32_t routes, hipStream_t s) {
-    switch (type) {
-        case T_F32: {
-            hipLaunchKernelGGL(k_ref_linear_f32, dim3((a.rows + 255u) / 256u, routes), dim3(256),
-                               a.in * sizeof(float), s, a);
-            return hipGetLastError();
-        }
-        case T_Q4_K: return ref_matvec_t<T_Q4_K>(a, routes, s);
-        case T_Q5_K: return ref_matvec_t<T_Q5_K>(a, routes, s);
-        case T_Q6_K: return ref_matvec_t<T_Q6_K>(a, routes, s);
-        case T_Q8_0: return ref_matvec_t<T_Q8_0>(a, routes, s);
-        case T_Q4_0: return ref_matvec_t<T_Q4_0>(a, routes, s);
-        default: return hipErrorInvalidValue;
+    if (type == T_F32) {
+        hipLaunchKernelGGL(k_ref_linear_f32, dim3(a.rows, routes), dim3(64),
+                           chain_floats(a.in) * sizeof(float), s, a);
+        return hipGetLastError();
     }
+    if (a.nseg) return hipErrorInvalidValue;
+    const uint32_t rpw = 256u / (a.in / ref_block_elems(type));
+    return ref_matvec_launch(type, a, (a.rows + rpw - 1u) / rpw, routes, s);
 }
 
-hipError_t launch_ref_rmsnorm(float* x, const float* delta, const float* w, float* out, uint32_t n,
-                              uint32_t rows, float eps, hipStream_t s) {
-    hipLaunchKernelGGL(k_ref_rmsnorm, dim3(rows), dim3(256), n * sizeof(float), s, x, delta, w, out,
-                       n, eps);
+hipError_t launch_ref_matvec_multi(uint32_t type, RefMatvecArgs a, const RefSeg* segs, uint32_t n,
+                                   uint32_t routes, hipStream_t s) {
+    if (type == T_F32 || n == 0 || n > kMaxRefSegs) return hipErrorInvalidValue;
+    const uint32_t rpw = 256u / (a.in / ref_block_elems(type));
+    uint32_t blocks = 0;
+    a.nseg = n;
+    for (uint32_t j = 0; j < n; ++j) {
+        a.seg[j] = segs[j];
+        a.seg[j].block0 = blocks;
+        blocks += (segs[j].rows + rpw - 1u) / rpw;
+    }
+    return ref_matvec_launch(type, a, blocks, routes, s);
+}
+
+hipError_t launch_ref_rmsnorm(float* x, const RefResidual& res, const float* w, float* out,
+                              uint32_t n, uint32_t rows, float eps, hipStream_t s) {
+    const size_t lds = chain_floats(n) * sizeof(float);
+    if (n == 0 || n > kMaxRefWidth || res.K > kMaxRefTopK) return hipErrorInvalidValue;
+    if (n <= 1024u) hipLaunchKernelGGL(k_ref_rmsnorm<1>, dim3(rows), dim3(1024), lds, s, x, res, w, out, n, eps);
+    else if (n <= 2048u) hipLaunchKernelGGL(k_ref_rmsnorm<2>, dim3(rows), dim3(1024), lds, s, x, res, w, out, n, eps);
+    else if (n <= 4096u) hipLaunchKernelGGL(k_ref_rmsnorm<4>, dim3(rows), dim3(1024), lds, s, x, res, w, out, n, eps);
+    else hipLaunchKernelGGL(k_ref_rmsnorm<8>, dim3(rows), dim3(1024), lds, s, x, res, w, out, n, eps);
     return hipGetLastError();
 }
 
-hipError_t launch_ref_layer_attention(const ModelArgs& a, const ModelLayer& L, hipStream_t s) {
-    hipLaunchKernelGGL(k_ref_qk_rope_kv, dim3(a.heads + 2u * a.kv_heads), dim3(a.head_dim), 0, s, a,
-                       L);
-    hipLaunchKernelGGL(k_ref_attention, dim3(a.heads), dim3(256), a.capacity * sizeof(float), s, a, L);
-    return hipGetLastError();
+bool ref_attention_supported(uint32_t head_dim, uint32_t capacity) {
+    return (head_dim == 64u || head_dim == 128u || head_dim == 256u) &&
+           (chain_floats(capacity) * 4ull + kAttnTileBytes) <= 160ull * 1024u - 2048u;
 }
 
-hipError_t launch_ref_moe(const ModelArgs& a, const ModelLayer& L, hipStream_t s) {
-    const MoeDecodeArgs& m = L.moe;
-    RefMatvecArgs r{};
-    // router logits into the act buffer's tail (free until the gate/up rows)
-    float* logits = a.ref_scratch;
-    float* g = logits + kMaxExperts256;
-    float* u = g + static_cast<uint64_t>(m.top_k) * m.ffn;
-    float* act = u + static_cast<uint64_t>(m.top_k) * m.ffn;
-    float* out = act + static_cast<uint64_t>(m.top_k) * m.ffn;
-    r.W = reinterpret_cast<const uint8_t*>(m.router);
-    r.row_bytes = static_cast<uint64_t>(m.hidden) * 4u;
-    r.rows = m.n_experts;
-    r.in = m.hidden;
-    r.x = m.x;
-    r.y = logits;
-    hipError_t err = launch_ref_matvec(T_F32, r, 1, s);
-    if (err != hipSuccess) return err;
-    hipLaunchKernelGGL(k_ref_routes, dim3(1), dim3(64), 0, s, logits, m.n_experts, m.top_k,
-                       m.normalize, m.ids, m.probs, m.status);
-    // gate / up of every selected expert
-    RefMatvecArgs e{};
-    e.ids = m.ids;
-    e.rows = m.ffn;
-    e.in = m.hidden;
-    e.x = m.x;
-    e.x_stride = 0;
-    e.y_stride = m.ffn;
-    e.W = m.gate;
-    e.row_bytes = m.gate_row;
-    e.slice_bytes = m.gate_slice;
-    e.y = g;
-    if ((err = launch_ref_matvec(m.gate_type, e, m.top_k, s))) return err;
-    e.W = m.up;
-    e.row_bytes = m.up_row;
-    e.slice_bytes = m.up_slice;
-    e.y = u;
-    if ((err = launch_ref_matvec(m.up_type, e, m.top_k, s))) return err;
-    const uint32_t n = m.top_k * m.ffn;
-    hipLaunchKernelGGL(k_ref_swiglu, dim3((n + 255u) / 256u), dim3(256), 0, s, g, u, act, n,
-                       a.expf_bucket, a.expf_pairs);
-    RefMatvecArgs d{};
-    d.ids = m.ids;
-    d.W = m.down;
-    d.row_bytes = m.down_row;
-    d.slice_bytes = m.down_slice;
-    d.rows = m.hidden;
-    d.in = m.ffn;
-    d.x = act;
-    d.x_stride = m.ffn;
-    d.y = out;
-    d.y_stride = m.hidden;
-    if ((err = launch_ref_matvec(m.down_type, d, m.top_k, s))) return err;
-    hipLaunchKernelGGL(k_ref_combine, dim3((m.hidden + 255u) / 256u), dim3(256), 0, s, out, m.probs,
-                       m.top_k, m.hidden, m.y);
-    return hipGetLastError();
+hipError_t launch_ref_step(const ModelArgs& a, const ModelLayer* layers, bool logits, hipStream_t s) {
+    const uint32_t qd = a.heads * a.head_dim, kd = a.kv_heads * a.head_dim;
+    RefResidual res{};  // what the next RMSNorm adds to the residual stream first
+    hipError_t err = hipSuccess;
+    for (uint32_t l = 0; l < a.layers; ++l) {
+        const ModelLayer& L = layers[l];
+        const MoeDecodeArgs& m = L.moe;
+        if ((err = launch_ref_rmsnorm(a.hidden_state, res, L.attn_norm, a.normed, a.hidden, 1,
+                                      a.rms_eps, s)))
+            return err;
+        RefMatvecArgs qkv{};
+        qkv.in = a.hidden;
+        qkv.x = a.normed;
+        const RefSeg qkv_segs[3] = {{L.q, L.q_row, 0, qd, 0, a.q},
+                                    {L.k, L.k_row, 0, kd, 0, a.k},
+                                    {L.v, L.v_row, 0, kd, 0, a.v}};
+        if ((err = launch_ref_matvec_multi(L.attn_type, qkv, qkv_segs, 3, 1, s))) return err;
+        hipLaunchKernelGGL(k_ref_qk_rope_kv, dim3(a.heads + 2u * a.kv_heads), dim3(a.head_dim), 0,
+                           s, a, L);
+        {
+            const size_t lds = chain_floats(a.capacity) * sizeof(float) + kAttnTileBytes;
+            switch (a.head_dim) {
+                case 64: hipLaunchKernelGGL(k_ref_attention<64>, dim3(a.heads), dim3(256), lds, s, a, L); break;
+                case 128: hipLaunchKernelGGL(k_ref_attention<128>, dim3(a.heads), dim3(256), lds, s, a, L); break;
+                case 256: hipLaunchKernelGGL(k_ref_attention<256>, dim3(a.heads), dim3(256), lds, s, a, L); break;
+                default: return hipErrorInvalidValue;
+            }
+        }
+        RefMatvecArgs o{};
+        o.W = L.o;
+        o.row_bytes = L.o_row;
+        o.rows = a.hidden;
+        o.in = qd;
+        o.x = a.att;
+        o.y = a.attn_out;
+        if ((err = launch_ref_matvec(L.attn_type, o, 1, s))) return err;
+        res = RefResidual{a.attn_out, nullptr, nullptr, 0};
+        if ((err = launch_ref_rmsnorm(a.hidden_state, res, L.ffn_norm, a.normed, a.hidden, 1,
+                                      a.rms_eps, s)))
+            return err;
+        // MoE block: router logits, routes, gate/up of every route, SwiGLU + down
+        float* rl = a.ref_scratch;
+        float* g = rl + kMaxExperts256;
+        float* u = g + static_cast<uint64_t>(m.top_k) * m.ffn;
+        float* out = u + static_cast<uint64_t>(m.top_k) * m.ffn;
+        RefMatvecArgs router{};
+        router.W = reinterpret_cast<const uint8_t*>(m.router);
+        router.row_bytes = static_cast<uint64_t>(m.hidden) * 4u;
+        router.rows = m.n_experts;
+        router.in = m.hidden;
+        router.x = a.normed;
+        router.y = rl;
+        if ((err = launch_ref_matvec(T_F32, router, 1, s))) return err;
+        hipLaunchKernelGGL(k_ref_routes, dim3(1), dim3(256), 0, s, rl, m.n_experts, m.top_k,
+                           m.normalize, m.ids, m.probs, m.status);
+        RefMatvecArgs gu{};
+        gu.ids = m.ids;
+        gu.in = m.hidden;
+        gu.x = a.normed;
+        gu.y_stride = m.ffn;
+        const RefSeg gu_segs[2] = {{m.gate, m.gate_row, m.gate_slice, m.ffn, 0, g},
+                                   {m.up, m.up_row, m.up_slice, m.ffn, 0, u}};
+        if (m.gate_type == m.up_type) {
+            if ((err = launch_ref_matvec_multi(m.gate_type, gu, gu_segs, 2, m.top_k, s))) return err;
+        } else {
+            if ((err = launch_ref_matvec_multi(m.gate_type, gu, gu_segs, 1, m.top_k, s))) return err;
+            if ((err = launch_ref_matvec_multi(m.up_type, gu, gu_segs + 1, 1, m.top_k, s))) return err;
+        }
+        RefMatvecArgs d{};
+        d.ids = m.ids;
+        d.W = m.down;
+        d.row_bytes = m.down_row;
+        d.slice_bytes = m.down_slice;
+        d.rows = m.hidden;
+        d.in = m.ffn;
+        d.x = g;
+        d.x_up = u;
+        d.x_stride = m.ffn;
+        d.expf = a.expf;
+        d.y = out;
+        d.y_stride = m.hidden;
+        if ((err = launch_ref_matvec(m.down_type, d, m.top_k, s))) return err;
+        res = RefResidual{nullptr, out, m.probs, m.top_k};
+    }
+    if (!logits) return hipGetLastError();
+    if ((err = launch_ref_rmsnorm(a.hidden_state, res, a.out_norm, a.normed, a.hidden, 1, a.rms_eps,
+                                  s)))
+        return err;
+    RefMatvecArgs h{};
+    h.W = a.out;
+    h.row_bytes = a.out_row;
+    h.rows = a.vocab;
+    h.in = a.hidden;
+    h.x = a.normed;
+    h.y = a.logits;
+    return launch_ref_matvec(a.out_type, h, 1, s);
 }
 
 }  // namespace pk

@@ -105,6 +105,16 @@ struct ModelLayer {
     uint16_t* vcache;
     MoeDecodeArgs moe;        // x = the normed state, y = this layer's MoE output
 };
+// The host libm's expf results that differ from the correctly rounded value,
+// as a two-choice cuckoo table: input bits b sit at slots[h0(b)] of the first
+// half or slots[h1(b)] of the second, h_t(b) = (b * mul_t) >> (32 - bits);
+// a slot is (input bits, result bits), empty slots hold input 0xffffffff.
+struct LibmExpf {
+    const uint32_t* slots;    // [2][1 << bits][2], or null (no exceptions)
+    uint32_t bits, mul0, mul1;
+};
+constexpr uint32_t kExpfEmpty = 0xffffffffu;
+
 struct ModelArgs {
     uint32_t layers, hidden, heads, kv_heads, head_dim, vocab, capacity;
     uint32_t embd_type, out_type;
@@ -127,11 +137,8 @@ struct ModelArgs {
     // reference-order mode: every kernel repeats the CPU's operation order
     uint32_t exact;
     const float* rope_table;  // [positions][head_dim]: cos, then sin (host libm)
-    float* ref_scratch;       // router logits, gate, up, act, expert outputs
-    // libm expf exceptions: pairs [n][2] (input bits, result bits) sorted by
-    // input; bucket[t] .. bucket[t + 1] the pairs whose input's top 16 bits are t
-    const uint32_t* expf_bucket;  // [65537], or null
-    const uint32_t* expf_pairs;
+    float* ref_scratch;       // router logits, gate, up, expert outputs
+    LibmExpf expf;            // reference order: the host libm's expf exceptions
 };
 bool model_supported(const ModelArgs& a);
 // logits: run the final norm, head and argmax (else only advance the position).
@@ -148,6 +155,15 @@ hipError_t launch_synth_fill(uint8_t* dst, uint64_t nbytes, uint64_t key, uint32
 constexpr uint32_t kMaxRefWidth = 8192;
 constexpr uint32_t kMaxRefTopK = 16;
 constexpr uint32_t kMaxExperts256 = 256;
+// Up to kMaxRefSegs matrices of one type and width in one launch: segment k
+// covers workgroups [seg[k].block0, seg[k + 1].block0) along x.
+constexpr uint32_t kMaxRefSegs = 3;
+struct RefSeg {
+    const uint8_t* W;
+    uint64_t row_bytes, slice_bytes;
+    uint32_t rows, block0;
+    float* y;
+};
 struct RefMatvecArgs {
     const uint8_t* W;
     uint64_t row_bytes, slice_bytes;
@@ -157,17 +173,36 @@ struct RefMatvecArgs {
     uint64_t x_stride;
     float* y;
     uint64_t y_stride;
+    // optional, set by launch_ref_matvec_multi / the SwiGLU staging
+    uint32_t nseg;            // 0: the single matrix above
+    RefSeg seg[kMaxRefSegs];
+    const float* x_up;        // non-null: stage g / (1 + expf(-g)) * u, g = x, u = x_up
+    LibmExpf expf;
 };
 bool ref_matvec_supported(uint32_t type, uint32_t in);
 hipError_t launch_ref_matvec(uint32_t type, const RefMatvecArgs& a, uint32_t routes,
                              hipStream_t stream);
-hipError_t launch_ref_rmsnorm(float* x, const float* delta, const float* w, float* out, uint32_t n,
-                              uint32_t rows, float eps, hipStream_t stream);
-hipError_t launch_ref_layer_attention(const ModelArgs& a, const ModelLayer& L, hipStream_t stream);
-hipError_t launch_ref_moe(const ModelArgs& a, const ModelLayer& L, hipStream_t stream);
+// Several matrices sharing x (q/k/v; gate/up per route): one launch.
+hipError_t launch_ref_matvec_multi(uint32_t type, RefMatvecArgs a, const RefSeg* segs, uint32_t n,
+                                   uint32_t routes, hipStream_t stream);
+// x += delta (or the route-order combine of parts, if set); out = RMSNorm(x) * w
+struct RefResidual {
+    const float* delta;       // [n], or null
+    const float* parts;       // [K][n] expert outputs, combined with probs in route order
+    const float* probs;
+    uint32_t K;
+};
+hipError_t launch_ref_rmsnorm(float* x, const RefResidual& res, const float* w, float* out,
+                              uint32_t n, uint32_t rows, float eps, hipStream_t stream);
+// Head dims 64/128/256 and a KV window whose scores fit LDS beside a V tile.
+bool ref_attention_supported(uint32_t head_dim, uint32_t capacity);
+// The reference-order token step after the embedding (all layers, then the
+// head when logits).
+hipError_t launch_ref_step(const ModelArgs& a, const ModelLayer* layers, bool logits,
+                           hipStream_t stream);
 // floats of ModelArgs::ref_scratch for one layer shape
 inline uint64_t ref_scratch_floats(uint32_t top_k, uint32_t ffn, uint32_t hidden) {
-    return kMaxExperts256 + 3ull * top_k * ffn + static_cast<uint64_t>(top_k) * hidden;
+    return kMaxExperts256 + 2ull * top_k * ffn + static_cast<uint64_t>(top_k) * hidden;
 }
 
 // Individual stages (timing and tests).

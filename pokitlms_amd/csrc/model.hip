@@ -371,25 +371,22 @@ hipError_t launch_model_step(const ModelArgs& a, const ModelLayer* layers, bool 
         default: return hipErrorInvalidValue;
     }
     if (err != hipSuccess) return err;
+    if (a.exact) {
+        if ((err = launch_ref_step(a, layers, logits, s))) return err;
+        if (logits) hipLaunchKernelGGL(k_argmax, dim3(1), dim3(1024), 0, s, a);
+        else hipLaunchKernelGGL(k_advance, dim3(1), dim3(64), 0, s, a.state);
+        return hipGetLastError();
+    }
     const uint32_t qd = a.heads * a.head_dim, kd = a.kv_heads * a.head_dim;
     const float* delta = nullptr;  // the residual the next RMSNorm adds first
     auto norm = [&](const float* d, const float* w) -> hipError_t {
-        if (a.exact) return launch_ref_rmsnorm(a.hidden_state, d, w, a.normed, a.hidden, 1, a.rms_eps, s);
         hipLaunchKernelGGL(k_add_rmsnorm, dim3(1), dim3(256), 0, s, a.hidden_state, d, w, a.normed,
                            a.hidden, a.rms_eps);
         return hipGetLastError();
     };
     auto matvec = [&](uint32_t type, const uint8_t* W, uint64_t row_bytes, uint32_t rows,
                       uint32_t in, const float* x, float* y) -> hipError_t {
-        if (!a.exact) return launch_matvec(type, W, row_bytes, rows, in, x, y, 1, s);
-        RefMatvecArgs r{};
-        r.W = W;
-        r.row_bytes = row_bytes;
-        r.rows = rows;
-        r.in = in;
-        r.x = x;
-        r.y = y;
-        return launch_ref_matvec(type, r, 1, s);
+        return launch_matvec(type, W, row_bytes, rows, in, x, y, 1, s);
     };
     for (uint32_t l = 0; l < a.layers; ++l) {
         const ModelLayer& L = layers[l];
@@ -397,17 +394,13 @@ hipError_t launch_model_step(const ModelArgs& a, const ModelLayer* layers, bool 
         if ((err = matvec(L.attn_type, L.q, L.q_row, qd, a.hidden, a.normed, a.q))) return err;
         if ((err = matvec(L.attn_type, L.k, L.k_row, kd, a.hidden, a.normed, a.k))) return err;
         if ((err = matvec(L.attn_type, L.v, L.v_row, kd, a.hidden, a.normed, a.v))) return err;
-        if (a.exact) {
-            if ((err = launch_ref_layer_attention(a, L, s))) return err;
-        } else {
-            hipLaunchKernelGGL(k_qk_rope_kv, dim3(a.heads + 2u * a.kv_heads), dim3(a.head_dim), 0,
-                               s, a, L);
-            hipLaunchKernelGGL(k_attention, dim3(a.heads), dim3(256), a.capacity * sizeof(float), s,
-                               a, L);
-        }
+        hipLaunchKernelGGL(k_qk_rope_kv, dim3(a.heads + 2u * a.kv_heads), dim3(a.head_dim), 0, s,
+                           a, L);
+        hipLaunchKernelGGL(k_attention, dim3(a.heads), dim3(256), a.capacity * sizeof(float), s, a,
+                           L);
         if ((err = matvec(L.attn_type, L.o, L.o_row, a.hidden, qd, a.att, a.attn_out))) return err;
         if ((err = norm(a.attn_out, L.ffn_norm))) return err;
-        err = a.exact ? launch_ref_moe(a, L, s) : launch_moe_decode(L.moe, s);  // normed -> moe_out
+        err = launch_moe_decode(L.moe, s);  // normed -> moe_out
         if (err != hipSuccess) return err;
         delta = L.moe.y;
     }
