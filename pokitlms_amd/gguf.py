@@ -139,7 +139,12 @@ class GgufFile:
         self._parse()
 
     def close(self) -> None:
-        self._mm.close()
+        # payload views handed out keep the mapping alive; it is released with
+        # the last of them
+        try:
+            self._mm.close()
+        except BufferError:
+            pass
         self._f.close()
 
     def __enter__(self):
@@ -201,4 +206,6 @@ class GgufFile:
     def payload(self, name: str) -> np.ndarray:
         t = self.tensors[name]
         start = self.data_offset + t.offset
+        if start + t.nbytes > len(self._mm):
+            raise ValueError(f"{name}: payload runs past the end of the file")
         return np.frombuffer(self._mm, dtype=np.uint8, count=t.nbytes, offset=start)
