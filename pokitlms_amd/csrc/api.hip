@@ -946,12 +946,13 @@ pk_hip_status pk_hip_qwen3moe_create(pk_hip_ctx* ctx, const pk_hip_qwen3moe_conf
         // device state and activations
         m->state.ensure(4);
         m->tokens.ensure(1);
-        const uint64_t wf = 3ull * c.hidden + 2 * qd + 2 * kd + c.head_dim + c.vocab;
+        const uint64_t wf = 4ull * c.hidden + 2 * qd + 2 * kd + c.head_dim + c.vocab;
         m->work.ensure(wf);
         float* p = m->work.ptr;
         a.hidden_state = p; p += c.hidden;
         a.normed = p; p += c.hidden;
         a.attn_out = p; p += c.hidden;
+        a.hidden_alt = p; p += c.hidden;
         a.q = p; p += qd;
         a.att = p; p += qd;
         a.k = p; p += kd;
@@ -978,8 +979,9 @@ pk_hip_status pk_hip_qwen3moe_create(pk_hip_ctx* ctx, const pk_hip_qwen3moe_conf
         if (exact) {
             if (max_experts > pk::kMaxExperts256 || c.top_k > pk::kMaxRefTopK)
                 throw Unsupported("reference-order MoE covers up to 256 experts and top-16");
-            if (!pk::ref_attention_supported(c.head_dim, c.kv_capacity) || c.hidden > pk::kMaxRefWidth)
-                throw Unsupported("reference-order attention covers head_dim 64/128/256");
+            if (!pk::ref_attention_supported(c.head_dim, c.kv_capacity) ||
+                c.hidden > pk::kMaxRefNormWidth)
+                throw Unsupported("reference-order kernels cover head_dim 64/128/256, hidden <= 4096");
             m->ref_scratch.ensure(pk::ref_scratch_floats(c.top_k, max_ffn, c.hidden));
             a.ref_scratch = m->ref_scratch.ptr;
             // prepare_qwen_rope (src/qwen3_moe_runner.cpp:141-155) with this host's libm,

@@ -207,17 +207,177 @@ __device__ float block_dot(const uint8_t* blk, const float* x) {
     return s;
 }
 
-// y[route][row] for rows of W (route: the expert ids[route] slice when ids
-// is set), x[route] staged in LDS -- or, with x_up, the SwiGLU activation
-// g / (1 + expf(-g)) * u of x[route] and x_up[route] (src/qwen3_moe_runner.cpp:
-// 682-684).  Lanes (row, block); one lane per row then sums the block dots in
+// ---------------------------------------------------------------------------
+// Prologues shared by the matvec kernels (whole workgroup of NT threads).
+
+// v = x + residual (route-order combine from 0, or delta) for the n values,
+// eight per thread per batch with every load of a batch in flight together;
+// the serial FP32 sum of the squares; then xs = (v * scale) * w with
+// scale = 1 / sqrt(sum / n + eps) (rms_norm, src/rms_norm.cpp:9-27, and the
+// residual adds of src/qwen3_moe_runner.cpp:640,692).  The leader writes v
+// and xs to x_out / normed_out.  LDS: xs [n], sq [chain_floats(n)], wb [n].
+template <uint32_t NT>
+__device__ void ref_norm_stage(const RefNormIn& p, uint32_t n, float* xs, float* sq, float* wb,
+                               float& s_scale, bool leader) {
+    const uint32_t tid = threadIdx.x;
+    for (uint32_t base = 0; base < n; base += 8u * NT) {
+        uint32_t ic[8];
+        float v[8], wv[8];
+#pragma unroll
+        for (uint32_t k = 0; k < 8; ++k) {
+            const uint32_t i = base + tid + NT * k;
+            ic[k] = i < n ? i : 0u;
+            v[k] = p.x[ic[k]];
+            wv[k] = p.w[ic[k]];
+        }
+        if (p.res.parts) {
+            float yv[8];
+#pragma unroll
+            for (uint32_t k = 0; k < 8; ++k) yv[k] = 0.0f;
+            for (uint32_t r0 = 0; r0 < p.res.K; r0 += 8u) {
+                float pr[8], pv[8][8];
+#pragma unroll
+                for (uint32_t j = 0; j < 8; ++j) {
+                    const uint32_t rc = r0 + j < p.res.K ? r0 + j : 0u;
+                    pr[j] = p.res.probs[rc];
+#pragma unroll
+                    for (uint32_t k = 0; k < 8; ++k)
+                        pv[j][k] = p.res.parts[static_cast<uint64_t>(rc) * n + ic[k]];
+                }
+#pragma unroll
+                for (uint32_t j = 0; j < 8; ++j)
+                    if (r0 + j < p.res.K) {
+#pragma unroll
+                        for (uint32_t k = 0; k < 8; ++k) yv[k] = __fadd_rn(yv[k], __fmul_rn(pr[j], pv[j][k]));
+                    }
+            }
+#pragma unroll
+            for (uint32_t k = 0; k < 8; ++k) v[k] = __fadd_rn(v[k], yv[k]);
+        } else if (p.res.delta) {
+            float dv[8];
+#pragma unroll
+            for (uint32_t k = 0; k < 8; ++k) dv[k] = p.res.delta[ic[k]];
+#pragma unroll
+            for (uint32_t k = 0; k < 8; ++k) v[k] = __fadd_rn(v[k], dv[k]);
+        }
+#pragma unroll
+        for (uint32_t k = 0; k < 8; ++k) {
+            const uint32_t i = base + tid + NT * k;
+            if (i < n) {
+                xs[i] = v[k];
+                sq[i] = __fmul_rn(v[k], v[k]);
+                wb[i] = wv[k];
+            }
+        }
+    }
+    __syncthreads();
+    if (tid == 0) s_scale = 1.0f / sqrtf(serial_sum(sq, n, 0.0f) / static_cast<float>(n) + p.eps);
+    __syncthreads();
+    const float scale = s_scale;
+    for (uint32_t i = tid; i < n; i += NT) {
+        const float vi = xs[i], o = __fmul_rn(__fmul_rn(vi, scale), wb[i]);
+        if (leader) {
+            if (p.x_out) p.x_out[i] = vi;
+            if (p.normed_out) p.normed_out[i] = o;
+        }
+        xs[i] = o;
+    }
+    __syncthreads();
+}
+
+struct RouteShared {
+    float lg[kMaxExperts256];
+    double ex[kMaxExperts256];
+    float wmax[4];
+    uint32_t sel[kMaxRefTopK];
+    float pr[kMaxRefTopK];
+    double den;
+};
+
+// route_experts (src/qwen3_moe_runner.cpp:267-305) over the serial FP32
+// logits, one thread per expert (256 threads, E <= 256): the route order is
+// each expert's rank under (logit desc, id asc) -- the order the reference's
+// stable insertion produces.  Returns the expert of `route`.  The leader also
+// forms the FP64 exponentials' sum in expert order, the FP32 probabilities and
+// the FP32 renormalisation, and writes ids and probs.  Non-finite logits: the
+// leader flags the status word and every workgroup uses expert 0 (its reads
+// stay in bounds; the result is reported as an error).
+__device__ uint32_t ref_route_block(const RefRouteIn& R, uint32_t route, bool leader,
+                                    RouteShared& sh) {
+    const uint32_t t = threadIdx.x, E = R.n_experts, K = R.top_k;
+    const bool on = t < E;
+    const float l = on ? R.logits[t] : -INFINITY;
+    sh.lg[t] = l;  // -inf past E: never ranks before a finite logit
+    if (__syncthreads_or(on && !isfinite(l))) {
+        if (leader) {
+            if (t < K) {
+                R.ids[t] = 0u;
+                R.probs[t] = 0.0f;
+            }
+            if (t == 0) atomicOr(R.status, 1u);
+        }
+        return 0u;
+    }
+    // the maximum (its value does not depend on the order it is found in)
+    float m = l;
+    for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+    if ((t & 63u) == 0u) sh.wmax[t >> 6] = m;
+    uint32_t rank = 0;
+    if (on) {
+        const uint32_t E4 = (E + 3u) / 4u;
+        for (uint32_t j4 = 0; j4 < E4; ++j4) {
+            const f32x4 q = reinterpret_cast<const f32x4*>(sh.lg)[j4];
+            const uint32_t j = 4u * j4;
+            rank += (q.x > l || (q.x == l && j < t)) ? 1u : 0u;
+            rank += (q.y > l || (q.y == l && j + 1u < t)) ? 1u : 0u;
+            rank += (q.z > l || (q.z == l && j + 2u < t)) ? 1u : 0u;
+            rank += (q.w > l || (q.w == l && j + 3u < t)) ? 1u : 0u;
+        }
+        if (rank < K) sh.sel[rank] = t;
+    }
+    __syncthreads();
+    if (leader) {  // uniform across the workgroup
+        const float mx = fmaxf(fmaxf(sh.wmax[0], sh.wmax[1]), fmaxf(sh.wmax[2], sh.wmax[3]));
+        const double e = on ? exp(static_cast<double>(__fsub_rn(l, mx))) : 0.0;
+        if (on) sh.ex[t] = e;
+        __syncthreads();
+        if (t == 0) {
+            double den = 0.0;
+            for (uint32_t i = 0; i < E; ++i) den += sh.ex[i];
+            sh.den = den;
+        }
+        __syncthreads();
+        if (on && rank < K) sh.pr[rank] = static_cast<float>(e / sh.den);
+        __syncthreads();
+        if (t == 0) {
+            float sum = 0.0f;
+            for (uint32_t r = 0; r < K; ++r) sum = __fadd_rn(sum, sh.pr[r]);
+            for (uint32_t r = 0; r < K; ++r) {
+                R.ids[r] = sh.sel[r];
+                R.probs[r] = R.normalize ? __fdiv_rn(sh.pr[r], sum) : sh.pr[r];
+            }
+        }
+    }
+    return sh.sel[route];
+}
+
+// ---------------------------------------------------------------------------
+// y[route][row] for rows of W (route: the expert slice ids[route], or the one
+// routing selects), x[route] staged in LDS -- or, with x_up, the SwiGLU
+// activation g / (1 + expf(-g)) * u of x[route] and x_up[route]
+// (src/qwen3_moe_runner.cpp:682-684), or, with a norm, RMSNorm of the residual
+// stream.  Lanes (row, block); one lane per row then sums the block dots in
 // block order starting from 0.  With segments, workgroups along x are split
 // between up to three matrices that share the input.
 template <int T>
 __global__ __launch_bounds__(256) void k_ref_matvec(RefMatvecArgs a) {
-    extern __shared__ __attribute__((aligned(64))) float lds[];  // x [in], then block dots [256]
+    // xs [in], part [256]; with a norm also sq [chain_floats(in)], wb [in]
+    extern __shared__ __attribute__((aligned(64))) float lds[];
+    __shared__ RouteShared rsh;
+    __shared__ float s_scale;
     constexpr uint32_t BE = RefBlock<T>::BE, BB = RefBlock<T>::BB;
     const uint32_t r = blockIdx.y, tid = threadIdx.x;
+    const bool leader = blockIdx.x == 0 && blockIdx.y == 0;
     const uint32_t nb = a.in / BE, rpw = 256u / nb;
     const uint8_t* W = a.W;
     uint64_t row_bytes = a.row_bytes, slice_bytes = a.slice_bytes;
@@ -236,12 +396,17 @@ __global__ __launch_bounds__(256) void k_ref_matvec(RefMatvecArgs a) {
             }
         }
     }
-    const float* x = a.x + static_cast<uint64_t>(r) * a.x_stride;
     float* xs = lds;
     float* part = lds + a.in;
-    // staging: every load of a batch is issued before any is used
+    uint64_t expert = 0;
+    if (a.route.logits) expert = ref_route_block(a.route, r, leader, rsh);
+    else if (a.ids) expert = a.ids[r];
+    const float* x = a.x + static_cast<uint64_t>(r) * a.x_stride;
     const uint32_t n4 = a.in / 4u;  // in is a multiple of 32
-    if (a.x_up) {
+    if (a.norm.w) {
+        ref_norm_stage<256>(a.norm, a.in, xs, part + 256, part + 256 + chain_floats(a.in), s_scale,
+                            leader);
+    } else if (a.x_up) {
         const f32x4* g4 = reinterpret_cast<const f32x4*>(x);
         const f32x4* u4 = reinterpret_cast<const f32x4*>(a.x_up + static_cast<uint64_t>(r) * a.x_stride);
         for (uint32_t base = 0; base < n4; base += 256u) {
@@ -264,7 +429,7 @@ __global__ __launch_bounds__(256) void k_ref_matvec(RefMatvecArgs a) {
         }
     }
     __syncthreads();
-    if (a.ids) W += static_cast<uint64_t>(a.ids[r]) * slice_bytes;
+    W += expert * slice_bytes;
     const uint32_t row0 = bx * rpw, lr = tid / nb, b = tid % nb, row = row0 + lr;
     if (lr < rpw && row < rows)
         part[tid] = block_dot<T>(W + static_cast<uint64_t>(row) * row_bytes + b * BB, xs + b * BE);
@@ -276,56 +441,50 @@ __global__ __launch_bounds__(256) void k_ref_matvec(RefMatvecArgs a) {
     }
 }
 
-// F32 linear: 0 + dot_f32(w_row, x).  One wave per row: the products are
-// formed in parallel from coalesced loads (eight 16-byte loads per lane in
-// flight), then lane 0 adds them in order.
-__global__ __launch_bounds__(64) void k_ref_linear_f32(RefMatvecArgs a) {
-    extern __shared__ __attribute__((aligned(64))) float prod[];  // [chain_floats(in)]
-    const uint32_t row = blockIdx.x, r = blockIdx.y, lane = threadIdx.x;
-    const float* x = a.x + static_cast<uint64_t>(r) * a.x_stride;
-    const float* w = reinterpret_cast<const float*>(a.W + static_cast<uint64_t>(row) * a.row_bytes);
-    if ((a.in & 3u) == 0u) {
-        const uint32_t n4 = a.in / 4u;
-        const f32x4* w4 = reinterpret_cast<const f32x4*>(w);
-        const f32x4* x4 = reinterpret_cast<const f32x4*>(x);
-        f32x4* p4 = reinterpret_cast<f32x4*>(prod);
-        for (uint32_t base = 0; base < n4; base += 512u) {
-            f32x4 wv[8], xv[8];
-#pragma unroll
-            for (uint32_t k = 0; k < 8; ++k) {
-                const uint32_t i = base + lane + 64u * k, ic = i < n4 ? i : 0u;
-                wv[k] = w4[ic];
-                xv[k] = x4[ic];
-            }
-#pragma unroll
-            for (uint32_t k = 0; k < 8; ++k) {
-                const uint32_t i = base + lane + 64u * k;
-                if (i < n4) {
-                    f32x4 pv;
-                    pv.x = __fmul_rn(wv[k].x, xv[k].x);
-                    pv.y = __fmul_rn(wv[k].y, xv[k].y);
-                    pv.z = __fmul_rn(wv[k].z, xv[k].z);
-                    pv.w = __fmul_rn(wv[k].w, xv[k].w);
-                    p4[i] = pv;
-                }
-            }
-        }
+// F32 linear: 0 + dot_f32(w_row, x), one 256-thread workgroup per row: x (or
+// RMSNorm of the residual stream) staged in LDS, the products formed in
+// parallel from coalesced loads, then one lane adds them in order.
+__global__ __launch_bounds__(256) void k_ref_linear_f32(RefMatvecArgs a) {
+    // prod [chain_floats(in)], xs [in]; with a norm also sq [chain_floats(in)], wb [in]
+    extern __shared__ __attribute__((aligned(64))) float lds[];
+    __shared__ float s_scale;
+    const uint32_t row = blockIdx.x, r = blockIdx.y, tid = threadIdx.x;
+    const bool leader = blockIdx.x == 0 && blockIdx.y == 0;
+    const uint32_t cf = chain_floats(a.in);
+    float* prod = lds;
+    float* xs = lds + cf;
+    if (a.norm.w) {
+        ref_norm_stage<256>(a.norm, a.in, xs, xs + a.in, xs + a.in + cf, s_scale, leader);
     } else {
-        for (uint32_t i = lane; i < a.in; i += 64u) prod[i] = __fmul_rn(w[i], x[i]);
+        const float* x = a.x + static_cast<uint64_t>(r) * a.x_stride;
+        for (uint32_t i = tid; i < a.in; i += 256u) xs[i] = x[i];
+        __syncthreads();
+    }
+    const float* w = reinterpret_cast<const float*>(a.W + static_cast<uint64_t>(row) * a.row_bytes);
+    for (uint32_t base = 0; base < a.in; base += 2048u) {
+        float wv[8];
+#pragma unroll
+        for (uint32_t k = 0; k < 8; ++k) {
+            const uint32_t i = base + tid + 256u * k;
+            wv[k] = w[i < a.in ? i : 0u];
+        }
+#pragma unroll
+        for (uint32_t k = 0; k < 8; ++k) {
+            const uint32_t i = base + tid + 256u * k;
+            if (i < a.in) prod[i] = __fmul_rn(wv[k], xs[i]);
+        }
     }
     __syncthreads();
-    if (lane == 0)
+    if (tid == 0)
         a.y[static_cast<uint64_t>(r) * a.y_stride + row] = __fadd_rn(0.0f, serial_sum(prod, a.in, 0.0f));
 }
 
-// x += the residual (delta, or sum_r p_r * parts_r added in route order from
-// 0, as the MoE block's moe_result, src/qwen3_moe_runner.cpp:688-692); then
-// out = (x * scale) * w with scale = 1 / sqrt(sum_sq / n + eps) and sum_sq the
-// serial FP32 sum of the rounded squares (rms_norm, src/rms_norm.cpp:9-27).
+// Standalone RMSNorm (the output norm): x += the residual; out = (x * scale) * w.
 // One 1024-thread workgroup per row of n <= 1024 * PER values; every load is
 // issued before any is used, and the values stay in registers across the sum.
 template <int PER>
 __global__ __launch_bounds__(1024) void k_ref_rmsnorm(float* x, RefResidual res, const float* w,
+
                                                       float* out, uint32_t n, float eps) {
     extern __shared__ __attribute__((aligned(64))) float sq[];  // [chain_floats(n)]
     __shared__ float s_scale;
@@ -392,90 +551,105 @@ __global__ __launch_bounds__(1024) void k_ref_rmsnorm(float* x, RefResidual res,
     }
 }
 
-// Per-head q/k RMSNorm (serial) and RoPE from the host-computed table, k and
-// v to the FP16 ring: q heads, then k heads, then v heads.
-__global__ __launch_bounds__(128) void k_ref_qk_rope_kv(ModelArgs a, ModelLayer L) {
-    __shared__ float vals[256];
-    __shared__ float s_scale;
-    const uint32_t h = blockIdx.x, d = threadIdx.x, hd = a.head_dim, half = hd / 2u;
-    const uint32_t pos = a.state[0], slot = pos % a.capacity;
-    if (h >= a.heads + a.kv_heads) {
-        const uint32_t j = h - a.heads - a.kv_heads;
-        L.vcache[(static_cast<uint64_t>(slot) * a.kv_heads + j) * hd + d] =
-            __half_as_ushort(__float2half_rn(a.v[j * hd + d]));
-        return;
-    }
-    const bool is_q = h < a.heads;
-    float* src = is_q ? a.q + h * hd : a.k + (h - a.heads) * hd;
-    const float* nw = is_q ? L.q_norm : L.k_norm;
-    const float x = src[d];
-    vals[d] = __fmul_rn(x, x);
-    __syncthreads();
-    if (d == 0) {
-        float s = 0.0f;
-        for (uint32_t i = 0; i < hd; ++i) s = __fadd_rn(s, vals[i]);
-        s_scale = 1.0f / sqrtf(s / static_cast<float>(hd) + a.rms_eps);
-    }
-    __syncthreads();
-    const float nv = __fmul_rn(__fmul_rn(x, s_scale), nw[d]);
-    __syncthreads();
-    vals[d] = nv;
-    __syncthreads();
-    const float* cs = a.rope_table + static_cast<uint64_t>(pos) * hd;  // cos [half], sin [half]
-    float r;
-    if (d < half) {
-        r = __fsub_rn(__fmul_rn(vals[d], cs[d]), __fmul_rn(vals[d + half], cs[half + d]));
-    } else {
-        const uint32_t i = d - half;
-        r = __fadd_rn(__fmul_rn(vals[d], cs[i]), __fmul_rn(vals[i], cs[half + i]));
-    }
-    if (is_q) {
-        src[d] = r;
-    } else {
-        L.kcache[(static_cast<uint64_t>(slot) * a.kv_heads + (h - a.heads)) * hd + d] =
-            __half_as_ushort(__float2half_rn(r));
-    }
-}
-
 // Attention of one q head over its KV window, in position order
-// (KvCache::attend, src/kv_cache.cpp:185-293): score_i = (serial dot of q
-// and k_i) * scale; the maximum; p_i = expf(score_i - max); the serial
-// denominator; out[d] = ((0 + (p_0 / den) v_0[d]) + (p_1 / den) v_1[d]) + ...
-// Each position's FP16 K row is loaded whole (HD / 8 16-byte loads), V rows
-// are staged through LDS a tile of positions at a time.
+// (KvCache::attend, src/kv_cache.cpp:185-293), with the step's own q/k/v
+// work in front of it (src/qwen3_moe_runner.cpp:600-640): RMSNorm of the q
+// head and of its kv head's k (serial sums, head-norm weights), RoPE from the
+// host-computed table (cos, then sin, per position), k and v rounded to FP16
+// as the ring stores them (the first q head of each group writes them).  Then
+// score_i = (serial dot of q and k_i) * scale; the maximum;
+// p_i = expf(score_i - max); the serial denominator;
+// out[d] = ((0 + (p_0 / den) v_0[d]) + (p_1 / den) v_1[d]) + ...  The
+// current position's k and v come from LDS, older ones from the ring: each
+// FP16 K row loaded whole (HD / 8 16-byte loads), V rows staged through LDS a
+// tile of positions at a time.
 constexpr uint32_t kAttnTileBytes = 64u * 1024u;
 template <int HD>
 __global__ __launch_bounds__(256) void k_ref_attention(ModelArgs a, ModelLayer L) {
     extern __shared__ __attribute__((aligned(64))) float lds[];  // sc [chain_floats(capacity)], V tile
-    __shared__ float qv[HD];
+    __shared__ float qv[HD], kcur[HD], sqq[HD], sqk[HD];
+    __shared__ __attribute__((aligned(16))) uint16_t vcur[HD];
     __shared__ float red[4];
-    __shared__ float s_den;
-    constexpr uint32_t TILE = kAttnTileBytes / (2u * HD);
+    __shared__ float s_den, s_qscale, s_kscale;
+    constexpr uint32_t TILE = kAttnTileBytes / (2u * HD), HALF = HD / 2u;
     const uint32_t h = blockIdx.x, tid = threadIdx.x;
-    const uint32_t kvh = h / (a.heads / a.kv_heads);
-    const uint32_t pos = a.state[0];
+    const uint32_t group = a.heads / a.kv_heads, kvh = h / group;
+    const uint32_t pos = a.state[0], slot_now = pos % a.capacity;
     const uint32_t n = pos + 1u < a.capacity ? pos + 1u : a.capacity;
     const uint32_t first = pos + 1u - n;
+    const uint64_t row_halves = static_cast<uint64_t>(a.kv_heads) * HD;
     float* sc = lds;
     uint16_t* vt = reinterpret_cast<uint16_t*>(lds + chain_floats(a.capacity));
-    for (uint32_t d = tid; d < HD; d += 256u) qv[d] = a.q[h * HD + d];
+    // q / k head norms and RoPE, v to FP16
+    float qx = 0.0f, kx = 0.0f, vx = 0.0f, qw = 0.0f, kw = 0.0f, c0 = 0.0f, s0 = 0.0f;
+    const uint32_t d = tid < HD ? tid : 0u, dp = d % HALF;
+    const float* cs = a.rope_table + static_cast<uint64_t>(pos) * HD;  // cos [HALF], sin [HALF]
+    qx = a.q[h * HD + d];
+    kx = a.k[kvh * HD + d];
+    vx = a.v[kvh * HD + d];
+    qw = L.q_norm[d];
+    kw = L.k_norm[d];
+    c0 = cs[dp];
+    s0 = cs[HALF + dp];
+    if (tid < HD) {
+        sqq[tid] = __fmul_rn(qx, qx);
+        sqk[tid] = __fmul_rn(kx, kx);
+    }
     __syncthreads();
-    const uint64_t row_halves = static_cast<uint64_t>(a.kv_heads) * HD;
+    if (tid == 0) {
+        float sum = 0.0f;
+        for (uint32_t i = 0; i < HD; ++i) sum = __fadd_rn(sum, sqq[i]);
+        s_qscale = 1.0f / sqrtf(sum / static_cast<float>(HD) + a.rms_eps);
+    } else if (tid == 64) {
+        float sum = 0.0f;
+        for (uint32_t i = 0; i < HD; ++i) sum = __fadd_rn(sum, sqk[i]);
+        s_kscale = 1.0f / sqrtf(sum / static_cast<float>(HD) + a.rms_eps);
+    }
+    __syncthreads();
+    if (tid < HD) {  // normed values (the squares are no longer needed)
+        sqq[tid] = __fmul_rn(__fmul_rn(qx, s_qscale), qw);
+        sqk[tid] = __fmul_rn(__fmul_rn(kx, s_kscale), kw);
+    }
+    __syncthreads();
+    if (tid < HD) {
+        float rq, rk;
+        if (tid < HALF) {
+            rq = __fsub_rn(__fmul_rn(sqq[tid], c0), __fmul_rn(sqq[tid + HALF], s0));
+            rk = __fsub_rn(__fmul_rn(sqk[tid], c0), __fmul_rn(sqk[tid + HALF], s0));
+        } else {
+            rq = __fadd_rn(__fmul_rn(sqq[tid], c0), __fmul_rn(sqq[dp], s0));
+            rk = __fadd_rn(__fmul_rn(sqk[tid], c0), __fmul_rn(sqk[dp], s0));
+        }
+        const uint16_t kb = __half_as_ushort(__float2half_rn(rk));
+        const uint16_t vb = __half_as_ushort(__float2half_rn(vx));
+        qv[tid] = rq;
+        kcur[tid] = __half2float(__ushort_as_half(kb));
+        vcur[tid] = vb;
+        if (h % group == 0u) {
+            L.kcache[static_cast<uint64_t>(slot_now) * row_halves + kvh * HD + tid] = kb;
+            L.vcache[static_cast<uint64_t>(slot_now) * row_halves + kvh * HD + tid] = vb;
+        }
+    }
+    __syncthreads();
     float m = -INFINITY;
     for (uint32_t i = tid; i < n; i += 256u) {
-        const uint32_t slot = (first + i) % a.capacity;
-        const u32x4_t* kr = reinterpret_cast<const u32x4_t*>(L.kcache + slot * row_halves + kvh * HD);
-        u32x4_t kw[HD / 8];
-#pragma unroll
-        for (int j = 0; j < HD / 8; ++j) kw[j] = kr[j];
         float s = 0.0f;
+        if (i + 1u == n) {  // the current position
+            for (uint32_t e = 0; e < HD; ++e) s = __fadd_rn(s, __fmul_rn(qv[e], kcur[e]));
+        } else {
+            const uint32_t slot = (first + i) % a.capacity;
+            const u32x4_t* kr = reinterpret_cast<const u32x4_t*>(L.kcache + slot * row_halves + kvh * HD);
+            u32x4_t kwv[HD / 8];
 #pragma unroll
-        for (int j = 0; j < HD / 8; ++j) {
-            const uint32_t w4[4] = {kw[j].x, kw[j].y, kw[j].z, kw[j].w};
+            for (int j = 0; j < HD / 8; ++j) kwv[j] = kr[j];
 #pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                const uint16_t bits = static_cast<uint16_t>(w4[e / 2] >> (16 * (e % 2)));
-                s = __fadd_rn(s, __fmul_rn(qv[8 * j + e], __half2float(__ushort_as_half(bits))));
+            for (int j = 0; j < HD / 8; ++j) {
+                const uint32_t w4[4] = {kwv[j].x, kwv[j].y, kwv[j].z, kwv[j].w};
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const uint16_t bits = static_cast<uint16_t>(w4[e / 2] >> (16 * (e % 2)));
+                    s = __fadd_rn(s, __fmul_rn(qv[8 * j + e], __half2float(__ushort_as_half(bits))));
+                }
             }
         }
         s = __fmul_rn(s, a.attn_scale);
@@ -504,8 +678,13 @@ __global__ __launch_bounds__(256) void k_ref_attention(ModelArgs a, ModelLayer L
 #pragma unroll
             for (int k = 0; k < 4; ++k) {
                 const uint32_t q = base + tid + 256u * k, qc = q < tn * PPR ? q : 0u;
-                const uint32_t slot = (first + t0 + qc / PPR) % a.capacity;
-                pv[k] = reinterpret_cast<const u32x4_t*>(L.vcache + slot * row_halves + kvh * HD)[qc % PPR];
+                const uint32_t i = t0 + qc / PPR;
+                if (i + 1u == n) {
+                    pv[k] = reinterpret_cast<const u32x4_t*>(vcur)[qc % PPR];
+                } else {
+                    const uint32_t slot = (first + i) % a.capacity;
+                    pv[k] = reinterpret_cast<const u32x4_t*>(L.vcache + slot * row_halves + kvh * HD)[qc % PPR];
+                }
             }
 #pragma unroll
             for (int k = 0; k < 4; ++k) {
@@ -524,79 +703,14 @@ __global__ __launch_bounds__(256) void k_ref_attention(ModelArgs a, ModelLayer L
     if (tid < HD) a.att[h * HD + tid] = o;
 }
 
-// route_experts over the serial FP32 logits, one thread per expert: the
-// FP64 exponentials in parallel, their sum in expert order by one lane, the
-// route order as each expert's rank under (logit desc, id asc) -- the order
-// the reference's stable insertion produces -- then FP32 probabilities and
-// the FP32 renormalisation.  Non-finite logits flag the status word.
-__global__ __launch_bounds__(256) void k_ref_routes(const float* logits, uint32_t E, uint32_t K,
-                                                    uint32_t normalize, uint32_t* ids,
-                                                    float* probs, uint32_t* status) {
-    __shared__ __attribute__((aligned(16))) float lg[kMaxExperts256];
-    __shared__ __attribute__((aligned(16))) double ex[kMaxExperts256];
-    __shared__ float wmax[4];
-    __shared__ uint32_t sel[kMaxRefTopK];
-    __shared__ float pr[kMaxRefTopK];
-    __shared__ double s_den;
-    const uint32_t t = threadIdx.x;
-    const bool on = t < E;
-    const float l = on ? logits[t] : -INFINITY;
-    lg[t] = l;  // -inf past E: never ranks before a finite logit
-    if (__syncthreads_or(on && !isfinite(l))) {
-        if (t < K) {
-            ids[t] = 0u;  // keep the expert reads in bounds; the error is reported
-            probs[t] = 0.0f;
-        }
-        if (t == 0) atomicOr(status, 1u);
-        return;
-    }
-    // the maximum (its value does not depend on the order it is found in)
-    float m = l;
-    for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
-    if ((t & 63u) == 0u) wmax[t >> 6] = m;
-    __syncthreads();
-    const float mx = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
-    const double e = on ? exp(static_cast<double>(__fsub_rn(l, mx))) : 0.0;
-    if (on) ex[t] = e;
-    uint32_t rank = 0;
-    if (on) {
-        const uint32_t E4 = (E + 3u) / 4u;  // lg is padded with -inf to a multiple of 4
-        for (uint32_t j4 = 0; j4 < E4; ++j4) {
-            const f32x4 q = reinterpret_cast<const f32x4*>(lg)[j4];
-            const uint32_t j = 4u * j4;
-            rank += (q.x > l || (q.x == l && j < t)) ? 1u : 0u;
-            rank += (q.y > l || (q.y == l && j + 1u < t)) ? 1u : 0u;
-            rank += (q.z > l || (q.z == l && j + 2u < t)) ? 1u : 0u;
-            rank += (q.w > l || (q.w == l && j + 3u < t)) ? 1u : 0u;
-        }
-        if (rank < K) sel[rank] = t;
-    }
-    __syncthreads();
-    if (t == 0) {
-        double den = 0.0;
-        for (uint32_t i = 0; i < E; ++i) den += ex[i];
-        s_den = den;
-    }
-    __syncthreads();
-    if (on && rank < K) pr[rank] = static_cast<float>(e / s_den);
-    __syncthreads();
-    if (t == 0) {
-        float sum = 0.0f;
-        for (uint32_t r = 0; r < K; ++r) sum = __fadd_rn(sum, pr[r]);
-        for (uint32_t r = 0; r < K; ++r) {
-            ids[r] = sel[r];
-            probs[r] = normalize ? __fdiv_rn(pr[r], sum) : pr[r];
-        }
-    }
-}
-
 uint32_t ref_block_elems(uint32_t type) {
     return type == T_Q8_0 || type == T_Q4_0 ? 32u : 256u;
 }
 
 template <int T>
 hipError_t ref_matvec_t(const RefMatvecArgs& a, uint32_t blocks, uint32_t routes, hipStream_t s) {
-    const size_t lds = (a.in + 256u) * sizeof(float);
+    size_t lds = (a.in + 256u) * sizeof(float);
+    if (a.norm.w) lds += (chain_floats(a.in) + a.in) * sizeof(float);
     hipLaunchKernelGGL(k_ref_matvec<T>, dim3(blocks, routes), dim3(256), lds, s, a);
     return hipGetLastError();
 }
@@ -625,10 +739,24 @@ bool ref_matvec_supported(uint32_t type, uint32_t in) {
     }
 }
 
+// Prologue limits: a fused norm covers one residual row of up to
+// kMaxRefNormWidth values, routing up to 256 experts and top-16.
+bool ref_prologue_ok(const RefMatvecArgs& a, uint32_t routes) {
+    if (a.norm.w && (a.in > kMaxRefNormWidth || a.norm.res.K > kMaxRefTopK || routes != 1u))
+        return false;
+    if (a.route.logits &&
+        (a.route.n_experts > kMaxExperts256 || a.route.top_k > kMaxRefTopK || routes > a.route.top_k))
+        return false;
+    return true;
+}
+
 hipError_t launch_ref_matvec(uint32_t type, const RefMatvecArgs& a, uint32_t routes, hipStream_t s) {
+    if (!ref_prologue_ok(a, routes)) return hipErrorInvalidValue;
     if (type == T_F32) {
-        hipLaunchKernelGGL(k_ref_linear_f32, dim3(a.rows, routes), dim3(64),
-                           chain_floats(a.in) * sizeof(float), s, a);
+        if (a.route.logits || a.x_up || a.nseg) return hipErrorInvalidValue;
+        size_t lds = (chain_floats(a.in) + a.in) * sizeof(float);
+        if (a.norm.w) lds += (chain_floats(a.in) + a.in) * sizeof(float);
+        hipLaunchKernelGGL(k_ref_linear_f32, dim3(a.rows, routes), dim3(256), lds, s, a);
         return hipGetLastError();
     }
     if (a.nseg) return hipErrorInvalidValue;
@@ -638,7 +766,8 @@ hipError_t launch_ref_matvec(uint32_t type, const RefMatvecArgs& a, uint32_t rou
 
 hipError_t launch_ref_matvec_multi(uint32_t type, RefMatvecArgs a, const RefSeg* segs, uint32_t n,
                                    uint32_t routes, hipStream_t s) {
-    if (type == T_F32 || n == 0 || n > kMaxRefSegs) return hipErrorInvalidValue;
+    if (type == T_F32 || n == 0 || n > kMaxRefSegs || !ref_prologue_ok(a, routes))
+        return hipErrorInvalidValue;
     const uint32_t rpw = 256u / (a.in / ref_block_elems(type));
     uint32_t blocks = 0;
     a.nseg = n;
@@ -663,37 +792,36 @@ hipError_t launch_ref_rmsnorm(float* x, const RefResidual& res, const float* w, 
 
 bool ref_attention_supported(uint32_t head_dim, uint32_t capacity) {
     return (head_dim == 64u || head_dim == 128u || head_dim == 256u) &&
-           (chain_floats(capacity) * 4ull + kAttnTileBytes) <= 160ull * 1024u - 2048u;
+           (chain_floats(capacity) * 4ull + kAttnTileBytes) <= 160ull * 1024u - 8192u;
 }
 
+// Six launches per layer; the residual stream alternates between
+// hidden_state and hidden_alt so no workgroup reads a row another one of the
+// same launch overwrites.
 hipError_t launch_ref_step(const ModelArgs& a, const ModelLayer* layers, bool logits, hipStream_t s) {
     const uint32_t qd = a.heads * a.head_dim, kd = a.kv_heads * a.head_dim;
     RefResidual res{};  // what the next RMSNorm adds to the residual stream first
     hipError_t err = hipSuccess;
+    const size_t attn_lds = chain_floats(a.capacity) * sizeof(float) + kAttnTileBytes;
     for (uint32_t l = 0; l < a.layers; ++l) {
         const ModelLayer& L = layers[l];
         const MoeDecodeArgs& m = L.moe;
-        if ((err = launch_ref_rmsnorm(a.hidden_state, res, L.attn_norm, a.normed, a.hidden, 1,
-                                      a.rms_eps, s)))
-            return err;
+        // 1. attention RMSNorm (hidden_state + residual -> hidden_alt) and q/k/v
         RefMatvecArgs qkv{};
         qkv.in = a.hidden;
-        qkv.x = a.normed;
+        qkv.norm = RefNormIn{a.hidden_state, res, L.attn_norm, a.hidden_alt, nullptr, a.rms_eps};
         const RefSeg qkv_segs[3] = {{L.q, L.q_row, 0, qd, 0, a.q},
                                     {L.k, L.k_row, 0, kd, 0, a.k},
                                     {L.v, L.v_row, 0, kd, 0, a.v}};
         if ((err = launch_ref_matvec_multi(L.attn_type, qkv, qkv_segs, 3, 1, s))) return err;
-        hipLaunchKernelGGL(k_ref_qk_rope_kv, dim3(a.heads + 2u * a.kv_heads), dim3(a.head_dim), 0,
-                           s, a, L);
-        {
-            const size_t lds = chain_floats(a.capacity) * sizeof(float) + kAttnTileBytes;
-            switch (a.head_dim) {
-                case 64: hipLaunchKernelGGL(k_ref_attention<64>, dim3(a.heads), dim3(256), lds, s, a, L); break;
-                case 128: hipLaunchKernelGGL(k_ref_attention<128>, dim3(a.heads), dim3(256), lds, s, a, L); break;
-                case 256: hipLaunchKernelGGL(k_ref_attention<256>, dim3(a.heads), dim3(256), lds, s, a, L); break;
-                default: return hipErrorInvalidValue;
-            }
+        // 2. q/k norms, RoPE, KV ring, attention
+        switch (a.head_dim) {
+            case 64: hipLaunchKernelGGL(k_ref_attention<64>, dim3(a.heads), dim3(256), attn_lds, s, a, L); break;
+            case 128: hipLaunchKernelGGL(k_ref_attention<128>, dim3(a.heads), dim3(256), attn_lds, s, a, L); break;
+            case 256: hipLaunchKernelGGL(k_ref_attention<256>, dim3(a.heads), dim3(256), attn_lds, s, a, L); break;
+            default: return hipErrorInvalidValue;
         }
+        // 3. output projection
         RefMatvecArgs o{};
         o.W = L.o;
         o.row_bytes = L.o_row;
@@ -702,11 +830,7 @@ hipError_t launch_ref_step(const ModelArgs& a, const ModelLayer* layers, bool lo
         o.x = a.att;
         o.y = a.attn_out;
         if ((err = launch_ref_matvec(L.attn_type, o, 1, s))) return err;
-        res = RefResidual{a.attn_out, nullptr, nullptr, 0};
-        if ((err = launch_ref_rmsnorm(a.hidden_state, res, L.ffn_norm, a.normed, a.hidden, 1,
-                                      a.rms_eps, s)))
-            return err;
-        // MoE block: router logits, routes, gate/up of every route, SwiGLU + down
+        // 4. FFN RMSNorm (hidden_alt + attn_out -> hidden_state, normed) and router logits
         float* rl = a.ref_scratch;
         float* g = rl + kMaxExperts256;
         float* u = g + static_cast<uint64_t>(m.top_k) * m.ffn;
@@ -716,24 +840,27 @@ hipError_t launch_ref_step(const ModelArgs& a, const ModelLayer* layers, bool lo
         router.row_bytes = static_cast<uint64_t>(m.hidden) * 4u;
         router.rows = m.n_experts;
         router.in = m.hidden;
-        router.x = a.normed;
+        router.norm = RefNormIn{a.hidden_alt, RefResidual{a.attn_out, nullptr, nullptr, 0},
+                                L.ffn_norm, a.hidden_state, a.normed, a.rms_eps};
         router.y = rl;
         if ((err = launch_ref_matvec(T_F32, router, 1, s))) return err;
-        hipLaunchKernelGGL(k_ref_routes, dim3(1), dim3(256), 0, s, rl, m.n_experts, m.top_k,
-                           m.normalize, m.ids, m.probs, m.status);
+        // 5. routing and gate/up of every route
         RefMatvecArgs gu{};
-        gu.ids = m.ids;
         gu.in = m.hidden;
         gu.x = a.normed;
         gu.y_stride = m.ffn;
+        gu.route = RefRouteIn{rl, m.n_experts, m.top_k, m.normalize, m.ids, m.probs, m.status};
         const RefSeg gu_segs[2] = {{m.gate, m.gate_row, m.gate_slice, m.ffn, 0, g},
                                    {m.up, m.up_row, m.up_slice, m.ffn, 0, u}};
         if (m.gate_type == m.up_type) {
             if ((err = launch_ref_matvec_multi(m.gate_type, gu, gu_segs, 2, m.top_k, s))) return err;
         } else {
             if ((err = launch_ref_matvec_multi(m.gate_type, gu, gu_segs, 1, m.top_k, s))) return err;
+            gu.route.logits = nullptr;  // the ids are written by now
+            gu.ids = m.ids;
             if ((err = launch_ref_matvec_multi(m.up_type, gu, gu_segs + 1, 1, m.top_k, s))) return err;
         }
+        // 6. SwiGLU staged in the down projection
         RefMatvecArgs d{};
         d.ids = m.ids;
         d.W = m.down;

@@ -132,6 +132,7 @@ struct ModelArgs {
     float* v;
     float* att;               // attention output [heads * head_dim]
     float* attn_out;          // [hidden]
+    float* hidden_alt;        // reference order: the residual stream's second buffer
     float* rope;              // cos [head_dim / 2], then sin
     float* logits;            // [vocab]
     // reference-order mode: every kernel repeats the CPU's operation order
@@ -155,6 +156,35 @@ hipError_t launch_synth_fill(uint8_t* dst, uint64_t nbytes, uint64_t key, uint32
 constexpr uint32_t kMaxRefWidth = 8192;
 constexpr uint32_t kMaxRefTopK = 16;
 constexpr uint32_t kMaxExperts256 = 256;
+// What an RMSNorm adds to the residual stream first: delta, or the
+// route-order combine of the MoE block's expert outputs.
+struct RefResidual {
+    const float* delta;       // [n], or null
+    const float* parts;       // [K][n] expert outputs, combined with probs in route order
+    const float* probs;
+    uint32_t K;
+};
+// An RMSNorm computed in a matvec's staging: every workgroup normalises
+// x + residual into its LDS; the leader workgroup (0, 0) also writes the
+// updated residual stream and/or the normed vector.
+struct RefNormIn {
+    const float* x;
+    RefResidual res;
+    const float* w;           // norm weights; null: no norm
+    float* x_out;
+    float* normed_out;
+    float eps;
+};
+// route_experts in a matvec's prologue: every workgroup ranks the logits for
+// its own route (blockIdx.y); the leader writes ids, probs and the status.
+struct RefRouteIn {
+    const float* logits;      // null: no routing (ids, if set, select the slices)
+    uint32_t n_experts, top_k, normalize;
+    uint32_t* ids;
+    float* probs;
+    uint32_t* status;
+};
+
 // Up to kMaxRefSegs matrices of one type and width in one launch: segment k
 // covers workgroups [seg[k].block0, seg[k + 1].block0) along x.
 constexpr uint32_t kMaxRefSegs = 3;
@@ -178,6 +208,8 @@ struct RefMatvecArgs {
     RefSeg seg[kMaxRefSegs];
     const float* x_up;        // non-null: stage g / (1 + expf(-g)) * u, g = x, u = x_up
     LibmExpf expf;
+    RefNormIn norm;           // norm.w set: x is RMSNorm(norm.x + norm.res) * norm.w
+    RefRouteIn route;         // route.logits set: the expert slices come from routing
 };
 bool ref_matvec_supported(uint32_t type, uint32_t in);
 hipError_t launch_ref_matvec(uint32_t type, const RefMatvecArgs& a, uint32_t routes,
@@ -185,17 +217,12 @@ hipError_t launch_ref_matvec(uint32_t type, const RefMatvecArgs& a, uint32_t rou
 // Several matrices sharing x (q/k/v; gate/up per route): one launch.
 hipError_t launch_ref_matvec_multi(uint32_t type, RefMatvecArgs a, const RefSeg* segs, uint32_t n,
                                    uint32_t routes, hipStream_t stream);
-// x += delta (or the route-order combine of parts, if set); out = RMSNorm(x) * w
-struct RefResidual {
-    const float* delta;       // [n], or null
-    const float* parts;       // [K][n] expert outputs, combined with probs in route order
-    const float* probs;
-    uint32_t K;
-};
 hipError_t launch_ref_rmsnorm(float* x, const RefResidual& res, const float* w, float* out,
                               uint32_t n, uint32_t rows, float eps, hipStream_t stream);
 // Head dims 64/128/256 and a KV window whose scores fit LDS beside a V tile.
 bool ref_attention_supported(uint32_t head_dim, uint32_t capacity);
+// Widths whose RMSNorm the matvec staging can carry.
+constexpr uint32_t kMaxRefNormWidth = 4096;
 // The reference-order token step after the embedding (all layers, then the
 // head when logits).
 hipError_t launch_ref_step(const ModelArgs& a, const ModelLayer* layers, bool logits,
