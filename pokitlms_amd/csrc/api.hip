@@ -946,7 +946,7 @@ pk_hip_status pk_hip_qwen3moe_create(pk_hip_ctx* ctx, const pk_hip_qwen3moe_conf
         // device state and activations
         m->state.ensure(4);
         m->tokens.ensure(1);
-        const uint64_t wf = 4ull * c.hidden + 2 * qd + 2 * kd + c.head_dim + c.vocab;
+        const uint64_t wf = 4ull * c.hidden + 2 * qd + 2 * kd + c.vocab + 2ull * (c.vocab / 2048 + 1);
         m->work.ensure(wf);
         float* p = m->work.ptr;
         a.hidden_state = p; p += c.hidden;
@@ -957,8 +957,8 @@ pk_hip_status pk_hip_qwen3moe_create(pk_hip_ctx* ctx, const pk_hip_qwen3moe_conf
         a.att = p; p += qd;
         a.k = p; p += kd;
         a.v = p; p += kd;
-        a.rope = p; p += c.head_dim;
-        a.logits = p;
+        a.logits = p; p += c.vocab;
+        a.argmax_part = p;
         a.state = m->state.ptr;
         m->kv.ensure(2ull * c.layers * c.kv_capacity * kd);
         uint32_t max_experts = 1, max_k = 1, max_ffn = 1;
@@ -976,32 +976,33 @@ pk_hip_status pk_hip_qwen3moe_create(pk_hip_ctx* ctx, const pk_hip_qwen3moe_conf
         m->row_sum.ensure(max_experts);
         m->row_bound.ensure(max_experts);
         m->moe_out.ensure(c.hidden);
+        if (!pk::ref_attention_supported(c.head_dim, c.kv_capacity))
+            throw Unsupported("attention covers head_dim 64/128/256");
+        // prepare_qwen_rope (src/qwen3_moe_runner.cpp:141-155) with this host's libm,
+        // for every position of the model context
+        const uint32_t half = c.head_dim / 2;
+        std::vector<float> table(uint64_t(c.context) * c.head_dim);
+        for (uint32_t pos = 0; pos < c.context; ++pos) {
+            float* row = table.data() + uint64_t(pos) * c.head_dim;
+            for (uint32_t p = 0; p < half; ++p) {
+                const float angle = static_cast<float>(pos) *
+                    std::pow(c.rope_theta, -static_cast<float>(p) / static_cast<float>(half));
+                row[p] = std::cos(angle);
+                row[half + p] = std::sin(angle);
+            }
+        }
+        m->rope_table.ensure(table.size());
+        check(hipMemcpy(m->rope_table.ptr, table.data(), table.size() * sizeof(float),
+                        hipMemcpyHostToDevice),
+              "copy RoPE table");
+        a.rope_table = m->rope_table.ptr;
         if (exact) {
             if (max_experts > pk::kMaxExperts256 || c.top_k > pk::kMaxRefTopK)
                 throw Unsupported("reference-order MoE covers up to 256 experts and top-16");
-            if (!pk::ref_attention_supported(c.head_dim, c.kv_capacity) ||
-                c.hidden > pk::kMaxRefNormWidth)
-                throw Unsupported("reference-order kernels cover head_dim 64/128/256, hidden <= 4096");
+            if (c.hidden > pk::kMaxRefNormWidth)
+                throw Unsupported("reference-order kernels cover hidden <= 4096");
             m->ref_scratch.ensure(pk::ref_scratch_floats(c.top_k, max_ffn, c.hidden));
             a.ref_scratch = m->ref_scratch.ptr;
-            // prepare_qwen_rope (src/qwen3_moe_runner.cpp:141-155) with this host's libm,
-            // for every position of the model context
-            const uint32_t half = c.head_dim / 2;
-            std::vector<float> table(uint64_t(c.context) * c.head_dim);
-            for (uint32_t pos = 0; pos < c.context; ++pos) {
-                float* row = table.data() + uint64_t(pos) * c.head_dim;
-                for (uint32_t p = 0; p < half; ++p) {
-                    const float angle = static_cast<float>(pos) *
-                        std::pow(c.rope_theta, -static_cast<float>(p) / static_cast<float>(half));
-                    row[p] = std::cos(angle);
-                    row[half + p] = std::sin(angle);
-                }
-            }
-            m->rope_table.ensure(table.size());
-            check(hipMemcpy(m->rope_table.ptr, table.data(), table.size() * sizeof(float),
-                            hipMemcpyHostToDevice),
-                  "copy RoPE table");
-            a.rope_table = m->rope_table.ptr;
             if (c.libm_expf_count) {
                 if (!c.libm_expf_pairs || c.libm_expf_count > (1ull << 24))
                     throw ArgError("libm_expf_pairs: missing or oversized table");

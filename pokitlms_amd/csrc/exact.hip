@@ -795,6 +795,17 @@ bool ref_attention_supported(uint32_t head_dim, uint32_t capacity) {
            (chain_floats(capacity) * 4ull + kAttnTileBytes) <= 160ull * 1024u - 8192u;
 }
 
+hipError_t launch_ref_attention(const ModelArgs& a, const ModelLayer& L, hipStream_t s) {
+    const size_t lds = chain_floats(a.capacity) * sizeof(float) + kAttnTileBytes;
+    switch (a.head_dim) {
+        case 64: hipLaunchKernelGGL(k_ref_attention<64>, dim3(a.heads), dim3(256), lds, s, a, L); break;
+        case 128: hipLaunchKernelGGL(k_ref_attention<128>, dim3(a.heads), dim3(256), lds, s, a, L); break;
+        case 256: hipLaunchKernelGGL(k_ref_attention<256>, dim3(a.heads), dim3(256), lds, s, a, L); break;
+        default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
 // Six launches per layer; the residual stream alternates between
 // hidden_state and hidden_alt so no workgroup reads a row another one of the
 // same launch overwrites.
@@ -802,7 +813,6 @@ hipError_t launch_ref_step(const ModelArgs& a, const ModelLayer* layers, bool lo
     const uint32_t qd = a.heads * a.head_dim, kd = a.kv_heads * a.head_dim;
     RefResidual res{};  // what the next RMSNorm adds to the residual stream first
     hipError_t err = hipSuccess;
-    const size_t attn_lds = chain_floats(a.capacity) * sizeof(float) + kAttnTileBytes;
     for (uint32_t l = 0; l < a.layers; ++l) {
         const ModelLayer& L = layers[l];
         const MoeDecodeArgs& m = L.moe;
@@ -815,12 +825,7 @@ hipError_t launch_ref_step(const ModelArgs& a, const ModelLayer* layers, bool lo
                                     {L.v, L.v_row, 0, kd, 0, a.v}};
         if ((err = launch_ref_matvec_multi(L.attn_type, qkv, qkv_segs, 3, 1, s))) return err;
         // 2. q/k norms, RoPE, KV ring, attention
-        switch (a.head_dim) {
-            case 64: hipLaunchKernelGGL(k_ref_attention<64>, dim3(a.heads), dim3(256), attn_lds, s, a, L); break;
-            case 128: hipLaunchKernelGGL(k_ref_attention<128>, dim3(a.heads), dim3(256), attn_lds, s, a, L); break;
-            case 256: hipLaunchKernelGGL(k_ref_attention<256>, dim3(a.heads), dim3(256), attn_lds, s, a, L); break;
-            default: return hipErrorInvalidValue;
-        }
+        if ((err = launch_ref_attention(a, L, s))) return err;
         // 3. output projection
         RefMatvecArgs o{};
         o.W = L.o;

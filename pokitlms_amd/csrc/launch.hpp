@@ -133,11 +133,11 @@ struct ModelArgs {
     float* att;               // attention output [heads * head_dim]
     float* attn_out;          // [hidden]
     float* hidden_alt;        // reference order: the residual stream's second buffer
-    float* rope;              // cos [head_dim / 2], then sin
     float* logits;            // [vocab]
+    float* argmax_part;       // per 2048-logit chunk: maximum, index bits
     // reference-order mode: every kernel repeats the CPU's operation order
     uint32_t exact;
-    const float* rope_table;  // [positions][head_dim]: cos, then sin (host libm)
+    const float* rope_table;  // [positions][head_dim]: cos, then sin (host libm; both modes)
     float* ref_scratch;       // router logits, gate, up, expert outputs
     LibmExpf expf;            // reference order: the host libm's expf exceptions
 };
@@ -223,6 +223,9 @@ hipError_t launch_ref_rmsnorm(float* x, const RefResidual& res, const float* w, 
 bool ref_attention_supported(uint32_t head_dim, uint32_t capacity);
 // Widths whose RMSNorm the matvec staging can carry.
 constexpr uint32_t kMaxRefNormWidth = 4096;
+// q/k head norms, RoPE, KV append and attention of one layer in the
+// reference's order (both modes use it).
+hipError_t launch_ref_attention(const ModelArgs& a, const ModelLayer& L, hipStream_t stream);
 // The reference-order token step after the embedding (all layers, then the
 // head when logits).
 hipError_t launch_ref_step(const ModelArgs& a, const ModelLayer* layers, bool logits,

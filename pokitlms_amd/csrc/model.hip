@@ -91,16 +91,6 @@ __device__ __forceinline__ float block_sum(float v, float* red) {
     return r;
 }
 
-__device__ __forceinline__ float block_max(float v, float* red) {
-    v = lane63(group_max<64>(v));
-    if ((threadIdx.x & 63u) == 0) red[threadIdx.x >> 6] = v;
-    __syncthreads();
-    float r = red[0];
-    for (uint32_t w = 1; w < (blockDim.x >> 6); ++w) r = fmaxf(r, red[w]);
-    __syncthreads();
-    return r;
-}
-
 // ---------------------------------------------------------------------------
 // Embedding row: the reference's FP32 values of 32 consecutive elements
 // (dequantize_quantized_row, src/quantized_linear.cpp:427-493, with the
@@ -153,24 +143,17 @@ __device__ void decode32(const uint8_t* row, uint32_t k0, float* v) {
     }
 }
 
-// Step start: hidden = embedding row of tokens[pos]; the RoPE table of pos
-// (prepare_qwen_rope, src/qwen3_moe_runner.cpp:141-155).
+// Step start: hidden = embedding row of tokens[pos].
 template <int T>
 __global__ __launch_bounds__(256) void k_embed(ModelArgs a) {
     const uint32_t pos = a.state[0];
     const uint32_t token = a.tokens[pos];
-    const uint32_t tid = threadIdx.x, half = a.head_dim / 2u;
+    const uint32_t tid = threadIdx.x;
     const uint8_t* row = a.embd + static_cast<uint64_t>(token) * a.embd_row;
     for (uint32_t c = tid; c < a.hidden / 32u; c += blockDim.x) {
         float v[32];
         decode32<T>(row, 32u * c, v);
         for (uint32_t i = 0; i < 32; ++i) a.hidden_state[32u * c + i] = v[i];
-    }
-    for (uint32_t p = tid; p < half; p += blockDim.x) {
-        const float angle = static_cast<float>(pos) *
-                            powf(a.rope_theta, -static_cast<float>(p) / static_cast<float>(half));
-        a.rope[p] = cosf(angle);
-        a.rope[half + p] = sinf(angle);
     }
 }
 
@@ -194,115 +177,54 @@ __global__ __launch_bounds__(256) void k_add_rmsnorm(float* __restrict__ x, cons
     for (uint32_t i = threadIdx.x; i < n; i += blockDim.x) out[i] = x[i] * scale * w[i];
 }
 
-// Per-head q/k RMSNorm and NeoX RoPE (apply_qwen_rope: pairs (i, i + half));
-// k and v go to the FP16 ring slot pos % capacity (src/kv_cache.cpp:131-183,
-// round to nearest even).  One workgroup of head_dim threads per head:
-// q heads, then k heads, then v heads.
-__global__ __launch_bounds__(128) void k_qk_rope_kv(ModelArgs a, ModelLayer L) {
-    __shared__ float vals[256];
-    __shared__ float red[4];
-    const uint32_t h = blockIdx.x, d = threadIdx.x, hd = a.head_dim, half = hd / 2u;
-    const uint32_t slot = a.state[0] % a.capacity;
-    if (h >= a.heads + a.kv_heads) {  // v heads: copy to the cache
-        const uint32_t j = h - a.heads - a.kv_heads;
-        L.vcache[(static_cast<uint64_t>(slot) * a.kv_heads + j) * hd + d] =
-            __half_as_ushort(__float2half_rn(a.v[j * hd + d]));
-        return;
-    }
-    const bool is_q = h < a.heads;
-    float* src = is_q ? a.q + h * hd : a.k + (h - a.heads) * hd;
-    const float* nw = is_q ? L.q_norm : L.k_norm;
-    const float x = src[d];
-    const float total = block_sum(x * x, red);
-    const float scale = 1.0f / sqrtf(total / static_cast<float>(hd) + a.rms_eps);
-    vals[d] = x * scale * nw[d];
-    __syncthreads();
-    float r;
-    if (d < half) {
-        r = vals[d] * a.rope[d] - vals[d + half] * a.rope[half + d];
-    } else {
-        const uint32_t i = d - half;
-        r = vals[d] * a.rope[i] + vals[i] * a.rope[half + i];
-    }
-    if (is_q) {
-        src[d] = r;
-    } else {
-        const uint32_t j = h - a.heads;
-        L.kcache[(static_cast<uint64_t>(slot) * a.kv_heads + j) * hd + d] =
-            __half_as_ushort(__float2half_rn(r));
+// First-max argmax of the logits in two launches: each workgroup of
+// k_argmax_part the maximum of one 2048-logit chunk (larger value, then smaller
+// index: the first maximum), non-finite logits flagged; k_argmax the maximum
+// of the chunks, then the next step's token: the prompt's while prompt tokens
+// remain, else the argmax (sample_token at temperature 0,
+// src/qwen3_moe_runner.cpp:320-333).
+constexpr uint32_t kArgmaxChunk = 2048;
+
+__device__ __forceinline__ void argmax_merge(float& best, uint32_t& idx, float ov, uint32_t oi) {
+    if (ov > best || (ov == best && oi < idx)) {
+        best = ov;
+        idx = oi;
     }
 }
 
-// Grouped-query attention of one q head over the ring's positions
-// (KvCache::attend, src/kv_cache.cpp:185-293): scores q.k in key order,
-// times 1/sqrt(head_dim); softmax; out[d] += p_i * v_i[d] in position order.
-__global__ __launch_bounds__(256) void k_attention(ModelArgs a, ModelLayer L) {
-    extern __shared__ float sc[];  // [capacity]
-    __shared__ float qv[256];
-    __shared__ float red[4];
-    const uint32_t h = blockIdx.x, tid = threadIdx.x, hd = a.head_dim;
-    const uint32_t kvh = h / (a.heads / a.kv_heads);
-    const uint32_t pos = a.state[0];
-    const uint32_t n = pos + 1u < a.capacity ? pos + 1u : a.capacity;
-    const uint32_t first = pos + 1u - n;
-    for (uint32_t d = tid; d < hd; d += blockDim.x) qv[d] = a.q[h * hd + d];
-    __syncthreads();
-    float mx = -INFINITY;
-    for (uint32_t i = tid; i < n; i += blockDim.x) {
-        const uint32_t slot = (first + i) % a.capacity;
-        const uint16_t* kr = L.kcache + (static_cast<uint64_t>(slot) * a.kv_heads + kvh) * hd;
-        float s = 0.0f;
-        for (uint32_t d = 0; d < hd; ++d) s = s + qv[d] * __half2float(__ushort_as_half(kr[d]));
-        s = s * a.attn_scale;
-        sc[i] = s;
-        mx = fmaxf(mx, s);
-    }
-    mx = block_max(mx, red);
-    float part = 0.0f;
-    for (uint32_t i = tid; i < n; i += blockDim.x) {
-        const float e = expf(sc[i] - mx);
-        sc[i] = e;
-        part += e;
-    }
-    const float denom = block_sum(part, red);
-    for (uint32_t d = tid; d < hd; d += blockDim.x) {
-        float o = 0.0f;
-        for (uint32_t i = 0; i < n; ++i) {
-            const uint32_t slot = (first + i) % a.capacity;
-            const float v = __half2float(__ushort_as_half(
-                L.vcache[(static_cast<uint64_t>(slot) * a.kv_heads + kvh) * hd + d]));
-            o = o + (sc[i] / denom) * v;
-        }
-        a.att[h * hd + d] = o;
-    }
-}
-
-// First-max argmax of the logits (NaN/inf flagged), then the next step's
-// token: the prompt's while prompt tokens remain, else the argmax.
-__global__ __launch_bounds__(1024) void k_argmax(ModelArgs a) {
-    __shared__ float bv[16];
-    __shared__ uint32_t bi[16];
-    const uint32_t tid = threadIdx.x;
-    float best = -INFINITY;
-    uint32_t idx = 0xffffffffu;
-    bool bad = false;
-    for (uint32_t i = tid; i < a.vocab; i += blockDim.x) {  // ascending: strict > keeps the first
-        const float v = a.logits[i];
-        bad = bad || !isfinite(v);
-        if (v > best || idx == 0xffffffffu) {
-            best = v;
-            idx = i;
-        }
-    }
-    // wave reduction: larger value, then smaller index
+__device__ __forceinline__ void argmax_wave(float& best, uint32_t& idx) {
     for (uint32_t off = 32; off > 0; off >>= 1) {
         const float ov = __shfl_down(best, off);
         const uint32_t oi = __shfl_down(idx, off);
-        if (ov > best || (ov == best && oi < idx)) {
-            best = ov;
-            idx = oi;
+        argmax_merge(best, idx, ov, oi);
+    }
+}
+
+__global__ __launch_bounds__(256) void k_argmax_part(ModelArgs a) {
+    __shared__ float bv[4];
+    __shared__ uint32_t bi[4];
+    const uint32_t tid = threadIdx.x, base = blockIdx.x * kArgmaxChunk;
+    float v[kArgmaxChunk / 256];
+#pragma unroll
+    for (uint32_t k = 0; k < kArgmaxChunk / 256; ++k) {
+        const uint32_t i = base + tid + 256u * k;
+        v[k] = a.logits[i < a.vocab ? i : 0u];
+    }
+    float best = -INFINITY;
+    uint32_t idx = 0xffffffffu;
+    bool bad = false;
+#pragma unroll
+    for (uint32_t k = 0; k < kArgmaxChunk / 256; ++k) {  // ascending: strict > keeps the first
+        const uint32_t i = base + tid + 256u * k;
+        if (i < a.vocab) {
+            bad = bad || !isfinite(v[k]);
+            if (v[k] > best || idx == 0xffffffffu) {
+                best = v[k];
+                idx = i;
+            }
         }
     }
+    argmax_wave(best, idx);
     const uint32_t any_bad = __any(bad);
     if ((tid & 63u) == 0) {
         bv[tid >> 6] = best;
@@ -311,21 +233,43 @@ __global__ __launch_bounds__(1024) void k_argmax(ModelArgs a) {
     }
     __syncthreads();
     if (tid == 0) {
-        float b = bv[0];
-        uint32_t id = bi[0];
-        for (uint32_t w = 1; w < (blockDim.x >> 6); ++w)
-            if (bv[w] > b || (bv[w] == b && bi[w] < id)) {
-                b = bv[w];
-                id = bi[w];
-            }
+        for (uint32_t w = 1; w < 4; ++w) argmax_merge(bv[0], bi[0], bv[w], bi[w]);
+        a.argmax_part[2u * blockIdx.x] = bv[0];
+        a.argmax_part[2u * blockIdx.x + 1u] = __uint_as_float(bi[0]);
+    }
+}
+
+__global__ __launch_bounds__(256) void k_argmax(ModelArgs a, uint32_t parts) {
+    __shared__ float bv[4];
+    __shared__ uint32_t bi[4];
+    const uint32_t tid = threadIdx.x;
+    float best = -INFINITY;
+    uint32_t idx = 0xffffffffu;
+    for (uint32_t c = tid; c < parts; c += 256u)
+        argmax_merge(best, idx, a.argmax_part[2u * c], __float_as_uint(a.argmax_part[2u * c + 1u]));
+    argmax_wave(best, idx);
+    if ((tid & 63u) == 0) {
+        bv[tid >> 6] = best;
+        bi[tid >> 6] = idx;
+    }
+    __syncthreads();
+    if (tid == 0) {
+        for (uint32_t w = 1; w < 4; ++w) argmax_merge(bv[0], bi[0], bv[w], bi[w]);
         const uint32_t pos = a.state[0];
-        if (pos + 1u >= a.state[1]) a.tokens[pos + 1u] = id;  // past the prompt: generated
+        if (pos + 1u >= a.state[1]) a.tokens[pos + 1u] = bi[0];  // past the prompt: generated
         a.state[0] = pos + 1u;
     }
 }
 
 __global__ void k_advance(uint32_t* state) {
     if (threadIdx.x == 0) state[0] = state[0] + 1u;
+}
+
+hipError_t launch_argmax(const ModelArgs& a, hipStream_t s) {
+    const uint32_t parts = (a.vocab + kArgmaxChunk - 1u) / kArgmaxChunk;
+    hipLaunchKernelGGL(k_argmax_part, dim3(parts), dim3(256), 0, s, a);
+    hipLaunchKernelGGL(k_argmax, dim3(1), dim3(256), 0, s, a, parts);
+    return hipGetLastError();
 }
 
 template <int T>
@@ -373,8 +317,8 @@ hipError_t launch_model_step(const ModelArgs& a, const ModelLayer* layers, bool 
     if (err != hipSuccess) return err;
     if (a.exact) {
         if ((err = launch_ref_step(a, layers, logits, s))) return err;
-        if (logits) hipLaunchKernelGGL(k_argmax, dim3(1), dim3(1024), 0, s, a);
-        else hipLaunchKernelGGL(k_advance, dim3(1), dim3(64), 0, s, a.state);
+        if (logits) return launch_argmax(a, s);
+        hipLaunchKernelGGL(k_advance, dim3(1), dim3(64), 0, s, a.state);
         return hipGetLastError();
     }
     const uint32_t qd = a.heads * a.head_dim, kd = a.kv_heads * a.head_dim;
@@ -394,10 +338,7 @@ hipError_t launch_model_step(const ModelArgs& a, const ModelLayer* layers, bool 
         if ((err = matvec(L.attn_type, L.q, L.q_row, qd, a.hidden, a.normed, a.q))) return err;
         if ((err = matvec(L.attn_type, L.k, L.k_row, kd, a.hidden, a.normed, a.k))) return err;
         if ((err = matvec(L.attn_type, L.v, L.v_row, kd, a.hidden, a.normed, a.v))) return err;
-        hipLaunchKernelGGL(k_qk_rope_kv, dim3(a.heads + 2u * a.kv_heads), dim3(a.head_dim), 0, s,
-                           a, L);
-        hipLaunchKernelGGL(k_attention, dim3(a.heads), dim3(256), a.capacity * sizeof(float), s, a,
-                           L);
+        if ((err = launch_ref_attention(a, L, s))) return err;  // the kernel of both modes
         if ((err = matvec(L.attn_type, L.o, L.o_row, a.hidden, qd, a.att, a.attn_out))) return err;
         if ((err = norm(a.attn_out, L.ffn_norm))) return err;
         err = launch_moe_decode(L.moe, s);  // normed -> moe_out
@@ -408,7 +349,7 @@ hipError_t launch_model_step(const ModelArgs& a, const ModelLayer* layers, bool 
         if ((err = norm(delta, a.out_norm))) return err;
         if ((err = matvec(a.out_type, a.out, a.out_row, a.vocab, a.hidden, a.normed, a.logits)))
             return err;
-        hipLaunchKernelGGL(k_argmax, dim3(1), dim3(1024), 0, s, a);
+        return launch_argmax(a, s);
     } else {
         hipLaunchKernelGGL(k_advance, dim3(1), dim3(64), 0, s, a.state);
     }
