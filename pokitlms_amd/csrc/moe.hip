@@ -82,6 +82,31 @@ __global__ __launch_bounds__(256) void k_gate_up(MoeDecodeArgs a, uint32_t units
     const XRegs xr = load_x_regs(a.x, a.hidden);
     RouteData<NS> rd;
     if (wave == 0) rd = load_route_data<NS>(a);
+    // everything about this wave's items but the experts, while the loads fly
+    const uint32_t G = 1u << glog2, RPP = 64u >> glog2;
+    const uint32_t sub = lane >> glog2, ul = lane & (G - 1u);
+    UnitPos pos[NU];
+    bool valid[NU];
+#pragma unroll
+    for (int k = 0; k < NU; ++k) {
+        const uint32_t u = ul + G * k;
+        valid[k] = u < units;
+        pos[k] = unit_pos<T, UB>(valid[k] ? u : 0u);
+    }
+    const uint32_t items = a.top_k * a.ffn;
+    const uint32_t passes = (items + RPP - 1u) / RPP;
+    const uint32_t first = (blockIdx.x * (blockDim.x >> 6) + wave) * NP;
+    uint32_t item[NP], route_of[NP];
+    uint64_t goff[NP], uoff[NP];
+#pragma unroll
+    for (int q = 0; q < NP; ++q) {
+        item[q] = (first + q) * RPP + sub;
+        const uint32_t it = item[q] < items ? item[q] : items - 1u;
+        route_of[q] = it / a.ffn;
+        const uint32_t row = it % a.ffn;
+        goff[q] = static_cast<uint64_t>(row) * a.gate_row;
+        uoff[q] = static_cast<uint64_t>(row) * a.up_row;
+    }
     store_x_regs(xs, xr, a.hidden);
     WaveRoutes<NS> w;
     if (wave == 0) {
@@ -120,36 +145,18 @@ __global__ __launch_bounds__(256) void k_gate_up(MoeDecodeArgs a, uint32_t units
     }
     if (first_wave) write_routes<NS>(a, sel, w.logit);
 
-    const uint32_t G = 1u << glog2, RPP = 64u >> glog2;
-    const uint32_t sub = lane >> glog2, ul = lane & (G - 1u);
-    UnitPos pos[NU];
-    bool valid[NU];
-#pragma unroll
-    for (int k = 0; k < NU; ++k) {
-        const uint32_t u = ul + G * k;
-        valid[k] = u < units;
-        pos[k] = unit_pos<T, UB>(valid[k] ? u : 0u);
-    }
-    const uint32_t items = a.top_k * a.ffn;
-    const uint32_t passes = (items + RPP - 1u) / RPP;
-    const uint32_t first = (blockIdx.x * (blockDim.x >> 6) + wave) * NP;
-
     // Loads are unconditional (items past the end re-read the last item,
     // absent units re-read unit 0, results unused), so no branch splits
     // them and none waits on another.
     UnitRaw<T, UB> rg[NP][NU], ru[NP][NU];
-    uint32_t item[NP];
 #pragma unroll
     for (int q = 0; q < NP; ++q) {
-        item[q] = (first + q) * RPP + sub;
-        const uint32_t it = item[q] < items ? item[q] : items - 1u;
-        const uint32_t route_i = it / a.ffn, row = it % a.ffn;
         uint32_t e = 0u;
 #pragma unroll
         for (uint32_t r = 0; r < kMaxTopK; ++r)
-            if (route_i == r) e = sel[r];
-        const uint8_t* gr = a.gate + static_cast<uint64_t>(e) * a.gate_slice + row * a.gate_row;
-        const uint8_t* ur = a.up + static_cast<uint64_t>(e) * a.up_slice + row * a.up_row;
+            if (route_of[q] == r) e = sel[r];
+        const uint8_t* gr = a.gate + static_cast<uint64_t>(e) * a.gate_slice + goff[q];
+        const uint8_t* ur = a.up + static_cast<uint64_t>(e) * a.up_slice + uoff[q];
 #pragma unroll
         for (int k = 0; k < NU; ++k) {
             unit_load<T, UB>(gr, pos[k], rg[q][k]);

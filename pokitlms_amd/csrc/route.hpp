@@ -185,8 +185,9 @@ __device__ __forceinline__ RouteData<NS> load_route_data(const MoeDecodeArgs& a)
 // replaced by 255 - id).  The key only proposes an order: certification
 // below checks it against the exact intervals [S - B, S + B], so an ordering
 // the truncated key gets wrong is never certified and goes to the exact
-// path.  Branch-free: always kMaxTopK selection rounds (ranks past top_k
-// only tighten the check), each taking the winner's interval by readlane.
+// path.  top_k selection rounds (a uniform condition per unrolled round),
+// each taking the winner's interval by readlane; then one wave maximum of
+// the unselected experts' upper bounds.
 template <int NS>
 __device__ __forceinline__ WaveRoutes<NS> wave_route(const MoeDecodeArgs& a, const RouteData<NS>& d) {
     const uint32_t lane = threadIdx.x & 63u;
@@ -210,21 +211,31 @@ __device__ __forceinline__ WaveRoutes<NS> wave_route(const MoeDecodeArgs& a, con
     double lo_r[kMaxTopK], hi_r[kMaxTopK];
 #pragma unroll
     for (uint32_t r = 0; r < kMaxTopK; ++r) {
-        uint32_t mk = key[0];
+        w.sel[r] = 0u;
+        lo_r[r] = -INFINITY;
+        hi_r[r] = -INFINITY;
+        if (r < K) {  // uniform
+            uint32_t mk = key[0];
 #pragma unroll
-        for (int m = 1; m < NS; ++m) mk = max(mk, key[m]);
-        const uint32_t best = wave_max_u32(mk);
-        const uint32_t e = 255u - (best & 0xffu);
-        w.sel[r] = e;
-        const bool present = best != 0u;  // fewer than kMaxTopK experts
-        lo_r[r] = present ? slot_at<NS>(lo, e) : -INFINITY;
-        hi_r[r] = present ? slot_at<NS>(hi, e) : -INFINITY;
+            for (int m = 1; m < NS; ++m) mk = max(mk, key[m]);
+            const uint32_t best = wave_max_u32(mk);
+            const uint32_t e = 255u - (best & 0xffu);
+            w.sel[r] = e;
+            lo_r[r] = slot_at<NS>(lo, e);
+            hi_r[r] = slot_at<NS>(hi, e);
 #pragma unroll
-        for (int m = 0; m < NS; ++m) key[m] = key[m] == best ? 0u : key[m];
+            for (int m = 0; m < NS; ++m) key[m] = key[m] == best ? 0u : key[m];
+        }
     }
+    // the largest upper bound of the experts left out (selected and absent
+    // experts have key 0)
+    double u = -INFINITY;
+#pragma unroll
+    for (int m = 0; m < NS; ++m) u = key[m] != 0u ? fmax(u, hi[m]) : u;
+    u = readlane_d(group_max<64>(u), 63u);
     // route r < top_k is certain when its lower bound clears the upper bound
-    // of everything ranked after it
-    double after = -INFINITY, lmin = INFINITY;
+    // of every expert ranked after it, routed or not
+    double after = u, lmin = INFINITY;
     bool ok = true;
 #pragma unroll
     for (int r = kMaxTopK - 1; r >= 0; --r) {
@@ -233,11 +244,7 @@ __device__ __forceinline__ WaveRoutes<NS> wave_route(const MoeDecodeArgs& a, con
         lmin = routed ? fmin(lmin, lo_r[r]) : lmin;
         after = fmax(after, hi_r[r]);
     }
-    // ... including every expert outside the first kMaxTopK ranks
-    bool reach = false;
-#pragma unroll
-    for (int m = 0; m < NS; ++m) reach = reach || (key[m] != 0u && hi[m] >= lmin);
-    w.certified = ok && !__any(reach);
+    w.certified = ok;
     w.lo_min_sel = lmin;
     return w;
 }
