@@ -178,6 +178,37 @@ pk_hip_status pk_hip_moe_decode_async(pk_hip_ctx* ctx, const pk_hip_moe_layer* l
                                       uint32_t* device_ids, float* device_probs, void* stream,
                                       char* error_buffer, size_t error_capacity);
 
+/* Qwen3.5-MoE block for one token (src/qwen35_runner.cpp:670-764) on the same
+ * kernels.  Routed experts come from select_experts (:131-173): the same
+ * top-k order as route_experts (ids bit-exact), weights from an FP32 softmax
+ * over all experts, optional FP32 renormalisation (routed.normalize =
+ * expert_weights_norm), then times routed.scale (expert_weights_scale).
+ * Activations are silu(g) * u (:111-123).  The shared expert is added last
+ * with weight sigmoid(shared_router . x).  shared_router is F32 [hidden]
+ * (ffn_gate_inp_shexp, uploaded as [hidden, 1]); shared_gate/shared_up
+ * [hidden, ffn] and shared_down [ffn, hidden] (ffn_*_shexp) must have the
+ * routed experts' types and ffn width (top_k <= 8 as for
+ * pk_hip_moe_decode), else UNSUPPORTED.  y
+ * receives mixer_output (:759-761); ids/weights the routes in order (weights
+ * include the scale).  Host buffers; synchronous. */
+typedef struct pk_hip_moe35_layer {
+    pk_hip_moe_layer routed;
+    const pk_hip_weight* shared_router;
+    const pk_hip_weight* shared_gate;
+    const pk_hip_weight* shared_up;
+    const pk_hip_weight* shared_down;
+} pk_hip_moe35_layer;
+
+pk_hip_status pk_hip_moe35_decode(pk_hip_ctx* ctx, const pk_hip_moe35_layer* layer,
+                                  const float* x, float* y, uint32_t* ids, float* weights,
+                                  char* error_buffer, size_t error_capacity);
+
+/* Device-buffer variant, enqueued on `stream` without synchronising. */
+pk_hip_status pk_hip_moe35_decode_async(pk_hip_ctx* ctx, const pk_hip_moe35_layer* layer,
+                                        const float* device_x, float* device_y,
+                                        uint32_t* device_ids, float* device_weights, void* stream,
+                                        char* error_buffer, size_t error_capacity);
+
 /* A batch of tokens through one MoE layer: the prompt loop of the reference
  * (src/qwen3_moe_runner.cpp:785-790), whose tokens each take the MoE block
  * (:644-691) independently.  x [tokens][hidden] holds the normalised hidden

@@ -74,6 +74,13 @@ class Oracle:
                                              ctypes.c_uint64]
             L.pko_route_experts.argtypes = [_f32p, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_int,
                                             _u32p, _f32p, _f32p]
+            L.pko_select_experts.argtypes = [_f32p, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_int,
+                                             _u32p, _f32p]
+            L.pko_moe35_block.argtypes = [
+                _f32p, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32, _u8p,
+                ctypes.c_uint32, _u8p, ctypes.c_uint32, _u8p, ctypes.c_uint32, ctypes.c_int,
+                ctypes.c_float, _f32p, ctypes.c_uint32, ctypes.c_uint32, _u8p, ctypes.c_uint32,
+                _u8p, ctypes.c_uint32, _u8p, _f32p, _f32p, _u32p, _f32p]
             L.pko_moe_block.argtypes = [_f32p, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32,
                                         ctypes.c_uint32, _u8p, ctypes.c_uint32, _u8p,
                                         ctypes.c_uint32, _u8p, ctypes.c_uint32, ctypes.c_int,
@@ -99,6 +106,16 @@ class Oracle:
             L.pkref_qwen3moe_greedy.argtypes = [ctypes.c_char_p, _u32p, ctypes.c_uint32,
                                                 ctypes.c_uint32, ctypes.c_uint64, _u32p, _f32p,
                                                 ctypes.POINTER(ctypes.c_double)]
+            L.pkref_select_experts.argtypes = [_f32p, ctypes.c_uint32, ctypes.c_uint32,
+                                               ctypes.c_int, _u32p, _f32p]
+            L.pkref_moe35_create.restype = ctypes.c_void_p
+            L.pkref_moe35_create.argtypes = [
+                _f32p, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32, _u8p,
+                ctypes.c_uint32, _u8p, ctypes.c_uint32, _u8p, ctypes.c_uint32, ctypes.c_int,
+                ctypes.c_float, _f32p, ctypes.c_uint32, ctypes.c_uint32, _u8p, ctypes.c_uint32,
+                _u8p, ctypes.c_uint32, _u8p]
+            L.pkref_moe35_forward.argtypes = [ctypes.c_void_p, _f32p, _f32p, _u32p, _f32p]
+            L.pkref_moe35_destroy.argtypes = [ctypes.c_void_p]
             L.pkref_qwen3moe_forward_times.argtypes = [
                 ctypes.c_char_p, _u32p, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint64,
                 ctypes.POINTER(ctypes.c_double)]
@@ -192,6 +209,20 @@ class Oracle:
             raise OracleError(rc, "pkref_qwen3moe_forward_times")
         return secs
 
+    def select_experts(self, logits: np.ndarray, top_k: int, normalize: bool):
+        """Qwen3.5 select_experts: (ids, weights) in route order."""
+        lg = np.ascontiguousarray(logits, dtype=np.float32)
+        ids = np.zeros(max(top_k, 1), dtype=np.uint32)
+        w = np.zeros(max(top_k, 1), dtype=np.float32)
+        fn = self.lib.pko_select_experts if self.kind == "port" else self.lib.pkref_select_experts
+        rc = fn(_fp(lg), lg.size, top_k, int(normalize), ids.ctypes.data_as(_u32p), _fp(w))
+        if rc:
+            raise OracleError(rc, "select_experts")
+        return ids[:top_k], w[:top_k]
+
+    def moe35(self, layer) -> "Moe35Block":
+        return Moe35Block(self, layer)
+
     def moe(self, layer) -> "MoeBlock":
         return MoeBlock(self, layer)
 
@@ -243,3 +274,46 @@ class MoeBlock:
             self.close()
         except Exception:
             pass
+
+
+class Moe35Block:
+    """A prepared Qwen3.5-MoE layer (synth.Moe35Layer); ``forward(x)``
+    returns (mixer_output, ids, weights)."""
+
+    def __init__(self, oracle: Oracle, layer):
+        self.o, self.layer = oracle, layer
+        L = layer
+        self._keep = tuple(np.ascontiguousarray(a) for a in (
+            np.asarray(L.router, np.float32), L.gate, L.up, L.down,
+            np.asarray(L.shared_router, np.float32), L.shared_gate, L.shared_up, L.shared_down))
+        r, g, u, d, sr, sg, su, sd = self._keep
+        self._args = (_fp(r), L.hidden, L.experts, L.ffn, L.gate_type, g.ctypes.data, L.up_type,
+                      u.ctypes.data, L.down_type, d.ctypes.data, L.top_k, int(L.normalize),
+                      float(L.scale), _fp(sr), L.shared_ffn, L.gate_type, sg.ctypes.data,
+                      L.up_type, su.ctypes.data, L.down_type, sd.ctypes.data)
+        self.handle = None
+        if oracle.kind == "reference":
+            self.handle = oracle.lib.pkref_moe35_create(*self._args)
+            if not self.handle:
+                raise OracleError(1, "pkref_moe35_create")
+
+    def forward(self, x: np.ndarray):
+        L = self.layer
+        xx = np.ascontiguousarray(x, dtype=np.float32)
+        y = np.zeros(L.hidden, np.float32)
+        ids = np.zeros(L.top_k, np.uint32)
+        w = np.zeros(L.top_k, np.float32)
+        if self.handle:
+            rc = self.o.lib.pkref_moe35_forward(self.handle, _fp(xx), _fp(y),
+                                                ids.ctypes.data_as(_u32p), _fp(w))
+        else:
+            rc = self.o.lib.pko_moe35_block(*self._args, _fp(xx), _fp(y),
+                                            ids.ctypes.data_as(_u32p), _fp(w))
+        if rc:
+            raise OracleError(rc, "moe35 forward")
+        return y, ids, w
+
+    def __del__(self):
+        if getattr(self, "handle", None):
+            self.o.lib.pkref_moe35_destroy(self.handle)
+            self.handle = None

@@ -345,3 +345,137 @@ done:
     free(out);
     return rc;
 }
+
+/* src/qwen35_runner.cpp:131-173 */
+int pko_select_experts(const float* logits, uint32_t n, uint32_t top_k, int normalize,
+                       uint32_t* ids, float* weights) {
+    if (top_k == 0 || top_k > n) return 1;
+    float mx = logits[0];
+    for (uint32_t i = 1; i < n; ++i)
+        if (mx < logits[i]) mx = logits[i];
+    if (!isfinite(mx)) return 2;
+    for (uint32_t i = 0; i < n; ++i)
+        if (!isfinite(logits[i])) return 2;
+    float* prob = (float*)malloc(sizeof(float) * n);
+    if (!prob) return 2;
+    float denominator = 0.0f;
+    for (uint32_t i = 0; i < n; ++i) {
+        prob[i] = expf(logits[i] - mx);
+        denominator += prob[i];
+    }
+    if (!isfinite(denominator) || denominator <= 0.0f) {
+        free(prob);
+        return 2;
+    }
+    for (uint32_t i = 0; i < n; ++i) prob[i] /= denominator;
+    uint32_t count = 0;
+    for (uint32_t id = 0; id < n; ++id) {
+        const float v = logits[id];
+        uint32_t where = 0;
+        while (where < count && (logits[ids[where]] > v ||
+                                 (logits[ids[where]] == v && ids[where] < id)))
+            ++where;
+        if (count < top_k) {
+            for (uint32_t j = count; j > where; --j) ids[j] = ids[j - 1];
+            ids[where] = id;
+            ++count;
+        } else if (where < count) {
+            for (uint32_t j = count - 1; j > where; --j) ids[j] = ids[j - 1];
+            ids[where] = id;
+        }
+    }
+    for (uint32_t i = 0; i < top_k; ++i) weights[i] = prob[ids[i]];
+    free(prob);
+    if (normalize) {
+        float sum = 0.0f;
+        for (uint32_t i = 0; i < top_k; ++i) sum += weights[i];
+        if (!isfinite(sum) || sum <= 0.0f) return 2;
+        for (uint32_t i = 0; i < top_k; ++i) weights[i] /= sum;
+    }
+    return 0;
+}
+
+/* src/qwen35_runner.cpp:111-115 and :123 */
+static float pko_sigmoid35(float v) {
+    if (v >= 0.0f) return 1.0f / (1.0f + expf(-v));
+    const float e = expf(v);
+    return e / (1.0f + e);
+}
+
+static int pko_ffn_silu(uint32_t gate_type, const uint8_t* gate, uint64_t gate_bytes,
+                        uint32_t up_type, const uint8_t* up, uint64_t up_bytes, uint32_t down_type,
+                        const uint8_t* down, uint64_t down_bytes, uint32_t hidden, uint32_t ffn,
+                        const float* x, float* g, float* u, float* act, float* out) {
+    int rc = pko_linear(gate_type, gate, gate_bytes, hidden, ffn, x, g);
+    if (!rc) rc = pko_linear(up_type, up, up_bytes, hidden, ffn, x, u);
+    if (rc) return rc;
+    for (uint32_t i = 0; i < ffn; ++i) act[i] = (g[i] * pko_sigmoid35(g[i])) * u[i];
+    return pko_linear(down_type, down, down_bytes, ffn, hidden, act, out);
+}
+
+/* src/qwen35_runner.cpp:690-761 (the norm before and the residual add after
+ * are the caller's). */
+int pko_moe35_block(const float* router, uint32_t hidden, uint32_t n_experts, uint32_t ffn,
+                    uint32_t gate_type, const uint8_t* gate, uint32_t up_type, const uint8_t* up,
+                    uint32_t down_type, const uint8_t* down, uint32_t top_k, int normalize,
+                    float scale, const float* shared_router, uint32_t shared_ffn,
+                    uint32_t sgate_type, const uint8_t* sgate, uint32_t sup_type,
+                    const uint8_t* sup, uint32_t sdown_type, const uint8_t* sdown,
+                    const float* x, float* y, uint32_t* ids, float* weights) {
+    if (hidden == 0 || n_experts == 0 || ffn == 0 || shared_ffn == 0 || top_k == 0 ||
+        top_k > n_experts)
+        return 1;
+    const uint32_t types[6] = {gate_type, up_type, down_type, sgate_type, sup_type, sdown_type};
+    const uint32_t ins[6] = {hidden, hidden, ffn, hidden, hidden, shared_ffn};
+    for (int i = 0; i < 6; ++i) {
+        const uint64_t be = pko_block_elements(types[i]);
+        if (!be || ins[i] % be) return 1;
+    }
+    const uint64_t gate_slice = (uint64_t)ffn * (hidden / pko_block_elements(gate_type)) * pko_block_bytes(gate_type);
+    const uint64_t up_slice = (uint64_t)ffn * (hidden / pko_block_elements(up_type)) * pko_block_bytes(up_type);
+    const uint64_t down_slice = (uint64_t)hidden * (ffn / pko_block_elements(down_type)) * pko_block_bytes(down_type);
+    const uint64_t sg_bytes = (uint64_t)shared_ffn * (hidden / pko_block_elements(sgate_type)) * pko_block_bytes(sgate_type);
+    const uint64_t su_bytes = (uint64_t)shared_ffn * (hidden / pko_block_elements(sup_type)) * pko_block_bytes(sup_type);
+    const uint64_t sd_bytes = (uint64_t)hidden * (shared_ffn / pko_block_elements(sdown_type)) * pko_block_bytes(sdown_type);
+    const uint32_t wmax = ffn > shared_ffn ? ffn : shared_ffn;
+    float* logits = (float*)malloc(sizeof(float) * n_experts);
+    float* g = (float*)malloc(sizeof(float) * wmax);
+    float* u = (float*)malloc(sizeof(float) * wmax);
+    float* act = (float*)malloc(sizeof(float) * wmax);
+    float* out = (float*)malloc(sizeof(float) * hidden);
+    float gate_value = 0.0f;
+    int rc = 2;
+    if (!logits || !g || !u || !act || !out) goto done;
+    rc = pko_linear(PKO_F32, (const uint8_t*)router, (uint64_t)hidden * n_experts * 4, hidden,
+                    n_experts, x, logits);
+    if (!rc) rc = pko_select_experts(logits, n_experts, top_k, normalize, ids, weights);
+    if (rc) goto done;
+    for (uint32_t i = 0; i < hidden; ++i) y[i] = 0.0f;
+    for (uint32_t r = 0; r < top_k; ++r) {
+        const uint64_t e = ids[r];
+        rc = pko_ffn_silu(gate_type, gate + e * gate_slice, gate_slice, up_type, up + e * up_slice,
+                          up_slice, down_type, down + e * down_slice, down_slice, hidden, ffn, x,
+                          g, u, act, out);
+        if (rc) goto done;
+        const float route_scale = weights[r] * scale;
+        for (uint32_t i = 0; i < hidden; ++i) y[i] += route_scale * out[i];
+    }
+    rc = pko_linear(PKO_F32, (const uint8_t*)shared_router, (uint64_t)hidden * 4, hidden, 1, x,
+                    &gate_value);
+    if (!rc)
+        rc = pko_ffn_silu(sgate_type, sgate, sg_bytes, sup_type, sup, su_bytes, sdown_type, sdown,
+                          sd_bytes, hidden, shared_ffn, x, g, u, act, out);
+    if (rc) goto done;
+    {
+        const float shared_scale = pko_sigmoid35(gate_value);
+        for (uint32_t i = 0; i < hidden; ++i) y[i] = y[i] + shared_scale * out[i];
+    }
+    rc = 0;
+done:
+    free(logits);
+    free(g);
+    free(u);
+    free(act);
+    free(out);
+    return rc;
+}

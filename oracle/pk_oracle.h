@@ -73,6 +73,29 @@ int pko_moe_block(const float* router, uint32_t hidden, uint32_t n_experts, uint
                   uint32_t down_type, const uint8_t* down, uint32_t top_k, int normalize,
                   const float* x, float* y, uint32_t* ids, float* probabilities);
 
+/* select_experts (src/qwen35_runner.cpp:131-173): FP32 softmax over all
+ * logits (expf of logit - max, FP32 denominator summed in id order, FP32
+ * division), top-k by (logit desc, id asc), weights the selected
+ * probabilities, optional FP32 renormalisation.  Returns 2 on non-finite
+ * logits or an invalid softmax / selected sum, 1 on a bad top_k. */
+int pko_select_experts(const float* logits, uint32_t count, uint32_t top_k, int normalize,
+                       uint32_t* ids, float* weights);
+
+/* The Qwen3.5-MoE block for one token (src/qwen35_runner.cpp:690-761):
+ * select_experts over the F32 router; per route in order gate/up,
+ * silu(g) * u (sigmoid :111-115, silu :123), down, moe += (w * scale) * y;
+ * then the shared expert: gate value = shared_router . x, gate/up [hidden,
+ * shared_ffn], silu, down [shared_ffn, hidden], mixer = moe + sigmoid(gate
+ * value) * y_shared.  y receives mixer_output; weights the route weights
+ * before the scale. */
+int pko_moe35_block(const float* router, uint32_t hidden, uint32_t n_experts, uint32_t ffn,
+                    uint32_t gate_type, const uint8_t* gate, uint32_t up_type, const uint8_t* up,
+                    uint32_t down_type, const uint8_t* down, uint32_t top_k, int normalize,
+                    float scale, const float* shared_router, uint32_t shared_ffn,
+                    uint32_t sgate_type, const uint8_t* sgate, uint32_t sup_type,
+                    const uint8_t* sup, uint32_t sdown_type, const uint8_t* sdown,
+                    const float* x, float* y, uint32_t* ids, float* weights);
+
 #ifdef __cplusplus
 }
 #endif

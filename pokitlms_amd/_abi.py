@@ -25,7 +25,8 @@ EXPORTS = (
     "pk_hip_version", "pk_hip_type_supported", "pk_hip_create", "pk_hip_destroy",
     "pk_hip_upload", "pk_hip_upload_device", "pk_hip_weight_release", "pk_hip_weight_bytes",
     "pk_hip_weight_device_ptr", "pk_hip_matvec", "pk_hip_matvec_async", "pk_hip_moe_decode",
-    "pk_hip_moe_decode_async", "pk_hip_sync", "pk_hip_get_stats", "pk_hip_reset_stats",
+    "pk_hip_moe_decode_async", "pk_hip_moe35_decode", "pk_hip_moe35_decode_async", "pk_hip_sync",
+    "pk_hip_get_stats", "pk_hip_reset_stats",
     "pk_hip_set_kernel_timing", "pk_hip_device_name", "pk_hip_moe_prefill",
     "pk_hip_moe_prefill_async", "pk_hip_qwen3moe_create", "pk_hip_qwen3moe_destroy",
     "pk_hip_qwen3moe_generate", "pk_hip_synth_weight", "pk_hip_matvec_reference_order",
@@ -54,6 +55,12 @@ class MoeLayerDesc(ctypes.Structure):
     _fields_ = [("router", ctypes.c_void_p), ("gate", ctypes.c_void_p), ("up", ctypes.c_void_p),
                 ("down", ctypes.c_void_p), ("top_k", ctypes.c_uint32),
                 ("normalize", ctypes.c_uint32), ("scale", ctypes.c_float)]
+
+
+class Moe35LayerDesc(ctypes.Structure):
+    _fields_ = [("routed", MoeLayerDesc), ("shared_router", ctypes.c_void_p),
+                ("shared_gate", ctypes.c_void_p), ("shared_up", ctypes.c_void_p),
+                ("shared_down", ctypes.c_void_p)]
 
 
 class Qwen3MoeConfig(ctypes.Structure):
@@ -121,6 +128,11 @@ def lib() -> ctypes.CDLL:
     L.pk_hip_matvec_async.argtypes = [vp, vp, u32, vp, u32, vp, vp, cp, sz]
     L.pk_hip_moe_decode.restype = ctypes.c_int
     L.pk_hip_moe_decode.argtypes = [vp, ctypes.POINTER(MoeLayerDesc), fp, fp, up, fp, cp, sz]
+    L.pk_hip_moe35_decode.restype = ctypes.c_int
+    L.pk_hip_moe35_decode.argtypes = [vp, ctypes.POINTER(Moe35LayerDesc), fp, fp, up, fp, cp, sz]
+    L.pk_hip_moe35_decode_async.restype = ctypes.c_int
+    L.pk_hip_moe35_decode_async.argtypes = [vp, ctypes.POINTER(Moe35LayerDesc), vp, vp, vp, vp,
+                                            vp, cp, sz]
     L.pk_hip_moe_decode_async.restype = ctypes.c_int
     L.pk_hip_moe_decode_async.argtypes = [vp, ctypes.POINTER(MoeLayerDesc), vp, vp, vp, vp, vp,
                                           cp, sz]

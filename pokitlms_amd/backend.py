@@ -103,6 +103,27 @@ class MoeLayerHandles:
             w.release()
 
 
+class Moe35LayerHandles(MoeLayerHandles):
+    """A Qwen3.5-MoE layer resident in HBM: the routed experts plus the shared
+    expert (router vector, gate, up, down); ``scale`` = expert_weights_scale."""
+
+    def __init__(self, routed: MoeLayerHandles, shared_router: Weight, shared_gate: Weight,
+                 shared_up: Weight, shared_down: Weight):
+        super().__init__(routed.router, routed.gate, routed.up, routed.down, routed.top_k,
+                         routed.normalize, routed.scale)
+        self.shared = (shared_router, shared_gate, shared_up, shared_down)
+        self.desc35 = _abi.Moe35LayerDesc(self.desc, shared_router.handle, shared_gate.handle,
+                                          shared_up.handle, shared_down.handle)
+
+    def routed_bytes(self) -> int:
+        return super().routed_bytes() + sum(w.nbytes for w in self.shared)
+
+    def release(self) -> None:
+        super().release()
+        for w in self.shared:
+            w.release()
+
+
 class HipBackend:
     def __init__(self, device: int = 0, time_kernels: bool = False):
         L = _abi.lib()
@@ -154,6 +175,16 @@ class HipBackend:
         u = self.upload(layer.up_type, layer.hidden, layer.ffn, layer.up, layer.experts)
         d = self.upload(layer.down_type, layer.ffn, layer.hidden, layer.down, layer.experts)
         return MoeLayerHandles(r, g, u, d, layer.top_k, layer.normalize)
+
+    def upload_moe35_layer(self, layer: "S.Moe35Layer") -> Moe35LayerHandles:
+        routed = self.upload_moe_layer(layer)
+        routed = MoeLayerHandles(routed.router, routed.gate, routed.up, routed.down, layer.top_k,
+                                 layer.normalize, layer.scale)
+        sr = self.upload(S.F32, layer.hidden, 1, layer.shared_router)
+        sg = self.upload(layer.gate_type, layer.hidden, layer.shared_ffn, layer.shared_gate)
+        su = self.upload(layer.up_type, layer.hidden, layer.shared_ffn, layer.shared_up)
+        sd = self.upload(layer.down_type, layer.shared_ffn, layer.hidden, layer.shared_down)
+        return Moe35LayerHandles(routed, sr, sg, su, sd)
 
     # ---- matvec -----------------------------------------------------------------
     def matvec(self, w: Weight, x: np.ndarray, expert: int | None = None) -> np.ndarray:
@@ -220,6 +251,28 @@ class HipBackend:
                                             _f32p(y), ids.ctypes.data_as(ctypes.POINTER(ctypes.c_uint32)),
                                             _f32p(probs), err, _ERRBUF), err)
         return y, ids, probs
+
+    def moe35_decode(self, layer: Moe35LayerHandles, x: np.ndarray):
+        """The Qwen3.5-MoE block (src/qwen35_runner.cpp:670-764): mixer output,
+        route ids and weights (times expert_weights_scale)."""
+        xx = np.ascontiguousarray(x, dtype=np.float32)
+        y = np.empty(layer.hidden, dtype=np.float32)
+        ids = np.zeros(layer.top_k, dtype=np.uint32)
+        w = np.zeros(layer.top_k, dtype=np.float32)
+        err = ctypes.create_string_buffer(_ERRBUF)
+        _raise(_abi.lib().pk_hip_moe35_decode(self.handle, ctypes.byref(layer.desc35), _f32p(xx),
+                                              _f32p(y),
+                                              ids.ctypes.data_as(ctypes.POINTER(ctypes.c_uint32)),
+                                              _f32p(w), err, _ERRBUF), err)
+        return y, ids, w
+
+    def moe35_decode_async(self, layer: Moe35LayerHandles, device_x: int, device_y: int,
+                           device_ids: int, device_weights: int, stream: int = 0) -> None:
+        err = ctypes.create_string_buffer(_ERRBUF)
+        _raise(_abi.lib().pk_hip_moe35_decode_async(self.handle, ctypes.byref(layer.desc35),
+                                                    device_x, device_y, device_ids,
+                                                    device_weights, stream or None, err,
+                                                    _ERRBUF), err)
 
     def moe_decode_async(self, layer: MoeLayerHandles, device_x: int, device_y: int,
                          device_ids: int, device_probs: int, stream: int = 0) -> None:

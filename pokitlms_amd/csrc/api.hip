@@ -292,18 +292,56 @@ MoeShape check_decode_layer(pk_hip_ctx* c, const pk_hip_moe_layer* L) {
     return m;
 }
 
+// The Qwen3.5 layer's shared expert, checked against the routed experts.
+MoeShape check_decode35(pk_hip_ctx* c, const pk_hip_moe35_layer* L) {
+    if (!L) throw ArgError("MoE layer is required");
+    const MoeShape m = check_layer(c, &L->routed);
+    const pk_hip_weight* sw[4] = {L->shared_router, L->shared_gate, L->shared_up, L->shared_down};
+    for (const pk_hip_weight* w : sw) {
+        if (!w) throw ArgError("Qwen3.5 layer needs the shared expert's router, gate, up and down");
+        if (w->ctx != c) throw ArgError("weight handle does not belong to this context");
+        if (w->n_experts != 0) throw ArgError("shared expert tensors are plain matrices");
+    }
+    const pk_hip_weight *r = L->shared_router, *g = L->shared_gate, *u = L->shared_up,
+                        *d = L->shared_down;
+    if (r->in != m.hidden || r->out != 1) throw ArgError("shared expert router must be [hidden]");
+    if (g->in != m.hidden || u->in != m.hidden || u->out != g->out || d->in != g->out ||
+        d->out != m.hidden)
+        throw ArgError("shared expert dimensions do not match");
+    if (r->type != 0) throw Unsupported("shared expert router must be F32");
+    if (g->out != m.ffn || g->type != L->routed.gate->type || u->type != L->routed.up->type ||
+        d->type != L->routed.down->type)
+        throw Unsupported("shared expert must have the routed experts' types and width");
+    if (!pk::moe_decode_supported(L->routed.gate->type, L->routed.up->type,
+                                  L->routed.down->type, m.hidden, m.ffn, m.experts,
+                                  L->routed.top_k, 1))
+        throw Unsupported("MoE shape not covered by the HIP kernels");
+    return m;
+}
+
 void ensure_moe_scratch(pk_hip_ctx* c, const MoeShape& m, uint32_t top_k) {
-    c->act.ensure(static_cast<size_t>(top_k) * m.ffn);
-    c->row_sum.ensure(m.experts);
-    c->row_bound.ensure(m.experts);
+    // one more route and router row for a shared expert
+    c->act.ensure(static_cast<size_t>(top_k + 1) * m.ffn);
+    c->row_sum.ensure(m.experts + 1);
+    c->row_bound.ensure(m.experts + 1);
     c->ids.ensure(16);
     c->probs.ensure(16);
 }
 
 void enqueue_moe(pk_hip_ctx* c, const pk_hip_moe_layer* L, const MoeShape& m, const float* dx,
-                 float* dy, uint32_t* dids, float* dprobs, hipStream_t s) {
+                 float* dy, uint32_t* dids, float* dprobs, hipStream_t s,
+                 const pk_hip_moe35_layer* shared = nullptr) {
     ensure_moe_scratch(c, m, L->top_k);
     pk::MoeDecodeArgs a{};
+    if (shared) {
+        a.variant = 1;
+        a.shared_router = reinterpret_cast<const float*>(shared->shared_router->dptr);
+        a.shared_gate = shared->shared_gate->dptr;
+        a.shared_up = shared->shared_up->dptr;
+        a.shared_down = shared->shared_down->dptr;
+        c->stats.weight_bytes += shared->shared_router->nbytes + shared->shared_gate->nbytes +
+                                 shared->shared_up->nbytes + shared->shared_down->nbytes;
+    }
     a.router = reinterpret_cast<const float*>(L->router->dptr);
     a.gate = L->gate->dptr;
     a.up = L->up->dptr;
@@ -621,6 +659,55 @@ pk_hip_status pk_hip_moe_decode_async(pk_hip_ctx* ctx, const pk_hip_moe_layer* l
         ctx->set_device();
         hipStream_t s = stream ? static_cast<hipStream_t>(stream) : ctx->stream;
         enqueue_moe(ctx, layer, m, dx, dy, dids, dprobs, s);
+        if (ctx->time_kernels) {
+            check(hipStreamSynchronize(s), "hipStreamSynchronize");
+            collect_timing_moe(ctx);
+        }
+    });
+}
+
+pk_hip_status pk_hip_moe35_decode(pk_hip_ctx* ctx, const pk_hip_moe35_layer* layer,
+                                  const float* x, float* y, uint32_t* ids, float* weights,
+                                  char* err, size_t cap) {
+    return guarded(ctx, err, cap, [&] {
+        require_usable(ctx);
+        if (!x || !y || !ids || !weights) throw ArgError("input and output buffers are required");
+        std::lock_guard lock(ctx->mutex);
+        const MoeShape m = check_decode35(ctx, layer);
+        ctx->set_device();
+        ctx->x.ensure(m.hidden);
+        ctx->y.ensure(m.hidden);
+        ensure_moe_scratch(ctx, m, layer->routed.top_k);
+        check(hipMemcpyAsync(ctx->x.ptr, x, m.hidden * sizeof(float), hipMemcpyHostToDevice,
+                             ctx->stream),
+              "copy input");
+        enqueue_moe(ctx, &layer->routed, m, ctx->x.ptr, ctx->y.ptr, ctx->ids.ptr, ctx->probs.ptr,
+                    ctx->stream, layer);
+        check(hipMemcpyAsync(y, ctx->y.ptr, m.hidden * sizeof(float), hipMemcpyDeviceToHost,
+                             ctx->stream),
+              "copy output");
+        check(hipMemcpyAsync(ids, ctx->ids.ptr, layer->routed.top_k * sizeof(uint32_t),
+                             hipMemcpyDeviceToHost, ctx->stream),
+              "copy ids");
+        check(hipMemcpyAsync(weights, ctx->probs.ptr, layer->routed.top_k * sizeof(float),
+                             hipMemcpyDeviceToHost, ctx->stream),
+              "copy weights");
+        sync_and_check(ctx, ctx->stream);
+        collect_timing_moe(ctx);
+    });
+}
+
+pk_hip_status pk_hip_moe35_decode_async(pk_hip_ctx* ctx, const pk_hip_moe35_layer* layer,
+                                        const float* dx, float* dy, uint32_t* dids,
+                                        float* dweights, void* stream, char* err, size_t cap) {
+    return guarded(ctx, err, cap, [&] {
+        require_usable(ctx);
+        if (!dx || !dy || !dids || !dweights) throw ArgError("device buffers are required");
+        std::lock_guard lock(ctx->mutex);
+        const MoeShape m = check_decode35(ctx, layer);
+        ctx->set_device();
+        hipStream_t s = stream ? static_cast<hipStream_t>(stream) : ctx->stream;
+        enqueue_moe(ctx, &layer->routed, m, dx, dy, dids, dweights, s, layer);
         if (ctx->time_kernels) {
             check(hipStreamSynchronize(s), "hipStreamSynchronize");
             collect_timing_moe(ctx);

@@ -33,19 +33,28 @@ struct MoeDecodeArgs {
     uint32_t hidden, ffn, n_experts, top_k;
     uint32_t normalize;
     float scale;
+    // Qwen3.5-MoE (variant 1): select_experts weights, silu activations and
+    // the shared expert as route top_k (the routed experts' types and rows),
+    // weighted by sigmoid(shared_router . x) (router row n_experts)
+    uint32_t variant;
+    const float* shared_router;   // F32 [hidden]
+    const uint8_t* shared_gate;
+    const uint8_t* shared_up;
+    const uint8_t* shared_down;
     const float* x;          // [hidden]
     float* y;                // [hidden] moe_result
     uint32_t* ids;           // [top_k] route order
     float* probs;            // [top_k]
     // context scratch (device)
-    double* row_sum;         // [n_experts]
-    double* row_bound;       // [n_experts]
-    float* act;              // [top_k][ffn]
+    double* row_sum;         // [n_experts + variant]
+    double* row_bound;       // [n_experts + variant]
+    float* act;              // [top_k + variant][ffn]
     uint32_t* status;        // [4]: error flag, serial-fallback count, candidates, spare
 };
 
 bool moe_decode_supported(uint32_t gate_type, uint32_t up_type, uint32_t down_type,
-                          uint32_t hidden, uint32_t ffn, uint32_t n_experts, uint32_t top_k);
+                          uint32_t hidden, uint32_t ffn, uint32_t n_experts, uint32_t top_k,
+                          uint32_t variant = 0);
 hipError_t launch_moe_decode(const MoeDecodeArgs& a, hipStream_t stream);
 
 // Batched prefill: tokens independent single-token MoE blocks, grouped per

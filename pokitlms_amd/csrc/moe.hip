@@ -41,6 +41,14 @@ namespace {
 constexpr uint32_t kGateUpPasses = 2;  // row passes whose loads a gate/up wave keeps in flight
 constexpr uint32_t kDownPasses = 2;    // row passes per down workgroup
 
+// Qwen3.5's sigmoid and silu (src/qwen35_runner.cpp:111-123).
+__device__ __forceinline__ float sigmoid35(float v) {
+    if (v >= 0.0f) return 1.0f / (1.0f + expf(-v));
+    const float e = expf(v);
+    return e / (1.0f + e);
+}
+__device__ __forceinline__ float silu(float v) { return v * sigmoid35(v); }
+
 // ---------------------------------------------------------------------------
 // 1. Router: exact sum and serial-error bound of one expert row per workgroup.
 
@@ -48,10 +56,10 @@ template <int C>  // consecutive products per thread: hidden = 256 * C
 __global__ __launch_bounds__(kRouterThreads) void k_router(MoeDecodeArgs a) {
     __shared__ double wtot[kRouterThreads / 64];
     __shared__ double red[kRouterThreads / 64];
-    const uint32_t e = blockIdx.x;
+    const uint32_t e = blockIdx.x;  // row n_experts: the shared expert's gate (variant 1)
+    const float* row = e < a.n_experts ? a.router + static_cast<uint64_t>(e) * a.hidden : a.shared_router;
     float p[C];
-    router_products<C>(a.router + static_cast<uint64_t>(e) * a.hidden + threadIdx.x * C,
-                       a.x + threadIdx.x * C, p);
+    router_products<C>(row + threadIdx.x * C, a.x + threadIdx.x * C, p);
     double total, bound;
     router_sum_bound<C>(p, wtot, red, total, bound);
     if (threadIdx.x == 0) {
@@ -93,7 +101,7 @@ __global__ __launch_bounds__(256) void k_gate_up(MoeDecodeArgs a, uint32_t units
         valid[k] = u < units;
         pos[k] = unit_pos<T, UB>(valid[k] ? u : 0u);
     }
-    const uint32_t items = a.top_k * a.ffn;
+    const uint32_t items = (a.top_k + a.variant) * a.ffn;  // variant 1: the shared expert last
     const uint32_t passes = (items + RPP - 1u) / RPP;
     const uint32_t first = (blockIdx.x * (blockDim.x >> 6) + wave) * NP;
     uint32_t item[NP], route_of[NP];
@@ -155,8 +163,9 @@ __global__ __launch_bounds__(256) void k_gate_up(MoeDecodeArgs a, uint32_t units
 #pragma unroll
         for (uint32_t r = 0; r < kMaxTopK; ++r)
             if (route_of[q] == r) e = sel[r];
-        const uint8_t* gr = a.gate + static_cast<uint64_t>(e) * a.gate_slice + goff[q];
-        const uint8_t* ur = a.up + static_cast<uint64_t>(e) * a.up_slice + uoff[q];
+        const bool shared = route_of[q] >= a.top_k;
+        const uint8_t* gr = (shared ? a.shared_gate : a.gate + static_cast<uint64_t>(e) * a.gate_slice) + goff[q];
+        const uint8_t* ur = (shared ? a.shared_up : a.up + static_cast<uint64_t>(e) * a.up_slice) + uoff[q];
 #pragma unroll
         for (int k = 0; k < NU; ++k) {
             unit_load<T, UB>(gr, pos[k], rg[q][k]);
@@ -182,24 +191,27 @@ __global__ __launch_bounds__(256) void k_gate_up(MoeDecodeArgs a, uint32_t units
         }
         const float gs = group_sum_dyn(g[0], G);
         const float us = group_sum_dyn(u[0], G);
-        if (live && ul == G - 1u) a.act[item[q]] = (gs / (1.0f + expf(-gs))) * us;
+        if (live && ul == G - 1u)
+            a.act[item[q]] = a.variant ? silu(gs) * us : (gs / (1.0f + expf(-gs))) * us;
     }
 }
 
 
 // ---------------------------------------------------------------------------
-// 3. down + combine.  blockDim = 64 * top_k: wave k owns route k; the
-// workgroup covers kDownPasses * RPP output rows.
+// 3. down + combine.  blockDim = 64 * (top_k + variant): wave k owns route k
+// (variant 1: wave top_k the shared expert); the workgroup covers
+// kDownPasses * RPP output rows.
 
 template <int T, int UB, int NU, int kDownPasses>
-__global__ __launch_bounds__(64 * kMaxTopK) void k_down(MoeDecodeArgs a, uint32_t units,
+__global__ __launch_bounds__(64 * (kMaxTopK + 1)) void k_down(MoeDecodeArgs a, uint32_t units,
                                                          uint32_t glog2) {
-    extern __shared__ float part[];  // [top_k][kDownPasses * RPP]
+    extern __shared__ float part[];  // [top_k + variant][kDownPasses * RPP]
     const uint32_t lane = threadIdx.x & 63u, k = threadIdx.x >> 6;
     const uint32_t G = 1u << glog2, RPP = 64u >> glog2;
     const uint32_t sub = lane >> glog2, ul = lane & (G - 1u);
-    uint64_t e = a.ids[k];
-    const bool ok = e < a.n_experts;  // router error: ids are marked invalid, output unused
+    const bool shared = k >= a.top_k;
+    uint64_t e = shared ? 0u : a.ids[k];
+    const bool ok = shared || e < a.n_experts;  // router error: ids are invalid, output unused
     if (!ok) e = 0;
     UnitPos pos[NU];
     bool valid[NU];
@@ -209,7 +221,7 @@ __global__ __launch_bounds__(64 * kMaxTopK) void k_down(MoeDecodeArgs a, uint32_
         valid[q] = u < units;
         pos[q] = unit_pos<T, UB>(valid[q] ? u : 0u);
     }
-    const uint8_t* base = a.down + e * a.down_slice;
+    const uint8_t* base = shared ? a.shared_down : a.down + e * a.down_slice;
     const uint32_t rows = a.hidden;
     const uint32_t row0 = blockIdx.x * kDownPasses * RPP;
     // unconditional loads (rows past the end re-read the last row, unused)
@@ -238,6 +250,10 @@ __global__ __launch_bounds__(64 * kMaxTopK) void k_down(MoeDecodeArgs a, uint32_
         const float v = group_sum_dyn(acc[0], G);
         if (ul == G - 1u) part[k * RB + p * RPP + sub] = v;
     }
+    // variant 1: mixer_output = moe_result + sigmoid(shared gate) * shared output
+    // (src/qwen35_runner.cpp:752-761)
+    const float shared_scale =
+        a.variant ? sigmoid35(static_cast<float>(a.row_sum[a.n_experts])) : 0.0f;
     __syncthreads();
     for (uint32_t i = threadIdx.x; i < RB; i += blockDim.x) {
         const uint32_t orow = row0 + i;
@@ -245,6 +261,7 @@ __global__ __launch_bounds__(64 * kMaxTopK) void k_down(MoeDecodeArgs a, uint32_
             float y = 0.0f;
             for (uint32_t r = 0; r < a.top_k; ++r)
                 y = __fadd_rn(y, __fmul_rn(a.probs[r], part[r * RB + i]));
+            if (a.variant) y = __fadd_rn(y, __fmul_rn(shared_scale, part[a.top_k * RB + i]));
             a.y[orow] = y;
         }
     }
@@ -282,7 +299,7 @@ hipError_t gate_up_t(const MoeDecodeArgs& a, hipStream_t s) {
     uint32_t units, glog2, nu;
     if (!moe_plan<T>(a.hidden, units, glog2, nu)) return hipErrorInvalidValue;
     const uint32_t RPP = 64u >> glog2;
-    const uint32_t passes = ceil_div(a.top_k * a.ffn, RPP);
+    const uint32_t passes = ceil_div((a.top_k + a.variant) * a.ffn, RPP);
     const uint32_t blocks = ceil_div(passes, 4u * kGateUpPasses);
     const size_t lds = a.hidden * sizeof(float);
 #define PK_GU(N, NS)                                                                            \
@@ -307,10 +324,11 @@ hipError_t down_t(const MoeDecodeArgs& a, hipStream_t s) {
     if (!moe_plan<T>(a.ffn, units, glog2, nu)) return hipErrorInvalidValue;
     const uint32_t RPP = 64u >> glog2;
     const uint32_t blocks = ceil_div(a.hidden, kDownPasses * RPP);
-    const size_t lds = static_cast<size_t>(a.top_k) * kDownPasses * RPP * sizeof(float);
+    const uint32_t waves = a.top_k + a.variant;
+    const size_t lds = static_cast<size_t>(waves) * kDownPasses * RPP * sizeof(float);
 #define PK_DN(N)                                                                              \
     case N:                                                                                   \
-        hipLaunchKernelGGL((k_down<T, UB, N, kDownPasses>), dim3(blocks), dim3(64u * a.top_k), lds, s, a,  \
+        hipLaunchKernelGGL((k_down<T, UB, N, kDownPasses>), dim3(blocks), dim3(64u * waves), lds, s, a,  \
                            units, glog2);                                                     \
         break;
     switch (nu) { PK_DN(1) PK_DN(2) default: return hipErrorInvalidValue; }
@@ -346,17 +364,19 @@ bool router_width_ok(uint32_t hidden) {
 }  // namespace
 
 bool moe_decode_supported(uint32_t gate_type, uint32_t up_type, uint32_t down_type,
-                          uint32_t hidden, uint32_t ffn, uint32_t n_experts, uint32_t top_k) {
+                          uint32_t hidden, uint32_t ffn, uint32_t n_experts, uint32_t top_k,
+                          uint32_t variant) {
     return gate_type == up_type && quant_plan_ok(gate_type, hidden) &&
            quant_plan_ok(down_type, ffn) && n_experts >= 1 && n_experts <= kMaxExperts &&
-           top_k >= 1 && top_k <= kMaxTopK && top_k <= n_experts && router_width_ok(hidden);
+           top_k >= 1 && top_k <= kMaxTopK && top_k <= n_experts &&
+           variant <= 1u && router_width_ok(hidden);
 }
 
 hipError_t launch_moe_router(const MoeDecodeArgs& a, hipStream_t s) {
     switch (a.hidden / kRouterThreads) {
 #define PK_RT(C)                                                                                \
     case C:                                                                                     \
-        hipLaunchKernelGGL(k_router<C>, dim3(a.n_experts), dim3(kRouterThreads), a.hidden * sizeof(float), s, a); \
+        hipLaunchKernelGGL(k_router<C>, dim3(a.n_experts + a.variant), dim3(kRouterThreads), a.hidden * sizeof(float), s, a); \
         break;
         PK_RT(2) PK_RT(4) PK_RT(8) PK_RT(12) PK_RT(16) PK_RT(24) PK_RT(32)
 #undef PK_RT

@@ -292,10 +292,15 @@ __device__ __forceinline__ void write_routes(const MoeDecodeArgs& a, const uint3
     const uint32_t lane = threadIdx.x & 63u, K = a.top_k;
     const float mxf = slot_at<NS>(l, sel[0]);
     double ex = 0.0;
+    float exf = 0.0f;  // variant 1: select_experts' FP32 softmax (src/qwen35_runner.cpp:139-148)
 #pragma unroll
     for (int m = 0; m < NS; ++m)
-        if (lane + 64u * m < a.n_experts) ex += exp(static_cast<double>(l[m] - mxf));
-    const double denom = lane63(group_sum<64>(ex));
+        if (lane + 64u * m < a.n_experts) {
+            if (a.variant) exf += expf(l[m] - mxf);
+            else ex += exp(static_cast<double>(l[m] - mxf));
+        }
+    const double denom = a.variant ? 0.0 : lane63(group_sum<64>(ex));
+    const float denomf = a.variant ? lane63(group_sum<64>(exf)) : 0.0f;
     float mine = mxf;  // logit of route `lane`
     uint32_t my_id = 0u;
 #pragma unroll
@@ -309,7 +314,9 @@ __device__ __forceinline__ void write_routes(const MoeDecodeArgs& a, const uint3
         }
     }
     float p = 0.0f;
-    if (lane < K) p = static_cast<float>(exp(static_cast<double>(mine - mxf)) / denom);
+    if (lane < K)
+        p = a.variant ? expf(mine - mxf) / denomf
+                      : static_cast<float>(exp(static_cast<double>(mine - mxf)) / denom);
     float selected_sum = 0.0f;
     for (uint32_t r = 0; r < K; ++r)
         selected_sum = __fadd_rn(selected_sum, __builtin_bit_cast(float, __builtin_amdgcn_readlane(

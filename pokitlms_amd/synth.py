@@ -116,6 +116,44 @@ def moe_layer(seed: int, hidden: int = 2048, experts: int = 128, ffn: int = 768,
                     down_type, top_k, normalize)
 
 
+class Moe35Layer(MoeLayer):
+    """A Qwen3.5-MoE layer (src/qwen35_runner.cpp:670-764): the routed
+    experts of MoeLayer (``normalize`` = expert_weights_norm, ``scale`` =
+    expert_weights_scale) plus the shared expert: ``shared_router`` float32
+    ``(hidden,)``, ``shared_gate``/``shared_up`` ``hidden -> shared_ffn`` and
+    ``shared_down`` ``shared_ffn -> hidden`` GGUF payloads (uint8)."""
+
+    def __init__(self, base: MoeLayer, scale, shared_router, shared_gate, shared_up,
+                 shared_down, shared_ffn):
+        super().__init__(base.router, base.gate, base.up, base.down, base.hidden, base.experts,
+                         base.ffn, base.gate_type, base.up_type, base.down_type, base.top_k,
+                         base.normalize)
+        self.scale = scale
+        self.shared_router = shared_router
+        self.shared_gate, self.shared_up, self.shared_down = shared_gate, shared_up, shared_down
+        self.shared_ffn = shared_ffn
+
+    def routed_bytes(self) -> int:
+        return (super().routed_bytes() + self.shared_router.nbytes + self.shared_gate.nbytes +
+                self.shared_up.nbytes + self.shared_down.nbytes)
+
+
+def moe35_layer(seed: int, hidden: int = 2048, experts: int = 128, ffn: int = 768,
+                gate_type: int = Q4_K, up_type: int = Q4_K, down_type: int = Q6_K,
+                top_k: int = 8, normalize: bool = True, scale: float = 1.0,
+                router_std: float = 0.02) -> Moe35Layer:
+    """Seeded Qwen3.5-MoE layer; the shared expert has the routed experts'
+    types and width."""
+    base = moe_layer(seed, hidden, experts, ffn, gate_type, up_type, down_type, top_k,
+                     normalize, router_std)
+    gen = rng(seed + 7919)
+    shared_router = normal_f32(gen, hidden, router_std * 10.0)
+    sg = quant_matrix(gate_type, ffn, hidden, gen)
+    su = quant_matrix(up_type, ffn, hidden, gen)
+    sd = quant_matrix(down_type, hidden, ffn, gen)
+    return Moe35Layer(base, scale, shared_router, sg, su, sd, ffn)
+
+
 def dyadic_matrix(gtype: int, rows: int, in_features: int, gen: np.random.Generator) -> np.ndarray:
     """Random quant fields with power-of-two scales (2^-4 or 2^-3).
 
