@@ -202,14 +202,15 @@ __global__ __launch_bounds__(256) void k_gate_up(MoeDecodeArgs a, uint32_t units
 // (variant 1: wave top_k the shared expert); the workgroup covers
 // kDownPasses * RPP output rows.
 
-template <int T, int UB, int NU, int kDownPasses>
-__global__ __launch_bounds__(64 * (kMaxTopK + 1)) void k_down(MoeDecodeArgs a, uint32_t units,
-                                                         uint32_t glog2) {
+template <int T, int UB, int NU, int kDownPasses, bool SHARED>
+__global__ __launch_bounds__(64 * (kMaxTopK + (SHARED ? 1 : 0))) void k_down(MoeDecodeArgs a,
+                                                                            uint32_t units,
+                                                                            uint32_t glog2) {
     extern __shared__ float part[];  // [top_k + variant][kDownPasses * RPP]
     const uint32_t lane = threadIdx.x & 63u, k = threadIdx.x >> 6;
     const uint32_t G = 1u << glog2, RPP = 64u >> glog2;
     const uint32_t sub = lane >> glog2, ul = lane & (G - 1u);
-    const bool shared = k >= a.top_k;
+    const bool shared = SHARED && k >= a.top_k;
     uint64_t e = shared ? 0u : a.ids[k];
     const bool ok = shared || e < a.n_experts;  // router error: ids are invalid, output unused
     if (!ok) e = 0;
@@ -252,8 +253,7 @@ __global__ __launch_bounds__(64 * (kMaxTopK + 1)) void k_down(MoeDecodeArgs a, u
     }
     // variant 1: mixer_output = moe_result + sigmoid(shared gate) * shared output
     // (src/qwen35_runner.cpp:752-761)
-    const float shared_scale =
-        a.variant ? sigmoid35(static_cast<float>(a.row_sum[a.n_experts])) : 0.0f;
+    const float shared_scale = SHARED ? sigmoid35(static_cast<float>(a.row_sum[a.n_experts])) : 0.0f;
     __syncthreads();
     for (uint32_t i = threadIdx.x; i < RB; i += blockDim.x) {
         const uint32_t orow = row0 + i;
@@ -261,7 +261,7 @@ __global__ __launch_bounds__(64 * (kMaxTopK + 1)) void k_down(MoeDecodeArgs a, u
             float y = 0.0f;
             for (uint32_t r = 0; r < a.top_k; ++r)
                 y = __fadd_rn(y, __fmul_rn(a.probs[r], part[r * RB + i]));
-            if (a.variant) y = __fadd_rn(y, __fmul_rn(shared_scale, part[a.top_k * RB + i]));
+            if (SHARED) y = __fadd_rn(y, __fmul_rn(shared_scale, part[a.top_k * RB + i]));
             a.y[orow] = y;
         }
     }
@@ -326,12 +326,14 @@ hipError_t down_t(const MoeDecodeArgs& a, hipStream_t s) {
     const uint32_t blocks = ceil_div(a.hidden, kDownPasses * RPP);
     const uint32_t waves = a.top_k + a.variant;
     const size_t lds = static_cast<size_t>(waves) * kDownPasses * RPP * sizeof(float);
-#define PK_DN(N)                                                                              \
-    case N:                                                                                   \
-        hipLaunchKernelGGL((k_down<T, UB, N, kDownPasses>), dim3(blocks), dim3(64u * waves), lds, s, a,  \
-                           units, glog2);                                                     \
-        break;
-    switch (nu) { PK_DN(1) PK_DN(2) default: return hipErrorInvalidValue; }
+#define PK_DN(N, SH)                                                                          \
+    hipLaunchKernelGGL((k_down<T, UB, N, kDownPasses, SH>), dim3(blocks), dim3(64u * waves), lds, s, \
+                       a, units, glog2)
+    if (nu == 1 && !a.variant) PK_DN(1, false);
+    else if (nu == 2 && !a.variant) PK_DN(2, false);
+    else if (nu == 1) PK_DN(1, true);
+    else if (nu == 2) PK_DN(2, true);
+    else return hipErrorInvalidValue;
 #undef PK_DN
     return hipGetLastError();
 }

@@ -125,10 +125,11 @@ __device__ __forceinline__ uint32_t bf16_pair(float lo, float hi) {  // exact fo
     return __builtin_amdgcn_perm(__float_as_uint(hi), __float_as_uint(lo), 0x07060302u);
 }
 
-// Four unsigned byte fields (each < 256) to two dwords of bf16.
+// Four unsigned byte fields (each < 256) to two dwords of bf16: one
+// v_cvt_f32_ubyteN per field (no separate byte extraction), one v_perm per pair.
 __device__ __forceinline__ void bf16_bytes(uint32_t w, uint32_t& lo, uint32_t& hi) {
-    lo = bf16_pair(static_cast<float>(w & 0xffu), static_cast<float>((w >> 8) & 0xffu));
-    hi = bf16_pair(static_cast<float>((w >> 16) & 0xffu), static_cast<float>(w >> 24));
+    lo = bf16_pair(ub<0>(w), ub<1>(w));
+    hi = bf16_pair(ub<2>(w), ub<3>(w));
 }
 
 template <int T>
