@@ -108,6 +108,36 @@ __device__ __forceinline__ void raw32_load(const uint8_t* row, uint32_t k0, Raw3
     }
 }
 
+// Q4_K in the expert GEMM: a thread loads its row's whole block once (36
+// words) and takes each 32-value group's fields out of it, so the header and
+// the nibble bytes two groups share are fetched once per 256 values, not once
+// per group.
+template <int T>
+constexpr bool kq_blocked() { return T == T_Q4_K; }  // Q5_K's 44-word blocks would spill
+template <int T>
+constexpr int kq_block_words() { return T == T_Q4_K ? 36 : 44; }
+
+template <int T>
+__device__ __forceinline__ void kq_block_load(const uint8_t* row, uint32_t blk,
+                                              uint32_t (&w)[kq_block_words<T>()]) {
+    ld_words<kq_block_words<T>()>(row + blk * Fmt<T>::BB, w);
+}
+
+// The fields raw32_load would read for group j (0..7) of the block in w.
+template <int T>
+__device__ __forceinline__ void raw32_from_block(const uint32_t (&w)[kq_block_words<T>()], uint32_t j,
+                                                 Raw32<T>& r) {
+    constexpr uint32_t QS = T == T_Q4_K ? 4u : 12u;
+#pragma unroll
+    for (uint32_t i = 0; i < 4; ++i) r.h[i] = w[i];
+#pragma unroll
+    for (uint32_t i = 0; i < 8; ++i) r.q[i] = w[QS + 8u * (j / 2u) + i];
+    if constexpr (T == T_Q5_K) {
+#pragma unroll
+        for (uint32_t i = 0; i < 8; ++i) r.qh[i] = w[4u + i];
+    }
+}
+
 __device__ __forceinline__ uint32_t byte_of(const uint32_t* w, uint32_t i) {
     return (w[i >> 2] >> (8u * (i & 3u))) & 0xffu;
 }
@@ -503,6 +533,15 @@ __device__ __forceinline__ void gemm_src(GemmSrc<TW, DUAL>& g, const uint8_t* wr
 }
 
 template <int TW, bool DUAL>
+__device__ __forceinline__ void gemm_load_act(GemmPrefetch<TW, DUAL>& f, const GemmSrc<TW, DUAL>& g,
+                                              uint32_t k0) {
+    using C = GemmCfg<TW, DUAL>;
+    f.ap0 = *reinterpret_cast<const u32x4_t*>(g.ap0 + k0);
+    f.ap1 = *reinterpret_cast<const u32x4_t*>(g.ap1 + k0);
+    f.xs = g.xs[k0 / C::G];
+}
+
+template <int TW, bool DUAL>
 __device__ __forceinline__ void gemm_load(GemmPrefetch<TW, DUAL>& f, const GemmSrc<TW, DUAL>& g,
                                           uint32_t k0) {
     using C = GemmCfg<TW, DUAL>;
@@ -513,13 +552,14 @@ __device__ __forceinline__ void gemm_load(GemmPrefetch<TW, DUAL>& f, const GemmS
 }
 
 template <int TW, bool DUAL>
-__device__ __forceinline__ void gemm_store(GemmStage<TW, DUAL>& st, const GemmPrefetch<TW, DUAL>& f,
-                                           const GemmSrc<TW, DUAL>& g, uint32_t k0) {
+__device__ __forceinline__ void gemm_store_raw(GemmStage<TW, DUAL>& st, const Raw32<TW>& raw,
+                                               const GemmPrefetch<TW, DUAL>& f,
+                                               const GemmSrc<TW, DUAL>& g, uint32_t k0) {
     using C = GemmCfg<TW, DUAL>;
     const uint32_t tid = threadIdx.x, wr = tid % C::NRW, part = tid / C::NRW;
     uint32_t bw[16];
     float ds[2], cn[2];
-    raw32_bf16<TW>(f.raw, k0 + 32u * part, bw, ds, cn);
+    raw32_bf16<TW>(raw, k0 + 32u * part, bw, ds, cn);
     uint4* bd = reinterpret_cast<uint4*>(st.b + wr * C::SR + part * 64u);
 #pragma unroll
     for (uint32_t j = 0; j < 4; ++j)
@@ -532,6 +572,12 @@ __device__ __forceinline__ void gemm_store(GemmStage<TW, DUAL>& st, const GemmPr
     *reinterpret_cast<u32x4_t*>(st.a + g.adst0) = f.ap0;
     *reinterpret_cast<u32x4_t*>(st.a + g.adst1) = f.ap1;
     st.xs[g.xdst] = f.xs;
+}
+
+template <int TW, bool DUAL>
+__device__ __forceinline__ void gemm_store(GemmStage<TW, DUAL>& st, const GemmPrefetch<TW, DUAL>& f,
+                                           const GemmSrc<TW, DUAL>& g, uint32_t k0) {
+    gemm_store_raw<TW, DUAL>(st, f.raw, f, g, k0);
 }
 
 __device__ __forceinline__ bf16x8 lds_bf16x8(const uint8_t* p) {
@@ -631,12 +677,59 @@ __global__ __launch_bounds__(256, 2) void k_expert_gemm(MoePrefillArgs a) {
     const uint32_t nst = kdim / C::KC, last = nst - 1u;
     auto stage_k = [&](uint32_t s) { return (s < last ? s : last) * C::KC; };  // tail: harmless reloads
     GemmPrefetch<TW, DUAL> f0, f1;
+    f32x16 acc = {}, acc2 = {};
+    if constexpr (kq_blocked<TW>()) {
+        static_assert(C::KC == 32u, "one scale group per stage");
+        // Whole blocks in two register buffers: block 2i in bA, 2i + 1 in bB.
+        // Stage s is group s % 8 of block s / 8.  Step s computes stage s,
+        // stores stage s + 1 with its fields taken from the block buffers and
+        // loads stage s + 3's activations; bA is free after step 16i + 6 and bB
+        // after step 16i + 14, when the blocks 2i + 2 and 2i + 3 are loaded
+        // into them (nine steps ahead of their first use).  Steps past the
+        // last stage store and load harmless repeats (the block index is
+        // clamped; their data is never computed).
+        const uint32_t nblk = kdim / 256u, lastb = nblk - 1u;
+        constexpr int NW = kq_block_words<TW>();
+        uint32_t bA[NW], bB[NW];
+        kq_block_load<TW>(src.wrow, 0u, bA);
+        kq_block_load<TW>(src.wrow, 1u < lastb ? 1u : lastb, bB);
+        gemm_load_act<TW, DUAL>(f0, src, 0u);
+        gemm_load_act<TW, DUAL>(f1, src, stage_k(1u));
+        {
+            Raw32<TW> r;
+            raw32_from_block<TW>(bA, 0u, r);
+            gemm_store_raw<TW, DUAL>(st[0], r, f0, src, 0u);
+        }
+        gemm_load_act<TW, DUAL>(f0, src, stage_k(2u));
+        __syncthreads();
+        auto body = [&](uint32_t s0, uint32_t count) {
+#pragma unroll
+            for (uint32_t t = 0; t < 16u; ++t) {
+                if (t < count) {  // uniform: count is 16, or 8 for an odd block count's last pair
+                    const uint32_t s = s0 + t;
+                    GemmPrefetch<TW, DUAL>& f = (t & 1u) ? f0 : f1;
+                    gemm_compute<TW, DUAL>(st[s & 1u], acc, acc2);
+                    Raw32<TW> r;
+                    if (((t + 1u) / 8u) % 2u == 0u) raw32_from_block<TW>(bA, (t + 1u) % 8u, r);
+                    else raw32_from_block<TW>(bB, (t + 1u) % 8u, r);
+                    gemm_store_raw<TW, DUAL>(st[(s + 1u) & 1u], r, f, src, (s + 1u) * C::KC);
+                    gemm_load_act<TW, DUAL>(f, src, stage_k(s + 3u));
+                    const uint32_t b = s0 / 8u;
+                    if (t == 6u) kq_block_load<TW>(src.wrow, b + 2u < lastb ? b + 2u : lastb, bA);
+                    if (t == 14u) kq_block_load<TW>(src.wrow, b + 3u < lastb ? b + 3u : lastb, bB);
+                    __syncthreads();
+                }
+            }
+        };
+        uint32_t s = 0;
+        for (; s + 16u <= nst; s += 16u) body(s, 16u);
+        if (s < nst) body(s, nst - s);
+    } else {
     gemm_load<TW, DUAL>(f0, src, 0u);
     gemm_load<TW, DUAL>(f1, src, stage_k(1u));
     gemm_store<TW, DUAL>(st[0], f0, src, 0u);
     gemm_load<TW, DUAL>(f0, src, stage_k(2u));
     __syncthreads();
-    f32x16 acc = {}, acc2 = {};
     // Stage j's loads live in f(j % 2); step s computes stage s, stages s + 1
     // and loads s + 3.  The steps carry no conditions, so the load counters
     // the compiler tracks stay exact across the loop (two sets in flight).
@@ -653,6 +746,7 @@ __global__ __launch_bounds__(256, 2) void k_expert_gemm(MoePrefillArgs a) {
     }
     if (s + 1u < nst) step(s++, f1);
     gemm_compute<TW, DUAL>(st[s & 1u], acc, acc2);
+    }
     const uint32_t col = n0 + wave * 32u + (lane % 32u);
 #pragma unroll
     for (uint32_t r = 0; r < 16; ++r) {
