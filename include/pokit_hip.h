@@ -11,7 +11,7 @@
  * backends serialize with a mutex, src/vulkan_linear.cpp:635; C handles
  * require serialized calls, pokitlms.h:81).
  *
- * GGUF type ids: F32 0, F16 1, Q4_0 2, Q8_0 8, Q4_K 12, Q5_K 13, Q6_K 14,
+ * GGUF type ids: F32 0, F16 1, Q4_0 2, Q4_1 3, Q8_0 8, Q4_K 12, Q5_K 13, Q6_K 14,
  * BF16 30 (src/gguf_reader.cpp:21-57).  Matrices are GGUF [in, out] tensors:
  * `out` rows of `in` elements, each row a run of encoded blocks.  Expert
  * tensors are [in, out, n_experts] with the expert index slowest, so expert e
@@ -74,13 +74,14 @@ typedef struct pk_hip_stats {
     uint64_t router_launches, gate_up_launches, down_launches, matvec_launches;
     uint64_t prefill_calls, prefill_tokens, prefill_ns;
     uint64_t prefill_route_ns, prefill_gate_up_ns, prefill_down_ns;
+    uint64_t q4_1_dispatches;
 } pk_hip_stats;
 
 const char* pk_hip_version(void);
 
-/* Non-zero when `ggml_type` has a matvec kernel: F32/F16/BF16/Q4_0/Q8_0/
- * Q4_K/Q5_K/Q6_K, i.e. the Vulkan backend's type list
- * (src/vulkan_linear.cpp:78-83) without Q4_1. */
+/* Non-zero when `ggml_type` has a matvec kernel: F32/F16/BF16/Q4_0/Q4_1/
+ * Q8_0/Q4_K/Q5_K/Q6_K, i.e. the Vulkan backend's type list
+ * (src/vulkan_linear.cpp:78-83). */
 int pk_hip_type_supported(uint32_t ggml_type);
 
 /* Backend construction / destruction: VulkanLinearBackend ctor and dtor
@@ -140,7 +141,7 @@ pk_hip_status pk_hip_matvec_async(pk_hip_ctx* ctx, const pk_hip_weight* weight,
  * linear_quantized, linear: src/quantized_linear.cpp:360-423,
  * src/linear.cpp:10-31), so outputs equal the reference's bit for bit.
  * Slower than pk_hip_matvec (one serial chain per row and block); used by the
- * reference-order model decode.  F32 and Q4_0/Q8_0/Q4_K/Q5_K/Q6_K, width up
+ * reference-order model decode.  F32 and Q4_0/Q4_1/Q8_0/Q4_K/Q5_K/Q6_K, width up
  * to 8192.  Host buffers, batch 1. */
 pk_hip_status pk_hip_matvec_reference_order(pk_hip_ctx* ctx, const pk_hip_weight* weight,
                                            uint32_t expert, const float* x, float* y,

@@ -20,7 +20,7 @@
 uint32_t pko_block_elements(uint32_t type) {
     switch (type) {
         case PKO_F32: case PKO_F16: case PKO_BF16: return 1;
-        case PKO_Q4_0: case PKO_Q8_0: return 32;
+        case PKO_Q4_0: case PKO_Q4_1: case PKO_Q8_0: return 32;
         case PKO_Q4_K: case PKO_Q5_K: case PKO_Q6_K: return 256;
         default: return 0;
     }
@@ -31,6 +31,7 @@ uint32_t pko_block_bytes(uint32_t type) {
         case PKO_F32: return 4;
         case PKO_F16: case PKO_BF16: return 2;
         case PKO_Q4_0: return 18;
+        case PKO_Q4_1: return 20;
         case PKO_Q8_0: return 34;
         case PKO_Q4_K: return 144;
         case PKO_Q5_K: return 176;
@@ -171,6 +172,14 @@ static void unpack_q4_0(const uint8_t* packed, int8_t* out) {
     }
 }
 
+void pko_decode_q4_1(const uint8_t* blk, float* out) {
+    const float d = pko_half_to_float(rd16(blk)), m = pko_half_to_float(rd16(blk + 2));
+    for (unsigned i = 0; i < 16; ++i) {
+        out[i] = (float)(blk[4 + i] & 0x0fu) * d + m;
+        out[i + 16] = (float)(blk[4 + i] >> 4) * d + m;
+    }
+}
+
 int pko_dequantize_row(uint32_t type, const uint8_t* enc, uint64_t enc_bytes, float* out,
                        uint64_t count) {
     const uint32_t be = pko_block_elements(type), bb = pko_block_bytes(type);
@@ -189,6 +198,7 @@ int pko_dequantize_row(uint32_t type, const uint8_t* enc, uint64_t enc_bytes, fl
                 for (unsigned i = 0; i < 32; ++i) row[i] = scale * (float)q[i];
                 break;
             }
+            case PKO_Q4_1: pko_decode_q4_1(blk, row); break;  /* :453-469 */
             case PKO_Q4_K: pko_decode_q4_k(blk, row); break;
             case PKO_Q5_K: pko_decode_q5_k(blk, row); break;
             case PKO_Q6_K: pko_decode_q6_k(blk, row); break;
@@ -241,6 +251,11 @@ int pko_linear(uint32_t type, const uint8_t* w, uint64_t w_bytes, uint64_t in, u
                 if (type == PKO_Q4_0) unpack_q4_0(blk + 2, q);
                 else memcpy(q, blk + 2, 32);
                 sum += scale * dot_i8_f32(xb, q, 32);
+            } else if (type == PKO_Q4_1) {
+                /* linear_k<32, 20> with decode_q4_1 (src/quantized_linear.cpp:503-507) */
+                float dec[32];
+                pko_decode_q4_1(blk, dec);
+                sum += dot_f32(dec, xb, 32);
             } else {
                 /* linear_k (src/quantized_linear.cpp:374-384); on x86 Q4_K takes
                  * this decode-then-dot branch (:541-549). */

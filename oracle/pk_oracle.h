@@ -25,7 +25,7 @@ extern "C" {
 
 /* GGUF tensor type ids (reference src/gguf_reader.cpp:21-57). */
 enum {
-    PKO_F32 = 0, PKO_F16 = 1, PKO_Q4_0 = 2, PKO_Q8_0 = 8,
+    PKO_F32 = 0, PKO_F16 = 1, PKO_Q4_0 = 2, PKO_Q4_1 = 3, PKO_Q8_0 = 8,
     PKO_Q4_K = 12, PKO_Q5_K = 13, PKO_Q6_K = 14, PKO_BF16 = 30
 };
 
@@ -43,7 +43,11 @@ void pko_decode_q4_k(const uint8_t* block, float* out256);
 void pko_decode_q5_k(const uint8_t* block, float* out256);
 void pko_decode_q6_k(const uint8_t* block, float* out256);
 
-/* dequantize_quantized_row for Q4_0/Q8_0/Q4_K/Q5_K/Q6_K
+/* One 32-element Q4_1 block to F32: fl(fl(q * d) + m), low nibbles first
+ * (decode_q4_1, src/quantized_linear.cpp:53-62). */
+void pko_decode_q4_1(const uint8_t* block, float* out32);
+
+/* dequantize_quantized_row for Q4_0/Q4_1/Q8_0/Q4_K/Q5_K/Q6_K
  * (src/quantized_linear.cpp:427-493). */
 int pko_dequantize_row(uint32_t type, const uint8_t* encoded, uint64_t encoded_bytes,
                        float* out, uint64_t count);

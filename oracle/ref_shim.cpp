@@ -142,9 +142,16 @@ pkref_moe* pkref_moe_create(const float* router, std::uint32_t hidden, std::uint
         moe->router = std::make_unique<pokitlms::model::TensorReader>(
             make_reader(0, hidden, experts, router, std::uint64_t{hidden} * experts * 4));
         const auto slice_bytes = [](std::uint32_t type, std::uint64_t in, std::uint64_t out) {
-            const std::uint64_t block = type >= 12 ? 256 : 32;
-            const std::uint64_t bytes = type == 2 ? 18 : type == 8 ? 34 : type == 12 ? 144
-                                        : type == 13 ? 176 : 210;
+            std::uint64_t block = 32, bytes = 0;
+            switch (type) {  // src/gguf_reader.cpp:21-57
+                case 2: bytes = 18; break;
+                case 3: bytes = 20; break;
+                case 8: bytes = 34; break;
+                case 12: block = 256; bytes = 144; break;
+                case 13: block = 256; bytes = 176; break;
+                case 14: block = 256; bytes = 210; break;
+                default: throw std::invalid_argument("expert type outside the shim's list");
+            }
             return out * (in / block) * bytes;
         };
         const auto gs = slice_bytes(gate_type, hidden, ffn);

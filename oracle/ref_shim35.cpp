@@ -32,10 +32,20 @@ int status35_of_current_exception() {
     }
 }
 
+// Payload bytes of `rows` rows of `in` elements (the layouts of
+// src/gguf_reader.cpp:21-57); throws for a type these shims do not pass.
 std::uint64_t gguf_bytes(std::uint32_t type, std::uint64_t in, std::uint64_t rows) {
-    const std::uint64_t block = type >= 12 ? 256 : type == 0 ? 1 : 32;
-    const std::uint64_t bytes = type == 0 ? 4 : type == 2 ? 18 : type == 8 ? 34 : type == 12 ? 144
-                                : type == 13 ? 176 : 210;
+    std::uint64_t block = 32, bytes = 0;
+    switch (type) {
+        case 0: block = 1; bytes = 4; break;
+        case 2: bytes = 18; break;
+        case 3: bytes = 20; break;
+        case 8: bytes = 34; break;
+        case 12: block = 256; bytes = 144; break;
+        case 13: block = 256; bytes = 176; break;
+        case 14: block = 256; bytes = 210; break;
+        default: throw std::invalid_argument("tensor type outside the shim's list");
+    }
     return rows * (in / block) * bytes;
 }
 

@@ -47,7 +47,7 @@ void check(hipError_t e, const char* what) {
 uint32_t block_elements(uint32_t t) {
     switch (t) {
         case 0: case 1: case 30: return 1;
-        case 2: case 8: return 32;
+        case 2: case 3: case 8: return 32;
         case 12: case 13: case 14: return 256;
         default: return 0;
     }
@@ -58,6 +58,7 @@ uint32_t block_bytes(uint32_t t) {
         case 0: return 4;
         case 1: case 30: return 2;
         case 2: return 18;
+        case 3: return 20;
         case 8: return 34;
         case 12: return 144;
         case 13: return 176;
@@ -162,6 +163,7 @@ void count_dispatch(pk_hip_ctx* c, uint32_t type) {
     ++c->stats.dispatches;
     switch (type) {
         case 2: ++c->stats.q4_0_dispatches; break;
+        case 3: ++c->stats.q4_1_dispatches; break;
         case 8: ++c->stats.q8_0_dispatches; break;
         case 12: ++c->stats.q4_k_dispatches; break;
         case 13: ++c->stats.q5_k_dispatches; break;
@@ -424,7 +426,7 @@ const char* pk_hip_version(void) { return "0.1.0"; }
 
 int pk_hip_type_supported(uint32_t t) {
     switch (t) {
-        case 0: case 1: case 2: case 8: case 12: case 13: case 14: case 30: return 1;
+        case 0: case 1: case 2: case 3: case 8: case 12: case 13: case 14: case 30: return 1;
         default: return 0;
     }
 }

@@ -66,6 +66,10 @@ template <>
 struct RefBlock<T_Q4_0> {
     static constexpr uint32_t BE = 32, BB = 18;
 };
+template <>
+struct RefBlock<T_Q4_1> {
+    static constexpr uint32_t BE = 32, BB = 20;
+};
 
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
@@ -127,9 +131,9 @@ __device__ __forceinline__ float q6_step4(float s, float dsc, uint32_t v, float4
 
 // dot of one block with x (x in LDS, 16-byte aligned), in element order.
 // The whole block is loaded into registers first (whole words; the 2-byte
-// aligned formats through v_alignbyte).  K-quants: the decoded FP32 weight
-// times x; Q8_0/Q4_0: d * dot_i8_f32 (the int8 value times x, then the scale
-// once).
+// aligned formats through v_alignbyte).  K-quants and Q4_1: the decoded FP32
+// weight times x; Q8_0/Q4_0: d * dot_i8_f32 (the int8 value times x, then the
+// scale once).
 template <int T>
 __device__ float block_dot(const uint8_t* blk, const float* x) {
     const float4* x4 = reinterpret_cast<const float4*>(x);
@@ -187,6 +191,20 @@ __device__ float block_dot(const uint8_t* blk, const float* x) {
             }
         }
         s = __fmul_rn(half_bits_to_float(w[0] & 0xffffu), s);
+    } else if constexpr (T == T_Q4_1) {  // weight fl(fl(q * d) + m), low nibbles first
+        uint32_t w[5];                   // d | m << 16, then quants 0..15
+        ld_words<5>(blk, w);
+        const float d = half_bits_to_float(w[0] & 0xffffu), m = half_bits_to_float(w[0] >> 16);
+#pragma unroll
+        for (uint32_t k = 0; k < 8; ++k) {
+            const uint32_t raw = w[1u + (k & 3u)];
+            const uint32_t v = k < 4u ? raw & 0x0f0f0f0fu : (raw >> 4) & 0x0f0f0f0fu;
+            const float4 xv = x4[k];
+            s = __fadd_rn(s, __fmul_rn(__fadd_rn(__fmul_rn(ub<0>(v), d), m), xv.x));
+            s = __fadd_rn(s, __fmul_rn(__fadd_rn(__fmul_rn(ub<1>(v), d), m), xv.y));
+            s = __fadd_rn(s, __fmul_rn(__fadd_rn(__fmul_rn(ub<2>(v), d), m), xv.z));
+            s = __fadd_rn(s, __fmul_rn(__fadd_rn(__fmul_rn(ub<3>(v), d), m), xv.w));
+        }
     } else {  // Q4_0: low nibbles are elements 0..15, high 16..31
         uint32_t w[5];
         ld_words_2a<5>(blk, w);
@@ -704,7 +722,7 @@ __global__ __launch_bounds__(256) void k_ref_attention(ModelArgs a, ModelLayer L
 }
 
 uint32_t ref_block_elems(uint32_t type) {
-    return type == T_Q8_0 || type == T_Q4_0 ? 32u : 256u;
+    return type == T_Q8_0 || type == T_Q4_0 || type == T_Q4_1 ? 32u : 256u;
 }
 
 template <int T>
@@ -723,6 +741,7 @@ hipError_t ref_matvec_launch(uint32_t type, const RefMatvecArgs& a, uint32_t blo
         case T_Q6_K: return ref_matvec_t<T_Q6_K>(a, blocks, routes, s);
         case T_Q8_0: return ref_matvec_t<T_Q8_0>(a, blocks, routes, s);
         case T_Q4_0: return ref_matvec_t<T_Q4_0>(a, blocks, routes, s);
+        case T_Q4_1: return ref_matvec_t<T_Q4_1>(a, blocks, routes, s);
         default: return hipErrorInvalidValue;
     }
 }
@@ -734,7 +753,7 @@ bool ref_matvec_supported(uint32_t type, uint32_t in) {
         case T_F32: return in >= 1u && in <= kMaxRefWidth;
         case T_Q4_K: case T_Q5_K: case T_Q6_K:
             return in % 256u == 0u && in <= kMaxRefWidth && in / 256u <= 256u;
-        case T_Q8_0: case T_Q4_0: return in % 32u == 0u && in <= kMaxRefWidth && in / 32u <= 256u;
+        case T_Q8_0: case T_Q4_0: case T_Q4_1: return in % 32u == 0u && in <= kMaxRefWidth && in / 32u <= 256u;
         default: return false;
     }
 }

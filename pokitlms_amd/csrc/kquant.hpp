@@ -18,7 +18,7 @@
 namespace pk {
 
 enum : uint32_t {
-    T_F32 = 0, T_F16 = 1, T_Q4_0 = 2, T_Q8_0 = 8, T_Q4_K = 12, T_Q5_K = 13, T_Q6_K = 14,
+    T_F32 = 0, T_F16 = 1, T_Q4_0 = 2, T_Q4_1 = 3, T_Q8_0 = 8, T_Q4_K = 12, T_Q5_K = 13, T_Q6_K = 14,
     T_BF16 = 30
 };
 
@@ -30,6 +30,7 @@ template <> struct Fmt<T_Q5_K> { static constexpr int BE = 256, BB = 176, PRIM =
 template <> struct Fmt<T_Q6_K> { static constexpr int BE = 256, BB = 210, PRIM = 128, RUNS = 2, MAXUB = 16; };
 template <> struct Fmt<T_Q8_0> { static constexpr int BE = 32, BB = 34, PRIM = 32, RUNS = 1, MAXUB = 16; };
 template <> struct Fmt<T_Q4_0> { static constexpr int BE = 32, BB = 18, PRIM = 16, RUNS = 2, MAXUB = 16; };
+template <> struct Fmt<T_Q4_1> { static constexpr int BE = 32, BB = 20, PRIM = 16, RUNS = 2, MAXUB = 16; };
 
 // ---------------------------------------------------------------------------
 // Loads.  Q4_K/Q5_K blocks (144/176 B) keep 16-byte alignment; Q6_K (210 B),
@@ -155,7 +156,7 @@ __device__ __forceinline__ UnitPos unit_pos(uint32_t u) {
     } else if constexpr (T == T_Q8_0) {
         p.col[0] = base + k0;
         p.col[1] = p.col[0];
-    } else {  // Q4_0
+    } else {  // Q4_0, Q4_1: low nibbles are elements 0..15, high nibbles 16..31
         p.col[0] = base + k0;
         p.col[1] = p.col[0] + 16u;
     }
@@ -217,7 +218,13 @@ __device__ __forceinline__ void unit_load(const uint8_t* __restrict__ row, const
                                           UnitRaw<T, UB>& r) {
     constexpr int NW = UB / 4;
     const uint8_t* blk = row + p.boff;
-    if constexpr (T == T_Q4_K || T == T_Q5_K) {
+    if constexpr (T == T_Q4_1) {  // 20-byte blocks keep 4-byte alignment: d, m, then quants
+        ld_weights<1>(blk, r.h);
+        uint32_t q[NW];
+        ld_weights<NW>(blk + 4 + p.k0, q);
+#pragma unroll
+        for (int i = 0; i < NW; ++i) r.q[i] = q[i];
+    } else if constexpr (T == T_Q4_K || T == T_Q5_K) {
         ld_weights<4>(blk, r.h);
         uint32_t q[NW];
         ld_weights<NW>(blk + (T == T_Q4_K ? 16 : 48) + p.k0, q);
@@ -317,6 +324,22 @@ __device__ __forceinline__ void unit_compute(const UnitRaw<T, UB>& r, const Unit
         const float d = half_bits_to_float(r.d);
 #pragma unroll
         for (int b = 0; b < B; ++b) acc[b] += d * __builtin_fmaf(-128.0f, ux.s[b][0], dot0[b]);
+    } else if constexpr (T == T_Q4_1) {  // w = d * q + m (decode_q4_1, src/quantized_linear.cpp:53-62)
+#pragma unroll
+        for (int t = 0; t < NW; ++t) {
+            const uint32_t lo = r.q[t] & 0x0f0f0f0fu;
+            const uint32_t hi = (r.q[t] >> 4) & 0x0f0f0f0fu;
+#pragma unroll
+            for (int b = 0; b < B; ++b) {
+                dot0[b] = dot4(lo, &ux.v[b][4 * t], dot0[b]);
+                dot1[b] = dot4(hi, &ux.v[b][UB + 4 * t], dot1[b]);
+            }
+        }
+        const float d = half_bits_to_float(r.h[0] & 0xffffu);
+        const float m = half_bits_to_float(r.h[0] >> 16);
+#pragma unroll
+        for (int b = 0; b < B; ++b)
+            acc[b] += __builtin_fmaf(d, dot0[b] + dot1[b], m * (ux.s[b][0] + ux.s[b][1]));
     } else {  // Q4_0
 #pragma unroll
         for (int t = 0; t < NW; ++t) {

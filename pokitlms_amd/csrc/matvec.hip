@@ -290,6 +290,7 @@ bool matvec_supported(uint32_t type, uint32_t in, uint32_t batch) {
     switch (type) {
         case T_F32: case T_F16: case T_BF16: return true;
         case T_Q4_0: return supported_q<T_Q4_0>(in, batch);
+        case T_Q4_1: return supported_q<T_Q4_1>(in, batch);
         case T_Q8_0: return supported_q<T_Q8_0>(in, batch);
         case T_Q4_K: return supported_q<T_Q4_K>(in, batch);
         case T_Q5_K: return supported_q<T_Q5_K>(in, batch);
@@ -307,6 +308,7 @@ hipError_t launch_matvec(uint32_t type, const uint8_t* W, uint64_t row_bytes, ui
         case T_F16: return dispatch_batch_f<T_F16>(batch, W, row_bytes, rows, x, in, y, stream);
         case T_BF16: return dispatch_batch_f<T_BF16>(batch, W, row_bytes, rows, x, in, y, stream);
         case T_Q4_0: return dispatch_batch_q<T_Q4_0>(batch, W, row_bytes, rows, x, in, y, stream);
+        case T_Q4_1: return dispatch_batch_q<T_Q4_1>(batch, W, row_bytes, rows, x, in, y, stream);
         case T_Q8_0: return dispatch_batch_q<T_Q8_0>(batch, W, row_bytes, rows, x, in, y, stream);
         case T_Q4_K: return dispatch_batch_q<T_Q4_K>(batch, W, row_bytes, rows, x, in, y, stream);
         case T_Q5_K: return dispatch_batch_q<T_Q5_K>(batch, W, row_bytes, rows, x, in, y, stream);

@@ -347,6 +347,7 @@ bool plan_ok(uint32_t in) {
 bool quant_plan_ok(uint32_t type, uint32_t in) {
     switch (type) {
         case T_Q4_0: return plan_ok<T_Q4_0>(in);
+        case T_Q4_1: return plan_ok<T_Q4_1>(in);
         case T_Q8_0: return plan_ok<T_Q8_0>(in);
         case T_Q4_K: return plan_ok<T_Q4_K>(in);
         case T_Q5_K: return plan_ok<T_Q5_K>(in);
@@ -390,6 +391,7 @@ hipError_t launch_moe_router(const MoeDecodeArgs& a, hipStream_t s) {
 hipError_t launch_moe_gate_up(const MoeDecodeArgs& a, hipStream_t s) {
     switch (a.gate_type) {
         case T_Q4_0: return gate_up_t<T_Q4_0>(a, s);
+        case T_Q4_1: return gate_up_t<T_Q4_1>(a, s);
         case T_Q8_0: return gate_up_t<T_Q8_0>(a, s);
         case T_Q4_K: return gate_up_t<T_Q4_K>(a, s);
         case T_Q5_K: return gate_up_t<T_Q5_K>(a, s);
@@ -401,6 +403,7 @@ hipError_t launch_moe_gate_up(const MoeDecodeArgs& a, hipStream_t s) {
 hipError_t launch_moe_down(const MoeDecodeArgs& a, hipStream_t s) {
     switch (a.down_type) {
         case T_Q4_0: return down_t<T_Q4_0>(a, s);
+        case T_Q4_1: return down_t<T_Q4_1>(a, s);
         case T_Q8_0: return down_t<T_Q8_0>(a, s);
         case T_Q4_K: return down_t<T_Q4_K>(a, s);
         case T_Q5_K: return down_t<T_Q5_K>(a, s);

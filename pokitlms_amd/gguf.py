@@ -24,7 +24,7 @@ DEFAULT_ALIGNMENT = 32
 U8, I8, U16, I16, U32, I32, F32T, BOOL, STRING, ARRAY, U64, I64, F64T = range(13)
 
 # (block elements, block bytes) of the tensor types this build reads or writes
-TYPE_LAYOUT = {0: (1, 4), 1: (1, 2), 30: (1, 2), 2: (32, 18), 8: (32, 34), 12: (256, 144),
+TYPE_LAYOUT = {0: (1, 4), 1: (1, 2), 30: (1, 2), 2: (32, 18), 3: (32, 20), 8: (32, 34), 12: (256, 144),
                13: (256, 176), 14: (256, 210)}
 
 

@@ -36,6 +36,7 @@ std::size_t encoded_row_bytes(std::uint32_t type, std::uint64_t in) {
         case 0: return in * 4;
         case 1: case 30: return in * 2;
         case 2: return in % 32 ? 0 : in / 32 * 18;
+        case 3: return in % 32 ? 0 : in / 32 * 20;
         case 8: return in % 32 ? 0 : in / 32 * 34;
         case 12: return in % 256 ? 0 : in / 256 * 144;
         case 13: return in % 256 ? 0 : in / 256 * 176;
@@ -46,7 +47,7 @@ std::size_t encoded_row_bytes(std::uint32_t type, std::uint64_t in) {
 
 bool block_aligned(std::uint32_t type, std::uint64_t in) {
     switch (type) {
-        case 2: case 8: return in % 32 == 0;
+        case 2: case 3: case 8: return in % 32 == 0;
         case 12: case 13: case 14: return in % 256 == 0;
         default: return true;
     }
@@ -278,7 +279,7 @@ HipLinearStats HipLinearBackend::stats() const {
         out.q4_k_dispatches = s.q4_k_dispatches;
         out.q5_k_dispatches = s.q5_k_dispatches;
         out.q6_k_dispatches = s.q6_k_dispatches;
-        out.other_dispatches = s.float_dispatches;
+        out.other_dispatches = s.float_dispatches + s.q4_1_dispatches;
         out.weight_bytes = s.weight_bytes;
         out.gpu_time_ns = s.matvec_ns + s.router_ns + s.gate_up_ns + s.down_ns;
         out.resident_bytes = s.resident_bytes;

@@ -50,7 +50,7 @@ struct HipLinearStats {
     std::uint64_t q4_k_dispatches{};
     std::uint64_t q5_k_dispatches{};
     std::uint64_t q6_k_dispatches{};
-    std::uint64_t other_dispatches{};    // F32 / F16 / BF16
+    std::uint64_t other_dispatches{};    // F32 / F16 / BF16 / Q4_1
     std::uint64_t weight_bytes{};        // algorithmic weight bytes streamed
     std::uint64_t gpu_time_ns{};         // with HipLinearOptions::time_kernels
     std::uint64_t resident_bytes{};      // device bytes of resident tensors

@@ -9,7 +9,7 @@ Randomness: NumPy ``Generator(PCG64(seed))``.  Quant fields are uniform random
 bytes; every fp16 scale (``d``, ``dmin``) is ``|N(0, std)|`` rounded to
 binary16; activations are ``N(0, 1)`` float32; the F32 router is
 ``N(0, 0.02)``.  Block layouts follow the reference decoders
-(src/quantized_linear.cpp:166-205, 286-358, 387-423 of the reference).
+(src/quantized_linear.cpp:53-62, 166-205, 286-358, 387-423 of the reference).
 """
 from __future__ import annotations
 
@@ -17,14 +17,18 @@ import hashlib
 
 import numpy as np
 
-F32, F16, Q4_0, Q8_0, Q4_K, Q5_K, Q6_K, BF16 = 0, 1, 2, 8, 12, 13, 14, 30
+F32, F16, Q4_0, Q4_1, Q8_0, Q4_K, Q5_K, Q6_K, BF16 = 0, 1, 2, 3, 8, 12, 13, 14, 30
 
-TYPE_NAMES = {F32: "F32", F16: "F16", Q4_0: "Q4_0", Q8_0: "Q8_0", Q4_K: "Q4_K",
+TYPE_NAMES = {F32: "F32", F16: "F16", Q4_0: "Q4_0", Q4_1: "Q4_1", Q8_0: "Q8_0", Q4_K: "Q4_K",
               Q5_K: "Q5_K", Q6_K: "Q6_K", BF16: "BF16"}
-BLOCK_ELEMENTS = {F32: 1, F16: 1, BF16: 1, Q4_0: 32, Q8_0: 32, Q4_K: 256, Q5_K: 256, Q6_K: 256}
-BLOCK_BYTES = {F32: 4, F16: 2, BF16: 2, Q4_0: 18, Q8_0: 34, Q4_K: 144, Q5_K: 176, Q6_K: 210}
+BLOCK_ELEMENTS = {F32: 1, F16: 1, BF16: 1, Q4_0: 32, Q4_1: 32, Q8_0: 32, Q4_K: 256, Q5_K: 256,
+                  Q6_K: 256}
+BLOCK_BYTES = {F32: 4, F16: 2, BF16: 2, Q4_0: 18, Q4_1: 20, Q8_0: 34, Q4_K: 144, Q5_K: 176,
+               Q6_K: 210}
 # Byte offsets of the fp16 scale fields inside one block.
-SCALE_OFFSETS = {Q4_0: (0,), Q8_0: (0,), Q4_K: (0, 2), Q5_K: (0, 2), Q6_K: (208,)}
+SCALE_OFFSETS = {Q4_0: (0,), Q4_1: (0, 2), Q8_0: (0,), Q4_K: (0, 2), Q5_K: (0, 2), Q6_K: (208,)}
+# Scale fields stored negative: Q4_1's m is the block minimum, w = q * d + m.
+NEGATIVE_SCALES = {Q4_1: (2,)}
 
 
 def rng(seed: int) -> np.random.Generator:
@@ -71,6 +75,8 @@ def quant_matrix(gtype: int, rows: int, in_features: int, gen: np.random.Generat
     blocks = gen.integers(0, 256, size=(nblocks, bb), dtype=np.uint8)
     for off in SCALE_OFFSETS[gtype]:
         blocks[:, off:off + 2] = half_abs_normal(gen, nblocks, scale_std).view(np.uint8).reshape(-1, 2)
+    for off in NEGATIVE_SCALES.get(gtype, ()):
+        blocks[:, off + 1] |= 0x80  # binary16 sign bit
     return blocks.reshape(rows, -1)
 
 
@@ -171,6 +177,8 @@ def dyadic_matrix(gtype: int, rows: int, in_features: int, gen: np.random.Genera
     for off in SCALE_OFFSETS[gtype]:
         exps = gen.integers(-4, -2, size=blocks.shape[0])
         blocks[:, off:off + 2] = np.ldexp(1.0, exps).astype(np.float16).view(np.uint8).reshape(-1, 2)
+    for off in NEGATIVE_SCALES.get(gtype, ()):
+        blocks[:, off + 1] |= 0x80
     if gtype == Q6_K:
         blocks[:, 192:208] = (gen.integers(-8, 8, size=(blocks.shape[0], 16))
                               .astype(np.int8).view(np.uint8))

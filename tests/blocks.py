@@ -2,7 +2,7 @@
 
 Each encoder writes chosen integer fields into one GGUF block following the
 published layouts (the reference decoders' field order, restated in
-src/quantized_linear.cpp:166-205, 286-358, 387-423) and returns the block with
+src/quantized_linear.cpp:53-62, 166-205, 286-358, 387-423) and returns the block with
 the value every element must decode to, computed in float64 from the fields.
 They share no code with the decoders under test.
 """
@@ -90,3 +90,14 @@ def q4_0_block(d, q):
     for i in range(16):
         b[2 + i] = ((int(q[i]) + 8) & 15) | (((int(q[16 + i]) + 8) & 15) << 4)
     return bytes(b), np.array([d * v for v in q])
+
+
+def q4_1_block(d, m, q):
+    """q: 32 ints in [0, 15]; element i = d*q[i] + m, element i < 16 in the
+    low nibble of byte i, element 16 + i in its high nibble."""
+    b = bytearray(20)
+    b[0:2] = _f16(d)
+    b[2:4] = _f16(m)
+    for i in range(16):
+        b[4 + i] = (int(q[i]) & 15) | ((int(q[16 + i]) & 15) << 4)
+    return bytes(b), np.array([d * v + m for v in q])

@@ -25,7 +25,7 @@ from pokitlms_amd import synth as S  # noqa: E402
 
 OUT = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden.npz")
 
-C2_TYPES = (S.Q4_0, S.Q8_0, S.Q4_K, S.Q5_K, S.Q6_K)
+C2_TYPES = (S.Q4_0, S.Q4_1, S.Q8_0, S.Q4_K, S.Q5_K, S.Q6_K)
 C2_SHAPES = ((2048, 6144), (6144, 2048))  # (rows, in) = out x in
 
 
@@ -97,7 +97,7 @@ def main():
             ys = np.stack([ref.linear(t, w, inn, rows, xs[b]) for b in range(8)])
             out[key + "_ysum"] = np.array(S.digest(ys))
 
-    for t in (S.F32, S.F16, S.BF16, S.Q4_0, S.Q8_0, S.Q4_K, S.Q5_K, S.Q6_K):
+    for t in (S.F32, S.F16, S.BF16, S.Q4_0, S.Q4_1, S.Q8_0, S.Q4_K, S.Q5_K, S.Q6_K):
         w, x, inn = small_inputs(t)
         key = f"small_{S.TYPE_NAMES[t]}"
         out[key + "_digest"] = np.array(S.digest(w, x))

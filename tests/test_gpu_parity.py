@@ -15,7 +15,7 @@ from tests.golden import make_golden as G
 
 pytestmark = pytest.mark.gpu
 
-QUANT = (S.Q4_0, S.Q8_0, S.Q4_K, S.Q5_K, S.Q6_K)
+QUANT = (S.Q4_0, S.Q4_1, S.Q8_0, S.Q4_K, S.Q5_K, S.Q6_K)
 FLOAT = (S.F32, S.F16, S.BF16)
 TOL = 1e-4
 
@@ -266,7 +266,8 @@ def test_router_near_ties_take_the_exact_path(hip, port):
 def test_moe_shapes_and_normalisation(hip, port, normalize):
     for (hidden, experts, ffn, k, gt, dt) in ((512, 16, 256, 2, S.Q4_K, S.Q6_K),
                                              (1024, 64, 512, 8, S.Q5_K, S.Q8_0),
-                                             (2048, 128, 768, 8, S.Q4_0, S.Q4_K)):
+                                             (2048, 128, 768, 8, S.Q4_0, S.Q4_K),
+                                             (1024, 32, 512, 4, S.Q4_1, S.Q4_1)):
         layer = S.moe_layer(seed=70 + hidden, hidden=hidden, experts=experts, ffn=ffn,
                             gate_type=gt, up_type=gt, down_type=dt, top_k=k,
                             normalize=normalize)

@@ -3,7 +3,7 @@ call sites: tests/native/hip_backend_cases.cpp, built by ``make -C oracle
 cases`` against the reference headers and CPU library in place.
 
 On the GPU it runs every case: try_linear through tensor_linear's backend hook
-(src/tensor_linear.cpp:213) for F32/F16/BF16/Q4_0/Q8_0/Q4_K/Q5_K/Q6_K against
+(src/tensor_linear.cpp:213) for F32/F16/BF16/Q4_0/Q4_1/Q8_0/Q4_K/Q5_K/Q6_K against
 the CPU kernels; false for the formats without a kernel; shape errors;
 file-backed tensors kept resident; the MoE block hook against the reference
 MoE block (ids exact, outputs normwise <= 1e-4); a non-finite router as a
@@ -44,5 +44,6 @@ def test_native_backend_cases():
     assert r.returncode == 0, r.stdout[-3000:]
     lines = r.stdout.splitlines()
     assert not [l for l in lines if l.startswith("FAIL")]
-    assert sum(l.startswith("PASS try_linear_parity") for l in lines) == 8
+    assert sum(l.startswith("PASS try_linear_parity") for l in lines) == 9
+    assert sum(l.startswith("PASS try_linear_unsupported") for l in lines) == 4
     assert sum(l.startswith("PASS moe_block_parity") for l in lines) == 2

@@ -16,7 +16,7 @@ from pokitlms_amd import synth as S
 from tests import blocks as KB
 from tests.golden import make_golden as G
 
-QUANT = (S.Q4_0, S.Q8_0, S.Q4_K, S.Q5_K, S.Q6_K)
+QUANT = (S.Q4_0, S.Q4_1, S.Q8_0, S.Q4_K, S.Q5_K, S.Q6_K)
 
 
 def bits(a):
@@ -71,6 +71,7 @@ def test_known_answer_blocks(port, seed):
                                                g.integers(-32, 32, 256)))
     _check_block(port, S.Q8_0, *KB.q8_0_block(d, g.integers(-128, 128, 32)))
     _check_block(port, S.Q4_0, *KB.q4_0_block(d, g.integers(-8, 8, 32)))
+    _check_block(port, S.Q4_1, *KB.q4_1_block(d, -dmin, g.integers(0, 16, 32)))
 
 
 def test_planted_mistake_is_caught():
