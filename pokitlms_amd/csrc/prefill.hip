@@ -108,33 +108,74 @@ __device__ __forceinline__ void raw32_load(const uint8_t* row, uint32_t k0, Raw3
     }
 }
 
-// Q4_K in the expert GEMM: a thread loads its row's whole block once (36
-// words) and takes each 32-value group's fields out of it, so the header and
-// the nibble bytes two groups share are fetched once per 256 values, not once
-// per group.
+// Q4_K and Q6_K in the expert GEMM: a thread loads a run of its row's
+// stages at once into registers (a unit) and takes each 32-value group's
+// fields out of it, so the fields several groups share are fetched once per
+// unit, not once per group.
+//  * Q4_K: the whole 144-byte block (36 words), eight stages; the header is
+//    shared by all eight groups, each nibble byte by two.
+//  * Q6_K: one 128-value half of a block, four stages: its 64 ql bytes (each
+//    shared by two groups), 32 qh bytes (shared by four), 8 scale bytes and d.
+//    Blocks are 210 bytes, so consecutive blocks alternate between 4- and
+//    2-byte alignment: each field is loaded as the dwords covering it (one
+//    extra) and realigned by the unit's `shift` when decoded.
+// (Q5_K's 44-word blocks would spill.)
 template <int T>
-constexpr bool kq_blocked() { return T == T_Q4_K; }  // Q5_K's 44-word blocks would spill
-template <int T>
-constexpr int kq_block_words() { return T == T_Q4_K ? 36 : 44; }
+constexpr bool kq_blocked() { return T == T_Q4_K || T == T_Q6_K; }
 
 template <int T>
-__device__ __forceinline__ void kq_block_load(const uint8_t* row, uint32_t blk,
-                                              uint32_t (&w)[kq_block_words<T>()]) {
-    ld_words<kq_block_words<T>()>(row + blk * Fmt<T>::BB, w);
+struct KqUnit;
+template <>
+struct KqUnit<T_Q4_K> {
+    static constexpr uint32_t STAGES = 8, PER_ROW_BLOCK = 1;
+    uint32_t w[36];
+};
+template <>
+struct KqUnit<T_Q6_K> {
+    static constexpr uint32_t STAGES = 4, PER_ROW_BLOCK = 2;
+    uint32_t ql[17], qh[9], sc[3];
+    uint32_t d, shift;
+};
+
+// Unit u of a row: block u / PER_ROW_BLOCK (Q6_K: half u % 2 of it).
+template <int T>
+__device__ __forceinline__ void kq_unit_load(const uint8_t* row, uint32_t u, KqUnit<T>& U) {
+    if constexpr (T == T_Q4_K) {
+        ld_words<36>(row + u * 144u, U.w);
+    } else {
+        const uint8_t* blk = row + (u / 2u) * 210u;
+        const uint32_t h = u % 2u;
+        U.shift = align_shift(blk);
+        const uint8_t* base = blk - U.shift;  // field offsets below are multiples of 4
+        ld_words<17>(base + 64u * h, U.ql);
+        ld_words<9>(base + 128u + 32u * h, U.qh);
+        ld_words<3>(base + 192u + 8u * h, U.sc);
+        U.d = ld_u16(blk + 208u);
+    }
 }
 
-// The fields raw32_load would read for group j (0..7) of the block in w.
+// The fields raw32_load would read for stage j of the unit in U (Q4_K: group
+// j of 8 in the block; Q6_K: group 4h + j of the block).
 template <int T>
-__device__ __forceinline__ void raw32_from_block(const uint32_t (&w)[kq_block_words<T>()], uint32_t j,
-                                                 Raw32<T>& r) {
-    constexpr uint32_t QS = T == T_Q4_K ? 4u : 12u;
+__device__ __forceinline__ void raw32_from_unit(const KqUnit<T>& U, uint32_t j, Raw32<T>& r) {
+    if constexpr (T == T_Q4_K) {
 #pragma unroll
-    for (uint32_t i = 0; i < 4; ++i) r.h[i] = w[i];
+        for (uint32_t i = 0; i < 4; ++i) r.h[i] = U.w[i];
 #pragma unroll
-    for (uint32_t i = 0; i < 8; ++i) r.q[i] = w[QS + 8u * (j / 2u) + i];
-    if constexpr (T == T_Q5_K) {
+        for (uint32_t i = 0; i < 8; ++i) r.q[i] = U.w[4u + 8u * (j / 2u) + i];
+    } else {
+        const uint32_t o = 8u * (j & 1u);  // low or high 32 ql bytes of the half
 #pragma unroll
-        for (uint32_t i = 0; i < 8; ++i) r.qh[i] = w[4u + i];
+        for (uint32_t i = 0; i < 8; ++i) r.ql[i] = U.ql[o + i];
+        r.ql8 = U.ql[o + 8u];
+#pragma unroll
+        for (uint32_t i = 0; i < 8; ++i) r.qh[i] = U.qh[i];
+        r.qh8 = U.qh[8];
+        const uint32_t sw = j < 2u ? __builtin_amdgcn_alignbyte(U.sc[1], U.sc[0], U.shift)
+                                   : __builtin_amdgcn_alignbyte(U.sc[2], U.sc[1], U.shift);
+        r.sc = (sw >> (16u * (j & 1u))) & 0xffffu;  // int8 scales of both 16-halves
+        r.d = U.d;
+        r.shift = U.shift;
     }
 }
 
@@ -679,50 +720,52 @@ __global__ __launch_bounds__(256, 2) void k_expert_gemm(MoePrefillArgs a) {
     GemmPrefetch<TW, DUAL> f0, f1;
     f32x16 acc = {}, acc2 = {};
     if constexpr (kq_blocked<TW>()) {
-        static_assert(C::KC == 32u, "one scale group per stage");
-        // Whole blocks in two register buffers: block 2i in bA, 2i + 1 in bB.
-        // Stage s is group s % 8 of block s / 8.  Step s computes stage s,
-        // stores stage s + 1 with its fields taken from the block buffers and
-        // loads stage s + 3's activations; bA is free after step 16i + 6 and bB
-        // after step 16i + 14, when the blocks 2i + 2 and 2i + 3 are loaded
-        // into them (nine steps ahead of their first use).  Steps past the
-        // last stage store and load harmless repeats (the block index is
-        // clamped; their data is never computed).
-        const uint32_t nblk = kdim / 256u, lastb = nblk - 1u;
-        constexpr int NW = kq_block_words<TW>();
-        uint32_t bA[NW], bB[NW];
-        kq_block_load<TW>(src.wrow, 0u, bA);
-        kq_block_load<TW>(src.wrow, 1u < lastb ? 1u : lastb, bB);
+        static_assert(C::KC == 32u, "one 32-value group per stage");
+        // Units in two register buffers: unit 2i in bA, 2i + 1 in bB.  Stage
+        // s is stage s % US of unit s / US.  Step s computes stage s, stores
+        // stage s + 1 with its fields taken from the unit buffers and loads
+        // stage s + 3's activations; bA is free after step 2US*i + US - 2 and
+        // bB after step 2US*i + 2US - 2, when units 2i + 2 and 2i + 3 are
+        // loaded into them (US + 1 steps ahead of their first use).  Steps
+        // past the last stage store and load harmless repeats (the unit
+        // index is clamped; their data is never computed).
+        using U = KqUnit<TW>;
+        constexpr uint32_t US = U::STAGES;
+        const uint32_t lastu = kdim / 256u * U::PER_ROW_BLOCK - 1u;
+        U bA, bB;
+        kq_unit_load<TW>(src.wrow, 0u, bA);
+        kq_unit_load<TW>(src.wrow, 1u < lastu ? 1u : lastu, bB);
         gemm_load_act<TW, DUAL>(f0, src, 0u);
         gemm_load_act<TW, DUAL>(f1, src, stage_k(1u));
         {
             Raw32<TW> r;
-            raw32_from_block<TW>(bA, 0u, r);
+            raw32_from_unit<TW>(bA, 0u, r);
             gemm_store_raw<TW, DUAL>(st[0], r, f0, src, 0u);
         }
         gemm_load_act<TW, DUAL>(f0, src, stage_k(2u));
         __syncthreads();
         auto body = [&](uint32_t s0, uint32_t count) {
 #pragma unroll
-            for (uint32_t t = 0; t < 16u; ++t) {
-                if (t < count) {  // uniform: count is 16, or 8 for an odd block count's last pair
+            for (uint32_t t = 0; t < 2u * US; ++t) {
+                if (t < count) {  // uniform: count is 2US except for the last steps
                     const uint32_t s = s0 + t;
                     GemmPrefetch<TW, DUAL>& f = (t & 1u) ? f0 : f1;
                     gemm_compute<TW, DUAL>(st[s & 1u], acc, acc2);
                     Raw32<TW> r;
-                    if (((t + 1u) / 8u) % 2u == 0u) raw32_from_block<TW>(bA, (t + 1u) % 8u, r);
-                    else raw32_from_block<TW>(bB, (t + 1u) % 8u, r);
+                    if (((t + 1u) / US) % 2u == 0u) raw32_from_unit<TW>(bA, (t + 1u) % US, r);
+                    else raw32_from_unit<TW>(bB, (t + 1u) % US, r);
                     gemm_store_raw<TW, DUAL>(st[(s + 1u) & 1u], r, f, src, (s + 1u) * C::KC);
                     gemm_load_act<TW, DUAL>(f, src, stage_k(s + 3u));
-                    const uint32_t b = s0 / 8u;
-                    if (t == 6u) kq_block_load<TW>(src.wrow, b + 2u < lastb ? b + 2u : lastb, bA);
-                    if (t == 14u) kq_block_load<TW>(src.wrow, b + 3u < lastb ? b + 3u : lastb, bB);
+                    const uint32_t u = s0 / US;
+                    if (t == US - 2u) kq_unit_load<TW>(src.wrow, u + 2u < lastu ? u + 2u : lastu, bA);
+                    if (t == 2u * US - 2u)
+                        kq_unit_load<TW>(src.wrow, u + 3u < lastu ? u + 3u : lastu, bB);
                     __syncthreads();
                 }
             }
         };
         uint32_t s = 0;
-        for (; s + 16u <= nst; s += 16u) body(s, 16u);
+        for (; s + 2u * US <= nst; s += 2u * US) body(s, 2u * US);
         if (s < nst) body(s, nst - s);
     } else {
     gemm_load<TW, DUAL>(f0, src, 0u);
