@@ -191,6 +191,8 @@ def prefill_leg(torch, hip, layers, stream, reps: int, cpu_ms_per_token):
                      "avg_us": round(phase_us["gate_up"], 2),
                      "algorithmic_flops": PREFILL_GEMM_FLOPS["gate_up"]},
         "phase_us": {k: round(v, 2) for k, v in phase_us.items()},
+        "router_fallbacks_per_batch": st["router_fallbacks"] / n,
+        "router_candidates_per_batch": st["router_candidates"] / n,
         "expert_load": {"max": int(counts.max()), "touched": int((counts > 0).sum()),
                         "zipf_fit": round(S.zipf_fit(counts), 3)},
         "parity_vs_decode": {"ids_equal": ids_ok, "normwise_rel": worst, "tokens": 128},

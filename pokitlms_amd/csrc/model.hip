@@ -100,6 +100,18 @@ template <int T>
 __device__ void decode32(const uint8_t* row, uint32_t k0, float* v) {
     if constexpr (T == T_F32) {
         for (uint32_t i = 0; i < 32; ++i) v[i] = reinterpret_cast<const float*>(row)[k0 + i];
+    } else if constexpr (T == T_F16 || T == T_BF16) {  // read_float_rows_into (src/tensor_reader.cpp:164-198)
+        const uint16_t* h = reinterpret_cast<const uint16_t*>(row) + k0;
+        for (uint32_t i = 0; i < 32; ++i)
+            v[i] = T == T_F16 ? half_bits_to_float(h[i]) : __uint_as_float(static_cast<uint32_t>(h[i]) << 16);
+    } else if constexpr (T == T_Q4_1) {  // decode_q4_1: fl(fl(q * d) + m) (src/quantized_linear.cpp:53-62)
+        const uint8_t* blk = row + (k0 / 32u) * 20u;
+        const float d = half_bits_to_float(blk[0] | (blk[1] << 8));
+        const float m = half_bits_to_float(blk[2] | (blk[3] << 8));
+        for (uint32_t i = 0; i < 16; ++i) {
+            v[i] = __fadd_rn(__fmul_rn(static_cast<float>(blk[4 + i] & 15u), d), m);
+            v[i + 16] = __fadd_rn(__fmul_rn(static_cast<float>(blk[4 + i] >> 4), d), m);
+        }
     } else if constexpr (T == T_Q4_K || T == T_Q5_K) {
         const uint8_t* blk = row + (k0 / 256u) * Fmt<T>::BB;
         const uint32_t j = (k0 % 256u) / 32u, chunk = j / 2u, hi = j & 1u;
@@ -281,8 +293,10 @@ hipError_t embed_t(const ModelArgs& a, hipStream_t s) {
 }  // namespace
 
 bool model_supported(const ModelArgs& a) {
-    const bool embd_ok = a.embd_type == T_F32 || a.embd_type == T_Q4_K || a.embd_type == T_Q5_K ||
-                         a.embd_type == T_Q6_K || a.embd_type == T_Q8_0 || a.embd_type == T_Q4_0;
+    // the matvec types (the reference also dequantizes Q5_0/Q5_1/Q2_K/Q3_K rows)
+    const bool embd_ok = a.embd_type == T_F32 || a.embd_type == T_F16 || a.embd_type == T_BF16 ||
+                         a.embd_type == T_Q4_K || a.embd_type == T_Q5_K || a.embd_type == T_Q6_K ||
+                         a.embd_type == T_Q8_0 || a.embd_type == T_Q4_0 || a.embd_type == T_Q4_1;
     return embd_ok && a.head_dim >= 2u && a.head_dim <= 256u && a.head_dim % 64u == 0u &&
            a.kv_heads >= 1u && a.heads % a.kv_heads == 0u && a.hidden % 256u == 0u &&
            a.capacity >= 1u && a.capacity <= kMaxModelContext;
@@ -307,6 +321,9 @@ hipError_t launch_model_step(const ModelArgs& a, const ModelLayer* layers, bool 
     hipError_t err = hipSuccess;
     switch (a.embd_type) {
         case T_F32: err = embed_t<T_F32>(a, s); break;
+        case T_F16: err = embed_t<T_F16>(a, s); break;
+        case T_BF16: err = embed_t<T_BF16>(a, s); break;
+        case T_Q4_1: err = embed_t<T_Q4_1>(a, s); break;
         case T_Q4_K: err = embed_t<T_Q4_K>(a, s); break;
         case T_Q5_K: err = embed_t<T_Q5_K>(a, s); break;
         case T_Q6_K: err = embed_t<T_Q6_K>(a, s); break;

@@ -134,7 +134,7 @@ __global__ __launch_bounds__(256) void k_gate_up(MoeDecodeArgs a, uint32_t units
     }
     uint32_t sel[kMaxTopK];
     if (state == 1u) {  // rare: exact serial logits of the candidates
-        exact_routes(a, sr.lo_min_sel, xs, fb, blockIdx.x == 0);
+        exact_routes<4>(a, sr.lo_min_sel, xs, fb, blockIdx.x == 0);
         if (fb.bad) {  // uniform
             if (first_wave) flag_router_error(a);
             return;

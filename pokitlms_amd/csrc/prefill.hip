@@ -332,7 +332,7 @@ __global__ __launch_bounds__(256) void k_route_batch(MoePrefillArgs A) {
     }
     uint32_t sel[kMaxTopK];
     if (state == 1u) {  // rare: exact serial logits of the candidates
-        exact_routes(a, s_lo, xs, fb, true);
+        exact_routes<8>(a, s_lo, xs, fb, true);
         if (fb.bad) {
             if (wave == 0) flag_router_error(a);
             return;

@@ -43,37 +43,9 @@ __device__ __forceinline__ double block_reduce_d(double v, double* red) {
     return r;
 }
 
-// The CPU's router logit, bit for bit: s = fl(s + fl(w_i * x_i)), i ascending,
-// then linear()'s bias-free 0.0F + dot (src/linear.cpp:203-204).  Two register
-// buffers of 32 weights ping-pong so loads run ahead of the dependent add
-// chain (hidden is a multiple of 256).
-__device__ __forceinline__ void serial_add32(float& s, const float4 (&w)[8], const float* xv) {
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-        s = __fadd_rn(s, __fmul_rn(w[j].x, xv[4 * j + 0]));
-        s = __fadd_rn(s, __fmul_rn(w[j].y, xv[4 * j + 1]));
-        s = __fadd_rn(s, __fmul_rn(w[j].z, xv[4 * j + 2]));
-        s = __fadd_rn(s, __fmul_rn(w[j].w, xv[4 * j + 3]));
-    }
-}
-
-__device__ __forceinline__ float serial_logit(const float* __restrict__ w,
-                                              const float* __restrict__ xs, uint32_t hidden) {
-    float s = 0.0f;
-    float4 a[8], b[8];
-#pragma unroll
-    for (int j = 0; j < 8; ++j) a[j] = *reinterpret_cast<const float4*>(w + 4 * j);
-    for (uint32_t i = 0; i < hidden; i += 64) {
-#pragma unroll
-        for (int j = 0; j < 8; ++j) b[j] = *reinterpret_cast<const float4*>(w + i + 32 + 4 * j);
-        serial_add32(s, a, xs + i);
-        const uint32_t next = i + 64 < hidden ? i + 64 : i;  // last pair: harmless reload
-#pragma unroll
-        for (int j = 0; j < 8; ++j) a[j] = *reinterpret_cast<const float4*>(w + next + 4 * j);
-        serial_add32(s, b, xs + i + 32);
-    }
-    return __fadd_rn(0.0f, s);
-}
+// (ext_vector_type arrays stay in registers; arrays of HIP's float4 class
+// can be left in scratch.)
+typedef float rf32x4 __attribute__((ext_vector_type(4)));
 
 // Ranks of all experts by key_before over v[0..E), two threads per expert
 // (E <= blockDim/2) or one; selected ids in rank order land in sel[0..K).
@@ -249,33 +221,126 @@ __device__ __forceinline__ WaveRoutes<NS> wave_route(const MoeDecodeArgs& a, con
     return w;
 }
 
-// Exact routing of an uncertified token, by the whole workgroup (rare).
+// Exact routing of an uncertified token, by the whole workgroup of 256
+// threads (rare).  The candidate experts' serial logits are chains of
+// dependent adds; fed from global memory one chunk ahead, each chunk would
+// wait a full memory latency.  Instead the workgroup streams the candidate
+// rows through LDS: up to kStageRows rows at a time, kStageChunk values per
+// row and chunk, D chunks in flight in registers spread over all threads,
+// two LDS buffers; one thread per candidate runs the chain over the staged
+// chunk.
+constexpr uint32_t kStageRows = 16;
+constexpr uint32_t kStageChunk = 128;               // hidden is a multiple of 4 chunks
+constexpr uint32_t kStageStride = kStageChunk + 4;  // floats: rows start on different banks
+
 struct FallbackShared {
     double logit[kMaxExperts];
     uint32_t rank[kMaxExperts];
     uint32_t sel[kMaxTopK];
+    uint32_t cand[kMaxExperts];
+    uint32_t ncand;
     uint32_t bad;  // a non-finite exact logit
+    alignas(16) float stage[2][kStageRows * kStageStride];
 };
 
+// D chunks in flight: 4 in the decode gate/up kernel (its register budget),
+// 8 in the prefill ranking kernel.
+template <uint32_t D>
 __device__ __forceinline__ void exact_routes(const MoeDecodeArgs& a, double lo_min_sel,
                                              const float* xs, FallbackShared& fb, bool count) {
-    const uint32_t t = threadIdx.x, E = a.n_experts;
+    constexpr uint32_t CH = kStageChunk;
+    constexpr uint32_t PIECES = kStageRows * CH / 4u;  // float4 pieces per chunk: 2 per thread
+    static_assert(PIECES == 512u, "two pieces per thread of 256");
+    const uint32_t t = threadIdx.x, E = a.n_experts, H = a.hidden;
+    if (t == 0) {
+        fb.ncand = 0u;
+        fb.bad = 0u;
+    }
+    __syncthreads();
     if (t < E) {
         const double s = a.row_sum[t], b = a.row_bound[t];
         // An expert with hi < lo_min_sel is below k certain experts; every other
         // expert gets its exact CPU logit.  FP32 rounding of S keeps the rest
         // below lo_min_sel (|fl(S) - S| <= u|S| <= bound).
-        if (!(s + b < lo_min_sel)) {
-            fb.logit[t] = static_cast<double>(
-                serial_logit(a.router + static_cast<uint64_t>(t) * a.hidden, xs, a.hidden));
-            if (count) atomicAdd(a.status + ST_CANDIDATES, 1u);
-        } else {
-            fb.logit[t] = static_cast<double>(static_cast<float>(s));
-        }
+        if (!(s + b < lo_min_sel)) fb.cand[atomicAdd(&fb.ncand, 1u)] = t;
+        else fb.logit[t] = static_cast<double>(static_cast<float>(s));
     }
-    if (t == 0 && count) atomicAdd(a.status + ST_FALLBACKS, 1u);
-    if (t == 0) fb.bad = 0u;
     __syncthreads();
+    const uint32_t nc = fb.ncand, nch = H / CH;
+    if (t == 0 && count) {
+        atomicAdd(a.status + ST_FALLBACKS, 1u);
+        atomicAdd(a.status + ST_CANDIDATES, nc);
+    }
+    for (uint32_t g0 = 0; g0 < nc; g0 += kStageRows) {
+        const uint32_t rows = nc - g0 < kStageRows ? nc - g0 : kStageRows;
+        const float* src[2];
+        uint32_t dst[2], xcol[2];
+#pragma unroll
+        for (uint32_t p = 0; p < 2; ++p) {
+            const uint32_t q = t + 256u * p, r = q / (CH / 4u), col = 4u * (q % (CH / 4u));
+            const uint32_t rr = r < rows ? r : 0u;  // rows past the group repeat row 0's loads
+            src[p] = a.router + static_cast<uint64_t>(fb.cand[g0 + rr]) * H + col;
+            dst[p] = r * kStageStride + col;
+            xcol[p] = col;
+        }
+        rf32x4 ring[D][2];
+#pragma unroll
+        for (uint32_t d = 0; d + 1u < D; ++d)
+#pragma unroll
+            for (uint32_t p = 0; p < 2; ++p)
+                ring[d][p] = *reinterpret_cast<const rf32x4*>(src[p] + (d < nch ? d : nch - 1u) * CH);
+        float s = 0.0f;
+        for (uint32_t c0 = 0; c0 < nch; c0 += D) {
+#pragma unroll
+            for (uint32_t k = 0; k < D; ++k) {
+                const uint32_t c = c0 + k;
+                if (c >= nch) break;  // uniform; only when nch is not a multiple of D
+                const uint32_t cn = c + D - 1u < nch ? c + D - 1u : nch - 1u;  // tail: harmless reload
+                // stage the CPU's rounded products fl(w_i * x_i); the chain then
+                // only adds (dot_f32's order, src/simd_kernels.hpp:12-24)
+#pragma unroll
+                for (uint32_t p = 0; p < 2; ++p) {
+                    const rf32x4 xv = *reinterpret_cast<const rf32x4*>(xs + c * CH + xcol[p]);
+                    rf32x4 pr;
+                    pr.x = __fmul_rn(ring[k][p].x, xv.x);
+                    pr.y = __fmul_rn(ring[k][p].y, xv.y);
+                    pr.z = __fmul_rn(ring[k][p].z, xv.z);
+                    pr.w = __fmul_rn(ring[k][p].w, xv.w);
+                    *reinterpret_cast<rf32x4*>(&fb.stage[c & 1u][dst[p]]) = pr;
+                    ring[(k + D - 1u) % D][p] = *reinterpret_cast<const rf32x4*>(src[p] + cn * CH);
+                }
+                __syncthreads();
+                if (t < rows) {
+                    // 32 products in registers while the previous 32 are added, so
+                    // the dependent adds do not wait on LDS latency
+                    const float* pr = &fb.stage[c & 1u][t * kStageStride];
+                    rf32x4 A[8], B[8];
+#pragma unroll
+                    for (uint32_t i = 0; i < 8; ++i) A[i] = *reinterpret_cast<const rf32x4*>(pr + 4u * i);
+#pragma unroll
+                    for (uint32_t j = 0; j < CH / 32u; ++j) {
+                        rf32x4(&cur)[8] = (j & 1u) ? B : A;
+                        rf32x4(&nxt)[8] = (j & 1u) ? A : B;
+                        if (j + 1u < CH / 32u) {
+#pragma unroll
+                            for (uint32_t i = 0; i < 8; ++i)
+                                nxt[i] = *reinterpret_cast<const rf32x4*>(pr + 32u * (j + 1u) + 4u * i);
+                        }
+#pragma unroll
+                        for (uint32_t i = 0; i < 8; ++i) {
+                            s = __fadd_rn(s, cur[i].x);
+                            s = __fadd_rn(s, cur[i].y);
+                            s = __fadd_rn(s, cur[i].z);
+                            s = __fadd_rn(s, cur[i].w);
+                        }
+                    }
+                }
+            }
+        }
+        // linear()'s bias-free 0.0F + dot (src/linear.cpp:203-204)
+        if (t < rows) fb.logit[fb.cand[g0 + t]] = static_cast<double>(__fadd_rn(0.0f, s));
+        __syncthreads();  // the next group's stores reuse both buffers
+    }
     // route_experts throws on any non-finite logit (src/qwen3_moe_runner.cpp:270-276)
     if (t < E && !isfinite(fb.logit[t])) fb.bad = 1u;
     __syncthreads();

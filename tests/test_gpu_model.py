@@ -144,3 +144,46 @@ def test_generation_is_repeatable_and_validated(hip):
         assert np.array_equal(t2, t3)
         with pytest.raises(ValueError, match="vocabulary"):
             model.generate(np.array([m.vocab], np.uint32), 2)
+
+
+@pytest.mark.parametrize("embd_type", (S.F16, S.BF16, S.Q4_1, S.Q8_0, S.Q5_K))
+def test_embedding_row_types(hip, port, embd_type):
+    """The token embedding decodes to the reference's FP32 row
+    (read_float_rows_into for F16/BF16, dequantize_quantized_row otherwise,
+    src/qwen3_moe_runner.cpp:592-600): the model with the embedding in
+    `embd_type` gives the same tokens and logits, bit for bit, as the same
+    model with an F32 embedding holding the decoded rows (numpy's exact
+    conversions, or the oracle's dequantize_row, which the reference's golden
+    rows pin)."""
+    from pokitlms_amd import _abi
+    from pokitlms_amd.model import Qwen3MoeModel
+    m = SM.Qwen3MoeShape(layers=1, vocab=4096, experts=16, top_k=4, context=1024)
+    enc = S.quant_matrix(embd_type, m.vocab, m.hidden, S.rng(60 + embd_type), scale_std=0.05)
+    if embd_type == S.F16:
+        dec = enc.view(np.float16).astype(np.float32)
+    elif embd_type == S.BF16:
+        dec = (enc.view(np.uint16).astype(np.uint32) << 16).view(np.float32)
+    else:
+        dec = port.dequantize_row(embd_type, enc, m.vocab * m.hidden).reshape(m.vocab, m.hidden)
+    prompt = SM.prompt_tokens(61, 12, m.vocab)
+    with Qwen3MoeModel.synthetic(hip, m, 61) as base:
+        e_typed = hip.upload(embd_type, m.hidden, m.vocab, enc)
+        e_f32 = hip.upload(S.F32, m.hidden, m.vocab, dec)
+        outs = []
+        try:
+            for e in (e_typed, e_f32):
+                w = dict(base.weights)
+                w["token_embd.weight"] = e
+                model = Qwen3MoeModel(hip, m, w)
+                try:
+                    outs.append(model.generate(prompt, 6, want_logits=True))
+                finally:  # the weights belong to `base` and this test
+                    _abi.lib().pk_hip_qwen3moe_destroy(model.handle)
+                    model.handle, model.weights = None, {}
+        finally:
+            e_typed.release()
+            e_f32.release()
+    (t0, l0, _), (t1, l1, _) = outs
+    say("embedding", S.TYPE_NAMES[embd_type], "tokens", t0)
+    assert np.array_equal(t0, t1)
+    assert np.array_equal(l0.view(np.uint32), l1.view(np.uint32))
