@@ -257,35 +257,88 @@ __device__ __forceinline__ void raw32_bf16(const Raw32<T>& r, uint32_t k0, uint3
 // ---------------------------------------------------------------------------
 // 1. Batched router.
 
+// Expert rows per workgroup: C = hidden / 256 router values per thread and
+// row stay in registers.
+template <int C>
+constexpr uint32_t router_rows_per_wg() { return C <= 8 ? 4u : C <= 16 ? 2u : 1u; }
+
+// Per (token, expert) the S and B of router_sum_bound, with its operations in
+// its order (so the decode path's bits).  A workgroup holds EB expert rows in
+// registers and walks kRouterTokens tokens, reading each token's x once for
+// all EB rows; the rows' scans and reductions share two barriers per token.
+// The cross-wave totals are double-buffered by token parity, so a wave that
+// runs ahead into the next token never overwrites what the finishing threads
+// still read.
 template <int C>
 __global__ __launch_bounds__(kRouterThreads) void k_router_batch(MoePrefillArgs a) {
-    __shared__ double wtot[kRouterThreads / 64];
-    __shared__ double red[kRouterThreads / 64];
-    const uint32_t e = blockIdx.x, E = a.layer.n_experts, H = a.layer.hidden;
+    constexpr uint32_t EB = router_rows_per_wg<C>(), NW = kRouterThreads / 64;
+    __shared__ double wtot[2][EB][NW];
+    __shared__ double red[2][EB][NW];
+    const uint32_t E = a.layer.n_experts, H = a.layer.hidden;
+    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+    const uint32_t e0 = blockIdx.x * EB;
     const uint32_t t0 = blockIdx.y * kRouterTokens;
     const uint32_t t1 = t0 + kRouterTokens < a.tokens ? t0 + kRouterTokens : a.tokens;
-    const float* w = a.layer.router + static_cast<uint64_t>(e) * H + threadIdx.x * C;
-    float wr[C];
+    float wr[EB][C];
 #pragma unroll
-    for (int i = 0; i < C; i += 2) {
-        const float2 v = *reinterpret_cast<const float2*>(w + i);
-        wr[i] = v.x;
-        wr[i + 1] = v.y;
-    }
-    for (uint32_t t = t0; t < t1; ++t) {
-        const float* xx = a.x + static_cast<uint64_t>(t) * H + threadIdx.x * C;
-        float p[C];
+    for (uint32_t e = 0; e < EB; ++e) {
+        const uint32_t ee = e0 + e < E ? e0 + e : E - 1u;  // rows past E repeat the last (never written)
+        const float* w = a.layer.router + static_cast<uint64_t>(ee) * H + threadIdx.x * C;
 #pragma unroll
         for (int i = 0; i < C; i += 2) {
-            const float2 xv = *reinterpret_cast<const float2*>(xx + i);
-            p[i] = __fmul_rn(wr[i], xv.x);  // the CPU's rounded products, exactly
-            p[i + 1] = __fmul_rn(wr[i + 1], xv.y);
+            const float2 v = *reinterpret_cast<const float2*>(w + i);
+            wr[e][i] = v.x;
+            wr[e][i + 1] = v.y;
         }
-        double total, bound;
-        router_sum_bound<C>(p, wtot, red, total, bound);
-        if (threadIdx.x == 0) {
-            a.row_sum[static_cast<uint64_t>(t) * E + e] = total;
-            a.row_bound[static_cast<uint64_t>(t) * E + e] = bound;
+    }
+    for (uint32_t t = t0; t < t1; ++t) {
+        const uint32_t par = t & 1u;
+        const float* xx = a.x + static_cast<uint64_t>(t) * H + threadIdx.x * C;
+        float xv[C];
+#pragma unroll
+        for (int i = 0; i < C; i += 2) {
+            const float2 v = *reinterpret_cast<const float2*>(xx + i);
+            xv[i] = v.x;
+            xv[i + 1] = v.y;
+        }
+        double local[EB], run_abs[EB], incl[EB];
+#pragma unroll
+        for (uint32_t e = 0; e < EB; ++e) {
+            local[e] = 0.0;
+            run_abs[e] = 0.0;
+#pragma unroll
+            for (int i = 0; i < C; ++i) {
+                local[e] += static_cast<double>(__fmul_rn(wr[e][i], xv[i]));  // the CPU's products
+                run_abs[e] += fabs(local[e]);
+            }
+        }
+#pragma unroll
+        for (uint32_t e = 0; e < EB; ++e) incl[e] = wave_inclusive_scan(local[e]);
+        if (lane == 63) {
+#pragma unroll
+            for (uint32_t e = 0; e < EB; ++e) wtot[par][e][wave] = incl[e];
+        }
+        __syncthreads();
+#pragma unroll
+        for (uint32_t e = 0; e < EB; ++e) {
+            double off = incl[e] - local[e];
+            for (uint32_t v = 0; v < wave; ++v) off += wtot[par][e][v];
+            run_abs[e] = lane63(group_sum<64>(__builtin_fma(static_cast<double>(C), fabs(off), run_abs[e])));
+        }
+        if (lane == 0) {
+#pragma unroll
+            for (uint32_t e = 0; e < EB; ++e) red[par][e][wave] = run_abs[e];
+        }
+        __syncthreads();
+        const uint32_t e = threadIdx.x;
+        if (e < EB && e0 + e < E) {
+            double total = 0.0, q = red[par][e][0];
+            for (uint32_t v = 0; v < NW; ++v) total += wtot[par][e][v];
+            for (uint32_t v = 1; v < NW; ++v) q += red[par][e][v];
+            double bound = q * (0x1p-24 * (1.0 + 0x1p-10) + 0x1p-39);
+            if (!(q < 5.0e35)) bound = INFINITY;  // near FP32 overflow: always recompute
+            a.row_sum[static_cast<uint64_t>(t) * E + e0 + e] = total;
+            a.row_bound[static_cast<uint64_t>(t) * E + e0 + e] = bound;
         }
     }
 }
@@ -896,7 +949,9 @@ bool moe_prefill_supported(uint32_t gate_type, uint32_t up_type, uint32_t down_t
 hipError_t launch_prefill_routing(const MoePrefillArgs& a, hipStream_t s) {
     const MoeDecodeArgs& L = a.layer;
     // 1. router
-    const dim3 rgrid(L.n_experts, ceil_div_u(a.tokens, kRouterTokens));
+    const uint32_t per = L.hidden / kRouterThreads;
+    const uint32_t eb = per <= 8u ? 4u : per <= 16u ? 2u : 1u;  // router_rows_per_wg<per>()
+    const dim3 rgrid(ceil_div_u(L.n_experts, eb), ceil_div_u(a.tokens, kRouterTokens));
     switch (L.hidden / kRouterThreads) {
 #define PK_RB(C)                                                                              \
     case C:                                                                                   \

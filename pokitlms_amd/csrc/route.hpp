@@ -430,36 +430,38 @@ __device__ __forceinline__ void router_products(const float* w, const float* xx,
 // S and B of the row whose products the workgroup holds (valid in thread 0).
 // Every thread must call it; wtot and red are kRouterThreads / 64 doubles of
 // shared memory, reusable by the next call.
+//
+// S: the FP64 sum of the products (thread sums in element order, a wave scan,
+// then the wave totals in wave order).  B bounds the CPU's serial FP32
+// rounding, u * sum_i |T_i| with T_i the exact prefix sums, in one pass
+// through the triangle inequality per thread: with O the thread's offset (the
+// earlier threads' products) and L_i its own running sum,
+// sum_i |O + L_i| <= C |O| + sum_i |L_i| (at most 2 sum |L_i| looser than the
+// exact prefixes).  sum_i |p_i| <= 2 sum_i |T_i| covers the FP64 rounding of
+// S.  The batched prefill router repeats these operations in this order, so
+// both paths rank on the same bits.
 template <int C>
 __device__ __forceinline__ void router_sum_bound(const float (&p)[C], double* wtot, double* red,
                                                  double& total, double& bound) {
     const uint32_t t = threadIdx.x, lane = t & 63u, wave = t >> 6;
-    double local = 0.0, abs_p = 0.0;
+    double local = 0.0, run_abs = 0.0;
 #pragma unroll
     for (int i = 0; i < C; ++i) {
         local += static_cast<double>(p[i]);
-        abs_p += fabs(static_cast<double>(p[i]));
+        run_abs += fabs(local);
     }
-    // exclusive prefix of the thread totals: wave scan + wave offsets
     const double incl = wave_inclusive_scan(local);
     if (lane == 63) wtot[wave] = incl;
     __syncthreads();
     double off = incl - local;
     for (uint32_t v = 0; v < wave; ++v) off += wtot[v];
-    double prefix_abs = 0.0;
-#pragma unroll
-    for (int i = 0; i < C; ++i) {
-        off += static_cast<double>(p[i]);
-        prefix_abs += fabs(off);
-    }
     total = 0.0;
     for (uint32_t v = 0; v < (kRouterThreads >> 6); ++v) total += wtot[v];
-    prefix_abs = block_reduce_d<false>(prefix_abs, red);
-    abs_p = block_reduce_d<false>(abs_p, red);
-    // u = 2^-24.  (1 + 2^-10) >= 1/(1 - n u) for n <= 2^13 and also covers
-    // the FP64 rounding of the prefix sums; abs_p * 2^-40 covers S itself.
-    bound = prefix_abs * 0x1p-24 * (1.0 + 0x1p-10) + abs_p * 0x1p-40;
-    if (!(abs_p < 1.0e36)) bound = INFINITY;  // near FP32 overflow: always recompute
+    const double q = block_reduce_d<false>(__builtin_fma(static_cast<double>(C), fabs(off), run_abs), red);
+    // u = 2^-24; (1 + 2^-10) >= 1/(1 - n u) for n <= 2^13 and covers the FP64
+    // rounding of the prefix sums; q * 2^-39 >= sum |p| * 2^-40 covers S
+    bound = q * (0x1p-24 * (1.0 + 0x1p-10) + 0x1p-39);
+    if (!(q < 5.0e35)) bound = INFINITY;  // near FP32 overflow: always recompute
 }
 
 // Marks a router error (wave 0 of gate/up workgroup 0): route_experts throws
