@@ -234,6 +234,23 @@ pk_hip_status pk_hip_moe_prefill_async(pk_hip_ctx* ctx, const pk_hip_moe_layer* 
                                        uint32_t* device_ids, float* device_probs, void* stream,
                                        char* error_buffer, size_t error_capacity);
 
+/* The Qwen3.5-MoE block (pk_hip_moe35_decode) for a batch of tokens: the
+ * reference runner's prompt loop takes the block once per token
+ * (src/qwen35_runner.cpp:670-764 per position).  The shared expert is one
+ * more expert group that every token joins; its output is added after the
+ * routed sum with weight sigmoid(shared_router . x).  ids/weights are
+ * [tokens][top_k] (routed experts).  Same limits as pk_hip_moe_prefill and
+ * pk_hip_moe35_decode; synchronous, host buffers. */
+pk_hip_status pk_hip_moe35_prefill(pk_hip_ctx* ctx, const pk_hip_moe35_layer* layer,
+                                   const float* x, uint32_t tokens, float* y, uint32_t* ids,
+                                   float* weights, char* error_buffer, size_t error_capacity);
+
+/* Device-buffer variant, enqueued on `stream` without synchronising. */
+pk_hip_status pk_hip_moe35_prefill_async(pk_hip_ctx* ctx, const pk_hip_moe35_layer* layer,
+                                         const float* device_x, uint32_t tokens, float* device_y,
+                                         uint32_t* device_ids, float* device_weights, void* stream,
+                                         char* error_buffer, size_t error_capacity);
+
 /* ---- Whole-model greedy decode (Qwen3-MoE) ------------------------------------
  * Qwen3MoeRunner (include/pokitlms/model/qwen3_moe_runner.hpp:57-110) with
  * every layer of a token step on the GPU: forward_into

@@ -28,6 +28,7 @@ EXPORTS = (
     "pk_hip_moe_decode_async", "pk_hip_moe35_decode", "pk_hip_moe35_decode_async", "pk_hip_sync",
     "pk_hip_get_stats", "pk_hip_reset_stats",
     "pk_hip_set_kernel_timing", "pk_hip_device_name", "pk_hip_moe_prefill",
+    "pk_hip_moe35_prefill", "pk_hip_moe35_prefill_async",
     "pk_hip_moe_prefill_async", "pk_hip_qwen3moe_create", "pk_hip_qwen3moe_destroy",
     "pk_hip_qwen3moe_generate", "pk_hip_synth_weight", "pk_hip_matvec_reference_order",
 )
@@ -150,6 +151,12 @@ def lib() -> ctypes.CDLL:
     L.pk_hip_moe_prefill_async.restype = ctypes.c_int
     L.pk_hip_moe_prefill_async.argtypes = [vp, ctypes.POINTER(MoeLayerDesc), vp, u32, vp, vp, vp,
                                            vp, cp, sz]
+    L.pk_hip_moe35_prefill.restype = ctypes.c_int
+    L.pk_hip_moe35_prefill.argtypes = [vp, ctypes.POINTER(Moe35LayerDesc), fp, u32, fp, up, fp,
+                                       cp, sz]
+    L.pk_hip_moe35_prefill_async.restype = ctypes.c_int
+    L.pk_hip_moe35_prefill_async.argtypes = [vp, ctypes.POINTER(Moe35LayerDesc), vp, u32, vp, vp,
+                                             vp, vp, cp, sz]
     L.pk_hip_device_name.argtypes = [vp, cp, sz]
     L.pk_hip_qwen3moe_create.restype = ctypes.c_int
     L.pk_hip_qwen3moe_create.argtypes = [vp, ctypes.POINTER(Qwen3MoeConfig),

@@ -274,6 +274,32 @@ class HipBackend:
                                                     device_weights, stream or None, err,
                                                     _ERRBUF), err)
 
+    def moe35_prefill(self, layer: Moe35LayerHandles, x: np.ndarray):
+        """A batch of tokens x [tokens, hidden] through the Qwen3.5-MoE block;
+        per token the result of moe35_decode."""
+        xx = np.ascontiguousarray(x, dtype=np.float32)
+        if xx.ndim != 2 or xx.shape[1] != layer.hidden:
+            raise ValueError(f"x must be [tokens, {layer.hidden}], got {xx.shape}")
+        tokens = xx.shape[0]
+        y = np.empty((tokens, layer.hidden), dtype=np.float32)
+        ids = np.zeros((tokens, layer.top_k), dtype=np.uint32)
+        w = np.zeros((tokens, layer.top_k), dtype=np.float32)
+        err = ctypes.create_string_buffer(_ERRBUF)
+        _raise(_abi.lib().pk_hip_moe35_prefill(self.handle, ctypes.byref(layer.desc35), _f32p(xx),
+                                               tokens, _f32p(y),
+                                               ids.ctypes.data_as(ctypes.POINTER(ctypes.c_uint32)),
+                                               _f32p(w), err, _ERRBUF), err)
+        return y, ids, w
+
+    def moe35_prefill_async(self, layer: Moe35LayerHandles, device_x: int, tokens: int,
+                            device_y: int, device_ids: int, device_weights: int,
+                            stream: int = 0) -> None:
+        err = ctypes.create_string_buffer(_ERRBUF)
+        _raise(_abi.lib().pk_hip_moe35_prefill_async(self.handle, ctypes.byref(layer.desc35),
+                                                     device_x, tokens, device_y, device_ids,
+                                                     device_weights, stream or None, err,
+                                                     _ERRBUF), err)
+
     def moe_decode_async(self, layer: MoeLayerHandles, device_x: int, device_y: int,
                          device_ids: int, device_probs: int, stream: int = 0) -> None:
         err = ctypes.create_string_buffer(_ERRBUF)

@@ -719,21 +719,27 @@ pk_hip_status pk_hip_moe35_decode_async(pk_hip_ctx* ctx, const pk_hip_moe35_laye
 
 namespace {
 
-MoeShape check_prefill(pk_hip_ctx* c, const pk_hip_moe_layer* L, uint32_t tokens) {
+MoeShape check_prefill(pk_hip_ctx* c, const pk_hip_moe_layer* L, uint32_t tokens,
+                       uint32_t variant = 0) {
     const MoeShape m = check_layer(c, L);
     if (tokens == 0 || tokens > pk::kMaxPrefillTokens)
         throw ArgError("prefill token count must be between 1 and " +
                        std::to_string(pk::kMaxPrefillTokens));
     if (!pk::moe_prefill_supported(L->gate->type, L->up->type, L->down->type, m.hidden, m.ffn,
-                                   m.experts, L->top_k, tokens))
+                                   m.experts, L->top_k, tokens, variant))
         throw Unsupported("MoE prefill shape not covered by the HIP kernels");
     return m;
 }
 
+// Variant 1 (shared != nullptr): the shared expert is one more route per token
+// and one more router row and expert group.
 void enqueue_prefill(pk_hip_ctx* c, const pk_hip_moe_layer* L, const MoeShape& m, uint32_t tokens,
-                     const float* dx, float* dy, uint32_t* dids, float* dprobs, hipStream_t s) {
-    const uint64_t T = tokens, K = L->top_k, E = m.experts;
-    const uint32_t max_tiles = pk::moe_prefill_max_tiles(tokens, L->top_k, m.experts);
+                     const float* dx, float* dy, uint32_t* dids, float* dprobs, hipStream_t s,
+                     const pk_hip_moe35_layer* shared = nullptr) {
+    const uint64_t V = shared ? 1u : 0u;
+    const uint64_t T = tokens, K = L->top_k + V, E = m.experts + V;
+    const uint32_t max_tiles = pk::moe_prefill_max_tiles(tokens, static_cast<uint32_t>(K),
+                                                         static_cast<uint32_t>(E));
     c->prow_sum.ensure(T * E);
     c->prow_bound.ensure(T * E);
     c->poffsets.ensure(E + 1);
@@ -767,6 +773,13 @@ void enqueue_prefill(pk_hip_ctx* c, const pk_hip_moe_layer* L, const MoeShape& m
     l.normalize = L->normalize ? 1u : 0u;
     l.scale = L->scale;
     l.status = status_words(c);
+    if (shared) {
+        l.variant = 1;
+        l.shared_router = reinterpret_cast<const float*>(shared->shared_router->dptr);
+        l.shared_gate = shared->shared_gate->dptr;
+        l.shared_up = shared->shared_up->dptr;
+        l.shared_down = shared->shared_down->dptr;
+    }
     a.tokens = tokens;
     a.max_tiles = max_tiles;
     a.x = dx;
@@ -857,6 +870,60 @@ pk_hip_status pk_hip_moe_prefill_async(pk_hip_ctx* ctx, const pk_hip_moe_layer* 
         ctx->set_device();
         hipStream_t s = stream ? static_cast<hipStream_t>(stream) : ctx->stream;
         enqueue_prefill(ctx, layer, m, tokens, dx, dy, dids, dprobs, s);
+        if (ctx->time_kernels) {
+            check(hipStreamSynchronize(s), "hipStreamSynchronize");
+            collect_timing_prefill(ctx);
+        }
+    });
+}
+
+pk_hip_status pk_hip_moe35_prefill(pk_hip_ctx* ctx, const pk_hip_moe35_layer* layer,
+                                   const float* x, uint32_t tokens, float* y, uint32_t* ids,
+                                   float* weights, char* err, size_t cap) {
+    return guarded(ctx, err, cap, [&] {
+        require_usable(ctx);
+        if (!x || !y || !ids || !weights) throw ArgError("input and output buffers are required");
+        std::lock_guard lock(ctx->mutex);
+        const MoeShape m = check_decode35(ctx, layer);
+        check_prefill(ctx, &layer->routed, tokens, 1);
+        ctx->set_device();
+        const uint64_t T = tokens, K = layer->routed.top_k;
+        ctx->px.ensure(T * m.hidden);
+        ctx->py.ensure(T * m.hidden);
+        ctx->pids.ensure(T * K);
+        ctx->pprobs.ensure(T * K);
+        check(hipMemcpyAsync(ctx->px.ptr, x, T * m.hidden * sizeof(float), hipMemcpyHostToDevice,
+                             ctx->stream),
+              "copy input");
+        enqueue_prefill(ctx, &layer->routed, m, tokens, ctx->px.ptr, ctx->py.ptr, ctx->pids.ptr,
+                        ctx->pprobs.ptr, ctx->stream, layer);
+        check(hipMemcpyAsync(y, ctx->py.ptr, T * m.hidden * sizeof(float), hipMemcpyDeviceToHost,
+                             ctx->stream),
+              "copy output");
+        check(hipMemcpyAsync(ids, ctx->pids.ptr, T * K * sizeof(uint32_t), hipMemcpyDeviceToHost,
+                             ctx->stream),
+              "copy ids");
+        check(hipMemcpyAsync(weights, ctx->pprobs.ptr, T * K * sizeof(float),
+                             hipMemcpyDeviceToHost, ctx->stream),
+              "copy weights");
+        sync_and_check(ctx, ctx->stream);
+        collect_timing_prefill(ctx);
+    });
+}
+
+pk_hip_status pk_hip_moe35_prefill_async(pk_hip_ctx* ctx, const pk_hip_moe35_layer* layer,
+                                         const float* dx, uint32_t tokens, float* dy,
+                                         uint32_t* dids, float* dweights, void* stream, char* err,
+                                         size_t cap) {
+    return guarded(ctx, err, cap, [&] {
+        require_usable(ctx);
+        if (!dx || !dy || !dids || !dweights) throw ArgError("device buffers are required");
+        std::lock_guard lock(ctx->mutex);
+        const MoeShape m = check_decode35(ctx, layer);
+        check_prefill(ctx, &layer->routed, tokens, 1);
+        ctx->set_device();
+        hipStream_t s = stream ? static_cast<hipStream_t>(stream) : ctx->stream;
+        enqueue_prefill(ctx, &layer->routed, m, tokens, dx, dy, dids, dweights, s, layer);
         if (ctx->time_kernels) {
             check(hipStreamSynchronize(s), "hipStreamSynchronize");
             collect_timing_prefill(ctx);

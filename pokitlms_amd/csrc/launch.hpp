@@ -62,7 +62,9 @@ hipError_t launch_moe_decode(const MoeDecodeArgs& a, hipStream_t stream);
 // n_experts (E), pairs P = T*K: row_sum/row_bound T*E, offsets E+1, tiles and
 // n_tiles moe_prefill_max_tiles(T, K, E) + 1, perm P, x_parts 3*T*hidden,
 // x_sums T*hidden/16, act P*ffn, act_parts 3*P*ffn, act_sums P*ffn/16,
-// out P*hidden.
+// out P*hidden.  Variant 1 (Qwen3.5) adds the shared expert as one more
+// route per token and one more router row and expert group: K = top_k + 1 and
+// E = n_experts + 1 in these sizes.
 constexpr uint32_t kMaxPrefillTokens = 4096;
 struct MoePrefillArgs {
     MoeDecodeArgs layer;     // weights, shapes, top_k, normalize, scale
@@ -88,7 +90,7 @@ struct MoePrefillArgs {
 uint32_t moe_prefill_max_tiles(uint32_t tokens, uint32_t top_k, uint32_t n_experts);
 bool moe_prefill_supported(uint32_t gate_type, uint32_t up_type, uint32_t down_type,
                            uint32_t hidden, uint32_t ffn, uint32_t n_experts, uint32_t top_k,
-                           uint32_t tokens);
+                           uint32_t tokens, uint32_t variant = 0);
 // The prefill's launches in three phases (timed separately): routing and
 // grouping (router, ranking, grouping), the gate/up GEMMs, and down + combine.
 hipError_t launch_prefill_routing(const MoePrefillArgs& a, hipStream_t stream);

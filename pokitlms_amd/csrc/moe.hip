@@ -41,14 +41,6 @@ namespace {
 constexpr uint32_t kGateUpPasses = 2;  // row passes whose loads a gate/up wave keeps in flight
 constexpr uint32_t kDownPasses = 2;    // row passes per down workgroup
 
-// Qwen3.5's sigmoid and silu (src/qwen35_runner.cpp:111-123).
-__device__ __forceinline__ float sigmoid35(float v) {
-    if (v >= 0.0f) return 1.0f / (1.0f + expf(-v));
-    const float e = expf(v);
-    return e / (1.0f + e);
-}
-__device__ __forceinline__ float silu(float v) { return v * sigmoid35(v); }
-
 // ---------------------------------------------------------------------------
 // 1. Router: exact sum and serial-error bound of one expert row per workgroup.
 

@@ -274,7 +274,8 @@ __global__ __launch_bounds__(kRouterThreads) void k_router_batch(MoePrefillArgs 
     constexpr uint32_t EB = router_rows_per_wg<C>(), NW = kRouterThreads / 64;
     __shared__ double wtot[2][EB][NW];
     __shared__ double red[2][EB][NW];
-    const uint32_t E = a.layer.n_experts, H = a.layer.hidden;
+    // rows: the n_experts router rows, then (variant 1) the shared expert's gate
+    const uint32_t E = a.layer.n_experts, ER = E + a.layer.variant, H = a.layer.hidden;
     const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
     const uint32_t e0 = blockIdx.x * EB;
     const uint32_t t0 = blockIdx.y * kRouterTokens;
@@ -282,8 +283,9 @@ __global__ __launch_bounds__(kRouterThreads) void k_router_batch(MoePrefillArgs 
     float wr[EB][C];
 #pragma unroll
     for (uint32_t e = 0; e < EB; ++e) {
-        const uint32_t ee = e0 + e < E ? e0 + e : E - 1u;  // rows past E repeat the last (never written)
-        const float* w = a.layer.router + static_cast<uint64_t>(ee) * H + threadIdx.x * C;
+        const uint32_t ee = e0 + e < ER ? e0 + e : ER - 1u;  // rows past the end repeat the last (never written)
+        const float* row = ee < E ? a.layer.router + static_cast<uint64_t>(ee) * H : a.layer.shared_router;
+        const float* w = row + threadIdx.x * C;
 #pragma unroll
         for (int i = 0; i < C; i += 2) {
             const float2 v = *reinterpret_cast<const float2*>(w + i);
@@ -331,14 +333,14 @@ __global__ __launch_bounds__(kRouterThreads) void k_router_batch(MoePrefillArgs 
         }
         __syncthreads();
         const uint32_t e = threadIdx.x;
-        if (e < EB && e0 + e < E) {
+        if (e < EB && e0 + e < ER) {
             double total = 0.0, q = red[par][e][0];
             for (uint32_t v = 0; v < NW; ++v) total += wtot[par][e][v];
             for (uint32_t v = 1; v < NW; ++v) q += red[par][e][v];
             double bound = q * (0x1p-24 * (1.0 + 0x1p-10) + 0x1p-39);
             if (!(q < 5.0e35)) bound = INFINITY;  // near FP32 overflow: always recompute
-            a.row_sum[static_cast<uint64_t>(t) * E + e0 + e] = total;
-            a.row_bound[static_cast<uint64_t>(t) * E + e0 + e] = bound;
+            a.row_sum[static_cast<uint64_t>(t) * ER + e0 + e] = total;
+            a.row_bound[static_cast<uint64_t>(t) * ER + e0 + e] = bound;
         }
     }
 }
@@ -357,8 +359,8 @@ __global__ __launch_bounds__(256) void k_route_batch(MoePrefillArgs A) {
     const uint32_t E = A.layer.n_experts, K = A.layer.top_k;
     MoeDecodeArgs a = A.layer;  // this token's view
     a.x = A.x + static_cast<uint64_t>(t) * a.hidden;
-    a.row_sum = A.row_sum + static_cast<uint64_t>(t) * E;
-    a.row_bound = A.row_bound + static_cast<uint64_t>(t) * E;
+    a.row_sum = A.row_sum + static_cast<uint64_t>(t) * (E + a.variant);
+    a.row_bound = A.row_bound + static_cast<uint64_t>(t) * (E + a.variant);
     a.ids = A.ids + static_cast<uint64_t>(t) * K;
     a.probs = A.probs + static_cast<uint64_t>(t) * K;
     a.status = A.status;
@@ -413,11 +415,11 @@ __global__ __launch_bounds__(256) void k_route_batch(MoePrefillArgs A) {
 constexpr uint32_t kGroupThreads = 1024;
 
 __global__ __launch_bounds__(kGroupThreads) void k_group(MoePrefillArgs a) {
-    __shared__ uint32_t cnt[kMaxExperts], off[kMaxExperts + 1], tb[kMaxExperts + 1],
-        fill[kMaxExperts];
-    const uint32_t E = a.layer.n_experts, K = a.layer.top_k, tid = threadIdx.x;
-    const uint32_t n = a.tokens * K;
-    if (tid < E) {
+    constexpr uint32_t NE = kMaxExperts + 1;  // + the shared expert (variant 1)
+    __shared__ uint32_t cnt[NE], off[NE + 1], tb[NE + 1], fill[NE];
+    const uint32_t E = a.layer.n_experts, K = a.layer.top_k, V = a.layer.variant, tid = threadIdx.x;
+    const uint32_t EE = E + V, KR = K + V, n = a.tokens * K;
+    if (tid < EE) {
         cnt[tid] = 0u;
         fill[tid] = 0u;
     }
@@ -426,29 +428,38 @@ __global__ __launch_bounds__(kGroupThreads) void k_group(MoePrefillArgs a) {
         const uint32_t e = a.ids[i];
         if (e < E) atomicAdd(&cnt[e], 1u);
     }
+    // the shared expert takes every token the router did not flag
+    if (V)
+        for (uint32_t t = tid; t < a.tokens; t += kGroupThreads)
+            if (a.ids[t * K] < E) atomicAdd(&cnt[E], 1u);
     __syncthreads();
     if (tid == 0) {
         uint32_t o = 0, b = 0;
-        for (uint32_t e = 0; e < E; ++e) {
+        for (uint32_t e = 0; e < EE; ++e) {
             off[e] = o;
             tb[e] = b;
             o += cnt[e];
             b += (cnt[e] + kTileM - 1u) / kTileM;
         }
-        off[E] = o;
-        tb[E] = b;
+        off[EE] = o;
+        tb[EE] = b;
         a.n_tiles[0] = b;
     }
     __syncthreads();
-    if (tid <= E) a.offsets[tid] = off[tid];
-    if (tid < E)
+    if (tid <= EE) a.offsets[tid] = off[tid];
+    if (tid < EE)
         for (uint32_t j = 0; j < (cnt[tid] + kTileM - 1u) / kTileM; ++j)
             a.tiles[tb[tid] + j] = (tid << 16) | j;
-    // the order inside a group is free: every row's result is independent
+    // grouped rows hold slots token * (top_k + variant) + route (the shared
+    // expert is route top_k); the order inside a group is free: every row's
+    // result is independent
     for (uint32_t i = tid; i < n; i += kGroupThreads) {
         const uint32_t e = a.ids[i];
-        if (e < E) a.perm[off[e] + atomicAdd(&fill[e], 1u)] = i;
+        if (e < E) a.perm[off[e] + atomicAdd(&fill[e], 1u)] = (i / K) * KR + i % K;
     }
+    if (V)
+        for (uint32_t t = tid; t < a.tokens; t += kGroupThreads)
+            if (a.ids[t * K] < E) a.perm[off[E] + atomicAdd(&fill[E], 1u)] = t * KR + K;
 }
 
 // ---------------------------------------------------------------------------
@@ -747,22 +758,23 @@ __global__ __launch_bounds__(256, 2) void k_expert_gemm(MoePrefillArgs a) {
     if (tid < kTileM) {
         const uint32_t i = tid < tr.rows ? tid : tr.rows - 1u;  // absent rows repeat a real one
         const uint32_t slot = a.perm[tr.base + i];  // token * top_k + route
-        arow[tid] = DUAL ? slot / L.top_k : tr.base + i;
+        arow[tid] = DUAL ? slot / (L.top_k + L.variant) : tr.base + i;
         oslot[tid] = slot;
     }
     const uint32_t wr = tid % C::NRW;
+    const bool sh = tr.e >= L.n_experts;  // the shared expert (variant 1): its own tensors
     const uint8_t* wrow;
     if constexpr (DUAL)
-        wrow = (wr < 128u ? L.gate + static_cast<uint64_t>(tr.e) * L.gate_slice +
+        wrow = (wr < 128u ? (sh ? L.shared_gate : L.gate + static_cast<uint64_t>(tr.e) * L.gate_slice) +
                                 static_cast<uint64_t>(n0 + wr) * L.gate_row
-                          : L.up + static_cast<uint64_t>(tr.e) * L.up_slice +
+                          : (sh ? L.shared_up : L.up + static_cast<uint64_t>(tr.e) * L.up_slice) +
                                 static_cast<uint64_t>(n0 + wr - 128u) * L.up_row);
     else  // rows n0 .. n0 + 255
-        wrow = L.down + static_cast<uint64_t>(tr.e) * L.down_slice +
+        wrow = (sh ? L.shared_down : L.down + static_cast<uint64_t>(tr.e) * L.down_slice) +
                static_cast<uint64_t>(n0 + wr) * L.down_row;
     const uint16_t* parts = DUAL ? a.x_parts : a.act_parts;
     const uint64_t plane = DUAL ? static_cast<uint64_t>(a.tokens) * L.hidden
-                                : static_cast<uint64_t>(a.tokens) * L.top_k * L.ffn;
+                                : static_cast<uint64_t>(a.tokens) * (L.top_k + L.variant) * L.ffn;
     const float* sums = DUAL ? a.x_sums : a.act_sums;
     __syncthreads();
     GemmSrc<TW, DUAL> src;
@@ -849,9 +861,11 @@ __global__ __launch_bounds__(256, 2) void k_expert_gemm(MoePrefillArgs a) {
         const uint32_t row = (r / 4u) * 8u + (lane / 32u) * 4u + (r % 4u);
         if (row < tr.rows) {
             if constexpr (DUAL) {
-                // SwiGLU g / (1 + expf(-g)) * u (src/qwen3_moe_runner.cpp:682-684)
+                // SwiGLU g / (1 + expf(-g)) * u (src/qwen3_moe_runner.cpp:682-684);
+                // variant 1: silu(g) * u (src/qwen35_runner.cpp:111-123)
                 const float g = acc[r], u = acc2[r];
-                a.act[static_cast<uint64_t>(tr.base + row) * ndim + col] = (g / (1.0f + expf(-g))) * u;
+                a.act[static_cast<uint64_t>(tr.base + row) * ndim + col] =
+                    L.variant ? silu(g) * u : (g / (1.0f + expf(-g))) * u;
             } else {
                 float* o = a.out + static_cast<uint64_t>(oslot[row]) * ndim + col;
                 o[0] = acc[r];
@@ -867,6 +881,7 @@ __global__ __launch_bounds__(256, 2) void k_expert_gemm(MoePrefillArgs a) {
 __global__ __launch_bounds__(256) void k_combine(MoePrefillArgs a) {
     const uint32_t t = blockIdx.x, i = blockIdx.y * 256u + threadIdx.x;
     const uint32_t K = a.layer.top_k, H = a.layer.hidden, E = a.layer.n_experts;
+    const uint32_t V = a.layer.variant, KR = K + V;
     if (i >= H) return;
     bool ok = true;
     for (uint32_t r = 0; r < K; ++r) ok = ok && a.ids[t * K + r] < E;
@@ -874,7 +889,11 @@ __global__ __launch_bounds__(256) void k_combine(MoePrefillArgs a) {
     float y = 0.0f;
     for (uint32_t r = 0; r < K; ++r)
         y = __fadd_rn(y, __fmul_rn(a.probs[t * K + r],
-                                   a.out[(static_cast<uint64_t>(t) * K + r) * H + i]));
+                                   a.out[(static_cast<uint64_t>(t) * KR + r) * H + i]));
+    if (V) {  // mixer_output = moe_result + sigmoid(shared gate) * shared (src/qwen35_runner.cpp:752-761)
+        const float gate = sigmoid35(static_cast<float>(a.row_sum[static_cast<uint64_t>(t) * (E + 1u) + E]));
+        y = __fadd_rn(y, __fmul_rn(gate, a.out[(static_cast<uint64_t>(t) * KR + K) * H + i]));
+    }
     a.y[static_cast<uint64_t>(t) * H + i] = y;
 }
 
@@ -902,8 +921,8 @@ hipError_t expert_gemm_t(const MoePrefillArgs& a, hipStream_t s) {
     if constexpr (DUAL)
         split_t<G>(a.x, a.tokens, L.hidden, a.x_parts, a.x_sums, s);
     else
-        split_t<G>(a.act, static_cast<uint64_t>(a.tokens) * L.top_k, L.ffn, a.act_parts,
-                   a.act_sums, s);
+        split_t<G>(a.act, static_cast<uint64_t>(a.tokens) * (L.top_k + L.variant), L.ffn,
+                   a.act_parts, a.act_sums, s);
     const uint32_t nb = DUAL ? L.ffn / kTileN : L.hidden / (2u * kTileN);
     const uint32_t blocks = 8u * ceil_div_u(a.max_tiles, 8u) * nb;  // xcd_tile's layout
     hipLaunchKernelGGL((k_expert_gemm<TW, DUAL>), dim3(blocks), dim3(256), 0, s, a);
@@ -931,7 +950,8 @@ uint32_t moe_prefill_max_tiles(uint32_t tokens, uint32_t top_k, uint32_t n_exper
 
 bool moe_prefill_supported(uint32_t gate_type, uint32_t up_type, uint32_t down_type,
                            uint32_t hidden, uint32_t ffn, uint32_t n_experts, uint32_t top_k,
-                           uint32_t tokens) {
+                           uint32_t tokens, uint32_t variant) {
+    if (variant > 1u) return false;
     if (gate_type != up_type || !prefill_type_ok(gate_type) || !prefill_type_ok(down_type))
         return false;
     if (tokens == 0 || tokens > kMaxPrefillTokens) return false;
@@ -951,7 +971,7 @@ hipError_t launch_prefill_routing(const MoePrefillArgs& a, hipStream_t s) {
     // 1. router
     const uint32_t per = L.hidden / kRouterThreads;
     const uint32_t eb = per <= 8u ? 4u : per <= 16u ? 2u : 1u;  // router_rows_per_wg<per>()
-    const dim3 rgrid(ceil_div_u(L.n_experts, eb), ceil_div_u(a.tokens, kRouterTokens));
+    const dim3 rgrid(ceil_div_u(L.n_experts + L.variant, eb), ceil_div_u(a.tokens, kRouterTokens));
     switch (L.hidden / kRouterThreads) {
 #define PK_RB(C)                                                                              \
     case C:                                                                                   \

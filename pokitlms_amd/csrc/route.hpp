@@ -26,6 +26,14 @@ constexpr uint32_t kMaxTopK = 8;      // routes per token: waves of the down/com
 // logits; it stays set until the host reads and clears it.
 enum : uint32_t { ST_ERROR = 0, ST_FALLBACKS = 1, ST_CANDIDATES = 2 };
 
+// Qwen3.5's sigmoid and silu (src/qwen35_runner.cpp:111-123).
+__device__ __forceinline__ float sigmoid35(float v) {
+    if (v >= 0.0f) return 1.0f / (1.0f + expf(-v));
+    const float e = expf(v);
+    return e / (1.0f + e);
+}
+__device__ __forceinline__ float silu(float v) { return v * sigmoid35(v); }
+
 // route_experts' sorted-insertion order: larger logit first, then smaller id.
 __device__ __forceinline__ bool key_before(double av, uint32_t aid, double bv, uint32_t bid) {
     return av > bv || (av == bv && aid < bid);

@@ -164,3 +164,53 @@ def test_gpu_moe35_async_and_errors(hip, port):
             hip.moe35_decode(h, poison)
     finally:
         h.release()
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("name,kw,n", LAYERS, ids=[l[0] for l in LAYERS])
+def test_gpu_moe35_prefill_matches_decode_and_golden(hip, g35, name, kw, n):
+    """The batched Qwen3.5 block (pk_hip_moe35_prefill): per token the decode
+    path's ids and weights bit for bit (the same router sums, bounds and
+    weight code), outputs within 1e-4 normwise of the decode path and of the
+    reference's golden outputs."""
+    layer, xs = layer_tokens(name, kw, n)
+    extra = S.normal_f32(S.rng(4040), 61 * layer.hidden).reshape(61, layer.hidden)
+    X = np.concatenate([xs, extra])
+    h = hip.upload_moe35_layer(layer)
+    worst = 0.0
+    try:
+        y, ids, w = hip.moe35_prefill(h, X)
+        for t in range(X.shape[0]):
+            dy, dids, dw = hip.moe35_decode(h, X[t])
+            assert np.array_equal(ids[t], dids), (t, ids[t], dids)
+            assert np.array_equal(w[t].view(np.uint32), dw.view(np.uint32)), t
+            worst = max(worst, normwise_rel(y[t], dy))
+        for t in range(len(xs)):
+            assert np.array_equal(ids[t], g35[f"{name}_ids"][t]), t
+        for t in range(min(4, len(xs))):
+            assert normwise_rel(y[t], g35[f"{name}_y"][t]) <= 1e-4, t
+    finally:
+        h.release()
+    print(f"qwen35 prefill {name}: {X.shape[0]} tokens, worst normwise vs decode {worst:.2e}",
+          flush=True)
+    assert worst <= 1e-4
+
+
+@pytest.mark.gpu
+def test_gpu_moe35_prefill_shared_expert_matters(hip):
+    """The shared expert's share is in the batched output: with its gate row
+    scaled so sigmoid saturates near 0 or 1 the outputs move by the shared
+    expert's output (both paths agree either way)."""
+    layer, xs = layer_tokens(*LAYERS[1][:2], 16)
+    outs = []
+    for gain in (-50.0, 50.0):
+        layer.shared_router = (np.sign(xs[0]) * np.float32(gain / layer.hidden)).astype(np.float32)
+        h = hip.upload_moe35_layer(layer)
+        try:
+            y, _, _ = hip.moe35_prefill(h, xs[:1])
+            dy, _, _ = hip.moe35_decode(h, xs[0])
+            assert normwise_rel(y[0], dy) <= 1e-4
+            outs.append(y[0])
+        finally:
+            h.release()
+    assert normwise_rel(outs[0], outs[1]) > 1e-2
