@@ -219,7 +219,7 @@ pk_hip_status pk_hip_moe35_decode_async(pk_hip_ctx* ctx, const pk_hip_moe35_laye
  * expert; the expert products run on bf16 MFMA with exact products (FP32
  * activations split into three bf16 parts, the quantised weights as exact
  * bf16 integers, scales applied per group in FP32).  1 <= tokens <=
- * 4096; gate/up and down of any K-quant/Q8_0/Q4_0 type, ffn a multiple of
+ * 4096; gate/up and down of any K-quant/Q8_0/Q4_0/Q4_1 type, ffn a multiple of
  * 256.  Host buffers; synchronous.  Non-finite router logits return
  * RUNTIME_ERROR. */
 pk_hip_status pk_hip_moe_prefill(pk_hip_ctx* ctx, const pk_hip_moe_layer* layer, const float* x,

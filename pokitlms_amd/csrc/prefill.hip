@@ -57,6 +57,7 @@ template <> struct Raw32<T_Q5_K> { uint32_t h[4]; uint32_t q[8]; uint32_t qh[8];
 template <> struct Raw32<T_Q6_K> { uint32_t ql[8], qh[8]; uint32_t ql8, qh8, sc, d, shift; };
 template <> struct Raw32<T_Q8_0> { uint32_t q[8]; uint32_t q8, d, shift; };
 template <> struct Raw32<T_Q4_0> { uint32_t q[4]; uint32_t q4, d, shift; };
+template <> struct Raw32<T_Q4_1> { uint32_t q[4]; uint32_t dm; };  // 20-byte blocks keep 4-byte alignment
 
 // Word i of a field loaded `shift` bytes early.
 template <int N>
@@ -99,6 +100,10 @@ __device__ __forceinline__ void raw32_load(const uint8_t* row, uint32_t k0, Raw3
         ld_words<8>(blk + 2u - r.shift, r.q);
         r.q8 = ld_word(blk + 34u - r.shift);
         r.d = ld_u16(blk);
+    } else if constexpr (T == T_Q4_1) {
+        const uint8_t* blk = row + (k0 / 32u) * 20u;
+        r.dm = ld_word(blk);
+        ld_words<4>(blk + 4u, r.q);
     } else {  // Q4_0
         const uint8_t* blk = row + (k0 / 32u) * 18u;
         r.shift = align_shift(blk + 2u);
@@ -241,6 +246,14 @@ __device__ __forceinline__ void raw32_bf16(const Raw32<T>& r, uint32_t k0, uint3
             bf16_bytes(word_at(r.q, r.q8, r.shift, i) ^ 0x80808080u, bw[2 * i], bw[2 * i + 1]);
         ds[0] = ds[1] = d;
         cn[0] = cn[1] = __fmul_rn(-128.0f, d);
+    } else if constexpr (T == T_Q4_1) {  // w = d * q + m: ds = d, cn = m (o = 0)
+#pragma unroll
+        for (uint32_t i = 0; i < 4; ++i) {
+            bf16_bytes(r.q[i] & 0x0f0f0f0fu, bw[2 * i], bw[2 * i + 1]);
+            bf16_bytes((r.q[i] >> 4) & 0x0f0f0f0fu, bw[8 + 2 * i], bw[9 + 2 * i]);
+        }
+        ds[0] = ds[1] = half_bits_to_float(r.dm & 0xffffu);
+        cn[0] = cn[1] = half_bits_to_float(r.dm >> 16);
     } else {  // Q4_0: low nibbles are elements 0..15, high nibbles 16..31
         const float d = half_bits_to_float(r.d);
 #pragma unroll
@@ -901,7 +914,7 @@ __global__ __launch_bounds__(256) void k_combine(MoePrefillArgs a) {
 // Host side.
 
 bool prefill_type_ok(uint32_t t) {
-    return t == T_Q4_K || t == T_Q5_K || t == T_Q6_K || t == T_Q8_0 || t == T_Q4_0;
+    return t == T_Q4_K || t == T_Q5_K || t == T_Q6_K || t == T_Q8_0 || t == T_Q4_0 || t == T_Q4_1;
 }
 
 uint32_t ceil_div_u(uint32_t a, uint32_t b) { return (a + b - 1u) / b; }
@@ -937,6 +950,7 @@ hipError_t expert_gemm(uint32_t type, const MoePrefillArgs& a, hipStream_t s) {
         case T_Q6_K: return expert_gemm_t<T_Q6_K, DUAL>(a, s);
         case T_Q8_0: return expert_gemm_t<T_Q8_0, DUAL>(a, s);
         case T_Q4_0: return expert_gemm_t<T_Q4_0, DUAL>(a, s);
+        case T_Q4_1: return expert_gemm_t<T_Q4_1, DUAL>(a, s);
         default: return hipErrorInvalidValue;
     }
 }

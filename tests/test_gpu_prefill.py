@@ -16,7 +16,7 @@ from tests.golden import make_golden as G
 
 pytestmark = pytest.mark.gpu
 
-QUANT = (S.Q4_0, S.Q8_0, S.Q4_K, S.Q5_K, S.Q6_K)
+QUANT = (S.Q4_0, S.Q4_1, S.Q8_0, S.Q4_K, S.Q5_K, S.Q6_K)
 TOL = 1e-4
 
 
