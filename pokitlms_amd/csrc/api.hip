@@ -101,7 +101,7 @@ struct pk_hip_ctx {
     DeviceBuffer<uint32_t> ids, words;  // words: [1..4] status
     DeviceBuffer<double> row_sum, row_bound;
     // prefill scratch (grown on demand)
-    DeviceBuffer<float> px, py, pprobs, pact, pout, pxsum, pasum;
+    DeviceBuffer<float> px, py, pprobs, pout, pxsum, pasum;
     DeviceBuffer<uint32_t> pids, poffsets, ptiles, pperm;
     DeviceBuffer<uint16_t> pxparts, paparts;
     DeviceBuffer<double> prow_sum, prow_bound;
@@ -476,7 +476,7 @@ void pk_hip_destroy(pk_hip_ctx* c) {
     c->words.release();
     c->row_sum.release();
     c->row_bound.release();
-    for (auto* b : {&c->px, &c->py, &c->pprobs, &c->pact, &c->pout, &c->pxsum, &c->pasum})
+    for (auto* b : {&c->px, &c->py, &c->pprobs, &c->pout, &c->pxsum, &c->pasum})
         b->release();
     for (auto* b : {&c->pids, &c->poffsets, &c->ptiles, &c->pperm}) b->release();
     c->pxparts.release();
@@ -745,7 +745,6 @@ void enqueue_prefill(pk_hip_ctx* c, const pk_hip_moe_layer* L, const MoeShape& m
     c->poffsets.ensure(E + 1);
     c->ptiles.ensure(static_cast<size_t>(max_tiles) + 1);
     c->pperm.ensure(T * K);
-    c->pact.ensure(T * K * m.ffn);
     c->pxparts.ensure(3 * T * m.hidden);
     c->pxsum.ensure(T * m.hidden / 16);
     c->paparts.ensure(3 * T * K * m.ffn);
@@ -794,7 +793,6 @@ void enqueue_prefill(pk_hip_ctx* c, const pk_hip_moe_layer* L, const MoeShape& m
     a.perm = c->pperm.ptr;
     a.x_parts = c->pxparts.ptr;
     a.x_sums = c->pxsum.ptr;
-    a.act = c->pact.ptr;
     a.act_parts = c->paparts.ptr;
     a.act_sums = c->pasum.ptr;
     a.out = c->pout.ptr;

@@ -61,7 +61,7 @@ hipError_t launch_moe_decode(const MoeDecodeArgs& a, hipStream_t stream);
 // expert for MFMA GEMMs.  Scratch sizes for `tokens` tokens (T), top_k (K),
 // n_experts (E), pairs P = T*K: row_sum/row_bound T*E, offsets E+1, tiles and
 // n_tiles moe_prefill_max_tiles(T, K, E) + 1, perm P, x_parts 3*T*hidden,
-// x_sums T*hidden/16, act P*ffn, act_parts 3*P*ffn, act_sums P*ffn/16,
+// x_sums T*hidden/16, act_parts 3*P*ffn, act_sums P*ffn/16,
 // out P*hidden.  Variant 1 (Qwen3.5) adds the shared expert as one more
 // route per token and one more router row and expert group: K = top_k + 1 and
 // E = n_experts + 1 in these sizes.
@@ -81,8 +81,7 @@ struct MoePrefillArgs {
     uint32_t* perm;          // [P]: grouped row -> token * top_k + route
     uint16_t* x_parts;       // 3 bf16 planes [tokens][hidden]: x = hi + mid + lo
     float* x_sums;           // [tokens][hidden / G]: sums over gate/up scale groups
-    float* act;              // [P][ffn], grouped rows
-    uint16_t* act_parts;     // 3 bf16 planes [P][ffn]
+    uint16_t* act_parts;     // 3 bf16 planes [P][ffn], grouped rows (gate/up epilogue)
     float* act_sums;         // [P][ffn / G]: sums over down scale groups
     float* out;              // [P][hidden], slot token * top_k + route
     uint32_t* status;        // as MoeDecodeArgs::status

@@ -869,17 +869,42 @@ __global__ __launch_bounds__(256, 2) void k_expert_gemm(MoePrefillArgs a) {
     gemm_compute<TW, DUAL>(st[s & 1u], acc, acc2);
     }
     const uint32_t col = n0 + wave * 32u + (lane % 32u);
+    if constexpr (DUAL) {
+        // SwiGLU g / (1 + expf(-g)) * u (src/qwen3_moe_runner.cpp:682-684);
+        // variant 1: silu(g) * u (src/qwen35_runner.cpp:111-123).  The value goes
+        // straight into the down GEMM's operands, as k_split would write them:
+        // three exact bf16 parts and, per scale group of the down format (16
+        // values for Q6_K, else 32: consecutive columns, so consecutive lanes),
+        // the FP64 sum of the group rounded once.  Absent rows (they repeat a
+        // real row) join the lane sums but are not stored.
+        const uint32_t gd = L.down_type == T_Q6_K ? 16u : 32u;
+        const uint64_t plane = static_cast<uint64_t>(a.tokens) * (L.top_k + L.variant) * ndim;
 #pragma unroll
-    for (uint32_t r = 0; r < 16; ++r) {
-        const uint32_t row = (r / 4u) * 8u + (lane / 32u) * 4u + (r % 4u);
-        if (row < tr.rows) {
-            if constexpr (DUAL) {
-                // SwiGLU g / (1 + expf(-g)) * u (src/qwen3_moe_runner.cpp:682-684);
-                // variant 1: silu(g) * u (src/qwen35_runner.cpp:111-123)
-                const float g = acc[r], u = acc2[r];
-                a.act[static_cast<uint64_t>(tr.base + row) * ndim + col] =
-                    L.variant ? silu(g) * u : (g / (1.0f + expf(-g))) * u;
-            } else {
+        for (uint32_t r = 0; r < 16; ++r) {
+            const uint32_t row = (r / 4u) * 8u + (lane / 32u) * 4u + (r % 4u);
+            const float g = acc[r], u = acc2[r];
+            const float v = L.variant ? silu(g) * u : (g / (1.0f + expf(-g))) * u;
+            const uint32_t h = bf16_rne_bits(v);
+            const float r1 = v - __uint_as_float(h << 16);
+            const uint32_t m = bf16_rne_bits(r1);
+            const float r2 = r1 - __uint_as_float(m << 16);  // at most 8 significant bits
+            const double sv = static_cast<double>(v);
+            const double gs = gd == 16u ? group_sum<16>(sv) : group_sum<32>(sv);
+            if (row < tr.rows) {
+                const uint64_t e = static_cast<uint64_t>(tr.base + row) * ndim + col;
+                a.act_parts[e] = static_cast<uint16_t>(h);
+                a.act_parts[plane + e] = static_cast<uint16_t>(m);
+                a.act_parts[2u * plane + e] = static_cast<uint16_t>(__float_as_uint(r2) >> 16);
+                if (col % gd == gd - 1u)
+                    a.act_sums[static_cast<uint64_t>(tr.base + row) * (ndim / gd) + col / gd] =
+                        static_cast<float>(gs);
+            }
+        }
+    } else {
+#pragma unroll
+        for (uint32_t r = 0; r < 16; ++r) {
+            const uint32_t row = (r / 4u) * 8u + (lane / 32u) * 4u + (r % 4u);
+            if (row < tr.rows) {
                 float* o = a.out + static_cast<uint64_t>(oslot[row]) * ndim + col;
                 o[0] = acc[r];
                 o[kTileN] = acc2[r];
@@ -931,11 +956,8 @@ template <int TW, bool DUAL>
 hipError_t expert_gemm_t(const MoePrefillArgs& a, hipStream_t s) {
     const MoeDecodeArgs& L = a.layer;
     constexpr uint32_t G = GemmCfg<TW, DUAL>::G;
-    if constexpr (DUAL)
+    if constexpr (DUAL)  // (the gate/up epilogue writes the down GEMM's split operands)
         split_t<G>(a.x, a.tokens, L.hidden, a.x_parts, a.x_sums, s);
-    else
-        split_t<G>(a.act, static_cast<uint64_t>(a.tokens) * (L.top_k + L.variant), L.ffn,
-                   a.act_parts, a.act_sums, s);
     const uint32_t nb = DUAL ? L.ffn / kTileN : L.hidden / (2u * kTileN);
     const uint32_t blocks = 8u * ceil_div_u(a.max_tiles, 8u) * nb;  // xcd_tile's layout
     hipLaunchKernelGGL((k_expert_gemm<TW, DUAL>), dim3(blocks), dim3(256), 0, s, a);
