@@ -3,10 +3,10 @@
 // The reference prefills a prompt one token at a time through the MoE block
 // of src/qwen3_moe_runner.cpp:643-692 (the loop at :785-790), so every
 // token's routes and output are those of a single-token pass.  Here the
-// whole batch goes through eight launches:
+// whole batch goes through seven launches:
 //
-//  1. k_router_batch: the exact logit value S and rounding bound B of every
-//     (token, expert) pair (the decode router's arithmetic, one expert row
+//  1. k_router_batch: the logit value S and rounding bound B of every
+//     (token, expert) pair (the decode router's arithmetic, a few expert rows
 //     held in registers across a tile of tokens).
 //  2. k_route_batch: one workgroup per token ranks the experts exactly as the
 //     decode path does (certified wave ranking, exact serial fallback) and
@@ -17,9 +17,10 @@
 //  4. k_split (x), then k_expert_gemm<gate/up>: per tile and 128 ffn rows,
 //     gate and up GEMMs on bf16 MFMA with exact products (x split into three
 //     bf16 planes, the quantised weights as bf16 integers, the scales applied
-//     per group outside the MFMA), and the SwiGLU epilogue.
-//  5. k_split (act), then k_expert_gemm<down>: per tile and 128 hidden rows;
-//     each output row goes to its (token, route) slot.
+//     per group outside the MFMA), and the SwiGLU epilogue, which writes the
+//     activations already split for the down GEMM.
+//  5. k_expert_gemm<down>: per tile and 128 hidden rows; each output row goes
+//     to its (token, route) slot.
 //  6. k_combine: y = ((0 + p0*o0) + p1*o1) + ... per token in route order
 //     (:688-690).
 //
