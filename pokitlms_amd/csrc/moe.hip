@@ -74,7 +74,7 @@ struct SharedRoutes {
 template <int T, int UB, int NU, int NP, int NS>
 __global__ __launch_bounds__(256) void k_gate_up(MoeDecodeArgs a, uint32_t units, uint32_t glog2) {
     extern __shared__ __attribute__((aligned(16))) float xs[];  // [hidden]
-    __shared__ FallbackShared fb;
+    __shared__ FallbackShared<128> fb;
     __shared__ SharedRoutes sr;
     const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
     const bool first_wave = blockIdx.x == 0 && wave == 0;
@@ -126,7 +126,7 @@ __global__ __launch_bounds__(256) void k_gate_up(MoeDecodeArgs a, uint32_t units
     }
     uint32_t sel[kMaxTopK];
     if (state == 1u) {  // rare: exact serial logits of the candidates
-        exact_routes<4>(a, sr.lo_min_sel, xs, fb, blockIdx.x == 0);
+        exact_routes<4, 128>(a, sr.lo_min_sel, xs, fb, blockIdx.x == 0);
         if (fb.bad) {  // uniform
             if (first_wave) flag_router_error(a);
             return;

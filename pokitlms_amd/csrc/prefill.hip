@@ -365,7 +365,7 @@ __global__ __launch_bounds__(kRouterThreads) void k_router_batch(MoePrefillArgs 
 template <int NS>
 __global__ __launch_bounds__(256) void k_route_batch(MoePrefillArgs A) {
     extern __shared__ __attribute__((aligned(16))) float xs[];  // [hidden]
-    __shared__ FallbackShared fb;
+    __shared__ FallbackShared<256> fb;
     __shared__ uint32_t s_sel[kMaxTopK];
     __shared__ uint32_t s_state;
     __shared__ double s_lo;
@@ -401,7 +401,7 @@ __global__ __launch_bounds__(256) void k_route_batch(MoePrefillArgs A) {
     }
     uint32_t sel[kMaxTopK];
     if (state == 1u) {  // rare: exact serial logits of the candidates
-        exact_routes<8>(a, s_lo, xs, fb, true);
+        exact_routes<4, 256>(a, s_lo, xs, fb, true);
         if (fb.bad) {
             if (wave == 0) flag_router_error(a);
             return;

@@ -233,14 +233,13 @@ __device__ __forceinline__ WaveRoutes<NS> wave_route(const MoeDecodeArgs& a, con
 // threads (rare).  The candidate experts' serial logits are chains of
 // dependent adds; fed from global memory one chunk ahead, each chunk would
 // wait a full memory latency.  Instead the workgroup streams the candidate
-// rows through LDS: up to kStageRows rows at a time, kStageChunk values per
-// row and chunk, D chunks in flight in registers spread over all threads,
+// rows through LDS: up to kStageRows rows at a time, CH values per row and
+// chunk, D chunks in flight in registers spread over all threads,
 // two LDS buffers; one thread per candidate runs the chain over the staged
 // chunk.
 constexpr uint32_t kStageRows = 16;
-constexpr uint32_t kStageChunk = 128;               // hidden is a multiple of 4 chunks
-constexpr uint32_t kStageStride = kStageChunk + 4;  // floats: rows start on different banks
 
+template <uint32_t CH>  // hidden is a multiple of CH
 struct FallbackShared {
     double logit[kMaxExperts];
     uint32_t rank[kMaxExperts];
@@ -248,17 +247,17 @@ struct FallbackShared {
     uint32_t cand[kMaxExperts];
     uint32_t ncand;
     uint32_t bad;  // a non-finite exact logit
-    alignas(16) float stage[2][kStageRows * kStageStride];
+    alignas(16) float stage[2][kStageRows * (CH + 4u)];  // rows start on different banks
 };
 
-// D chunks in flight: 4 in the decode gate/up kernel (its register budget),
-// 8 in the prefill ranking kernel.
-template <uint32_t D>
+// The decode gate/up kernel stages 128-value chunks (its LDS and register
+// budget), the prefill ranking kernel 256-value chunks (half the barriers).
+template <uint32_t D, uint32_t CH>
 __device__ __forceinline__ void exact_routes(const MoeDecodeArgs& a, double lo_min_sel,
-                                             const float* xs, FallbackShared& fb, bool count) {
-    constexpr uint32_t CH = kStageChunk;
-    constexpr uint32_t PIECES = kStageRows * CH / 4u;  // float4 pieces per chunk: 2 per thread
-    static_assert(PIECES == 512u, "two pieces per thread of 256");
+                                             const float* xs, FallbackShared<CH>& fb, bool count) {
+    constexpr uint32_t PP = kStageRows * CH / 4u / 256u;  // float4 pieces per thread and chunk
+    constexpr uint32_t SS = CH + 4u;
+    static_assert(PP * 256u * 4u == kStageRows * CH, "whole pieces per thread of 256");
     const uint32_t t = threadIdx.x, E = a.n_experts, H = a.hidden;
     if (t == 0) {
         fb.ncand = 0u;
@@ -281,21 +280,21 @@ __device__ __forceinline__ void exact_routes(const MoeDecodeArgs& a, double lo_m
     }
     for (uint32_t g0 = 0; g0 < nc; g0 += kStageRows) {
         const uint32_t rows = nc - g0 < kStageRows ? nc - g0 : kStageRows;
-        const float* src[2];
-        uint32_t dst[2], xcol[2];
+        const float* src[PP];
+        uint32_t dst[PP], xcol[PP];
 #pragma unroll
-        for (uint32_t p = 0; p < 2; ++p) {
+        for (uint32_t p = 0; p < PP; ++p) {
             const uint32_t q = t + 256u * p, r = q / (CH / 4u), col = 4u * (q % (CH / 4u));
             const uint32_t rr = r < rows ? r : 0u;  // rows past the group repeat row 0's loads
             src[p] = a.router + static_cast<uint64_t>(fb.cand[g0 + rr]) * H + col;
-            dst[p] = r * kStageStride + col;
+            dst[p] = r * SS + col;
             xcol[p] = col;
         }
-        rf32x4 ring[D][2];
+        rf32x4 ring[D][PP];
 #pragma unroll
         for (uint32_t d = 0; d + 1u < D; ++d)
 #pragma unroll
-            for (uint32_t p = 0; p < 2; ++p)
+            for (uint32_t p = 0; p < PP; ++p)
                 ring[d][p] = *reinterpret_cast<const rf32x4*>(src[p] + (d < nch ? d : nch - 1u) * CH);
         float s = 0.0f;
         for (uint32_t c0 = 0; c0 < nch; c0 += D) {
@@ -307,7 +306,7 @@ __device__ __forceinline__ void exact_routes(const MoeDecodeArgs& a, double lo_m
                 // stage the CPU's rounded products fl(w_i * x_i); the chain then
                 // only adds (dot_f32's order, src/simd_kernels.hpp:12-24)
 #pragma unroll
-                for (uint32_t p = 0; p < 2; ++p) {
+                for (uint32_t p = 0; p < PP; ++p) {
                     const rf32x4 xv = *reinterpret_cast<const rf32x4*>(xs + c * CH + xcol[p]);
                     rf32x4 pr;
                     pr.x = __fmul_rn(ring[k][p].x, xv.x);
@@ -321,7 +320,7 @@ __device__ __forceinline__ void exact_routes(const MoeDecodeArgs& a, double lo_m
                 if (t < rows) {
                     // 32 products in registers while the previous 32 are added, so
                     // the dependent adds do not wait on LDS latency
-                    const float* pr = &fb.stage[c & 1u][t * kStageStride];
+                    const float* pr = &fb.stage[c & 1u][t * SS];
                     rf32x4 A[8], B[8];
 #pragma unroll
                     for (uint32_t i = 0; i < 8; ++i) A[i] = *reinterpret_cast<const rf32x4*>(pr + 4u * i);
