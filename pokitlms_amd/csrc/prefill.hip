@@ -284,7 +284,7 @@ constexpr uint32_t router_rows_per_wg() { return C <= 8 ? 4u : C <= 16 ? 2u : 1u
 // runs ahead into the next token never overwrites what the finishing threads
 // still read.
 template <int C>
-__global__ __launch_bounds__(kRouterThreads) void k_router_batch(MoePrefillArgs a) {
+__global__ __launch_bounds__(kRouterThreads, 4) void k_router_batch(MoePrefillArgs a) {
     constexpr uint32_t EB = router_rows_per_wg<C>(), NW = kRouterThreads / 64;
     __shared__ double wtot[2][EB][NW];
     __shared__ double red[2][EB][NW];
