@@ -917,23 +917,45 @@ __global__ __launch_bounds__(256, 2) void k_expert_gemm(MoePrefillArgs a) {
 // ---------------------------------------------------------------------------
 // 6. Ordered combine.
 
+// Four consecutive outputs per thread (hidden is a multiple of 256), every
+// route's loads issued before the ordered sums.
 __global__ __launch_bounds__(256) void k_combine(MoePrefillArgs a) {
-    const uint32_t t = blockIdx.x, i = blockIdx.y * 256u + threadIdx.x;
+    const uint32_t t = blockIdx.x, i = (blockIdx.y * 256u + threadIdx.x) * 4u;
     const uint32_t K = a.layer.top_k, H = a.layer.hidden, E = a.layer.n_experts;
     const uint32_t V = a.layer.variant, KR = K + V;
     if (i >= H) return;
     bool ok = true;
     for (uint32_t r = 0; r < K; ++r) ok = ok && a.ids[t * K + r] < E;
     if (!ok) return;  // the router flagged this token
-    float y = 0.0f;
-    for (uint32_t r = 0; r < K; ++r)
-        y = __fadd_rn(y, __fmul_rn(a.probs[t * K + r],
-                                   a.out[(static_cast<uint64_t>(t) * KR + r) * H + i]));
-    if (V) {  // mixer_output = moe_result + sigmoid(shared gate) * shared (src/qwen35_runner.cpp:752-761)
-        const float gate = sigmoid35(static_cast<float>(a.row_sum[static_cast<uint64_t>(t) * (E + 1u) + E]));
-        y = __fadd_rn(y, __fmul_rn(gate, a.out[(static_cast<uint64_t>(t) * KR + K) * H + i]));
+    rf32x4 o[kMaxTopK + 1];
+    float p[kMaxTopK + 1];
+#pragma unroll
+    for (uint32_t r = 0; r < kMaxTopK + 1; ++r) {
+        const uint32_t rr = r < KR ? r : 0u;  // routes past the last re-read route 0 (unused)
+        o[r] = *reinterpret_cast<const rf32x4*>(a.out + (static_cast<uint64_t>(t) * KR + rr) * H + i);
+        p[r] = r < K ? a.probs[t * K + rr] : 0.0f;
     }
-    a.y[static_cast<uint64_t>(t) * H + i] = y;
+    rf32x4 y = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (uint32_t r = 0; r < kMaxTopK; ++r) {
+        if (r < K) {
+            y.x = __fadd_rn(y.x, __fmul_rn(p[r], o[r].x));
+            y.y = __fadd_rn(y.y, __fmul_rn(p[r], o[r].y));
+            y.z = __fadd_rn(y.z, __fmul_rn(p[r], o[r].z));
+            y.w = __fadd_rn(y.w, __fmul_rn(p[r], o[r].w));
+        }
+    }
+    if (V) {  // mixer_output = moe_result + sigmoid(shared gate) * shared (src/qwen35_runner.cpp:752-761)
+        const float g = sigmoid35(static_cast<float>(a.row_sum[static_cast<uint64_t>(t) * (E + 1u) + E]));
+        rf32x4 sh = o[0];
+#pragma unroll
+        for (uint32_t r = 1; r < kMaxTopK + 1; ++r) sh = r == K ? o[r] : sh;
+        y.x = __fadd_rn(y.x, __fmul_rn(g, sh.x));
+        y.y = __fadd_rn(y.y, __fmul_rn(g, sh.y));
+        y.z = __fadd_rn(y.z, __fmul_rn(g, sh.z));
+        y.w = __fadd_rn(y.w, __fmul_rn(g, sh.w));
+    }
+    *reinterpret_cast<rf32x4*>(a.y + static_cast<uint64_t>(t) * H + i) = y;
 }
 
 // ---------------------------------------------------------------------------
@@ -1038,7 +1060,7 @@ hipError_t launch_prefill_down(const MoePrefillArgs& a, hipStream_t s) {
     const MoeDecodeArgs& L = a.layer;
     const hipError_t err = expert_gemm<false>(L.down_type, a, s);
     if (err != hipSuccess) return err;
-    hipLaunchKernelGGL(k_combine, dim3(a.tokens, ceil_div_u(L.hidden, 256u)), dim3(256), 0, s, a);
+    hipLaunchKernelGGL(k_combine, dim3(a.tokens, ceil_div_u(L.hidden, 1024u)), dim3(256), 0, s, a);
     return hipGetLastError();
 }
 

@@ -214,3 +214,53 @@ def test_gpu_moe35_prefill_shared_expert_matters(hip):
         finally:
             h.release()
     assert normwise_rel(outs[0], outs[1]) > 1e-2
+
+
+@pytest.mark.gpu
+def test_gpu_moe35_prefill_async_graph_and_errors(hip):
+    """pk_hip_moe35_prefill_async on device buffers equals the synchronous
+    call bit for bit, also when captured in a HIP graph and replayed; a
+    narrower shared expert and a non-finite token are rejected like the
+    decode path rejects them."""
+    import torch
+    from pokitlms_amd.backend import HipError, Moe35LayerHandles, Unsupported
+    layer, xs = layer_tokens(*LAYERS[1][:2], 40)
+    h = hip.upload_moe35_layer(layer)
+    try:
+        y, ids, w = hip.moe35_prefill(h, xs)
+        dev = torch.device("cuda:0")
+        X = torch.from_numpy(xs.copy()).to(dev)
+        Y = torch.empty(xs.shape, device=dev)
+        I = torch.empty((xs.shape[0], layer.top_k), dtype=torch.int32, device=dev)
+        W = torch.empty((xs.shape[0], layer.top_k), device=dev)
+        torch.cuda.synchronize()
+        s = torch.cuda.Stream()
+        with torch.cuda.stream(s):
+            hip.moe35_prefill_async(h, X.data_ptr(), xs.shape[0], Y.data_ptr(), I.data_ptr(),
+                                    W.data_ptr(), s.cuda_stream)
+        s.synchronize()
+        assert np.array_equal(Y.cpu().numpy().view(np.uint32), y.view(np.uint32))
+        assert np.array_equal(I.cpu().numpy().astype(np.uint32), ids)
+        assert np.array_equal(W.cpu().numpy().view(np.uint32), w.view(np.uint32))
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=s):
+            hip.moe35_prefill_async(h, X.data_ptr(), xs.shape[0], Y.data_ptr(), I.data_ptr(),
+                                    W.data_ptr(), torch.cuda.current_stream().cuda_stream)
+        for _ in range(3):
+            Y.zero_()
+            torch.cuda.synchronize()
+            g.replay()
+            torch.cuda.synchronize()
+            assert np.array_equal(Y.cpu().numpy().view(np.uint32), y.view(np.uint32))
+        narrow = hip.upload(layer.gate_type, layer.hidden, 256,
+                            S.quant_matrix(layer.gate_type, 256, layer.hidden, S.rng(1)))
+        bad = Moe35LayerHandles(h, h.shared[0], narrow, h.shared[2], h.shared[3])
+        with pytest.raises((Unsupported, ValueError)):
+            hip.moe35_prefill(bad, xs[:4])
+        narrow.release()
+        poison = xs[:4].copy()
+        poison[2, 5] = np.nan
+        with pytest.raises(HipError):
+            hip.moe35_prefill(h, poison)
+    finally:
+        h.release()
