@@ -69,6 +69,8 @@ __device__ __forceinline__ void rank_select(const double* __restrict__ v, uint32
         const uint32_t half = (E + 1) / 2;
         const uint32_t j0 = paired ? (t & 1u) * half : 0u;
         const uint32_t j1 = paired ? ((t & 1u) ? E : half) : E;
+        // unrolled so the LDS reads of several experts are in flight together
+#pragma unroll 16
         for (uint32_t j = j0; j < j1; ++j) cnt += key_before(v[j], j, vc, c) ? 1u : 0u;
     }
     if (paired) cnt += static_cast<uint32_t>(__shfl_xor(static_cast<int>(cnt), 1, 64));
