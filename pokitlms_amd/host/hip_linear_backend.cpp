@@ -134,16 +134,16 @@ class HipMoeLayer {
 public:
     std::shared_ptr<HipLinearBackend::Impl> owner;
     WeightPtr router, gate, up, down;
+    WeightPtr shared_router, shared_gate, shared_up, shared_down;  // Qwen3.5 only
     std::uint32_t hidden = 0, ffn = 0, experts = 0, top_k = 0;
     bool normalize = false;
     float scale = 1.0F;
 
     ~HipMoeLayer() {
         std::lock_guard lock(owner->mutex);
-        router.reset();
-        gate.reset();
-        up.reset();
-        down.reset();
+        for (WeightPtr* w : {&router, &gate, &up, &down, &shared_router, &shared_gate, &shared_up,
+                             &shared_down})
+            w->reset();
     }
 };
 
@@ -233,6 +233,38 @@ std::shared_ptr<HipMoeLayer> HipLinearBackend::upload_moe_layer(
     return layer;
 }
 
+void HipLinearBackend::attach_shared_expert(HipMoeLayer& layer,
+                                            const model::TensorReader& shared_router,
+                                            const model::TensorReader& shared_gate,
+                                            const model::TensorReader& shared_up,
+                                            const model::TensorReader& shared_down) {
+    if (layer.owner != impl_)
+        throw std::invalid_argument("HIP MoE layer belongs to another backend");
+    const auto& rd = shared_router.tensor().dimensions;
+    const auto& gd = shared_gate.tensor().dimensions;
+    const auto& ud = shared_up.tensor().dimensions;
+    const auto& dd = shared_down.tensor().dimensions;
+    const bool router_ok = (rd.size() == 1 && rd[0] == layer.hidden) ||
+                           (rd.size() == 2 && rd[0] == layer.hidden && rd[1] == 1);
+    if (!router_ok || gd.size() != 2 || ud != gd || dd.size() != 2 || gd[0] != layer.hidden ||
+        dd[0] != gd[1] || dd[1] != layer.hidden || gd[1] > UINT32_MAX)
+        throw std::invalid_argument("HIP MoE layer: shared expert dimensions disagree");
+    const std::uint64_t ffn = gd[1];
+    WeightPtr r, g, u, d;
+    {
+        std::lock_guard lock(impl_->mutex);
+        impl_->require_usable();
+        r = impl_->upload(shared_router, layer.hidden, 1, 0);
+        g = impl_->upload(shared_gate, layer.hidden, ffn, 0);
+        u = impl_->upload(shared_up, layer.hidden, ffn, 0);
+        d = impl_->upload(shared_down, ffn, layer.hidden, 0);
+        layer.shared_router = std::move(r);
+        layer.shared_gate = std::move(g);
+        layer.shared_up = std::move(u);
+        layer.shared_down = std::move(d);
+    }
+}
+
 bool HipLinearBackend::try_moe_block(const HipMoeLayer& layer, std::span<const float> normalized,
                                      std::span<float> moe_result,
                                      std::span<std::uint32_t> route_ids,
@@ -257,8 +289,20 @@ bool HipLinearBackend::try_moe_block(const HipMoeLayer& layer, std::span<const f
     std::lock_guard lock(impl_->mutex);
     impl_->require_usable();
     ErrorBuffer err;
-    const auto st = pk_hip_moe_decode(impl_->ctx, &desc, normalized.data(), moe_result.data(),
-                                      ids.data(), probs.data(), err.data(), kErrorCapacity);
+    pk_hip_status st;
+    if (layer.shared_router) {  // Qwen3.5: select_experts weights and the shared expert
+        pk_hip_moe35_layer desc35{};
+        desc35.routed = desc;
+        desc35.shared_router = layer.shared_router.get();
+        desc35.shared_gate = layer.shared_gate.get();
+        desc35.shared_up = layer.shared_up.get();
+        desc35.shared_down = layer.shared_down.get();
+        st = pk_hip_moe35_decode(impl_->ctx, &desc35, normalized.data(), moe_result.data(),
+                                 ids.data(), probs.data(), err.data(), kErrorCapacity);
+    } else {
+        st = pk_hip_moe_decode(impl_->ctx, &desc, normalized.data(), moe_result.data(), ids.data(),
+                               probs.data(), err.data(), kErrorCapacity);
+    }
     if (st == PK_HIP_STATUS_UNSUPPORTED) return false;
     if (st != PK_HIP_STATUS_OK) impl_->raise(st, err);
     if (!route_ids.empty()) std::copy(ids.begin(), ids.end(), route_ids.begin());

@@ -84,6 +84,18 @@ public:
         std::size_t experts_per_token, bool expert_weights_norm,
         float expert_weights_scale = 1.0F);
 
+    // Qwen3.5-MoE: attaches the layer's shared expert (ffn_gate_inp_shexp
+    // [hidden], ffn_gate_shexp / ffn_up_shexp [hidden, ffn], ffn_down_shexp
+    // [ffn, hidden]; qwen35_runner.cpp:670-764).  try_moe_block then returns
+    // the block's mixer output: the routed sum with select_experts' weights
+    // (times expert_weights_scale) plus sigmoid(shared gate) * shared output.
+    // The shared expert must have the routed experts' types and width, or
+    // try_moe_block returns false.
+    void attach_shared_expert(HipMoeLayer& layer, const model::TensorReader& shared_router,
+                              const model::TensorReader& shared_gate,
+                              const model::TensorReader& shared_up,
+                              const model::TensorReader& shared_down);
+
     // moe_result = the MoE block of src/qwen3_moe_runner.cpp:644-691 for one
     // normalised hidden state (the residual add stays with the caller).
     // route_ids / route_probabilities (optional, size experts_per_token)

@@ -46,6 +46,21 @@ pkref_moe* pkref_moe_create(const float* router, std::uint32_t hidden, std::uint
 int pkref_moe_forward(pkref_moe* moe, const float* x, float* y, std::uint32_t* ids,
                       float* probabilities);
 void pkref_moe_destroy(pkref_moe* moe);
+
+// The reference Qwen3.5-MoE block (src/qwen35_runner.cpp:670-764, with its
+// select_experts, silu and sigmoid), compiled by oracle/ref_shim35.cpp.
+struct pkref_moe35;
+pkref_moe35* pkref_moe35_create(const float* router, std::uint32_t hidden, std::uint32_t experts,
+                                std::uint32_t ffn, std::uint32_t gate_type, const void* gate,
+                                std::uint32_t up_type, const void* up, std::uint32_t down_type,
+                                const void* down, std::uint32_t top_k, int normalize, float scale,
+                                const float* shared_router, std::uint32_t shared_ffn,
+                                std::uint32_t sgate_type, const void* sgate,
+                                std::uint32_t sup_type, const void* sup,
+                                std::uint32_t sdown_type, const void* sdown);
+int pkref_moe35_forward(pkref_moe35* m, const float* x, float* y, std::uint32_t* ids,
+                        float* weights);
+void pkref_moe35_destroy(pkref_moe35* m);
 }
 
 namespace {
@@ -386,6 +401,75 @@ void moe_cases(HipLinearBackend& hip, const Layer& L, const char* label, int tok
     report(ok, "moe_block_parity", d);
 }
 
+TensorReader tensor2(std::uint32_t type, std::uint64_t in, std::uint64_t out,
+                     const std::vector<std::byte>& bytes) {
+    TensorInfo t;
+    t.name = "shared";
+    t.dimensions = {in, out};
+    t.type = type;
+    t.payload_size = bytes.size();
+    return TensorReader(t, std::make_shared<const std::vector<std::byte>>(bytes));
+}
+
+// The Qwen3.5 block through try_moe_block with the shared expert attached,
+// against the reference block: ids equal, weights and mixer outputs within
+// 1e-4 normwise.
+void moe35_cases(HipLinearBackend& hip, const Layer& L, float scale, const char* label, int tokens) {
+    Rng g(0x35 + L.hidden);
+    std::vector<float> shared_router(L.hidden);
+    for (auto& v : shared_router) v = g.normal(0.2F);
+    const auto sgate = make_matrix(12, L.ffn, L.hidden, g), sup = make_matrix(12, L.ffn, L.hidden, g);
+    const auto sdown = make_matrix(14, L.hidden, L.ffn, g);
+    std::vector<std::byte> router_bytes(L.router.size() * 4), srouter_bytes(L.hidden * 4);
+    std::memcpy(router_bytes.data(), L.router.data(), router_bytes.size());
+    std::memcpy(srouter_bytes.data(), shared_router.data(), srouter_bytes.size());
+    TensorInfo rt;
+    rt.name = "router";
+    rt.dimensions = {L.hidden, L.experts};
+    rt.type = 0;
+    rt.payload_size = router_bytes.size();
+    const TensorReader router(rt, std::make_shared<const std::vector<std::byte>>(router_bytes));
+    TensorInfo st;
+    st.name = "ffn_gate_inp_shexp";
+    st.dimensions = {L.hidden};
+    st.type = 0;
+    st.payload_size = srouter_bytes.size();
+    const TensorReader srouter(st, std::make_shared<const std::vector<std::byte>>(srouter_bytes));
+    const auto layer = hip.upload_moe_layer(router, tensor3(12, L.hidden, L.ffn, L.experts, L.gate),
+                                            tensor3(12, L.hidden, L.ffn, L.experts, L.up),
+                                            tensor3(14, L.ffn, L.hidden, L.experts, L.down),
+                                            L.top_k, L.normalize, scale);
+    hip.attach_shared_expert(*layer, srouter, tensor2(12, L.hidden, L.ffn, sgate),
+                             tensor2(12, L.hidden, L.ffn, sup), tensor2(14, L.ffn, L.hidden, sdown));
+    pkref_moe35* ref = pkref_moe35_create(
+        L.router.data(), L.hidden, L.experts, L.ffn, 12, L.gate.data(), 12, L.up.data(), 14,
+        L.down.data(), L.top_k, L.normalize ? 1 : 0, scale, shared_router.data(), L.ffn, 12,
+        sgate.data(), 12, sup.data(), 14, sdown.data());
+    if (!ref) {
+        report(false, "moe35_block", std::string(label) + ": reference block not created");
+        return;
+    }
+    std::vector<float> x(L.hidden), y(L.hidden), cy(L.hidden), w(L.top_k), cw(L.top_k);
+    std::vector<std::uint32_t> ids(L.top_k), cids(L.top_k);
+    bool ok = true;
+    double worst = 0.0, worst_w = 0.0;
+    for (int t = 0; t < tokens; ++t) {
+        for (auto& v : x) v = g.normal(1.0F);
+        ok = ok && hip.try_moe_block(*layer, x, y, ids, w);
+        ok = ok && pkref_moe35_forward(ref, x.data(), cy.data(), cids.data(), cw.data()) == 0;
+        ok = ok && ids == cids;
+        for (auto& v : cw) v *= scale;  // the shim returns select_experts' weights before the scale
+        worst_w = std::max(worst_w, compare(w, cw).normwise);
+        worst = std::max(worst, compare(y, cy).normwise);
+    }
+    ok = ok && worst <= 1e-4 && worst_w <= 1e-4;
+    pkref_moe35_destroy(ref);
+    char d[200];
+    std::snprintf(d, sizeof d, "%s: %d tokens, ids equal, max_normwise=%.3g, weights %.3g", label,
+                  tokens, worst, worst_w);
+    report(ok, "moe35_block_parity", d);
+}
+
 void moe_error_cases(HipLinearBackend& hip) {
     Layer L = make_layer(512, 16, 256, 4, true, 0xbad);
     L.router[5 * 512 + 17] = INFINITY;  // expert 5's logit is not finite
@@ -434,6 +518,8 @@ int main(int argc, char** argv) {
         shape_error_cases(hip);
         file_backed_cases(hip);
         moe_cases(hip, make_layer(512, 16, 256, 4, false, 0x5eed0005), "hidden 512, 16 experts, top-4", 16);
+        moe35_cases(hip, make_layer(1024, 32, 512, 6, true, 0x5eed0035), 2.5F,
+                    "Qwen3.5 hidden 1024, 32 experts, top-6, scale 2.5", 16);
         moe_cases(hip, make_layer(2048, 128, 768, 8, true, 0x5eed0006),
                   "hidden 2048, 128 experts, top-8 (config 3 shape)", 16);
         moe_error_cases(hip);

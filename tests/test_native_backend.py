@@ -6,7 +6,8 @@ On the GPU it runs every case: try_linear through tensor_linear's backend hook
 (src/tensor_linear.cpp:213) for F32/F16/BF16/Q4_0/Q4_1/Q8_0/Q4_K/Q5_K/Q6_K against
 the CPU kernels; false for the formats without a kernel; shape errors;
 file-backed tensors kept resident; the MoE block hook against the reference
-MoE block (ids exact, outputs normwise <= 1e-4); a non-finite router as a
+MoE block and the Qwen3.5 block with its shared expert (ids exact, outputs
+normwise <= 1e-4); a non-finite router as a
 data error that leaves the backend usable.
 """
 import os
@@ -47,3 +48,4 @@ def test_native_backend_cases():
     assert sum(l.startswith("PASS try_linear_parity") for l in lines) == 9
     assert sum(l.startswith("PASS try_linear_unsupported") for l in lines) == 4
     assert sum(l.startswith("PASS moe_block_parity") for l in lines) == 2
+    assert sum(l.startswith("PASS moe35_block_parity") for l in lines) == 1
