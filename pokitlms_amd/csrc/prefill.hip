@@ -447,17 +447,35 @@ __global__ __launch_bounds__(kGroupThreads) void k_group(MoePrefillArgs a) {
         for (uint32_t t = tid; t < a.tokens; t += kGroupThreads)
             if (a.ids[t * K] < E) atomicAdd(&cnt[E], 1u);
     __syncthreads();
-    if (tid == 0) {
-        uint32_t o = 0, b = 0;
-        for (uint32_t e = 0; e < EE; ++e) {
-            off[e] = o;
-            tb[e] = b;
-            o += cnt[e];
-            b += (cnt[e] + kTileM - 1u) / kTileM;
+    if (tid < 64) {  // exclusive prefix of rows and tiles: PER experts a lane, one wave scan
+        constexpr uint32_t PER = (NE + 63u) / 64u;
+        uint32_t c[PER], tl[PER];
+        double lc = 0.0, lt = 0.0;  // integer sums, exact in FP64
+#pragma unroll
+        for (uint32_t k = 0; k < PER; ++k) {
+            const uint32_t e = tid * PER + k;
+            c[k] = e < EE ? cnt[e] : 0u;
+            tl[k] = (c[k] + kTileM - 1u) / kTileM;
+            lc += static_cast<double>(c[k]);
+            lt += static_cast<double>(tl[k]);
         }
-        off[EE] = o;
-        tb[EE] = b;
-        a.n_tiles[0] = b;
+        const double ic = wave_inclusive_scan(lc), it = wave_inclusive_scan(lt);
+        uint32_t o = static_cast<uint32_t>(ic - lc), b = static_cast<uint32_t>(it - lt);
+#pragma unroll
+        for (uint32_t k = 0; k < PER; ++k) {
+            const uint32_t e = tid * PER + k;
+            if (e < EE) {
+                off[e] = o;
+                tb[e] = b;
+            }
+            o += c[k];
+            b += tl[k];
+        }
+        if (tid == 63u) {
+            off[EE] = static_cast<uint32_t>(ic);
+            tb[EE] = static_cast<uint32_t>(it);
+            a.n_tiles[0] = static_cast<uint32_t>(it);
+        }
     }
     __syncthreads();
     if (tid <= EE) a.offsets[tid] = off[tid];
