@@ -183,7 +183,7 @@ def prefill_leg(torch, hip, layers, stream, reps: int, cpu_ms_per_token):
         "flops_per_batch": PREFILL_FLOPS,
         "tflops": round(whole_tflops, 2),
         "roofline": {"bound": "mfma",
-                     "kernel": "k_split + k_expert_gemm<Q4_K, gate/up> (v_mfma_f32_32x32x16_bf16)",
+                     "kernel": "k_expert_gemm<Q4_K, gate/up> (v_mfma_f32_32x32x16_bf16)",
                      "achieved": round(gu_tflops, 2), "peak": MFMA_BF16_PEAK_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(gu_tflops / MFMA_BF16_PEAK_TFLOPS, 4),
                      "mfma_issued_tflops": round(SPLIT_PASSES * gu_tflops, 2),

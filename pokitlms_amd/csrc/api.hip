@@ -807,7 +807,7 @@ void enqueue_prefill(pk_hip_ctx* c, const pk_hip_moe_layer* L, const MoeShape& m
     begin_timing(c, s, 9);
     ++c->stats.prefill_calls;
     c->stats.prefill_tokens += tokens;
-    c->stats.dispatches += 7;
+    c->stats.dispatches += 6;
     count_dispatch(c, L->gate->type);
     count_dispatch(c, L->down->type);
     c->stats.dispatches -= 2;

@@ -3,7 +3,7 @@
 // The reference prefills a prompt one token at a time through the MoE block
 // of src/qwen3_moe_runner.cpp:643-692 (the loop at :785-790), so every
 // token's routes and output are those of a single-token pass.  Here the
-// whole batch goes through seven launches:
+// whole batch goes through six launches:
 //
 //  1. k_router_batch: the logit value S and rounding bound B of every
 //     (token, expert) pair (the decode router's arithmetic, a few expert rows
@@ -13,8 +13,9 @@
 //     writes ids and route weights.
 //  3. k_group: one workgroup counts each expert's tokens and lays out
 //     per-expert row ranges, a list of 32-row tiles and the assignments
-//     (token * top_k + route) grouped by expert.
-//  4. k_split (x), then k_expert_gemm<gate/up>: per tile and 128 ffn rows,
+//     (token * top_k + route) grouped by expert; its other workgroups split
+//     x into the gate/up GEMM's operands meanwhile.
+//  4. k_expert_gemm<gate/up>: per tile and 128 ffn rows,
 //     gate and up GEMMs on bf16 MFMA with exact products (x split into three
 //     bf16 planes, the quantised weights as bf16 integers, the scales applied
 //     per group outside the MFMA), and the SwiGLU epilogue, which writes the
@@ -421,14 +422,88 @@ __global__ __launch_bounds__(256) void k_route_batch(MoePrefillArgs A) {
 }
 
 // ---------------------------------------------------------------------------
-// 3. Grouping (one workgroup of 1024 threads): per-expert counts from the
+// 3. Split-bf16 operands.  Every FP32 value x is exactly hi + mid + lo with
+// three bf16 values (8 significant bits each and FP32's exponent range:
+// hi = RNE(x), mid = RNE(x - hi), lo = x - hi - mid, each difference exact).
+// With the weights' integer fields as bf16 (raw32_bf16), every product of the
+// expert GEMMs is exact in the FP32 accumulators of the bf16 MFMA; the
+// per-group scales are applied outside it.  split_piece writes the three planes
+// of `rows` x `cols` FP32 values and, per G consecutive values of a row,
+// their sum (accumulated in FP64, rounded once).
+
+__device__ __forceinline__ uint32_t bf16_rne_bits(float x) {  // finite x
+    const uint32_t u = __float_as_uint(x);
+    return (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+}
+
+template <uint32_t G>
+__device__ __forceinline__ void split_piece(const float* __restrict__ src, uint32_t i,
+                                            uint32_t pieces, uint16_t* __restrict__ parts,
+                                            uint64_t plane, float* __restrict__ sums) {
+    // i: this lane's 16-value piece (pairs of pieces in neighbouring lanes)
+    const uint32_t ic = i < pieces ? i : pieces - 1u;    // every lane loads (and shuffles)
+    const float4* sp = reinterpret_cast<const float4*>(src + static_cast<uint64_t>(ic) * 16u);
+    float v[16];
+#pragma unroll
+    for (uint32_t j = 0; j < 4; ++j) {
+        const float4 f = sp[j];
+        v[4 * j] = f.x;
+        v[4 * j + 1] = f.y;
+        v[4 * j + 2] = f.z;
+        v[4 * j + 3] = f.w;
+    }
+    uint32_t ph[8], pm[8], pl[8];
+    double sum = 0.0;
+#pragma unroll
+    for (uint32_t e = 0; e < 16; e += 2) {
+        uint32_t h2[2], m2[2], l2[2];
+#pragma unroll
+        for (uint32_t t = 0; t < 2; ++t) {
+            const float x = v[e + t];
+            sum += static_cast<double>(x);
+            h2[t] = bf16_rne_bits(x);
+            const float r1 = x - __uint_as_float(h2[t] << 16);
+            m2[t] = bf16_rne_bits(r1);
+            const float r2 = r1 - __uint_as_float(m2[t] << 16);
+            l2[t] = __float_as_uint(r2) >> 16;  // r2 has at most 8 significant bits
+        }
+        ph[e / 2] = h2[0] | (h2[1] << 16);
+        pm[e / 2] = m2[0] | (m2[1] << 16);
+        pl[e / 2] = l2[0] | (l2[1] << 16);
+    }
+    if constexpr (G == 32) sum += __shfl_xor(sum, 1);
+    if (i >= pieces) return;
+    uint4* d0 = reinterpret_cast<uint4*>(parts + static_cast<uint64_t>(i) * 16u);
+    uint4* d1 = reinterpret_cast<uint4*>(parts + plane + static_cast<uint64_t>(i) * 16u);
+    uint4* d2 = reinterpret_cast<uint4*>(parts + 2u * plane + static_cast<uint64_t>(i) * 16u);
+    d0[0] = make_uint4(ph[0], ph[1], ph[2], ph[3]);
+    d0[1] = make_uint4(ph[4], ph[5], ph[6], ph[7]);
+    d1[0] = make_uint4(pm[0], pm[1], pm[2], pm[3]);
+    d1[1] = make_uint4(pm[4], pm[5], pm[6], pm[7]);
+    d2[0] = make_uint4(pl[0], pl[1], pl[2], pl[3]);
+    d2[1] = make_uint4(pl[4], pl[5], pl[6], pl[7]);
+    if (G == 16 || (i & 1u) == 0u) sums[i * 16u / G] = static_cast<float>(sum);
+}
+
+// ---------------------------------------------------------------------------
+// 4. Grouping (workgroup 0, 1024 threads): per-expert counts from the
 // ids (LDS atomics), row ranges, the 32-row tile list and the assignments
 // (token * top_k + route) grouped by expert.  Tokens the router flagged
 // (ids 0xffffffff) take no rows.
 
 constexpr uint32_t kGroupThreads = 1024;
 
+// Workgroup 0 groups; the others split x into the gate/up GEMM's operands
+// (G: the gate/up format's scale group) while it does, since the grouping
+// alone would leave the rest of the chip idle.
+template <uint32_t G>
 __global__ __launch_bounds__(kGroupThreads) void k_group(MoePrefillArgs a) {
+    if (blockIdx.x > 0u) {
+        const uint64_t plane = static_cast<uint64_t>(a.tokens) * a.layer.hidden;
+        split_piece<G>(a.x, (blockIdx.x - 1u) * kGroupThreads + threadIdx.x,
+                       static_cast<uint32_t>(plane / 16u), a.x_parts, plane, a.x_sums);
+        return;
+    }
     constexpr uint32_t NE = kMaxExperts + 1;  // + the shared expert (variant 1)
     __shared__ uint32_t cnt[NE], off[NE + 1], tb[NE + 1], fill[NE];
     const uint32_t E = a.layer.n_experts, K = a.layer.top_k, V = a.layer.variant, tid = threadIdx.x;
@@ -492,70 +567,6 @@ __global__ __launch_bounds__(kGroupThreads) void k_group(MoePrefillArgs a) {
     if (V)
         for (uint32_t t = tid; t < a.tokens; t += kGroupThreads)
             if (a.ids[t * K] < E) a.perm[off[E] + atomicAdd(&fill[E], 1u)] = t * KR + K;
-}
-
-// ---------------------------------------------------------------------------
-// 4. Split-bf16 operands.  Every FP32 value x is exactly hi + mid + lo with
-// three bf16 values (8 significant bits each and FP32's exponent range:
-// hi = RNE(x), mid = RNE(x - hi), lo = x - hi - mid, each difference exact).
-// With the weights' integer fields as bf16 (raw32_bf16), every product of the
-// expert GEMMs is exact in the FP32 accumulators of the bf16 MFMA; the
-// per-group scales are applied outside it.  k_split writes the three planes
-// of `rows` x `cols` FP32 values and, per G consecutive values of a row,
-// their sum (accumulated in FP64, rounded once).
-
-__device__ __forceinline__ uint32_t bf16_rne_bits(float x) {  // finite x
-    const uint32_t u = __float_as_uint(x);
-    return (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
-}
-
-template <uint32_t G>
-__global__ __launch_bounds__(256) void k_split(const float* __restrict__ src, uint32_t pieces,
-                                               uint16_t* __restrict__ parts, uint64_t plane,
-                                               float* __restrict__ sums) {
-    const uint32_t i = blockIdx.x * 256u + threadIdx.x;  // 16-value piece
-    const uint32_t ic = i < pieces ? i : pieces - 1u;    // every lane loads (and shuffles)
-    const float4* sp = reinterpret_cast<const float4*>(src + static_cast<uint64_t>(ic) * 16u);
-    float v[16];
-#pragma unroll
-    for (uint32_t j = 0; j < 4; ++j) {
-        const float4 f = sp[j];
-        v[4 * j] = f.x;
-        v[4 * j + 1] = f.y;
-        v[4 * j + 2] = f.z;
-        v[4 * j + 3] = f.w;
-    }
-    uint32_t ph[8], pm[8], pl[8];
-    double sum = 0.0;
-#pragma unroll
-    for (uint32_t e = 0; e < 16; e += 2) {
-        uint32_t h2[2], m2[2], l2[2];
-#pragma unroll
-        for (uint32_t t = 0; t < 2; ++t) {
-            const float x = v[e + t];
-            sum += static_cast<double>(x);
-            h2[t] = bf16_rne_bits(x);
-            const float r1 = x - __uint_as_float(h2[t] << 16);
-            m2[t] = bf16_rne_bits(r1);
-            const float r2 = r1 - __uint_as_float(m2[t] << 16);
-            l2[t] = __float_as_uint(r2) >> 16;  // r2 has at most 8 significant bits
-        }
-        ph[e / 2] = h2[0] | (h2[1] << 16);
-        pm[e / 2] = m2[0] | (m2[1] << 16);
-        pl[e / 2] = l2[0] | (l2[1] << 16);
-    }
-    if constexpr (G == 32) sum += __shfl_xor(sum, 1);
-    if (i >= pieces) return;
-    uint4* d0 = reinterpret_cast<uint4*>(parts + static_cast<uint64_t>(i) * 16u);
-    uint4* d1 = reinterpret_cast<uint4*>(parts + plane + static_cast<uint64_t>(i) * 16u);
-    uint4* d2 = reinterpret_cast<uint4*>(parts + 2u * plane + static_cast<uint64_t>(i) * 16u);
-    d0[0] = make_uint4(ph[0], ph[1], ph[2], ph[3]);
-    d0[1] = make_uint4(ph[4], ph[5], ph[6], ph[7]);
-    d1[0] = make_uint4(pm[0], pm[1], pm[2], pm[3]);
-    d1[1] = make_uint4(pm[4], pm[5], pm[6], pm[7]);
-    d2[0] = make_uint4(pl[0], pl[1], pl[2], pl[3]);
-    d2[1] = make_uint4(pl[4], pl[5], pl[6], pl[7]);
-    if (G == 16 || (i & 1u) == 0u) sums[i * 16u / G] = static_cast<float>(sum);
 }
 
 // ---------------------------------------------------------------------------
@@ -985,20 +996,10 @@ bool prefill_type_ok(uint32_t t) {
 
 uint32_t ceil_div_u(uint32_t a, uint32_t b) { return (a + b - 1u) / b; }
 
-template <uint32_t G>
-void split_t(const float* src, uint64_t rows, uint32_t cols, uint16_t* parts, float* sums,
-             hipStream_t s) {
-    const uint32_t pieces = static_cast<uint32_t>(rows * cols / 16u);
-    hipLaunchKernelGGL(k_split<G>, dim3(ceil_div_u(pieces, 256u)), dim3(256), 0, s, src, pieces,
-                       parts, rows * cols, sums);
-}
-
 template <int TW, bool DUAL>
 hipError_t expert_gemm_t(const MoePrefillArgs& a, hipStream_t s) {
     const MoeDecodeArgs& L = a.layer;
-    constexpr uint32_t G = GemmCfg<TW, DUAL>::G;
-    if constexpr (DUAL)  // (the gate/up epilogue writes the down GEMM's split operands)
-        split_t<G>(a.x, a.tokens, L.hidden, a.x_parts, a.x_sums, s);
+    // (x is split beside the grouping, the activations by the gate/up epilogue)
     const uint32_t nb = DUAL ? L.ffn / kTileN : L.hidden / (2u * kTileN);
     const uint32_t blocks = 8u * ceil_div_u(a.max_tiles, 8u) * nb;  // xcd_tile's layout
     hipLaunchKernelGGL((k_expert_gemm<TW, DUAL>), dim3(blocks), dim3(256), 0, s, a);
@@ -1066,7 +1067,10 @@ hipError_t launch_prefill_routing(const MoePrefillArgs& a, hipStream_t s) {
         default: hipLaunchKernelGGL(k_route_batch<4>, dim3(a.tokens), dim3(256), xlds, s, a); break;
     }
     // 3. grouping
-    hipLaunchKernelGGL(k_group, dim3(1), dim3(kGroupThreads), 0, s, a);
+    const uint32_t xpieces = a.tokens * L.hidden / 16u;
+    const dim3 ggrid(1u + ceil_div_u(xpieces, kGroupThreads));
+    if (L.gate_type == T_Q6_K) hipLaunchKernelGGL(k_group<16>, ggrid, dim3(kGroupThreads), 0, s, a);
+    else hipLaunchKernelGGL(k_group<32>, ggrid, dim3(kGroupThreads), 0, s, a);
     return hipGetLastError();
 }
 
