@@ -902,7 +902,7 @@ __global__ __launch_bounds__(256, 2) void k_expert_gemm(MoePrefillArgs a) {
     if constexpr (DUAL) {
         // SwiGLU g / (1 + expf(-g)) * u (src/qwen3_moe_runner.cpp:682-684);
         // variant 1: silu(g) * u (src/qwen35_runner.cpp:111-123).  The value goes
-        // straight into the down GEMM's operands, as k_split would write them:
+        // straight into the down GEMM's operands, as split_piece writes x:
         // three exact bf16 parts and, per scale group of the down format (16
         // values for Q6_K, else 32: consecutive columns, so consecutive lanes),
         // the FP64 sum of the group rounded once.  Absent rows (they repeat a
