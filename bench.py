@@ -50,6 +50,10 @@ def parse():
     ap.add_argument("--no-prefill", action="store_true", help="skip the batched-prefill leg")
     ap.add_argument("--prefill-reps", type=int, default=40)
     ap.add_argument("--no-decode", action="store_true", help="skip the whole-model decode leg")
+    ap.add_argument("--no-matvec", action="store_true", help="skip the C1/C2 matvec leg")
+    ap.add_argument("--matvec-reps", type=int, default=10)
+    ap.add_argument("--matvec-only", action="store_true",
+                    help="run only the C1/C2 matvec leg (prints its JSON)")
     ap.add_argument("--calibrate-copy-mib", type=int, default=0,
                     help="first run a plain device copy of this many MiB three times "
                          "(the known-size kernel that scales rocprofv3 FETCH/WRITE_SIZE)")
@@ -205,6 +209,87 @@ def prefill_leg(torch, hip, layers, stream, reps: int, cpu_ms_per_token):
                                          "single-token pass time of the decode baseline"}
         out["speedup_vs_cpu"] = round(out["tokens_per_s"] / cpu_tps, 1)
     r.release()
+    return out
+
+
+MATVEC_COPIES = 64  # distinct weight copies per case (at most; > 2x the 256 MB MALL)
+
+
+def matvec_cases():
+    """BASELINE configs[0] (Q4_K 4096x4096, one vector) and configs[1] (five
+    formats at 2048x6144 and 6144x2048, out x in, batches of 1, 4 and 8)."""
+    from pokitlms_amd import synth as S
+    cases = [("c1", S.Q4_K, 4096, 4096, 1)]
+    for t in (S.Q4_0, S.Q8_0, S.Q4_K, S.Q5_K, S.Q6_K):
+        for out, inn in ((2048, 6144), (6144, 2048)):
+            for b in (1, 4, 8):
+                cases.append(("c2", t, out, inn, b))
+    # the config-5 model's Q6_K output head (151936 x 2048, 255 MB), one vector
+    cases.append(("c5_head", S.Q6_K, 151936, 2048, 1))
+    return cases
+
+
+def matvec_leg(torch, hip, stream, reps: int, only=None):
+    """K-quant matvec throughput (configs[0..1]).  Each case's weights are one
+    expert tensor of MATVEC_COPIES distinct random matrices made on the GPU;
+    a HIP graph launches the matvec once per copy, so the weights stream from
+    HBM, and replays `reps` times (per-launch time = graph time / launches,
+    inter-kernel gaps included).  The library's launch-stream events then
+    time 64 single launches (each queued behind a hold kernel), which is the
+    kernel's own duration plus its dispatch.  GB/s counts the algorithmic
+    bytes: the weights once plus 4 * batch * (in + out)."""
+    from pokitlms_amd import synth as S
+    dev = torch.device("cuda:0")
+    out = []
+    for name, gtype, rows, inn, batch in matvec_cases():
+        if only and (S.TYPE_NAMES[gtype], rows, inn, batch) not in only:
+            continue
+        gen = torch.Generator(device=dev)
+        gen.manual_seed(5000 + gtype * 64 + batch + (rows // 2048))
+        copies = max(4, min(MATVEC_COPIES, (1 << 31) // S.matrix_bytes(gtype, inn, rows)))
+        buf = device_quant(torch, gtype, copies * rows, inn, gen, dev)
+        w = hip.upload_device(gtype, inn, rows, buf.data_ptr(), buf.numel(), copies)
+        del buf
+        X = torch.randn(batch, inn, device=dev, generator=gen)
+        Y = torch.empty(copies, batch, rows, device=dev)
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=stream):
+            cs = torch.cuda.current_stream().cuda_stream
+            for e in range(copies):
+                hip.matvec_async(w, X.data_ptr(), batch, Y[e].data_ptr(), cs, expert=e)
+        with torch.cuda.stream(stream):
+            g.replay()
+            torch.cuda.synchronize()
+            ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            ev0.record(stream)
+            for _ in range(reps):
+                g.replay()
+            ev1.record(stream)
+            ev1.synchronize()
+        us_graph = ev0.elapsed_time(ev1) * 1e3 / (reps * copies)
+        hip.reset_stats()
+        hip.set_kernel_timing(True)
+        with torch.cuda.stream(stream):
+            for e in range(copies):
+                hip.matvec_async(w, X.data_ptr(), batch, Y[e].data_ptr(),
+                                 stream.cuda_stream, expert=e)
+        hip.set_kernel_timing(False)
+        st = hip.stats()
+        us_event = st["matvec_ns"] / st["matvec_launches"] / 1e3
+        nbytes = S.matrix_bytes(gtype, inn, rows) + 4 * batch * (inn + rows)
+        out.append({"config": name, "type": S.TYPE_NAMES[gtype], "out": rows, "in": inn,
+                    "batch": batch, "bytes": nbytes, "copies": copies,
+                    "us_graph": round(us_graph, 3), "us_event": round(us_event, 3),
+                    "gbs_graph": round(nbytes / us_graph / 1e3, 1),
+                    "gbs_event": round(nbytes / us_event / 1e3, 1),
+                    "frac_event": round(nbytes / us_event / 1e3 / HBM_PEAK_GBS, 4)})
+        log(f"matvec {name} {S.TYPE_NAMES[gtype]} {rows}x{inn} B={batch}: "
+            f"{us_graph:.2f} us/launch (graph), {us_event:.2f} us (event), "
+            f"{nbytes / us_graph / 1e3:.0f} GB/s")
+        del g, X, Y
+        w.release()
+        torch.cuda.synchronize()
     return out
 
 
@@ -370,6 +455,11 @@ def main():
         log(f"copy calibration: 3 x {args.calibrate_copy_mib} MiB device copies")
         del src, dst
     hip = HipBackend(0)
+    if args.matvec_only:
+        print(json.dumps({"matvec": matvec_leg(torch, hip, torch.cuda.Stream(),
+                                               args.matvec_reps)}), flush=True)
+        hip.close()
+        return
     log(f"building {args.layers} resident layers ...")
     layers = build_layers(torch, hip, args.layers, dev)
     step_bytes = layers[0].routed_bytes()
@@ -508,6 +598,11 @@ def main():
         prefill = prefill_leg(torch, hip, layers[:4], stream, args.prefill_reps,
                               cpu["ms_per_token"] if cpu else None)
 
+    matvec = None
+    if not args.no_matvec:
+        log("matvec leg ...")
+        matvec = matvec_leg(torch, hip, stream, args.matvec_reps)
+
     decode = None
     if not args.no_decode:
         log("whole-model decode leg ...")
@@ -549,6 +644,7 @@ def main():
         "parity": parity,
         "cpu_baseline": cpu,
         "prefill": prefill,
+        "matvec": matvec,
         "decode": decode,
     }
     if cpu:

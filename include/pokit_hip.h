@@ -115,8 +115,19 @@ pk_hip_status pk_hip_upload_device(pk_hip_ctx* ctx, uint32_t ggml_type, uint64_t
 
 void pk_hip_weight_release(pk_hip_weight* weight);
 uint64_t pk_hip_weight_bytes(const pk_hip_weight* weight);
-/* Device address of the encoded payload (read-only use by the caller). */
+/* Device address of the resident weight (read-only use by the caller).  Q4_0,
+ * Q8_0, Q6_K, Q5_0 and Q3_K are held in a planar layout (each block field in
+ * a plane of its own per slice, expert slices 256-byte aligned), the other
+ * types in their GGUF encoding; pk_hip_weight_download returns the GGUF
+ * bytes of any type. */
 const void* pk_hip_weight_device_ptr(const pk_hip_weight* weight);
+
+/* Copies the weight's GGUF encoding (nbytes = the uploaded size) into
+ * caller-owned host memory: TensorReader::read_all of the resident tensor
+ * (include/pokitlms/model/tensor_reader.hpp:34). */
+pk_hip_status pk_hip_weight_download(const pk_hip_weight* weight, void* host_bytes,
+                                     uint64_t nbytes, char* error_buffer,
+                                     size_t error_capacity);
 
 /* y[b] = W . x[b] for b < batch (1..8): TensorLinearBackend::try_linear
  * (tensor_linear.hpp:16-17; Vulkan: src/vulkan_linear.cpp:612-736), with

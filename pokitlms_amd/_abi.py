@@ -31,6 +31,7 @@ EXPORTS = (
     "pk_hip_moe35_prefill", "pk_hip_moe35_prefill_async",
     "pk_hip_moe_prefill_async", "pk_hip_qwen3moe_create", "pk_hip_qwen3moe_destroy",
     "pk_hip_qwen3moe_generate", "pk_hip_synth_weight", "pk_hip_matvec_reference_order",
+    "pk_hip_weight_download",
 )
 
 
@@ -121,6 +122,8 @@ def lib() -> ctypes.CDLL:
     L.pk_hip_weight_bytes.argtypes = [vp]
     L.pk_hip_weight_device_ptr.restype = vp
     L.pk_hip_weight_device_ptr.argtypes = [vp]
+    L.pk_hip_weight_download.restype = ctypes.c_int
+    L.pk_hip_weight_download.argtypes = [vp, vp, u64, ctypes.c_char_p, ctypes.c_size_t]
     L.pk_hip_matvec.restype = ctypes.c_int
     L.pk_hip_matvec.argtypes = [vp, vp, u32, fp, u32, fp, cp, sz]
     L.pk_hip_matvec_reference_order.restype = ctypes.c_int

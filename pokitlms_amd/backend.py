@@ -77,6 +77,14 @@ class Weight:
     def slice_bytes(self) -> int:
         return self.nbytes // max(self.n_experts, 1)
 
+    def download(self) -> np.ndarray:
+        """The weight's GGUF encoding, read back from HBM (uint8[nbytes])."""
+        out = np.empty(self.nbytes, dtype=np.uint8)
+        err = ctypes.create_string_buffer(_ERRBUF)
+        _raise(_abi.lib().pk_hip_weight_download(self.handle, out.ctypes.data, self.nbytes, err,
+                                                 _ERRBUF), err)
+        return out
+
     def release(self) -> None:
         if self.handle:
             _abi.lib().pk_hip_weight_release(self.handle)

@@ -20,6 +20,7 @@
 
 #include "../../include/pokit_hip.h"
 #include "launch.hpp"
+#include "layout.hpp"
 
 namespace {
 
@@ -117,6 +118,9 @@ struct pk_hip_weight {
     uint64_t in = 0, out = 0;
     uint32_t n_experts = 0;
     uint64_t row_bytes = 0, slice_bytes = 0, nbytes = 0;
+    // Device bytes between consecutive expert slices: slice_bytes, rounded up
+    // to pk::kSlicePitchAlign for the planar types (see layout.hpp).
+    uint64_t slice_pitch = 0;
     uint8_t* dptr = nullptr;
 };
 
@@ -194,14 +198,76 @@ pk_hip_weight* make_weight(pk_hip_ctx* ctx, uint32_t type, uint64_t in, uint64_t
     w->row_bytes = row;
     w->slice_bytes = slice;
     w->nbytes = nbytes;
+    w->slice_pitch = slice;
+    if (pk::planar_type(type) && n_experts > 1)
+        w->slice_pitch = (slice + pk::kSlicePitchAlign - 1) / pk::kSlicePitchAlign * pk::kSlicePitchAlign;
+    const uint64_t device_bytes = w->slice_pitch * experts;
     ctx->set_device();
-    const hipError_t e = hipMalloc(&w->dptr, nbytes + pk::kWeightTailPad);
+    const hipError_t e = hipMalloc(&w->dptr, device_bytes + pk::kWeightTailPad);
     if (e != hipSuccess) {
         delete w;
         throw DeviceError(std::string("hipMalloc weights: ") + hipGetErrorString(e));
     }
-    check(hipMemsetAsync(w->dptr + nbytes, 0, pk::kWeightTailPad, ctx->stream), "pad weights");
+    check(hipMemsetAsync(w->dptr + device_bytes, 0, pk::kWeightTailPad, ctx->stream), "pad weights");
     return w;
+}
+
+uint32_t slices_of(const pk_hip_weight* w) { return w->n_experts ? w->n_experts : 1u; }
+uint64_t slice_blocks(const pk_hip_weight* w) {
+    return w->slice_bytes / block_bytes(w->type);
+}
+
+// Fills w from GGUF-form bytes at src (device memory, slices slice_bytes
+// apart), moving planar types into their planes.  Enqueued on the context
+// stream.
+void fill_from_device(pk_hip_ctx* c, pk_hip_weight* w, const uint8_t* src) {
+    if (!pk::planar_type(w->type)) {
+        check(hipMemcpyAsync(w->dptr, src, w->nbytes, hipMemcpyDeviceToDevice, c->stream),
+              "weight copy");
+        return;
+    }
+    check(pk::launch_to_planar(w->type, src, w->slice_bytes, w->dptr, w->slice_pitch,
+                               slice_blocks(w), slices_of(w), c->stream),
+          "planar weight layout");
+}
+
+// Staging bound for host uploads of planar types (whole slices per chunk).
+constexpr uint64_t kStageBytes = 256ull << 20;
+
+// As fill_from_device from host (or device, `kind`) bytes; synchronises.
+void fill_weight(pk_hip_ctx* c, pk_hip_weight* w, const void* src, hipMemcpyKind kind) {
+    if (!pk::planar_type(w->type)) {
+        check(hipMemcpyAsync(w->dptr, src, w->nbytes, kind, c->stream), "weight upload");
+        check(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+        return;
+    }
+    if (kind == hipMemcpyDeviceToDevice) {
+        fill_from_device(c, w, static_cast<const uint8_t*>(src));
+        check(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+        return;
+    }
+    const uint32_t n = slices_of(w);
+    const uint32_t per = static_cast<uint32_t>(std::max<uint64_t>(1, std::min<uint64_t>(n, kStageBytes / w->slice_bytes)));
+    DeviceBuffer<uint8_t> stage;
+    stage.ensure(static_cast<size_t>(per) * w->slice_bytes);
+    try {
+        for (uint32_t s0 = 0; s0 < n; s0 += per) {
+            const uint32_t k = std::min(per, n - s0);
+            const uint8_t* hs = static_cast<const uint8_t*>(src) + static_cast<uint64_t>(s0) * w->slice_bytes;
+            check(hipMemcpyAsync(stage.ptr, hs, static_cast<uint64_t>(k) * w->slice_bytes, kind, c->stream),
+                  "weight upload");
+            check(pk::launch_to_planar(w->type, stage.ptr, w->slice_bytes,
+                                       w->dptr + static_cast<uint64_t>(s0) * w->slice_pitch,
+                                       w->slice_pitch, slice_blocks(w), k, c->stream),
+                  "planar weight layout");
+            check(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+        }
+    } catch (...) {
+        (void)hipStreamSynchronize(c->stream);
+        stage.release();
+        throw;
+    }
+    stage.release();
 }
 
 // Holds the stream for `ticks` of the constant-rate wall clock so that the
@@ -245,7 +311,7 @@ void enqueue_matvec(pk_hip_ctx* c, const pk_hip_weight* w, uint32_t expert, cons
     if (expert != UINT32_MAX) {
         if (w->n_experts == 0 || expert >= w->n_experts)
             throw ArgError("expert index out of range");
-        offset = static_cast<uint64_t>(expert) * w->slice_bytes;
+        offset = static_cast<uint64_t>(expert) * w->slice_pitch;
     }
     if (!pk::matvec_supported(w->type, static_cast<uint32_t>(w->in), batch))
         throw Unsupported("matrix width/batch not covered by the HIP matvec kernels");
@@ -351,9 +417,9 @@ void enqueue_moe(pk_hip_ctx* c, const pk_hip_moe_layer* L, const MoeShape& m, co
     a.gate_type = L->gate->type;
     a.up_type = L->up->type;
     a.down_type = L->down->type;
-    a.gate_slice = L->gate->slice_bytes;
-    a.up_slice = L->up->slice_bytes;
-    a.down_slice = L->down->slice_bytes;
+    a.gate_slice = L->gate->slice_pitch;
+    a.up_slice = L->up->slice_pitch;
+    a.down_slice = L->down->slice_pitch;
     a.gate_row = L->gate->row_bytes;
     a.up_row = L->up->row_bytes;
     a.down_row = L->down->row_bytes;
@@ -503,12 +569,12 @@ static pk_hip_status upload_impl(pk_hip_ctx* ctx, uint32_t type, uint64_t in, ui
         // caller's generator or loader): uploads are rare, so wait for all
         // earlier work on the device before copying.
         if (kind == hipMemcpyDeviceToDevice) check(hipDeviceSynchronize(), "hipDeviceSynchronize");
-        const hipError_t e = hipMemcpyAsync(w->dptr, src, nbytes, kind, ctx->stream);
-        const hipError_t s = e == hipSuccess ? hipStreamSynchronize(ctx->stream) : e;
-        if (s != hipSuccess) {
+        try {
+            fill_weight(ctx, w, src, kind);
+        } catch (...) {
             (void)hipFree(w->dptr);
             delete w;
-            check(s, "weight upload");
+            throw;
         }
         ctx->stats.resident_bytes += nbytes;
         ctx->stats.uploaded_bytes += nbytes;
@@ -545,6 +611,48 @@ void pk_hip_weight_release(pk_hip_weight* w) {
 }
 
 uint64_t pk_hip_weight_bytes(const pk_hip_weight* w) { return w ? w->nbytes : 0; }
+
+pk_hip_status pk_hip_weight_download(const pk_hip_weight* w, void* host_bytes, uint64_t nbytes,
+                                     char* err, size_t cap) {
+    pk_hip_ctx* ctx = w ? w->ctx : nullptr;
+    return guarded(ctx, err, cap, [&] {
+        if (!w || !host_bytes) throw ArgError("weight and destination are required");
+        if (nbytes != w->nbytes) throw ArgError("destination size does not match the weight");
+        require_usable(ctx);
+        std::lock_guard lock(ctx->mutex);
+        ctx->set_device();
+        if (!pk::planar_type(w->type)) {
+            check(hipMemcpyAsync(host_bytes, w->dptr, nbytes, hipMemcpyDeviceToHost, ctx->stream),
+                  "weight download");
+            check(hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
+            return;
+        }
+        const uint32_t n = slices_of(w);
+        const uint32_t per = static_cast<uint32_t>(
+            std::max<uint64_t>(1, std::min<uint64_t>(n, kStageBytes / w->slice_bytes)));
+        DeviceBuffer<uint8_t> stage;
+        stage.ensure(static_cast<size_t>(per) * w->slice_bytes);
+        try {
+            for (uint32_t s0 = 0; s0 < n; s0 += per) {
+                const uint32_t k = std::min(per, n - s0);
+                check(pk::launch_from_planar(w->type, w->dptr + static_cast<uint64_t>(s0) * w->slice_pitch,
+                                             w->slice_pitch, stage.ptr, w->slice_bytes,
+                                             slice_blocks(w), k, ctx->stream),
+                      "GGUF weight layout");
+                check(hipMemcpyAsync(static_cast<uint8_t*>(host_bytes) + static_cast<uint64_t>(s0) * w->slice_bytes,
+                                     stage.ptr, static_cast<uint64_t>(k) * w->slice_bytes,
+                                     hipMemcpyDeviceToHost, ctx->stream),
+                      "weight download");
+                check(hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
+            }
+        } catch (...) {
+            (void)hipStreamSynchronize(ctx->stream);
+            stage.release();
+            throw;
+        }
+        stage.release();
+    });
+}
 const void* pk_hip_weight_device_ptr(const pk_hip_weight* w) { return w ? w->dptr : nullptr; }
 
 pk_hip_status pk_hip_matvec(pk_hip_ctx* ctx, const pk_hip_weight* w, uint32_t expert,
@@ -589,7 +697,7 @@ pk_hip_status pk_hip_matvec_reference_order(pk_hip_ctx* ctx, const pk_hip_weight
                              ctx->stream),
               "copy input");
         pk::RefMatvecArgs a{};
-        a.W = w->dptr + (w->n_experts ? uint64_t(expert) * w->slice_bytes : 0u);
+        a.W = w->dptr + (w->n_experts ? uint64_t(expert) * w->slice_pitch : 0u);
         a.row_bytes = w->row_bytes;
         a.rows = static_cast<uint32_t>(w->out);
         a.in = static_cast<uint32_t>(w->in);
@@ -759,9 +867,9 @@ void enqueue_prefill(pk_hip_ctx* c, const pk_hip_moe_layer* L, const MoeShape& m
     l.gate_type = L->gate->type;
     l.up_type = L->up->type;
     l.down_type = L->down->type;
-    l.gate_slice = L->gate->slice_bytes;
-    l.up_slice = L->up->slice_bytes;
-    l.down_slice = L->down->slice_bytes;
+    l.gate_slice = L->gate->slice_pitch;
+    l.up_slice = L->up->slice_pitch;
+    l.down_slice = L->down->slice_pitch;
     l.gate_row = L->gate->row_bytes;
     l.up_row = L->up->row_bytes;
     l.down_row = L->down->row_bytes;
@@ -1216,9 +1324,9 @@ pk_hip_status pk_hip_qwen3moe_create(pk_hip_ctx* ctx, const pk_hip_qwen3moe_conf
             g.gate_type = L.gate->type;
             g.up_type = L.up->type;
             g.down_type = L.down->type;
-            g.gate_slice = L.gate->slice_bytes;
-            g.up_slice = L.up->slice_bytes;
-            g.down_slice = L.down->slice_bytes;
+            g.gate_slice = L.gate->slice_pitch;
+            g.up_slice = L.up->slice_pitch;
+            g.down_slice = L.down->slice_pitch;
             g.gate_row = L.gate->row_bytes;
             g.up_row = L.up->row_bytes;
             g.down_row = L.down->row_bytes;
@@ -1341,13 +1449,25 @@ pk_hip_status pk_hip_synth_weight(pk_hip_ctx* ctx, uint32_t type, uint64_t in, u
         const uint64_t nbytes = in / be * bb * out * (n_experts ? n_experts : 1);
         std::lock_guard lock(ctx->mutex);
         pk_hip_weight* w = make_weight(ctx, type, in, out, n_experts, nbytes);
-        const hipError_t e = pk::launch_synth_fill(w->dptr, nbytes, key, kind, bb, ctx->stream);
-        const hipError_t s = e == hipSuccess ? hipStreamSynchronize(ctx->stream) : e;
-        if (s != hipSuccess) {
+        // planar types: generated in GGUF form in a staging buffer, then moved
+        DeviceBuffer<uint8_t> stage;
+        try {
+            uint8_t* dst = w->dptr;
+            if (pk::planar_type(type)) {
+                stage.ensure(nbytes);
+                dst = stage.ptr;
+            }
+            check(pk::launch_synth_fill(dst, nbytes, key, kind, bb, ctx->stream), "synthetic weights");
+            if (pk::planar_type(type)) fill_from_device(ctx, w, dst);
+            check(hipStreamSynchronize(ctx->stream), "synthetic weights");
+        } catch (...) {
+            (void)hipStreamSynchronize(ctx->stream);
+            stage.release();
             (void)hipFree(w->dptr);
             delete w;
-            check(s, "synthetic weights");
+            throw;
         }
+        stage.release();
         ctx->stats.resident_bytes += nbytes;
         ++ctx->live_weights;
         *out_w = w;

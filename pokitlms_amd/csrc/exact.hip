@@ -129,19 +129,19 @@ __device__ __forceinline__ float q6_step4(float s, float dsc, uint32_t v, float4
     return __fadd_rn(s, __fmul_rn(__fmul_rn(dsc, ub<3>(v) - 32.0f), x.w));
 }
 
-// dot of one block with x (x in LDS, 16-byte aligned), in element order.
-// The whole block is loaded into registers first (whole words; the 2-byte
-// aligned formats through v_alignbyte).  K-quants and Q4_1: the decoded FP32
-// weight times x; Q8_0/Q4_0: d * dot_i8_f32 (the int8 value times x, then the
-// scale once).
+// dot of block b of row `row` with x (x in LDS, 16-byte aligned), in element
+// order.  The whole block is loaded into registers first (whole words; the
+// planar formats field by field).  K-quants and Q4_1: the decoded FP32 weight
+// times x; Q8_0/Q4_0: d * dot_i8_f32 (the int8 value times x, then the scale
+// once).
 template <int T>
-__device__ float block_dot(const uint8_t* blk, const float* x) {
+__device__ float block_dot(const QRow& row, uint32_t b, const float* x) {
     const float4* x4 = reinterpret_cast<const float4*>(x);
     float s = 0.0f;
     if constexpr (T == T_Q4_K || T == T_Q5_K) {
         constexpr int NW = T == T_Q4_K ? 36 : 44, QS = T == T_Q4_K ? 4 : 12;
         uint32_t w[NW];
-        ld_words<NW>(blk, w);
+        ld_words<NW>(block_ptr<RefBlock<T>::BB>(row, b), w);
         const uint32_t h[4] = {w[0], w[1], w[2], w[3]};
         const float d = half_bits_to_float(w[0] & 0xffffu), dmin = half_bits_to_float(w[0] >> 16);
 #pragma unroll
@@ -158,42 +158,46 @@ __device__ float block_dot(const uint8_t* blk, const float* x) {
             }
         }
     } else if constexpr (T == T_Q6_K) {
-        uint32_t w[53];  // ql words 0..31, qh 32..47, scales 48..51, d in 52
-        ld_words_2a<53>(blk, w);
-        const float d = half_bits_to_float(w[52] & 0xffffu);
+        using L = Planar<T_Q6_K>;
+        uint32_t ql[32], qh[16], sw[4];
+        ld_words<32>(field_ptr<L::QL, 128>(row, b), ql);
+        ld_words<16>(field_ptr<L::QH, 64>(row, b), qh);
+        ld_words<4>(field_ptr<L::SC, 16>(row, b), sw);
+        const float d = half_bits_to_float(ld_u16(field_ptr<L::D, 2>(row, b)));
 #pragma unroll
         for (uint32_t c = 0; c < 8; ++c) {
             const uint32_t half = c / 4u, g = c % 4u;
 #pragma unroll
             for (uint32_t k = 0; k < 8; ++k) {
                 const uint32_t sb = 8u * half + 2u * g + (k >= 4u ? 1u : 0u);
-                const int sc = static_cast<int8_t>(w[48u + sb / 4u] >> (8u * (sb % 4u)));
+                const int sc = static_cast<int8_t>(sw[sb / 4u] >> (8u * (sb % 4u)));
                 const float dsc = __fmul_rn(d, static_cast<float>(sc));
-                const uint32_t ql = w[16u * half + 8u * (g & 1u) + k];
-                const uint32_t qh = w[32u + 8u * half + k];
-                const uint32_t v = (g >= 2u ? (ql >> 4) & 0x0f0f0f0fu : ql & 0x0f0f0f0fu) |
-                                   (((qh >> (2u * g)) & 0x03030303u) << 4);
+                const uint32_t lw = ql[16u * half + 8u * (g & 1u) + k];
+                const uint32_t hw = qh[8u * half + k];
+                const uint32_t v = (g >= 2u ? (lw >> 4) & 0x0f0f0f0fu : lw & 0x0f0f0f0fu) |
+                                   (((hw >> (2u * g)) & 0x03030303u) << 4);
                 s = q6_step4(s, dsc, v, x4[8u * c + k]);
             }
         }
     } else if constexpr (T == T_Q8_0) {
-        uint32_t w[9];  // d in the low half of word 0, quant i in byte 2 + i
-        ld_words_2a<9>(blk, w);
+        using L = Planar<T_Q8_0>;
+        uint32_t w[8];  // quant i in byte i
+        ld_words<8>(field_ptr<L::QS, 32>(row, b), w);
+        const float d = half_bits_to_float(ld_u16(field_ptr<L::D, 2>(row, b)));
 #pragma unroll
         for (uint32_t k = 0; k < 8; ++k) {
             const float4 xv = x4[k];
             const float xs[4] = {xv.x, xv.y, xv.z, xv.w};
 #pragma unroll
             for (uint32_t m = 0; m < 4; ++m) {
-                const uint32_t byte = 2u + 4u * k + m;
-                const int q = static_cast<int8_t>(w[byte / 4u] >> (8u * (byte % 4u)));
+                const int q = static_cast<int8_t>(w[k] >> (8u * m));
                 s = __fadd_rn(s, __fmul_rn(xs[m], static_cast<float>(q)));
             }
         }
-        s = __fmul_rn(half_bits_to_float(w[0] & 0xffffu), s);
+        s = __fmul_rn(d, s);
     } else if constexpr (T == T_Q4_1) {  // weight fl(fl(q * d) + m), low nibbles first
         uint32_t w[5];                   // d | m << 16, then quants 0..15
-        ld_words<5>(blk, w);
+        ld_words<5>(block_ptr<20>(row, b), w);
         const float d = half_bits_to_float(w[0] & 0xffffu), m = half_bits_to_float(w[0] >> 16);
 #pragma unroll
         for (uint32_t k = 0; k < 8; ++k) {
@@ -206,21 +210,23 @@ __device__ float block_dot(const uint8_t* blk, const float* x) {
             s = __fadd_rn(s, __fmul_rn(__fadd_rn(__fmul_rn(ub<3>(v), d), m), xv.w));
         }
     } else {  // Q4_0: low nibbles are elements 0..15, high 16..31
-        uint32_t w[5];
-        ld_words_2a<5>(blk, w);
+        using L = Planar<T_Q4_0>;
+        uint32_t w[4];  // quant byte i in byte i
+        ld_words<4>(field_ptr<L::QS, 16>(row, b), w);
+        const float d = half_bits_to_float(ld_u16(field_ptr<L::D, 2>(row, b)));
 #pragma unroll
         for (uint32_t k = 0; k < 8; ++k) {
             const float4 xv = x4[k];
             const float xs[4] = {xv.x, xv.y, xv.z, xv.w};
 #pragma unroll
             for (uint32_t m = 0; m < 4; ++m) {
-                const uint32_t i = 4u * k + m, byte = 2u + (i & 15u);
-                const uint32_t b = (w[byte / 4u] >> (8u * (byte % 4u))) & 0xffu;
-                const int q = static_cast<int>(i < 16u ? (b & 15u) : (b >> 4)) - 8;
+                const uint32_t i = 4u * k + m, byte = i & 15u;
+                const uint32_t v = (w[byte / 4u] >> (8u * (byte % 4u))) & 0xffu;
+                const int q = static_cast<int>(i < 16u ? (v & 15u) : (v >> 4)) - 8;
                 s = __fadd_rn(s, __fmul_rn(xs[m], static_cast<float>(q)));
             }
         }
-        s = __fmul_rn(half_bits_to_float(w[0] & 0xffffu), s);
+        s = __fmul_rn(d, s);
     }
     return s;
 }
@@ -450,7 +456,8 @@ __global__ __launch_bounds__(256) void k_ref_matvec(RefMatvecArgs a) {
     W += expert * slice_bytes;
     const uint32_t row0 = bx * rpw, lr = tid / nb, b = tid % nb, row = row0 + lr;
     if (lr < rpw && row < rows)
-        part[tid] = block_dot<T>(W + static_cast<uint64_t>(row) * row_bytes + b * BB, xs + b * BE);
+        part[tid] = block_dot<T>(QRow{W, static_cast<uint64_t>(rows) * nb, static_cast<uint64_t>(row) * nb},
+                                 b, xs + b * BE);
     __syncthreads();
     if (tid < rpw && row0 + tid < rows) {
         float acc = 0.0f;

@@ -15,6 +15,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "layout.hpp"
+
 namespace pk {
 
 enum : uint32_t {
@@ -132,7 +134,7 @@ __device__ __forceinline__ void kq_scale_min(const uint32_t (&h)[4], uint32_t j,
 // of the first element of run r.  All of it is row-independent.
 
 struct UnitPos {
-    uint32_t boff;    // byte offset of the block inside the row
+    uint32_t b;       // block index inside the row
     uint32_t k0;      // primary-stream byte offset inside the block
     uint32_t col[2];  // activation column of run 0 / run 1
 };
@@ -143,7 +145,7 @@ __device__ __forceinline__ UnitPos unit_pos(uint32_t u) {
     constexpr uint32_t UPB = F::PRIM / UB;
     const uint32_t b = u / UPB, j = u % UPB, k0 = j * UB;
     UnitPos p;
-    p.boff = b * F::BB;
+    p.b = b;
     p.k0 = k0;
     const uint32_t base = b * F::BE;
     if constexpr (T == T_Q4_K || T == T_Q5_K) {
@@ -203,55 +205,45 @@ __device__ __forceinline__ void load_unit_x(const float* x, uint32_t x_stride, c
 template <int T, int UB>
 struct UnitRaw {
     static constexpr int NW = UB / 4;
-    // Q4_K/Q5_K: h = 16-byte block header; q = quants; qh = Q5_K fifth bits.
-    // Q6_K/Q8_0/Q4_0: q/qh hold NW+1 dword-aligned words re-aligned at use.
+    // Q4_K/Q5_K/Q4_1: h = block header; q = quants; qh = Q5_K fifth bits.
+    // Q6_K/Q8_0/Q4_0 (planar): q = quants, qh = Q6_K high bits, sc = the two
+    // Q6_K scale dwords of the unit's half block, d = fp16 bits of d.
     uint32_t h[(T == T_Q4_K || T == T_Q5_K) ? 4 : 1];
-    uint32_t q[NW + 1];
-    uint32_t qh[(T == T_Q5_K || T == T_Q6_K) ? NW + 1 : 1];
-    uint32_t shift;  // byte misalignment (0 or 2) of the 2-byte-aligned formats
-    int32_t s0, s1;  // Q6_K int8 sub-block scales
-    uint32_t d;      // fp16 bits of d (Q6_K, Q8_0, Q4_0)
+    uint32_t q[NW];
+    uint32_t qh[(T == T_Q5_K || T == T_Q6_K) ? NW : 1];
+    uint32_t sc[T == T_Q6_K ? 2 : 1];
+    uint32_t d;
 };
 
+// Loads of one unit of row `r`: quants with one (UB = 16) aligned load per
+// field, scales as whole dwords.
 template <int T, int UB>
-__device__ __forceinline__ void unit_load(const uint8_t* __restrict__ row, const UnitPos& p,
-                                          UnitRaw<T, UB>& r) {
+__device__ __forceinline__ void unit_load(const QRow& r, const UnitPos& p, UnitRaw<T, UB>& u) {
     constexpr int NW = UB / 4;
-    const uint8_t* blk = row + p.boff;
     if constexpr (T == T_Q4_1) {  // 20-byte blocks keep 4-byte alignment: d, m, then quants
-        ld_weights<1>(blk, r.h);
-        uint32_t q[NW];
-        ld_weights<NW>(blk + 4 + p.k0, q);
-#pragma unroll
-        for (int i = 0; i < NW; ++i) r.q[i] = q[i];
+        const uint8_t* blk = block_ptr<20>(r, p.b);
+        ld_weights<1>(blk, u.h);
+        ld_weights<NW>(blk + 4 + p.k0, u.q);
     } else if constexpr (T == T_Q4_K || T == T_Q5_K) {
-        ld_weights<4>(blk, r.h);
-        uint32_t q[NW];
-        ld_weights<NW>(blk + (T == T_Q4_K ? 16 : 48) + p.k0, q);
-#pragma unroll
-        for (int i = 0; i < NW; ++i) r.q[i] = q[i];
-        if constexpr (T == T_Q5_K) {
-            uint32_t qh[NW];
-            ld_weights<NW>(blk + 16 + (p.k0 % 32u), qh);
-#pragma unroll
-            for (int i = 0; i < NW; ++i) r.qh[i] = qh[i];
-        }
-    } else {
-        const uint8_t* qp = T == T_Q6_K ? blk + p.k0 : blk + 2 + p.k0;
-        r.shift = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(qp) & 3u);
-        ld_weights<NW + 1>(qp - r.shift, r.q);  // pointer arithmetic keeps global loads
-        if constexpr (T == T_Q6_K) {
-            const uint32_t kk = p.k0 % 64u;
-            const uint8_t* hp = blk + 128u + 32u * (p.k0 / 64u) + (kk % 32u);
-            // qh and ql share the block's alignment (both offsets are even)
-            ld_weights<NW + 1>(hp - r.shift, r.qh);
-            const uint32_t sidx = (p.col[0] % 256u) / 16u;
-            r.s0 = static_cast<int8_t>(blk[192u + sidx]);
-            r.s1 = static_cast<int8_t>(blk[192u + sidx + 4u]);
-            r.d = ld_u16(blk + 208);
-        } else {
-            r.d = ld_u16(blk);
-        }
+        const uint8_t* blk = block_ptr<Fmt<T>::BB>(r, p.b);
+        ld_weights<4>(blk, u.h);
+        ld_weights<NW>(blk + (T == T_Q4_K ? 16 : 48) + p.k0, u.q);
+        if constexpr (T == T_Q5_K) ld_weights<NW>(blk + 16 + (p.k0 % 32u), u.qh);
+    } else if constexpr (T == T_Q6_K) {
+        using L = Planar<T_Q6_K>;
+        const uint32_t half = p.k0 / 64u, kk = p.k0 % 64u;
+        ld_weights<NW>(field_ptr<L::QL, 128>(r, p.b) + p.k0, u.q);
+        ld_weights<NW>(field_ptr<L::QH, 64>(r, p.b) + 32u * half + (kk % 32u), u.qh);
+        ld_weights<2>(field_ptr<L::SC, 16>(r, p.b) + 8u * half, u.sc);
+        u.d = ld_u16(field_ptr<L::D, 2>(r, p.b));
+    } else if constexpr (T == T_Q8_0) {
+        using L = Planar<T_Q8_0>;
+        ld_weights<NW>(field_ptr<L::QS, 32>(r, p.b) + p.k0, u.q);
+        u.d = ld_u16(field_ptr<L::D, 2>(r, p.b));
+    } else {  // Q4_0
+        using L = Planar<T_Q4_0>;
+        ld_weights<NW>(field_ptr<L::QS, 16>(r, p.b) + p.k0, u.q);
+        u.d = ld_u16(field_ptr<L::D, 2>(r, p.b));
     }
 }
 
@@ -295,8 +287,7 @@ __device__ __forceinline__ void unit_compute(const UnitRaw<T, UB>& r, const Unit
         const uint32_t sl = (p.k0 % 64u) >= 32u ? 2u : 0u;
 #pragma unroll
         for (int t = 0; t < NW; ++t) {
-            const uint32_t ql = __builtin_amdgcn_alignbyte(r.q[t + 1], r.q[t], r.shift);
-            const uint32_t qh = __builtin_amdgcn_alignbyte(r.qh[t + 1], r.qh[t], r.shift);
+            const uint32_t ql = r.q[t], qh = r.qh[t];
             const uint32_t lo = (ql & 0x0f0f0f0fu) | ((qh << (4u - sl)) & 0x30303030u);
             const uint32_t hi = ((ql >> 4) & 0x0f0f0f0fu) | ((qh >> sl) & 0x30303030u);
 #pragma unroll
@@ -305,8 +296,13 @@ __device__ __forceinline__ void unit_compute(const UnitRaw<T, UB>& r, const Unit
                 dot1[b] = dot4(hi, &ux.v[b][UB + 4 * t], dot1[b]);
             }
         }
+        // the unit's scales: sc[s] and sc[s + 4] of the block, s = its 16-group
+        // (s % 4 is the same byte of the half's two scale dwords)
+        const uint32_t sb = 8u * (((p.k0 % 64u) >= 32u ? 2u : 0u) + ((p.k0 % 32u) / 16u));
         const float d = half_bits_to_float(r.d);
-        const float ds0 = d * static_cast<float>(r.s0), ds1 = d * static_cast<float>(r.s1);
+        const float s0 = static_cast<float>(static_cast<int8_t>((r.sc[0] >> sb) & 0xffu));
+        const float s1 = static_cast<float>(static_cast<int8_t>((r.sc[1] >> sb) & 0xffu));
+        const float ds0 = d * s0, ds1 = d * s1;
 #pragma unroll
         for (int b = 0; b < B; ++b) {
             const float t0 = __builtin_fmaf(-32.0f, ux.s[b][0], dot0[b]);
@@ -316,8 +312,7 @@ __device__ __forceinline__ void unit_compute(const UnitRaw<T, UB>& r, const Unit
     } else if constexpr (T == T_Q8_0) {
 #pragma unroll
         for (int t = 0; t < NW; ++t) {
-            const uint32_t q = __builtin_amdgcn_alignbyte(r.q[t + 1], r.q[t], r.shift);
-            const uint32_t biased = q ^ 0x80808080u;  // int8 q -> q + 128
+            const uint32_t biased = r.q[t] ^ 0x80808080u;  // int8 q -> q + 128
 #pragma unroll
             for (int b = 0; b < B; ++b) dot0[b] = dot4(biased, &ux.v[b][4 * t], dot0[b]);
         }
@@ -343,7 +338,7 @@ __device__ __forceinline__ void unit_compute(const UnitRaw<T, UB>& r, const Unit
     } else {  // Q4_0
 #pragma unroll
         for (int t = 0; t < NW; ++t) {
-            const uint32_t q = __builtin_amdgcn_alignbyte(r.q[t + 1], r.q[t], r.shift);
+            const uint32_t q = r.q[t];
             const uint32_t lo = q & 0x0f0f0f0fu;
             const uint32_t hi = (q >> 4) & 0x0f0f0f0fu;
 #pragma unroll
@@ -360,14 +355,6 @@ __device__ __forceinline__ void unit_compute(const UnitRaw<T, UB>& r, const Unit
             acc[b] += d * (t0 + t1);
         }
     }
-}
-
-template <int T, int UB, int B>
-__device__ __forceinline__ void unit_fma(const uint8_t* __restrict__ row, const UnitPos& p,
-                                         const UnitX<T, UB, B>& ux, float (&acc)[B]) {
-    UnitRaw<T, UB> r;
-    unit_load<T, UB>(row, p, r);
-    unit_compute<T, UB, B>(r, p, ux, acc);
 }
 
 // ---------------------------------------------------------------------------

@@ -26,8 +26,23 @@ template <int B> constexpr int passes_for() { return B > 4 ? 1 : 2; }
 template <int B> constexpr int max_threads_for() { return B > 4 ? 768 : 512; }
 
 template <int T, int B, int UB, int NU>
+struct MvState {
+    static constexpr int kPasses = passes_for<B>();
+    UnitPos pos[NU];
+    bool valid[NU];
+    UnitX<T, UB, B> ux[NU];
+    UnitRaw<T, UB> raw[kPasses][NU];
+    uint32_t row[kPasses];
+    bool live[kPasses];
+};
+
+// Each wave issues its first passes' weight loads, then reads its units'
+// activations (kept in registers for every later row), then dots.  x is read
+// from global memory (L2) by every wave: a workgroup barrier to share it
+// through LDS would wait for the weight loads as well.
+template <int T, int B, int UB, int NU>
 __global__ __launch_bounds__(max_threads_for<B>()) void k_matvec_q(
-    const uint8_t* __restrict__ W, uint64_t row_bytes, const float* __restrict__ x,
+    const uint8_t* __restrict__ W, uint32_t nb, const float* __restrict__ x,
     uint32_t x_stride, float* __restrict__ y, uint32_t y_stride, uint32_t rows, uint32_t units,
     uint32_t slice_units, uint32_t S, uint32_t glog2) {
     extern __shared__ float partial[];  // [waves][kPasses][RPP][B] when S > 1
@@ -38,60 +53,47 @@ __global__ __launch_bounds__(max_threads_for<B>()) void k_matvec_q(
     const uint32_t group = wave / S, slice = wave % S;
     const uint32_t G = 1u << glog2, RPP = 64u >> glog2;
     const uint32_t sub = lane >> glog2, ul = lane & (G - 1u);
+    const uint64_t nblk = static_cast<uint64_t>(rows) * nb;
+    const uint32_t passes = (rows + RPP - 1u) / RPP;
+    const uint32_t stride = gridDim.x * groups * kPasses;
+    uint32_t p0 = blockIdx.x * groups * kPasses;
+    if (p0 >= passes) return;  // uniform per workgroup
 
-    UnitPos pos[NU];
-    bool valid[NU];
+    MvState<T, B, UB, NU> st;
 #pragma unroll
     for (int k = 0; k < NU; ++k) {
         const uint32_t local = ul + G * k;
         const uint32_t u = slice * slice_units + local;
-        valid[k] = local < slice_units && u < units;
-        pos[k] = unit_pos<T, UB>(valid[k] ? u : 0u);
+        st.valid[k] = local < slice_units && u < units;
+        st.pos[k] = unit_pos<T, UB>(st.valid[k] ? u : 0u);
     }
-    UnitX<T, UB, B> ux[NU];
-    bool have_x = false;
-
-    const uint32_t passes = (rows + RPP - 1u) / RPP;
-    const uint32_t stride = gridDim.x * groups * kPasses;
-    for (uint32_t p0 = blockIdx.x * groups * kPasses; p0 < passes; p0 += stride) {
-        // passes p0 + group*kPasses + q, q < kPasses: loads first
-        UnitRaw<T, UB> raw[kPasses][NU];
-        uint32_t row[kPasses];
-        bool live[kPasses];
+    auto issue = [&](uint32_t pp) {  // weight loads of passes pp + group*kPasses + q
 #pragma unroll
         for (int q = 0; q < kPasses; ++q) {
-            const uint32_t p = p0 + group * kPasses + q;
-            row[q] = p * RPP + sub;
-            live[q] = p < passes && row[q] < rows;
-            if (live[q]) {
-                const uint8_t* rp = W + static_cast<uint64_t>(row[q]) * row_bytes;
+            const uint32_t p = pp + group * kPasses + q;
+            st.row[q] = p * RPP + sub;
+            st.live[q] = p < passes && st.row[q] < rows;
+            const QRow qr{W, nblk, static_cast<uint64_t>(st.live[q] ? st.row[q] : 0u) * nb};
 #pragma unroll
-                for (int k = 0; k < NU; ++k)
-                    if (valid[k]) unit_load<T, UB>(rp, pos[k], raw[q][k]);
-            }
+            for (int k = 0; k < NU; ++k) unit_load<T, UB>(qr, st.pos[k], st.raw[q][k]);
         }
-        if (!have_x) {  // activations arrive while the first weights are in flight
-#pragma unroll
-            for (int k = 0; k < NU; ++k) load_unit_x<T, UB, B>(x, x_stride, pos[k], valid[k], ux[k]);
-            have_x = true;
-        }
+    };
+    auto finish = [&](uint32_t pp) {  // dots, reductions and stores of the issued passes
 #pragma unroll
         for (int q = 0; q < kPasses; ++q) {
             float acc[B];
 #pragma unroll
             for (int b = 0; b < B; ++b) acc[b] = 0.0f;
-            if (live[q]) {
 #pragma unroll
-                for (int k = 0; k < NU; ++k)
-                    if (valid[k]) unit_compute<T, UB, B>(raw[q][k], pos[k], ux[k], acc);
-            }
+            for (int k = 0; k < NU; ++k)
+                if (st.valid[k]) unit_compute<T, UB, B>(st.raw[q][k], st.pos[k], st.ux[k], acc);
 #pragma unroll
             for (int b = 0; b < B; ++b) acc[b] = group_sum_dyn(acc[b], G);
             if (ul == G - 1u) {
                 if (S == 1) {
-                    if (live[q]) {
+                    if (st.live[q]) {
 #pragma unroll
-                        for (int b = 0; b < B; ++b) y[b * y_stride + row[q]] = acc[b];
+                        for (int b = 0; b < B; ++b) y[b * y_stride + st.row[q]] = acc[b];
                     }
                 } else {
 #pragma unroll
@@ -106,7 +108,7 @@ __global__ __launch_bounds__(max_threads_for<B>()) void k_matvec_q(
             if (slice == 0) {
                 for (uint32_t t = lane; t < kPasses * RPP * B; t += 64u) {
                     const uint32_t q = t / (RPP * B), rs = (t / B) % RPP, b = t % B;
-                    const uint32_t p = p0 + group * kPasses + q;
+                    const uint32_t p = pp + group * kPasses + q;
                     const uint32_t s_row = p * RPP + rs;
                     if (p < passes && s_row < rows) {
                         float v = 0.0f;
@@ -118,6 +120,15 @@ __global__ __launch_bounds__(max_threads_for<B>()) void k_matvec_q(
             }
             __syncthreads();
         }
+    };
+
+    issue(p0);  // the first passes' weight loads, then the activations
+#pragma unroll
+    for (int k = 0; k < NU; ++k) load_unit_x<T, UB, B>(x, x_stride, st.pos[k], st.valid[k], st.ux[k]);
+    finish(p0);
+    for (p0 += stride; p0 < passes; p0 += stride) {
+        issue(p0);
+        finish(p0);
     }
 }
 
@@ -204,33 +215,32 @@ bool plan_for(uint32_t in, uint32_t batch, int ub, Plan& p) {
 }
 
 template <int T, int B, int UB, int NU>
-hipError_t run_q(const Plan& pl, const uint8_t* W, uint64_t row_bytes, uint32_t rows,
+hipError_t run_q(const Plan& pl, const uint8_t* W, uint32_t nb, uint32_t rows,
                  const float* x, uint32_t in, float* y, hipStream_t stream) {
     const uint32_t RPP = 64u >> pl.glog2;
     constexpr int kPasses = passes_for<B>();
     const uint32_t groups = pl.waves_per_block / pl.S;
     const uint32_t passes = ceil_div(rows, RPP);
     uint32_t blocks = ceil_div(passes, groups * kPasses);
-    // ~8 waves per CU: enough loads in flight, and each wave reuses its
-    // register-resident activations over several rows.
-    const uint32_t max_blocks = 256u * 8u / pl.waves_per_block;
+    // up to 16 waves per CU: loads of four waves per SIMD in flight
+    const uint32_t max_blocks = 256u * 16u / pl.waves_per_block;
     if (blocks > max_blocks) blocks = max_blocks;
     const size_t lds =
         pl.S > 1 ? static_cast<size_t>(pl.waves_per_block) * kPasses * RPP * B * sizeof(float) : 0;
     hipLaunchKernelGGL((k_matvec_q<T, B, UB, NU>), dim3(blocks), dim3(64u * pl.waves_per_block),
-                       lds, stream, W, row_bytes, x, in, y, rows, rows, pl.units, pl.slice_units,
-                       pl.S, pl.glog2);
+                       lds, stream, W, nb, x, in, y, rows, rows, pl.units, pl.slice_units, pl.S,
+                       pl.glog2);
     return hipGetLastError();
 }
 
 template <int T, int B, int UB>
-hipError_t dispatch_nu(const Plan& pl, const uint8_t* W, uint64_t rb, uint32_t rows,
+hipError_t dispatch_nu(const Plan& pl, const uint8_t* W, uint32_t nb, uint32_t rows,
                        const float* x, uint32_t in, float* y, hipStream_t s) {
     if constexpr (Fmt<T>::RUNS * UB * B > 32) {
-        return run_q<T, B, UB, 1>(pl, W, rb, rows, x, in, y, s);  // plan_for caps nu at 1
+        return run_q<T, B, UB, 1>(pl, W, nb, rows, x, in, y, s);  // plan_for caps nu at 1
     } else {
-        if (pl.nu == 1) return run_q<T, B, UB, 1>(pl, W, rb, rows, x, in, y, s);
-        return run_q<T, B, UB, 2>(pl, W, rb, rows, x, in, y, s);
+        if (pl.nu == 1) return run_q<T, B, UB, 1>(pl, W, nb, rows, x, in, y, s);
+        return run_q<T, B, UB, 2>(pl, W, nb, rows, x, in, y, s);
     }
 }
 
@@ -240,7 +250,8 @@ hipError_t dispatch_q(const uint8_t* W, uint64_t rb, uint32_t rows, const float*
     constexpr int UB = unit_bytes_for(B, Fmt<T>::MAXUB);
     Plan pl;
     if (!plan_for<T>(in, B, UB, pl)) return hipErrorInvalidValue;
-    return dispatch_nu<T, B, UB>(pl, W, rb, rows, x, in, y, s);
+    (void)rb;
+    return dispatch_nu<T, B, UB>(pl, W, in / Fmt<T>::BE, rows, x, in, y, s);
 }
 
 template <int T>

@@ -97,15 +97,16 @@ __device__ __forceinline__ float block_sum(float v, float* red) {
 // linear decoders' arithmetic: :166-205, 286-358, 387-423).
 
 template <int T>
-__device__ void decode32(const uint8_t* row, uint32_t k0, float* v) {
-    if constexpr (T == T_F32) {
-        for (uint32_t i = 0; i < 32; ++i) v[i] = reinterpret_cast<const float*>(row)[k0 + i];
+__device__ void decode32(const QRow& row, uint32_t k0, float* v) {
+    if constexpr (T == T_F32) {  // blocks of one element
+        const float* f = reinterpret_cast<const float*>(block_ptr<4>(row, k0));
+        for (uint32_t i = 0; i < 32; ++i) v[i] = f[i];
     } else if constexpr (T == T_F16 || T == T_BF16) {  // read_float_rows_into (src/tensor_reader.cpp:164-198)
-        const uint16_t* h = reinterpret_cast<const uint16_t*>(row) + k0;
+        const uint16_t* h = reinterpret_cast<const uint16_t*>(block_ptr<2>(row, k0));
         for (uint32_t i = 0; i < 32; ++i)
             v[i] = T == T_F16 ? half_bits_to_float(h[i]) : __uint_as_float(static_cast<uint32_t>(h[i]) << 16);
     } else if constexpr (T == T_Q4_1) {  // decode_q4_1: fl(fl(q * d) + m) (src/quantized_linear.cpp:53-62)
-        const uint8_t* blk = row + (k0 / 32u) * 20u;
+        const uint8_t* blk = block_ptr<20>(row, k0 / 32u);
         const float d = half_bits_to_float(blk[0] | (blk[1] << 8));
         const float m = half_bits_to_float(blk[2] | (blk[3] << 8));
         for (uint32_t i = 0; i < 16; ++i) {
@@ -113,7 +114,7 @@ __device__ void decode32(const uint8_t* row, uint32_t k0, float* v) {
             v[i + 16] = __fadd_rn(__fmul_rn(static_cast<float>(blk[4 + i] >> 4), d), m);
         }
     } else if constexpr (T == T_Q4_K || T == T_Q5_K) {
-        const uint8_t* blk = row + (k0 / 256u) * Fmt<T>::BB;
+        const uint8_t* blk = block_ptr<Fmt<T>::BB>(row, k0 / 256u);
         const uint32_t j = (k0 % 256u) / 32u, chunk = j / 2u, hi = j & 1u;
         uint32_t h[4];
         for (int i = 0; i < 4; ++i)
@@ -128,29 +129,32 @@ __device__ void decode32(const uint8_t* row, uint32_t k0, float* v) {
             if constexpr (T == T_Q5_K) q += ((blk[16u + i] >> j) & 1u) << 4;
             v[i] = __fsub_rn(__fmul_rn(ds, static_cast<float>(q)), dm);
         }
-    } else if constexpr (T == T_Q6_K) {
-        const uint8_t* blk = row + (k0 / 256u) * 210u;
-        const uint32_t c = (k0 % 256u) / 32u, half = c / 4u, g = c % 4u;
-        const float d = half_bits_to_float(blk[208] | (blk[209] << 8));
-        const uint8_t* ql = blk + 64u * half + 32u * (g & 1u);
-        const uint8_t* qh = blk + 128u + 32u * half;
+    } else if constexpr (T == T_Q6_K) {  // planar fields (layout.hpp)
+        using L = Planar<T_Q6_K>;
+        const uint32_t b = k0 / 256u, c = (k0 % 256u) / 32u, half = c / 4u, g = c % 4u;
+        const float d = half_bits_to_float(ld_u16(field_ptr<L::D, 2>(row, b)));
+        const uint8_t* ql = field_ptr<L::QL, 128>(row, b) + 64u * half + 32u * (g & 1u);
+        const uint8_t* qh = field_ptr<L::QH, 64>(row, b) + 32u * half;
+        const uint8_t* sc = field_ptr<L::SC, 16>(row, b) + 8u * half + 2u * g;
         for (uint32_t i = 0; i < 32; ++i) {
-            const int s = static_cast<int8_t>(blk[192u + 8u * half + 2u * g + (i >= 16u ? 1u : 0u)]);
+            const int s = static_cast<int8_t>(sc[i >= 16u ? 1u : 0u]);
             const uint32_t nib = g >= 2u ? ql[i] >> 4 : ql[i] & 15u;
             const int q = static_cast<int>(nib | (((qh[i] >> (2u * g)) & 3u) << 4)) - 32;
             v[i] = __fmul_rn(__fmul_rn(d, static_cast<float>(s)), static_cast<float>(q));
         }
     } else if constexpr (T == T_Q8_0) {
-        const uint8_t* blk = row + (k0 / 32u) * 34u;
-        const float d = half_bits_to_float(blk[0] | (blk[1] << 8));
+        using L = Planar<T_Q8_0>;
+        const uint8_t* qs = field_ptr<L::QS, 32>(row, k0 / 32u);
+        const float d = half_bits_to_float(ld_u16(field_ptr<L::D, 2>(row, k0 / 32u)));
         for (uint32_t i = 0; i < 32; ++i)
-            v[i] = __fmul_rn(d, static_cast<float>(static_cast<int8_t>(blk[2 + i])));
+            v[i] = __fmul_rn(d, static_cast<float>(static_cast<int8_t>(qs[i])));
     } else {  // Q4_0
-        const uint8_t* blk = row + (k0 / 32u) * 18u;
-        const float d = half_bits_to_float(blk[0] | (blk[1] << 8));
+        using L = Planar<T_Q4_0>;
+        const uint8_t* qs = field_ptr<L::QS, 16>(row, k0 / 32u);
+        const float d = half_bits_to_float(ld_u16(field_ptr<L::D, 2>(row, k0 / 32u)));
         for (uint32_t i = 0; i < 16; ++i) {
-            v[i] = __fmul_rn(d, static_cast<float>(static_cast<int>(blk[2 + i] & 15u) - 8));
-            v[i + 16] = __fmul_rn(d, static_cast<float>(static_cast<int>(blk[2 + i] >> 4) - 8));
+            v[i] = __fmul_rn(d, static_cast<float>(static_cast<int>(qs[i] & 15u) - 8));
+            v[i + 16] = __fmul_rn(d, static_cast<float>(static_cast<int>(qs[i] >> 4) - 8));
         }
     }
 }
@@ -161,7 +165,10 @@ __global__ __launch_bounds__(256) void k_embed(ModelArgs a) {
     const uint32_t pos = a.state[0];
     const uint32_t token = a.tokens[pos];
     const uint32_t tid = threadIdx.x;
-    const uint8_t* row = a.embd + static_cast<uint64_t>(token) * a.embd_row;
+    // blocks per row (one element per block for the float types)
+    uint32_t nb = a.hidden;
+    if constexpr (!(T == T_F32 || T == T_F16 || T == T_BF16)) nb = a.hidden / Fmt<T>::BE;
+    const QRow row{a.embd, static_cast<uint64_t>(a.vocab) * nb, static_cast<uint64_t>(token) * nb};
     for (uint32_t c = tid; c < a.hidden / 32u; c += blockDim.x) {
         float v[32];
         decode32<T>(row, 32u * c, v);

@@ -96,16 +96,16 @@ __global__ __launch_bounds__(256) void k_gate_up(MoeDecodeArgs a, uint32_t units
     const uint32_t items = (a.top_k + a.variant) * a.ffn;  // variant 1: the shared expert last
     const uint32_t passes = (items + RPP - 1u) / RPP;
     const uint32_t first = (blockIdx.x * (blockDim.x >> 6) + wave) * NP;
+    const uint32_t nb = a.hidden / Fmt<T>::BE;  // blocks per gate/up row
+    const uint64_t nblk = static_cast<uint64_t>(a.ffn) * nb;  // blocks per expert slice
     uint32_t item[NP], route_of[NP];
-    uint64_t goff[NP], uoff[NP];
+    uint64_t blk0[NP];
 #pragma unroll
     for (int q = 0; q < NP; ++q) {
         item[q] = (first + q) * RPP + sub;
         const uint32_t it = item[q] < items ? item[q] : items - 1u;
         route_of[q] = it / a.ffn;
-        const uint32_t row = it % a.ffn;
-        goff[q] = static_cast<uint64_t>(row) * a.gate_row;
-        uoff[q] = static_cast<uint64_t>(row) * a.up_row;
+        blk0[q] = static_cast<uint64_t>(it % a.ffn) * nb;
     }
     store_x_regs(xs, xr, a.hidden);
     WaveRoutes<NS> w;
@@ -156,8 +156,8 @@ __global__ __launch_bounds__(256) void k_gate_up(MoeDecodeArgs a, uint32_t units
         for (uint32_t r = 0; r < kMaxTopK; ++r)
             if (route_of[q] == r) e = sel[r];
         const bool shared = route_of[q] >= a.top_k;
-        const uint8_t* gr = (shared ? a.shared_gate : a.gate + static_cast<uint64_t>(e) * a.gate_slice) + goff[q];
-        const uint8_t* ur = (shared ? a.shared_up : a.up + static_cast<uint64_t>(e) * a.up_slice) + uoff[q];
+        const QRow gr{shared ? a.shared_gate : a.gate + static_cast<uint64_t>(e) * a.gate_slice, nblk, blk0[q]};
+        const QRow ur{shared ? a.shared_up : a.up + static_cast<uint64_t>(e) * a.up_slice, nblk, blk0[q]};
 #pragma unroll
         for (int k = 0; k < NU; ++k) {
             unit_load<T, UB>(gr, pos[k], rg[q][k]);
@@ -216,15 +216,17 @@ __global__ __launch_bounds__(64 * (kMaxTopK + (SHARED ? 1 : 0))) void k_down(Moe
     }
     const uint8_t* base = shared ? a.shared_down : a.down + e * a.down_slice;
     const uint32_t rows = a.hidden;
+    const uint32_t nb = a.ffn / Fmt<T>::BE;  // blocks per down row
     const uint32_t row0 = blockIdx.x * kDownPasses * RPP;
     // unconditional loads (rows past the end re-read the last row, unused)
     UnitRaw<T, UB> raw[kDownPasses][NU];
 #pragma unroll
     for (int p = 0; p < kDownPasses; ++p) {
         const uint32_t row = row0 + p * RPP + sub;
-        const uint8_t* rp = base + static_cast<uint64_t>(row < rows ? row : rows - 1u) * a.down_row;
+        const QRow qr{base, static_cast<uint64_t>(rows) * nb,
+                      static_cast<uint64_t>(row < rows ? row : rows - 1u) * nb};
 #pragma unroll
-        for (int q = 0; q < NU; ++q) unit_load<T, UB>(rp, pos[q], raw[p][q]);
+        for (int q = 0; q < NU; ++q) unit_load<T, UB>(qr, pos[q], raw[p][q]);
     }
     UnitX<T, UB, 1> ux[NU];
     const float* act = a.act + k * a.ffn;

@@ -51,67 +51,44 @@ template <int T>
 struct Raw32;
 template <> struct Raw32<T_Q4_K> { uint32_t h[4]; uint32_t q[8]; };
 template <> struct Raw32<T_Q5_K> { uint32_t h[4]; uint32_t q[8]; uint32_t qh[8]; };
-// Q6_K, Q8_0 and Q4_0 blocks keep only 2-byte alignment: their fields are
-// loaded as the dwords that cover them (one extra) and realigned by `shift`
-// bytes when decoded, so no load result is needed before its use.
-// (Each field keeps a power-of-two word array plus one trailing word: such
-// arrays stay in registers.)
-template <> struct Raw32<T_Q6_K> { uint32_t ql[8], qh[8]; uint32_t ql8, qh8, sc, d, shift; };
-template <> struct Raw32<T_Q8_0> { uint32_t q[8]; uint32_t q8, d, shift; };
-template <> struct Raw32<T_Q4_0> { uint32_t q[4]; uint32_t q4, d, shift; };
+// Q6_K, Q8_0 and Q4_0 are stored planar (layout.hpp): every field is an
+// aligned load of its own.
+template <> struct Raw32<T_Q6_K> { uint32_t ql[8], qh[8]; uint32_t sc, d; };
+template <> struct Raw32<T_Q8_0> { uint32_t q[8]; uint32_t d; };
+template <> struct Raw32<T_Q4_0> { uint32_t q[4]; uint32_t d; };
 template <> struct Raw32<T_Q4_1> { uint32_t q[4]; uint32_t dm; };  // 20-byte blocks keep 4-byte alignment
-
-// Word i of a field loaded `shift` bytes early.
-template <int N>
-__device__ __forceinline__ uint32_t word_at(const uint32_t (&raw)[N], uint32_t tail, uint32_t shift,
-                                            uint32_t i) {
-    return __builtin_amdgcn_alignbyte(i + 1u < N ? raw[i + 1u] : tail, raw[i], shift);
-}
 
 __device__ __forceinline__ uint32_t ld_word(const uint8_t* p) {
     return *reinterpret_cast<const uint32_t*>(__builtin_assume_aligned(p, 4));
 }
 
-__device__ __forceinline__ uint32_t align_shift(const uint8_t* p) {
-    return static_cast<uint32_t>(reinterpret_cast<uintptr_t>(p) & 3u);
-}
-
 template <int T>
-__device__ __forceinline__ void raw32_load(const uint8_t* row, uint32_t k0, Raw32<T>& r) {
+__device__ __forceinline__ void raw32_load(const QRow& row, uint32_t k0, Raw32<T>& r) {
     if constexpr (T == T_Q4_K || T == T_Q5_K) {
-        const uint8_t* blk = row + (k0 / 256u) * Fmt<T>::BB;
+        const uint8_t* blk = block_ptr<Fmt<T>::BB>(row, k0 / 256u);
         const uint32_t j = (k0 % 256u) / 32u, chunk = j / 2u;
         ld_words<4>(blk, r.h);
         ld_words<8>(blk + (T == T_Q4_K ? 16u : 48u) + 32u * chunk, r.q);
         if constexpr (T == T_Q5_K) ld_words<8>(blk + 16u, r.qh);
     } else if constexpr (T == T_Q6_K) {
-        const uint8_t* blk = row + (k0 / 256u) * 210u;
-        const uint32_t c = (k0 % 256u) / 32u, half = c / 4u, g = c % 4u;
-        r.shift = align_shift(blk);  // field offsets below are multiples of 4
-        const uint8_t* pl = blk - r.shift + 64u * half + 32u * (g & 1u);
-        const uint8_t* ph = blk - r.shift + 128u + 32u * half;
-        ld_words<8>(pl, r.ql);
-        r.ql8 = ld_word(pl + 32u);
-        ld_words<8>(ph, r.qh);
-        r.qh8 = ld_word(ph + 32u);
-        r.sc = ld_u16(blk + 192u + 8u * half + 2u * g);  // int8 scales of both 16-halves
-        r.d = ld_u16(blk + 208u);
+        using L = Planar<T_Q6_K>;
+        const uint32_t b = k0 / 256u, c = (k0 % 256u) / 32u, half = c / 4u, g = c % 4u;
+        ld_words<8>(field_ptr<L::QL, 128>(row, b) + 64u * half + 32u * (g & 1u), r.ql);
+        ld_words<8>(field_ptr<L::QH, 64>(row, b) + 32u * half, r.qh);
+        r.sc = ld_u16(field_ptr<L::SC, 16>(row, b) + 8u * half + 2u * g);  // int8 scales of both 16-halves
+        r.d = ld_u16(field_ptr<L::D, 2>(row, b));
     } else if constexpr (T == T_Q8_0) {
-        const uint8_t* blk = row + (k0 / 32u) * 34u;
-        r.shift = align_shift(blk + 2u);
-        ld_words<8>(blk + 2u - r.shift, r.q);
-        r.q8 = ld_word(blk + 34u - r.shift);
-        r.d = ld_u16(blk);
+        using L = Planar<T_Q8_0>;
+        ld_words<8>(field_ptr<L::QS, 32>(row, k0 / 32u), r.q);
+        r.d = ld_u16(field_ptr<L::D, 2>(row, k0 / 32u));
     } else if constexpr (T == T_Q4_1) {
-        const uint8_t* blk = row + (k0 / 32u) * 20u;
+        const uint8_t* blk = block_ptr<20>(row, k0 / 32u);
         r.dm = ld_word(blk);
         ld_words<4>(blk + 4u, r.q);
     } else {  // Q4_0
-        const uint8_t* blk = row + (k0 / 32u) * 18u;
-        r.shift = align_shift(blk + 2u);
-        ld_words<4>(blk + 2u - r.shift, r.q);
-        r.q4 = ld_word(blk + 18u - r.shift);
-        r.d = ld_u16(blk);
+        using L = Planar<T_Q4_0>;
+        ld_words<4>(field_ptr<L::QS, 16>(row, k0 / 32u), r.q);
+        r.d = ld_u16(field_ptr<L::D, 2>(row, k0 / 32u));
     }
 }
 
@@ -122,10 +99,8 @@ __device__ __forceinline__ void raw32_load(const uint8_t* row, uint32_t k0, Raw3
 //  * Q4_K: the whole 144-byte block (36 words), eight stages; the header is
 //    shared by all eight groups, each nibble byte by two.
 //  * Q6_K: one 128-value half of a block, four stages: its 64 ql bytes (each
-//    shared by two groups), 32 qh bytes (shared by four), 8 scale bytes and d.
-//    Blocks are 210 bytes, so consecutive blocks alternate between 4- and
-//    2-byte alignment: each field is loaded as the dwords covering it (one
-//    extra) and realigned by the unit's `shift` when decoded.
+//    shared by two groups), 32 qh bytes (shared by four), 8 scale bytes and d,
+//    each from its own plane.
 // (Q5_K's 44-word blocks would spill.)
 template <int T>
 constexpr bool kq_blocked() { return T == T_Q4_K || T == T_Q6_K; }
@@ -140,24 +115,22 @@ struct KqUnit<T_Q4_K> {
 template <>
 struct KqUnit<T_Q6_K> {
     static constexpr uint32_t STAGES = 4, PER_ROW_BLOCK = 2;
-    uint32_t ql[17], qh[9], sc[3];
-    uint32_t d, shift;
+    uint32_t ql[16], qh[8], sc[2];
+    uint32_t d;
 };
 
 // Unit u of a row: block u / PER_ROW_BLOCK (Q6_K: half u % 2 of it).
 template <int T>
-__device__ __forceinline__ void kq_unit_load(const uint8_t* row, uint32_t u, KqUnit<T>& U) {
+__device__ __forceinline__ void kq_unit_load(const QRow& row, uint32_t u, KqUnit<T>& U) {
     if constexpr (T == T_Q4_K) {
-        ld_words<36>(row + u * 144u, U.w);
+        ld_words<36>(block_ptr<144>(row, u), U.w);
     } else {
-        const uint8_t* blk = row + (u / 2u) * 210u;
-        const uint32_t h = u % 2u;
-        U.shift = align_shift(blk);
-        const uint8_t* base = blk - U.shift;  // field offsets below are multiples of 4
-        ld_words<17>(base + 64u * h, U.ql);
-        ld_words<9>(base + 128u + 32u * h, U.qh);
-        ld_words<3>(base + 192u + 8u * h, U.sc);
-        U.d = ld_u16(blk + 208u);
+        using L = Planar<T_Q6_K>;
+        const uint32_t b = u / 2u, h = u % 2u;
+        ld_words<16>(field_ptr<L::QL, 128>(row, b) + 64u * h, U.ql);
+        ld_words<8>(field_ptr<L::QH, 64>(row, b) + 32u * h, U.qh);
+        ld_words<2>(field_ptr<L::SC, 16>(row, b) + 8u * h, U.sc);
+        U.d = ld_u16(field_ptr<L::D, 2>(row, b));
     }
 }
 
@@ -174,15 +147,10 @@ __device__ __forceinline__ void raw32_from_unit(const KqUnit<T>& U, uint32_t j, 
         const uint32_t o = 8u * (j & 1u);  // low or high 32 ql bytes of the half
 #pragma unroll
         for (uint32_t i = 0; i < 8; ++i) r.ql[i] = U.ql[o + i];
-        r.ql8 = U.ql[o + 8u];
 #pragma unroll
         for (uint32_t i = 0; i < 8; ++i) r.qh[i] = U.qh[i];
-        r.qh8 = U.qh[8];
-        const uint32_t sw = j < 2u ? __builtin_amdgcn_alignbyte(U.sc[1], U.sc[0], U.shift)
-                                   : __builtin_amdgcn_alignbyte(U.sc[2], U.sc[1], U.shift);
-        r.sc = (sw >> (16u * (j & 1u))) & 0xffffu;  // int8 scales of both 16-halves
+        r.sc = (U.sc[j / 2u] >> (16u * (j & 1u))) & 0xffffu;  // int8 scales of both 16-halves
         r.d = U.d;
-        r.shift = U.shift;
     }
 }
 
@@ -232,8 +200,7 @@ __device__ __forceinline__ void raw32_bf16(const Raw32<T>& r, uint32_t k0, uint3
         const float d = half_bits_to_float(r.d);
 #pragma unroll
         for (uint32_t i = 0; i < 8; ++i) {
-            const uint32_t ql = word_at(r.ql, r.ql8, r.shift, i);
-            const uint32_t qh = word_at(r.qh, r.qh8, r.shift, i);
+            const uint32_t ql = r.ql[i], qh = r.qh[i];
             const uint32_t nib = (g >= 2u ? ql >> 4 : ql) & 0x0f0f0f0fu;
             bf16_bytes(nib | (((qh >> (2u * g)) & 0x03030303u) << 4), bw[2 * i], bw[2 * i + 1]);
         }
@@ -245,7 +212,7 @@ __device__ __forceinline__ void raw32_bf16(const Raw32<T>& r, uint32_t k0, uint3
         const float d = half_bits_to_float(r.d);
 #pragma unroll
         for (uint32_t i = 0; i < 8; ++i)
-            bf16_bytes(word_at(r.q, r.q8, r.shift, i) ^ 0x80808080u, bw[2 * i], bw[2 * i + 1]);
+            bf16_bytes(r.q[i] ^ 0x80808080u, bw[2 * i], bw[2 * i + 1]);
         ds[0] = ds[1] = d;
         cn[0] = cn[1] = __fmul_rn(-128.0f, d);
     } else if constexpr (T == T_Q4_1) {  // w = d * q + m: ds = d, cn = m (o = 0)
@@ -260,7 +227,7 @@ __device__ __forceinline__ void raw32_bf16(const Raw32<T>& r, uint32_t k0, uint3
         const float d = half_bits_to_float(r.d);
 #pragma unroll
         for (uint32_t i = 0; i < 4; ++i) {
-            const uint32_t q = word_at(r.q, r.q4, r.shift, i);
+            const uint32_t q = r.q[i];
             bf16_bytes(q & 0x0f0f0f0fu, bw[2 * i], bw[2 * i + 1]);
             bf16_bytes((q >> 4) & 0x0f0f0f0fu, bw[8 + 2 * i], bw[9 + 2 * i]);
         }
@@ -646,7 +613,7 @@ struct GemmPrefetch {
 // places).
 template <int TW, bool DUAL>
 struct GemmSrc {
-    const uint8_t* wrow;
+    QRow wrow;
     const uint16_t *ap0, *ap1;
     uint32_t adst0, adst1;
     const float* xs;
@@ -666,7 +633,7 @@ __device__ __forceinline__ void gemm_piece(const uint16_t* parts, uint64_t plane
 }
 
 template <int TW, bool DUAL>
-__device__ __forceinline__ void gemm_src(GemmSrc<TW, DUAL>& g, const uint8_t* wrow,
+__device__ __forceinline__ void gemm_src(GemmSrc<TW, DUAL>& g, const QRow& wrow,
                                          const uint16_t* parts, uint64_t plane, uint32_t kdim,
                                          const float* sums, const uint32_t* arow) {
     using C = GemmCfg<TW, DUAL>;
@@ -806,15 +773,20 @@ __global__ __launch_bounds__(256, 2) void k_expert_gemm(MoePrefillArgs a) {
     }
     const uint32_t wr = tid % C::NRW;
     const bool sh = tr.e >= L.n_experts;  // the shared expert (variant 1): its own tensors
-    const uint8_t* wrow;
-    if constexpr (DUAL)
-        wrow = (wr < 128u ? (sh ? L.shared_gate : L.gate + static_cast<uint64_t>(tr.e) * L.gate_slice) +
-                                static_cast<uint64_t>(n0 + wr) * L.gate_row
-                          : (sh ? L.shared_up : L.up + static_cast<uint64_t>(tr.e) * L.up_slice) +
-                                static_cast<uint64_t>(n0 + wr - 128u) * L.up_row);
-    else  // rows n0 .. n0 + 255
-        wrow = (sh ? L.shared_down : L.down + static_cast<uint64_t>(tr.e) * L.down_slice) +
-               static_cast<uint64_t>(n0 + wr) * L.down_row;
+    // the slice, its blocks and the row's first block (gate/up rows have hidden
+    // elements, down rows ffn)
+    const uint32_t rnb = kdim / Fmt<TW>::BE;
+    QRow wrow;
+    if constexpr (DUAL) {
+        wrow.slice = wr < 128u ? (sh ? L.shared_gate : L.gate + static_cast<uint64_t>(tr.e) * L.gate_slice)
+                               : (sh ? L.shared_up : L.up + static_cast<uint64_t>(tr.e) * L.up_slice);
+        wrow.nblk = static_cast<uint64_t>(L.ffn) * rnb;
+        wrow.blk0 = static_cast<uint64_t>(wr < 128u ? n0 + wr : n0 + wr - 128u) * rnb;
+    } else {  // rows n0 .. n0 + 255
+        wrow.slice = sh ? L.shared_down : L.down + static_cast<uint64_t>(tr.e) * L.down_slice;
+        wrow.nblk = static_cast<uint64_t>(L.hidden) * rnb;
+        wrow.blk0 = static_cast<uint64_t>(n0 + wr) * rnb;
+    }
     const uint16_t* parts = DUAL ? a.x_parts : a.act_parts;
     const uint64_t plane = DUAL ? static_cast<uint64_t>(a.tokens) * L.hidden
                                 : static_cast<uint64_t>(a.tokens) * (L.top_k + L.variant) * L.ffn;

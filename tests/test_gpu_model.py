@@ -30,18 +30,6 @@ def mg():
         return {k: z[k] for k in z.files}
 
 
-def _device_bytes(w, nbytes):
-    import torch
-    import ctypes
-    t = torch.empty(nbytes, dtype=torch.uint8, device="cuda:0")
-    torch.cuda.synchronize()
-    from pokitlms_amd.backend import HipBackend  # noqa: F401  (library loaded after torch)
-    hip_memcpy = ctypes.CDLL("libamdhip64.so.7").hipMemcpy  # torch's runtime (loaded first)
-    hip_memcpy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int]
-    assert hip_memcpy(t.data_ptr(), w.device_ptr, nbytes, 3) == 0  # device to device
-    return t.cpu().numpy()
-
-
 def test_device_generator_matches_numpy(hip):
     """pk_hip_synth_weight writes the bytes synth_model.tensor_payload computes,
     for every fix-up recipe."""
@@ -59,7 +47,7 @@ def test_device_generator_matches_numpy(hip):
                                               ctypes.byref(h), err, _ERRBUF), err)
         nbytes = S.row_bytes(gtype, inn) * out * max(ne, 1)
         w = Weight(hip, h.value, gtype, inn, out, ne, nbytes)
-        got = _device_bytes(w, nbytes)
+        got = w.download()
         want = SM.tensor_payload(99, i, gtype, kind, nbytes)
         assert np.array_equal(got, want), (gtype, kind)
         w.release()

@@ -156,6 +156,28 @@ def test_expert_slice_matvec(hip, port):
         hip.matvec(g, x, expert=4)
     g.release()
     d.release()
+    # planar types whose slices are padded to 256 bytes between experts
+    for gtype in (S.Q4_0, S.Q8_0, S.Q6_K):
+        ws = [S.quant_matrix(gtype, 37, 512, S.rng(24 + e)) for e in range(3)]
+        wt = hip.upload(gtype, 512, 37, np.concatenate([w.reshape(-1) for w in ws]), n_experts=3)
+        for e in range(3):
+            assert normwise_rel(hip.matvec(wt, x, expert=e), port.linear(gtype, ws[e], 512, 37, x)) <= TOL
+        wt.release()
+
+
+@pytest.mark.parametrize("gtype", FLOAT + QUANT)
+@pytest.mark.parametrize("rows,experts", ((37, 0), (37, 3), (5, 2)))
+def test_weight_layout_round_trip(hip, gtype, rows, experts):
+    """Q4_0, Q8_0 and Q6_K sit in HBM as per-slice field planes (odd slice
+    sizes padded between experts); reading the weight back returns the GGUF
+    bytes of every type unchanged."""
+    say("round trip", S.TYPE_NAMES[gtype], rows, experts)
+    inn = 512
+    nbytes = S.row_bytes(gtype, inn) * rows * max(experts, 1)
+    w = S.rng(40 + gtype).integers(0, 256, nbytes, dtype=np.uint8)
+    wt = hip.upload(gtype, inn, rows, w, experts)
+    assert np.array_equal(wt.download(), w)
+    wt.release()
 
 
 def test_try_linear_contract(hip, port):
