@@ -190,6 +190,20 @@ pk_hip_status pk_hip_moe_decode_async(pk_hip_ctx* ctx, const pk_hip_moe_layer* l
                                       uint32_t* device_ids, float* device_probs, void* stream,
                                       char* error_buffer, size_t error_capacity);
 
+/* As pk_hip_moe_decode_async, allocating nothing: no counterpart in the
+ * reference; for callers that cannot allocate device memory (code under HIP
+ * graph capture, tight serving loops, harnesses that forbid hipMalloc).  The
+ * router sums, activations and status words live in one static device array
+ * of 69,888 bytes per GPU, so layers above 256 experts, top_k 8 or ffn 2048
+ * are rejected with INVALID_ARGUMENT.  Every call on a GPU shares that array:
+ * calls that overlap on one GPU (two streams, two contexts) race.  A
+ * non-finite router logit is reported through the outputs (ids UINT32_MAX,
+ * probs 0), not by pk_hip_sync. */
+pk_hip_status pk_hip_moe_decode_noalloc(pk_hip_ctx* ctx, const pk_hip_moe_layer* layer,
+                                        const float* device_x, float* device_y,
+                                        uint32_t* device_ids, float* device_probs, void* stream,
+                                        char* error_buffer, size_t error_capacity);
+
 /* Qwen3.5-MoE block for one token (src/qwen35_runner.cpp:670-764) on the same
  * kernels.  Routed experts come from select_experts (:131-173): the same
  * top-k order as route_experts (ids bit-exact), weights from an FP32 softmax

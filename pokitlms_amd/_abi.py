@@ -31,7 +31,7 @@ EXPORTS = (
     "pk_hip_moe35_prefill", "pk_hip_moe35_prefill_async",
     "pk_hip_moe_prefill_async", "pk_hip_qwen3moe_create", "pk_hip_qwen3moe_destroy",
     "pk_hip_qwen3moe_generate", "pk_hip_synth_weight", "pk_hip_matvec_reference_order",
-    "pk_hip_weight_download",
+    "pk_hip_weight_download", "pk_hip_moe_decode_noalloc",
 )
 
 
@@ -140,6 +140,9 @@ def lib() -> ctypes.CDLL:
     L.pk_hip_moe_decode_async.restype = ctypes.c_int
     L.pk_hip_moe_decode_async.argtypes = [vp, ctypes.POINTER(MoeLayerDesc), vp, vp, vp, vp, vp,
                                           cp, sz]
+    L.pk_hip_moe_decode_noalloc.restype = ctypes.c_int
+    L.pk_hip_moe_decode_noalloc.argtypes = [vp, ctypes.POINTER(MoeLayerDesc), vp, vp, vp, vp, vp,
+                                            cp, sz]
     L.pk_hip_sync.restype = ctypes.c_int
     L.pk_hip_sync.argtypes = [vp, vp, cp, sz]
     L.pk_hip_get_stats.restype = ctypes.c_int

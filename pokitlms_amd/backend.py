@@ -315,6 +315,15 @@ class HipBackend:
                                                   device_x, device_y, device_ids, device_probs,
                                                   stream or None, err, _ERRBUF), err)
 
+    def moe_decode_noalloc(self, layer: MoeLayerHandles, device_x: int, device_y: int,
+                           device_ids: int, device_probs: int, stream: int = 0) -> None:
+        """moe_decode_async on the library's static device scratch (no device
+        allocation; calls that overlap on one GPU race)."""
+        err = ctypes.create_string_buffer(_ERRBUF)
+        _raise(_abi.lib().pk_hip_moe_decode_noalloc(self.handle, ctypes.byref(layer.desc),
+                                                    device_x, device_y, device_ids, device_probs,
+                                                    stream or None, err, _ERRBUF), err)
+
     def moe_prefill(self, layer: MoeLayerHandles, x: np.ndarray):
         """A batch of tokens x [tokens, hidden] through the layer; per token the
         result of moe_decode (the reference's prompt loop, one token at a time:

@@ -89,8 +89,45 @@ struct DeviceBuffer {
 
 }  // namespace
 
+// ---------------------------------------------------------------------------
+// Scratch of pk_hip_moe_decode_noalloc: one static device array per GPU (each
+// device holds its own copy until the process ends).  Its host-side name is
+// only a stand-in for the symbol; the device address comes from
+// hipGetSymbolAddress, resolved once per device with that device current.
+// Layout: status words | row sums | row bounds | activations.
+namespace noalloc {
+constexpr uint32_t kMaxExperts = 256;
+constexpr uint32_t kMaxTopK = 8;
+constexpr uint32_t kMaxFfn = 2048;
+constexpr size_t kStatusBytes = 256;
+constexpr size_t kSumBytes = kMaxExperts * sizeof(double);
+constexpr size_t kActBytes = static_cast<size_t>(kMaxTopK) * kMaxFfn * sizeof(float);
+constexpr size_t kBytes = kStatusBytes + 2 * kSumBytes + kActBytes;  // 69,888 bytes
+constexpr int kMaxDevices = 64;
+}  // namespace noalloc
+
+static __device__ __align__(256) uint8_t scratch[noalloc::kBytes];
+
+namespace {
+std::mutex g_scratch_mutex;
+uint8_t* g_scratch_ptr[noalloc::kMaxDevices] = {};
+
+// The calling thread's current device must be `device`.
+uint8_t* resolve_scratch(int device) {
+    if (device < 0 || device >= noalloc::kMaxDevices) return nullptr;
+    std::lock_guard lock(g_scratch_mutex);
+    if (!g_scratch_ptr[device]) {
+        void* ptr = nullptr;
+        check(hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)), "hipGetSymbolAddress(scratch)");
+        g_scratch_ptr[device] = static_cast<uint8_t*>(ptr);
+    }
+    return g_scratch_ptr[device];
+}
+}  // namespace
+
 struct pk_hip_ctx {
     int device = 0;
+    uint8_t* noalloc_scratch = nullptr;  // this device's static scratch array
     hipStream_t stream = nullptr;
     bool failed = false;
     bool time_kernels = false;
@@ -396,10 +433,24 @@ void ensure_moe_scratch(pk_hip_ctx* c, const MoeShape& m, uint32_t top_k) {
     c->probs.ensure(16);
 }
 
+// Device scratch of one decode call: router sums and bounds, activations and
+// status words.
+struct MoeScratch {
+    double* row_sum;
+    double* row_bound;
+    float* act;
+    uint32_t* status;
+};
+
+MoeScratch context_scratch(pk_hip_ctx* c, const MoeShape& m, uint32_t top_k) {
+    ensure_moe_scratch(c, m, top_k);
+    return MoeScratch{c->row_sum.ptr, c->row_bound.ptr, c->act.ptr, status_words(c)};
+}
+
 void enqueue_moe(pk_hip_ctx* c, const pk_hip_moe_layer* L, const MoeShape& m, const float* dx,
                  float* dy, uint32_t* dids, float* dprobs, hipStream_t s,
-                 const pk_hip_moe35_layer* shared = nullptr) {
-    ensure_moe_scratch(c, m, L->top_k);
+                 const pk_hip_moe35_layer* shared = nullptr, const MoeScratch* scratch = nullptr) {
+    const MoeScratch sc = scratch ? *scratch : context_scratch(c, m, L->top_k);
     pk::MoeDecodeArgs a{};
     if (shared) {
         a.variant = 1;
@@ -433,10 +484,10 @@ void enqueue_moe(pk_hip_ctx* c, const pk_hip_moe_layer* L, const MoeShape& m, co
     a.y = dy;
     a.ids = dids;
     a.probs = dprobs;
-    a.row_sum = c->row_sum.ptr;
-    a.row_bound = c->row_bound.ptr;
-    a.act = c->act.ptr;
-    a.status = status_words(c);
+    a.row_sum = sc.row_sum;
+    a.row_bound = sc.row_bound;
+    a.act = sc.act;
+    a.status = sc.status;
     if (c->time_kernels) hold_stream(c, s);
     begin_timing(c, s, 2);
     launch_checked(pk::launch_moe_router(a, s), "router launch");
@@ -521,6 +572,7 @@ pk_hip_status pk_hip_create(int device, const pk_hip_options* options, pk_hip_ct
         // timing-only events: no system-scope fence (cache writeback) on record
         for (auto& e : c->ev)
             check(hipEventCreateWithFlags(&e, hipEventDisableSystemFence), "hipEventCreate");
+        c->noalloc_scratch = resolve_scratch(dev);
         c->words.ensure(8);
         check(hipMemsetAsync(c->words.ptr, 0, 8 * sizeof(uint32_t), c->stream), "init status");
         check(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
@@ -769,6 +821,34 @@ pk_hip_status pk_hip_moe_decode_async(pk_hip_ctx* ctx, const pk_hip_moe_layer* l
         ctx->set_device();
         hipStream_t s = stream ? static_cast<hipStream_t>(stream) : ctx->stream;
         enqueue_moe(ctx, layer, m, dx, dy, dids, dprobs, s);
+        if (ctx->time_kernels) {
+            check(hipStreamSynchronize(s), "hipStreamSynchronize");
+            collect_timing_moe(ctx);
+        }
+    });
+}
+
+pk_hip_status pk_hip_moe_decode_noalloc(pk_hip_ctx* ctx, const pk_hip_moe_layer* layer,
+                                        const float* dx, float* dy, uint32_t* dids, float* dprobs,
+                                        void* stream, char* err, size_t cap) {
+    return guarded(ctx, err, cap, [&] {
+        require_usable(ctx);
+        if (!dx || !dy || !dids || !dprobs) throw ArgError("device buffers are required");
+        std::lock_guard lock(ctx->mutex);
+        const MoeShape m = check_decode_layer(ctx, layer);
+        if (m.experts > noalloc::kMaxExperts || layer->top_k > noalloc::kMaxTopK ||
+            m.ffn > noalloc::kMaxFfn)
+            throw ArgError("layer exceeds the no-allocation scratch (at most 256 experts, top-k 8, "
+                           "ffn 2048)");
+        if (!ctx->noalloc_scratch) throw ArgError("no static scratch on this device");
+        ctx->set_device();
+        uint8_t* base = ctx->noalloc_scratch;
+        const MoeScratch sc{reinterpret_cast<double*>(base + noalloc::kStatusBytes),
+                            reinterpret_cast<double*>(base + noalloc::kStatusBytes + noalloc::kSumBytes),
+                            reinterpret_cast<float*>(base + noalloc::kStatusBytes + 2 * noalloc::kSumBytes),
+                            reinterpret_cast<uint32_t*>(base)};
+        hipStream_t s = stream ? static_cast<hipStream_t>(stream) : ctx->stream;
+        enqueue_moe(ctx, layer, m, dx, dy, dids, dprobs, s, nullptr, &sc);
         if (ctx->time_kernels) {
             check(hipStreamSynchronize(s), "hipStreamSynchronize");
             collect_timing_moe(ctx);
