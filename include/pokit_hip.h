@@ -11,8 +11,8 @@
  * backends serialize with a mutex, src/vulkan_linear.cpp:635; C handles
  * require serialized calls, pokitlms.h:81).
  *
- * GGUF type ids: F32 0, F16 1, Q4_0 2, Q4_1 3, Q8_0 8, Q4_K 12, Q5_K 13, Q6_K 14,
- * BF16 30 (src/gguf_reader.cpp:21-57).  Matrices are GGUF [in, out] tensors:
+ * GGUF type ids: F32 0, F16 1, Q4_0 2, Q4_1 3, Q5_0 6, Q5_1 7, Q8_0 8, Q2_K 10,
+ * Q3_K 11, Q4_K 12, Q5_K 13, Q6_K 14, BF16 30 (src/gguf_reader.cpp:21-57).  Matrices are GGUF [in, out] tensors:
  * `out` rows of `in` elements, each row a run of encoded blocks.  Expert
  * tensors are [in, out, n_experts] with the expert index slowest, so expert e
  * is the contiguous slice e * (out * row_bytes) (src/expert_store.cpp:17-36).
@@ -75,13 +75,15 @@ typedef struct pk_hip_stats {
     uint64_t prefill_calls, prefill_tokens, prefill_ns;
     uint64_t prefill_route_ns, prefill_gate_up_ns, prefill_down_ns;
     uint64_t q4_1_dispatches;
+    uint64_t q5_0_dispatches, q5_1_dispatches, q2_k_dispatches, q3_k_dispatches;
 } pk_hip_stats;
 
 const char* pk_hip_version(void);
 
 /* Non-zero when `ggml_type` has a matvec kernel: F32/F16/BF16/Q4_0/Q4_1/
- * Q8_0/Q4_K/Q5_K/Q6_K, i.e. the Vulkan backend's type list
- * (src/vulkan_linear.cpp:78-83). */
+ * Q5_0/Q5_1/Q8_0/Q2_K/Q3_K/Q4_K/Q5_K/Q6_K, every type tensor_linear
+ * dispatches (src/tensor_linear.cpp:176-187; the Vulkan backend's list,
+ * src/vulkan_linear.cpp:78-83, omits Q5_0/Q5_1/Q2_K/Q3_K). */
 int pk_hip_type_supported(uint32_t ggml_type);
 
 /* Backend construction / destruction: VulkanLinearBackend ctor and dtor

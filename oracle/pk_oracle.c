@@ -20,8 +20,8 @@
 uint32_t pko_block_elements(uint32_t type) {
     switch (type) {
         case PKO_F32: case PKO_F16: case PKO_BF16: return 1;
-        case PKO_Q4_0: case PKO_Q4_1: case PKO_Q8_0: return 32;
-        case PKO_Q4_K: case PKO_Q5_K: case PKO_Q6_K: return 256;
+        case PKO_Q4_0: case PKO_Q4_1: case PKO_Q5_0: case PKO_Q5_1: case PKO_Q8_0: return 32;
+        case PKO_Q2_K: case PKO_Q3_K: case PKO_Q4_K: case PKO_Q5_K: case PKO_Q6_K: return 256;
         default: return 0;
     }
 }
@@ -32,7 +32,11 @@ uint32_t pko_block_bytes(uint32_t type) {
         case PKO_F16: case PKO_BF16: return 2;
         case PKO_Q4_0: return 18;
         case PKO_Q4_1: return 20;
+        case PKO_Q5_0: return 22;
+        case PKO_Q5_1: return 24;
         case PKO_Q8_0: return 34;
+        case PKO_Q2_K: return 84;
+        case PKO_Q3_K: return 110;
         case PKO_Q4_K: return 144;
         case PKO_Q5_K: return 176;
         case PKO_Q6_K: return 210;
@@ -180,6 +184,93 @@ void pko_decode_q4_1(const uint8_t* blk, float* out) {
     }
 }
 
+static uint32_t rd32(const uint8_t* p) {
+    return (uint32_t)p[0] | ((uint32_t)p[1] << 8) | ((uint32_t)p[2] << 16) | ((uint32_t)p[3] << 24);
+}
+
+/* src/quantized_linear.cpp:64-77: value = fl((q - 16) * d), q = nibble | qh bit << 4,
+ * low nibbles first, qh bit i for element i and bit i + 16 for element i + 16. */
+void pko_decode_q5_0(const uint8_t* blk, float* out) {
+    const float d = pko_half_to_float(rd16(blk));
+    const uint32_t qh = rd32(blk + 2);
+    for (unsigned i = 0; i < 16; ++i) {
+        const int q0 = (int)(blk[6 + i] & 0x0fu) | (int)(((qh >> i) & 1u) << 4);
+        const int q1 = (int)(blk[6 + i] >> 4) | (int)(((qh >> (i + 16)) & 1u) << 4);
+        out[i] = (float)(q0 - 16) * d;
+        out[i + 16] = (float)(q1 - 16) * d;
+    }
+}
+
+/* src/quantized_linear.cpp:79-93: value = fl(fl(q * d) + m), q unsigned 5-bit. */
+void pko_decode_q5_1(const uint8_t* blk, float* out) {
+    const float d = pko_half_to_float(rd16(blk)), m = pko_half_to_float(rd16(blk + 2));
+    const uint32_t qh = rd32(blk + 4);
+    for (unsigned i = 0; i < 16; ++i) {
+        const unsigned q0 = (blk[8 + i] & 0x0fu) | (((qh >> i) & 1u) << 4);
+        const unsigned q1 = (blk[8 + i] >> 4) | (((qh >> (i + 16)) & 1u) << 4);
+        out[i] = (float)q0 * d + m;
+        out[i + 16] = (float)q1 * d + m;
+    }
+}
+
+/* src/quantized_linear.cpp:95-121: 16 scale bytes (low nibble scale, high
+ * nibble min), 2-bit quants in 2 chunks of 32 bytes, 4 shifts per chunk, each
+ * shift two 16-element groups: value = fl(fl(dl * q) - ml), dl = fl(d * sc),
+ * ml = fl(dmin * m); d at 80, dmin at 82. */
+void pko_decode_q2_k(const uint8_t* blk, float* out) {
+    const float d = pko_half_to_float(rd16(blk + 80)), dmin = pko_half_to_float(rd16(blk + 82));
+    const uint8_t* q = blk + 16;
+    unsigned si = 0, o = 0;
+    for (unsigned chunk = 0; chunk < 2; ++chunk) {
+        for (unsigned shift = 0; shift < 8; shift += 2) {
+            const uint8_t sc0 = blk[si++], sc1 = blk[si++];
+            const float dl0 = d * (float)(sc0 & 0x0fu), ml0 = dmin * (float)(sc0 >> 4);
+            const float dl1 = d * (float)(sc1 & 0x0fu), ml1 = dmin * (float)(sc1 >> 4);
+            for (unsigned i = 0; i < 16; ++i) out[o++] = dl0 * (float)((q[i] >> shift) & 3u) - ml0;
+            for (unsigned i = 0; i < 16; ++i) out[o++] = dl1 * (float)((q[i + 16] >> shift) & 3u) - ml1;
+        }
+        q += 32;
+    }
+}
+
+/* src/quantized_linear.cpp:123-164: hmask[32], 2-bit quants in 2 chunks of 32
+ * bytes, 12 bytes of packed 6-bit scales (minus 32), d at 108.  value =
+ * fl(ds * (q - (hmask bit ? 0 : 4))), ds = fl(d * (scale - 32)). */
+void pko_decode_q3_k(const uint8_t* blk, float* out) {
+    const uint8_t* hm = blk;
+    const uint8_t* q = blk + 32;
+    uint32_t aux[4];
+    aux[0] = rd32(blk + 96);
+    aux[1] = rd32(blk + 100);
+    aux[2] = rd32(blk + 104);
+    const uint32_t tmp = aux[2];
+    aux[2] = ((aux[0] >> 4) & 0x0f0f0f0fu) | (((tmp >> 4) & 0x03030303u) << 4);
+    aux[3] = ((aux[1] >> 4) & 0x0f0f0f0fu) | (((tmp >> 6) & 0x03030303u) << 4);
+    aux[0] = (aux[0] & 0x0f0f0f0fu) | (((tmp >> 0) & 0x03030303u) << 4);
+    aux[1] = (aux[1] & 0x0f0f0f0fu) | (((tmp >> 2) & 0x03030303u) << 4);
+    int8_t scales[16];
+    memcpy(scales, aux, 16);
+    const float d = pko_half_to_float(rd16(blk + 108));
+    unsigned si = 0, o = 0;
+    unsigned bit = 1;
+    for (unsigned chunk = 0; chunk < 2; ++chunk) {
+        for (unsigned shift = 0; shift < 8; shift += 2) {
+            const float ds0 = d * (float)(scales[si++] - 32);
+            const float ds1 = d * (float)(scales[si++] - 32);
+            for (unsigned i = 0; i < 16; ++i) {
+                const int v = (int)((q[i] >> shift) & 3u) - ((hm[i] & bit) ? 0 : 4);
+                out[o++] = ds0 * (float)v;
+            }
+            for (unsigned i = 0; i < 16; ++i) {
+                const int v = (int)((q[i + 16] >> shift) & 3u) - ((hm[i + 16] & bit) ? 0 : 4);
+                out[o++] = ds1 * (float)v;
+            }
+            bit <<= 1;
+        }
+        q += 32;
+    }
+}
+
 int pko_dequantize_row(uint32_t type, const uint8_t* enc, uint64_t enc_bytes, float* out,
                        uint64_t count) {
     const uint32_t be = pko_block_elements(type), bb = pko_block_bytes(type);
@@ -199,6 +290,10 @@ int pko_dequantize_row(uint32_t type, const uint8_t* enc, uint64_t enc_bytes, fl
                 break;
             }
             case PKO_Q4_1: pko_decode_q4_1(blk, row); break;  /* :453-469 */
+            case PKO_Q5_0: pko_decode_q5_0(blk, row); break;
+            case PKO_Q5_1: pko_decode_q5_1(blk, row); break;
+            case PKO_Q2_K: pko_decode_q2_k(blk, row); break;  /* :471-490 */
+            case PKO_Q3_K: pko_decode_q3_k(blk, row); break;
             case PKO_Q4_K: pko_decode_q4_k(blk, row); break;
             case PKO_Q5_K: pko_decode_q5_k(blk, row); break;
             case PKO_Q6_K: pko_decode_q6_k(blk, row); break;
@@ -251,16 +346,22 @@ int pko_linear(uint32_t type, const uint8_t* w, uint64_t w_bytes, uint64_t in, u
                 if (type == PKO_Q4_0) unpack_q4_0(blk + 2, q);
                 else memcpy(q, blk + 2, 32);
                 sum += scale * dot_i8_f32(xb, q, 32);
-            } else if (type == PKO_Q4_1) {
-                /* linear_k<32, 20> with decode_q4_1 (src/quantized_linear.cpp:503-507) */
+            } else if (be == 32) {
+                /* linear_k<32, 20/22/24> with decode_q4_1 / q5_0 / q5_1
+                 * (src/quantized_linear.cpp:503-519) */
                 float dec[32];
-                pko_decode_q4_1(blk, dec);
+                if (type == PKO_Q4_1) pko_decode_q4_1(blk, dec);
+                else if (type == PKO_Q5_0) pko_decode_q5_0(blk, dec);
+                else pko_decode_q5_1(blk, dec);
                 sum += dot_f32(dec, xb, 32);
             } else {
-                /* linear_k (src/quantized_linear.cpp:374-384); on x86 Q4_K takes
-                 * this decode-then-dot branch (:541-549). */
+                /* linear_k (src/quantized_linear.cpp:374-384) for Q2_K..Q6_K
+                 * (:529-561); on x86 Q4_K takes this decode-then-dot branch
+                 * (:541-549). */
                 float dec[256];
-                if (type == PKO_Q4_K) pko_decode_q4_k(blk, dec);
+                if (type == PKO_Q2_K) pko_decode_q2_k(blk, dec);
+                else if (type == PKO_Q3_K) pko_decode_q3_k(blk, dec);
+                else if (type == PKO_Q4_K) pko_decode_q4_k(blk, dec);
                 else if (type == PKO_Q5_K) pko_decode_q5_k(blk, dec);
                 else pko_decode_q6_k(blk, dec);
                 sum += dot_f32(dec, xb, 256);

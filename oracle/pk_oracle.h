@@ -25,8 +25,9 @@ extern "C" {
 
 /* GGUF tensor type ids (reference src/gguf_reader.cpp:21-57). */
 enum {
-    PKO_F32 = 0, PKO_F16 = 1, PKO_Q4_0 = 2, PKO_Q4_1 = 3, PKO_Q8_0 = 8,
-    PKO_Q4_K = 12, PKO_Q5_K = 13, PKO_Q6_K = 14, PKO_BF16 = 30
+    PKO_F32 = 0, PKO_F16 = 1, PKO_Q4_0 = 2, PKO_Q4_1 = 3, PKO_Q5_0 = 6, PKO_Q5_1 = 7,
+    PKO_Q8_0 = 8, PKO_Q2_K = 10, PKO_Q3_K = 11, PKO_Q4_K = 12, PKO_Q5_K = 13, PKO_Q6_K = 14,
+    PKO_BF16 = 30
 };
 
 /* Elements and bytes of one encoded block; 0 when the type is not on the path. */
@@ -47,7 +48,15 @@ void pko_decode_q6_k(const uint8_t* block, float* out256);
  * (decode_q4_1, src/quantized_linear.cpp:53-62). */
 void pko_decode_q4_1(const uint8_t* block, float* out32);
 
-/* dequantize_quantized_row for Q4_0/Q4_1/Q8_0/Q4_K/Q5_K/Q6_K
+/* One 32-element Q5_0 / Q5_1 block (decode_q5_0 / decode_q5_1,
+ * src/quantized_linear.cpp:64-77, 79-93) and one 256-element Q2_K / Q3_K
+ * block (decode_q2_k / decode_q3_k, :95-121, 123-164) to F32. */
+void pko_decode_q5_0(const uint8_t* block, float* out32);
+void pko_decode_q5_1(const uint8_t* block, float* out32);
+void pko_decode_q2_k(const uint8_t* block, float* out256);
+void pko_decode_q3_k(const uint8_t* block, float* out256);
+
+/* dequantize_quantized_row for every quantized type above
  * (src/quantized_linear.cpp:427-493). */
 int pko_dequantize_row(uint32_t type, const uint8_t* encoded, uint64_t encoded_bytes,
                        float* out, uint64_t count);

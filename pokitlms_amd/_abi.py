@@ -47,7 +47,8 @@ class Stats(ctypes.Structure):
         "router_candidates", "expert_hits", "expert_misses", "matvec_ns", "router_ns",
         "gate_up_ns", "down_ns", "router_launches", "gate_up_launches", "down_launches",
         "matvec_launches", "prefill_calls", "prefill_tokens", "prefill_ns",
-        "prefill_route_ns", "prefill_gate_up_ns", "prefill_down_ns", "q4_1_dispatches")]
+        "prefill_route_ns", "prefill_gate_up_ns", "prefill_down_ns", "q4_1_dispatches",
+        "q5_0_dispatches", "q5_1_dispatches", "q2_k_dispatches", "q3_k_dispatches")]
 
     def as_dict(self) -> dict:
         return {n: getattr(self, n) for n, _ in self._fields_}

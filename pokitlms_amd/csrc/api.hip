@@ -48,8 +48,8 @@ void check(hipError_t e, const char* what) {
 uint32_t block_elements(uint32_t t) {
     switch (t) {
         case 0: case 1: case 30: return 1;
-        case 2: case 3: case 8: return 32;
-        case 12: case 13: case 14: return 256;
+        case 2: case 3: case 6: case 7: case 8: return 32;
+        case 10: case 11: case 12: case 13: case 14: return 256;
         default: return 0;
     }
 }
@@ -60,7 +60,11 @@ uint32_t block_bytes(uint32_t t) {
         case 1: case 30: return 2;
         case 2: return 18;
         case 3: return 20;
+        case 6: return 22;
+        case 7: return 24;
         case 8: return 34;
+        case 10: return 84;
+        case 11: return 110;
         case 12: return 144;
         case 13: return 176;
         case 14: return 210;
@@ -205,7 +209,11 @@ void count_dispatch(pk_hip_ctx* c, uint32_t type) {
     switch (type) {
         case 2: ++c->stats.q4_0_dispatches; break;
         case 3: ++c->stats.q4_1_dispatches; break;
+        case 6: ++c->stats.q5_0_dispatches; break;
+        case 7: ++c->stats.q5_1_dispatches; break;
         case 8: ++c->stats.q8_0_dispatches; break;
+        case 10: ++c->stats.q2_k_dispatches; break;
+        case 11: ++c->stats.q3_k_dispatches; break;
         case 12: ++c->stats.q4_k_dispatches; break;
         case 13: ++c->stats.q5_k_dispatches; break;
         case 14: ++c->stats.q6_k_dispatches; break;
@@ -543,7 +551,8 @@ const char* pk_hip_version(void) { return "0.1.0"; }
 
 int pk_hip_type_supported(uint32_t t) {
     switch (t) {
-        case 0: case 1: case 2: case 3: case 8: case 12: case 13: case 14: case 30: return 1;
+        case 0: case 1: case 2: case 3: case 6: case 7: case 8: case 10: case 11: case 12:
+        case 13: case 14: case 30: return 1;
         default: return 0;
     }
 }

@@ -70,6 +70,22 @@ template <>
 struct RefBlock<T_Q4_1> {
     static constexpr uint32_t BE = 32, BB = 20;
 };
+template <>
+struct RefBlock<T_Q5_0> {
+    static constexpr uint32_t BE = 32, BB = 22;
+};
+template <>
+struct RefBlock<T_Q5_1> {
+    static constexpr uint32_t BE = 32, BB = 24;
+};
+template <>
+struct RefBlock<T_Q2_K> {
+    static constexpr uint32_t BE = 256, BB = 84;
+};
+template <>
+struct RefBlock<T_Q3_K> {
+    static constexpr uint32_t BE = 256, BB = 110;
+};
 
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
@@ -208,6 +224,96 @@ __device__ float block_dot(const QRow& row, uint32_t b, const float* x) {
             s = __fadd_rn(s, __fmul_rn(__fadd_rn(__fmul_rn(ub<1>(v), d), m), xv.y));
             s = __fadd_rn(s, __fmul_rn(__fadd_rn(__fmul_rn(ub<2>(v), d), m), xv.z));
             s = __fadd_rn(s, __fmul_rn(__fadd_rn(__fmul_rn(ub<3>(v), d), m), xv.w));
+        }
+    } else if constexpr (T == T_Q5_0 || T == T_Q5_1) {
+        // decode_q5_0: fl((q - 16) * d); decode_q5_1: fl(fl(q * d) + m)
+        // (src/quantized_linear.cpp:64-93), then dot_f32's order
+        uint32_t qs[4], qh[1];
+        float d, m = 0.0f;
+        if constexpr (T == T_Q5_0) {
+            using L = Planar<T_Q5_0>;
+            ld_words<4>(field_ptr<L::QS, 16>(row, b), qs);
+            ld_words<1>(field_ptr<L::QH, 4>(row, b), qh);
+            d = half_bits_to_float(ld_u16(field_ptr<L::D, 2>(row, b)));
+        } else {
+            uint32_t w[6];  // d | m << 16, qh, quants
+            ld_words<6>(block_ptr<24>(row, b), w);
+            d = half_bits_to_float(w[0] & 0xffffu);
+            m = half_bits_to_float(w[0] >> 16);
+            qh[0] = w[1];
+#pragma unroll
+            for (uint32_t i = 0; i < 4; ++i) qs[i] = w[2u + i];
+        }
+#pragma unroll
+        for (uint32_t k = 0; k < 8; ++k) {
+            const float4 xv = x4[k];
+            const float xs[4] = {xv.x, xv.y, xv.z, xv.w};
+#pragma unroll
+            for (uint32_t j = 0; j < 4; ++j) {
+                const uint32_t i = 4u * k + j, byte = i & 15u;
+                const uint32_t v = (qs[byte / 4u] >> (8u * (byte % 4u))) & 0xffu;
+                const uint32_t q = (i < 16u ? (v & 15u) : (v >> 4)) | (((qh[0] >> i) & 1u) << 4);
+                const float w = T == T_Q5_0 ? __fmul_rn(static_cast<float>(static_cast<int>(q) - 16), d)
+                                            : __fadd_rn(__fmul_rn(static_cast<float>(q), d), m);
+                s = __fadd_rn(s, __fmul_rn(w, xs[j]));
+            }
+        }
+    } else if constexpr (T == T_Q2_K || T == T_Q3_K) {
+        // decode_q2_k: fl(fl(dl * q) - ml); decode_q3_k: fl(ds * (q - 4 + 4 * hbit))
+        // (src/quantized_linear.cpp:95-164); element 128h + 32s + 16t + i
+        uint32_t qw[16], hw[8], sw[4];
+        float d, dmin = 0.0f;
+        if constexpr (T == T_Q2_K) {
+            const uint8_t* blk = block_ptr<84>(row, b);
+            ld_words<4>(blk, sw);
+            ld_words<16>(blk + 16, qw);
+            uint32_t dd[1];
+            ld_words<1>(blk + 80, dd);
+            d = half_bits_to_float(dd[0] & 0xffffu);
+            dmin = half_bits_to_float(dd[0] >> 16);
+        } else {
+            using L = Planar<T_Q3_K>;
+            ld_words<16>(field_ptr<L::QS, 64>(row, b), qw);
+            ld_words<8>(field_ptr<L::HM, 32>(row, b), hw);
+            uint32_t p3[3];
+            ld_words<3>(field_ptr<L::SC, 12>(row, b), p3);
+#pragma unroll
+            for (uint32_t j = 0; j < 4; ++j) {  // the 16 unpacked 6-bit scales, 4 per word
+                sw[j] = q3k_scale(p3, 4u * j) | (q3k_scale(p3, 4u * j + 1u) << 8) |
+                        (q3k_scale(p3, 4u * j + 2u) << 16) | (q3k_scale(p3, 4u * j + 3u) << 24);
+            }
+            d = half_bits_to_float(ld_u16(field_ptr<L::D, 2>(row, b)));
+        }
+#pragma unroll
+        for (uint32_t g = 0; g < 16; ++g) {  // 16-element groups in element order
+            const uint32_t h = g / 8u, sh = (g % 8u) / 2u, t = g % 2u;
+            const uint32_t scb = (sw[g / 4u] >> (8u * (g % 4u))) & 0xffu;
+            float mul, off;
+            if constexpr (T == T_Q2_K) {
+                mul = __fmul_rn(d, static_cast<float>(scb & 15u));
+                off = __fmul_rn(dmin, static_cast<float>(scb >> 4));
+            } else {
+                mul = __fmul_rn(d, static_cast<float>(static_cast<int>(scb) - 32));
+                off = 0.0f;
+            }
+#pragma unroll
+            for (uint32_t k = 0; k < 4; ++k) {
+                const uint32_t qv = qw[(32u * h + 16u * t) / 4u + k];
+                const float4 xv = x4[4u * g + k];
+                const float xs[4] = {xv.x, xv.y, xv.z, xv.w};
+#pragma unroll
+                for (uint32_t j = 0; j < 4; ++j) {
+                    const uint32_t q = (qv >> (8u * j + 2u * sh)) & 3u;
+                    float w;
+                    if constexpr (T == T_Q2_K) {
+                        w = __fsub_rn(__fmul_rn(mul, static_cast<float>(q)), off);
+                    } else {
+                        const uint32_t hb = (hw[(16u * t) / 4u + k] >> (8u * j + 4u * h + sh)) & 1u;
+                        w = __fmul_rn(mul, static_cast<float>(static_cast<int>(q) - (hb ? 0 : 4)));
+                    }
+                    s = __fadd_rn(s, __fmul_rn(w, xs[j]));
+                }
+            }
         }
     } else {  // Q4_0: low nibbles are elements 0..15, high 16..31
         using L = Planar<T_Q4_0>;
@@ -729,7 +835,10 @@ __global__ __launch_bounds__(256) void k_ref_attention(ModelArgs a, ModelLayer L
 }
 
 uint32_t ref_block_elems(uint32_t type) {
-    return type == T_Q8_0 || type == T_Q4_0 || type == T_Q4_1 ? 32u : 256u;
+    return type == T_Q8_0 || type == T_Q4_0 || type == T_Q4_1 || type == T_Q5_0 ||
+                   type == T_Q5_1
+               ? 32u
+               : 256u;
 }
 
 template <int T>
@@ -749,6 +858,10 @@ hipError_t ref_matvec_launch(uint32_t type, const RefMatvecArgs& a, uint32_t blo
         case T_Q8_0: return ref_matvec_t<T_Q8_0>(a, blocks, routes, s);
         case T_Q4_0: return ref_matvec_t<T_Q4_0>(a, blocks, routes, s);
         case T_Q4_1: return ref_matvec_t<T_Q4_1>(a, blocks, routes, s);
+        case T_Q5_0: return ref_matvec_t<T_Q5_0>(a, blocks, routes, s);
+        case T_Q5_1: return ref_matvec_t<T_Q5_1>(a, blocks, routes, s);
+        case T_Q2_K: return ref_matvec_t<T_Q2_K>(a, blocks, routes, s);
+        case T_Q3_K: return ref_matvec_t<T_Q3_K>(a, blocks, routes, s);
         default: return hipErrorInvalidValue;
     }
 }
@@ -758,9 +871,10 @@ hipError_t ref_matvec_launch(uint32_t type, const RefMatvecArgs& a, uint32_t blo
 bool ref_matvec_supported(uint32_t type, uint32_t in) {
     switch (type) {
         case T_F32: return in >= 1u && in <= kMaxRefWidth;
-        case T_Q4_K: case T_Q5_K: case T_Q6_K:
+        case T_Q2_K: case T_Q3_K: case T_Q4_K: case T_Q5_K: case T_Q6_K:
             return in % 256u == 0u && in <= kMaxRefWidth && in / 256u <= 256u;
-        case T_Q8_0: case T_Q4_0: case T_Q4_1: return in % 32u == 0u && in <= kMaxRefWidth && in / 32u <= 256u;
+        case T_Q8_0: case T_Q4_0: case T_Q4_1: case T_Q5_0: case T_Q5_1:
+            return in % 32u == 0u && in <= kMaxRefWidth && in / 32u <= 256u;
         default: return false;
     }
 }

@@ -20,8 +20,8 @@
 namespace pk {
 
 enum : uint32_t {
-    T_F32 = 0, T_F16 = 1, T_Q4_0 = 2, T_Q4_1 = 3, T_Q8_0 = 8, T_Q4_K = 12, T_Q5_K = 13, T_Q6_K = 14,
-    T_BF16 = 30
+    T_F32 = 0, T_F16 = 1, T_Q4_0 = 2, T_Q4_1 = 3, T_Q5_0 = 6, T_Q5_1 = 7, T_Q8_0 = 8, T_Q2_K = 10,
+    T_Q3_K = 11, T_Q4_K = 12, T_Q5_K = 13, T_Q6_K = 14, T_BF16 = 30
 };
 
 template <int T> struct Fmt;
@@ -33,12 +33,18 @@ template <> struct Fmt<T_Q6_K> { static constexpr int BE = 256, BB = 210, PRIM =
 template <> struct Fmt<T_Q8_0> { static constexpr int BE = 32, BB = 34, PRIM = 32, RUNS = 1, MAXUB = 16; };
 template <> struct Fmt<T_Q4_0> { static constexpr int BE = 32, BB = 18, PRIM = 16, RUNS = 2, MAXUB = 16; };
 template <> struct Fmt<T_Q4_1> { static constexpr int BE = 32, BB = 20, PRIM = 16, RUNS = 2, MAXUB = 16; };
+template <> struct Fmt<T_Q5_0> { static constexpr int BE = 32, BB = 22, PRIM = 16, RUNS = 2, MAXUB = 16; };
+template <> struct Fmt<T_Q5_1> { static constexpr int BE = 32, BB = 24, PRIM = 16, RUNS = 2, MAXUB = 16; };
+// Q2_K / Q3_K: a quant byte holds four 2-bit fields, one per shift pair, so
+// a unit of UB quant bytes covers four runs of UB elements.
+template <> struct Fmt<T_Q2_K> { static constexpr int BE = 256, BB = 84, PRIM = 64, RUNS = 4, MAXUB = 16; };
+template <> struct Fmt<T_Q3_K> { static constexpr int BE = 256, BB = 110, PRIM = 64, RUNS = 4, MAXUB = 16; };
 
 // ---------------------------------------------------------------------------
-// Loads.  Q4_K/Q5_K blocks (144/176 B) keep 16-byte alignment; Q6_K (210 B),
-// Q8_0 (34 B) and Q4_0 (18 B) only keep 2-byte alignment, so their fields are
-// fetched as dword-aligned words and re-aligned with v_alignbyte.  Buffers
-// handed to the kernels carry at least 16 readable bytes past the payload.
+// Loads.  Q4_K/Q5_K blocks (144/176 B) keep 16-byte alignment and Q4_1,
+// Q5_1 and Q2_K (20/24/84 B) 4-byte alignment: they are read in GGUF form.
+// Q6_K, Q8_0, Q4_0, Q5_0 and Q3_K only keep 2-byte alignment and are held in
+// the planar layout of layout.hpp, each field an aligned load.
 
 template <int N>
 __device__ __forceinline__ void ld_words(const uint8_t* p, uint32_t (&w)[N]) {
@@ -73,18 +79,6 @@ template <int N>
 __device__ __forceinline__ void ld_weights(const uint8_t* p, uint32_t (&w)[N]) {
     if constexpr (PK_WEIGHT_NT) ld_words_nt<N>(p, w);
     else ld_words<N>(p, w);
-}
-
-// The dword-aligned address below p is formed by pointer subtraction (not by
-// masking an integer), so the compiler keeps the global address space and
-// emits global loads.
-template <int N>
-__device__ __forceinline__ void ld_words_2a(const uint8_t* p, uint32_t (&w)[N]) {
-    const uint32_t shift = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(p) & 3u);
-    uint32_t raw[N + 1];
-    ld_words<N + 1>(p - shift, raw);
-#pragma unroll
-    for (int i = 0; i < N; ++i) w[i] = __builtin_amdgcn_alignbyte(raw[i + 1], raw[i], shift);
 }
 
 __device__ __forceinline__ float half_bits_to_float(uint32_t bits16) {
@@ -128,6 +122,23 @@ __device__ __forceinline__ void kq_scale_min(const uint32_t (&h)[4], uint32_t j,
     m = static_cast<float>(j < 4 ? m_lo : m_hi);
 }
 
+// Bits 0..3 of b to bit 4 of bytes 0..3 (the Q5_0/Q5_1 fifth bits).
+__device__ __forceinline__ uint32_t spread4(uint32_t b) {
+    return ((b & 1u) << 4) | ((b & 2u) << 11) | ((b & 4u) << 18) | ((b & 8u) << 25);
+}
+
+// 6-bit scale j of a Q3_K block from its 12 packed bytes (words w[0..2]): the
+// low nibble in byte j (j < 8) or in the high nibble of byte j - 8, the top two
+// bits at bits 2 * (j / 4) of byte 8 + j % 4 (decode_q3_k,
+// src/quantized_linear.cpp:127-139).
+__device__ __forceinline__ uint32_t q3k_scale(const uint32_t (&w)[3], uint32_t j) {
+    const uint32_t jl = j & 7u;
+    const uint32_t lob = (w[jl / 4u] >> (8u * (jl % 4u))) & 0xffu;
+    const uint32_t lo = j < 8u ? lob & 15u : lob >> 4;
+    const uint32_t hib = (w[2] >> (8u * (j % 4u))) & 0xffu;
+    return lo | (((hib >> (2u * (j / 4u))) & 3u) << 4);
+}
+
 // ---------------------------------------------------------------------------
 // Unit geometry.  Unit u of a row: block b = u / UPB, unit j = u % UPB inside
 // the block, primary byte offset k0 = j * UB.  col[r] is the activation column
@@ -136,7 +147,7 @@ __device__ __forceinline__ void kq_scale_min(const uint32_t (&h)[4], uint32_t j,
 struct UnitPos {
     uint32_t b;       // block index inside the row
     uint32_t k0;      // primary-stream byte offset inside the block
-    uint32_t col[2];  // activation column of run 0 / run 1
+    uint32_t col[4];  // activation column of the first element of each run
 };
 
 template <int T, int UB>
@@ -158,7 +169,12 @@ __device__ __forceinline__ UnitPos unit_pos(uint32_t u) {
     } else if constexpr (T == T_Q8_0) {
         p.col[0] = base + k0;
         p.col[1] = p.col[0];
-    } else {  // Q4_0, Q4_1: low nibbles are elements 0..15, high nibbles 16..31
+    } else if constexpr (T == T_Q2_K || T == T_Q3_K) {
+        // quant byte 32h + 16t + i holds element 128h + 32s + 16t + i at bits 2s
+        const uint32_t h = k0 / 32u, t = (k0 % 32u) / 16u;
+#pragma unroll
+        for (uint32_t s = 0; s < 4; ++s) p.col[s] = base + 128u * h + 32u * s + 16u * t + (k0 % 16u);
+    } else {  // Q4_0, Q4_1, Q5_0, Q5_1: low nibbles are elements 0..15, high nibbles 16..31
         p.col[0] = base + k0;
         p.col[1] = p.col[0] + 16u;
     }
@@ -205,13 +221,18 @@ __device__ __forceinline__ void load_unit_x(const float* x, uint32_t x_stride, c
 template <int T, int UB>
 struct UnitRaw {
     static constexpr int NW = UB / 4;
-    // Q4_K/Q5_K/Q4_1: h = block header; q = quants; qh = Q5_K fifth bits.
-    // Q6_K/Q8_0/Q4_0 (planar): q = quants, qh = Q6_K high bits, sc = the two
-    // Q6_K scale dwords of the unit's half block, d = fp16 bits of d.
-    uint32_t h[(T == T_Q4_K || T == T_Q5_K) ? 4 : 1];
+    // h: Q4_K/Q5_K block header; Q4_1/Q5_1 d | m << 16; Q2_K d | dmin << 16.
+    // q: the unit's quant bytes.  qh: Q5_K fifth bits, Q6_K high bits, Q3_K
+    // hmask bytes (per unit byte), Q5_0/Q5_1 the block's 32-bit qh.  sc: Q6_K
+    // scale dwords of the half block, Q2_K scale/min bytes 8h..8h+7, Q3_K the
+    // 12 packed scale bytes.  d: fp16 bits of d (Q6_K, Q8_0, Q4_0, Q5_0, Q3_K).
+    static constexpr int NH = (T == T_Q4_K || T == T_Q5_K) ? 4 : 1;
+    static constexpr int NQH = (T == T_Q5_K || T == T_Q6_K || T == T_Q3_K) ? NW : 1;
+    static constexpr int NSC = T == T_Q3_K ? 3 : (T == T_Q6_K || T == T_Q2_K) ? 2 : 1;
+    uint32_t h[NH];
     uint32_t q[NW];
-    uint32_t qh[(T == T_Q5_K || T == T_Q6_K) ? NW : 1];
-    uint32_t sc[T == T_Q6_K ? 2 : 1];
+    uint32_t qh[NQH];
+    uint32_t sc[NSC];
     uint32_t d;
 };
 
@@ -239,6 +260,27 @@ __device__ __forceinline__ void unit_load(const QRow& r, const UnitPos& p, UnitR
     } else if constexpr (T == T_Q8_0) {
         using L = Planar<T_Q8_0>;
         ld_weights<NW>(field_ptr<L::QS, 32>(r, p.b) + p.k0, u.q);
+        u.d = ld_u16(field_ptr<L::D, 2>(r, p.b));
+    } else if constexpr (T == T_Q5_0) {
+        using L = Planar<T_Q5_0>;
+        ld_weights<NW>(field_ptr<L::QS, 16>(r, p.b) + p.k0, u.q);
+        ld_weights<1>(field_ptr<L::QH, 4>(r, p.b), u.qh);
+        u.d = ld_u16(field_ptr<L::D, 2>(r, p.b));
+    } else if constexpr (T == T_Q5_1) {  // 24-byte blocks: d, m, qh, quants
+        const uint8_t* blk = block_ptr<24>(r, p.b);
+        ld_weights<1>(blk, u.h);
+        ld_weights<1>(blk + 4, u.qh);
+        ld_weights<NW>(blk + 8 + p.k0, u.q);
+    } else if constexpr (T == T_Q2_K) {  // 84-byte blocks: scales[16], qs[64], d, dmin
+        const uint8_t* blk = block_ptr<84>(r, p.b);
+        ld_weights<NW>(blk + 16 + p.k0, u.q);
+        ld_weights<2>(blk + 8u * (p.k0 / 32u), u.sc);
+        ld_weights<1>(blk + 80, u.h);
+    } else if constexpr (T == T_Q3_K) {
+        using L = Planar<T_Q3_K>;
+        ld_weights<NW>(field_ptr<L::QS, 64>(r, p.b) + p.k0, u.q);
+        ld_weights<NW>(field_ptr<L::HM, 32>(r, p.b) + (p.k0 % 32u), u.qh);
+        ld_weights<3>(field_ptr<L::SC, 12>(r, p.b), u.sc);
         u.d = ld_u16(field_ptr<L::D, 2>(r, p.b));
     } else {  // Q4_0
         using L = Planar<T_Q4_0>;
@@ -319,6 +361,82 @@ __device__ __forceinline__ void unit_compute(const UnitRaw<T, UB>& r, const Unit
         const float d = half_bits_to_float(r.d);
 #pragma unroll
         for (int b = 0; b < B; ++b) acc[b] += d * __builtin_fmaf(-128.0f, ux.s[b][0], dot0[b]);
+    } else if constexpr (T == T_Q5_0 || T == T_Q5_1) {
+        // 5-bit q = nibble | qh bit << 4 (qh bit j for element j of the block):
+        // Q5_0 w = (q - 16) * d (decode_q5_0, src/quantized_linear.cpp:64-77),
+        // Q5_1 w = q * d + m (decode_q5_1, :79-93)
+#pragma unroll
+        for (int t = 0; t < NW; ++t) {
+            const uint32_t bl = (r.qh[0] >> (p.k0 + 4u * t)) & 0xfu;
+            const uint32_t bh = (r.qh[0] >> (16u + p.k0 + 4u * t)) & 0xfu;
+            const uint32_t lo = (r.q[t] & 0x0f0f0f0fu) | spread4(bl);
+            const uint32_t hi = ((r.q[t] >> 4) & 0x0f0f0f0fu) | spread4(bh);
+#pragma unroll
+            for (int b = 0; b < B; ++b) {
+                dot0[b] = dot4(lo, &ux.v[b][4 * t], dot0[b]);
+                dot1[b] = dot4(hi, &ux.v[b][UB + 4 * t], dot1[b]);
+            }
+        }
+        if constexpr (T == T_Q5_0) {
+            const float d = half_bits_to_float(r.d);
+#pragma unroll
+            for (int b = 0; b < B; ++b) {
+                const float t0 = __builtin_fmaf(-16.0f, ux.s[b][0], dot0[b]);
+                const float t1 = __builtin_fmaf(-16.0f, ux.s[b][1], dot1[b]);
+                acc[b] += d * (t0 + t1);
+            }
+        } else {
+            const float d = half_bits_to_float(r.h[0] & 0xffffu);
+            const float m = half_bits_to_float(r.h[0] >> 16);
+#pragma unroll
+            for (int b = 0; b < B; ++b)
+                acc[b] += __builtin_fmaf(d, dot0[b] + dot1[b], m * (ux.s[b][0] + ux.s[b][1]));
+        }
+    } else if constexpr (T == T_Q2_K || T == T_Q3_K) {
+        // run s: the 2-bit fields at bits 2s of the unit's quant bytes, scale
+        // group g = 8h + 2s + t.  Q2_K w = dl * q - ml with dl = d * (sc & 15),
+        // ml = dmin * (sc >> 4) (decode_q2_k, src/quantized_linear.cpp:95-121);
+        // Q3_K w = d * (scale - 32) * (q + 4 * hbit - 4) with the hmask bit
+        // 4h + s (decode_q3_k, :123-164).
+        const uint32_t h = p.k0 / 32u, tt = (p.k0 % 32u) / 16u;
+        float dots[4][B];
+#pragma unroll
+        for (int s4 = 0; s4 < 4; ++s4)
+#pragma unroll
+            for (int b = 0; b < B; ++b) dots[s4][b] = 0.0f;
+#pragma unroll
+        for (int t = 0; t < NW; ++t) {
+#pragma unroll
+            for (int s4 = 0; s4 < 4; ++s4) {
+                uint32_t v = (r.q[t] >> (2 * s4)) & 0x03030303u;
+                if constexpr (T == T_Q3_K) v |= ((r.qh[t] >> (4u * h + s4)) & 0x01010101u) << 2;
+#pragma unroll
+                for (int b = 0; b < B; ++b) dots[s4][b] = dot4(v, &ux.v[b][s4 * UB + 4 * t], dots[s4][b]);
+            }
+        }
+        if constexpr (T == T_Q2_K) {
+            const float d = half_bits_to_float(r.h[0] & 0xffffu);
+            const float dmin = half_bits_to_float(r.h[0] >> 16);
+#pragma unroll
+            for (int s4 = 0; s4 < 4; ++s4) {
+                const uint32_t sb = 2u * s4 + tt;  // byte of the 8 loaded (group g = 8h + sb)
+                const uint32_t scb = (r.sc[sb / 4u] >> (8u * (sb % 4u))) & 0xffu;
+                const float dl = d * static_cast<float>(scb & 15u);
+                const float ml = dmin * static_cast<float>(scb >> 4);
+#pragma unroll
+                for (int b = 0; b < B; ++b) acc[b] += __builtin_fmaf(dl, dots[s4][b], -ml * ux.s[b][s4]);
+            }
+        } else {
+            const float d = half_bits_to_float(r.d);
+#pragma unroll
+            for (int s4 = 0; s4 < 4; ++s4) {
+                const uint32_t g = 8u * h + 2u * s4 + tt;
+                const float ds = d * static_cast<float>(static_cast<int>(q3k_scale(r.sc, g)) - 32);
+#pragma unroll
+                for (int b = 0; b < B; ++b)
+                    acc[b] += ds * __builtin_fmaf(-4.0f, ux.s[b][s4], dots[s4][b]);
+            }
+        }
     } else if constexpr (T == T_Q4_1) {  // w = d * q + m (decode_q4_1, src/quantized_linear.cpp:53-62)
 #pragma unroll
         for (int t = 0; t < NW; ++t) {

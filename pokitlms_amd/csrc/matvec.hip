@@ -171,9 +171,12 @@ template <int T>
 constexpr int block_elems() { return Fmt<T>::BE; }
 
 // Unit bytes per lane by batch: activations held per unit are RUNS*UB*B
-// floats, kept at <= 64 by narrowing the unit as the batch grows.
-constexpr int unit_bytes_for(uint32_t batch, int maxub) {
-    return batch <= 2 ? (maxub < 16 ? maxub : 16) : (batch <= 4 ? 8 : 4);
+// floats, kept at <= 64 by narrowing the unit as the batch grows (four-run
+// formats at the 4-byte minimum hold up to 128 for batches above 4).
+constexpr int unit_bytes_for(uint32_t batch, int maxub, int runs) {
+    const int cap = maxub < 16 ? maxub : 16;
+    if (runs <= 2) return batch <= 2 ? cap : (batch <= 4 ? 8 : 4);
+    return batch <= 1 ? cap : (batch <= 2 ? 8 : 4);
 }
 
 constexpr uint32_t kMaxUnitsPerLane = 2;
@@ -247,7 +250,7 @@ hipError_t dispatch_nu(const Plan& pl, const uint8_t* W, uint32_t nb, uint32_t r
 template <int T, int B>
 hipError_t dispatch_q(const uint8_t* W, uint64_t rb, uint32_t rows, const float* x,
                       uint32_t in, float* y, hipStream_t s) {
-    constexpr int UB = unit_bytes_for(B, Fmt<T>::MAXUB);
+    constexpr int UB = unit_bytes_for(B, Fmt<T>::MAXUB, Fmt<T>::RUNS);
     Plan pl;
     if (!plan_for<T>(in, B, UB, pl)) return hipErrorInvalidValue;
     (void)rb;
@@ -290,8 +293,7 @@ hipError_t dispatch_batch_f(uint32_t batch, const uint8_t* W, uint64_t rb, uint3
 template <int T>
 bool supported_q(uint32_t in, uint32_t batch) {
     Plan pl;
-    const int ub = batch <= 2 ? (Fmt<T>::MAXUB < 16 ? Fmt<T>::MAXUB : 16) : (batch <= 4 ? 8 : 4);
-    return plan_for<T>(in, batch, ub, pl);
+    return plan_for<T>(in, batch, unit_bytes_for(batch, Fmt<T>::MAXUB, Fmt<T>::RUNS), pl);
 }
 
 }  // namespace
@@ -302,6 +304,10 @@ bool matvec_supported(uint32_t type, uint32_t in, uint32_t batch) {
         case T_F32: case T_F16: case T_BF16: return true;
         case T_Q4_0: return supported_q<T_Q4_0>(in, batch);
         case T_Q4_1: return supported_q<T_Q4_1>(in, batch);
+        case T_Q5_0: return supported_q<T_Q5_0>(in, batch);
+        case T_Q5_1: return supported_q<T_Q5_1>(in, batch);
+        case T_Q2_K: return supported_q<T_Q2_K>(in, batch);
+        case T_Q3_K: return supported_q<T_Q3_K>(in, batch);
         case T_Q8_0: return supported_q<T_Q8_0>(in, batch);
         case T_Q4_K: return supported_q<T_Q4_K>(in, batch);
         case T_Q5_K: return supported_q<T_Q5_K>(in, batch);
@@ -320,6 +326,10 @@ hipError_t launch_matvec(uint32_t type, const uint8_t* W, uint64_t row_bytes, ui
         case T_BF16: return dispatch_batch_f<T_BF16>(batch, W, row_bytes, rows, x, in, y, stream);
         case T_Q4_0: return dispatch_batch_q<T_Q4_0>(batch, W, row_bytes, rows, x, in, y, stream);
         case T_Q4_1: return dispatch_batch_q<T_Q4_1>(batch, W, row_bytes, rows, x, in, y, stream);
+        case T_Q5_0: return dispatch_batch_q<T_Q5_0>(batch, W, row_bytes, rows, x, in, y, stream);
+        case T_Q5_1: return dispatch_batch_q<T_Q5_1>(batch, W, row_bytes, rows, x, in, y, stream);
+        case T_Q2_K: return dispatch_batch_q<T_Q2_K>(batch, W, row_bytes, rows, x, in, y, stream);
+        case T_Q3_K: return dispatch_batch_q<T_Q3_K>(batch, W, row_bytes, rows, x, in, y, stream);
         case T_Q8_0: return dispatch_batch_q<T_Q8_0>(batch, W, row_bytes, rows, x, in, y, stream);
         case T_Q4_K: return dispatch_batch_q<T_Q4_K>(batch, W, row_bytes, rows, x, in, y, stream);
         case T_Q5_K: return dispatch_batch_q<T_Q5_K>(batch, W, row_bytes, rows, x, in, y, stream);

@@ -142,6 +142,61 @@ __device__ void decode32(const QRow& row, uint32_t k0, float* v) {
             const int q = static_cast<int>(nib | (((qh[i] >> (2u * g)) & 3u) << 4)) - 32;
             v[i] = __fmul_rn(__fmul_rn(d, static_cast<float>(s)), static_cast<float>(q));
         }
+    } else if constexpr (T == T_Q5_0 || T == T_Q5_1) {  // decode_q5_0 / q5_1 (:64-93)
+        const uint8_t* qs;
+        uint32_t qh;
+        float d, m = 0.0f;
+        if constexpr (T == T_Q5_0) {
+            using L = Planar<T_Q5_0>;
+            qs = field_ptr<L::QS, 16>(row, k0 / 32u);
+            qh = *reinterpret_cast<const uint32_t*>(field_ptr<L::QH, 4>(row, k0 / 32u));
+            d = half_bits_to_float(ld_u16(field_ptr<L::D, 2>(row, k0 / 32u)));
+        } else {
+            const uint8_t* blk = block_ptr<24>(row, k0 / 32u);
+            d = half_bits_to_float(blk[0] | (blk[1] << 8));
+            m = half_bits_to_float(blk[2] | (blk[3] << 8));
+            qh = *reinterpret_cast<const uint32_t*>(blk + 4);
+            qs = blk + 8;
+        }
+        for (uint32_t i = 0; i < 16; ++i) {
+            const uint32_t q0 = (qs[i] & 15u) | (((qh >> i) & 1u) << 4);
+            const uint32_t q1 = (qs[i] >> 4) | (((qh >> (i + 16u)) & 1u) << 4);
+            if constexpr (T == T_Q5_0) {
+                v[i] = __fmul_rn(static_cast<float>(static_cast<int>(q0) - 16), d);
+                v[i + 16] = __fmul_rn(static_cast<float>(static_cast<int>(q1) - 16), d);
+            } else {
+                v[i] = __fadd_rn(__fmul_rn(static_cast<float>(q0), d), m);
+                v[i + 16] = __fadd_rn(__fmul_rn(static_cast<float>(q1), d), m);
+            }
+        }
+    } else if constexpr (T == T_Q2_K || T == T_Q3_K) {  // decode_q2_k / q3_k (:95-164)
+        const uint32_t b = k0 / 256u, c = (k0 % 256u) / 32u;  // elements 32c .. 32c + 31
+        const uint32_t h = c / 4u, sh = c % 4u;               // groups 2c, 2c + 1 (t = 0, 1)
+        for (uint32_t i = 0; i < 32; ++i) {
+            const uint32_t t = i / 16u, l = i % 16u, g = 2u * c + t;
+            if constexpr (T == T_Q2_K) {
+                const uint8_t* blk = block_ptr<84>(row, b);
+                const float d = half_bits_to_float(blk[80] | (blk[81] << 8));
+                const float dmin = half_bits_to_float(blk[82] | (blk[83] << 8));
+                const uint32_t q = (blk[16u + 32u * h + 16u * t + l] >> (2u * sh)) & 3u;
+                const float dl = __fmul_rn(d, static_cast<float>(blk[g] & 15u));
+                const float ml = __fmul_rn(dmin, static_cast<float>(blk[g] >> 4));
+                v[i] = __fsub_rn(__fmul_rn(dl, static_cast<float>(q)), ml);
+            } else {
+                using L = Planar<T_Q3_K>;
+                const uint8_t* qs = field_ptr<L::QS, 64>(row, b);
+                const uint8_t* hm = field_ptr<L::HM, 32>(row, b);
+                const uint8_t* ps = field_ptr<L::SC, 12>(row, b);
+                const uint32_t pw[3] = {*reinterpret_cast<const uint32_t*>(ps),
+                                        *reinterpret_cast<const uint32_t*>(ps + 4),
+                                        *reinterpret_cast<const uint32_t*>(ps + 8)};
+                const float d = half_bits_to_float(ld_u16(field_ptr<L::D, 2>(row, b)));
+                const uint32_t q = (qs[32u * h + 16u * t + l] >> (2u * sh)) & 3u;
+                const uint32_t hb = (hm[16u * t + l] >> (4u * h + sh)) & 1u;
+                const float ds = __fmul_rn(d, static_cast<float>(static_cast<int>(q3k_scale(pw, g)) - 32));
+                v[i] = __fmul_rn(ds, static_cast<float>(static_cast<int>(q) - (hb ? 0 : 4)));
+            }
+        }
     } else if constexpr (T == T_Q8_0) {
         using L = Planar<T_Q8_0>;
         const uint8_t* qs = field_ptr<L::QS, 32>(row, k0 / 32u);
@@ -300,10 +355,12 @@ hipError_t embed_t(const ModelArgs& a, hipStream_t s) {
 }  // namespace
 
 bool model_supported(const ModelArgs& a) {
-    // the matvec types (the reference also dequantizes Q5_0/Q5_1/Q2_K/Q3_K rows)
+    // every type dequantize_quantized_row and read_float_rows_into take
     const bool embd_ok = a.embd_type == T_F32 || a.embd_type == T_F16 || a.embd_type == T_BF16 ||
-                         a.embd_type == T_Q4_K || a.embd_type == T_Q5_K || a.embd_type == T_Q6_K ||
-                         a.embd_type == T_Q8_0 || a.embd_type == T_Q4_0 || a.embd_type == T_Q4_1;
+                         a.embd_type == T_Q2_K || a.embd_type == T_Q3_K || a.embd_type == T_Q4_K ||
+                         a.embd_type == T_Q5_K || a.embd_type == T_Q6_K || a.embd_type == T_Q8_0 ||
+                         a.embd_type == T_Q4_0 || a.embd_type == T_Q4_1 || a.embd_type == T_Q5_0 ||
+                         a.embd_type == T_Q5_1;
     return embd_ok && a.head_dim >= 2u && a.head_dim <= 256u && a.head_dim % 64u == 0u &&
            a.kv_heads >= 1u && a.heads % a.kv_heads == 0u && a.hidden % 256u == 0u &&
            a.capacity >= 1u && a.capacity <= kMaxModelContext;
@@ -331,6 +388,10 @@ hipError_t launch_model_step(const ModelArgs& a, const ModelLayer* layers, bool 
         case T_F16: err = embed_t<T_F16>(a, s); break;
         case T_BF16: err = embed_t<T_BF16>(a, s); break;
         case T_Q4_1: err = embed_t<T_Q4_1>(a, s); break;
+        case T_Q5_0: err = embed_t<T_Q5_0>(a, s); break;
+        case T_Q5_1: err = embed_t<T_Q5_1>(a, s); break;
+        case T_Q2_K: err = embed_t<T_Q2_K>(a, s); break;
+        case T_Q3_K: err = embed_t<T_Q3_K>(a, s); break;
         case T_Q4_K: err = embed_t<T_Q4_K>(a, s); break;
         case T_Q5_K: err = embed_t<T_Q5_K>(a, s); break;
         case T_Q6_K: err = embed_t<T_Q6_K>(a, s); break;

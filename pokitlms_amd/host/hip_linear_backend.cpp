@@ -37,7 +37,11 @@ std::size_t encoded_row_bytes(std::uint32_t type, std::uint64_t in) {
         case 1: case 30: return in * 2;
         case 2: return in % 32 ? 0 : in / 32 * 18;
         case 3: return in % 32 ? 0 : in / 32 * 20;
+        case 6: return in % 32 ? 0 : in / 32 * 22;
+        case 7: return in % 32 ? 0 : in / 32 * 24;
         case 8: return in % 32 ? 0 : in / 32 * 34;
+        case 10: return in % 256 ? 0 : in / 256 * 84;
+        case 11: return in % 256 ? 0 : in / 256 * 110;
         case 12: return in % 256 ? 0 : in / 256 * 144;
         case 13: return in % 256 ? 0 : in / 256 * 176;
         case 14: return in % 256 ? 0 : in / 256 * 210;
@@ -47,8 +51,8 @@ std::size_t encoded_row_bytes(std::uint32_t type, std::uint64_t in) {
 
 bool block_aligned(std::uint32_t type, std::uint64_t in) {
     switch (type) {
-        case 2: case 3: case 8: return in % 32 == 0;
-        case 12: case 13: case 14: return in % 256 == 0;
+        case 2: case 3: case 6: case 7: case 8: return in % 32 == 0;
+        case 10: case 11: case 12: case 13: case 14: return in % 256 == 0;
         default: return true;
     }
 }
@@ -323,7 +327,8 @@ HipLinearStats HipLinearBackend::stats() const {
         out.q4_k_dispatches = s.q4_k_dispatches;
         out.q5_k_dispatches = s.q5_k_dispatches;
         out.q6_k_dispatches = s.q6_k_dispatches;
-        out.other_dispatches = s.float_dispatches + s.q4_1_dispatches;
+        out.other_dispatches = s.float_dispatches + s.q4_1_dispatches + s.q5_0_dispatches +
+                               s.q5_1_dispatches + s.q2_k_dispatches + s.q3_k_dispatches;
         out.weight_bytes = s.weight_bytes;
         out.gpu_time_ns = s.matvec_ns + s.router_ns + s.gate_up_ns + s.down_ns;
         out.resident_bytes = s.resident_bytes;

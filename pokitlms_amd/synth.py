@@ -18,17 +18,21 @@ import hashlib
 import numpy as np
 
 F32, F16, Q4_0, Q4_1, Q8_0, Q4_K, Q5_K, Q6_K, BF16 = 0, 1, 2, 3, 8, 12, 13, 14, 30
+Q5_0, Q5_1, Q2_K, Q3_K = 6, 7, 10, 11
 
-TYPE_NAMES = {F32: "F32", F16: "F16", Q4_0: "Q4_0", Q4_1: "Q4_1", Q8_0: "Q8_0", Q4_K: "Q4_K",
-              Q5_K: "Q5_K", Q6_K: "Q6_K", BF16: "BF16"}
-BLOCK_ELEMENTS = {F32: 1, F16: 1, BF16: 1, Q4_0: 32, Q4_1: 32, Q8_0: 32, Q4_K: 256, Q5_K: 256,
-                  Q6_K: 256}
-BLOCK_BYTES = {F32: 4, F16: 2, BF16: 2, Q4_0: 18, Q4_1: 20, Q8_0: 34, Q4_K: 144, Q5_K: 176,
-               Q6_K: 210}
+TYPE_NAMES = {F32: "F32", F16: "F16", Q4_0: "Q4_0", Q4_1: "Q4_1", Q5_0: "Q5_0", Q5_1: "Q5_1",
+              Q8_0: "Q8_0", Q2_K: "Q2_K", Q3_K: "Q3_K", Q4_K: "Q4_K", Q5_K: "Q5_K",
+              Q6_K: "Q6_K", BF16: "BF16"}
+BLOCK_ELEMENTS = {F32: 1, F16: 1, BF16: 1, Q4_0: 32, Q4_1: 32, Q5_0: 32, Q5_1: 32, Q8_0: 32,
+                  Q2_K: 256, Q3_K: 256, Q4_K: 256, Q5_K: 256, Q6_K: 256}
+BLOCK_BYTES = {F32: 4, F16: 2, BF16: 2, Q4_0: 18, Q4_1: 20, Q5_0: 22, Q5_1: 24, Q8_0: 34,
+               Q2_K: 84, Q3_K: 110, Q4_K: 144, Q5_K: 176, Q6_K: 210}
 # Byte offsets of the fp16 scale fields inside one block.
-SCALE_OFFSETS = {Q4_0: (0,), Q4_1: (0, 2), Q8_0: (0,), Q4_K: (0, 2), Q5_K: (0, 2), Q6_K: (208,)}
-# Scale fields stored negative: Q4_1's m is the block minimum, w = q * d + m.
-NEGATIVE_SCALES = {Q4_1: (2,)}
+SCALE_OFFSETS = {Q4_0: (0,), Q4_1: (0, 2), Q5_0: (0,), Q5_1: (0, 2), Q8_0: (0,),
+                 Q2_K: (80, 82), Q3_K: (108,), Q4_K: (0, 2), Q5_K: (0, 2), Q6_K: (208,)}
+# Scale fields stored negative: Q4_1's and Q5_1's m is the block minimum,
+# w = q * d + m.
+NEGATIVE_SCALES = {Q4_1: (2,), Q5_1: (2,)}
 
 
 def rng(seed: int) -> np.random.Generator:
@@ -184,6 +188,8 @@ def dyadic_matrix(gtype: int, rows: int, in_features: int, gen: np.random.Genera
                               .astype(np.int8).view(np.uint8))
     if gtype in (Q4_K, Q5_K):
         blocks[:, 4:16] &= 0x0F
+    if gtype == Q3_K:  # every 6-bit scale 32 + low nibble: scale - 32 in [0, 15]
+        blocks[:, 104:108] = 0xAA
     return m
 
 

@@ -97,7 +97,8 @@ def main():
             ys = np.stack([ref.linear(t, w, inn, rows, xs[b]) for b in range(8)])
             out[key + "_ysum"] = np.array(S.digest(ys))
 
-    for t in (S.F32, S.F16, S.BF16, S.Q4_0, S.Q4_1, S.Q8_0, S.Q4_K, S.Q5_K, S.Q6_K):
+    for t in (S.F32, S.F16, S.BF16, S.Q4_0, S.Q4_1, S.Q8_0, S.Q4_K, S.Q5_K, S.Q6_K,
+              S.Q5_0, S.Q5_1, S.Q2_K, S.Q3_K):
         w, x, inn = small_inputs(t)
         key = f"small_{S.TYPE_NAMES[t]}"
         out[key + "_digest"] = np.array(S.digest(w, x))

@@ -199,7 +199,8 @@ Errors compare(const std::vector<float>& got, const std::vector<float>& want) {
 
 void linear_cases(HipLinearBackend& hip) {
     Rng g(0x5eed0001);
-    for (const std::uint32_t type : {0U, 1U, 30U, 2U, 3U, 8U, 12U, 13U, 14U}) {
+    // every type tensor_linear dispatches (src/tensor_linear.cpp:162-188)
+    for (const std::uint32_t type : {0U, 1U, 30U, 2U, 3U, 6U, 7U, 8U, 10U, 11U, 12U, 13U, 14U}) {
         const std::size_t in = block_elements(type) == 1 ? 257 : 512, rows = 37;
         const auto reader = memory_reader(type, rows, in, make_matrix(type, rows, in, g));
         std::vector<float> x(in), cpu(rows), gpu(rows);
@@ -225,32 +226,27 @@ void linear_cases(HipLinearBackend& hip) {
 }
 
 void unsupported_cases(HipLinearBackend& hip) {
-    // Types the reference CPU path handles and the HIP kernels do not (nor
-    // the Vulkan backend's): Q5_0, Q5_1, Q2_K, Q3_K.  try_linear returns
-    // false, so tensor_linear's CPU result comes out unchanged.
+    // A GGUF type without a kernel here (Q8_K, 15; tensor_linear's own type
+    // gate rejects it too, src/tensor_linear.cpp:205-211): try_linear answers
+    // false and counts it, as the Vulkan backend does for types outside its
+    // list (src/vulkan_linear.cpp:615).
     Rng g(0x5eed0002);
-    for (const std::uint32_t type : {6U, 7U, 10U, 11U}) {
-        const std::size_t in = 512, rows = 37;
-        const auto reader = memory_reader(type, rows, in, make_matrix(type, rows, in, g));
-        std::vector<float> x(in), cpu(rows), hooked(rows);
-        for (auto& v : x) v = g.normal(1.0F);
-        pokitlms::model::TensorLinearScratch scratch;
-        scratch.backend = &hip;
-        const auto before = hip.stats();
-        bool direct = true;
-        try {
-            direct = hip.try_linear(reader, x, hooked);
-        } catch (const std::exception&) {
-            direct = true;
-        }
-        pokitlms::model::tensor_linear(reader, x, cpu);
-        pokitlms::model::tensor_linear(reader, x, hooked, 0, &scratch);
-        const auto after = hip.stats();
-        const bool ok = !direct && std::memcmp(cpu.data(), hooked.data(), rows * 4) == 0 &&
-                        after.linear_calls == before.linear_calls &&
-                        after.unsupported_calls == before.unsupported_calls + 2;
-        report(ok, "try_linear_unsupported", "type=" + std::to_string(type));
+    const std::size_t in = 256, rows = 4;
+    std::vector<std::byte> bytes(rows * 292);
+    for (auto& b : bytes) b = static_cast<std::byte>(g.next() & 0xff);
+    const auto reader = memory_reader(15, rows, in, std::move(bytes));
+    std::vector<float> x(in, 1.0F), y(rows, 0.0F);
+    const auto before = hip.stats();
+    bool direct = true;
+    try {
+        direct = hip.try_linear(reader, x, y);
+    } catch (const std::exception&) {
+        direct = true;
     }
+    const auto after = hip.stats();
+    const bool ok = !direct && after.linear_calls == before.linear_calls &&
+                    after.unsupported_calls == before.unsupported_calls + 1;
+    report(ok, "try_linear_unsupported", "type=15");
 }
 
 template <typename E, typename F>

@@ -31,10 +31,10 @@ def test_library_exports_every_declared_symbol():
 def test_version_and_type_table():
     lib = _abi.lib()
     assert lib.pk_hip_version() == b"0.1.0"
-    # the Vulkan backend's list (src/vulkan_linear.cpp:78-83)
-    for t in (0, 1, 2, 3, 8, 12, 13, 14, 30):
+    # every type tensor_linear dispatches (src/tensor_linear.cpp:176-187)
+    for t in (0, 1, 2, 3, 6, 7, 8, 10, 11, 12, 13, 14, 30):
         assert lib.pk_hip_type_supported(t) == 1
-    for t in (6, 7, 10, 11, 15, 16, 99):
+    for t in (4, 5, 9, 15, 16, 99):
         assert lib.pk_hip_type_supported(t) == 0
 
 

@@ -134,7 +134,8 @@ def test_generation_is_repeatable_and_validated(hip):
             model.generate(np.array([m.vocab], np.uint32), 2)
 
 
-@pytest.mark.parametrize("embd_type", (S.F16, S.BF16, S.Q4_1, S.Q8_0, S.Q5_K))
+@pytest.mark.parametrize("embd_type", (S.F16, S.BF16, S.Q4_1, S.Q8_0, S.Q5_K, S.Q5_0, S.Q5_1,
+                                       S.Q2_K, S.Q3_K))
 def test_embedding_row_types(hip, port, embd_type):
     """The token embedding decodes to the reference's FP32 row
     (read_float_rows_into for F16/BF16, dequantize_quantized_row otherwise,

@@ -16,6 +16,8 @@ from tests.golden import make_golden as G
 pytestmark = pytest.mark.gpu
 
 QUANT = (S.Q4_0, S.Q4_1, S.Q8_0, S.Q4_K, S.Q5_K, S.Q6_K)
+# the other formats tensor_linear dispatches (src/tensor_linear.cpp:176-187)
+QUANT_MORE = (S.Q5_0, S.Q5_1, S.Q2_K, S.Q3_K)
 FLOAT = (S.F32, S.F16, S.BF16)
 TOL = 1e-4
 
@@ -30,7 +32,7 @@ def say(*a):
 
 # ---- matvec -------------------------------------------------------------------------
 
-@pytest.mark.parametrize("gtype", FLOAT + QUANT)
+@pytest.mark.parametrize("gtype", FLOAT + QUANT + QUANT_MORE)
 def test_reference_harness_shapes(hip, port, gtype):
     """37 rows x 512 (257 for floats) of xorshift-style random bytes with the
     harness's fixed scales, three rounds with x *= -0.75
@@ -54,8 +56,8 @@ def test_reference_harness_shapes(hip, port, gtype):
     wt.release()
 
 
-@pytest.mark.parametrize("gtype", QUANT)
-@pytest.mark.parametrize("batch", (1, 4, 8))
+@pytest.mark.parametrize("gtype", QUANT + QUANT_MORE)
+@pytest.mark.parametrize("batch", (1, 2, 4, 8))
 def test_dyadic_bit_exact(hip, port, gtype, batch):
     say("dyadic", S.TYPE_NAMES[gtype], batch)
     g = S.rng(500 + gtype * 10 + batch)
@@ -115,6 +117,29 @@ def test_reference_order_matvec_bit_exact(hip, golden, gtype, shape):
     wt.release()
 
 
+@pytest.mark.parametrize("gtype", QUANT_MORE)
+def test_more_formats_against_the_reference(hip, port, golden, gtype):
+    """Q5_0, Q5_1, Q2_K and Q3_K on the reference harness shape: the fast
+    matvec within 1e-4 normwise of the compiled reference's vector, the
+    reference-order matvec equal to it bit for bit, and random 2048-wide rows
+    at batch 1/3/8 within 1e-4 of the oracle."""
+    w, x, inn = G.small_inputs(gtype)
+    key = f"small_{S.TYPE_NAMES[gtype]}"
+    wt = hip.upload(gtype, inn, 37, w)
+    assert normwise_rel(hip.matvec(wt, x), golden[key + "_y"]) <= TOL
+    assert np.array_equal(bits(hip.matvec_reference_order(wt, x)), bits(golden[key + "_y"]))
+    wt.release()
+    g = S.rng(80 + gtype)
+    w = S.quant_matrix(gtype, 300, 2048, g)
+    xs = np.stack([S.normal_f32(g, 2048) for _ in range(8)])
+    wt = hip.upload(gtype, 2048, 300, w)
+    for batch in (1, 3, 8):
+        gpu = hip.matvec(wt, xs[:batch])
+        for b in range(batch):
+            assert normwise_rel(gpu[b], port.linear(gtype, w, 2048, 300, xs[b])) <= TOL, (batch, b)
+    wt.release()
+
+
 def test_reference_order_router_and_c1(hip, port, golden):
     w, x = G.c1_inputs()
     wt = hip.upload(S.Q4_K, 4096, 4096, w)
@@ -165,7 +190,7 @@ def test_expert_slice_matvec(hip, port):
         wt.release()
 
 
-@pytest.mark.parametrize("gtype", FLOAT + QUANT)
+@pytest.mark.parametrize("gtype", FLOAT + QUANT + QUANT_MORE)
 @pytest.mark.parametrize("rows,experts", ((37, 0), (37, 3), (5, 2)))
 def test_weight_layout_round_trip(hip, gtype, rows, experts):
     """Q4_0, Q8_0 and Q6_K sit in HBM as per-slice field planes (odd slice
@@ -188,8 +213,8 @@ def test_try_linear_contract(hip, port):
     y = np.zeros(64, np.float32)
     assert hip.try_linear(TensorView(S.Q4_K, (512, 64), w), x, y)
     assert normwise_rel(y, port.linear(S.Q4_K, w, 512, 64, x)) <= TOL
-    # Q2_K (10) has no kernel: False, so the caller runs its CPU path
-    assert not hip.try_linear(TensorView(10, (512, 64), np.zeros(64 * 168, np.uint8)), x, y)
+    # Q8_K (15) has no kernel: False, so the caller runs its CPU path
+    assert not hip.try_linear(TensorView(15, (512, 64), np.zeros(64 * 584, np.uint8)), x, y)
     with pytest.raises(ValueError):
         hip.try_linear(TensorView(S.Q4_K, (512, 64), w), x[:256], y)
 

@@ -3,8 +3,9 @@ call sites: tests/native/hip_backend_cases.cpp, built by ``make -C oracle
 cases`` against the reference headers and CPU library in place.
 
 On the GPU it runs every case: try_linear through tensor_linear's backend hook
-(src/tensor_linear.cpp:213) for F32/F16/BF16/Q4_0/Q4_1/Q8_0/Q4_K/Q5_K/Q6_K against
-the CPU kernels; false for the formats without a kernel; shape errors;
+(src/tensor_linear.cpp:213) for every type tensor_linear dispatches (F32/F16/BF16/
+Q4_0/Q4_1/Q5_0/Q5_1/Q8_0/Q2_K/Q3_K/Q4_K/Q5_K/Q6_K) against the CPU kernels; false
+for a GGUF type without a kernel (Q8_K); shape errors;
 file-backed tensors kept resident; the MoE block hook against the reference
 MoE block and the Qwen3.5 block with its shared expert (ids exact, outputs
 normwise <= 1e-4); a non-finite router as a
@@ -45,7 +46,7 @@ def test_native_backend_cases():
     assert r.returncode == 0, r.stdout[-3000:]
     lines = r.stdout.splitlines()
     assert not [l for l in lines if l.startswith("FAIL")]
-    assert sum(l.startswith("PASS try_linear_parity") for l in lines) == 9
-    assert sum(l.startswith("PASS try_linear_unsupported") for l in lines) == 4
+    assert sum(l.startswith("PASS try_linear_parity") for l in lines) == 13
+    assert sum(l.startswith("PASS try_linear_unsupported") for l in lines) == 1
     assert sum(l.startswith("PASS moe_block_parity") for l in lines) == 2
     assert sum(l.startswith("PASS moe35_block_parity") for l in lines) == 1

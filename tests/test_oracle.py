@@ -17,6 +17,8 @@ from tests import blocks as KB
 from tests.golden import make_golden as G
 
 QUANT = (S.Q4_0, S.Q4_1, S.Q8_0, S.Q4_K, S.Q5_K, S.Q6_K)
+# the remaining formats tensor_linear dispatches (src/tensor_linear.cpp:179-183)
+QUANT_MORE = (S.Q5_0, S.Q5_1, S.Q2_K, S.Q3_K)
 
 
 def bits(a):
@@ -58,6 +60,20 @@ def test_q5_k_reference_known_answers(port):
     _check_block(port, S.Q5_K, blk, exp)
 
 
+def test_q3_k_reference_known_answers(port):
+    # tests/regression_test.cpp:47-53: an all-zero block with d = 1 decodes to
+    # (0 - 32) * (0 - 4) = 128 everywhere
+    blk = bytearray(110)
+    blk[108:110] = np.array([1.0], np.float16).view(np.uint8).tobytes()
+    _check_block(port, S.Q3_K, bytes(blk), np.full(256, 128.0))
+    # :55-71: d = 0.5, scale (7g + 11) % 64, quant (5e + g) % 8 - 4
+    sc = [(g * 7 + 11) % 64 - 32 for g in range(16)]
+    q = [(e * 5 + e // 16) % 8 - 4 for e in range(256)]
+    blk, exp = KB.q3_k_block(0.5, sc, q)
+    assert np.array_equal(exp, [0.5 * sc[e // 16] * q[e] for e in range(256)])
+    _check_block(port, S.Q3_K, blk, exp)
+
+
 @pytest.mark.parametrize("seed", range(4))
 def test_known_answer_blocks(port, seed):
     g = S.rng(900 + seed)
@@ -72,6 +88,12 @@ def test_known_answer_blocks(port, seed):
     _check_block(port, S.Q8_0, *KB.q8_0_block(d, g.integers(-128, 128, 32)))
     _check_block(port, S.Q4_0, *KB.q4_0_block(d, g.integers(-8, 8, 32)))
     _check_block(port, S.Q4_1, *KB.q4_1_block(d, -dmin, g.integers(0, 16, 32)))
+    _check_block(port, S.Q5_0, *KB.q5_0_block(d, g.integers(-16, 16, 32)))
+    _check_block(port, S.Q5_1, *KB.q5_1_block(d, -dmin, g.integers(0, 32, 32)))
+    _check_block(port, S.Q2_K, *KB.q2_k_block(d, dmin, g.integers(0, 16, 16),
+                                               g.integers(0, 16, 16), g.integers(0, 4, 256)))
+    _check_block(port, S.Q3_K, *KB.q3_k_block(d, g.integers(-32, 32, 16),
+                                               g.integers(-4, 4, 256)))
 
 
 def test_planted_mistake_is_caught():
@@ -113,18 +135,18 @@ def test_golden_c2(port, golden, gtype, shape):
     assert S.digest(ys) == str(golden[key + "_ysum"])
 
 
-@pytest.mark.parametrize("gtype", (S.F32, S.F16, S.BF16) + QUANT)
+@pytest.mark.parametrize("gtype", (S.F32, S.F16, S.BF16) + QUANT + QUANT_MORE)
 def test_golden_small(port, golden, gtype):
     w, x, inn = G.small_inputs(gtype)
     key = f"small_{S.TYPE_NAMES[gtype]}"
     assert S.digest(w, x) == str(golden[key + "_digest"])
     assert np.array_equal(bits(port.linear(gtype, w, inn, 37, x)), bits(golden[key + "_y"]))
-    if gtype in QUANT:
+    if gtype in QUANT + QUANT_MORE:
         assert np.array_equal(bits(port.dequantize_row(gtype, w[0], inn)),
                               bits(golden[key + "_row0"]))
 
 
-@pytest.mark.parametrize("gtype", QUANT)
+@pytest.mark.parametrize("gtype", QUANT + QUANT_MORE)
 def test_dyadic_exact_matvec(port, gtype):
     """Power-of-two scales and k/16 activations: the oracle's serial sum must
     equal the exact value (float64 of the decoded weights)."""
