@@ -355,6 +355,30 @@ pk_hip_status pk_hip_synth_weight(pk_hip_ctx* ctx, uint32_t ggml_type, uint64_t 
                                   pk_hip_weight** out_weight, char* error_buffer,
                                   size_t error_capacity);
 
+/* Rows [first_row, first_row + rows) of a resident weight as FP32 into host
+ * memory (rows * in floats; expert selects a slice of an expert tensor,
+ * UINT32_MAX for a plain matrix): TensorReader::read_float_rows_into for
+ * F32/F16/BF16 (src/tensor_reader.cpp:164-198) and dequantize_quantized_row
+ * for the quantized types (src/quantized_linear.cpp:427-493), bit for bit; the
+ * device decode the embedding row and the kernels' scales use. */
+pk_hip_status pk_hip_dequantize_rows(pk_hip_ctx* ctx, const pk_hip_weight* weight,
+                                     uint32_t expert, uint64_t first_row, uint32_t rows,
+                                     float* out, char* error_buffer, size_t error_capacity);
+
+/* Checksums of the reference-order decode's expf (no counterpart in the
+ * reference; it pins the device side of the host libm's expf, which the
+ * reference calls in the softmax and SwiGLU, src/kv_cache.cpp:249,
+ * src/qwen3_moe_runner.cpp:683): the exponential in double rounded once to
+ * float, replaced from the (input bits, result bits) pairs as
+ * pk_hip_qwen3moe_config.libm_expf_pairs.  Block k covers the float bit
+ * patterns b = first_bits + k * block_size + i, i < block_size, and sums[k] =
+ * sum over i of (((uint64) result_bits << 32) | b) * 0xD6E8FEB86659FD93 mod
+ * 2^64, so a host evaluating its libm the same way compares n_blocks words. */
+pk_hip_status pk_hip_expf_block_sums(pk_hip_ctx* ctx, const uint32_t* libm_expf_pairs,
+                                     uint64_t pair_count, uint32_t first_bits,
+                                     uint32_t block_size, uint32_t n_blocks, uint64_t* sums,
+                                     char* error_buffer, size_t error_capacity);
+
 /* Waits for the context's work (and `stream`, if not NULL) and reports any
  * deferred router error. */
 pk_hip_status pk_hip_sync(pk_hip_ctx* ctx, void* stream, char* error_buffer,

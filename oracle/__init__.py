@@ -68,6 +68,9 @@ class Oracle:
         if kind == "port":
             L.pko_half_to_float.restype = ctypes.c_float
             L.pko_half_to_float.argtypes = [ctypes.c_uint16]
+            L.pko_expf_block_sums.argtypes = [ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32,
+                                              ctypes.c_void_p, ctypes.c_uint32]
+            L.pko_expf_block_sums.restype = None
             L.pko_linear.argtypes = [ctypes.c_uint32, _u8p, ctypes.c_uint64, ctypes.c_uint64,
                                      ctypes.c_uint64, _f32p, _f32p]
             L.pko_dequantize_row.argtypes = [ctypes.c_uint32, _u8p, ctypes.c_uint64, _f32p,
@@ -121,6 +124,13 @@ class Oracle:
                 ctypes.POINTER(ctypes.c_double)]
 
     # ---- single ops -------------------------------------------------------
+    def expf_block_sums(self, first_bits: int, block_size: int, n_blocks: int,
+                        threads: int = 16) -> np.ndarray:
+        """The host libm's expf as block checksums (pko_expf_block_sums)."""
+        out = np.empty(n_blocks, dtype=np.uint64)
+        self.lib.pko_expf_block_sums(first_bits, block_size, n_blocks, out.ctypes.data, threads)
+        return out
+
     def half_to_float(self, bits: int) -> float:
         if self.kind != "port":
             raise NotImplementedError("half_to_float is exported by the port only")

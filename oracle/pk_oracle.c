@@ -15,6 +15,7 @@
 
 #include <math.h>
 #include <stdlib.h>
+#include <pthread.h>
 #include <string.h>
 
 uint32_t pko_block_elements(uint32_t type) {
@@ -594,4 +595,50 @@ done:
     free(act);
     free(out);
     return rc;
+}
+
+
+/* ---- the host libm's expf as block checksums ---------------------------------- */
+
+typedef struct {
+    uint32_t first_bits, block_size, k0, k1;
+    uint64_t* sums;
+} ExpfJob;
+
+static void* expf_job(void* arg) {
+    const ExpfJob* j = (const ExpfJob*)arg;
+    for (uint32_t k = j->k0; k < j->k1; ++k) {
+        uint64_t acc = 0;
+        const uint32_t base = j->first_bits + k * j->block_size;
+        for (uint32_t i = 0; i < j->block_size; ++i) {
+            const uint32_t b = base + i;
+            float x, r;
+            memcpy(&x, &b, 4);
+            r = expf(x);
+            uint32_t rb;
+            memcpy(&rb, &r, 4);
+            acc += (((uint64_t)rb << 32) | b) * 0xD6E8FEB86659FD93ull;
+        }
+        j->sums[k] = acc;
+    }
+    return NULL;
+}
+
+void pko_expf_block_sums(uint32_t first_bits, uint32_t block_size, uint32_t n_blocks,
+                         uint64_t* sums, uint32_t threads) {
+    if (threads == 0) threads = 1;
+    if (threads > 64) threads = 64;
+    pthread_t th[64];
+    int created[64] = {0};
+    ExpfJob jobs[64];
+    const uint32_t per = (n_blocks + threads - 1) / threads;
+    for (uint32_t t = 0; t < threads; ++t) {
+        const uint32_t k0 = t * per, k1 = k0 + per < n_blocks ? k0 + per : n_blocks;
+        if (k0 >= k1) break;
+        jobs[t] = (ExpfJob){first_bits, block_size, k0, k1, sums};
+        created[t] = pthread_create(&th[t], NULL, expf_job, &jobs[t]) == 0;
+        if (!created[t]) expf_job(&jobs[t]);  /* inline when a thread cannot start */
+    }
+    for (uint32_t t = 0; t < threads; ++t)
+        if (created[t]) pthread_join(th[t], NULL);
 }

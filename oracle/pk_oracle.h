@@ -109,6 +109,16 @@ int pko_moe35_block(const float* router, uint32_t hidden, uint32_t n_experts, ui
                     const uint8_t* sup, uint32_t sdown_type, const uint8_t* sdown,
                     const float* x, float* y, uint32_t* ids, float* weights);
 
+/* The host libm's expf over float bit patterns, as block checksums: block k
+ * covers b = first_bits + k * block_size + i (i < block_size) and sums[k] =
+ * sum over i of (((uint64) bits(expf(x_b)) << 32) | b) * 0xD6E8FEB86659FD93
+ * mod 2^64 (the device's pk_hip_expf_block_sums computes the same over its
+ * expf).  The reference calls this libm's expf in the softmax and SwiGLU
+ * (src/kv_cache.cpp:249, src/qwen3_moe_runner.cpp:683).  threads > 0 splits
+ * the blocks over that many threads. */
+void pko_expf_block_sums(uint32_t first_bits, uint32_t block_size, uint32_t n_blocks,
+                         uint64_t* sums, uint32_t threads);
+
 #ifdef __cplusplus
 }
 #endif

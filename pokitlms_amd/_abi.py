@@ -31,7 +31,8 @@ EXPORTS = (
     "pk_hip_moe35_prefill", "pk_hip_moe35_prefill_async",
     "pk_hip_moe_prefill_async", "pk_hip_qwen3moe_create", "pk_hip_qwen3moe_destroy",
     "pk_hip_qwen3moe_generate", "pk_hip_synth_weight", "pk_hip_matvec_reference_order",
-    "pk_hip_weight_download", "pk_hip_moe_decode_noalloc",
+    "pk_hip_weight_download", "pk_hip_moe_decode_noalloc", "pk_hip_dequantize_rows",
+    "pk_hip_expf_block_sums",
 )
 
 
@@ -123,6 +124,12 @@ def lib() -> ctypes.CDLL:
     L.pk_hip_weight_bytes.argtypes = [vp]
     L.pk_hip_weight_device_ptr.restype = vp
     L.pk_hip_weight_device_ptr.argtypes = [vp]
+    L.pk_hip_dequantize_rows.restype = ctypes.c_int
+    L.pk_hip_dequantize_rows.argtypes = [vp, vp, ctypes.c_uint32, u64, ctypes.c_uint32, vp,
+                                         ctypes.c_char_p, ctypes.c_size_t]
+    L.pk_hip_expf_block_sums.restype = ctypes.c_int
+    L.pk_hip_expf_block_sums.argtypes = [vp, vp, u64, ctypes.c_uint32, ctypes.c_uint32,
+                                         ctypes.c_uint32, vp, ctypes.c_char_p, ctypes.c_size_t]
     L.pk_hip_weight_download.restype = ctypes.c_int
     L.pk_hip_weight_download.argtypes = [vp, vp, u64, ctypes.c_char_p, ctypes.c_size_t]
     L.pk_hip_matvec.restype = ctypes.c_int

@@ -315,6 +315,31 @@ class HipBackend:
                                                   device_x, device_y, device_ids, device_probs,
                                                   stream or None, err, _ERRBUF), err)
 
+    def dequantize_rows(self, w: Weight, first_row: int = 0, rows: int | None = None,
+                        expert: int | None = None) -> np.ndarray:
+        """Rows of a resident weight as FP32 (the reference's
+        read_float_rows_into / dequantize_quantized_row)."""
+        rows = w.out_features - first_row if rows is None else rows
+        out = np.empty((rows, w.in_features), dtype=np.float32)
+        err = ctypes.create_string_buffer(_ERRBUF)
+        _raise(_abi.lib().pk_hip_dequantize_rows(self.handle, w.handle,
+                                                 _abi.NO_EXPERT if expert is None else expert,
+                                                 first_row, rows, out.ctypes.data, err, _ERRBUF),
+               err)
+        return out
+
+    def expf_block_sums(self, pairs: np.ndarray, first_bits: int, block_size: int,
+                        n_blocks: int) -> np.ndarray:
+        """Checksums of the reference-order expf over float bit patterns
+        (see pk_hip_expf_block_sums)."""
+        p = np.ascontiguousarray(pairs, dtype=np.uint32).reshape(-1)
+        out = np.empty(n_blocks, dtype=np.uint64)
+        err = ctypes.create_string_buffer(_ERRBUF)
+        _raise(_abi.lib().pk_hip_expf_block_sums(self.handle, p.ctypes.data if p.size else None,
+                                                 p.size // 2, first_bits, block_size, n_blocks,
+                                                 out.ctypes.data, err, _ERRBUF), err)
+        return out
+
     def moe_decode_noalloc(self, layer: MoeLayerHandles, device_x: int, device_y: int,
                            device_ids: int, device_probs: int, stream: int = 0) -> None:
         """moe_decode_async on the library's static device scratch (no device

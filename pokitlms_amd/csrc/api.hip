@@ -1563,6 +1563,80 @@ pk_hip_status pk_hip_synth_weight(pk_hip_ctx* ctx, uint32_t type, uint64_t in, u
     });
 }
 
+pk_hip_status pk_hip_dequantize_rows(pk_hip_ctx* ctx, const pk_hip_weight* w, uint32_t expert,
+                                     uint64_t first_row, uint32_t rows, float* out, char* err,
+                                     size_t cap) {
+    return guarded(ctx, err, cap, [&] {
+        require_usable(ctx);
+        if (!w || !out) throw ArgError("weight and output are required");
+        if (w->ctx != ctx) throw ArgError("weight handle does not belong to this context");
+        if (rows == 0) return;
+        if (first_row > w->out || rows > w->out - first_row) throw ArgError("rows out of range");
+        uint64_t offset = 0;
+        if (expert != UINT32_MAX) {
+            if (w->n_experts == 0 || expert >= w->n_experts) throw ArgError("expert index out of range");
+            offset = static_cast<uint64_t>(expert) * w->slice_pitch;
+        } else if (w->n_experts) {
+            throw ArgError("an expert tensor needs an expert index");
+        }
+        if (w->in > 0xffffffffull || !pk::dequant_rows_supported(w->type, static_cast<uint32_t>(w->in)))
+            throw Unsupported("row decoding not covered for this type/width");
+        std::lock_guard lock(ctx->mutex);
+        ctx->set_device();
+        const size_t n = static_cast<size_t>(rows) * w->in;
+        ctx->y.ensure(n);
+        launch_checked(pk::launch_dequant_rows(w->type, w->dptr + offset, w->out,
+                                               static_cast<uint32_t>(w->in), first_row, rows,
+                                               ctx->y.ptr, ctx->stream),
+                       "row decode launch");
+        check(hipMemcpyAsync(out, ctx->y.ptr, n * sizeof(float), hipMemcpyDeviceToHost, ctx->stream),
+              "copy rows");
+        check(hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
+    });
+}
+
+pk_hip_status pk_hip_expf_block_sums(pk_hip_ctx* ctx, const uint32_t* pairs, uint64_t count,
+                                     uint32_t first_bits, uint32_t block_size, uint32_t n_blocks,
+                                     uint64_t* sums, char* err, size_t cap) {
+    return guarded(ctx, err, cap, [&] {
+        require_usable(ctx);
+        if (!sums || (count && !pairs)) throw ArgError("output and pairs are required");
+        if (block_size == 0 || n_blocks == 0) return;
+        if (static_cast<uint64_t>(first_bits) + static_cast<uint64_t>(block_size) * n_blocks > (1ull << 32))
+            throw ArgError("input bit patterns past 0xffffffff");
+        std::lock_guard lock(ctx->mutex);
+        ctx->set_device();
+        pk::LibmExpf t{nullptr, 0, 0, 0};
+        DeviceBuffer<uint32_t> slots;
+        DeviceBuffer<unsigned long long> dsums;
+        try {
+            if (count) {
+                std::vector<uint32_t> host;
+                t = build_expf_cuckoo(pairs, count, host);
+                slots.ensure(host.size());
+                check(hipMemcpy(slots.ptr, host.data(), host.size() * 4, hipMemcpyHostToDevice),
+                      "copy expf table");
+                t.slots = slots.ptr;
+            }
+            dsums.ensure(n_blocks);
+            check(pk::launch_expf_block_sums(t, first_bits, block_size, n_blocks, dsums.ptr,
+                                             ctx->stream),
+                  "expf launch");
+            check(hipMemcpyAsync(sums, dsums.ptr, n_blocks * sizeof(uint64_t), hipMemcpyDeviceToHost,
+                                 ctx->stream),
+                  "copy sums");
+            check(hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
+        } catch (...) {
+            (void)hipStreamSynchronize(ctx->stream);
+            slots.release();
+            dsums.release();
+            throw;
+        }
+        slots.release();
+        dsums.release();
+    });
+}
+
 pk_hip_status pk_hip_get_stats(const pk_hip_ctx* ctx, pk_hip_stats* out) {
     if (!ctx || !out) return PK_HIP_STATUS_INVALID_ARGUMENT;
     std::lock_guard lock(ctx->mutex);

@@ -1036,4 +1036,34 @@ hipError_t launch_ref_step(const ModelArgs& a, const ModelLayer* layers, bool lo
     return launch_ref_matvec(a.out_type, h, 1, s);
 }
 
+namespace {
+
+__global__ __launch_bounds__(256) void k_expf_block_sums(LibmExpf t, uint32_t first_bits,
+                                                         uint32_t block_size,
+                                                         unsigned long long* sums) {
+    const uint32_t base = first_bits + blockIdx.x * block_size;
+    unsigned long long acc = 0;
+    for (uint32_t i = threadIdx.x; i < block_size; i += 256u) {
+        const uint32_t b = base + i;
+        const uint32_t r = __float_as_uint(expf_libm(__uint_as_float(b), t));
+        acc += ((static_cast<unsigned long long>(r) << 32) | b) * 0xD6E8FEB86659FD93ull;
+    }
+    __shared__ unsigned long long part[4];
+    // wave sums with integer shuffles (order-independent: addition mod 2^64)
+    for (int off = 32; off > 0; off >>= 1) acc += __shfl_xor(acc, off, 64);
+    if ((threadIdx.x & 63u) == 0) part[threadIdx.x >> 6] = acc;
+    __syncthreads();
+    if (threadIdx.x == 0) sums[blockIdx.x] = part[0] + part[1] + part[2] + part[3];
+}
+
+}  // namespace
+
+hipError_t launch_expf_block_sums(const LibmExpf& t, uint32_t first_bits, uint32_t block_size,
+                                  uint32_t n_blocks, unsigned long long* sums, hipStream_t s) {
+    if (n_blocks == 0) return hipSuccess;
+    hipLaunchKernelGGL(k_expf_block_sums, dim3(n_blocks), dim3(256), 0, s, t, first_bits,
+                       block_size, sums);
+    return hipGetLastError();
+}
+
 }  // namespace pk

@@ -156,6 +156,20 @@ bool model_supported(const ModelArgs& a);
 hipError_t launch_model_step(const ModelArgs& a, const ModelLayer* layers, bool logits,
                              hipStream_t stream);
 
+// Rows [first_row, first_row + rows) of a slice (rows_in_slice rows of `in`
+// elements) as FP32, decoded exactly as the embedding row (every type the
+// embedding takes): out is rows * in floats (device).
+bool dequant_rows_supported(uint32_t type, uint32_t in);
+hipError_t launch_dequant_rows(uint32_t type, const uint8_t* slice, uint64_t rows_in_slice,
+                               uint32_t in, uint64_t first_row, uint32_t rows, float* out,
+                               hipStream_t stream);
+
+// Checksums of the reference-order expf over float bit patterns: block k
+// covers patterns first_bits + k * block_size + i (i < block_size) and sums
+// (uint64) ((result bits << 32) | input bits) * 0xD6E8FEB86659FD93 mod 2^64.
+hipError_t launch_expf_block_sums(const LibmExpf& t, uint32_t first_bits, uint32_t block_size,
+                                  uint32_t n_blocks, unsigned long long* sums, hipStream_t stream);
+
 // Seeded synthetic weight bytes (see pokitlms_amd/synth_model.py): kind 0 raw,
 // 1 K-quant scale fix-up (block_bytes 144/176), 2 Q6_K, 3 F32 norm, 4 F32 router.
 hipError_t launch_synth_fill(uint8_t* dst, uint64_t nbytes, uint64_t key, uint32_t kind,

@@ -354,6 +354,64 @@ hipError_t embed_t(const ModelArgs& a, hipStream_t s) {
 
 }  // namespace
 
+namespace {
+
+// One thread per 32 consecutive elements of the requested rows.
+template <int T>
+__global__ __launch_bounds__(256) void k_dequant_rows(const uint8_t* __restrict__ slice,
+                                                      uint64_t rows_in_slice, uint32_t in,
+                                                      uint64_t first_row, uint32_t rows,
+                                                      float* __restrict__ out) {
+    const uint64_t chunks = static_cast<uint64_t>(rows) * (in / 32u);
+    uint32_t nb = in;
+    if constexpr (!(T == T_F32 || T == T_F16 || T == T_BF16)) nb = in / Fmt<T>::BE;
+    for (uint64_t k = blockIdx.x * 256ull + threadIdx.x; k < chunks;
+         k += static_cast<uint64_t>(gridDim.x) * 256u) {
+        const uint64_t r = k / (in / 32u), c = k % (in / 32u);
+        const QRow row{slice, rows_in_slice * nb, (first_row + r) * nb};
+        float v[32];
+        decode32<T>(row, 32u * static_cast<uint32_t>(c), v);
+        float* o = out + r * in + 32u * c;
+        for (uint32_t i = 0; i < 32; ++i) o[i] = v[i];
+    }
+}
+
+template <int T>
+hipError_t dequant_t(const uint8_t* slice, uint64_t rows_in_slice, uint32_t in, uint64_t first_row,
+                     uint32_t rows, float* out, hipStream_t s) {
+    const uint64_t chunks = static_cast<uint64_t>(rows) * (in / 32u);
+    const uint32_t blocks = static_cast<uint32_t>(chunks / 256u + 1u < 4096u ? chunks / 256u + 1u : 4096u);
+    hipLaunchKernelGGL(k_dequant_rows<T>, dim3(blocks), dim3(256), 0, s, slice, rows_in_slice, in,
+                       first_row, rows, out);
+    return hipGetLastError();
+}
+
+}  // namespace
+
+bool dequant_rows_supported(uint32_t type, uint32_t in) {
+    if (in == 0 || in % 32u) return false;
+    switch (type) {
+        case T_F32: case T_F16: case T_BF16: case T_Q4_0: case T_Q4_1: case T_Q5_0: case T_Q5_1:
+        case T_Q8_0: return true;
+        case T_Q2_K: case T_Q3_K: case T_Q4_K: case T_Q5_K: case T_Q6_K: return in % 256u == 0;
+        default: return false;
+    }
+}
+
+hipError_t launch_dequant_rows(uint32_t type, const uint8_t* slice, uint64_t rows_in_slice,
+                               uint32_t in, uint64_t first_row, uint32_t rows, float* out,
+                               hipStream_t s) {
+    if (!dequant_rows_supported(type, in)) return hipErrorInvalidValue;
+    switch (type) {
+#define PK_DQ(TT) case TT: return dequant_t<TT>(slice, rows_in_slice, in, first_row, rows, out, s);
+        PK_DQ(T_F32) PK_DQ(T_F16) PK_DQ(T_BF16) PK_DQ(T_Q4_0) PK_DQ(T_Q4_1) PK_DQ(T_Q5_0)
+        PK_DQ(T_Q5_1) PK_DQ(T_Q8_0) PK_DQ(T_Q2_K) PK_DQ(T_Q3_K) PK_DQ(T_Q4_K) PK_DQ(T_Q5_K)
+        PK_DQ(T_Q6_K)
+#undef PK_DQ
+        default: return hipErrorInvalidValue;
+    }
+}
+
 bool model_supported(const ModelArgs& a) {
     // every type dequantize_quantized_row and read_float_rows_into take
     const bool embd_ok = a.embd_type == T_F32 || a.embd_type == T_F16 || a.embd_type == T_BF16 ||
