@@ -186,7 +186,8 @@ pk_hip_status pk_hip_moe_decode(pk_hip_ctx* ctx, const pk_hip_moe_layer* layer, 
                                 size_t error_capacity);
 
 /* Device-buffer variant, enqueued on `stream` without synchronising.  A
- * router error is reported by the next pk_hip_sync. */
+ * router error is reported by the next pk_hip_sync.  Scratch and stream
+ * capture as for pk_hip_moe_prefill_async. */
 pk_hip_status pk_hip_moe_decode_async(pk_hip_ctx* ctx, const pk_hip_moe_layer* layer,
                                       const float* device_x, float* device_y,
                                       uint32_t* device_ids, float* device_probs, void* stream,
@@ -254,8 +255,13 @@ pk_hip_status pk_hip_moe_prefill(pk_hip_ctx* ctx, const pk_hip_moe_layer* layer,
                                  char* error_buffer, size_t error_capacity);
 
 /* Device-buffer variant, enqueued on `stream` without synchronising.  The
- * first call for a given batch shape allocates scratch; capture it into a
- * HIP graph only after one such call. */
+ * first call for a given batch shape allocates the context's scratch; capture
+ * it into a HIP graph only after one such call: a call under stream capture
+ * that would need more scratch returns INVALID_ARGUMENT.  When a later call
+ * needs more, the context allocates anew and keeps the old scratch until
+ * pk_hip_destroy, so graphs captured earlier stay valid.  Every *_async call
+ * on one context shares that scratch: enqueue them on one stream (or order
+ * them yourself), as a replayed graph uses the scratch it captured. */
 pk_hip_status pk_hip_moe_prefill_async(pk_hip_ctx* ctx, const pk_hip_moe_layer* layer,
                                        const float* device_x, uint32_t tokens, float* device_y,
                                        uint32_t* device_ids, float* device_probs, void* stream,

@@ -72,23 +72,49 @@ uint32_t block_bytes(uint32_t t) {
     }
 }
 
+// Set while an entry point enqueues onto a stream that is being captured:
+// scratch may not grow then (an allocation would not be part of the graph).
+thread_local bool t_capturing = false;
+
+// Context scratch.  Growing it retires the old allocation instead of freeing
+// it: a graph captured from an earlier call keeps its pointers, and they stay
+// valid until the context is destroyed.  Growth is refused during capture.
 template <typename T>
 struct DeviceBuffer {
     T* ptr = nullptr;
     size_t count = 0;
+    std::vector<T*> retired;
     void ensure(size_t n) {
         if (n <= count) return;
-        if (ptr) (void)hipFree(ptr);
-        ptr = nullptr;
-        count = 0;
-        check(hipMalloc(&ptr, n * sizeof(T)), "hipMalloc scratch");
+        if (t_capturing)
+            throw ArgError("scratch for this shape must be sized by a call outside stream "
+                           "capture first");
+        T* fresh = nullptr;
+        check(hipMalloc(&fresh, n * sizeof(T)), "hipMalloc scratch");
+        if (ptr) retired.push_back(ptr);
+        ptr = fresh;
         count = n;
     }
     void release() noexcept {
         if (ptr) (void)hipFree(ptr);
+        for (T* p : retired) (void)hipFree(p);
+        retired.clear();
         ptr = nullptr;
         count = 0;
     }
+};
+
+// Marks the calling thread as enqueueing onto `s` for the guard's lifetime,
+// recording whether `s` is being captured.
+struct CaptureScope {
+    explicit CaptureScope(hipStream_t s) {
+        hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+        t_capturing = hipStreamIsCapturing(s, &st) == hipSuccess &&
+                      st == hipStreamCaptureStatusActive;
+    }
+    ~CaptureScope() { t_capturing = false; }
+    CaptureScope(const CaptureScope&) = delete;
+    CaptureScope& operator=(const CaptureScope&) = delete;
 };
 
 }  // namespace
@@ -781,6 +807,7 @@ pk_hip_status pk_hip_matvec_async(pk_hip_ctx* ctx, const pk_hip_weight* w, uint3
         std::lock_guard lock(ctx->mutex);
         ctx->set_device();
         hipStream_t s = stream ? static_cast<hipStream_t>(stream) : ctx->stream;
+        const CaptureScope capture(s);
         enqueue_matvec(ctx, w, expert, dx, batch, dy, s);
         if (ctx->time_kernels) {
             check(hipStreamSynchronize(s), "hipStreamSynchronize");
@@ -829,6 +856,7 @@ pk_hip_status pk_hip_moe_decode_async(pk_hip_ctx* ctx, const pk_hip_moe_layer* l
         const MoeShape m = check_decode_layer(ctx, layer);
         ctx->set_device();
         hipStream_t s = stream ? static_cast<hipStream_t>(stream) : ctx->stream;
+        const CaptureScope capture(s);
         enqueue_moe(ctx, layer, m, dx, dy, dids, dprobs, s);
         if (ctx->time_kernels) {
             check(hipStreamSynchronize(s), "hipStreamSynchronize");
@@ -857,6 +885,7 @@ pk_hip_status pk_hip_moe_decode_noalloc(pk_hip_ctx* ctx, const pk_hip_moe_layer*
                             reinterpret_cast<float*>(base + noalloc::kStatusBytes + 2 * noalloc::kSumBytes),
                             reinterpret_cast<uint32_t*>(base)};
         hipStream_t s = stream ? static_cast<hipStream_t>(stream) : ctx->stream;
+        const CaptureScope capture(s);
         enqueue_moe(ctx, layer, m, dx, dy, dids, dprobs, s, nullptr, &sc);
         if (ctx->time_kernels) {
             check(hipStreamSynchronize(s), "hipStreamSynchronize");
@@ -906,6 +935,7 @@ pk_hip_status pk_hip_moe35_decode_async(pk_hip_ctx* ctx, const pk_hip_moe35_laye
         const MoeShape m = check_decode35(ctx, layer);
         ctx->set_device();
         hipStream_t s = stream ? static_cast<hipStream_t>(stream) : ctx->stream;
+        const CaptureScope capture(s);
         enqueue_moe(ctx, &layer->routed, m, dx, dy, dids, dweights, s, layer);
         if (ctx->time_kernels) {
             check(hipStreamSynchronize(s), "hipStreamSynchronize");
@@ -1064,6 +1094,7 @@ pk_hip_status pk_hip_moe_prefill_async(pk_hip_ctx* ctx, const pk_hip_moe_layer* 
         const MoeShape m = check_prefill(ctx, layer, tokens);
         ctx->set_device();
         hipStream_t s = stream ? static_cast<hipStream_t>(stream) : ctx->stream;
+        const CaptureScope capture(s);
         enqueue_prefill(ctx, layer, m, tokens, dx, dy, dids, dprobs, s);
         if (ctx->time_kernels) {
             check(hipStreamSynchronize(s), "hipStreamSynchronize");
@@ -1118,6 +1149,7 @@ pk_hip_status pk_hip_moe35_prefill_async(pk_hip_ctx* ctx, const pk_hip_moe35_lay
         check_prefill(ctx, &layer->routed, tokens, 1);
         ctx->set_device();
         hipStream_t s = stream ? static_cast<hipStream_t>(stream) : ctx->stream;
+        const CaptureScope capture(s);
         enqueue_prefill(ctx, &layer->routed, m, tokens, dx, dy, dids, dweights, s, layer);
         if (ctx->time_kernels) {
             check(hipStreamSynchronize(s), "hipStreamSynchronize");

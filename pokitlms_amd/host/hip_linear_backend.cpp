@@ -4,16 +4,21 @@
 // (src/vulkan_linear.cpp:612-736): the same type gate, the same shape and
 // row-size checks with std::invalid_argument, one internal mutex, and a
 // permanent failed state after any device error.  Weights differ by design:
-// file-backed tensors are uploaded once and stay resident in HBM (keyed by
-// model file and offset); in-memory tensors are uploaded for the call.
+// file-backed tensors are uploaded once and stay resident in HBM, keyed by
+// model file and offset and held only while that file is alive (the Vulkan
+// cache holds the file's shared_ptr, src/vulkan_linear.cpp:519-526); in-memory
+// tensors go through a content-checked LRU set.
 #include "hip_linear_backend.hpp"
 
 #include "pokit_hip.h"
 
 #include <array>
 #include <cstring>
+#include <iterator>
 #include <limits>
+#include <list>
 #include <map>
+#include <tuple>
 #include <mutex>
 #include <stdexcept>
 #include <utility>
@@ -66,7 +71,9 @@ using WeightPtr = std::unique_ptr<pk_hip_weight, WeightDeleter>;
 
 class HipLinearBackend::Impl {
 public:
-    explicit Impl(const HipLinearOptions& options) : cache_file_tensors(options.cache_file_tensors) {
+    explicit Impl(const HipLinearOptions& options)
+        : cache_file_tensors(options.cache_file_tensors),
+          transient_budget(options.transient_cache_bytes) {
         pk_hip_options opts{};
         opts.struct_size = sizeof(opts);
         opts.time_kernels = options.time_kernels ? 1U : 0U;
@@ -77,6 +84,8 @@ public:
     }
     ~Impl() {
         resident.clear();  // weights before the context that owns them
+        transient_index.clear();
+        transient_lru.clear();
         if (ctx) pk_hip_destroy(ctx);
     }
     Impl(const Impl&) = delete;
@@ -100,37 +109,116 @@ public:
 
     WeightPtr upload(const model::TensorReader& reader, std::uint64_t in, std::uint64_t out,
                      std::uint32_t experts) {
-        const auto bytes = reader.read_all();
-        pk_hip_weight* w = nullptr;
-        ErrorBuffer err;
-        const auto st = pk_hip_upload(ctx, reader.tensor().type, in, out, experts, bytes.data(),
-                                      bytes.size(), &w, err.data(), kErrorCapacity);
-        if (st != PK_HIP_STATUS_OK) raise(st, err);
-        return WeightPtr(w);
+        return upload_bytes(reader.tensor().type, in, out, experts, reader.read_all());
     }
 
     // The resident copy of a file-backed matrix, uploading it on first use;
-    // nullptr for an in-memory reader (the caller uploads it for the call).
+    // nullptr for an in-memory reader.  An entry belongs to the file it was
+    // read from: it is dropped once that file is gone (another file opened at
+    // the same address is a different key) or when the tensor at the offset
+    // no longer has the entry's type and shape.
     pk_hip_weight* resident_matrix(const model::TensorReader& reader, std::uint64_t in,
                                    std::uint64_t out) {
         const auto& file = reader.model_file();
         if (!file || !cache_file_tensors) return nullptr;
+        const auto type = reader.tensor().type;
         const Key key{file.get(), reader.tensor().file_offset};
-        if (const auto it = resident.find(key); it != resident.end()) return it->second.get();
+        if (const auto it = resident.find(key); it != resident.end()) {
+            const auto& e = it->second;
+            if (e.file.lock() == file && e.type == type && e.in == in && e.out == out)
+                return e.weight.get();
+            resident.erase(it);
+        }
+        for (auto it = resident.begin(); it != resident.end();)  // files closed since
+            it = it->second.file.expired() ? resident.erase(it) : std::next(it);
         auto w = upload(reader, in, out, 0);
         auto* raw = w.get();
-        resident.emplace(key, std::move(w));
+        resident.emplace(key, ResidentEntry{file, type, in, out, std::move(w)});
         ++counters.resident_tensors;
         return raw;
     }
 
+    // An in-memory matrix from the LRU set, uploading it on a miss; `bytes`
+    // is the reader's payload.  Sets `transient` (and returns it) when the
+    // set is disabled or the tensor is larger than the whole set.
+    pk_hip_weight* cached_transient(const model::TensorReader& reader, std::uint64_t in,
+                                    std::uint64_t out, std::vector<std::byte>&& bytes,
+                                    WeightPtr& transient) {
+        const auto& t = reader.tensor();
+        if (transient_budget == 0 || bytes.size() > transient_budget) {
+            transient = upload_bytes(t.type, in, out, 0, bytes);
+            ++counters.transient_uploads;
+            return transient.get();
+        }
+        TransientKey key{t.name, t.file_offset, t.type, in, out};
+        if (const auto it = transient_index.find(key); it != transient_index.end()) {
+            auto entry = it->second;
+            if (entry->host == bytes) {
+                transient_lru.splice(transient_lru.begin(), transient_lru, entry);
+                ++counters.transient_hits;
+                return entry->weight.get();
+            }
+            transient_held -= entry->host.size();
+            transient_index.erase(it);
+            transient_lru.erase(entry);
+        }
+        while (!transient_lru.empty() && transient_held + bytes.size() > transient_budget) {
+            auto& last = transient_lru.back();
+            transient_held -= last.host.size();
+            transient_index.erase(last.key);
+            transient_lru.pop_back();
+        }
+        auto w = upload_bytes(t.type, in, out, 0, bytes);
+        ++counters.transient_uploads;
+        transient_held += bytes.size();
+        transient_lru.push_front(TransientEntry{key, std::move(bytes), std::move(w)});
+        transient_index.emplace(std::move(key), transient_lru.begin());
+        return transient_lru.front().weight.get();
+    }
+
+    WeightPtr upload_bytes(std::uint32_t type, std::uint64_t in, std::uint64_t out,
+                           std::uint32_t experts, const std::vector<std::byte>& bytes) {
+        pk_hip_weight* w = nullptr;
+        ErrorBuffer err;
+        const auto st = pk_hip_upload(ctx, type, in, out, experts, bytes.data(), bytes.size(), &w,
+                                      err.data(), kErrorCapacity);
+        if (st != PK_HIP_STATUS_OK) raise(st, err);
+        return WeightPtr(w);
+    }
+
     using Key = std::pair<const void*, std::uint64_t>;
+    struct ResidentEntry {
+        std::weak_ptr<storage::ModelFile> file;
+        std::uint32_t type;
+        std::uint64_t in, out;
+        WeightPtr weight;
+    };
+    struct TransientKey {
+        std::string name;
+        std::uint64_t offset;
+        std::uint32_t type;
+        std::uint64_t in, out;
+        bool operator<(const TransientKey& o) const {
+            return std::tie(name, offset, type, in, out) <
+                   std::tie(o.name, o.offset, o.type, o.in, o.out);
+        }
+    };
+    struct TransientEntry {
+        TransientKey key;
+        std::vector<std::byte> host;
+        WeightPtr weight;
+    };
 
     pk_hip_ctx* ctx = nullptr;
     bool cache_file_tensors = true;
+    std::size_t transient_budget = 0;
+    std::size_t transient_held = 0;
     bool failed = false;
     std::mutex mutex;
-    std::map<Key, WeightPtr> resident;
+    std::map<Key, ResidentEntry> resident;
+    std::list<TransientEntry> transient_lru;  // most recent first
+    std::map<TransientKey, std::list<TransientEntry>::iterator> transient_index;
+    std::uint64_t expert_bytes = 0;  // expert tensors of live MoE layers
     HipLinearStats counters{};  // fields the C ABI does not keep
 };
 
@@ -142,9 +230,11 @@ public:
     std::uint32_t hidden = 0, ffn = 0, experts = 0, top_k = 0;
     bool normalize = false;
     float scale = 1.0F;
+    std::uint64_t expert_bytes = 0;  // gate + up + down payload bytes
 
     ~HipMoeLayer() {
         std::lock_guard lock(owner->mutex);
+        owner->expert_bytes -= expert_bytes;
         for (WeightPtr* w : {&router, &gate, &up, &down, &shared_router, &shared_gate, &shared_up,
                              &shared_down})
             w->reset();
@@ -182,11 +272,9 @@ bool HipLinearBackend::try_linear(const model::TensorReader& weights,
     impl_->require_usable();
     pk_hip_weight* w = impl_->resident_matrix(weights, input.size(), output.size());
     WeightPtr transient;
-    if (!w) {
-        transient = impl_->upload(weights, input.size(), output.size(), 0);
-        w = transient.get();
-        ++impl_->counters.transient_uploads;
-    }
+    if (!w)
+        w = impl_->cached_transient(weights, input.size(), output.size(), weights.read_all(),
+                                    transient);
     ErrorBuffer err;
     const auto st = pk_hip_matvec(impl_->ctx, w, UINT32_MAX, input.data(), 1, output.data(),
                                   err.data(), kErrorCapacity);
@@ -228,6 +316,10 @@ std::shared_ptr<HipMoeLayer> HipLinearBackend::upload_moe_layer(
     layer->gate = impl_->upload(gate_exps, hidden, ffn, n);
     layer->up = impl_->upload(up_exps, hidden, ffn, n);
     layer->down = impl_->upload(down_exps, ffn, hidden, n);
+    layer->expert_bytes = gate_exps.tensor().payload_size.value_or(0) +
+                          up_exps.tensor().payload_size.value_or(0) +
+                          down_exps.tensor().payload_size.value_or(0);
+    impl_->expert_bytes += layer->expert_bytes;
     layer->hidden = static_cast<std::uint32_t>(hidden);
     layer->ffn = static_cast<std::uint32_t>(ffn);
     layer->experts = static_cast<std::uint32_t>(experts);
@@ -334,6 +426,23 @@ HipLinearStats HipLinearBackend::stats() const {
         out.resident_bytes = s.resident_bytes;
         out.uploaded_bytes = s.uploaded_bytes;
         out.router_fallbacks = s.router_fallbacks;
+        out.expert_hits = s.expert_hits;
+        out.expert_misses = s.expert_misses;
+    }
+    out.transient_bytes = impl_->transient_held;
+    out.expert_resident_bytes = impl_->expert_bytes;
+    return out;
+}
+
+HipExpertCacheStats HipLinearBackend::expert_cache_stats() const {
+    std::lock_guard lock(impl_->mutex);
+    HipExpertCacheStats out;
+    out.capacity_bytes = static_cast<std::size_t>(impl_->expert_bytes);
+    out.resident_bytes = static_cast<std::size_t>(impl_->expert_bytes);
+    pk_hip_stats s{};
+    if (pk_hip_get_stats(impl_->ctx, &s) == PK_HIP_STATUS_OK) {
+        out.hits = s.expert_hits;
+        out.misses = s.expert_misses;
     }
     return out;
 }

@@ -35,8 +35,15 @@ struct HipLinearOptions {
     bool time_kernels = false;
     // Keep file-backed tensors resident in HBM after their first use (the
     // whole-model cache of the Vulkan backend, src/vulkan_linear.cpp:516-563).
-    // In-memory tensors are uploaded for the call and released.
     bool cache_file_tensors = true;
+    // In-memory tensors (the expert slices a runner's ExpertStore hands to
+    // tensor_linear, src/qwen35_runner.cpp:716-733) are kept in HBM in a
+    // least-recently-used set of at most this many bytes, keyed by tensor
+    // name, offset, type and shape.  An entry is reused only when the call's
+    // bytes equal the bytes it was uploaded from (a host copy is kept for the
+    // comparison), so a hit never serves stale weights.  0 uploads every
+    // in-memory tensor for its call and releases it.
+    std::size_t transient_cache_bytes = std::size_t{1} << 30;
 };
 
 // Counters in the style of VulkanLinearStats (vulkan_linear.hpp:41-67).
@@ -58,6 +65,26 @@ struct HipLinearStats {
     std::uint64_t resident_tensors{};    // file-backed tensors kept in HBM
     std::uint64_t transient_uploads{};   // in-memory tensors uploaded per call
     std::uint64_t router_fallbacks{};    // tokens routed through exact serial logits
+    std::uint64_t transient_hits{};      // in-memory tensors served from the LRU set
+    std::uint64_t transient_bytes{};     // device bytes held by the LRU set
+    std::uint64_t expert_hits{};         // routed expert accesses of try_moe_block
+    std::uint64_t expert_misses{};       // always 0: uploaded experts never leave HBM
+    std::uint64_t expert_resident_bytes{};  // expert tensor bytes of live MoE layers
+};
+
+// ExpertCacheStats of the runners (include/pokitlms/model/qwen3_moe_runner.hpp:44-52,
+// qwen35_runner.hpp:47-55) for the experts of the MoE layers this backend holds:
+// every expert is resident from upload on, so capacity and resident bytes are the
+// uploaded expert bytes, nothing is read from the file afterwards, and every
+// routed access is a hit.
+struct HipExpertCacheStats {
+    std::size_t capacity_bytes{};
+    std::size_t resident_bytes{};
+    std::uint64_t bytes_read{};
+    std::uint64_t read_operations{};
+    std::uint64_t read_time_ns{};
+    std::uint64_t hits{};
+    std::uint64_t misses{};
 };
 
 // A routed MoE layer resident in HBM (router F32 [hidden, experts]; gate/up
@@ -108,6 +135,7 @@ public:
                        std::span<float> route_probabilities = {});
 
     [[nodiscard]] HipLinearStats stats() const;
+    [[nodiscard]] HipExpertCacheStats expert_cache_stats() const;
     [[nodiscard]] std::string device_name() const;
 
     class Impl;

@@ -11,12 +11,16 @@
 // kernels as the comparison, here through tensor_linear's backend hook
 // (src/tensor_linear.cpp:213) rather than by calling try_linear directly.
 //
-//   hip_backend_cases                 run every case on HIP device 0
+//   hip_backend_cases [DENSE.gguf MOE.gguf]
+//                                     run every case on HIP device 0; with the
+//                                     two Qwen3.5 smoke models, also the runner
+//                                     parity of tests/vulkan_linear_test.cpp:9-36
 //   hip_backend_cases --expect-no-device
 //                                     check that construction fails cleanly
 //                                     on a host without a GPU
 #include "hip_linear_backend.hpp"
 
+#include "pokitlms/model/qwen35_runner.hpp"
 #include "pokitlms/model/tensor_linear.hpp"
 #include "pokitlms/model/tensor_reader.hpp"
 #include "pokitlms/storage/model_file.hpp"
@@ -66,6 +70,7 @@ void pkref_moe35_destroy(pkref_moe35* m);
 namespace {
 
 using pokitlms::gpu::HipLinearBackend;
+using pokitlms::gpu::HipLinearOptions;
 using pokitlms::model::TensorInfo;
 using pokitlms::model::TensorReader;
 
@@ -323,6 +328,127 @@ void file_backed_cases(HipLinearBackend& hip) {
     report(ok, "file_backed_resident", d);
 }
 
+// Two files opened one after the other, with different tensors at the same
+// offset: the second must not be served the first one's resident copy, even
+// when its ModelFile lands at the address the first one had.
+void file_reload_cases(HipLinearBackend& hip) {
+    Rng g(0x5eed0014);
+    const std::size_t rows = 40, in = 512, offset = 4096;
+    char path[] = "/tmp/pk_hip_reloadXXXXXX";
+    const int fd = mkstemp(path);
+    if (fd < 0) {
+        report(false, "file_reload", "mkstemp failed");
+        return;
+    }
+    close(fd);
+    const std::uint32_t types[2] = {12, 14};
+    bool ok = true;
+    double worst = 0.0;
+    const auto before = hip.stats();
+    for (int round = 0; round < 2; ++round) {
+        const auto bytes = make_matrix(types[round], rows, in, g);
+        {
+            std::ofstream f(path, std::ios::binary | std::ios::trunc);
+            const std::vector<char> pad(offset, 0);
+            f.write(pad.data(), static_cast<std::streamsize>(pad.size()));
+            f.write(reinterpret_cast<const char*>(bytes.data()),
+                    static_cast<std::streamsize>(bytes.size()));
+        }
+        auto file = std::make_shared<pokitlms::storage::ModelFile>(path);
+        TensorInfo t;
+        t.name = "reloaded";
+        t.dimensions = {in, rows};
+        t.type = types[round];
+        t.file_offset = offset;
+        t.payload_size = bytes.size();
+        const TensorReader reader(file, t);
+        std::vector<float> x(in), cpu(rows), gpu(rows);
+        for (auto& v : x) v = g.normal(1.0F);
+        pokitlms::model::tensor_linear(reader, x, cpu);
+        ok = ok && hip.try_linear(reader, x, gpu);
+        const auto e = compare(gpu, cpu);
+        worst = std::max(worst, e.normwise);
+        ok = ok && e.harness_ok && e.normwise <= 1e-4;
+    }  // each file is released before the next one is opened
+    const auto after = hip.stats();
+    ok = ok && after.resident_tensors == before.resident_tensors + 2;
+    std::filesystem::remove(path);
+    char d[160];
+    std::snprintf(d, sizeof d, "Q4_K then Q6_K at one offset, 2 uploads, max_normwise=%.3g", worst);
+    report(ok, "file_reload", d);
+}
+
+// In-memory tensors: a repeat with the same bytes is served from the LRU set;
+// the same name, offset and shape with different bytes is uploaded again.
+void transient_cache_cases(HipLinearBackend& hip) {
+    Rng g(0x5eed0015);
+    const std::size_t rows = 48, in = 1024;
+    std::vector<float> x(in), cpu(rows), gpu(rows);
+    for (auto& v : x) v = g.normal(1.0F);
+    bool ok = true;
+    double worst = 0.0;
+    const auto before = hip.stats();
+    for (int round = 0; round < 3; ++round) {
+        // rounds 0 and 1: one matrix; round 2: new bytes under the same key
+        static std::vector<std::byte> bytes;
+        if (round != 1) bytes = make_matrix(13, rows, in, g);
+        TensorInfo t;
+        t.name = "blk.0.ffn_gate_exps.weight";
+        t.dimensions = {in, rows};
+        t.type = 13;
+        t.file_offset = 123456;
+        t.payload_size = bytes.size();
+        auto payload = std::make_shared<std::vector<std::byte>>(bytes.size());
+        std::memcpy(payload->data(), bytes.data(), bytes.size());
+        const TensorReader reader(t, payload);
+        pokitlms::model::tensor_linear(reader, x, cpu);
+        ok = ok && hip.try_linear(reader, x, gpu);
+        const auto e = compare(gpu, cpu);
+        worst = std::max(worst, e.normwise);
+        ok = ok && e.harness_ok && e.normwise <= 1e-4;
+    }
+    const auto after = hip.stats();
+    ok = ok && after.transient_hits == before.transient_hits + 1 &&
+         after.transient_uploads == before.transient_uploads + 2;
+    char d[160];
+    std::snprintf(d, sizeof d, "Q5_K in-memory: 2 uploads, 1 hit, max_normwise=%.3g", worst);
+    report(ok, "transient_cache", d);
+}
+
+// The reference runner driven through the backend (tests/vulkan_linear_test.cpp:9-36):
+// Qwen35Runner::set_linear_backend, then generate_chat must equal the CPU runner's,
+// with and without the file-tensor cache, on the dense and MoE smoke models.
+void runner_cases(const char* dense, const char* moe) {
+    for (const bool cache : {true, false}) {
+        HipLinearOptions options;
+        options.cache_file_tensors = cache;
+        auto backend = std::make_shared<HipLinearBackend>(options);
+        bool ok = true;
+        std::string detail;
+        for (const char* path : {dense, moe}) {
+            pokitlms::model::Qwen35Runner cpu(path), gpu(path);
+            gpu.set_linear_backend(backend);
+            for (const char* prompt : {"hi", "hello", "again"}) {
+                const auto expected = cpu.generate_chat(prompt, 5);
+                const auto got = gpu.generate_chat(prompt, 5);
+                if (got != expected) {
+                    ok = false;
+                    detail += std::string(" mismatch on '") + prompt + "'";
+                }
+            }
+        }
+        const auto s = backend->stats();
+        ok = ok && s.linear_calls > 0 && (cache ? s.resident_tensors > 0 : s.resident_tensors == 0);
+        char d[200];
+        std::snprintf(d, sizeof d, "file cache %s: linear_calls=%llu resident=%llu transient=%llu/%llu%s",
+                      cache ? "on" : "off", static_cast<unsigned long long>(s.linear_calls),
+                      static_cast<unsigned long long>(s.resident_tensors),
+                      static_cast<unsigned long long>(s.transient_hits),
+                      static_cast<unsigned long long>(s.transient_uploads), detail.c_str());
+        report(ok, "runner_parity", d);
+    }
+}
+
 // ---- the MoE block hook -----------------------------------------------------------------
 
 struct Layer {
@@ -513,12 +639,18 @@ int main(int argc, char** argv) {
         unsupported_cases(hip);
         shape_error_cases(hip);
         file_backed_cases(hip);
+        file_reload_cases(hip);
+        transient_cache_cases(hip);
         moe_cases(hip, make_layer(512, 16, 256, 4, false, 0x5eed0005), "hidden 512, 16 experts, top-4", 16);
         moe35_cases(hip, make_layer(1024, 32, 512, 6, true, 0x5eed0035), 2.5F,
                     "Qwen3.5 hidden 1024, 32 experts, top-6, scale 2.5", 16);
         moe_cases(hip, make_layer(2048, 128, 768, 8, true, 0x5eed0006),
                   "hidden 2048, 128 experts, top-8 (config 3 shape)", 16);
         moe_error_cases(hip);
+        const auto ec = hip.expert_cache_stats();
+        report(ec.capacity_bytes == 0 && ec.hits > 0 && ec.misses == 0, "expert_cache_stats",
+               "layers released: no resident expert bytes, every routed access a hit");
+        if (argc > 2) runner_cases(argv[1], argv[2]);
         const auto s = hip.stats();
         std::printf("stats linear_calls=%llu moe_calls=%llu dispatches=%llu resident_tensors=%llu "
                     "transient_uploads=%llu router_fallbacks=%llu\n",

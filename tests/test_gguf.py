@@ -108,3 +108,148 @@ def test_reference_runner_reads_the_seeded_file(tmp_path):
                                             want_logits=True, vocab=TINY.vocab)
     assert tokens.shape == (4,) and np.all(tokens < TINY.vocab)
     assert np.all(np.isfinite(logits)) and int(np.argmax(logits)) == int(tokens[0])
+
+
+# ---- validation (GgufReader's checks, src/gguf_reader.cpp:173-255) ------------------
+
+def _build(metadata=(), tensors=(), alignment_pad=32, tail=b"", version=3, magic=b"GGUF"):
+    """Raw GGUF bytes from explicit fields: metadata [(key, type, payload bytes)],
+    tensors [(name, dims, gtype, offset)], the data section padded to
+    alignment_pad and followed by `tail`."""
+    import struct
+    out = bytearray(magic + struct.pack("<IQQ", version, len(tensors), len(metadata)))
+    for k, t, payload in metadata:
+        out += gguf._str(k) + struct.pack("<I", t) + payload
+    for name, dims, gtype, off in tensors:
+        out += gguf._str(name) + struct.pack("<I", len(dims))
+        out += struct.pack(f"<{len(dims)}Q", *dims) + struct.pack("<IQ", gtype, off)
+    out += b"\0" * ((-len(out)) % alignment_pad)
+    return bytes(out) + tail
+
+
+def _u32(v):
+    import struct
+    return struct.pack("<I", v)
+
+
+def _parse(tmp_path, raw):
+    p = tmp_path / "t.gguf"
+    p.write_bytes(raw)
+    return gguf.GgufFile(str(p))
+
+
+F32_4x2 = ("a", [4, 2], S.F32, 0)  # 32 bytes
+F32_4x2b = ("b", [4, 2], S.F32, 32)
+
+
+def test_valid_minimal_file(tmp_path):
+    with _parse(tmp_path, _build(tensors=[F32_4x2, F32_4x2b], tail=bytes(64))) as f:
+        assert f.alignment == 32 and f.tensors["b"].offset == 32
+        assert f.payload("b").size == 32
+
+
+@pytest.mark.parametrize("raw, message", [
+    (b"GGUX" + bytes(60), "magic"),
+    (_build(version=2), "version 3"),
+    (b"GGUF" + _u32(3), "truncated"),
+    (b"", "truncated"),
+])
+def test_rejects_bad_headers(tmp_path, raw, message):
+    with pytest.raises(ValueError, match=message):
+        _parse(tmp_path, raw)
+
+
+def test_rejects_truncated_directory(tmp_path):
+    raw = _build(tensors=[F32_4x2], tail=bytes(32))
+    for cut in (30, 40, 50):
+        with pytest.raises(ValueError, match="truncated|oversized|limits"):
+            _parse(tmp_path, raw[:cut])
+
+
+def test_rejects_payload_past_the_end(tmp_path):
+    with pytest.raises(ValueError, match="extends beyond file"):
+        _parse(tmp_path, _build(tensors=[F32_4x2, F32_4x2b], tail=bytes(60)))
+
+
+def test_rejects_overlapping_payloads(tmp_path):
+    over = ("b", [4, 2], S.F32, 0)  # same offset as "a"
+    with pytest.raises(ValueError, match="overlapping"):
+        _parse(tmp_path, _build(tensors=[F32_4x2, over], tail=bytes(64)))
+    big = ("a", [8, 2], S.F32, 0)  # 64 bytes reach into "b" at 32
+    with pytest.raises(ValueError, match="overlapping"):
+        _parse(tmp_path, _build(tensors=[big, F32_4x2b], tail=bytes(96)))
+
+
+def test_rejects_misaligned_offset(tmp_path):
+    with pytest.raises(ValueError, match="data offset"):
+        _parse(tmp_path, _build(tensors=[("a", [4, 2], S.F32, 8)], tail=bytes(64)))
+
+
+def test_rejects_duplicate_names_and_keys(tmp_path):
+    dup = ("a", [4, 2], S.F32, 32)
+    with pytest.raises(ValueError, match="duplicate GGUF tensor name"):
+        _parse(tmp_path, _build(tensors=[F32_4x2, dup], tail=bytes(64)))
+    md = [("k", gguf.U32, _u32(1)), ("k", gguf.U32, _u32(2))]
+    with pytest.raises(ValueError, match="duplicate GGUF metadata key"):
+        _parse(tmp_path, _build(metadata=md))
+
+
+@pytest.mark.parametrize("t, v, ok", [(gguf.U32, 0, False), (gguf.U32, 12, False),
+                                      (gguf.U32, 4, False), (gguf.I32, 32, False),
+                                      (gguf.U32, 24, True), (gguf.U64, 64, True)])
+def test_alignment_rules(tmp_path, t, v, ok):
+    import struct
+    payload = struct.pack("<i" if t == gguf.I32 else ("<Q" if t == gguf.U64 else "<I"), v)
+    raw = _build(metadata=[("general.alignment", t, payload)], tensors=[F32_4x2],
+                 alignment_pad=v if ok else 32, tail=bytes(64))
+    if ok:
+        with _parse(tmp_path, raw) as f:
+            assert f.alignment == v
+    else:
+        with pytest.raises(ValueError, match="alignment"):
+            _parse(tmp_path, raw)
+
+
+def test_rejects_bad_tensor_shapes(tmp_path):
+    with pytest.raises(ValueError, match="rank"):
+        _parse(tmp_path, _build(tensors=[("a", [], S.F32, 0)], tail=bytes(32)))
+    with pytest.raises(ValueError, match="zero-sized"):
+        _parse(tmp_path, _build(tensors=[("a", [4, 0], S.F32, 0)], tail=bytes(32)))
+    with pytest.raises(ValueError, match="multiple of 256"):
+        _parse(tmp_path, _build(tensors=[("a", [100, 1], S.Q4_K, 0)], tail=bytes(256)))
+
+
+def test_rejects_bad_metadata_values(tmp_path):
+    with pytest.raises(ValueError, match="boolean"):
+        _parse(tmp_path, _build(metadata=[("b", gguf.BOOL, b"\x02")]))
+    with pytest.raises(ValueError, match="value type"):
+        _parse(tmp_path, _build(metadata=[("x", 13, _u32(0))]))
+    import struct
+    huge = struct.pack("<Q", 1 << 40)
+    with pytest.raises(ValueError, match="oversized GGUF string"):
+        _parse(tmp_path, _build(metadata=[("s", gguf.STRING, huge)]))
+    arr = struct.pack("<IQ", gguf.U8, 1 << 40)
+    with pytest.raises(ValueError, match="oversized GGUF array"):
+        _parse(tmp_path, _build(metadata=[("a", gguf.ARRAY, arr)]))
+
+
+def test_unknown_tensor_type_parses_but_has_no_payload(tmp_path):
+    """A type without a known layout parses, as in the reference (its payload
+    size is unknown there), and its payload is refused."""
+    with _parse(tmp_path, _build(tensors=[("a", [4, 2], 99, 0), F32_4x2b], tail=bytes(64))) as f:
+        assert f.tensors["a"].gtype == 99 and not f.tensors["a"].known_layout
+        with pytest.raises(ValueError, match="no known block layout"):
+            f.payload("a")
+        assert f.payload("b").size == 32
+
+
+def test_reference_data_files_parse():
+    """Every GGUF file the reference ships under tests/data parses (the Q/K/V
+    smoke models; skipped where the reference checkout is absent)."""
+    import glob
+    files = sorted(glob.glob("/root/reference/tests/data/*.gguf"))
+    if not files:
+        pytest.skip("reference checkout absent")
+    for path in files:
+        with gguf.GgufFile(path) as f:
+            assert f.tensors and all(t.known_layout for t in f.tensors.values())

@@ -244,6 +244,65 @@ def test_prefill_graph_replays_match_eager(hip, c4):
         hip.moe_decode(h, x[rep])  # eager work between replays
 
 
+def test_capture_refuses_scratch_growth_and_old_graphs_survive_it():
+    """A fresh context: a call under stream capture that would need more
+    scratch than earlier calls sized is refused with INVALID_ARGUMENT (an
+    allocation cannot be part of the graph); an eager call may grow it, and
+    a graph captured before the growth still replays to its eager results,
+    because the old scratch is kept until the context is destroyed."""
+    import torch
+    from pokitlms_amd.backend import HipBackend
+    layer = S.moe_layer(seed=777, hidden=512, experts=16, ffn=256, top_k=4)
+    x = S.normal_f32(S.rng(778), 64 * 512).reshape(64, 512)
+    dev = torch.device("cuda:0")
+    with HipBackend(0) as fresh:
+        h = fresh.upload_moe_layer(layer)
+        dx = torch.from_numpy(np.ascontiguousarray(x)).to(dev)
+        dy = torch.empty(64, 512, device=dev)
+        di = torch.empty(64, 4, dtype=torch.int32, device=dev)
+        dp = torch.empty(64, 4, device=dev)
+        stream = torch.cuda.Stream()
+
+        def run(s, tokens):
+            fresh.moe_prefill_async(h, dx.data_ptr(), tokens, dy.data_ptr(), di.data_ptr(),
+                                    dp.data_ptr(), s)
+        with torch.cuda.stream(stream):
+            run(stream.cuda_stream, 8)
+        fresh.sync(stream.cuda_stream)
+        y8, i8, p8 = dy[:8].clone(), di[:8].clone(), dp[:8].clone()
+        g8 = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g8, stream=stream):
+            run(torch.cuda.current_stream().cuda_stream, 8)
+        refused = None
+        g64 = torch.cuda.CUDAGraph()
+        try:
+            with torch.cuda.graph(g64, stream=stream):
+                run(torch.cuda.current_stream().cuda_stream, 64)
+        except ValueError as e:  # INVALID_ARGUMENT
+            refused = e
+        assert refused is not None and "outside stream capture" in str(refused), refused
+        torch.cuda.synchronize()
+        with torch.cuda.stream(stream):  # eager: grows the scratch
+            run(stream.cuda_stream, 64)
+        fresh.sync(stream.cuda_stream)
+        y64, i64 = dy.clone(), di.clone()
+        assert torch.equal(i64[:8], i8)
+        assert normwise_rel(y64[:8].cpu().numpy(), y8.cpu().numpy()) <= TOL
+        for rep in range(3):
+            dy.zero_()
+            di.zero_()
+            dp.zero_()
+            torch.cuda.synchronize()
+            g8.replay()
+            torch.cuda.synchronize()
+            fresh.sync(0)
+            assert torch.equal(dy[:8], y8) and torch.equal(di[:8], i8), rep
+            assert torch.equal(dp[:8], p8), rep
+            fresh.moe_decode(h, x[rep])  # eager work between replays
+        del g8, g64
+        h.release()
+
+
 def test_prefill_kernel_timing(hip, c4):
     _, h, x = c4
     hip.set_kernel_timing(True)

@@ -9,7 +9,13 @@ for a GGUF type without a kernel (Q8_K); shape errors;
 file-backed tensors kept resident; the MoE block hook against the reference
 MoE block and the Qwen3.5 block with its shared expert (ids exact, outputs
 normwise <= 1e-4); a non-finite router as a
-data error that leaves the backend usable.
+data error that leaves the backend usable; two files opened one after the
+other with different tensors at one offset (no stale resident copy); the
+content-checked LRU set for in-memory tensors; the expert-cache counters; and
+the reference's Qwen35Runner driven through set_linear_backend on its dense and
+MoE smoke models (tests/golden/qwen35-smoke.gguf and qwen35moe-smoke.gguf,
+copies of the reference's tests/data files), whose generate_chat output must
+equal the CPU runner's, as in the reference's tests/vulkan_linear_test.cpp:9-36.
 """
 import os
 import subprocess
@@ -42,7 +48,9 @@ def test_native_backend_without_a_device_fails_cleanly():
 @pytest.mark.gpu
 @pytest.mark.skipif(not os.path.exists(CASES), reason=MISSING)
 def test_native_backend_cases():
-    r = _run(timeout=300)
+    golden = os.path.join(ROOT, "tests", "golden")
+    r = _run(os.path.join(golden, "qwen35-smoke.gguf"), os.path.join(golden, "qwen35moe-smoke.gguf"),
+             timeout=300)
     assert r.returncode == 0, r.stdout[-3000:]
     lines = r.stdout.splitlines()
     assert not [l for l in lines if l.startswith("FAIL")]
@@ -50,3 +58,6 @@ def test_native_backend_cases():
     assert sum(l.startswith("PASS try_linear_unsupported") for l in lines) == 1
     assert sum(l.startswith("PASS moe_block_parity") for l in lines) == 2
     assert sum(l.startswith("PASS moe35_block_parity") for l in lines) == 1
+    for name in ("file_reload", "transient_cache", "expert_cache_stats"):
+        assert sum(l.startswith("PASS " + name) for l in lines) == 1, name
+    assert sum(l.startswith("PASS runner_parity") for l in lines) == 2
