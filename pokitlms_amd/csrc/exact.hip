@@ -102,6 +102,15 @@ __device__ __forceinline__ float add16(float s, const f32x16 v) {
 constexpr uint32_t kChainPad = 32;
 __host__ __device__ constexpr uint32_t chain_floats(uint32_t n) { return (n + 15u) / 16u * 16u + kChainPad; }
 
+// x of the reference matvec sits in LDS one block (BE values) per 16-byte
+// padded stretch: the lanes of a wave read the same offset of different
+// blocks, and without the pad those reads (1 KB apart for 256-value blocks)
+// all fall in one LDS bank.
+template <uint32_t BE>
+__host__ __device__ constexpr uint32_t xpad(uint32_t i) { return i + i / BE * 4u; }
+template <uint32_t BE>
+__host__ __device__ constexpr uint32_t xpad_floats(uint32_t n) { return n + (n + BE - 1u) / BE * 4u; }
+
 // s = ((s + p[0]) + p[1]) + ... + p[n - 1], by the calling lane.  p is in LDS,
 // 64-byte aligned, readable for chain_floats(n) floats: the next 32 values
 // are read while the current 32 are added, so the chain of dependent adds
@@ -113,6 +122,9 @@ __device__ float serial_sum(const float* p, uint32_t n, float s) {
     uint32_t k = 0;
     for (; k + 2u <= nb; k += 2u) {
         const f32x16 na = v[k + 2u], nb2 = v[k + 3u];
+        // keep the next 32 reads ahead of the 32 adds: the scheduler would
+        // otherwise sink them next to their use and expose the LDS latency
+        __builtin_amdgcn_sched_barrier(0);
         s = add16(s, a);
         s = add16(s, b);
         a = na;
@@ -145,23 +157,99 @@ __device__ __forceinline__ float q6_step4(float s, float dsc, uint32_t v, float4
     return __fadd_rn(s, __fmul_rn(__fmul_rn(dsc, ub<3>(v) - 32.0f), x.w));
 }
 
-// dot of block b of row `row` with x (x in LDS, 16-byte aligned), in element
-// order.  The whole block is loaded into registers first (whole words; the
-// planar formats field by field).  K-quants and Q4_1: the decoded FP32 weight
-// times x; Q8_0/Q4_0: d * dot_i8_f32 (the int8 value times x, then the scale
-// once).
+// Block b of row `row`, loaded whole into registers (whole words; the planar
+// formats field by field), so a kernel can issue the loads before it stages x.
+template <int T> struct RefRaw;
+template <> struct RefRaw<T_Q4_K> { uint32_t w[36]; };
+template <> struct RefRaw<T_Q5_K> { uint32_t w[44]; };
+template <> struct RefRaw<T_Q6_K> { uint32_t ql[32], qh[16], sw[4]; float d; };
+template <> struct RefRaw<T_Q8_0> { uint32_t w[8]; float d; };
+template <> struct RefRaw<T_Q4_1> { uint32_t w[5]; };
+template <> struct RefRaw<T_Q5_0> { uint32_t qs[4], qh[1]; float d; };
+template <> struct RefRaw<T_Q5_1> { uint32_t w[6]; };
+template <> struct RefRaw<T_Q2_K> { uint32_t sw[4], qw[16], dd[1]; };
+template <> struct RefRaw<T_Q3_K> { uint32_t qw[16], hw[8], p3[3]; float d; };
+template <> struct RefRaw<T_Q4_0> { uint32_t w[4]; float d; };
+
 template <int T>
-__device__ float block_dot(const QRow& row, uint32_t b, const float* x) {
+__device__ __forceinline__ void ref_load(const QRow& row, uint32_t b, RefRaw<T>& r) {
+    if constexpr (T == T_Q4_K || T == T_Q5_K) {
+        ld_words<T == T_Q4_K ? 36 : 44>(block_ptr<RefBlock<T>::BB>(row, b), r.w);
+    } else if constexpr (T == T_Q6_K) {
+        using L = Planar<T_Q6_K>;
+        ld_words<32>(field_ptr<L::QL, 128>(row, b), r.ql);
+        ld_words<16>(field_ptr<L::QH, 64>(row, b), r.qh);
+        ld_words<4>(field_ptr<L::SC, 16>(row, b), r.sw);
+        r.d = half_bits_to_float(ld_u16(field_ptr<L::D, 2>(row, b)));
+    } else if constexpr (T == T_Q8_0) {
+        using L = Planar<T_Q8_0>;
+        ld_words<8>(field_ptr<L::QS, 32>(row, b), r.w);
+        r.d = half_bits_to_float(ld_u16(field_ptr<L::D, 2>(row, b)));
+    } else if constexpr (T == T_Q4_1) {
+        ld_words<5>(block_ptr<20>(row, b), r.w);
+    } else if constexpr (T == T_Q5_0) {
+        using L = Planar<T_Q5_0>;
+        ld_words<4>(field_ptr<L::QS, 16>(row, b), r.qs);
+        ld_words<1>(field_ptr<L::QH, 4>(row, b), r.qh);
+        r.d = half_bits_to_float(ld_u16(field_ptr<L::D, 2>(row, b)));
+    } else if constexpr (T == T_Q5_1) {
+        ld_words<6>(block_ptr<24>(row, b), r.w);
+    } else if constexpr (T == T_Q2_K) {
+        const uint8_t* blk = block_ptr<84>(row, b);
+        ld_words<4>(blk, r.sw);
+        ld_words<16>(blk + 16, r.qw);
+        ld_words<1>(blk + 80, r.dd);
+    } else if constexpr (T == T_Q3_K) {
+        using L = Planar<T_Q3_K>;
+        ld_words<16>(field_ptr<L::QS, 64>(row, b), r.qw);
+        ld_words<8>(field_ptr<L::HM, 32>(row, b), r.hw);
+        ld_words<3>(field_ptr<L::SC, 12>(row, b), r.p3);
+        r.d = half_bits_to_float(ld_u16(field_ptr<L::D, 2>(row, b)));
+    } else {  // Q4_0
+        using L = Planar<T_Q4_0>;
+        ld_words<4>(field_ptr<L::QS, 16>(row, b), r.w);
+        r.d = half_bits_to_float(ld_u16(field_ptr<L::D, 2>(row, b)));
+    }
+}
+
+// Eight float4 of x from LDS.  The block dots below read x one 32-value
+// chunk ahead of the chain: the reads of chunk c + 1 take their address from
+// a zero that depends on the chain's value at the start of chunk c.  Without
+// that the scheduler hoists all 256 reads of a block to the top, and the
+// registers they need spill into AGPRs, on the chain's critical path.
+struct X8 {
+    float4 v[8];
+};
+__device__ __forceinline__ X8 ldx8(const float4* x4, uint32_t i) {
+    X8 r;
+#pragma unroll
+    for (uint32_t k = 0; k < 8; ++k) r.v[k] = x4[i + k];
+    return r;
+}
+// 0, computed from v so that nothing using it can move above v's definition.
+__device__ __forceinline__ uint32_t zero_after(float v) {
+    uint32_t z;
+    asm volatile("v_and_b32 %0, 0, %1" : "=v"(z) : "v"(__builtin_bit_cast(uint32_t, v)));
+    return z;
+}
+
+// dot of a loaded block with x (x in LDS, 16-byte aligned), in element
+// order.  K-quants and Q4_1: the decoded FP32 weight times x; Q8_0/Q4_0:
+// d * dot_i8_f32 (the int8 value times x, then the scale once).
+template <int T>
+__device__ float ref_dot(const RefRaw<T>& r, const float* x) {
     const float4* x4 = reinterpret_cast<const float4*>(x);
     float s = 0.0f;
     if constexpr (T == T_Q4_K || T == T_Q5_K) {
-        constexpr int NW = T == T_Q4_K ? 36 : 44, QS = T == T_Q4_K ? 4 : 12;
-        uint32_t w[NW];
-        ld_words<NW>(block_ptr<RefBlock<T>::BB>(row, b), w);
+        constexpr int QS = T == T_Q4_K ? 4 : 12;
+        const uint32_t* w = r.w;
         const uint32_t h[4] = {w[0], w[1], w[2], w[3]};
         const float d = half_bits_to_float(w[0] & 0xffffu), dmin = half_bits_to_float(w[0] >> 16);
+        X8 xa = ldx8(x4, 0u);
 #pragma unroll
         for (uint32_t j = 0; j < 8; ++j) {
+            X8 xb;
+            if (j < 7u) xb = ldx8(x4 + zero_after(s), 8u * (j + 1u));
             float sc, mn;
             kq_scale_min(h, j, sc, mn);
             const float ds = __fmul_rn(d, sc), dm = __fmul_rn(dmin, mn);
@@ -170,50 +258,45 @@ __device__ float block_dot(const QRow& row, uint32_t b, const float* x) {
                 const uint32_t raw = w[QS + 8u * (j / 2u) + k];
                 uint32_t v = (j & 1u) ? (raw >> 4) & 0x0f0f0f0fu : raw & 0x0f0f0f0fu;
                 if constexpr (T == T_Q5_K) v |= ((w[4u + k] >> j) & 0x01010101u) << 4;
-                s = kq_step4(s, ds, dm, v, x4[8u * j + k]);
+                s = kq_step4(s, ds, dm, v, xa.v[k]);
             }
+            if (j < 7u) xa = xb;
         }
     } else if constexpr (T == T_Q6_K) {
-        using L = Planar<T_Q6_K>;
-        uint32_t ql[32], qh[16], sw[4];
-        ld_words<32>(field_ptr<L::QL, 128>(row, b), ql);
-        ld_words<16>(field_ptr<L::QH, 64>(row, b), qh);
-        ld_words<4>(field_ptr<L::SC, 16>(row, b), sw);
-        const float d = half_bits_to_float(ld_u16(field_ptr<L::D, 2>(row, b)));
+        const float d = r.d;
+        X8 xa = ldx8(x4, 0u);
 #pragma unroll
         for (uint32_t c = 0; c < 8; ++c) {
+            X8 xb;
+            if (c < 7u) xb = ldx8(x4 + zero_after(s), 8u * (c + 1u));
             const uint32_t half = c / 4u, g = c % 4u;
 #pragma unroll
             for (uint32_t k = 0; k < 8; ++k) {
                 const uint32_t sb = 8u * half + 2u * g + (k >= 4u ? 1u : 0u);
-                const int sc = static_cast<int8_t>(sw[sb / 4u] >> (8u * (sb % 4u)));
+                const int sc = static_cast<int8_t>(r.sw[sb / 4u] >> (8u * (sb % 4u)));
                 const float dsc = __fmul_rn(d, static_cast<float>(sc));
-                const uint32_t lw = ql[16u * half + 8u * (g & 1u) + k];
-                const uint32_t hw = qh[8u * half + k];
+                const uint32_t lw = r.ql[16u * half + 8u * (g & 1u) + k];
+                const uint32_t hw = r.qh[8u * half + k];
                 const uint32_t v = (g >= 2u ? (lw >> 4) & 0x0f0f0f0fu : lw & 0x0f0f0f0fu) |
                                    (((hw >> (2u * g)) & 0x03030303u) << 4);
-                s = q6_step4(s, dsc, v, x4[8u * c + k]);
+                s = q6_step4(s, dsc, v, xa.v[k]);
             }
+            if (c < 7u) xa = xb;
         }
     } else if constexpr (T == T_Q8_0) {
-        using L = Planar<T_Q8_0>;
-        uint32_t w[8];  // quant i in byte i
-        ld_words<8>(field_ptr<L::QS, 32>(row, b), w);
-        const float d = half_bits_to_float(ld_u16(field_ptr<L::D, 2>(row, b)));
 #pragma unroll
         for (uint32_t k = 0; k < 8; ++k) {
             const float4 xv = x4[k];
             const float xs[4] = {xv.x, xv.y, xv.z, xv.w};
 #pragma unroll
             for (uint32_t m = 0; m < 4; ++m) {
-                const int q = static_cast<int8_t>(w[k] >> (8u * m));
+                const int q = static_cast<int8_t>(r.w[k] >> (8u * m));
                 s = __fadd_rn(s, __fmul_rn(xs[m], static_cast<float>(q)));
             }
         }
-        s = __fmul_rn(d, s);
+        s = __fmul_rn(r.d, s);
     } else if constexpr (T == T_Q4_1) {  // weight fl(fl(q * d) + m), low nibbles first
-        uint32_t w[5];                   // d | m << 16, then quants 0..15
-        ld_words<5>(block_ptr<20>(row, b), w);
+        const uint32_t* w = r.w;         // d | m << 16, then quants 0..15
         const float d = half_bits_to_float(w[0] & 0xffffu), m = half_bits_to_float(w[0] >> 16);
 #pragma unroll
         for (uint32_t k = 0; k < 8; ++k) {
@@ -228,21 +311,19 @@ __device__ float block_dot(const QRow& row, uint32_t b, const float* x) {
     } else if constexpr (T == T_Q5_0 || T == T_Q5_1) {
         // decode_q5_0: fl((q - 16) * d); decode_q5_1: fl(fl(q * d) + m)
         // (src/quantized_linear.cpp:64-93), then dot_f32's order
-        uint32_t qs[4], qh[1];
+        uint32_t qs[4], qh;
         float d, m = 0.0f;
         if constexpr (T == T_Q5_0) {
-            using L = Planar<T_Q5_0>;
-            ld_words<4>(field_ptr<L::QS, 16>(row, b), qs);
-            ld_words<1>(field_ptr<L::QH, 4>(row, b), qh);
-            d = half_bits_to_float(ld_u16(field_ptr<L::D, 2>(row, b)));
-        } else {
-            uint32_t w[6];  // d | m << 16, qh, quants
-            ld_words<6>(block_ptr<24>(row, b), w);
-            d = half_bits_to_float(w[0] & 0xffffu);
-            m = half_bits_to_float(w[0] >> 16);
-            qh[0] = w[1];
 #pragma unroll
-            for (uint32_t i = 0; i < 4; ++i) qs[i] = w[2u + i];
+            for (uint32_t i = 0; i < 4; ++i) qs[i] = r.qs[i];
+            qh = r.qh[0];
+            d = r.d;
+        } else {  // d | m << 16, qh, quants
+            d = half_bits_to_float(r.w[0] & 0xffffu);
+            m = half_bits_to_float(r.w[0] >> 16);
+            qh = r.w[1];
+#pragma unroll
+            for (uint32_t i = 0; i < 4; ++i) qs[i] = r.w[2u + i];
         }
 #pragma unroll
         for (uint32_t k = 0; k < 8; ++k) {
@@ -252,7 +333,7 @@ __device__ float block_dot(const QRow& row, uint32_t b, const float* x) {
             for (uint32_t j = 0; j < 4; ++j) {
                 const uint32_t i = 4u * k + j, byte = i & 15u;
                 const uint32_t v = (qs[byte / 4u] >> (8u * (byte % 4u))) & 0xffu;
-                const uint32_t q = (i < 16u ? (v & 15u) : (v >> 4)) | (((qh[0] >> i) & 1u) << 4);
+                const uint32_t q = (i < 16u ? (v & 15u) : (v >> 4)) | (((qh >> i) & 1u) << 4);
                 const float w = T == T_Q5_0 ? __fmul_rn(static_cast<float>(static_cast<int>(q) - 16), d)
                                             : __fadd_rn(__fmul_rn(static_cast<float>(q), d), m);
                 s = __fadd_rn(s, __fmul_rn(w, xs[j]));
@@ -261,31 +342,27 @@ __device__ float block_dot(const QRow& row, uint32_t b, const float* x) {
     } else if constexpr (T == T_Q2_K || T == T_Q3_K) {
         // decode_q2_k: fl(fl(dl * q) - ml); decode_q3_k: fl(ds * (q - 4 + 4 * hbit))
         // (src/quantized_linear.cpp:95-164); element 128h + 32s + 16t + i
-        uint32_t qw[16], hw[8], sw[4];
+        uint32_t sw[4];
         float d, dmin = 0.0f;
+        const uint32_t* qw = r.qw;
         if constexpr (T == T_Q2_K) {
-            const uint8_t* blk = block_ptr<84>(row, b);
-            ld_words<4>(blk, sw);
-            ld_words<16>(blk + 16, qw);
-            uint32_t dd[1];
-            ld_words<1>(blk + 80, dd);
-            d = half_bits_to_float(dd[0] & 0xffffu);
-            dmin = half_bits_to_float(dd[0] >> 16);
+#pragma unroll
+            for (uint32_t j = 0; j < 4; ++j) sw[j] = r.sw[j];
+            d = half_bits_to_float(r.dd[0] & 0xffffu);
+            dmin = half_bits_to_float(r.dd[0] >> 16);
         } else {
-            using L = Planar<T_Q3_K>;
-            ld_words<16>(field_ptr<L::QS, 64>(row, b), qw);
-            ld_words<8>(field_ptr<L::HM, 32>(row, b), hw);
-            uint32_t p3[3];
-            ld_words<3>(field_ptr<L::SC, 12>(row, b), p3);
 #pragma unroll
             for (uint32_t j = 0; j < 4; ++j) {  // the 16 unpacked 6-bit scales, 4 per word
-                sw[j] = q3k_scale(p3, 4u * j) | (q3k_scale(p3, 4u * j + 1u) << 8) |
-                        (q3k_scale(p3, 4u * j + 2u) << 16) | (q3k_scale(p3, 4u * j + 3u) << 24);
+                sw[j] = q3k_scale(r.p3, 4u * j) | (q3k_scale(r.p3, 4u * j + 1u) << 8) |
+                        (q3k_scale(r.p3, 4u * j + 2u) << 16) | (q3k_scale(r.p3, 4u * j + 3u) << 24);
             }
-            d = half_bits_to_float(ld_u16(field_ptr<L::D, 2>(row, b)));
+            d = r.d;
         }
+        X8 xa = ldx8(x4, 0u), xb;
 #pragma unroll
         for (uint32_t g = 0; g < 16; ++g) {  // 16-element groups in element order
+            if ((g & 1u) == 0u && g < 14u)  // the next two groups' x ahead of this pair
+                xb = ldx8(x4 + zero_after(s), 4u * (g + 2u));
             const uint32_t h = g / 8u, sh = (g % 8u) / 2u, t = g % 2u;
             const uint32_t scb = (sw[g / 4u] >> (8u * (g % 4u))) & 0xffu;
             float mul, off;
@@ -299,7 +376,7 @@ __device__ float block_dot(const QRow& row, uint32_t b, const float* x) {
 #pragma unroll
             for (uint32_t k = 0; k < 4; ++k) {
                 const uint32_t qv = qw[(32u * h + 16u * t) / 4u + k];
-                const float4 xv = x4[4u * g + k];
+                const float4 xv = xa.v[4u * (g & 1u) + k];
                 const float xs[4] = {xv.x, xv.y, xv.z, xv.w};
 #pragma unroll
                 for (uint32_t j = 0; j < 4; ++j) {
@@ -308,18 +385,15 @@ __device__ float block_dot(const QRow& row, uint32_t b, const float* x) {
                     if constexpr (T == T_Q2_K) {
                         w = __fsub_rn(__fmul_rn(mul, static_cast<float>(q)), off);
                     } else {
-                        const uint32_t hb = (hw[(16u * t) / 4u + k] >> (8u * j + 4u * h + sh)) & 1u;
+                        const uint32_t hb = (r.hw[(16u * t) / 4u + k] >> (8u * j + 4u * h + sh)) & 1u;
                         w = __fmul_rn(mul, static_cast<float>(static_cast<int>(q) - (hb ? 0 : 4)));
                     }
                     s = __fadd_rn(s, __fmul_rn(w, xs[j]));
                 }
             }
+            if ((g & 1u) == 1u && g < 15u) xa = xb;
         }
     } else {  // Q4_0: low nibbles are elements 0..15, high 16..31
-        using L = Planar<T_Q4_0>;
-        uint32_t w[4];  // quant byte i in byte i
-        ld_words<4>(field_ptr<L::QS, 16>(row, b), w);
-        const float d = half_bits_to_float(ld_u16(field_ptr<L::D, 2>(row, b)));
 #pragma unroll
         for (uint32_t k = 0; k < 8; ++k) {
             const float4 xv = x4[k];
@@ -327,12 +401,12 @@ __device__ float block_dot(const QRow& row, uint32_t b, const float* x) {
 #pragma unroll
             for (uint32_t m = 0; m < 4; ++m) {
                 const uint32_t i = 4u * k + m, byte = i & 15u;
-                const uint32_t v = (w[byte / 4u] >> (8u * (byte % 4u))) & 0xffu;
+                const uint32_t v = (r.w[byte / 4u] >> (8u * (byte % 4u))) & 0xffu;
                 const int q = static_cast<int>(i < 16u ? (v & 15u) : (v >> 4)) - 8;
                 s = __fadd_rn(s, __fmul_rn(xs[m], static_cast<float>(q)));
             }
         }
-        s = __fmul_rn(d, s);
+        s = __fmul_rn(r.d, s);
     }
     return s;
 }
@@ -346,9 +420,10 @@ __device__ float block_dot(const QRow& row, uint32_t b, const float* x) {
 // scale = 1 / sqrt(sum / n + eps) (rms_norm, src/rms_norm.cpp:9-27, and the
 // residual adds of src/qwen3_moe_runner.cpp:640,692).  The leader writes v
 // and xs to x_out / normed_out.  LDS: xs [n], sq [chain_floats(n)], wb [n].
-template <uint32_t NT>
+template <uint32_t NT, uint32_t PADB = 0>
 __device__ void ref_norm_stage(const RefNormIn& p, uint32_t n, float* xs, float* sq, float* wb,
                                float& s_scale, bool leader) {
+    auto xi = [](uint32_t i) { return PADB ? xpad<(PADB ? PADB : 1u)>(i) : i; };
     const uint32_t tid = threadIdx.x;
     for (uint32_t base = 0; base < n; base += 8u * NT) {
         uint32_t ic[8];
@@ -394,7 +469,7 @@ __device__ void ref_norm_stage(const RefNormIn& p, uint32_t n, float* xs, float*
         for (uint32_t k = 0; k < 8; ++k) {
             const uint32_t i = base + tid + NT * k;
             if (i < n) {
-                xs[i] = v[k];
+                xs[xi(i)] = v[k];
                 sq[i] = __fmul_rn(v[k], v[k]);
                 wb[i] = wv[k];
             }
@@ -405,12 +480,12 @@ __device__ void ref_norm_stage(const RefNormIn& p, uint32_t n, float* xs, float*
     __syncthreads();
     const float scale = s_scale;
     for (uint32_t i = tid; i < n; i += NT) {
-        const float vi = xs[i], o = __fmul_rn(__fmul_rn(vi, scale), wb[i]);
+        const float vi = xs[xi(i)], o = __fmul_rn(__fmul_rn(vi, scale), wb[i]);
         if (leader) {
             if (p.x_out) p.x_out[i] = vi;
             if (p.normed_out) p.normed_out[i] = o;
         }
-        xs[i] = o;
+        xs[xi(i)] = o;
     }
     __syncthreads();
 }
@@ -526,16 +601,28 @@ __global__ __launch_bounds__(256) void k_ref_matvec(RefMatvecArgs a) {
             }
         }
     }
-    float* xs = lds;
-    float* part = lds + a.in;
-    uint64_t expert = 0;
-    if (a.route.logits) expert = ref_route_block(a.route, r, leader, rsh);
-    else if (a.ids) expert = a.ids[r];
+    float* xs = lds;  // padded: block b at b * (BE + 4)
+    float* part = lds + xpad_floats<BE>(a.in);
+    const uint32_t row0 = bx * rpw, lr = tid / nb, b = tid % nb, row = row0 + lr;
+    const bool active = lr < rpw && row < rows;
+    const uint64_t nblk = static_cast<uint64_t>(rows) * nb;
+    const QRow qrow{W, nblk, static_cast<uint64_t>(active ? row : 0u) * nb};
+    // With the expert known up front (a plain matrix, or ids of an earlier
+    // launch) the block is loaded before x is staged, so the weight loads
+    // overlap the staging (the norm's serial sum, the SwiGLU exponentials).
+    RefRaw<T> raw;
+    if (a.route.logits) {
+        const uint64_t expert = ref_route_block(a.route, r, leader, rsh);
+        ref_load<T>(QRow{W + expert * slice_bytes, nblk, qrow.blk0}, b, raw);
+    } else {
+        const uint64_t expert = a.ids ? a.ids[r] : 0u;
+        ref_load<T>(QRow{W + expert * slice_bytes, nblk, qrow.blk0}, b, raw);
+    }
     const float* x = a.x + static_cast<uint64_t>(r) * a.x_stride;
     const uint32_t n4 = a.in / 4u;  // in is a multiple of 32
     if (a.norm.w) {
-        ref_norm_stage<256>(a.norm, a.in, xs, part + 256, part + 256 + chain_floats(a.in), s_scale,
-                            leader);
+        ref_norm_stage<256, BE>(a.norm, a.in, xs, part + 256, part + 256 + chain_floats(a.in),
+                                s_scale, leader);
     } else if (a.x_up) {
         const f32x4* g4 = reinterpret_cast<const f32x4*>(x);
         const f32x4* u4 = reinterpret_cast<const f32x4*>(a.x_up + static_cast<uint64_t>(r) * a.x_stride);
@@ -547,23 +634,19 @@ __global__ __launch_bounds__(256) void k_ref_matvec(RefMatvecArgs a) {
             act.y = __fmul_rn(__fdiv_rn(gv.y, __fadd_rn(1.0f, expf_libm(-gv.y, a.expf))), uv.y);
             act.z = __fmul_rn(__fdiv_rn(gv.z, __fadd_rn(1.0f, expf_libm(-gv.z, a.expf))), uv.z);
             act.w = __fmul_rn(__fdiv_rn(gv.w, __fadd_rn(1.0f, expf_libm(-gv.w, a.expf))), uv.w);
-            if (i < n4) reinterpret_cast<f32x4*>(xs)[i] = act;
+            if (i < n4) *reinterpret_cast<f32x4*>(xs + xpad<BE>(4u * i)) = act;
         }
     } else {
         const f32x4* x4 = reinterpret_cast<const f32x4*>(x);
         for (uint32_t base = 0; base < n4; base += 512u) {
             const uint32_t i0 = base + tid, i1 = i0 + 256u;
             const f32x4 v0 = x4[i0 < n4 ? i0 : 0u], v1 = x4[i1 < n4 ? i1 : 0u];
-            if (i0 < n4) reinterpret_cast<f32x4*>(xs)[i0] = v0;
-            if (i1 < n4) reinterpret_cast<f32x4*>(xs)[i1] = v1;
+            if (i0 < n4) *reinterpret_cast<f32x4*>(xs + xpad<BE>(4u * i0)) = v0;
+            if (i1 < n4) *reinterpret_cast<f32x4*>(xs + xpad<BE>(4u * i1)) = v1;
         }
     }
     __syncthreads();
-    W += expert * slice_bytes;
-    const uint32_t row0 = bx * rpw, lr = tid / nb, b = tid % nb, row = row0 + lr;
-    if (lr < rpw && row < rows)
-        part[tid] = block_dot<T>(QRow{W, static_cast<uint64_t>(rows) * nb, static_cast<uint64_t>(row) * nb},
-                                 b, xs + b * BE);
+    if (active) part[tid] = ref_dot<T>(raw, xs + b * (BE + 4u));
     __syncthreads();
     if (tid < rpw && row0 + tid < rows) {
         float acc = 0.0f;
@@ -584,6 +667,15 @@ __global__ __launch_bounds__(256) void k_ref_linear_f32(RefMatvecArgs a) {
     const uint32_t cf = chain_floats(a.in);
     float* prod = lds;
     float* xs = lds + cf;
+    const float* w = reinterpret_cast<const float*>(a.W + static_cast<uint64_t>(row) * a.row_bytes);
+    // the first 2048 weights of the row go out before x is staged (the norm's
+    // serial sum runs while they arrive)
+    float w0[8];
+#pragma unroll
+    for (uint32_t k = 0; k < 8; ++k) {
+        const uint32_t i = tid + 256u * k;
+        w0[k] = w[i < a.in ? i : 0u];
+    }
     if (a.norm.w) {
         ref_norm_stage<256>(a.norm, a.in, xs, xs + a.in, xs + a.in + cf, s_scale, leader);
     } else {
@@ -591,13 +683,12 @@ __global__ __launch_bounds__(256) void k_ref_linear_f32(RefMatvecArgs a) {
         for (uint32_t i = tid; i < a.in; i += 256u) xs[i] = x[i];
         __syncthreads();
     }
-    const float* w = reinterpret_cast<const float*>(a.W + static_cast<uint64_t>(row) * a.row_bytes);
     for (uint32_t base = 0; base < a.in; base += 2048u) {
         float wv[8];
 #pragma unroll
         for (uint32_t k = 0; k < 8; ++k) {
             const uint32_t i = base + tid + 256u * k;
-            wv[k] = w[i < a.in ? i : 0u];
+            wv[k] = base == 0u ? w0[k] : w[i < a.in ? i : 0u];
         }
 #pragma unroll
         for (uint32_t k = 0; k < 8; ++k) {
@@ -843,7 +934,7 @@ uint32_t ref_block_elems(uint32_t type) {
 
 template <int T>
 hipError_t ref_matvec_t(const RefMatvecArgs& a, uint32_t blocks, uint32_t routes, hipStream_t s) {
-    size_t lds = (a.in + 256u) * sizeof(float);
+    size_t lds = (xpad_floats<RefBlock<T>::BE>(a.in) + 256u) * sizeof(float);
     if (a.norm.w) lds += (chain_floats(a.in) + a.in) * sizeof(float);
     hipLaunchKernelGGL(k_ref_matvec<T>, dim3(blocks, routes), dim3(256), lds, s, a);
     return hipGetLastError();
