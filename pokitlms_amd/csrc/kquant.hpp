@@ -190,6 +190,10 @@ struct UnitX {
     float s[B][R];
 };
 
+// The loads are unconditional (an absent unit's position is unit 0's, in
+// bounds) and the values are zeroed afterwards: a load inside a branch makes
+// the wave wait at the branch's end for every load issued before it, here
+// the weight loads the caller has just issued.
 template <int T, int UB, int B>
 __device__ __forceinline__ void load_unit_x(const float* x, uint32_t x_stride, const UnitPos& p,
                                             bool valid, UnitX<T, UB, B>& ux) {
@@ -201,8 +205,8 @@ __device__ __forceinline__ void load_unit_x(const float* x, uint32_t x_stride, c
             float sum = 0.0f;
 #pragma unroll
             for (int i = 0; i < UB; i += 4) {
-                float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-                if (valid) v = *reinterpret_cast<const float4*>(x + b * x_stride + p.col[r] + i);
+                float4 v = *reinterpret_cast<const float4*>(x + b * x_stride + p.col[r] + i);
+                if (!valid) v = make_float4(0.f, 0.f, 0.f, 0.f);
                 ux.v[b][r * UB + i + 0] = v.x;
                 ux.v[b][r * UB + i + 1] = v.y;
                 ux.v[b][r * UB + i + 2] = v.z;
