@@ -371,6 +371,15 @@ pk_hip_status pk_hip_dequantize_rows(pk_hip_ctx* ctx, const pk_hip_weight* weigh
                                      uint32_t expert, uint64_t first_row, uint32_t rows,
                                      float* out, char* error_buffer, size_t error_capacity);
 
+/* out[r] = rms_norm(x[r], w, eps) for rows r < rows of n values
+ * (src/rms_norm.cpp:9-27): the serial FP32 sum of the squares x_i * x_i,
+ * scale = 1 / sqrt(sum / n + eps), out_i = (x_i * scale) * w_i -- bit for bit
+ * the reference's result, with the same kernel the reference-order decode
+ * uses for its norms.  Host buffers x and out [rows][n], w [n]; n <= 8192. */
+pk_hip_status pk_hip_rmsnorm(pk_hip_ctx* ctx, const float* x, const float* w, uint32_t rows,
+                             uint32_t n, float eps, float* out, char* error_buffer,
+                             size_t error_capacity);
+
 /* Checksums of the reference-order decode's expf (no counterpart in the
  * reference; it pins the device side of the host libm's expf, which the
  * reference calls in the softmax and SwiGLU, src/kv_cache.cpp:249,

@@ -71,6 +71,8 @@ class Oracle:
             L.pko_expf_block_sums.argtypes = [ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32,
                                               ctypes.c_void_p, ctypes.c_uint32]
             L.pko_expf_block_sums.restype = None
+            L.pko_rms_norm.argtypes = [_f32p, _f32p, ctypes.c_uint64, ctypes.c_uint64, ctypes.c_float,
+                                       _f32p]
             L.pko_linear.argtypes = [ctypes.c_uint32, _u8p, ctypes.c_uint64, ctypes.c_uint64,
                                      ctypes.c_uint64, _f32p, _f32p]
             L.pko_dequantize_row.argtypes = [ctypes.c_uint32, _u8p, ctypes.c_uint64, _f32p,
@@ -90,6 +92,8 @@ class Oracle:
                                         _f32p, _f32p, _u32p, _f32p]
         else:
             L.pkref_row_workers.restype = ctypes.c_uint
+            L.pkref_rms_norm.argtypes = [_f32p, _f32p, ctypes.c_uint64, ctypes.c_uint64,
+                                         ctypes.c_float, _f32p]
             L.pkref_tensor_linear.argtypes = [ctypes.c_uint32, ctypes.c_uint64, ctypes.c_uint64,
                                               _u8p, ctypes.c_uint64, _f32p, _f32p]
             L.pkref_tensor_linear_repeat.argtypes = [ctypes.c_uint32, ctypes.c_uint64,
@@ -161,6 +165,18 @@ class Oracle:
         if rc:
             raise OracleError(rc, "linear_repeat")
         return y
+
+    def rms_norm(self, x: np.ndarray, w: np.ndarray, eps: float) -> np.ndarray:
+        """rms_norm of each row (src/rms_norm.cpp:9-27)."""
+        xx = np.ascontiguousarray(x, dtype=np.float32)
+        rows, n = (1, xx.size) if xx.ndim == 1 else xx.shape
+        ww = np.ascontiguousarray(w, dtype=np.float32).reshape(-1)
+        out = np.empty_like(xx)
+        fn = self.lib.pko_rms_norm if self.kind == "port" else self.lib.pkref_rms_norm
+        rc = fn(_fp(xx), _fp(ww), rows, n, float(eps), _fp(out))
+        if rc:
+            raise OracleError(rc, "rms_norm")
+        return out
 
     def dequantize_row(self, gtype: int, encoded: np.ndarray, count: int) -> np.ndarray:
         e = np.ascontiguousarray(encoded, dtype=np.uint8)

@@ -642,3 +642,22 @@ void pko_expf_block_sums(uint32_t first_bits, uint32_t block_size, uint32_t n_bl
     for (uint32_t t = 0; t < threads; ++t)
         if (created[t]) pthread_join(th[t], NULL);
 }
+
+/* rms_norm (src/rms_norm.cpp:9-27): sum_squares = dot_f32(x, x, n), the serial
+ * unfused chain of src/simd_kernels.hpp:12-24 (x86 branch); mean = sum / n;
+ * scale = 1 / sqrt(mean + eps); out_i = (x_i * scale) * w_i
+ * (rms_scale_f32, simd_kernels.hpp:109-122).  Rows of n values, row-major. */
+int pko_rms_norm(const float* x, const float* w, uint64_t rows, uint64_t n, float eps,
+                 float* out) {
+    if (!x || !w || !out || n == 0) return 1;
+    for (uint64_t r = 0; r < rows; ++r) {
+        const float* xr = x + r * n;
+        float* o = out + r * n;
+        float sum = 0.0f;
+        for (uint64_t i = 0; i < n; ++i) sum += xr[i] * xr[i];
+        const float mean = sum / (float)n;
+        const float scale = 1.0f / sqrtf(mean + eps);
+        for (uint64_t i = 0; i < n; ++i) o[i] = xr[i] * scale * w[i];
+    }
+    return 0;
+}

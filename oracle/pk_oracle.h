@@ -109,6 +109,11 @@ int pko_moe35_block(const float* router, uint32_t hidden, uint32_t n_experts, ui
                     const uint8_t* sup, uint32_t sdown_type, const uint8_t* sdown,
                     const float* x, float* y, uint32_t* ids, float* weights);
 
+/* rms_norm of each row (src/rms_norm.cpp:9-27): serial FP32 sum of squares,
+ * scale = 1 / sqrt(sum / n + eps), out_i = (x_i * scale) * w_i. */
+int pko_rms_norm(const float* x, const float* w, uint64_t rows, uint64_t n, float eps,
+                 float* out);
+
 /* The host libm's expf over float bit patterns, as block checksums: block k
  * covers b = first_bits + k * block_size + i (i < block_size) and sums[k] =
  * sum over i of (((uint64) bits(expf(x_b)) << 32) | b) * 0xD6E8FEB86659FD93

@@ -12,6 +12,7 @@
 #include "pokitlms/model/tensor_linear.hpp"
 #include "pokitlms/model/tensor_reader.hpp"
 #include "pokitlms/ops/quantized_linear.hpp"
+#include "pokitlms/ops/rms_norm.hpp"
 
 #include <algorithm>
 #include <chrono>
@@ -83,6 +84,19 @@ int pkref_tensor_linear_repeat(std::uint32_t type, std::uint64_t in, std::uint64
             pokitlms::model::tensor_linear(reader, std::span<const float>(x, in),
                                            std::span<float>(y, rows));
         }
+        return 0;
+    } catch (...) {
+        return status_of_current_exception();
+    }
+}
+
+// The reference rms_norm (src/rms_norm.cpp:9-27) of each row.
+int pkref_rms_norm(const float* x, const float* w, std::uint64_t rows, std::uint64_t n, float eps,
+                   float* out) {
+    try {
+        for (std::uint64_t r = 0; r < rows; ++r)
+            pokitlms::rms_norm(std::span<const float>(x + r * n, n), std::span<const float>(w, n),
+                               std::span<float>(out + r * n, n), eps);
         return 0;
     } catch (...) {
         return status_of_current_exception();

@@ -32,7 +32,7 @@ EXPORTS = (
     "pk_hip_moe_prefill_async", "pk_hip_qwen3moe_create", "pk_hip_qwen3moe_destroy",
     "pk_hip_qwen3moe_generate", "pk_hip_synth_weight", "pk_hip_matvec_reference_order",
     "pk_hip_weight_download", "pk_hip_moe_decode_noalloc", "pk_hip_dequantize_rows",
-    "pk_hip_expf_block_sums",
+    "pk_hip_expf_block_sums", "pk_hip_rmsnorm",
 )
 
 
@@ -130,6 +130,9 @@ def lib() -> ctypes.CDLL:
     L.pk_hip_expf_block_sums.restype = ctypes.c_int
     L.pk_hip_expf_block_sums.argtypes = [vp, vp, u64, ctypes.c_uint32, ctypes.c_uint32,
                                          ctypes.c_uint32, vp, ctypes.c_char_p, ctypes.c_size_t]
+    L.pk_hip_rmsnorm.restype = ctypes.c_int
+    L.pk_hip_rmsnorm.argtypes = [vp, vp, vp, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_float, vp,
+                                 ctypes.c_char_p, ctypes.c_size_t]
     L.pk_hip_weight_download.restype = ctypes.c_int
     L.pk_hip_weight_download.argtypes = [vp, vp, u64, ctypes.c_char_p, ctypes.c_size_t]
     L.pk_hip_matvec.restype = ctypes.c_int

@@ -328,6 +328,20 @@ class HipBackend:
                err)
         return out
 
+    def rmsnorm(self, x: np.ndarray, w: np.ndarray, eps: float) -> np.ndarray:
+        """rms_norm of each row of x (the reference's src/rms_norm.cpp:9-27),
+        bit for bit."""
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        rows, n = (1, x.size) if x.ndim == 1 else x.shape
+        w = np.ascontiguousarray(w, dtype=np.float32).reshape(-1)
+        if w.size != n:
+            raise ValueError("weight size must equal the row width")
+        out = np.empty_like(x)
+        err = ctypes.create_string_buffer(_ERRBUF)
+        _raise(_abi.lib().pk_hip_rmsnorm(self.handle, x.ctypes.data, w.ctypes.data, rows, n,
+                                         float(eps), out.ctypes.data, err, _ERRBUF), err)
+        return out
+
     def expf_block_sums(self, pairs: np.ndarray, first_bits: int, block_size: int,
                         n_blocks: int) -> np.ndarray:
         """Checksums of the reference-order expf over float bit patterns

@@ -1627,6 +1627,41 @@ pk_hip_status pk_hip_dequantize_rows(pk_hip_ctx* ctx, const pk_hip_weight* w, ui
     });
 }
 
+pk_hip_status pk_hip_rmsnorm(pk_hip_ctx* ctx, const float* x, const float* w, uint32_t rows,
+                             uint32_t n, float eps, float* out, char* err, size_t cap) {
+    return guarded(ctx, err, cap, [&] {
+        require_usable(ctx);
+        if (!x || !w || !out) throw ArgError("input, weight and output are required");
+        if (rows == 0) return;
+        if (n == 0 || n > pk::kMaxRefWidth) throw ArgError("row width must be between 1 and 8192");
+        std::lock_guard lock(ctx->mutex);
+        ctx->set_device();
+        const size_t total = static_cast<size_t>(rows) * n;
+        DeviceBuffer<float> dx, dw;
+        try {
+            dx.ensure(total);
+            dw.ensure(n);
+            check(hipMemcpyAsync(dx.ptr, x, total * sizeof(float), hipMemcpyHostToDevice, ctx->stream),
+                  "copy rows");
+            check(hipMemcpyAsync(dw.ptr, w, n * sizeof(float), hipMemcpyHostToDevice, ctx->stream),
+                  "copy weight");
+            launch_checked(pk::launch_ref_rmsnorm(dx.ptr, pk::RefResidual{nullptr, nullptr, nullptr, 0},
+                                                  dw.ptr, dx.ptr, n, rows, eps, ctx->stream),
+                           "rmsnorm launch");
+            check(hipMemcpyAsync(out, dx.ptr, total * sizeof(float), hipMemcpyDeviceToHost, ctx->stream),
+                  "copy output");
+            check(hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
+        } catch (...) {
+            (void)hipStreamSynchronize(ctx->stream);
+            dx.release();
+            dw.release();
+            throw;
+        }
+        dx.release();
+        dw.release();
+    });
+}
+
 pk_hip_status pk_hip_expf_block_sums(pk_hip_ctx* ctx, const uint32_t* pairs, uint64_t count,
                                      uint32_t first_bits, uint32_t block_size, uint32_t n_blocks,
                                      uint64_t* sums, char* err, size_t cap) {

@@ -135,6 +135,103 @@ __device__ float serial_sum(const float* p, uint32_t n, float s) {
     return s;
 }
 
+// v of the lane the DPP control selects, 0 where it selects none.
+template <int CTRL, int ROW_MASK = 0xf>
+__device__ __forceinline__ uint32_t dpp_u0(uint32_t v) {
+    return static_cast<uint32_t>(
+        __builtin_amdgcn_update_dpp(0, static_cast<int>(v), CTRL, ROW_MASK, 0xf, false));
+}
+
+// Inclusive prefix sum of uint32 values over the 64 lanes of a wave.
+__device__ __forceinline__ uint32_t wave_scan_u32(uint32_t v) {
+    v += dpp_u0<0x111>(v);       // row_shr:1
+    v += dpp_u0<0x112>(v);       // row_shr:2
+    v += dpp_u0<0x114>(v);       // row_shr:4
+    v += dpp_u0<0x118>(v);       // row_shr:8
+    v += dpp_u0<0x142, 0xa>(v);  // row_bcast:15 into rows 1, 3
+    v += dpp_u0<0x143, 0xc>(v);  // row_bcast:31 into rows 2, 3
+    return v;
+}
+
+// ((0 + p[0]) + p[1]) + ... + p[n - 1] for values p >= 0 in LDS (the squares
+// of an RMSNorm), bit for bit the serial FP32 chain, computed by one whole
+// wave (every lane active; the result is uniform).
+//
+// While the running sum s stays in one binade [2^e, 2^(e+1)), every step
+// rounds to that binade's grid u = 2^(e-23): RN(s + p) = s + u * rn(p / u),
+// except when p / u is exactly half an integer (the tie goes to the even
+// multiple of u, which depends on s) or when s + p reaches 2^(e+1) (the grid
+// changes).  Between such steps the chain is therefore an integer prefix sum
+// of rn(p / u), which the wave forms 256 values at a time (four per lane, a
+// wave scan); the step that ties, crosses or meets a non-finite value is then
+// added by one FP32 add and the scan restarts after it.  The first 64 values
+// (where the binade still changes at almost every step), a zero or extreme
+// running sum and non-finite values take the plain serial add.
+__device__ float serial_sum_nonneg(const float* p, uint32_t n) {
+    const uint32_t lane = threadIdx.x & 63u;
+    constexpr uint32_t kTop = 1u << 24;  // a + P reaching this is a binade crossing
+    float s = 0.0f;
+    uint32_t t = 0;
+    const uint32_t head = n < 64u ? n : 64u;
+    for (; t < head; ++t) s = __fadd_rn(s, p[t]);
+    while (t < n) {  // uniform
+        const uint32_t bits = __builtin_bit_cast(uint32_t, s);
+        const int e = static_cast<int>((bits >> 23) & 0xffu) - 127;
+        if (!(s > 0.0f) || !(s < INFINITY) || e < -100 || e > 100) {  // uniform
+            s = __fadd_rn(s, p[t]);
+            ++t;
+            continue;
+        }
+        const float inv_u = __builtin_bit_cast(float, static_cast<uint32_t>(150 - e) << 23);  // 2^(23-e)
+        const float u = __builtin_bit_cast(float, static_cast<uint32_t>(104 + e) << 23);      // 2^(e-23)
+        const uint32_t a = static_cast<uint32_t>(__fmul_rn(s, inv_u));  // in [2^23, 2^24), exact
+        // the next (up to) 256 values, four consecutive per lane
+        const uint32_t i0 = t + 4u * lane;
+        uint32_t cm[4];
+        bool cut[4];
+        uint32_t c = 0u;
+#pragma unroll
+        for (uint32_t i = 0; i < 4; ++i) {
+            const uint32_t idx = i0 + i;
+            const bool ok = idx < n;
+            const float x = ok ? p[ok ? idx : 0u] : 0.0f;
+            const float q = __fmul_rn(x, inv_u);  // exact: a power-of-two scale
+            const float r = __builtin_rintf(q);  // the nearest multiple (ties handled below)
+            const bool tie = __fsub_rn(q, floorf(q)) == 0.5f;
+            const uint32_t m = static_cast<uint32_t>(fminf(r, 16777216.0f));  // 2^24 forces a cut
+            c = min(c + m, kTop);  // saturated: a lane past 2^24 has already cut
+            cm[i] = c;
+            cut[i] = ok && (tie || !(x < INFINITY));
+        }
+        const uint32_t incl = wave_scan_u32(c);
+        const uint32_t excl = incl - c;
+        uint32_t first = 4u, before = excl;  // first cut of this lane, prefix in front of it
+#pragma unroll
+        for (int i = 3; i >= 0; --i) {
+            const uint32_t P = excl + cm[i];
+            if (i0 + static_cast<uint32_t>(i) < n && (cut[i] || a + P >= kTop)) {
+                first = static_cast<uint32_t>(i);
+                before = i ? excl + cm[i - 1] : excl;
+            }
+        }
+        const uint64_t any = __ballot(first < 4u);
+        if (any == 0u) {  // uniform: the whole chunk stays on the grid
+            const uint32_t total = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(incl), 63));
+            s = __fmul_rn(static_cast<float>(a + total), u);  // a + total < 2^24: exact
+            t = n - t > 256u ? t + 256u : n;
+        } else {
+            const int L = __ffsll(static_cast<unsigned long long>(any)) - 1;
+            const uint32_t fi = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(first), L));
+            const uint32_t pb = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(before), L));
+            const uint32_t b = t + 4u * static_cast<uint32_t>(L) + fi;
+            s = __fmul_rn(static_cast<float>(a + pb), u);  // the sum just before element b: exact
+            s = __fadd_rn(s, p[b]);
+            t = b + 1u;
+        }
+    }
+    return s;
+}
+
 // s + ((ds * q) - dm) * x: one element of a K-quant block dot (decode_q4_k /
 // decode_q5_k weight, then dot_f32's rounded product and add).
 __device__ __forceinline__ float kq_step(float s, float ds, float dm, float q, float x) {
@@ -476,7 +573,10 @@ __device__ void ref_norm_stage(const RefNormIn& p, uint32_t n, float* xs, float*
         }
     }
     __syncthreads();
-    if (tid == 0) s_scale = 1.0f / sqrtf(serial_sum(sq, n, 0.0f) / static_cast<float>(n) + p.eps);
+    if (tid < 64u) {  // wave 0
+        const float sum = serial_sum_nonneg(sq, n);
+        if (tid == 0) s_scale = 1.0f / sqrtf(sum / static_cast<float>(n) + p.eps);
+    }
     __syncthreads();
     const float scale = s_scale;
     for (uint32_t i = tid; i < n; i += NT) {
@@ -757,9 +857,9 @@ __global__ __launch_bounds__(1024) void k_ref_rmsnorm(float* x, RefResidual res,
     for (int k = 0; k < PER; ++k)
         if (tid + 1024u * k < n) sq[tid + 1024u * k] = __fmul_rn(v[k], v[k]);
     __syncthreads();
-    if (tid == 0) {
-        const float sum = serial_sum(sq, n, 0.0f);
-        s_scale = 1.0f / sqrtf(sum / static_cast<float>(n) + eps);
+    if (tid < 64u) {  // wave 0
+        const float sum = serial_sum_nonneg(sq, n);
+        if (tid == 0) s_scale = 1.0f / sqrtf(sum / static_cast<float>(n) + eps);
     }
     __syncthreads();
     const float scale = s_scale;
