@@ -155,25 +155,25 @@ __device__ __forceinline__ uint32_t wave_scan_u32(uint32_t v) {
 
 // ((0 + p[0]) + p[1]) + ... + p[n - 1] for values p >= 0 in LDS (the squares
 // of an RMSNorm), bit for bit the serial FP32 chain, computed by one whole
-// wave (every lane active; the result is uniform).
+// wave (every lane active; the result is uniform).  p is readable for
+// chain_floats(n) floats.
 //
 // While the running sum s stays in one binade [2^e, 2^(e+1)), every step
 // rounds to that binade's grid u = 2^(e-23): RN(s + p) = s + u * rn(p / u),
 // except when p / u is exactly half an integer (the tie goes to the even
 // multiple of u, which depends on s) or when s + p reaches 2^(e+1) (the grid
 // changes).  Between such steps the chain is therefore an integer prefix sum
-// of rn(p / u), which the wave forms 256 values at a time (four per lane, a
-// wave scan); the step that ties, crosses or meets a non-finite value is then
-// added by one FP32 add and the scan restarts after it.  The first 64 values
-// (where the binade still changes at almost every step), a zero or extreme
-// running sum and non-finite values take the plain serial add.
+// of rn(p / u), which the wave forms 256 values at a time (four consecutive
+// per lane, a wave scan).  The first lane holding a tie, a non-finite value or
+// the step that reaches 2^(e+1) starts from the exact sum in front of it and
+// adds its four values by plain FP32 adds; the scan restarts after them.  The
+// first 64 values (where the binade still changes at almost every step), a
+// zero or extreme running sum take the plain serial add.
 __device__ float serial_sum_nonneg(const float* p, uint32_t n) {
     const uint32_t lane = threadIdx.x & 63u;
     constexpr uint32_t kTop = 1u << 24;  // a + P reaching this is a binade crossing
-    float s = 0.0f;
-    uint32_t t = 0;
-    const uint32_t head = n < 64u ? n : 64u;
-    for (; t < head; ++t) s = __fadd_rn(s, p[t]);
+    uint32_t t = n < 64u ? n : 64u;
+    float s = serial_sum(p, t, 0.0f);
     while (t < n) {  // uniform
         const uint32_t bits = __builtin_bit_cast(uint32_t, s);
         const int e = static_cast<int>((bits >> 23) & 0xffu) - 127;
@@ -185,48 +185,40 @@ __device__ float serial_sum_nonneg(const float* p, uint32_t n) {
         const float inv_u = __builtin_bit_cast(float, static_cast<uint32_t>(150 - e) << 23);  // 2^(23-e)
         const float u = __builtin_bit_cast(float, static_cast<uint32_t>(104 + e) << 23);      // 2^(e-23)
         const uint32_t a = static_cast<uint32_t>(__fmul_rn(s, inv_u));  // in [2^23, 2^24), exact
-        // the next (up to) 256 values, four consecutive per lane
         const uint32_t i0 = t + 4u * lane;
-        uint32_t cm[4];
-        bool cut[4];
+        float x[4];
+#pragma unroll
+        for (uint32_t i = 0; i < 4; ++i) x[i] = p[min(i0 + i, n - 1u)];
         uint32_t c = 0u;
+        bool stop = false;
 #pragma unroll
         for (uint32_t i = 0; i < 4; ++i) {
-            const uint32_t idx = i0 + i;
-            const bool ok = idx < n;
-            const float x = ok ? p[ok ? idx : 0u] : 0.0f;
-            const float q = __fmul_rn(x, inv_u);  // exact: a power-of-two scale
-            const float r = __builtin_rintf(q);  // the nearest multiple (ties handled below)
-            const bool tie = __fsub_rn(q, floorf(q)) == 0.5f;
-            const uint32_t m = static_cast<uint32_t>(fminf(r, 16777216.0f));  // 2^24 forces a cut
-            c = min(c + m, kTop);  // saturated: a lane past 2^24 has already cut
-            cm[i] = c;
-            cut[i] = ok && (tie || !(x < INFINITY));
+            const float xi = i0 + i < n ? x[i] : 0.0f;
+            const float q = __fmul_rn(xi, inv_u);  // exact: a power-of-two scale
+            const float r = __builtin_rintf(q);
+            // a tie (|q - r| is exact) or a non-finite value
+            stop = stop || fabsf(__fsub_rn(q, r)) == 0.5f || !(xi < INFINITY);
+            c += static_cast<uint32_t>(fminf(r, 16777216.0f));  // 2^24 forces a stop
         }
+        c = min(c, kTop);  // at most 2^24 per lane: the wave's sum fits 32 bits
         const uint32_t incl = wave_scan_u32(c);
-        const uint32_t excl = incl - c;
-        uint32_t first = 4u, before = excl;  // first cut of this lane, prefix in front of it
-#pragma unroll
-        for (int i = 3; i >= 0; --i) {
-            const uint32_t P = excl + cm[i];
-            if (i0 + static_cast<uint32_t>(i) < n && (cut[i] || a + P >= kTop)) {
-                first = static_cast<uint32_t>(i);
-                before = i ? excl + cm[i - 1] : excl;
-            }
-        }
-        const uint64_t any = __ballot(first < 4u);
+        const uint64_t any = __ballot(stop || a + incl >= kTop);
         if (any == 0u) {  // uniform: the whole chunk stays on the grid
             const uint32_t total = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(incl), 63));
             s = __fmul_rn(static_cast<float>(a + total), u);  // a + total < 2^24: exact
             t = n - t > 256u ? t + 256u : n;
         } else {
             const int L = __ffsll(static_cast<unsigned long long>(any)) - 1;
-            const uint32_t fi = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(first), L));
-            const uint32_t pb = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(before), L));
-            const uint32_t b = t + 4u * static_cast<uint32_t>(L) + fi;
-            s = __fmul_rn(static_cast<float>(a + pb), u);  // the sum just before element b: exact
-            s = __fadd_rn(s, p[b]);
-            t = b + 1u;
+            const uint32_t pb = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(incl - c), L));
+            s = __fmul_rn(static_cast<float>(a + pb), u);  // the sum in front of lane L: exact
+            const uint32_t b = t + 4u * static_cast<uint32_t>(L);
+            float y[4];
+#pragma unroll
+            for (uint32_t i = 0; i < 4; ++i) y[i] = p[min(b + i, n - 1u)];
+#pragma unroll
+            for (uint32_t i = 0; i < 4; ++i)
+                if (b + i < n) s = __fadd_rn(s, y[i]);
+            t = n - b > 4u ? b + 4u : n;
         }
     }
     return s;

@@ -26,15 +26,12 @@ def serial_sum(p):
 
 def segmented_sum(p):
     """serial_sum_nonneg of exact.hip, step for step in float32 (chunks of 256,
-    four values per lane, the wave's scan as a cumulative sum)."""
+    four values per lane, the wave's scan as a cumulative sum, the first lane
+    that ties, meets a non-finite value or crosses the binade added serially)."""
     p = np.asarray(p, F)
     n = p.size
-    s = F(0.0)
-    t = 0
-    head = min(n, 64)
-    while t < head:
-        s = F(s + p[t])
-        t += 1
+    t = min(n, 64)
+    s = serial_sum(p[:t])
     top = 1 << 24
     while t < n:
         e = int((np.frombuffer(s.tobytes(), np.uint32)[0] >> 23) & 0xff) - 127
@@ -45,46 +42,33 @@ def segmented_sum(p):
         inv_u = F(2.0) ** (23 - e)
         u = F(2.0) ** (e - 23)
         a = int(F(s * inv_u))
-        chunk = p[t:t + 256]
-        lanes = []
+        incl = 0
+        stop_lane = None
         for L in range(64):
             c = 0
-            vals = []
+            stop = False
             for i in range(4):
-                idx = 4 * L + i
-                if idx < chunk.size:
-                    x = chunk[idx]
-                    q = F(x * inv_u)
-                    r = np.rint(q)
-                    tie = F(q - np.floor(q)) == F(0.5)
-                    m = int(min(r, F(16777216.0)))
-                    c = min(c + m, top)
-                    vals.append((idx, c, tie or not np.isfinite(x)))
-                else:
-                    vals.append((idx, c, False))
-            lanes.append((c, vals))
-        excl = 0
-        cut_at = None
-        total = 0
-        for c, vals in lanes:
-            prev = excl
-            for idx, cm, cut in vals:
-                if idx < chunk.size and (cut or a + excl + cm >= top):
-                    cut_at = (idx, prev)
-                    break
-                prev = excl + cm
-            if cut_at:
+                idx = t + 4 * L + i
+                x = p[idx] if idx < n else F(0.0)
+                q = F(x * inv_u)
+                r = np.rint(q)
+                stop = stop or abs(F(q - r)) == F(0.5) or not (x < np.inf)
+                c += int(np.fmin(r, F(16777216.0)))
+            c = min(c, top)
+            if stop or a + incl + c >= top:
+                stop_lane = (L, incl)
                 break
-            excl += c
-            total = excl
-        if cut_at is None:
-            s = F(F(a + total) * u)
+            incl += c
+        if stop_lane is None:
+            s = F(F(a + incl) * u)
             t = min(t + 256, n)
         else:
-            idx, before = cut_at
+            L, before = stop_lane
             s = F(F(a + before) * u)
-            s = F(s + chunk[idx])
-            t = t + idx + 1
+            b = t + 4 * L
+            for idx in range(b, min(b + 4, n)):
+                s = F(s + p[idx])
+            t = min(b + 4, n)
     return s
 
 
