@@ -19,7 +19,9 @@
 //     gate and up GEMMs on bf16 MFMA with exact products (x split into three
 //     bf16 planes, the quantised weights as bf16 integers, the scales applied
 //     per group outside the MFMA), and the SwiGLU epilogue, which writes the
-//     activations already split for the down GEMM.
+//     activations already split for the down GEMM.  Q4_K and Q6_K weights go
+//     from memory straight into the registers of the wave that uses them
+//     (k_expert_gemm_w); the other formats are staged through LDS.
 //  5. k_expert_gemm<down>: per tile and 128 hidden rows; each output row goes
 //     to its (token, route) slot.
 //  6. k_combine: y = ((0 + p0*o0) + p1*o1) + ... per token in route order
@@ -89,68 +91,6 @@ __device__ __forceinline__ void raw32_load(const QRow& row, uint32_t k0, Raw32<T
         using L = Planar<T_Q4_0>;
         ld_words<4>(field_ptr<L::QS, 16>(row, k0 / 32u), r.q);
         r.d = ld_u16(field_ptr<L::D, 2>(row, k0 / 32u));
-    }
-}
-
-// Q4_K and Q6_K in the expert GEMM: a thread loads a run of its row's
-// stages at once into registers (a unit) and takes each 32-value group's
-// fields out of it, so the fields several groups share are fetched once per
-// unit, not once per group.
-//  * Q4_K: the whole 144-byte block (36 words), eight stages; the header is
-//    shared by all eight groups, each nibble byte by two.
-//  * Q6_K: one 128-value half of a block, four stages: its 64 ql bytes (each
-//    shared by two groups), 32 qh bytes (shared by four), 8 scale bytes and d,
-//    each from its own plane.
-// (Q5_K's 44-word blocks would spill.)
-template <int T>
-constexpr bool kq_blocked() { return T == T_Q4_K || T == T_Q6_K; }
-
-template <int T>
-struct KqUnit;
-template <>
-struct KqUnit<T_Q4_K> {
-    static constexpr uint32_t STAGES = 8, PER_ROW_BLOCK = 1;
-    uint32_t w[36];
-};
-template <>
-struct KqUnit<T_Q6_K> {
-    static constexpr uint32_t STAGES = 4, PER_ROW_BLOCK = 2;
-    uint32_t ql[16], qh[8], sc[2];
-    uint32_t d;
-};
-
-// Unit u of a row: block u / PER_ROW_BLOCK (Q6_K: half u % 2 of it).
-template <int T>
-__device__ __forceinline__ void kq_unit_load(const QRow& row, uint32_t u, KqUnit<T>& U) {
-    if constexpr (T == T_Q4_K) {
-        ld_words<36>(block_ptr<144>(row, u), U.w);
-    } else {
-        using L = Planar<T_Q6_K>;
-        const uint32_t b = u / 2u, h = u % 2u;
-        ld_words<16>(field_ptr<L::QL, 128>(row, b) + 64u * h, U.ql);
-        ld_words<8>(field_ptr<L::QH, 64>(row, b) + 32u * h, U.qh);
-        ld_words<2>(field_ptr<L::SC, 16>(row, b) + 8u * h, U.sc);
-        U.d = ld_u16(field_ptr<L::D, 2>(row, b));
-    }
-}
-
-// The fields raw32_load would read for stage j of the unit in U (Q4_K: group
-// j of 8 in the block; Q6_K: group 4h + j of the block).
-template <int T>
-__device__ __forceinline__ void raw32_from_unit(const KqUnit<T>& U, uint32_t j, Raw32<T>& r) {
-    if constexpr (T == T_Q4_K) {
-#pragma unroll
-        for (uint32_t i = 0; i < 4; ++i) r.h[i] = U.w[i];
-#pragma unroll
-        for (uint32_t i = 0; i < 8; ++i) r.q[i] = U.w[4u + 8u * (j / 2u) + i];
-    } else {
-        const uint32_t o = 8u * (j & 1u);  // low or high 32 ql bytes of the half
-#pragma unroll
-        for (uint32_t i = 0; i < 8; ++i) r.ql[i] = U.ql[o + i];
-#pragma unroll
-        for (uint32_t i = 0; i < 8; ++i) r.qh[i] = U.qh[i];
-        r.sc = (U.sc[j / 2u] >> (16u * (j & 1u))) & 0xffffu;  // int8 scales of both 16-halves
-        r.d = U.d;
     }
 }
 
@@ -747,6 +687,208 @@ __device__ __forceinline__ void gemm_compute(const GemmStage<TW, DUAL>& st, f32x
     }
 }
 
+// ---------------------------------------------------------------------------
+// Q4_K / Q6_K weights: each wave streams its own rows into registers.
+//
+// A wave computes rows n (lane % 32) of its two 32-row matrices (gate and up,
+// or the two down row blocks) and gives the MFMA its B operand straight from
+// registers: lane (n, kq = lane / 32) holds, of every 32-value stage of its
+// row, the elements 8kq .. 8kq + 7 (first MFMA of the stage) and
+// 16 + 8kq .. 16 + 8kq + 7 (second), which is the B fragment of
+// v_mfma_f32_32x32x16_bf16, and computes the row's scales itself.  Only the
+// activation planes, which the four waves share, pass through LDS, so a
+// workgroup needs a fraction of the LDS of the staged-weight kernel and more
+// waves fit on a SIMD to hide each other's waits.
+//
+// A lane's unit is half a block (128 values, four stages) of one row:
+//  * Q4_K: the 16-byte header and, of the half's two 32-byte nibble chunks,
+//    bytes 8kq..8kq+7 and 16+8kq..16+8kq+7 of each (stage 2c of the half:
+//    chunk c's low nibbles, stage 2c + 1: its high nibbles);
+//  * Q6_K: bytes 8kq.. and 16+8kq.. of each of the half's two 32-byte ql runs
+//    (stages g and g + 2 share run g & 1: low and high nibbles), of its 32 qh
+//    bytes (all four stages: bits 2g, 2g + 1), its 8 int8 scales and d.
+template <int T> struct WUnit;
+template <> struct WUnit<T_Q4_K> { uint32_t h[4]; uint32_t q[8]; };
+template <> struct WUnit<T_Q6_K> { uint32_t ql[8], qh[4], sc[2]; uint32_t d; };
+
+__device__ __forceinline__ void ld8(const uint8_t* p, uint32_t& lo, uint32_t& hi) {
+    const uint2 v = *reinterpret_cast<const uint2*>(__builtin_assume_aligned(p, 8));
+    lo = v.x;
+    hi = v.y;
+}
+
+// Unit u of the row (block u / 2, half u % 2) for lanes kq.
+template <int T>
+__device__ __forceinline__ void wunit_load(const QRow& row, uint32_t u, uint32_t kq, WUnit<T>& U) {
+    const uint32_t b = u / 2u, hh = u % 2u;
+    if constexpr (T == T_Q4_K) {
+        const uint8_t* blk = block_ptr<144>(row, b);
+        ld_words<4>(blk, U.h);
+        const uint8_t* qs = blk + 16u + 64u * hh + 8u * kq;
+#pragma unroll
+        for (uint32_t i = 0; i < 4; ++i) ld8(qs + 16u * i, U.q[2u * i], U.q[2u * i + 1u]);
+    } else {
+        using L = Planar<T_Q6_K>;
+        const uint8_t* ql = field_ptr<L::QL, 128>(row, b) + 64u * hh + 8u * kq;
+#pragma unroll
+        for (uint32_t i = 0; i < 4; ++i) ld8(ql + 16u * i, U.ql[2u * i], U.ql[2u * i + 1u]);
+        const uint8_t* qh = field_ptr<L::QH, 64>(row, b) + 32u * hh + 8u * kq;
+        ld8(qh, U.qh[0], U.qh[1]);
+        ld8(qh + 16u, U.qh[2], U.qh[3]);
+        ld8(field_ptr<L::SC, 16>(row, b) + 8u * hh, U.sc[0], U.sc[1]);
+        U.d = ld_u16(field_ptr<L::D, 2>(row, b));
+    }
+}
+
+// Stage j (0..3) of the unit in half hh of its block: the lane's two bf16x8
+// B fragments, the scale of each (Q4_K: one scale group per stage, Q6_K: one
+// per fragment) and the bias operand cb = cn of scale group kq of the stage
+// (0 where the stage has a single group and kq = 1); weights are
+// ds * f + cn per group as in raw32_bf16.
+template <int T>
+__device__ __forceinline__ void wunit_stage(const WUnit<T>& U, uint32_t hh, uint32_t j, uint32_t kq,
+                                            bf16x8 (&b)[2], float (&ds)[2], float& cb) {
+    uint32_t w[8];
+    if constexpr (T == T_Q4_K) {
+        const uint32_t c = j / 2u, hi = j & 1u;
+#pragma unroll
+        for (uint32_t i = 0; i < 4; ++i) {
+            const uint32_t q = (hi ? U.q[4u * c + i] >> 4 : U.q[4u * c + i]) & 0x0f0f0f0fu;
+            bf16_bytes(q, w[2u * i], w[2u * i + 1u]);
+        }
+        const float d = half_bits_to_float(U.h[0] & 0xffffu);
+        const float dmin = half_bits_to_float(U.h[0] >> 16);
+        float sc, mn;
+        kq_scale_min(U.h, 4u * hh + j, sc, mn);
+        ds[0] = ds[1] = __fmul_rn(d, sc);
+        cb = kq ? 0.0f : -__fmul_rn(dmin, mn);
+    } else {
+        const uint32_t r = 4u * (j & 1u), sh = j >= 2u ? 4u : 0u;
+#pragma unroll
+        for (uint32_t i = 0; i < 4; ++i) {
+            const uint32_t nib = (U.ql[r + i] >> sh) & 0x0f0f0f0fu;
+            const uint32_t hb = ((U.qh[i] >> (2u * j)) & 0x03030303u) << 4;
+            bf16_bytes(nib | hb, w[2u * i], w[2u * i + 1u]);
+        }
+        const float d = half_bits_to_float(U.d);
+        const uint32_t s2 = (U.sc[j / 2u] >> (16u * (j & 1u))) & 0xffffu;  // scales of the two halves
+        ds[0] = __fmul_rn(d, static_cast<float>(static_cast<int8_t>(s2 & 0xffu)));
+        ds[1] = __fmul_rn(d, static_cast<float>(static_cast<int8_t>(s2 >> 8)));
+        cb = __fmul_rn(-32.0f, kq ? ds[1] : ds[0]);
+    }
+    b[0] = __builtin_bit_cast(bf16x8, make_uint4(w[0], w[1], w[2], w[3]));
+    b[1] = __builtin_bit_cast(bf16x8, make_uint4(w[4], w[5], w[6], w[7]));
+}
+
+// Activation planes and group sums of one stage, shared by the workgroup.
+template <int TW, bool DUAL>
+struct alignas(16) GemmStageA {
+    using C = GemmCfg<TW, DUAL>;
+    uint8_t a[3 * kTileM * C::SR];  // planes hi, mid, lo: [m][k]
+    float xs[C::NG * kTileM];       // [g][m]
+};
+
+template <int TW, bool DUAL>
+__device__ __forceinline__ void gemm_store_a(GemmStageA<TW, DUAL>& st, const GemmPrefetch<TW, DUAL>& f,
+                                             const GemmSrc<TW, DUAL>& g) {
+    *reinterpret_cast<u32x4_t*>(st.a + g.adst0) = f.ap0;
+    *reinterpret_cast<u32x4_t*>(st.a + g.adst1) = f.ap1;
+    st.xs[g.xdst] = f.xs;
+}
+
+// One stage of one wave from register weights: the bias MFMA, then per
+// fragment h the three plane MFMAs; each scale group's sum is scaled into the
+// accumulator when it closes.
+template <int TW, bool DUAL>
+__device__ __forceinline__ void gemm_compute_w(const GemmStageA<TW, DUAL>& st, const WUnit<TW>& U0,
+                                               const WUnit<TW>& U1, uint32_t hh, uint32_t j,
+                                               f32x16& acc, f32x16& acc2) {
+    using C = GemmCfg<TW, DUAL>;
+    const uint32_t lane = threadIdx.x & 63u, m = lane % 32u, kq = lane / 32u;
+    bf16x8 b0[2], b1[2];
+    float d0[2], d1[2], c0, c1;
+    wunit_stage<TW>(U0, hh, j, kq, b0, d0, c0);
+    wunit_stage<TW>(U1, hh, j, kq, b1, d1, c1);
+    const float av = (C::NG == 1u && kq) ? 0.0f : st.xs[(C::NG == 1u ? 0u : kq) * kTileM + m];
+    acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av, c0, acc, 0, 0, 0);
+    acc2 = __builtin_amdgcn_mfma_f32_32x32x2f32(av, c1, acc2, 0, 0, 0);
+    f32x16 P, Q;
+#pragma unroll
+    for (uint32_t h = 0; h < 2; ++h) {
+        const uint32_t koff = (16u * h + 8u * kq) * 2u;
+        const bf16x8 a0 = lds_bf16x8(st.a + (0u * kTileM + m) * C::SR + koff);
+        const bf16x8 a1 = lds_bf16x8(st.a + (1u * kTileM + m) * C::SR + koff);
+        const bf16x8 a2 = lds_bf16x8(st.a + (2u * kTileM + m) * C::SR + koff);
+        const bool first = C::G == 16u || h == 0u;
+        P = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a2, b0[h], first ? f32x16{} : P, 0, 0, 0);
+        Q = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a2, b1[h], first ? f32x16{} : Q, 0, 0, 0);
+        P = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1, b0[h], P, 0, 0, 0);
+        Q = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1, b1[h], Q, 0, 0, 0);
+        P = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, b0[h], P, 0, 0, 0);
+        Q = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, b1[h], Q, 0, 0, 0);
+        if (C::G == 16u || h == 1u) {
+#pragma unroll
+            for (uint32_t r = 0; r < 16; ++r) acc[r] = __builtin_fmaf(d0[h], P[r], acc[r]);
+#pragma unroll
+            for (uint32_t r = 0; r < 16; ++r) acc2[r] = __builtin_fmaf(d1[h], Q[r], acc2[r]);
+        }
+    }
+}
+
+// The tile's results: DUAL, the SwiGLU activations split for the down GEMM;
+// otherwise each output row to its (token, route) slot.
+template <int TW, bool DUAL>
+__device__ __forceinline__ void gemm_epilogue(const MoePrefillArgs& a, const TileRef& tr, uint32_t n0,
+                                              const uint32_t* oslot, const f32x16& acc,
+                                              const f32x16& acc2) {
+    const MoeDecodeArgs& L = a.layer;
+    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+    const uint32_t ndim = DUAL ? L.ffn : L.hidden;
+    const uint32_t col = n0 + wave * 32u + (lane % 32u);
+    if constexpr (DUAL) {
+        // SwiGLU g / (1 + expf(-g)) * u (src/qwen3_moe_runner.cpp:682-684);
+        // variant 1: silu(g) * u (src/qwen35_runner.cpp:111-123).  The value goes
+        // straight into the down GEMM's operands, as split_piece writes x:
+        // three exact bf16 parts and, per scale group of the down format (16
+        // values for Q6_K, else 32: consecutive columns, so consecutive lanes),
+        // the FP64 sum of the group rounded once.  Absent rows (they repeat a
+        // real row) join the lane sums but are not stored.
+        const uint32_t gd = L.down_type == T_Q6_K ? 16u : 32u;
+        const uint64_t plane = static_cast<uint64_t>(a.tokens) * (L.top_k + L.variant) * ndim;
+#pragma unroll
+        for (uint32_t r = 0; r < 16; ++r) {
+            const uint32_t row = (r / 4u) * 8u + (lane / 32u) * 4u + (r % 4u);
+            const float g = acc[r], u = acc2[r];
+            const float v = L.variant ? silu(g) * u : (g / (1.0f + expf(-g))) * u;
+            const uint32_t h = bf16_rne_bits(v);
+            const float r1 = v - __uint_as_float(h << 16);
+            const uint32_t m = bf16_rne_bits(r1);
+            const float r2 = r1 - __uint_as_float(m << 16);  // at most 8 significant bits
+            const double sv = static_cast<double>(v);
+            const double gs = gd == 16u ? group_sum<16>(sv) : group_sum<32>(sv);
+            if (row < tr.rows) {
+                const uint64_t e = static_cast<uint64_t>(tr.base + row) * ndim + col;
+                a.act_parts[e] = static_cast<uint16_t>(h);
+                a.act_parts[plane + e] = static_cast<uint16_t>(m);
+                a.act_parts[2u * plane + e] = static_cast<uint16_t>(__float_as_uint(r2) >> 16);
+                if (col % gd == gd - 1u)
+                    a.act_sums[static_cast<uint64_t>(tr.base + row) * (ndim / gd) + col / gd] =
+                        static_cast<float>(gs);
+            }
+        }
+    } else {
+#pragma unroll
+        for (uint32_t r = 0; r < 16; ++r) {
+            const uint32_t row = (r / 4u) * 8u + (lane / 32u) * 4u + (r % 4u);
+            if (row < tr.rows) {
+                float* o = a.out + static_cast<uint64_t>(oslot[row]) * ndim + col;
+                o[0] = acc[r];
+                o[kTileN] = acc2[r];
+            }
+        }
+    }
+}
+
 // DUAL: gate/up over x (token rows), SwiGLU into act (grouped rows).
 // Otherwise: down over act, each row to its (token, route) slot of out.
 // Global loads run two stages ahead of the MFMAs (two register sets), LDS
@@ -799,55 +941,6 @@ __global__ __launch_bounds__(256, 2) void k_expert_gemm(MoePrefillArgs a) {
     auto stage_k = [&](uint32_t s) { return (s < last ? s : last) * C::KC; };  // tail: harmless reloads
     GemmPrefetch<TW, DUAL> f0, f1;
     f32x16 acc = {}, acc2 = {};
-    if constexpr (kq_blocked<TW>()) {
-        static_assert(C::KC == 32u, "one 32-value group per stage");
-        // Units in two register buffers: unit 2i in bA, 2i + 1 in bB.  Stage
-        // s is stage s % US of unit s / US.  Step s computes stage s, stores
-        // stage s + 1 with its fields taken from the unit buffers and loads
-        // stage s + 3's activations; bA is free after step 2US*i + US - 2 and
-        // bB after step 2US*i + 2US - 2, when units 2i + 2 and 2i + 3 are
-        // loaded into them (US + 1 steps ahead of their first use).  Steps
-        // past the last stage store and load harmless repeats (the unit
-        // index is clamped; their data is never computed).
-        using U = KqUnit<TW>;
-        constexpr uint32_t US = U::STAGES;
-        const uint32_t lastu = kdim / 256u * U::PER_ROW_BLOCK - 1u;
-        U bA, bB;
-        kq_unit_load<TW>(src.wrow, 0u, bA);
-        kq_unit_load<TW>(src.wrow, 1u < lastu ? 1u : lastu, bB);
-        gemm_load_act<TW, DUAL>(f0, src, 0u);
-        gemm_load_act<TW, DUAL>(f1, src, stage_k(1u));
-        {
-            Raw32<TW> r;
-            raw32_from_unit<TW>(bA, 0u, r);
-            gemm_store_raw<TW, DUAL>(st[0], r, f0, src, 0u);
-        }
-        gemm_load_act<TW, DUAL>(f0, src, stage_k(2u));
-        __syncthreads();
-        auto body = [&](uint32_t s0, uint32_t count) {
-#pragma unroll
-            for (uint32_t t = 0; t < 2u * US; ++t) {
-                if (t < count) {  // uniform: count is 2US except for the last steps
-                    const uint32_t s = s0 + t;
-                    GemmPrefetch<TW, DUAL>& f = (t & 1u) ? f0 : f1;
-                    gemm_compute<TW, DUAL>(st[s & 1u], acc, acc2);
-                    Raw32<TW> r;
-                    if (((t + 1u) / US) % 2u == 0u) raw32_from_unit<TW>(bA, (t + 1u) % US, r);
-                    else raw32_from_unit<TW>(bB, (t + 1u) % US, r);
-                    gemm_store_raw<TW, DUAL>(st[(s + 1u) & 1u], r, f, src, (s + 1u) * C::KC);
-                    gemm_load_act<TW, DUAL>(f, src, stage_k(s + 3u));
-                    const uint32_t u = s0 / US;
-                    if (t == US - 2u) kq_unit_load<TW>(src.wrow, u + 2u < lastu ? u + 2u : lastu, bA);
-                    if (t == 2u * US - 2u)
-                        kq_unit_load<TW>(src.wrow, u + 3u < lastu ? u + 3u : lastu, bB);
-                    __syncthreads();
-                }
-            }
-        };
-        uint32_t s = 0;
-        for (; s + 2u * US <= nst; s += 2u * US) body(s, 2u * US);
-        if (s < nst) body(s, nst - s);
-    } else {
     gemm_load<TW, DUAL>(f0, src, 0u);
     gemm_load<TW, DUAL>(f1, src, stage_k(1u));
     gemm_store<TW, DUAL>(st[0], f0, src, 0u);
@@ -869,50 +962,97 @@ __global__ __launch_bounds__(256, 2) void k_expert_gemm(MoePrefillArgs a) {
     }
     if (s + 1u < nst) step(s++, f1);
     gemm_compute<TW, DUAL>(st[s & 1u], acc, acc2);
+    gemm_epilogue<TW, DUAL>(a, tr, n0, oslot, acc, acc2);
+}
+
+// Q4_K and Q6_K weights: the same tiles and results as k_expert_gemm, with
+// each wave's weight rows in registers (half-block units, one unit ahead) and
+// only the activation planes staged through LDS (two stages; their global
+// loads run two stages ahead).
+template <int TW, bool DUAL>
+__global__ __launch_bounds__(256, 2) void k_expert_gemm_w(MoePrefillArgs a) {
+    using C = GemmCfg<TW, DUAL>;
+    __shared__ GemmStageA<TW, DUAL> st[2];
+    __shared__ uint32_t arow[kTileM], oslot[kTileM];
+    const MoeDecodeArgs& L = a.layer;
+    const uint32_t kdim = DUAL ? L.hidden : L.ffn, ndim = DUAL ? L.ffn : L.hidden;
+    const uint32_t nblk = DUAL ? kTileN : 2u * kTileN;  // output rows per workgroup
+    uint32_t tile, yb;
+    xcd_tile(ndim / nblk, tile, yb);
+    TileRef tr;
+    if (!tile_ref(a, tile, tr)) return;  // uniform
+    const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
+    const uint32_t n0 = yb * nblk, kq = lane / 32u;
+    if (tid < kTileM) {
+        const uint32_t i = tid < tr.rows ? tid : tr.rows - 1u;  // absent rows repeat a real one
+        const uint32_t slot = a.perm[tr.base + i];  // token * top_k + route
+        arow[tid] = DUAL ? slot / (L.top_k + L.variant) : tr.base + i;
+        oslot[tid] = slot;
     }
-    const uint32_t col = n0 + wave * 32u + (lane % 32u);
-    if constexpr (DUAL) {
-        // SwiGLU g / (1 + expf(-g)) * u (src/qwen3_moe_runner.cpp:682-684);
-        // variant 1: silu(g) * u (src/qwen35_runner.cpp:111-123).  The value goes
-        // straight into the down GEMM's operands, as split_piece writes x:
-        // three exact bf16 parts and, per scale group of the down format (16
-        // values for Q6_K, else 32: consecutive columns, so consecutive lanes),
-        // the FP64 sum of the group rounded once.  Absent rows (they repeat a
-        // real row) join the lane sums but are not stored.
-        const uint32_t gd = L.down_type == T_Q6_K ? 16u : 32u;
-        const uint64_t plane = static_cast<uint64_t>(a.tokens) * (L.top_k + L.variant) * ndim;
+    const bool sh = tr.e >= L.n_experts;  // the shared expert (variant 1): its own tensors
+    const uint32_t rnb = kdim / Fmt<TW>::BE;
+    const uint32_t r = n0 + wave * 32u + lane % 32u;  // this lane's row of matrix 0
+    QRow w0, w1;
+    if constexpr (DUAL) {  // gate row r, up row r
+        w0 = QRow{sh ? L.shared_gate : L.gate + static_cast<uint64_t>(tr.e) * L.gate_slice,
+                  static_cast<uint64_t>(L.ffn) * rnb, static_cast<uint64_t>(r) * rnb};
+        w1 = QRow{sh ? L.shared_up : L.up + static_cast<uint64_t>(tr.e) * L.up_slice,
+                  static_cast<uint64_t>(L.ffn) * rnb, static_cast<uint64_t>(r) * rnb};
+    } else {  // down rows r and r + 128
+        const uint8_t* base = sh ? L.shared_down : L.down + static_cast<uint64_t>(tr.e) * L.down_slice;
+        w0 = QRow{base, static_cast<uint64_t>(L.hidden) * rnb, static_cast<uint64_t>(r) * rnb};
+        w1 = QRow{base, static_cast<uint64_t>(L.hidden) * rnb, static_cast<uint64_t>(r + kTileN) * rnb};
+    }
+    const uint32_t nu = kdim / 128u, lastu = nu - 1u;  // units per row
+    WUnit<TW> ua0, ua1, ub0, ub1;  // matrices 0 and 1: units 2i (a) and 2i + 1 (b)
+    wunit_load<TW>(w0, 0u, kq, ua0);
+    wunit_load<TW>(w1, 0u, kq, ua1);
+    wunit_load<TW>(w0, 1u < lastu ? 1u : lastu, kq, ub0);
+    wunit_load<TW>(w1, 1u < lastu ? 1u : lastu, kq, ub1);
+    const uint16_t* parts = DUAL ? a.x_parts : a.act_parts;
+    const uint64_t plane = DUAL ? static_cast<uint64_t>(a.tokens) * L.hidden
+                                : static_cast<uint64_t>(a.tokens) * (L.top_k + L.variant) * L.ffn;
+    const float* sums = DUAL ? a.x_sums : a.act_sums;
+    __syncthreads();
+    GemmSrc<TW, DUAL> src;
+    gemm_src<TW, DUAL>(src, w0, parts, plane, kdim, sums, arow);
+    const uint32_t nst = kdim / C::KC, last = nst - 1u;  // a multiple of 8 (kdim % 256 == 0)
+    auto stage_k = [&](uint32_t s) { return (s < last ? s : last) * C::KC; };  // tail: harmless reloads
+    GemmPrefetch<TW, DUAL> f0, f1;
+    gemm_load_act<TW, DUAL>(f0, src, 0u);
+    gemm_load_act<TW, DUAL>(f1, src, stage_k(1u));
+    gemm_store_a<TW, DUAL>(st[0], f0, src);
+    gemm_load_act<TW, DUAL>(f0, src, stage_k(2u));
+    __syncthreads();
+    f32x16 acc = {}, acc2 = {};
+    // Stage s's activations live in f(s % 2); step s computes stage s, stores
+    // stage s + 1 and loads stage s + 3.  Steps 0-3 of an iteration use units
+    // a, steps 4-7 units b; each buffer reloads (two units on) after its last
+    // step, four steps before its next use.
+    for (uint32_t s0 = 0; s0 < nst; s0 += 8u) {
+        const uint32_t u0 = s0 / 4u;
 #pragma unroll
-        for (uint32_t r = 0; r < 16; ++r) {
-            const uint32_t row = (r / 4u) * 8u + (lane / 32u) * 4u + (r % 4u);
-            const float g = acc[r], u = acc2[r];
-            const float v = L.variant ? silu(g) * u : (g / (1.0f + expf(-g))) * u;
-            const uint32_t h = bf16_rne_bits(v);
-            const float r1 = v - __uint_as_float(h << 16);
-            const uint32_t m = bf16_rne_bits(r1);
-            const float r2 = r1 - __uint_as_float(m << 16);  // at most 8 significant bits
-            const double sv = static_cast<double>(v);
-            const double gs = gd == 16u ? group_sum<16>(sv) : group_sum<32>(sv);
-            if (row < tr.rows) {
-                const uint64_t e = static_cast<uint64_t>(tr.base + row) * ndim + col;
-                a.act_parts[e] = static_cast<uint16_t>(h);
-                a.act_parts[plane + e] = static_cast<uint16_t>(m);
-                a.act_parts[2u * plane + e] = static_cast<uint16_t>(__float_as_uint(r2) >> 16);
-                if (col % gd == gd - 1u)
-                    a.act_sums[static_cast<uint64_t>(tr.base + row) * (ndim / gd) + col / gd] =
-                        static_cast<float>(gs);
+        for (uint32_t t = 0; t < 8u; ++t) {
+            const uint32_t s = s0 + t;
+            GemmPrefetch<TW, DUAL>& f = (t & 1u) ? f0 : f1;
+            if (t < 4u) gemm_compute_w<TW, DUAL>(st[s & 1u], ua0, ua1, 0u, t, acc, acc2);
+            else gemm_compute_w<TW, DUAL>(st[s & 1u], ub0, ub1, 1u, t - 4u, acc, acc2);
+            gemm_store_a<TW, DUAL>(st[(s + 1u) & 1u], f, src);
+            gemm_load_act<TW, DUAL>(f, src, stage_k(s + 3u));
+            if (t == 3u) {
+                const uint32_t un = u0 + 2u < lastu ? u0 + 2u : lastu;
+                wunit_load<TW>(w0, un, kq, ua0);
+                wunit_load<TW>(w1, un, kq, ua1);
             }
-        }
-    } else {
-#pragma unroll
-        for (uint32_t r = 0; r < 16; ++r) {
-            const uint32_t row = (r / 4u) * 8u + (lane / 32u) * 4u + (r % 4u);
-            if (row < tr.rows) {
-                float* o = a.out + static_cast<uint64_t>(oslot[row]) * ndim + col;
-                o[0] = acc[r];
-                o[kTileN] = acc2[r];
+            if (t == 7u) {
+                const uint32_t un = u0 + 3u < lastu ? u0 + 3u : lastu;
+                wunit_load<TW>(w0, un, kq, ub0);
+                wunit_load<TW>(w1, un, kq, ub1);
             }
+            __syncthreads();
         }
     }
+    gemm_epilogue<TW, DUAL>(a, tr, n0, oslot, acc, acc2);
 }
 
 // ---------------------------------------------------------------------------
@@ -974,7 +1114,10 @@ hipError_t expert_gemm_t(const MoePrefillArgs& a, hipStream_t s) {
     // (x is split beside the grouping, the activations by the gate/up epilogue)
     const uint32_t nb = DUAL ? L.ffn / kTileN : L.hidden / (2u * kTileN);
     const uint32_t blocks = 8u * ceil_div_u(a.max_tiles, 8u) * nb;  // xcd_tile's layout
-    hipLaunchKernelGGL((k_expert_gemm<TW, DUAL>), dim3(blocks), dim3(256), 0, s, a);
+    if constexpr (TW == T_Q4_K || TW == T_Q6_K)
+        hipLaunchKernelGGL((k_expert_gemm_w<TW, DUAL>), dim3(blocks), dim3(256), 0, s, a);
+    else
+        hipLaunchKernelGGL((k_expert_gemm<TW, DUAL>), dim3(blocks), dim3(256), 0, s, a);
     return hipGetLastError();
 }
 
