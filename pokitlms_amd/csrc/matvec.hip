@@ -25,22 +25,32 @@ constexpr int kMaxS = 12;  // waves per K-split group
 template <int B> constexpr int passes_for() { return B > 4 ? 1 : 2; }
 template <int B> constexpr int max_threads_for() { return B > 4 ? 768 : 512; }
 
-template <int T, int B, int UB, int NU>
+template <int T, int B, int UB, int NU, bool PIPE>
 struct MvState {
     static constexpr int kPasses = passes_for<B>();
+    static constexpr int kBufs = PIPE ? 2 : 1;
     UnitPos pos[NU];
     bool valid[NU];
     UnitX<T, UB, B> ux[NU];
-    UnitRaw<T, UB> raw[kPasses][NU];
-    uint32_t row[kPasses];
-    bool live[kPasses];
+    UnitRaw<T, UB> raw[kBufs][kPasses][NU];
+    uint32_t row[kBufs][kPasses];
+    bool live[kBufs][kPasses];
+};
+
+template <int I>
+struct Buf {
+    static constexpr int value = I;
 };
 
 // Each wave issues its first passes' weight loads, then reads its units'
 // activations (kept in registers for every later row), then dots.  x is read
 // from global memory (L2) by every wave: a workgroup barrier to share it
-// through LDS would wait for the weight loads as well.
-template <int T, int B, int UB, int NU>
+// through LDS would wait for the weight loads as well.  PIPE (waves that walk
+// many rows, such as an output head): two register sets, the next passes'
+// loads issued before the current ones are consumed; past the last pass the
+// extra issue re-reads the current rows (cache hits), so every issue is
+// unconditional and the load counts stay static.
+template <int T, int B, int UB, int NU, bool PIPE>
 __global__ __launch_bounds__(max_threads_for<B>()) void k_matvec_q(
     const uint8_t* __restrict__ W, uint32_t nb, const float* __restrict__ x,
     uint32_t x_stride, float* __restrict__ y, uint32_t y_stride, uint32_t rows, uint32_t units,
@@ -59,7 +69,7 @@ __global__ __launch_bounds__(max_threads_for<B>()) void k_matvec_q(
     uint32_t p0 = blockIdx.x * groups * kPasses;
     if (p0 >= passes) return;  // uniform per workgroup
 
-    MvState<T, B, UB, NU> st;
+    MvState<T, B, UB, NU, PIPE> st;
 #pragma unroll
     for (int k = 0; k < NU; ++k) {
         const uint32_t local = ul + G * k;
@@ -67,18 +77,20 @@ __global__ __launch_bounds__(max_threads_for<B>()) void k_matvec_q(
         st.valid[k] = local < slice_units && u < units;
         st.pos[k] = unit_pos<T, UB>(st.valid[k] ? u : 0u);
     }
-    auto issue = [&](uint32_t pp) {  // weight loads of passes pp + group*kPasses + q
+    auto issue = [&](uint32_t pp, auto buf) {  // weight loads of passes pp + group*kPasses + q
+        constexpr int bi = decltype(buf)::value;
 #pragma unroll
         for (int q = 0; q < kPasses; ++q) {
             const uint32_t p = pp + group * kPasses + q;
-            st.row[q] = p * RPP + sub;
-            st.live[q] = p < passes && st.row[q] < rows;
-            const QRow qr{W, nblk, static_cast<uint64_t>(st.live[q] ? st.row[q] : 0u) * nb};
+            st.row[bi][q] = p * RPP + sub;
+            st.live[bi][q] = p < passes && st.row[bi][q] < rows;
+            const QRow qr{W, nblk, static_cast<uint64_t>(st.live[bi][q] ? st.row[bi][q] : 0u) * nb};
 #pragma unroll
-            for (int k = 0; k < NU; ++k) unit_load<T, UB>(qr, st.pos[k], st.raw[q][k]);
+            for (int k = 0; k < NU; ++k) unit_load<T, UB>(qr, st.pos[k], st.raw[bi][q][k]);
         }
     };
-    auto finish = [&](uint32_t pp) {  // dots, reductions and stores of the issued passes
+    auto finish = [&](uint32_t pp, auto buf) {  // dots, reductions and stores of the issued passes
+        constexpr int bi = decltype(buf)::value;
 #pragma unroll
         for (int q = 0; q < kPasses; ++q) {
             float acc[B];
@@ -86,14 +98,14 @@ __global__ __launch_bounds__(max_threads_for<B>()) void k_matvec_q(
             for (int b = 0; b < B; ++b) acc[b] = 0.0f;
 #pragma unroll
             for (int k = 0; k < NU; ++k)
-                if (st.valid[k]) unit_compute<T, UB, B>(st.raw[q][k], st.pos[k], st.ux[k], acc);
+                if (st.valid[k]) unit_compute<T, UB, B>(st.raw[bi][q][k], st.pos[k], st.ux[k], acc);
 #pragma unroll
             for (int b = 0; b < B; ++b) acc[b] = group_sum_dyn(acc[b], G);
             if (ul == G - 1u) {
                 if (S == 1) {
-                    if (st.live[q]) {
+                    if (st.live[bi][q]) {
 #pragma unroll
-                        for (int b = 0; b < B; ++b) y[b * y_stride + st.row[q]] = acc[b];
+                        for (int b = 0; b < B; ++b) y[b * y_stride + st.row[bi][q]] = acc[b];
                     }
                 } else {
 #pragma unroll
@@ -122,13 +134,27 @@ __global__ __launch_bounds__(max_threads_for<B>()) void k_matvec_q(
         }
     };
 
-    issue(p0);  // the first passes' weight loads, then the activations
+    issue(p0, Buf<0>{});  // the first passes' weight loads, then the activations
 #pragma unroll
     for (int k = 0; k < NU; ++k) load_unit_x<T, UB, B>(x, x_stride, st.pos[k], st.valid[k], st.ux[k]);
-    finish(p0);
-    for (p0 += stride; p0 < passes; p0 += stride) {
-        issue(p0);
-        finish(p0);
+    if constexpr (!PIPE) {
+        finish(p0, Buf<0>{});
+        for (p0 += stride; p0 < passes; p0 += stride) {
+            issue(p0, Buf<0>{});
+            finish(p0, Buf<0>{});
+        }
+    } else {
+        for (;;) {  // uniform per workgroup; p0 < passes here
+            const uint32_t pn = p0 + stride;
+            issue(pn < passes ? pn : p0, Buf<1>{});
+            finish(p0, Buf<0>{});
+            if (pn >= passes) break;
+            const uint32_t pm = pn + stride;
+            issue(pm < passes ? pm : pn, Buf<0>{});
+            finish(pn, Buf<1>{});
+            if (pm >= passes) break;
+            p0 = pm;
+        }
     }
 }
 
@@ -230,7 +256,15 @@ hipError_t run_q(const Plan& pl, const uint8_t* W, uint32_t nb, uint32_t rows,
     if (blocks > max_blocks) blocks = max_blocks;
     const size_t lds =
         pl.S > 1 ? static_cast<size_t>(pl.waves_per_block) * kPasses * RPP * B * sizeof(float) : 0;
-    hipLaunchKernelGGL((k_matvec_q<T, B, UB, NU>), dim3(blocks), dim3(64u * pl.waves_per_block),
+    if constexpr (B == 1) {
+        if (passes >= 3u * blocks * groups * kPasses) {  // three or more passes per wave
+            hipLaunchKernelGGL((k_matvec_q<T, B, UB, NU, true>), dim3(blocks),
+                               dim3(64u * pl.waves_per_block), lds, stream, W, nb, x, in, y, rows,
+                               rows, pl.units, pl.slice_units, pl.S, pl.glog2);
+            return hipGetLastError();
+        }
+    }
+    hipLaunchKernelGGL((k_matvec_q<T, B, UB, NU, false>), dim3(blocks), dim3(64u * pl.waves_per_block),
                        lds, stream, W, nb, x, in, y, rows, rows, pl.units, pl.slice_units, pl.S,
                        pl.glog2);
     return hipGetLastError();
