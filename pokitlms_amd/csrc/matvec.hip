@@ -256,8 +256,12 @@ hipError_t run_q(const Plan& pl, const uint8_t* W, uint32_t nb, uint32_t rows,
     if (blocks > max_blocks) blocks = max_blocks;
     const size_t lds =
         pl.S > 1 ? static_cast<size_t>(pl.waves_per_block) * kPasses * RPP * B * sizeof(float) : 0;
-    if constexpr (B == 1) {
-        if (passes >= 3u * blocks * groups * kPasses) {  // three or more passes per wave
+    // the pipelined loop: one vector whose waves walk three or more passes
+    // (the output head), or batches whose rows are split over eight or more
+    // waves (their extra registers cost narrower splits more occupancy than
+    // the overlap gains; Q2_K/Q3_K batches would spill)
+    if constexpr (T != T_Q2_K && T != T_Q3_K) {
+        if (passes >= 3u * blocks * groups * kPasses && (B == 1 || pl.S >= 8u)) {
             hipLaunchKernelGGL((k_matvec_q<T, B, UB, NU, true>), dim3(blocks),
                                dim3(64u * pl.waves_per_block), lds, stream, W, nb, x, in, y, rows,
                                rows, pl.units, pl.slice_units, pl.S, pl.glog2);
