@@ -665,7 +665,11 @@ __device__ uint32_t ref_route_block(const RefRouteIn& R, uint32_t route, bool le
 // (src/qwen3_moe_runner.cpp:682-684), or, with a norm, RMSNorm of the residual
 // stream.  Lanes (row, block); one lane per row then sums the block dots in
 // block order starting from 0.  With segments, workgroups along x are split
-// between up to three matrices that share the input.
+// between up to three matrices that share the input.  With act (gate and up,
+// segments 0 and 1), half of each workgroup's lanes take rows of gate and
+// half the same rows of up, and the row sums become the SwiGLU activations
+// g / (1 + expf(-g)) * u (src/qwen3_moe_runner.cpp:682-684), bit for bit
+// what staging them in the down projection computes.
 template <int T>
 __global__ __launch_bounds__(256) void k_ref_matvec(RefMatvecArgs a) {
     // xs [in], part [256]; with a norm also sq [chain_floats(in)], wb [in]
@@ -675,12 +679,19 @@ __global__ __launch_bounds__(256) void k_ref_matvec(RefMatvecArgs a) {
     constexpr uint32_t BE = RefBlock<T>::BE, BB = RefBlock<T>::BB;
     const uint32_t r = blockIdx.y, tid = threadIdx.x;
     const bool leader = blockIdx.x == 0 && blockIdx.y == 0;
-    const uint32_t nb = a.in / BE, rpw = 256u / nb;
+    const bool paired = a.act != nullptr;
+    const uint32_t mat = paired ? tid / 128u : 0u, lt = paired ? tid % 128u : tid;
+    const uint32_t nb = a.in / BE, rpw = (paired ? 128u : 256u) / nb;
     const uint8_t* W = a.W;
     uint64_t row_bytes = a.row_bytes, slice_bytes = a.slice_bytes;
     uint32_t rows = a.rows, bx = blockIdx.x;
     float* y = a.y;
-    if (a.nseg) {
+    if (paired) {
+        W = a.seg[mat].W;
+        row_bytes = a.seg[mat].row_bytes;
+        slice_bytes = a.seg[mat].slice_bytes;
+        rows = a.seg[mat].rows;
+    } else if (a.nseg) {
 #pragma unroll
         for (uint32_t j = 0; j < kMaxRefSegs; ++j) {
             if (j < a.nseg && blockIdx.x >= a.seg[j].block0) {
@@ -695,7 +706,7 @@ __global__ __launch_bounds__(256) void k_ref_matvec(RefMatvecArgs a) {
     }
     float* xs = lds;  // padded: block b at b * (BE + 4)
     float* part = lds + xpad_floats<BE>(a.in);
-    const uint32_t row0 = bx * rpw, lr = tid / nb, b = tid % nb, row = row0 + lr;
+    const uint32_t row0 = bx * rpw, lr = lt / nb, b = lt % nb, row = row0 + lr;
     const bool active = lr < rpw && row < rows;
     const uint64_t nblk = static_cast<uint64_t>(rows) * nb;
     const QRow qrow{W, nblk, static_cast<uint64_t>(active ? row : 0u) * nb};
@@ -740,6 +751,23 @@ __global__ __launch_bounds__(256) void k_ref_matvec(RefMatvecArgs a) {
     __syncthreads();
     if (active) part[tid] = ref_dot<T>(raw, xs + b * (BE + 4u));
     __syncthreads();
+    if (paired) {
+        // the gate and up row sums (xs is free now), then the activations
+        float* gu = xs;  // [2][rpw]
+        if (tid < 2u * rpw) {
+            const uint32_t m = tid / rpw, rr = tid % rpw;
+            float acc = 0.0f;
+            for (uint32_t k = 0; k < nb; ++k) acc = __fadd_rn(acc, part[128u * m + rr * nb + k]);
+            gu[tid] = acc;
+        }
+        __syncthreads();
+        if (tid < rpw && row0 + tid < rows) {
+            const float g = gu[tid], u = gu[rpw + tid];
+            a.act[static_cast<uint64_t>(r) * a.y_stride + row0 + tid] =
+                __fmul_rn(__fdiv_rn(g, __fadd_rn(1.0f, expf_libm(-g, a.expf))), u);
+        }
+        return;
+    }
     if (tid < rpw && row0 + tid < rows) {
         float acc = 0.0f;
         for (uint32_t k = 0; k < nb; ++k) acc = __fadd_rn(acc, part[tid * nb + k]);
@@ -1102,6 +1130,22 @@ hipError_t launch_ref_matvec_multi(uint32_t type, RefMatvecArgs a, const RefSeg*
     return ref_matvec_launch(type, a, blocks, routes, s);
 }
 
+bool ref_gate_up_act_supported(uint32_t type, uint32_t in) {
+    return type != T_F32 && ref_matvec_supported(type, in) && in / ref_block_elems(type) <= 128u;
+}
+
+hipError_t launch_ref_gate_up_act(uint32_t type, RefMatvecArgs a, const RefSeg& gate,
+                                  const RefSeg& up, uint32_t routes, hipStream_t s) {
+    if (!ref_gate_up_act_supported(type, a.in) || !a.act || gate.rows != up.rows ||
+        !ref_prologue_ok(a, routes))
+        return hipErrorInvalidValue;
+    const uint32_t rpw = 128u / (a.in / ref_block_elems(type));
+    a.nseg = 2;
+    a.seg[0] = gate;
+    a.seg[1] = up;
+    return ref_matvec_launch(type, a, (gate.rows + rpw - 1u) / rpw, routes, s);
+}
+
 hipError_t launch_ref_rmsnorm(float* x, const RefResidual& res, const float* w, float* out,
                               uint32_t n, uint32_t rows, float eps, hipStream_t s) {
     const size_t lds = chain_floats(n) * sizeof(float);
@@ -1180,7 +1224,13 @@ hipError_t launch_ref_step(const ModelArgs& a, const ModelLayer* layers, bool lo
         gu.route = RefRouteIn{rl, m.n_experts, m.top_k, m.normalize, m.ids, m.probs, m.status};
         const RefSeg gu_segs[2] = {{m.gate, m.gate_row, m.gate_slice, m.ffn, 0, g},
                                    {m.up, m.up_row, m.up_slice, m.ffn, 0, u}};
-        if (m.gate_type == m.up_type) {
+        const bool paired = m.gate_type == m.up_type && ref_gate_up_act_supported(m.gate_type, m.hidden);
+        if (paired) {  // the SwiGLU activations written by gate/up, into g
+            gu.act = g;
+            gu.expf = a.expf;
+            if ((err = launch_ref_gate_up_act(m.gate_type, gu, gu_segs[0], gu_segs[1], m.top_k, s)))
+                return err;
+        } else if (m.gate_type == m.up_type) {
             if ((err = launch_ref_matvec_multi(m.gate_type, gu, gu_segs, 2, m.top_k, s))) return err;
         } else {
             if ((err = launch_ref_matvec_multi(m.gate_type, gu, gu_segs, 1, m.top_k, s))) return err;
@@ -1188,7 +1238,7 @@ hipError_t launch_ref_step(const ModelArgs& a, const ModelLayer* layers, bool lo
             gu.ids = m.ids;
             if ((err = launch_ref_matvec_multi(m.up_type, gu, gu_segs + 1, 1, m.top_k, s))) return err;
         }
-        // 6. SwiGLU staged in the down projection
+        // 6. down (the SwiGLU staged in it unless gate/up wrote the activations)
         RefMatvecArgs d{};
         d.ids = m.ids;
         d.W = m.down;
@@ -1197,7 +1247,7 @@ hipError_t launch_ref_step(const ModelArgs& a, const ModelLayer* layers, bool lo
         d.rows = m.hidden;
         d.in = m.ffn;
         d.x = g;
-        d.x_up = u;
+        d.x_up = paired ? nullptr : u;
         d.x_stride = m.ffn;
         d.expf = a.expf;
         d.y = out;

@@ -231,6 +231,7 @@ struct RefMatvecArgs {
     uint32_t nseg;            // 0: the single matrix above
     RefSeg seg[kMaxRefSegs];
     const float* x_up;        // non-null: stage g / (1 + expf(-g)) * u, g = x, u = x_up
+    float* act;               // non-null (with seg[0] gate, seg[1] up): write the SwiGLU activations
     LibmExpf expf;
     RefNormIn norm;           // norm.w set: x is RMSNorm(norm.x + norm.res) * norm.w
     RefRouteIn route;         // route.logits set: the expert slices come from routing
@@ -241,6 +242,14 @@ hipError_t launch_ref_matvec(uint32_t type, const RefMatvecArgs& a, uint32_t rou
 // Several matrices sharing x (q/k/v; gate/up per route): one launch.
 hipError_t launch_ref_matvec_multi(uint32_t type, RefMatvecArgs a, const RefSeg* segs, uint32_t n,
                                    uint32_t routes, hipStream_t stream);
+// Gate and up of every route in one launch, each workgroup computing the same
+// rows of both, with the SwiGLU activations g / (1 + expf(-g)) * u written to
+// a.act (row stride a.y_stride) instead of the two outputs; false when the
+// row is too wide for the pairing (then the caller launches the two
+// matrices and stages the SwiGLU in the down projection).
+bool ref_gate_up_act_supported(uint32_t type, uint32_t in);
+hipError_t launch_ref_gate_up_act(uint32_t type, RefMatvecArgs a, const RefSeg& gate,
+                                  const RefSeg& up, uint32_t routes, hipStream_t s);
 hipError_t launch_ref_rmsnorm(float* x, const RefResidual& res, const float* w, float* out,
                               uint32_t n, uint32_t rows, float eps, hipStream_t stream);
 // Head dims 64/128/256 and a KV window whose scores fit LDS beside a V tile.
