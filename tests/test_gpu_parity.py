@@ -166,6 +166,24 @@ def test_odd_batches(hip, port, batch):
     wt.release()
 
 
+@pytest.mark.parametrize("gtype", (S.Q4_K, S.Q6_K, S.Q8_0))
+def test_long_matvec_pipelined_rows(hip, port, gtype):
+    """Rows enough that every wave walks several row passes (the pipelined
+    loop an output head takes: 40,003 rows of 2048, one vector, an odd pass
+    count and a partial last pass) against the CPU's linear."""
+    g = S.rng(77 + gtype)
+    rows, inn = 40003, 2048
+    w = S.quant_matrix(gtype, rows, inn, g)
+    x = S.normal_f32(g, inn).reshape(1, inn)
+    wt = hip.upload(gtype, inn, rows, w)
+    gpu = hip.matvec(wt, x)[0]
+    cpu = port.linear(gtype, w, inn, rows, x[0])
+    err = normwise_rel(gpu, cpu)
+    say("long matvec", gtype, "normwise", err)
+    assert err <= TOL
+    wt.release()
+
+
 def test_expert_slice_matvec(hip, port):
     layer = S.moe_layer(seed=21, hidden=512, experts=4, ffn=256)
     g = hip.upload(layer.gate_type, 512, 256, layer.gate, n_experts=4)
