@@ -218,6 +218,51 @@ __device__ __forceinline__ void load_unit_x(const float* x, uint32_t x_stride, c
     }
 }
 
+// One vector's activations staged in LDS lane-major, for waves that share
+// them: piece q (float4 q of the unit's runs, run q / (UB / 4)) of unit slot
+// k of unit lane ul sits at [(k * Q + q) * G + ul], so every LDS read of a
+// wave is G consecutive float4s (lanes that share a unit read the same
+// address) and no two lanes of a read meet in one bank, whatever the format's
+// column pattern.
+template <int T, int UB>
+constexpr int x_pieces() { return Fmt<T>::RUNS * UB / 4; }
+
+// (a vector type: an array of HIP's float4 class would live in scratch)
+typedef float xf32x4 __attribute__((ext_vector_type(4)));
+
+// Activation column of piece q of the unit at p: selects, not an indexed
+// array (which would live in scratch when q is not a constant).
+template <int T, int UB>
+__device__ __forceinline__ uint32_t piece_col(const UnitPos& p, uint32_t q) {
+    const uint32_t r = q / (UB / 4), i = q % (UB / 4);
+    uint32_t col = p.col[0];
+#pragma unroll
+    for (int rr = 1; rr < Fmt<T>::RUNS; ++rr) col = r == static_cast<uint32_t>(rr) ? p.col[rr] : col;
+    return col + 4u * i;
+}
+
+// load_unit_x for one vector from staged pieces (slot = the unit slot's
+// piece 0 for this lane, pieces G float4s apart).
+template <int T, int UB>
+__device__ __forceinline__ void load_unit_x_staged(const xf32x4* slot, uint32_t G,
+                                                   UnitX<T, UB, 1>& ux) {
+    constexpr int R = Fmt<T>::RUNS;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        float sum = 0.0f;
+#pragma unroll
+        for (int i = 0; i < UB; i += 4) {
+            const xf32x4 v = slot[(r * (UB / 4) + i / 4) * G];
+            ux.v[0][r * UB + i + 0] = v.x;
+            ux.v[0][r * UB + i + 1] = v.y;
+            ux.v[0][r * UB + i + 2] = v.z;
+            ux.v[0][r * UB + i + 3] = v.w;
+            sum += (v.x + v.y) + (v.z + v.w);
+        }
+        ux.s[0][r] = sum;
+    }
+}
+
 // ---------------------------------------------------------------------------
 // Unit decode in two phases, so a wave can issue the loads of several rows
 // before it consumes any of them.

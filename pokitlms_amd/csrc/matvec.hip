@@ -44,12 +44,12 @@ struct Buf {
 
 // Each wave issues its first passes' weight loads, then reads its units'
 // activations (kept in registers for every later row), then dots.  x is read
-// from global memory (L2) by every wave: a workgroup barrier to share it
-// through LDS would wait for the weight loads as well.  PIPE (waves that walk
-// many rows, such as an output head): two register sets, the next passes'
-// loads issued before the current ones are consumed; past the last pass the
-// extra issue re-reads the current rows (cache hits), so every issue is
-// unconditional and the load counts stay static.
+// from global memory (L2) by every wave (k_matvec_q_staged shares one vector
+// through LDS instead).  PIPE (waves that walk many rows, such as an output
+// head): two register sets, the next passes' loads issued before the current
+// ones are consumed; past the last pass the extra issue re-reads the current
+// rows (cache hits), so every issue is unconditional and the load counts stay
+// static.
 template <int T, int B, int UB, int NU, bool PIPE>
 __global__ __launch_bounds__(max_threads_for<B>()) void k_matvec_q(
     const uint8_t* __restrict__ W, uint32_t nb, const float* __restrict__ x,
@@ -155,6 +155,124 @@ __global__ __launch_bounds__(max_threads_for<B>()) void k_matvec_q(
             if (pm >= passes) break;
             p0 = pm;
         }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// One vector, every row on the 64 lanes of a wave (G = 64), and XG waves per
+// K-slice in a workgroup: the workgroup stages x once in LDS instead of every
+// wave reading all of it from L2 (for a 4096-wide Q4_K row that is 16 KB per
+// wave against 4.6 KB of weights, and the loads' issue, not HBM, set the
+// pace).  Piece q of unit slot k of lane l (a float4 of run q / (UB / 4))
+// sits at [(slice * NU + k) * Q + q][l], so each LDS read of a wave is 64
+// consecutive float4s.  Each wave stages NU * Q / XG pieces per lane, its
+// share of its slice's slots.
+//
+// The staging loads go out first, then the weight loads, then the stores to
+// LDS, which wait for the staging loads alone (the memory counter is in
+// order).  W and x are not __restrict__ here: loads the compiler may not take
+// for invariant keep that program order around the barrier.
+
+template <int T, int UB, int NU, int XG>
+__global__ __launch_bounds__(512) void k_matvec_q_staged(
+    const uint8_t* W, uint32_t nb, const float* x, float* y, uint32_t rows, uint32_t units,
+    uint32_t slice_units, uint32_t S) {
+    // staged x [S][NU][Q][64], then partial [waves][kPasses] when S > 1
+    extern __shared__ xf32x4 smem[];
+    constexpr int kPasses = passes_for<1>(), Q = x_pieces<T, UB>(), XP = NU * Q / XG;
+    static_assert(XP * XG == NU * Q, "pieces split evenly over the waves of a slice");
+    const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
+    const uint32_t group = wave / S, slice = wave % S;
+    const uint64_t nblk = static_cast<uint64_t>(rows) * nb;
+    const uint32_t stride = gridDim.x * XG * kPasses;
+    float* partial = reinterpret_cast<float*>(smem + S * NU * Q * 64u);
+    uint32_t p0 = blockIdx.x * XG * kPasses;
+    if (p0 >= rows) return;  // uniform per workgroup
+
+    MvState<T, 1, UB, NU, false> st;
+#pragma unroll
+    for (int k = 0; k < NU; ++k) {
+        const uint32_t local = lane + 64u * k;
+        const uint32_t u = slice * slice_units + local;
+        st.valid[k] = local < slice_units && u < units;
+        st.pos[k] = unit_pos<T, UB>(st.valid[k] ? u : 0u);
+    }
+    auto issue = [&](uint32_t pp) {
+#pragma unroll
+        for (int q = 0; q < kPasses; ++q) {
+            const uint32_t row = pp + group * kPasses + q;
+            st.row[0][q] = row;
+            st.live[0][q] = row < rows;
+            const QRow qr{W, nblk, static_cast<uint64_t>(row < rows ? row : 0u) * nb};
+#pragma unroll
+            for (int k = 0; k < NU; ++k) unit_load<T, UB>(qr, st.pos[k], st.raw[0][q][k]);
+        }
+    };
+    auto finish = [&](uint32_t pp) {
+#pragma unroll
+        for (int q = 0; q < kPasses; ++q) {
+            float acc[1] = {0.0f};
+#pragma unroll
+            for (int k = 0; k < NU; ++k) {
+                // unconditional, the absent unit's share dropped by a select:
+                // a branch around the dots would let the compiler sink their
+                // weight loads past the staging barrier
+                float t[1] = {0.0f};
+                unit_compute<T, UB, 1>(st.raw[0][q][k], st.pos[k], st.ux[k], t);
+                acc[0] += st.valid[k] ? t[0] : 0.0f;
+            }
+            acc[0] = group_sum<64>(acc[0]);
+            if (lane == 63u) {
+                if (S == 1) {
+                    if (st.live[0][q]) y[st.row[0][q]] = acc[0];
+                } else {
+                    partial[wave * kPasses + q] = acc[0];
+                }
+            }
+        }
+        if (S > 1) {
+            __syncthreads();
+            // the group's first wave adds the slices in order
+            if (slice == 0 && lane < kPasses) {
+                const uint32_t row = pp + group * kPasses + lane;
+                if (row < rows) {
+                    float v = 0.0f;
+                    for (uint32_t sl = 0; sl < S; ++sl) v += partial[(group * S + sl) * kPasses + lane];
+                    y[row] = v;
+                }
+            }
+            __syncthreads();
+        }
+    };
+
+    // staging loads: unconditional (an absent unit reads unit 0's
+    // activations, which no lane uses)
+    xf32x4 xv[XP];
+#pragma unroll
+    for (int j = 0; j < XP; ++j) {
+        const uint32_t piece = group * XP + j;  // (k, q) of this lane's units
+        const uint32_t k = piece / Q, q = piece % Q;
+        const uint32_t local = lane + 64u * k, u = slice * slice_units + local;
+        const bool valid = local < slice_units && u < units;
+        const UnitPos pos = unit_pos<T, UB>(valid ? u : 0u);
+        xv[j] = *reinterpret_cast<const xf32x4*>(x + piece_col<T, UB>(pos, q));
+    }
+    issue(p0);
+    __builtin_amdgcn_sched_barrier(0);
+    // (always true: a block of its own ends at the barrier, so no
+    // dequantisation of the weights is scheduled, and waited for, above it)
+    if (wave < (blockDim.x >> 6)) {
+#pragma unroll
+        for (int j = 0; j < XP; ++j) smem[(slice * (NU * Q) + group * XP + j) * 64u + lane] = xv[j];
+        __syncthreads();
+    }
+#pragma unroll
+    for (int k = 0; k < NU; ++k)
+        load_unit_x_staged<T, UB>(smem + (slice * NU + k) * Q * 64u + lane, 64u, st.ux[k]);
+    finish(p0);
+    for (p0 += stride; p0 < rows; p0 += stride) {
+        issue(p0);
+        finish(p0);
     }
 }
 
@@ -265,6 +383,21 @@ hipError_t run_q(const Plan& pl, const uint8_t* W, uint32_t nb, uint32_t rows,
             hipLaunchKernelGGL((k_matvec_q<T, B, UB, NU, true>), dim3(blocks),
                                dim3(64u * pl.waves_per_block), lds, stream, W, nb, x, in, y, rows,
                                rows, pl.units, pl.slice_units, pl.S, pl.glog2);
+            return hipGetLastError();
+        }
+    }
+    // one vector, rows on 64 lanes, two or four row streams per workgroup
+    // sharing a slice: the activations staged once in LDS (at most 32 KB)
+    if constexpr (B == 1) {
+        const uint32_t xl = pl.S * NU * x_pieces<T, UB>() * 64u * 16u;
+        if (pl.glog2 == 6u && xl <= 32768u && (groups == 4u || groups == 2u)) {
+            const dim3 grid(blocks), block(64u * pl.waves_per_block);
+            if (groups == 4u)
+                hipLaunchKernelGGL((k_matvec_q_staged<T, UB, NU, 4>), grid, block, xl + lds, stream,
+                                   W, nb, x, y, rows, pl.units, pl.slice_units, pl.S);
+            else
+                hipLaunchKernelGGL((k_matvec_q_staged<T, UB, NU, 2>), grid, block, xl + lds, stream,
+                                   W, nb, x, y, rows, pl.units, pl.slice_units, pl.S);
             return hipGetLastError();
         }
     }
