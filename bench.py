@@ -52,6 +52,8 @@ def parse():
     ap.add_argument("--no-decode", action="store_true", help="skip the whole-model decode leg")
     ap.add_argument("--no-matvec", action="store_true", help="skip the C1/C2 matvec leg")
     ap.add_argument("--matvec-reps", type=int, default=10)
+    ap.add_argument("--decode-cpu-full", action="store_true",
+                    help="only time the reference CPU runner on the full 48-layer model")
     ap.add_argument("--matvec-only", action="store_true",
                     help="run only the C1/C2 matvec leg (prints its JSON)")
     ap.add_argument("--calibrate-copy-mib", type=int, default=0,
@@ -348,6 +350,56 @@ def decode_cpu_baseline(prompt_len: int = 32, forwards: int = 20):
                       f"row pool of {workers} workers; host nproc {os.cpu_count()}"}
 
 
+def decode_cpu_full(prompt_len: int = 16, forwards: int = 8):
+    """The reference Qwen3MoeRunner (oracle/_ref) on the full 48-layer
+    config-5 model itself (a ~19 GB GGUF in /dev/shm, or /tmp when /dev/shm
+    is too small), all experts cached after the prompt: seconds of each
+    greedy forward (about 40 s on the GPU box's host).  None when the
+    reference library is not built or no directory has room for the file;
+    the decode leg then extrapolates from 1 and 4 layers."""
+    import shutil
+
+    import numpy as np
+
+    import oracle
+    from pokitlms_amd import gguf
+    from pokitlms_amd import synth_model as SM
+    if not oracle.available("reference"):
+        return None
+    cpu = oracle.Oracle("reference")
+    m = SM.Qwen3MoeShape()
+    need = sum(gguf.payload_bytes(g, dims) for _, dims, g, _ in SM.tensor_list(m))
+    d = next((c for c in ("/dev/shm", "/tmp")
+              if os.path.isdir(c) and shutil.disk_usage(c).free > need * 1.1 + (1 << 30)), None)
+    if d is None:
+        log(f"no directory with {need / 1e9:.1f} GB free for the 48-layer model file")
+        return None
+    path = os.path.join(d, f"pk_bench_decode_full_{os.getpid()}.gguf")
+    step = [0]
+
+    def progress(done, total):
+        if done * 20 // total > step[0]:
+            step[0] = done * 20 // total
+            log(f"writing the 48-layer model: {done}/{total} tensors")
+
+    try:
+        SM.write_gguf(path, m, 1234, progress)
+        log(f"model file {os.path.getsize(path) / 1e9:.2f} GB in {d}; running the reference runner")
+        secs = cpu.qwen3moe_forward_times(path, SM.prompt_tokens(1234, prompt_len, m.vocab), forwards)
+    finally:
+        if os.path.exists(path):
+            os.remove(path)
+    steady = secs[forwards // 4:]
+    per_forward = float(np.median(steady))
+    workers = cpu.lib.pkref_row_workers()
+    return {"value": round(1.0 / per_forward, 4), "unit": "tokens/s", "cores": int(workers),
+            "kind": "reference", "s_per_forward": round(per_forward, 4),
+            "forward_seconds": [round(float(t), 4) for t in secs],
+            "sample": f"reference runner on the full 48-layer config-5 model ({prompt_len}-token "
+                      f"prompt, median of the last {steady.size} of {forwards} greedy forwards); "
+                      f"row pool of {workers} workers; host nproc {os.cpu_count()}"}
+
+
 def divergence_report(ref, fast):
     """Where fast greedy tokens leave the golden ones: the golden logits' top-2
     gap against the fast logits' error at that step.  near_tie: the gap is
@@ -413,8 +465,10 @@ def decode_leg(torch, hip, with_cpu: bool):
     if ref_decode_s:
         out["golden_cpu_s_per_forward"] = round(ref_decode_s / (n_new - 1), 4)
     if with_cpu:
-        log("decode cpu baseline ...")
-        cpu = decode_cpu_baseline()
+        log("decode cpu baseline (the reference runner on the full model) ...")
+        cpu = decode_cpu_full()
+        if cpu is None:
+            cpu = decode_cpu_baseline()
         out["cpu_baseline"] = cpu
         if cpu:
             for mode in ("reference_order", "fast"):
@@ -465,6 +519,10 @@ def main():
         print(json.dumps({"error": "this build runs on one GPU only; --gpus must be 1",
                           "n_gpus": args.gpus}))
         sys.exit(2)
+
+    if args.decode_cpu_full:
+        print(json.dumps({"decode_cpu_full": decode_cpu_full()}), flush=True)
+        return
 
     import numpy as np
     import torch

@@ -176,10 +176,11 @@ def byte_to_unicode() -> list[str]:
     return [out[b] for b in range(256)]
 
 
-def write_gguf(path: str, m: Qwen3MoeShape, seed: int) -> None:
+def write_gguf(path: str, m: Qwen3MoeShape, seed: int, progress=None) -> None:
     """The seeded model as a GGUF v3 file the reference loads (qwen3moe
     architecture, gpt2/qwen2 tokenizer with the 256 byte tokens and unique
-    filler tokens, no merges)."""
+    filler tokens, no merges).  progress(done, total), if given, is called
+    after each tensor's payload is made."""
     w = gguf.GgufWriter()
     md = w.metadata
     md["general.architecture"] = "qwen3moe"
@@ -208,9 +209,16 @@ def write_gguf(path: str, m: Qwen3MoeShape, seed: int) -> None:
     md["tokenizer.ggml.merges"] = ("array", [])
     md["tokenizer.ggml.bos_token_id"] = m.vocab - 1
     md["tokenizer.ggml.eos_token_id"] = m.vocab - 2
-    for i, (name, dims, gtype, kind) in enumerate(tensor_list(m)):
+    items = tensor_list(m)
+
+    def payload(i, gtype, kind, nbytes):
+        data = tensor_payload(seed, i, gtype, kind, nbytes)
+        if progress is not None:
+            progress(i + 1, len(items))
+        return data
+
+    for i, (name, dims, gtype, kind) in enumerate(items):
         nbytes = gguf.payload_bytes(gtype, dims)
         w.add_tensor(name, dims, gtype,
-                     lambda i=i, gtype=gtype, kind=kind, nbytes=nbytes:
-                     tensor_payload(seed, i, gtype, kind, nbytes))
+                     lambda i=i, gtype=gtype, kind=kind, nbytes=nbytes: payload(i, gtype, kind, nbytes))
     w.write(path)
