@@ -166,6 +166,27 @@ def test_odd_batches(hip, port, batch):
     wt.release()
 
 
+@pytest.mark.parametrize("gtype", QUANT + (S.Q2_K, S.Q3_K))
+def test_staged_single_vector_widths(hip, port, gtype):
+    """One vector through the kernel that stages x in LDS for the workgroup:
+    widths whose last unit slot is partly absent (2304, 5120), two K-slices
+    (5120, 8192), and a row count that makes each workgroup walk its loop
+    more than once with a partial last pass (10,001 rows of 2048)."""
+    g = S.rng(91 + gtype)
+    for rows, inn in ((1000, 2304), (777, 4096), (1000, 5120), (513, 8192), (10001, 2048)):
+        if inn % (256 if gtype in (S.Q4_K, S.Q5_K, S.Q6_K, S.Q2_K, S.Q3_K) else 32):
+            continue
+        w = S.quant_matrix(gtype, rows, inn, g)
+        x = S.normal_f32(g, inn).reshape(1, inn)
+        wt = hip.upload(gtype, inn, rows, w)
+        gpu = hip.matvec(wt, x)[0]
+        cpu = port.linear(gtype, w, inn, rows, x[0])
+        err = normwise_rel(gpu, cpu)
+        say("staged matvec", gtype, rows, inn, "normwise", err)
+        assert err <= TOL, (rows, inn)
+        wt.release()
+
+
 @pytest.mark.parametrize("gtype", (S.Q4_K, S.Q6_K, S.Q8_0))
 def test_long_matvec_pipelined_rows(hip, port, gtype):
     """Rows enough that every wave walks several row passes (the pipelined
