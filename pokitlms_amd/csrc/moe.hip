@@ -3,7 +3,7 @@
 // Three launches replace the MoE block of the reference runner
 // (src/qwen3_moe_runner.cpp:643-692) and its route_experts (:267-305):
 //
-//  1. k_router: one workgroup per expert row computes the router logit's
+//  1. k_router: one wave per expert row computes the router logit's
 //     exact value S (FP64 sum of the FP32 products the CPU forms) and a
 //     rigorous bound B on how far the CPU's serial, unfused FP32 sum
 //     (src/linear.cpp:26-30, src/simd_kernels.hpp:22) can be from S:
@@ -42,19 +42,50 @@ constexpr uint32_t kGateUpPasses = 2;  // row passes whose loads a gate/up wave 
 constexpr uint32_t kDownPasses = 2;    // row passes per down workgroup
 
 // ---------------------------------------------------------------------------
-// 1. Router: exact sum and serial-error bound of one expert row per workgroup.
+// 1. Router: exact sum and serial-error bound of one expert row per
+// single-wave workgroup (router_wave_sum_bound, the batched prefill router's
+// arithmetic, so the same bits).
 
-template <int C>  // consecutive products per thread: hidden = 256 * C
-__global__ __launch_bounds__(kRouterThreads) void k_router(MoeDecodeArgs a) {
-    __shared__ double wtot[kRouterThreads / 64];
-    __shared__ double red[kRouterThreads / 64];
+template <int C>  // hidden = 256 * C: 4 * C consecutive products per lane
+__global__ __launch_bounds__(64) void k_router(MoeDecodeArgs a) {
     const uint32_t e = blockIdx.x;  // row n_experts: the shared expert's gate (variant 1)
+    const uint32_t lane = threadIdx.x;
     const float* row = e < a.n_experts ? a.router + static_cast<uint64_t>(e) * a.hidden : a.shared_router;
-    float p[C];
-    router_products<C>(row + threadIdx.x * C, a.x + threadIdx.x * C, p);
+    rf32x4 w[C], x[C];
+    if constexpr (C <= 16) {
+        // through LDS: loaded with consecutive lanes on consecutive float4s
+        // (whole cache lines per load), read back lane-contiguous, one float4
+        // of padding per C so no two lanes of a read meet in one bank
+        __shared__ rf32x4 buf[2][64u * (C + 1u)];
+        const rf32x4* wg = reinterpret_cast<const rf32x4*>(row);
+        const rf32x4* xg = reinterpret_cast<const rf32x4*>(a.x);
+#pragma unroll
+        for (uint32_t m = 0; m < C; ++m) {
+            w[m] = wg[m * 64u + lane];
+            x[m] = xg[m * 64u + lane];
+        }
+#pragma unroll
+        for (uint32_t m = 0; m < C; ++m) {
+            const uint32_t g = m * 64u + lane, pos = g + g / C;
+            buf[0][pos] = w[m];
+            buf[1][pos] = x[m];
+        }
+        __syncthreads();
+#pragma unroll
+        for (uint32_t j = 0; j < C; ++j) {
+            w[j] = buf[0][lane * (C + 1u) + j];
+            x[j] = buf[1][lane * (C + 1u) + j];
+        }
+    } else {
+        router_lane_load<C>(row, lane, w);
+        router_lane_load<C>(a.x, lane, x);
+        __builtin_amdgcn_sched_barrier(0);  // every load out before the first is waited for
+    }
+    RouterLane<C> r;
     double total, bound;
-    router_sum_bound<C>(p, wtot, red, total, bound);
-    if (threadIdx.x == 0) {
+    router_lane_sums<C>(w, x, r);
+    router_wave_sum_bound<C>(r, total, bound);
+    if (lane == 0) {
         a.row_sum[e] = total;
         a.row_bound[e] = bound;
     }
@@ -373,7 +404,7 @@ hipError_t launch_moe_router(const MoeDecodeArgs& a, hipStream_t s) {
     switch (a.hidden / kRouterThreads) {
 #define PK_RT(C)                                                                                \
     case C:                                                                                     \
-        hipLaunchKernelGGL(k_router<C>, dim3(a.n_experts + a.variant), dim3(kRouterThreads), a.hidden * sizeof(float), s, a); \
+        hipLaunchKernelGGL(k_router<C>, dim3(a.n_experts + a.variant), dim3(64), 0, s, a);     \
         break;
         PK_RT(2) PK_RT(4) PK_RT(8) PK_RT(12) PK_RT(16) PK_RT(24) PK_RT(32)
 #undef PK_RT

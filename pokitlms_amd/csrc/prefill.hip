@@ -6,8 +6,8 @@
 // whole batch goes through six launches:
 //
 //  1. k_router_batch: the logit value S and rounding bound B of every
-//     (token, expert) pair (the decode router's arithmetic, a few expert rows
-//     held in registers across a tile of tokens).
+//     (token, expert) pair (the decode router's arithmetic, one expert row
+//     per wave held in registers across a tile of tokens).
 //  2. k_route_batch: one workgroup per token ranks the experts exactly as the
 //     decode path does (certified wave ranking, exact serial fallback) and
 //     writes ids and route weights.
@@ -179,91 +179,53 @@ __device__ __forceinline__ void raw32_bf16(const Raw32<T>& r, uint32_t k0, uint3
 // ---------------------------------------------------------------------------
 // 1. Batched router.
 
-// Expert rows per workgroup: C = hidden / 256 router values per thread and
-// row stay in registers.
+// Expert rows per wave: C = hidden / 256, so 4 * C router values per lane
+// and row stay in registers.
 template <int C>
-constexpr uint32_t router_rows_per_wg() { return C <= 8 ? 4u : C <= 16 ? 2u : 1u; }
+constexpr uint32_t router_rows_per_wave() { return C <= 8 ? 4u : C <= 16 ? 2u : 1u; }
 
-// Per (token, expert) the S and B of router_sum_bound, with its operations in
-// its order (so the decode path's bits).  A workgroup holds EB expert rows in
+// Per (token, expert) the S and B of router_wave_sum_bound, from the same
+// lane sums (so the decode path's bits).  Each wave holds R expert rows in
 // registers and walks kRouterTokens tokens, reading each token's x once for
-// all EB rows; the rows' scans and reductions share two barriers per token.
-// The cross-wave totals are double-buffered by token parity, so a wave that
-// runs ahead into the next token never overwrites what the finishing threads
-// still read.
+// its R rows (the next token's x while the current one is summed); the four
+// waves of a workgroup take 4 R rows and the same tokens.  No barrier: the
+// waves never wait for one another.
 template <int C>
-__global__ __launch_bounds__(kRouterThreads, 4) void k_router_batch(MoePrefillArgs a) {
-    constexpr uint32_t EB = router_rows_per_wg<C>(), NW = kRouterThreads / 64;
-    __shared__ double wtot[2][EB][NW];
-    __shared__ double red[2][EB][NW];
-    // rows: the n_experts router rows, then (variant 1) the shared expert's gate
+__global__ __launch_bounds__(256) void k_router_batch(MoePrefillArgs a) {
+    constexpr uint32_t R = router_rows_per_wave<C>();
     const uint32_t E = a.layer.n_experts, ER = E + a.layer.variant, H = a.layer.hidden;
     const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
-    const uint32_t e0 = blockIdx.x * EB;
+    // rows: the n_experts router rows, then (variant 1) the shared expert's gate
+    const uint32_t e0 = (blockIdx.x * 4u + wave) * R;
     const uint32_t t0 = blockIdx.y * kRouterTokens;
     const uint32_t t1 = t0 + kRouterTokens < a.tokens ? t0 + kRouterTokens : a.tokens;
-    float wr[EB][C];
+    rf32x4 w[R][C], xc[C];
 #pragma unroll
-    for (uint32_t e = 0; e < EB; ++e) {
-        const uint32_t ee = e0 + e < ER ? e0 + e : ER - 1u;  // rows past the end repeat the last (never written)
+    for (uint32_t r = 0; r < R; ++r) {
+        const uint32_t ee = e0 + r < ER ? e0 + r : ER - 1u;  // rows past the end repeat the last, write nothing
         const float* row = ee < E ? a.layer.router + static_cast<uint64_t>(ee) * H : a.layer.shared_router;
-        const float* w = row + threadIdx.x * C;
-#pragma unroll
-        for (int i = 0; i < C; i += 2) {
-            const float2 v = *reinterpret_cast<const float2*>(w + i);
-            wr[e][i] = v.x;
-            wr[e][i + 1] = v.y;
-        }
+        router_lane_load<C>(row, lane, w[r]);
     }
+    router_lane_load<C>(a.x + static_cast<uint64_t>(t0) * H, lane, xc);
     for (uint32_t t = t0; t < t1; ++t) {
-        const uint32_t par = t & 1u;
-        const float* xx = a.x + static_cast<uint64_t>(t) * H + threadIdx.x * C;
-        float xv[C];
+        // the next token's x (the last token reloads its own: unconditional)
+        const uint32_t tn = t + 1u < t1 ? t + 1u : t;
+        rf32x4 xn[C];
+        router_lane_load<C>(a.x + static_cast<uint64_t>(tn) * H, lane, xn);
+        __builtin_amdgcn_sched_barrier(0);  // the loads out before the sums wait
 #pragma unroll
-        for (int i = 0; i < C; i += 2) {
-            const float2 v = *reinterpret_cast<const float2*>(xx + i);
-            xv[i] = v.x;
-            xv[i + 1] = v.y;
-        }
-        double local[EB], run_abs[EB], incl[EB];
-#pragma unroll
-        for (uint32_t e = 0; e < EB; ++e) {
-            local[e] = 0.0;
-            run_abs[e] = 0.0;
-#pragma unroll
-            for (int i = 0; i < C; ++i) {
-                local[e] += static_cast<double>(__fmul_rn(wr[e][i], xv[i]));  // the CPU's products
-                run_abs[e] += fabs(local[e]);
+        for (uint32_t r = 0; r < R; ++r) {
+            RouterLane<C> rl;
+            double total, bound;
+            router_lane_sums<C>(w[r], xc, rl);
+            router_wave_sum_bound<C>(rl, total, bound);
+            if (lane == 0 && e0 + r < ER) {
+                a.row_sum[static_cast<uint64_t>(t) * ER + e0 + r] = total;
+                a.row_bound[static_cast<uint64_t>(t) * ER + e0 + r] = bound;
             }
         }
 #pragma unroll
-        for (uint32_t e = 0; e < EB; ++e) incl[e] = wave_inclusive_scan(local[e]);
-        if (lane == 63) {
-#pragma unroll
-            for (uint32_t e = 0; e < EB; ++e) wtot[par][e][wave] = incl[e];
-        }
-        __syncthreads();
-#pragma unroll
-        for (uint32_t e = 0; e < EB; ++e) {
-            double off = incl[e] - local[e];
-            for (uint32_t v = 0; v < wave; ++v) off += wtot[par][e][v];
-            run_abs[e] = lane63(group_sum<64>(__builtin_fma(static_cast<double>(C), fabs(off), run_abs[e])));
-        }
-        if (lane == 0) {
-#pragma unroll
-            for (uint32_t e = 0; e < EB; ++e) red[par][e][wave] = run_abs[e];
-        }
-        __syncthreads();
-        const uint32_t e = threadIdx.x;
-        if (e < EB && e0 + e < ER) {
-            double total = 0.0, q = red[par][e][0];
-            for (uint32_t v = 0; v < NW; ++v) total += wtot[par][e][v];
-            for (uint32_t v = 1; v < NW; ++v) q += red[par][e][v];
-            double bound = q * (0x1p-24 * (1.0 + 0x1p-10) + 0x1p-39);
-            if (!(q < 5.0e35)) bound = INFINITY;  // near FP32 overflow: always recompute
-            a.row_sum[static_cast<uint64_t>(t) * ER + e0 + e] = total;
-            a.row_bound[static_cast<uint64_t>(t) * ER + e0 + e] = bound;
-        }
+        for (int j = 0; j < C; ++j) xc[j] = xn[j];
     }
 }
 
@@ -1163,8 +1125,8 @@ hipError_t launch_prefill_routing(const MoePrefillArgs& a, hipStream_t s) {
     const MoeDecodeArgs& L = a.layer;
     // 1. router
     const uint32_t per = L.hidden / kRouterThreads;
-    const uint32_t eb = per <= 8u ? 4u : per <= 16u ? 2u : 1u;  // router_rows_per_wg<per>()
-    const dim3 rgrid(ceil_div_u(L.n_experts + L.variant, eb), ceil_div_u(a.tokens, kRouterTokens));
+    const uint32_t rw = per <= 8u ? 4u : per <= 16u ? 2u : 1u;  // router_rows_per_wave<per>()
+    const dim3 rgrid(ceil_div_u(L.n_experts + L.variant, 4u * rw), ceil_div_u(a.tokens, kRouterTokens));
     switch (L.hidden / kRouterThreads) {
 #define PK_RB(C)                                                                              \
     case C:                                                                                   \

@@ -409,64 +409,79 @@ __device__ __forceinline__ void write_routes(const MoeDecodeArgs& a, const uint3
 // products it forms) and a rigorous bound B on how far the CPU's serial,
 // unfused FP32 sum (src/linear.cpp:26-30, src/simd_kernels.hpp:22) can be
 // from S:  |serial - S| <= u * sum_i |T_i| / (1 - n u),  T_i = exact prefix
-// sums.  A workgroup of kRouterThreads threads handles one row, thread t
-// holding the C consecutive products t*C .. t*C + C - 1 (hidden = 256 * C).
+// sums.  One wave handles a row, lane l holding the N = 4 * N4 consecutive
+// products l*N .. l*N + N - 1 (hidden = 64 * N): no barrier and no LDS.
 
-template <int C>
-__device__ __forceinline__ void router_products(const float* w, const float* xx, float (&p)[C]) {
-    static_assert(C % 2 == 0, "router rows split into pairs of products per thread");
-    if constexpr (C % 4 == 0) {
+// The row's and x's pieces of one lane (float4 pieces, loads only).
+template <int N4>
+__device__ __forceinline__ void router_lane_load(const float* v, uint32_t lane, rf32x4 (&r)[N4]) {
+    const rf32x4* p = reinterpret_cast<const rf32x4*>(v) + lane * N4;
 #pragma unroll
-        for (int i = 0; i < C; i += 4) {
-            const float4 wv = *reinterpret_cast<const float4*>(w + i);
-            const float4 xv = *reinterpret_cast<const float4*>(xx + i);
-            p[i + 0] = __fmul_rn(wv.x, xv.x);  // the CPU's rounded products, exactly
-            p[i + 1] = __fmul_rn(wv.y, xv.y);
-            p[i + 2] = __fmul_rn(wv.z, xv.z);
-            p[i + 3] = __fmul_rn(wv.w, xv.w);
-        }
-    } else {
+    for (int j = 0; j < N4; ++j) r[j] = p[j];
+}
+
+// A lane's products in chunks of 8 consecutive elements (K = N / 8 chunks):
+// per chunk the sum L and the sum of |running sums| over its elements.  The
+// chunks' chains are independent, so their adds overlap.
+template <int N4>
+struct RouterLane {
+    static constexpr int K = N4 / 2;  // N = 4 * N4 = 8 * K
+    double local[K], run_abs[K];
+};
+
+// One chunk's running sums over its products fl(w_i * x_i) (the CPU's
+// rounded products, exactly), in element order (w, x: the chunk's two float4
+// pieces from index j).
+__device__ __forceinline__ void router_chunk_sums(const rf32x4* w, const rf32x4* x, double& l,
+                                                  double& ra) {
+    l = 0.0;
+    ra = 0.0;
 #pragma unroll
-        for (int i = 0; i < C; i += 2) {
-            const float2 wv = *reinterpret_cast<const float2*>(w + i);
-            const float2 xv = *reinterpret_cast<const float2*>(xx + i);
-            p[i + 0] = __fmul_rn(wv.x, xv.x);
-            p[i + 1] = __fmul_rn(wv.y, xv.y);
+    for (int j = 0; j < 2; ++j) {
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            l += static_cast<double>(__fmul_rn(w[j][c], x[j][c]));
+            ra += fabs(l);
         }
     }
 }
 
-// S and B of the row whose products the workgroup holds (valid in thread 0).
-// Every thread must call it; wtot and red are kRouterThreads / 64 doubles of
-// shared memory, reusable by the next call.
-//
-// S: the FP64 sum of the products (thread sums in element order, a wave scan,
-// then the wave totals in wave order).  B bounds the CPU's serial FP32
-// rounding, u * sum_i |T_i| with T_i the exact prefix sums, in one pass
-// through the triangle inequality per thread: with O the thread's offset (the
-// earlier threads' products) and L_i its own running sum,
-// sum_i |O + L_i| <= C |O| + sum_i |L_i| (at most 2 sum |L_i| looser than the
-// exact prefixes).  sum_i |p_i| <= 2 sum_i |T_i| covers the FP64 rounding of
-// S.  The batched prefill router repeats these operations in this order, so
-// both paths rank on the same bits.
-template <int C>
-__device__ __forceinline__ void router_sum_bound(const float (&p)[C], double* wtot, double* red,
-                                                 double& total, double& bound) {
-    const uint32_t t = threadIdx.x, lane = t & 63u, wave = t >> 6;
-    double local = 0.0, run_abs = 0.0;
+// Every chunk of the lane.
+template <int N4>
+__device__ __forceinline__ void router_lane_sums(const rf32x4 (&w)[N4], const rf32x4 (&x)[N4],
+                                                 RouterLane<N4>& r) {
+    static_assert(N4 % 2 == 0, "whole chunks of 8 products per lane");
 #pragma unroll
-    for (int i = 0; i < C; ++i) {
-        local += static_cast<double>(p[i]);
-        run_abs += fabs(local);
+    for (int k = 0; k < RouterLane<N4>::K; ++k) router_chunk_sums(&w[2 * k], &x[2 * k], r.local[k], r.run_abs[k]);
+}
+
+// S and B of the row whose chunk sums the wave holds (uniform results).
+//
+// S: the FP64 sum of the products (chunk sums in chunk order within a lane,
+// then a wave scan; S is the last lane's inclusive value).  B bounds the
+// CPU's serial FP32 rounding, u * sum_i |T_i| with T_i the exact prefix sums,
+// in one pass through the triangle inequality per chunk of 8: with O the
+// chunk's offset (every earlier product) and L_i its own running sum,
+// sum_i |O + L_i| <= 8 |O| + sum_i |L_i| (about 8% above the exact prefixes
+// on router-like rows of 2,048).  sum_i |p_i| <= 2 sum_i |T_i| covers the FP64
+// rounding of S.  The batched prefill router calls the same functions, so
+// both paths rank on the same bits.
+template <int N4>
+__device__ __forceinline__ void router_wave_sum_bound(const RouterLane<N4>& r, double& total,
+                                                      double& bound) {
+    constexpr int K = RouterLane<N4>::K;
+    double lane_sum = r.local[0];
+#pragma unroll
+    for (int k = 1; k < K; ++k) lane_sum += r.local[k];
+    const double incl = wave_inclusive_scan(lane_sum);
+    total = lane63(incl);
+    double off = incl - lane_sum, qs = 0.0;
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+        qs += __builtin_fma(8.0, fabs(off), r.run_abs[k]);
+        off += r.local[k];
     }
-    const double incl = wave_inclusive_scan(local);
-    if (lane == 63) wtot[wave] = incl;
-    __syncthreads();
-    double off = incl - local;
-    for (uint32_t v = 0; v < wave; ++v) off += wtot[v];
-    total = 0.0;
-    for (uint32_t v = 0; v < (kRouterThreads >> 6); ++v) total += wtot[v];
-    const double q = block_reduce_d<false>(__builtin_fma(static_cast<double>(C), fabs(off), run_abs), red);
+    const double q = lane63(group_sum<64>(qs));
     // u = 2^-24; (1 + 2^-10) >= 1/(1 - n u) for n <= 2^13 and covers the FP64
     // rounding of the prefix sums; q * 2^-39 >= sum |p| * 2^-40 covers S
     bound = q * (0x1p-24 * (1.0 + 0x1p-10) + 0x1p-39);

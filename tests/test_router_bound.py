@@ -2,9 +2,9 @@
 
 The GPU ranks experts by the FP64 sum S of the CPU's rounded FP32 products
 and certifies the order with B = q (2^-24 (1 + 2^-10) + 2^-39), where, for
-the 256 threads of C consecutive products each, q = sum_t (C |O_t| +
-sum_i |L_{t,i}|) with O_t the sum of the earlier threads' products and
-L_{t,i} the thread's running sum.  The certified ids are only exact if
+the chunks of 8 consecutive products (a wave's lanes hold whole chunks),
+q = sum_t (8 |O_t| + sum_i |L_{t,i}|) with O_t the sum of the earlier
+chunks' products and L_{t,i} the chunk's running sum.  The certified ids are only exact if
 |serial FP32 sum - S| <= B always holds; here the serial sum is computed
 independently (numpy's sequential float32 cumulative sum, the order of
 dot_f32 in src/simd_kernels.hpp:12-24) and the exact value with math.fsum,
