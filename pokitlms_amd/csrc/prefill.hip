@@ -669,9 +669,25 @@ __device__ __forceinline__ void gemm_compute(const GemmStage<TW, DUAL>& st, f32x
 //  * Q6_K: bytes 8kq.. and 16+8kq.. of each of the half's two 32-byte ql runs
 //    (stages g and g + 2 share run g & 1: low and high nibbles), of its 32 qh
 //    bytes (all four stages: bits 2g, 2g + 1), its 8 int8 scales and d.
+// A 32-byte run is loaded as one 16-byte piece per lane (lane kq: bytes
+// 16kq..16kq+15, half the load instructions of two 8-byte pieces) and the two
+// lanes of a row exchange the middle 8 bytes with v_permlane32_swap when a
+// stage uses the run (run_words), not at the load, which would wait for it.
 template <int T> struct WUnit;
 template <> struct WUnit<T_Q4_K> { uint32_t h[4]; uint32_t q[8]; };
 template <> struct WUnit<T_Q6_K> { uint32_t ql[8], qh[4], sc[2]; uint32_t d; };
+
+// Words (bytes 8kq..8kq+7, then 16+8kq..16+8kq+7) of a 32-byte run loaded as
+// lane kq's bytes 16kq..16kq+15 (w[0..3]): lanes 32-63 of the first operand
+// of v_permlane32_swap trade with lanes 0-31 of the second.
+__device__ __forceinline__ void run_words(const uint32_t* w, uint32_t (&o)[4]) {
+    const auto s02 = __builtin_amdgcn_permlane32_swap(w[0], w[2], false, false);
+    const auto s13 = __builtin_amdgcn_permlane32_swap(w[1], w[3], false, false);
+    o[0] = s02[0];
+    o[1] = s13[0];
+    o[2] = s02[1];
+    o[3] = s13[1];
+}
 
 __device__ __forceinline__ void ld8(const uint8_t* p, uint32_t& lo, uint32_t& hi) {
     const uint2 v = *reinterpret_cast<const uint2*>(__builtin_assume_aligned(p, 8));
@@ -679,26 +695,37 @@ __device__ __forceinline__ void ld8(const uint8_t* p, uint32_t& lo, uint32_t& hi
     hi = v.y;
 }
 
-// Unit u of the row (block u / 2, half u % 2) for lanes kq.
-template <int T>
+// Unit u of the row (block u / 2, half u % 2) for lanes kq.  Without HEAD the
+// fields the block's two halves share (Q4_K: the header; Q6_K: d) are left to
+// the caller, who copies them from the block's other unit.
+template <int T, bool HEAD = true>
 __device__ __forceinline__ void wunit_load(const QRow& row, uint32_t u, uint32_t kq, WUnit<T>& U) {
     const uint32_t b = u / 2u, hh = u % 2u;
     if constexpr (T == T_Q4_K) {
         const uint8_t* blk = block_ptr<144>(row, b);
-        ld_words<4>(blk, U.h);
-        const uint8_t* qs = blk + 16u + 64u * hh + 8u * kq;
-#pragma unroll
-        for (uint32_t i = 0; i < 4; ++i) ld8(qs + 16u * i, U.q[2u * i], U.q[2u * i + 1u]);
+        if constexpr (HEAD) ld_words<4>(blk, U.h);
+        const uint8_t* qs = blk + 16u + 64u * hh + 16u * kq;
+        ld_words<4>(qs, *reinterpret_cast<uint32_t(*)[4]>(&U.q[0]));
+        ld_words<4>(qs + 32u, *reinterpret_cast<uint32_t(*)[4]>(&U.q[4]));
     } else {
         using L = Planar<T_Q6_K>;
-        const uint8_t* ql = field_ptr<L::QL, 128>(row, b) + 64u * hh + 8u * kq;
-#pragma unroll
-        for (uint32_t i = 0; i < 4; ++i) ld8(ql + 16u * i, U.ql[2u * i], U.ql[2u * i + 1u]);
-        const uint8_t* qh = field_ptr<L::QH, 64>(row, b) + 32u * hh + 8u * kq;
-        ld8(qh, U.qh[0], U.qh[1]);
-        ld8(qh + 16u, U.qh[2], U.qh[3]);
+        const uint8_t* ql = field_ptr<L::QL, 128>(row, b) + 64u * hh + 16u * kq;
+        ld_words<4>(ql, *reinterpret_cast<uint32_t(*)[4]>(&U.ql[0]));
+        ld_words<4>(ql + 32u, *reinterpret_cast<uint32_t(*)[4]>(&U.ql[4]));
+        ld_words<4>(field_ptr<L::QH, 64>(row, b) + 32u * hh + 16u * kq, U.qh);
         ld8(field_ptr<L::SC, 16>(row, b) + 8u * hh, U.sc[0], U.sc[1]);
-        U.d = ld_u16(field_ptr<L::D, 2>(row, b));
+        if constexpr (HEAD) U.d = ld_u16(field_ptr<L::D, 2>(row, b));
+    }
+}
+
+// The fields of a block that its two halves share.
+template <int T>
+__device__ __forceinline__ void wunit_share(const WUnit<T>& from, WUnit<T>& to) {
+    if constexpr (T == T_Q4_K) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) to.h[i] = from.h[i];
+    } else {
+        to.d = from.d;
     }
 }
 
@@ -713,9 +740,11 @@ __device__ __forceinline__ void wunit_stage(const WUnit<T>& U, uint32_t hh, uint
     uint32_t w[8];
     if constexpr (T == T_Q4_K) {
         const uint32_t c = j / 2u, hi = j & 1u;
+        uint32_t qc[4];
+        run_words(&U.q[4u * c], qc);
 #pragma unroll
         for (uint32_t i = 0; i < 4; ++i) {
-            const uint32_t q = (hi ? U.q[4u * c + i] >> 4 : U.q[4u * c + i]) & 0x0f0f0f0fu;
+            const uint32_t q = (hi ? qc[i] >> 4 : qc[i]) & 0x0f0f0f0fu;
             bf16_bytes(q, w[2u * i], w[2u * i + 1u]);
         }
         const float d = half_bits_to_float(U.h[0] & 0xffffu);
@@ -726,10 +755,13 @@ __device__ __forceinline__ void wunit_stage(const WUnit<T>& U, uint32_t hh, uint
         cb = kq ? 0.0f : -__fmul_rn(dmin, mn);
     } else {
         const uint32_t r = 4u * (j & 1u), sh = j >= 2u ? 4u : 0u;
+        uint32_t ql[4], qh[4];
+        run_words(&U.ql[r], ql);
+        run_words(U.qh, qh);
 #pragma unroll
         for (uint32_t i = 0; i < 4; ++i) {
-            const uint32_t nib = (U.ql[r + i] >> sh) & 0x0f0f0f0fu;
-            const uint32_t hb = ((U.qh[i] >> (2u * j)) & 0x03030303u) << 4;
+            const uint32_t nib = (ql[i] >> sh) & 0x0f0f0f0fu;
+            const uint32_t hb = ((qh[i] >> (2u * j)) & 0x03030303u) << 4;
             bf16_bytes(nib | hb, w[2u * i], w[2u * i + 1u]);
         }
         const float d = half_bits_to_float(U.d);
@@ -967,10 +999,14 @@ __global__ __launch_bounds__(256, 2) void k_expert_gemm_w(MoePrefillArgs a) {
     }
     const uint32_t nu = kdim / 128u, lastu = nu - 1u;  // units per row
     WUnit<TW> ua0, ua1, ub0, ub1;  // matrices 0 and 1: units 2i (a) and 2i + 1 (b)
+    // units a and b are the two halves of one block (clamped units stay in
+    // the last block): b takes the shared fields from a
     wunit_load<TW>(w0, 0u, kq, ua0);
     wunit_load<TW>(w1, 0u, kq, ua1);
-    wunit_load<TW>(w0, 1u < lastu ? 1u : lastu, kq, ub0);
-    wunit_load<TW>(w1, 1u < lastu ? 1u : lastu, kq, ub1);
+    wunit_load<TW, false>(w0, 1u < lastu ? 1u : lastu, kq, ub0);
+    wunit_load<TW, false>(w1, 1u < lastu ? 1u : lastu, kq, ub1);
+    wunit_share<TW>(ua0, ub0);
+    wunit_share<TW>(ua1, ub1);
     const uint16_t* parts = DUAL ? a.x_parts : a.act_parts;
     const uint64_t plane = DUAL ? static_cast<uint64_t>(a.tokens) * L.hidden
                                 : static_cast<uint64_t>(a.tokens) * (L.top_k + L.variant) * L.ffn;
@@ -1008,8 +1044,10 @@ __global__ __launch_bounds__(256, 2) void k_expert_gemm_w(MoePrefillArgs a) {
             }
             if (t == 7u) {
                 const uint32_t un = u0 + 3u < lastu ? u0 + 3u : lastu;
-                wunit_load<TW>(w0, un, kq, ub0);
-                wunit_load<TW>(w1, un, kq, ub1);
+                wunit_load<TW, false>(w0, un, kq, ub0);
+                wunit_load<TW, false>(w1, un, kq, ub1);
+                wunit_share<TW>(ua0, ub0);  // ua holds unit u0 + 2, of the same block
+                wunit_share<TW>(ua1, ub1);
             }
             __syncthreads();
         }
