@@ -774,6 +774,36 @@ __device__ __forceinline__ void wunit_stage(const WUnit<T>& U, uint32_t hh, uint
     b[1] = __builtin_bit_cast(bf16x8, make_uint4(w[4], w[5], w[6], w[7]));
 }
 
+// The register-weight kernel's activation loads per stage, with no duplicate
+// loads: the stage's 384 pieces go to pieces tid (every thread) and tid + 256
+// (waves 0 and 1), its group sums to wave 2 (lane t: sum t, clamped).  The
+// branches are uniform per wave.
+template <int TW, bool DUAL>
+__device__ __forceinline__ void gemm_src_w(GemmSrc<TW, DUAL>& g, const QRow& wrow,
+                                           const uint16_t* parts, uint64_t plane, uint32_t kdim,
+                                           const float* sums, const uint32_t* arow) {
+    using C = GemmCfg<TW, DUAL>;
+    static_assert(C::NQ == 384u, "pieces tid and, in waves 0 and 1, tid + 256");
+    static_assert(C::NG * kTileM <= 64u, "one wave of group sums");
+    const uint32_t tid = threadIdx.x, lane = tid & 63u;
+    g.wrow = wrow;
+    gemm_piece<TW, DUAL>(parts, plane, kdim, arow, tid, g.ap0, g.adst0);
+    gemm_piece<TW, DUAL>(parts, plane, kdim, arow, tid + 256u, g.ap1, g.adst1);
+    const uint32_t t = lane < C::NG * kTileM ? lane : C::NG * kTileM - 1u;
+    g.xs = sums + static_cast<uint64_t>(arow[t % kTileM]) * (kdim / C::G) + t / kTileM;
+    g.xdst = t;
+}
+
+template <int TW, bool DUAL>
+__device__ __forceinline__ void gemm_load_act_w(GemmPrefetch<TW, DUAL>& f, const GemmSrc<TW, DUAL>& g,
+                                                uint32_t k0) {
+    using C = GemmCfg<TW, DUAL>;
+    const uint32_t wave = threadIdx.x >> 6;
+    f.ap0 = *reinterpret_cast<const u32x4_t*>(g.ap0 + k0);
+    if (wave < 2u) f.ap1 = *reinterpret_cast<const u32x4_t*>(g.ap1 + k0);
+    if (wave == 2u) f.xs = g.xs[k0 / C::G];
+}
+
 // Activation planes and group sums of one stage, shared by the workgroup.
 template <int TW, bool DUAL>
 struct alignas(16) GemmStageA {
@@ -785,9 +815,10 @@ struct alignas(16) GemmStageA {
 template <int TW, bool DUAL>
 __device__ __forceinline__ void gemm_store_a(GemmStageA<TW, DUAL>& st, const GemmPrefetch<TW, DUAL>& f,
                                              const GemmSrc<TW, DUAL>& g) {
+    const uint32_t wave = threadIdx.x >> 6;
     *reinterpret_cast<u32x4_t*>(st.a + g.adst0) = f.ap0;
-    *reinterpret_cast<u32x4_t*>(st.a + g.adst1) = f.ap1;
-    st.xs[g.xdst] = f.xs;
+    if (wave < 2u) *reinterpret_cast<u32x4_t*>(st.a + g.adst1) = f.ap1;
+    if (wave == 2u) st.xs[g.xdst] = f.xs;
 }
 
 // One stage of one wave from register weights: the bias MFMA, then per
@@ -1013,14 +1044,14 @@ __global__ __launch_bounds__(256, 2) void k_expert_gemm_w(MoePrefillArgs a) {
     const float* sums = DUAL ? a.x_sums : a.act_sums;
     __syncthreads();
     GemmSrc<TW, DUAL> src;
-    gemm_src<TW, DUAL>(src, w0, parts, plane, kdim, sums, arow);
+    gemm_src_w<TW, DUAL>(src, w0, parts, plane, kdim, sums, arow);
     const uint32_t nst = kdim / C::KC, last = nst - 1u;  // a multiple of 8 (kdim % 256 == 0)
     auto stage_k = [&](uint32_t s) { return (s < last ? s : last) * C::KC; };  // tail: harmless reloads
     GemmPrefetch<TW, DUAL> f0, f1;
-    gemm_load_act<TW, DUAL>(f0, src, 0u);
-    gemm_load_act<TW, DUAL>(f1, src, stage_k(1u));
+    gemm_load_act_w<TW, DUAL>(f0, src, 0u);
+    gemm_load_act_w<TW, DUAL>(f1, src, stage_k(1u));
     gemm_store_a<TW, DUAL>(st[0], f0, src);
-    gemm_load_act<TW, DUAL>(f0, src, stage_k(2u));
+    gemm_load_act_w<TW, DUAL>(f0, src, stage_k(2u));
     __syncthreads();
     f32x16 acc = {}, acc2 = {};
     // Stage s's activations live in f(s % 2); step s computes stage s, stores
@@ -1036,7 +1067,7 @@ __global__ __launch_bounds__(256, 2) void k_expert_gemm_w(MoePrefillArgs a) {
             if (t < 4u) gemm_compute_w<TW, DUAL>(st[s & 1u], ua0, ua1, 0u, t, acc, acc2);
             else gemm_compute_w<TW, DUAL>(st[s & 1u], ub0, ub1, 1u, t - 4u, acc, acc2);
             gemm_store_a<TW, DUAL>(st[(s + 1u) & 1u], f, src);
-            gemm_load_act<TW, DUAL>(f, src, stage_k(s + 3u));
+            gemm_load_act_w<TW, DUAL>(f, src, stage_k(s + 3u));
             if (t == 3u) {
                 const uint32_t un = u0 + 2u < lastu ? u0 + 2u : lastu;
                 wunit_load<TW>(w0, un, kq, ua0);
