@@ -118,6 +118,15 @@ __device__ __forceinline__ void bf16_bytes(uint32_t w, uint32_t& lo, uint32_t& h
     hi = bf16_pair(ub<2>(w), ub<3>(w));
 }
 
+// The bytes f0..f3 of w as the bf16 pairs of 128 + f (bits 0x4300 | f: the
+// exponent of 128 leaves f in the low mantissa bits), one v_perm per pair:
+// the weight operand of the register-weight GEMM, whose group bias absorbs
+// the -128 * ds (a bf16 of 128 + f is exact for f < 128).
+__device__ __forceinline__ void bf16_bytes_b128(uint32_t w, uint32_t& lo, uint32_t& hi) {
+    lo = __builtin_amdgcn_perm(0x43434343u, w, 0x04010400u);  // bytes f0, 0x43, f1, 0x43
+    hi = __builtin_amdgcn_perm(0x43434343u, w, 0x04030402u);  // bytes f2, 0x43, f3, 0x43
+}
+
 template <int T>
 __device__ __forceinline__ void raw32_bf16(const Raw32<T>& r, uint32_t k0, uint32_t (&bw)[16],
                                            float (&ds)[2], float (&cn)[2]) {
@@ -731,9 +740,10 @@ __device__ __forceinline__ void wunit_share(const WUnit<T>& from, WUnit<T>& to) 
 
 // Stage j (0..3) of the unit in half hh of its block: the lane's two bf16x8
 // B fragments, the scale of each (Q4_K: one scale group per stage, Q6_K: one
-// per fragment) and the bias operand cb = cn of scale group kq of the stage
-// (0 where the stage has a single group and kq = 1); weights are
-// ds * f + cn per group as in raw32_bf16.
+// per fragment) and the bias operand cb of scale group kq of the stage (0
+// where the stage has a single group and kq = 1).  Weights are ds * f + cn
+// per group as in raw32_bf16; the fragments hold 128 + f (bf16_bytes_b128),
+// so cb = cn - 128 ds.
 template <int T>
 __device__ __forceinline__ void wunit_stage(const WUnit<T>& U, uint32_t hh, uint32_t j, uint32_t kq,
                                             bf16x8 (&b)[2], float (&ds)[2], float& cb) {
@@ -745,14 +755,14 @@ __device__ __forceinline__ void wunit_stage(const WUnit<T>& U, uint32_t hh, uint
 #pragma unroll
         for (uint32_t i = 0; i < 4; ++i) {
             const uint32_t q = (hi ? qc[i] >> 4 : qc[i]) & 0x0f0f0f0fu;
-            bf16_bytes(q, w[2u * i], w[2u * i + 1u]);
+            bf16_bytes_b128(q, w[2u * i], w[2u * i + 1u]);
         }
         const float d = half_bits_to_float(U.h[0] & 0xffffu);
         const float dmin = half_bits_to_float(U.h[0] >> 16);
         float sc, mn;
         kq_scale_min(U.h, 4u * hh + j, sc, mn);
         ds[0] = ds[1] = __fmul_rn(d, sc);
-        cb = kq ? 0.0f : -__fmul_rn(dmin, mn);
+        cb = kq ? 0.0f : -__fmaf_rn(128.0f, ds[0], __fmul_rn(dmin, mn));
     } else {
         const uint32_t r = 4u * (j & 1u), sh = j >= 2u ? 4u : 0u;
         uint32_t ql[4], qh[4];
@@ -762,13 +772,13 @@ __device__ __forceinline__ void wunit_stage(const WUnit<T>& U, uint32_t hh, uint
         for (uint32_t i = 0; i < 4; ++i) {
             const uint32_t nib = (ql[i] >> sh) & 0x0f0f0f0fu;
             const uint32_t hb = ((qh[i] >> (2u * j)) & 0x03030303u) << 4;
-            bf16_bytes(nib | hb, w[2u * i], w[2u * i + 1u]);
+            bf16_bytes_b128(nib | hb, w[2u * i], w[2u * i + 1u]);
         }
         const float d = half_bits_to_float(U.d);
         const uint32_t s2 = (U.sc[j / 2u] >> (16u * (j & 1u))) & 0xffffu;  // scales of the two halves
         ds[0] = __fmul_rn(d, static_cast<float>(static_cast<int8_t>(s2 & 0xffu)));
         ds[1] = __fmul_rn(d, static_cast<float>(static_cast<int8_t>(s2 >> 8)));
-        cb = __fmul_rn(-32.0f, kq ? ds[1] : ds[0]);
+        cb = __fmul_rn(-160.0f, kq ? ds[1] : ds[0]);  // (q - 32) * ds as (128 + q) * ds - 160 ds
     }
     b[0] = __builtin_bit_cast(bf16x8, make_uint4(w[0], w[1], w[2], w[3]));
     b[1] = __builtin_bit_cast(bf16x8, make_uint4(w[4], w[5], w[6], w[7]));
