@@ -740,10 +740,10 @@ __device__ __forceinline__ void wunit_share(const WUnit<T>& from, WUnit<T>& to) 
 
 // Stage j (0..3) of the unit in half hh of its block: the lane's two bf16x8
 // B fragments, the scale of each (Q4_K: one scale group per stage, Q6_K: one
-// per fragment) and the bias operand cb of scale group kq of the stage (0
-// where the stage has a single group and kq = 1).  Weights are ds * f + cn
-// per group as in raw32_bf16; the fragments hold 128 + f (bf16_bytes_b128),
-// so cb = cn - 128 ds.
+// per fragment) and the bias operand cb of scale group kq of the stage (of
+// its single group for Q4_K).  Weights are ds * f + cn per group as in
+// raw32_bf16; the fragments hold 128 + f (bf16_bytes_b128), so
+// cb = cn - 128 ds.
 template <int T>
 __device__ __forceinline__ void wunit_stage(const WUnit<T>& U, uint32_t hh, uint32_t j, uint32_t kq,
                                             bf16x8 (&b)[2], float (&ds)[2], float& cb) {
@@ -762,7 +762,7 @@ __device__ __forceinline__ void wunit_stage(const WUnit<T>& U, uint32_t hh, uint
         float sc, mn;
         kq_scale_min(U.h, 4u * hh + j, sc, mn);
         ds[0] = ds[1] = __fmul_rn(d, sc);
-        cb = kq ? 0.0f : -__fmaf_rn(128.0f, ds[0], __fmul_rn(dmin, mn));
+        cb = -__fmaf_rn(128.0f, ds[0], __fmul_rn(dmin, mn));  // every lane: see gemm_compute_w
     } else {
         const uint32_t r = 4u * (j & 1u), sh = j >= 2u ? 4u : 0u;
         uint32_t ql[4], qh[4];
@@ -833,20 +833,40 @@ __device__ __forceinline__ void gemm_store_a(GemmStageA<TW, DUAL>& st, const Gem
 
 // One stage of one wave from register weights: the bias MFMA, then per
 // fragment h the three plane MFMAs; each scale group's sum is scaled into the
-// accumulator when it closes.
+// accumulator when it closes.  The bias MFMA (K = 2: lanes kq hold group kq)
+// covers the stage's two groups (Q6_K) or, for one group per stage (Q4_K),
+// the groups of stages j - 1 and j at odd j: even stages keep their group
+// sum and bias operands in bias_prev.
+struct BiasPrev {
+    float av, c0, c1;
+};
+
 template <int TW, bool DUAL>
 __device__ __forceinline__ void gemm_compute_w(const GemmStageA<TW, DUAL>& st, const WUnit<TW>& U0,
                                                const WUnit<TW>& U1, uint32_t hh, uint32_t j,
-                                               f32x16& acc, f32x16& acc2) {
+                                               f32x16& acc, f32x16& acc2, BiasPrev& bp) {
     using C = GemmCfg<TW, DUAL>;
     const uint32_t lane = threadIdx.x & 63u, m = lane % 32u, kq = lane / 32u;
     bf16x8 b0[2], b1[2];
     float d0[2], d1[2], c0, c1;
     wunit_stage<TW>(U0, hh, j, kq, b0, d0, c0);
     wunit_stage<TW>(U1, hh, j, kq, b1, d1, c1);
-    const float av = (C::NG == 1u && kq) ? 0.0f : st.xs[(C::NG == 1u ? 0u : kq) * kTileM + m];
-    acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av, c0, acc, 0, 0, 0);
-    acc2 = __builtin_amdgcn_mfma_f32_32x32x2f32(av, c1, acc2, 0, 0, 0);
+    if constexpr (C::NG == 1u) {
+        const float av = st.xs[m];
+        if ((j & 1u) == 0u) {
+            bp.av = av;
+            bp.c0 = c0;
+            bp.c1 = c1;
+        } else {
+            const float a2 = kq ? av : bp.av;
+            acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a2, kq ? c0 : bp.c0, acc, 0, 0, 0);
+            acc2 = __builtin_amdgcn_mfma_f32_32x32x2f32(a2, kq ? c1 : bp.c1, acc2, 0, 0, 0);
+        }
+    } else {
+        const float av = st.xs[kq * kTileM + m];
+        acc = __builtin_amdgcn_mfma_f32_32x32x2f32(av, c0, acc, 0, 0, 0);
+        acc2 = __builtin_amdgcn_mfma_f32_32x32x2f32(av, c1, acc2, 0, 0, 0);
+    }
     f32x16 P, Q;
 #pragma unroll
     for (uint32_t h = 0; h < 2; ++h) {
@@ -1064,6 +1084,7 @@ __global__ __launch_bounds__(256, 2) void k_expert_gemm_w(MoePrefillArgs a) {
     gemm_load_act_w<TW, DUAL>(f0, src, stage_k(2u));
     __syncthreads();
     f32x16 acc = {}, acc2 = {};
+    BiasPrev bp{0.0f, 0.0f, 0.0f};
     // Stage s's activations live in f(s % 2); step s computes stage s, stores
     // stage s + 1 and loads stage s + 3.  Steps 0-3 of an iteration use units
     // a, steps 4-7 units b; each buffer reloads (two units on) after its last
@@ -1074,8 +1095,8 @@ __global__ __launch_bounds__(256, 2) void k_expert_gemm_w(MoePrefillArgs a) {
         for (uint32_t t = 0; t < 8u; ++t) {
             const uint32_t s = s0 + t;
             GemmPrefetch<TW, DUAL>& f = (t & 1u) ? f0 : f1;
-            if (t < 4u) gemm_compute_w<TW, DUAL>(st[s & 1u], ua0, ua1, 0u, t, acc, acc2);
-            else gemm_compute_w<TW, DUAL>(st[s & 1u], ub0, ub1, 1u, t - 4u, acc, acc2);
+            if (t < 4u) gemm_compute_w<TW, DUAL>(st[s & 1u], ua0, ua1, 0u, t, acc, acc2, bp);
+            else gemm_compute_w<TW, DUAL>(st[s & 1u], ub0, ub1, 1u, t - 4u, acc, acc2, bp);
             gemm_store_a<TW, DUAL>(st[(s + 1u) & 1u], f, src);
             gemm_load_act_w<TW, DUAL>(f, src, stage_k(s + 3u));
             if (t == 3u) {
