@@ -241,25 +241,28 @@ __device__ __forceinline__ uint32_t piece_col(const UnitPos& p, uint32_t q) {
     return col + 4u * i;
 }
 
-// load_unit_x for one vector from staged pieces (slot = the unit slot's
-// piece 0 for this lane, pieces G float4s apart).
-template <int T, int UB>
+// load_unit_x from staged pieces (slot = the unit slot's piece 0 for this
+// lane, pieces G float4s apart; vector b's pieces follow vector b - 1's).
+template <int T, int UB, int B = 1>
 __device__ __forceinline__ void load_unit_x_staged(const xf32x4* slot, uint32_t G,
-                                                   UnitX<T, UB, 1>& ux) {
-    constexpr int R = Fmt<T>::RUNS;
+                                                   UnitX<T, UB, B>& ux) {
+    constexpr int R = Fmt<T>::RUNS, Q = x_pieces<T, UB>();
 #pragma unroll
-    for (int r = 0; r < R; ++r) {
-        float sum = 0.0f;
+    for (int b = 0; b < B; ++b) {
 #pragma unroll
-        for (int i = 0; i < UB; i += 4) {
-            const xf32x4 v = slot[(r * (UB / 4) + i / 4) * G];
-            ux.v[0][r * UB + i + 0] = v.x;
-            ux.v[0][r * UB + i + 1] = v.y;
-            ux.v[0][r * UB + i + 2] = v.z;
-            ux.v[0][r * UB + i + 3] = v.w;
-            sum += (v.x + v.y) + (v.z + v.w);
+        for (int r = 0; r < R; ++r) {
+            float sum = 0.0f;
+#pragma unroll
+            for (int i = 0; i < UB; i += 4) {
+                const xf32x4 v = slot[(b * Q + r * (UB / 4) + i / 4) * G];
+                ux.v[b][r * UB + i + 0] = v.x;
+                ux.v[b][r * UB + i + 1] = v.y;
+                ux.v[b][r * UB + i + 2] = v.z;
+                ux.v[b][r * UB + i + 3] = v.w;
+                sum += (v.x + v.y) + (v.z + v.w);
+            }
+            ux.s[b][r] = sum;
         }
-        ux.s[0][r] = sum;
     }
 }
 

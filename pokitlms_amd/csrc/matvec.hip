@@ -159,37 +159,38 @@ __global__ __launch_bounds__(max_threads_for<B>()) void k_matvec_q(
 }
 
 // ---------------------------------------------------------------------------
-// One vector, every row on the 64 lanes of a wave (G = 64), and XG waves per
-// K-slice in a workgroup: the workgroup stages x once in LDS instead of every
-// wave reading all of it from L2 (for a 4096-wide Q4_K row that is 16 KB per
-// wave against 4.6 KB of weights, and the loads' issue, not HBM, set the
-// pace).  Piece q of unit slot k of lane l (a float4 of run q / (UB / 4))
-// sits at [(slice * NU + k) * Q + q][l], so each LDS read of a wave is 64
-// consecutive float4s.  Each wave stages NU * Q / XG pieces per lane, its
-// share of its slice's slots.
+// Up to four vectors, every row on the 64 lanes of a wave (G = 64), and XG
+// waves per K-slice in a workgroup: the workgroup stages x once in LDS instead
+// of every wave reading all of it from L2 (for a 4096-wide Q4_K row and one
+// vector that is 16 KB per wave against 4.6 KB of weights, and the loads'
+// issue, not HBM, set the pace).  Piece q of vector b of unit slot k of lane
+// l (a float4 of run q / (UB / 4)) sits at [((slice * NU + k) * B + b) * Q +
+// q][l], so each LDS read of a wave is 64 consecutive float4s.  Each wave
+// stages NU * B * Q / XG pieces per lane, its share of its slice's slots.
 //
 // The staging loads go out first, then the weight loads, then the stores to
 // LDS, which wait for the staging loads alone (the memory counter is in
 // order).  W and x are not __restrict__ here: loads the compiler may not take
 // for invariant keep that program order around the barrier.
 
-template <int T, int UB, int NU, int XG>
+template <int T, int B, int UB, int NU, int XG>
 __global__ __launch_bounds__(512) void k_matvec_q_staged(
     const uint8_t* W, uint32_t nb, const float* x, float* y, uint32_t rows, uint32_t units,
     uint32_t slice_units, uint32_t S) {
-    // staged x [S][NU][Q][64], then partial [waves][kPasses] when S > 1
+    // vector b of x starts at b * nb * BE, of y at b * rows
+    // staged x [S][NU][B][Q][64], then partial [waves][kPasses][B] when S > 1
     extern __shared__ xf32x4 smem[];
-    constexpr int kPasses = passes_for<1>(), Q = x_pieces<T, UB>(), XP = NU * Q / XG;
-    static_assert(XP * XG == NU * Q, "pieces split evenly over the waves of a slice");
+    constexpr int kPasses = passes_for<B>(), Q = x_pieces<T, UB>(), QB = Q * B, XP = NU * QB / XG;
+    static_assert(XP * XG == NU * QB, "pieces split evenly over the waves of a slice");
     const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
     const uint32_t group = wave / S, slice = wave % S;
     const uint64_t nblk = static_cast<uint64_t>(rows) * nb;
     const uint32_t stride = gridDim.x * XG * kPasses;
-    float* partial = reinterpret_cast<float*>(smem + S * NU * Q * 64u);
+    float* partial = reinterpret_cast<float*>(smem + S * NU * QB * 64u);
     uint32_t p0 = blockIdx.x * XG * kPasses;
     if (p0 >= rows) return;  // uniform per workgroup
 
-    MvState<T, 1, UB, NU, false> st;
+    MvState<T, B, UB, NU, false> st;
 #pragma unroll
     for (int k = 0; k < NU; ++k) {
         const uint32_t local = lane + 64u * k;
@@ -211,34 +212,44 @@ __global__ __launch_bounds__(512) void k_matvec_q_staged(
     auto finish = [&](uint32_t pp) {
 #pragma unroll
         for (int q = 0; q < kPasses; ++q) {
-            float acc[1] = {0.0f};
+            float acc[B];
+#pragma unroll
+            for (int b = 0; b < B; ++b) acc[b] = 0.0f;
 #pragma unroll
             for (int k = 0; k < NU; ++k) {
                 // unconditional, the absent unit's share dropped by a select:
                 // a branch around the dots would let the compiler sink their
                 // weight loads past the staging barrier
-                float t[1] = {0.0f};
-                unit_compute<T, UB, 1>(st.raw[0][q][k], st.pos[k], st.ux[k], t);
-                acc[0] += st.valid[k] ? t[0] : 0.0f;
+                float t[B];
+#pragma unroll
+                for (int b = 0; b < B; ++b) t[b] = 0.0f;
+                unit_compute<T, UB, B>(st.raw[0][q][k], st.pos[k], st.ux[k], t);
+#pragma unroll
+                for (int b = 0; b < B; ++b) acc[b] += st.valid[k] ? t[b] : 0.0f;
             }
-            acc[0] = group_sum<64>(acc[0]);
+#pragma unroll
+            for (int b = 0; b < B; ++b) acc[b] = group_sum<64>(acc[b]);
             if (lane == 63u) {
                 if (S == 1) {
-                    if (st.live[0][q]) y[st.row[0][q]] = acc[0];
+                    if (st.live[0][q]) {
+#pragma unroll
+                        for (int b = 0; b < B; ++b) y[b * rows + st.row[0][q]] = acc[b];
+                    }
                 } else {
-                    partial[wave * kPasses + q] = acc[0];
+#pragma unroll
+                    for (int b = 0; b < B; ++b) partial[(wave * kPasses + q) * B + b] = acc[b];
                 }
             }
         }
         if (S > 1) {
             __syncthreads();
-            // the group's first wave adds the slices in order
-            if (slice == 0 && lane < kPasses) {
-                const uint32_t row = pp + group * kPasses + lane;
+            // the group's first wave adds the slices in order: lane (pass, vector)
+            if (slice == 0 && lane < kPasses * B) {
+                const uint32_t q = lane / B, b = lane % B, row = pp + group * kPasses + q;
                 if (row < rows) {
                     float v = 0.0f;
-                    for (uint32_t sl = 0; sl < S; ++sl) v += partial[(group * S + sl) * kPasses + lane];
-                    y[row] = v;
+                    for (uint32_t sl = 0; sl < S; ++sl) v += partial[((group * S + sl) * kPasses + q) * B + b];
+                    y[b * rows + row] = v;
                 }
             }
             __syncthreads();
@@ -250,12 +261,13 @@ __global__ __launch_bounds__(512) void k_matvec_q_staged(
     xf32x4 xv[XP];
 #pragma unroll
     for (int j = 0; j < XP; ++j) {
-        const uint32_t piece = group * XP + j;  // (k, q) of this lane's units
-        const uint32_t k = piece / Q, q = piece % Q;
+        const uint32_t piece = group * XP + j;  // (k, vector, q) of this lane's units
+        const uint32_t k = piece / QB, bq = piece % QB;
+        const uint32_t b = B == 1 ? 0u : bq / Q, q = B == 1 ? bq : bq % Q;
         const uint32_t local = lane + 64u * k, u = slice * slice_units + local;
         const bool valid = local < slice_units && u < units;
         const UnitPos pos = unit_pos<T, UB>(valid ? u : 0u);
-        xv[j] = *reinterpret_cast<const xf32x4*>(x + piece_col<T, UB>(pos, q));
+        xv[j] = *reinterpret_cast<const xf32x4*>(x + b * (nb * Fmt<T>::BE) + piece_col<T, UB>(pos, q));
     }
     issue(p0);
     __builtin_amdgcn_sched_barrier(0);
@@ -263,12 +275,12 @@ __global__ __launch_bounds__(512) void k_matvec_q_staged(
     // dequantisation of the weights is scheduled, and waited for, above it)
     if (wave < (blockDim.x >> 6)) {
 #pragma unroll
-        for (int j = 0; j < XP; ++j) smem[(slice * (NU * Q) + group * XP + j) * 64u + lane] = xv[j];
+        for (int j = 0; j < XP; ++j) smem[(slice * (NU * QB) + group * XP + j) * 64u + lane] = xv[j];
         __syncthreads();
     }
 #pragma unroll
     for (int k = 0; k < NU; ++k)
-        load_unit_x_staged<T, UB>(smem + (slice * NU + k) * Q * 64u + lane, 64u, st.ux[k]);
+        load_unit_x_staged<T, UB, B>(smem + (slice * NU + k) * QB * 64u + lane, 64u, st.ux[k]);
     finish(p0);
     for (p0 += stride; p0 < rows; p0 += stride) {
         issue(p0);
@@ -386,19 +398,31 @@ hipError_t run_q(const Plan& pl, const uint8_t* W, uint32_t nb, uint32_t rows,
             return hipGetLastError();
         }
     }
-    // one vector, rows on 64 lanes, two or four row streams per workgroup
-    // sharing a slice: the activations staged once in LDS (at most 32 KB)
-    if constexpr (B == 1) {
-        const uint32_t xl = pl.S * NU * x_pieces<T, UB>() * 64u * 16u;
-        if (pl.glog2 == 6u && xl <= 32768u && (groups == 4u || groups == 2u)) {
+    // up to four vectors (one for Q2_K/Q3_K, whose batches would spill), rows
+    // on 64 lanes, two or four row streams per workgroup sharing a slice: the
+    // activations staged once in LDS (at most 32 KB)
+    if constexpr (B == 1 || (B <= 4 && T != T_Q2_K && T != T_Q3_K)) {
+        // (each wave of a slice stages the same number of pieces)
+        constexpr int kPieces = NU * x_pieces<T, UB>() * B;
+        const uint32_t xl = pl.S * kPieces * 64u * 16u;
+        if (pl.glog2 == 6u && xl <= 32768u) {
             const dim3 grid(blocks), block(64u * pl.waves_per_block);
-            if (groups == 4u)
-                hipLaunchKernelGGL((k_matvec_q_staged<T, UB, NU, 4>), grid, block, xl + lds, stream,
-                                   W, nb, x, y, rows, pl.units, pl.slice_units, pl.S);
-            else
-                hipLaunchKernelGGL((k_matvec_q_staged<T, UB, NU, 2>), grid, block, xl + lds, stream,
-                                   W, nb, x, y, rows, pl.units, pl.slice_units, pl.S);
-            return hipGetLastError();
+            if constexpr (kPieces % 4 == 0) {
+                if (groups == 4u) {
+                    hipLaunchKernelGGL((k_matvec_q_staged<T, B, UB, NU, 4>), grid, block, xl + lds,
+                                       stream, W, nb, x, y, rows, pl.units, pl.slice_units,
+                                       pl.S);
+                    return hipGetLastError();
+                }
+            }
+            if constexpr (kPieces % 2 == 0) {
+                if (groups == 2u) {
+                    hipLaunchKernelGGL((k_matvec_q_staged<T, B, UB, NU, 2>), grid, block, xl + lds,
+                                       stream, W, nb, x, y, rows, pl.units, pl.slice_units,
+                                       pl.S);
+                    return hipGetLastError();
+                }
+            }
         }
     }
     hipLaunchKernelGGL((k_matvec_q<T, B, UB, NU, false>), dim3(blocks), dim3(64u * pl.waves_per_block),

@@ -187,6 +187,28 @@ def test_staged_single_vector_widths(hip, port, gtype):
         wt.release()
 
 
+@pytest.mark.parametrize("gtype", QUANT)
+def test_staged_batched_widths(hip, port, gtype):
+    """Two to four vectors through the staging kernel (each vector's pieces
+    after the previous one's in LDS): one K-slice (1024 wide), two (2048,
+    with 10,001 rows so workgroups loop with a partial last pass), and a width
+    whose slices are narrower than a wave (1536), which takes the plain
+    kernel; every vector checked against the CPU's linear."""
+    g = S.rng(171 + gtype)
+    for rows, inn in ((1000, 1024), (10001, 2048), (777, 1536)):
+        w = S.quant_matrix(gtype, rows, inn, g)
+        wt = hip.upload(gtype, inn, rows, w)
+        for batch in (2, 3, 4):
+            x = S.normal_f32(g, batch * inn).reshape(batch, inn)
+            gpu = hip.matvec(wt, x)
+            for b in range(batch):
+                cpu = port.linear(gtype, w, inn, rows, x[b])
+                err = normwise_rel(gpu[b], cpu)
+                assert err <= TOL, (rows, inn, batch, b, err)
+            say("staged batched matvec", gtype, rows, inn, batch, "ok")
+        wt.release()
+
+
 @pytest.mark.parametrize("gtype", (S.Q4_K, S.Q6_K, S.Q8_0))
 def test_long_matvec_pipelined_rows(hip, port, gtype):
     """Rows enough that every wave walks several row passes (the pipelined
