@@ -620,4 +620,19 @@ __device__ __forceinline__ V lane63(V v) {
     }
 }
 
+// bf16 bits of a finite x, rounded to nearest even.
+__device__ __forceinline__ uint32_t bf16_rne_bits(float x) {
+    const uint32_t u = __float_as_uint(x);
+    return (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+}
+
+// The bytes f0..f3 of w as the bf16 pairs of 128 + f (bits 0x4300 | f: the
+// exponent of 128 leaves f in the low mantissa bits), one v_perm per pair:
+// the weight operand of the MFMA kernels, whose group bias absorbs the
+// -128 * ds (a bf16 of 128 + f is exact for f < 128).
+__device__ __forceinline__ void bf16_bytes_b128(uint32_t w, uint32_t& lo, uint32_t& hi) {
+    lo = __builtin_amdgcn_perm(0x43434343u, w, 0x04010400u);  // bytes f0, 0x43, f1, 0x43
+    hi = __builtin_amdgcn_perm(0x43434343u, w, 0x04030402u);  // bytes f2, 0x43, f3, 0x43
+}
+
 }  // namespace pk

@@ -20,6 +20,13 @@ hipError_t launch_matvec(uint32_t type, const uint8_t* W, uint64_t row_bytes, ui
                          uint32_t in, const float* x, float* y, uint32_t batch,
                          hipStream_t stream);
 
+// Batched Q4_K matvecs on MFMA (matvec_mfma.hip): K blocks per wave for
+// (type, in, batch), 0 where that kernel does not apply; launch_matvec takes
+// it where it applies.
+uint32_t matvec_mfma_blocks_per_wave(uint32_t type, uint32_t in, uint32_t batch);
+hipError_t launch_matvec_mfma(uint32_t type, const uint8_t* W, uint32_t rows, uint32_t in,
+                              const float* x, float* y, uint32_t batch, hipStream_t stream);
+
 // One single-token routed-MoE layer (router -> top-k -> gate/up SwiGLU ->
 // down -> weighted combine).  Device pointers throughout.
 struct MoeDecodeArgs {

@@ -495,6 +495,7 @@ bool supported_q(uint32_t in, uint32_t batch) {
 
 bool matvec_supported(uint32_t type, uint32_t in, uint32_t batch) {
     if (batch == 0 || batch > 8 || in == 0) return false;
+    if (matvec_mfma_blocks_per_wave(type, in, batch)) return true;
     switch (type) {
         case T_F32: case T_F16: case T_BF16: return true;
         case T_Q4_0: return supported_q<T_Q4_0>(in, batch);
@@ -515,6 +516,8 @@ hipError_t launch_matvec(uint32_t type, const uint8_t* W, uint64_t row_bytes, ui
                          uint32_t in, const float* x, float* y, uint32_t batch,
                          hipStream_t stream) {
     if (rows == 0) return hipSuccess;
+    if (matvec_mfma_blocks_per_wave(type, in, batch) && row_bytes == in / 256u * 144u)
+        return launch_matvec_mfma(type, W, rows, in, x, y, batch, stream);
     switch (type) {
         case T_F32: return dispatch_batch_f<T_F32>(batch, W, row_bytes, rows, x, in, y, stream);
         case T_F16: return dispatch_batch_f<T_F16>(batch, W, row_bytes, rows, x, in, y, stream);

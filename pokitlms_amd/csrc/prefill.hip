@@ -118,15 +118,6 @@ __device__ __forceinline__ void bf16_bytes(uint32_t w, uint32_t& lo, uint32_t& h
     hi = bf16_pair(ub<2>(w), ub<3>(w));
 }
 
-// The bytes f0..f3 of w as the bf16 pairs of 128 + f (bits 0x4300 | f: the
-// exponent of 128 leaves f in the low mantissa bits), one v_perm per pair:
-// the weight operand of the register-weight GEMM, whose group bias absorbs
-// the -128 * ds (a bf16 of 128 + f is exact for f < 128).
-__device__ __forceinline__ void bf16_bytes_b128(uint32_t w, uint32_t& lo, uint32_t& hi) {
-    lo = __builtin_amdgcn_perm(0x43434343u, w, 0x04010400u);  // bytes f0, 0x43, f1, 0x43
-    hi = __builtin_amdgcn_perm(0x43434343u, w, 0x04030402u);  // bytes f2, 0x43, f3, 0x43
-}
-
 template <int T>
 __device__ __forceinline__ void raw32_bf16(const Raw32<T>& r, uint32_t k0, uint32_t (&bw)[16],
                                            float (&ds)[2], float (&cn)[2]) {
@@ -308,11 +299,6 @@ __global__ __launch_bounds__(256) void k_route_batch(MoePrefillArgs A) {
 // per-group scales are applied outside it.  split_piece writes the three planes
 // of `rows` x `cols` FP32 values and, per G consecutive values of a row,
 // their sum (accumulated in FP64, rounded once).
-
-__device__ __forceinline__ uint32_t bf16_rne_bits(float x) {  // finite x
-    const uint32_t u = __float_as_uint(x);
-    return (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
-}
 
 template <uint32_t G>
 __device__ __forceinline__ void split_piece(const float* __restrict__ src, uint32_t i,
