@@ -620,6 +620,19 @@ __device__ __forceinline__ V lane63(V v) {
     }
 }
 
+// The upper halves of two floats as one dword of bf16 (exact for small
+// integers).
+__device__ __forceinline__ uint32_t bf16_pair(float lo, float hi) {
+    return __builtin_amdgcn_perm(__float_as_uint(hi), __float_as_uint(lo), 0x07060302u);
+}
+
+// Four unsigned byte fields (each < 256) to two dwords of bf16: one
+// v_cvt_f32_ubyteN per field (no separate byte extraction), one v_perm per pair.
+__device__ __forceinline__ void bf16_bytes(uint32_t w, uint32_t& lo, uint32_t& hi) {
+    lo = bf16_pair(ub<0>(w), ub<1>(w));
+    hi = bf16_pair(ub<2>(w), ub<3>(w));
+}
+
 // bf16 bits of a finite x, rounded to nearest even.
 __device__ __forceinline__ uint32_t bf16_rne_bits(float x) {
     const uint32_t u = __float_as_uint(x);

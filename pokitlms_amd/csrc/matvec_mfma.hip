@@ -1,25 +1,29 @@
-// matvec_mfma.hip -- batched Q4_K matvecs (5 to 8 vectors) on bf16 MFMA.
+// matvec_mfma.hip -- batched matvecs (5 to 8 vectors) on bf16 MFMA, for
+// Q4_K, Q5_K, Q8_0 and Q4_0.
 //
 // The batched case of tensor_linear (src/tensor_linear.cpp:232-263 of the
-// reference, per-row linear_k of src/quantized_linear.cpp:360-423): y[b][r] =
-// W[r] . x[b].  The register kernels of matvec.hip hold every vector's
-// activations in each lane and reduce every (row, vector) dot across the 64
-// lanes, which costs about 36 VALU operations per weight at 8 vectors.  Here
-// the vectors are the A operand and the decoded weights the B operand of
-// v_mfma_f32_16x16x32_bf16, so the dots and their reductions run on the
-// matrix cores:
+// reference, per-row linear_k / linear_quantized of
+// src/quantized_linear.cpp:360-423): y[b][r] = W[r] . x[b].  The register
+// kernels of matvec.hip hold every vector's activations in each lane and
+// reduce every (row, vector) dot across the 64 lanes, which costs about 36
+// VALU operations per weight at 8 vectors.  Here the vectors are the A
+// operand and the decoded weights the B operand of v_mfma_f32_16x16x32_bf16,
+// so the dots and their reductions run on the matrix cores:
 //
 //  * A wave owns 16·NT rows (NT tiles of 16, lane n = lane % 16 of each tile)
-//    and KB consecutive 256-value blocks of K; the W waves of a workgroup own
+//    and KB consecutive 256-value ranges of K; the waves of a workgroup own
 //    the same rows and consecutive K ranges, and their partial results are
 //    added through LDS in wave order (deterministic).
-//  * Lane (n, kq = lane / 16) loads, per block and tile, the 16-byte header
-//    and bytes 8kq .. 8kq+7 of each 32-byte nibble chunk: chunk c's low
-//    nibbles are scale group 2c, its high nibbles group 2c+1, each group one
-//    MFMA K step of 32 values (lane kq holding values 8kq .. 8kq+7).
-//  * Weights enter the MFMA as bf16 of 128 + q (one v_perm per pair, exact);
-//    per group, acc += ds · (x . (128 + q)) + cb · sum(x) with ds = d·sc and
-//    cb = -(128·ds + dmin·m), the CPU's ds·q - dmin·m per weight.
+//  * Every scale group of the formats here is 32 values, one MFMA K step,
+//    lane kq = lane / 16 holding values 8kq .. 8kq+7 of it.  Per 256 values
+//    lane (n, kq) loads (Q4_K, Q5_K) the block header and bytes 8kq .. 8kq+7
+//    of each 32-byte nibble chunk (chunk c's low nibbles are group 2c, its
+//    high nibbles group 2c+1; Q5_K also bytes 8kq .. 8kq+7 of qh, bit g for
+//    group g), or (Q8_0, Q4_0) the 8 bytes of each of 8 blocks that hold its
+//    values and the 8 blocks' scales in one 16-byte load.
+//  * Weights enter the MFMA as bf16 of an unsigned field f (128 + q for the
+//    nibble formats, one v_perm per pair; q + 128 for Q8_0), all exact; per
+//    group the CPU's weight is ds·f + cb, so acc += ds · (x . f) + cb · sum(x).
 //  * x enters as three bf16 planes (hi, mid, lo: x = hi + mid + lo exactly),
 //    split by each lane from FP32 for its (vector m = lane % 16, kq) slot;
 //    vectors m >= batch are zero.  The group sums go in through one
@@ -37,21 +41,49 @@ namespace {
 typedef __bf16 mbf16x8 __attribute__((ext_vector_type(8)));
 typedef float mf32x4 __attribute__((ext_vector_type(4)));
 
-// One lane's share of one 256-value Q4_K block: the header words and the
-// 8 bytes it takes of each of the four nibble chunks.
-struct Q4kPart {
-    uint32_t h[4];
-    uint32_t q[8];  // chunk c: q[2c], q[2c + 1]
-};
+// One lane's share of 256 values of a row.
+template <int T> struct MmPart;
+template <> struct MmPart<T_Q4_K> { uint32_t h[4], q[8]; };           // q[2c..2c+1]: chunk c
+template <> struct MmPart<T_Q5_K> { uint32_t h[4], q[8], qh[2]; };
+template <> struct MmPart<T_Q8_0> { uint32_t q[16], d[4]; };          // q[2i..2i+1]: block i
+template <> struct MmPart<T_Q4_0> { uint32_t q[16], d[4]; };
 
-__device__ __forceinline__ void q4k_part_load(const uint8_t* blk, uint32_t kq, Q4kPart& p) {
-    ld_words<4>(blk, p.h);
+__device__ __forceinline__ void ld2(const uint8_t* p, uint32_t* w) {
+    const uint2 v = *reinterpret_cast<const uint2*>(__builtin_assume_aligned(p, 8));
+    w[0] = v.x;
+    w[1] = v.y;
+}
+
+__device__ __forceinline__ void ld4_16(const uint8_t* p, uint32_t* w) {
+    const uint4 v = *reinterpret_cast<const uint4*>(__builtin_assume_aligned(p, 16));
+    w[0] = v.x;
+    w[1] = v.y;
+    w[2] = v.z;
+    w[3] = v.w;
+}
+
+// Values 256·sb .. 256·sb + 255 of the row (K-quants: block sb; Q8_0/Q4_0:
+// blocks 8sb .. 8sb+7, whose scales are 16 consecutive bytes of the d plane).
+template <int T>
+__device__ __forceinline__ void mm_load(const QRow& r, uint32_t sb, uint32_t kq, MmPart<T>& p) {
+    if constexpr (T == T_Q4_K || T == T_Q5_K) {
+        const uint8_t* blk = block_ptr<Fmt<T>::BB>(r, sb);
+        ld_words<4>(blk, p.h);
+        const uint8_t* qs = blk + (T == T_Q4_K ? 16u : 48u) + 8u * kq;
 #pragma unroll
-    for (uint32_t c = 0; c < 4; ++c) {
-        const uint2 v = *reinterpret_cast<const uint2*>(
-            __builtin_assume_aligned(blk + 16u + 32u * c + 8u * kq, 8));
-        p.q[2u * c] = v.x;
-        p.q[2u * c + 1u] = v.y;
+        for (uint32_t c = 0; c < 4; ++c) ld2(qs + 32u * c, &p.q[2u * c]);
+        if constexpr (T == T_Q5_K) ld2(blk + 16u + 8u * kq, p.qh);
+    } else if constexpr (T == T_Q8_0) {
+        using L = Planar<T_Q8_0>;
+#pragma unroll
+        for (uint32_t i = 0; i < 8; ++i) ld2(field_ptr<L::QS, 32>(r, 8u * sb + i) + 8u * kq, &p.q[2u * i]);
+        ld4_16(field_ptr<L::D, 2>(r, 8u * sb), p.d);
+    } else {  // Q4_0: values 8kq.. are the low (kq < 2) or high nibbles of bytes 8(kq & 1)..
+        using L = Planar<T_Q4_0>;
+#pragma unroll
+        for (uint32_t i = 0; i < 8; ++i)
+            ld2(field_ptr<L::QS, 16>(r, 8u * sb + i) + 8u * (kq & 1u), &p.q[2u * i]);
+        ld4_16(field_ptr<L::D, 2>(r, 8u * sb), p.d);
     }
 }
 
@@ -100,26 +132,46 @@ __device__ __forceinline__ void x_split(const XRaw& r, bool live, XFrag& f) {
     f.part = ((v[0] + v[1]) + (v[2] + v[3])) + ((v[4] + v[5]) + (v[6] + v[7]));
 }
 
-// Group g (0..7) of a block part: the lane's B fragment, ds and cb.
-__device__ __forceinline__ void q4k_group(const Q4kPart& p, uint32_t g, mbf16x8& b, float& ds,
-                                          float& cb) {
-    const uint32_t c = g / 2u, sh = 4u * (g & 1u);
+// Group g (0..7) of a part: the lane's B fragment, ds and cb.
+template <int T>
+__device__ __forceinline__ void mm_group(const MmPart<T>& p, uint32_t g, uint32_t kq, mbf16x8& b,
+                                         float& ds, float& cb) {
     uint32_t w[4];
-    bf16_bytes_b128((p.q[2u * c] >> sh) & 0x0f0f0f0fu, w[0], w[1]);
-    bf16_bytes_b128((p.q[2u * c + 1u] >> sh) & 0x0f0f0f0fu, w[2], w[3]);
+    if constexpr (T == T_Q4_K || T == T_Q5_K) {
+        const uint32_t c = g / 2u, sh = 4u * (g & 1u);
+#pragma unroll
+        for (uint32_t i = 0; i < 2; ++i) {
+            uint32_t q = (p.q[2u * c + i] >> sh) & 0x0f0f0f0fu;
+            if constexpr (T == T_Q5_K) q |= ((p.qh[i] >> g) & 0x01010101u) << 4;
+            bf16_bytes_b128(q, w[2u * i], w[2u * i + 1u]);
+        }
+        const float d = half_bits_to_float(p.h[0] & 0xffffu);
+        const float dmin = half_bits_to_float(p.h[0] >> 16);
+        float sc, mn;
+        kq_scale_min(p.h, g, sc, mn);
+        ds = __fmul_rn(d, sc);
+        cb = -__fmaf_rn(128.0f, ds, __fmul_rn(dmin, mn));  // ds·q - dmin·m
+    } else {
+        ds = half_bits_to_float((p.d[g / 2u] >> (16u * (g & 1u))) & 0xffffu);
+        if constexpr (T == T_Q8_0) {
+#pragma unroll
+            for (uint32_t i = 0; i < 2; ++i) bf16_bytes(p.q[2u * g + i] ^ 0x80808080u, w[2u * i], w[2u * i + 1u]);
+            cb = __fmul_rn(-128.0f, ds);  // d·q = d·(q + 128) - 128·d
+        } else {
+            const uint32_t sh = 4u * (kq >> 1);
+#pragma unroll
+            for (uint32_t i = 0; i < 2; ++i)
+                bf16_bytes_b128((p.q[2u * g + i] >> sh) & 0x0f0f0f0fu, w[2u * i], w[2u * i + 1u]);
+            cb = __fmul_rn(-136.0f, ds);  // d·(q - 8) = d·(128 + q) - 136·d
+        }
+    }
     b = __builtin_bit_cast(mbf16x8, make_uint4(w[0], w[1], w[2], w[3]));
-    const float d = half_bits_to_float(p.h[0] & 0xffffu);
-    const float dmin = half_bits_to_float(p.h[0] >> 16);
-    float sc, mn;
-    kq_scale_min(p.h, g, sc, mn);
-    ds = __fmul_rn(d, sc);
-    cb = -__fmaf_rn(128.0f, ds, __fmul_rn(dmin, mn));
 }
 
-template <int NT, int KB>
-__global__ __launch_bounds__(1024) void k_matvec_mfma_q4k(const uint8_t* W, uint32_t nb,
-                                                         const float* x, float* __restrict__ y,
-                                                         uint32_t rows, uint32_t batch) {
+template <int T, int NT, int KB>
+__global__ __launch_bounds__(1024) void k_matvec_mfma(const uint8_t* W, uint32_t nb,
+                                                     const float* x, float* __restrict__ y,
+                                                     uint32_t rows, uint32_t batch) {
     // W and x are not __restrict__: loads the compiler may not take for
     // invariant stay in program order, so every weight load and the first x
     // loads are issued before the first wait (the memory counter is in order)
@@ -132,13 +184,16 @@ __global__ __launch_bounds__(1024) void k_matvec_mfma_q4k(const uint8_t* W, uint
     const uint32_t in = nb * 256u;
     const bool live = n < batch;  // A operand row m = n of this lane
 
-    Q4kPart part[NT][KB];
+    // nb: 256-value ranges per row
+    constexpr uint32_t kPer = 256u / Fmt<T>::BE;  // GGUF blocks per 256 values
+    const uint64_t nblk = static_cast<uint64_t>(rows) * nb * kPer;
+    MmPart<T> part[NT][KB];
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
         const uint32_t row = r0 + 16u * t + n;
-        const uint8_t* rp = W + static_cast<uint64_t>(row < rows ? row : rows - 1u) * nb * 144u;
+        const QRow qr{W, nblk, static_cast<uint64_t>(row < rows ? row : rows - 1u) * nb * kPer};
 #pragma unroll
-        for (int j = 0; j < KB; ++j) q4k_part_load(rp + (wave * KB + j) * 144u, kq, part[t][j]);
+        for (int j = 0; j < KB; ++j) mm_load<T>(qr, wave * KB + j, kq, part[t][j]);
     }
 
     // the x of the wave's first XD groups, then XD groups ahead of their use
@@ -162,7 +217,7 @@ __global__ __launch_bounds__(1024) void k_matvec_mfma_q4k(const uint8_t* W, uint
         for (int t = 0; t < NT; ++t) {
             mbf16x8 b;
             float ds, cb;
-            q4k_group(part[t][j], g, b, ds, cb);
+            mm_group<T>(part[t][j], g, kq, b, ds, cb);
             mf32x4 P = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xf.lo, b, mf32x4{0.0f, 0.0f, 0.0f, 0.0f},
                                                                0, 0, 0);
             P = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xf.mid, b, P, 0, 0, 0);
@@ -192,27 +247,43 @@ __global__ __launch_bounds__(1024) void k_matvec_mfma_q4k(const uint8_t* W, uint
     }
 }
 
-template <int NT, int KB>
+template <int T, int NT, int KB>
 hipError_t launch_nt_kb(const uint8_t* W, uint32_t nb, uint32_t rows, const float* x, float* y,
                         uint32_t batch, hipStream_t s) {
     const uint32_t waves = nb / KB;
     const uint32_t blocks = (rows + 16u * NT - 1u) / (16u * NT);
     const size_t lds = static_cast<size_t>(waves) * NT * 64u * sizeof(mf32x4);
-    hipLaunchKernelGGL((k_matvec_mfma_q4k<NT, KB>), dim3(blocks), dim3(64u * waves), lds, s, W, nb,
+    hipLaunchKernelGGL((k_matvec_mfma<T, NT, KB>), dim3(blocks), dim3(64u * waves), lds, s, W, nb,
                        x, y, rows, batch);
     return hipGetLastError();
 }
 
+
+template <int T>
+hipError_t launch_t(uint32_t kb, const uint8_t* W, uint32_t nb, uint32_t rows, const float* x,
+                    float* y, uint32_t batch, hipStream_t s) {
+    switch (kb) {
+        case 1: return launch_nt_kb<T, 2, 1>(W, nb, rows, x, y, batch, s);
+        case 2: return launch_nt_kb<T, 1, 2>(W, nb, rows, x, y, batch, s);
+        case 3: return launch_nt_kb<T, 1, 3>(W, nb, rows, x, y, batch, s);
+        case 4: return launch_nt_kb<T, 1, 4>(W, nb, rows, x, y, batch, s);
+        default: return hipErrorInvalidValue;
+    }
+}
+
 }  // namespace
 
-// K blocks per wave: one (two row tiles per wave) up to 8 blocks per row,
-// else the fewest (2..4) that leave at most 16 waves (one tile per wave).
-// Batches of 5 to 8: at 4 vectors the register kernels are faster.
+// 256-value ranges of K per wave: one (two row tiles per wave) up to 8 per
+// row, else the fewest (2..4, Q8_0/Q4_0 2..3) that leave at most 16 waves
+// (one tile per wave).  Batches of 5 to 8: at 4 vectors the register kernels are faster.
 uint32_t matvec_mfma_blocks_per_wave(uint32_t type, uint32_t in, uint32_t batch) {
-    if (type != T_Q4_K || batch < 5u || batch > 8u || in == 0 || in % 256u) return 0;
+    if (type != T_Q4_K && type != T_Q5_K && type != T_Q8_0 && type != T_Q4_0) return 0;
+    if (batch < 5u || batch > 8u || in == 0 || in % 256u) return 0;
     const uint32_t nb = in / 256u;
     if (nb <= 8u) return 1;
-    for (uint32_t kb = 2; kb <= 4u; ++kb)
+    // four ranges of 8 Q8_0/Q4_0 blocks would spill
+    const uint32_t max_kb = type == T_Q8_0 || type == T_Q4_0 ? 3u : 4u;
+    for (uint32_t kb = 2; kb <= max_kb; ++kb)
         if (nb % kb == 0 && nb / kb <= 16u) return kb;
     return 0;
 }
@@ -221,11 +292,11 @@ hipError_t launch_matvec_mfma(uint32_t type, const uint8_t* W, uint32_t rows, ui
                               const float* x, float* y, uint32_t batch, hipStream_t s) {
     const uint32_t kb = matvec_mfma_blocks_per_wave(type, in, batch);
     const uint32_t nb = in / 256u;
-    switch (kb) {
-        case 1: return launch_nt_kb<2, 1>(W, nb, rows, x, y, batch, s);
-        case 2: return launch_nt_kb<1, 2>(W, nb, rows, x, y, batch, s);
-        case 3: return launch_nt_kb<1, 3>(W, nb, rows, x, y, batch, s);
-        case 4: return launch_nt_kb<1, 4>(W, nb, rows, x, y, batch, s);
+    switch (type) {
+        case T_Q4_K: return launch_t<T_Q4_K>(kb, W, nb, rows, x, y, batch, s);
+        case T_Q5_K: return launch_t<T_Q5_K>(kb, W, nb, rows, x, y, batch, s);
+        case T_Q8_0: return launch_t<T_Q8_0>(kb, W, nb, rows, x, y, batch, s);
+        case T_Q4_0: return launch_t<T_Q4_0>(kb, W, nb, rows, x, y, batch, s);
         default: return hipErrorInvalidValue;
     }
 }

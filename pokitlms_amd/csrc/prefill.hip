@@ -107,16 +107,6 @@ __device__ __forceinline__ uint32_t byte_of(const uint32_t* w, uint32_t i) {
 // ds * sum(x * f) + cn * sum(x) with cn = -(dm + o * ds): K-quants o = 0
 // (cn = -dm), Q6_K o = 32, Q4_0 o = 8, Q8_0 o = 128 (its int8 read as
 // q + 128).
-__device__ __forceinline__ uint32_t bf16_pair(float lo, float hi) {  // exact for small integers
-    return __builtin_amdgcn_perm(__float_as_uint(hi), __float_as_uint(lo), 0x07060302u);
-}
-
-// Four unsigned byte fields (each < 256) to two dwords of bf16: one
-// v_cvt_f32_ubyteN per field (no separate byte extraction), one v_perm per pair.
-__device__ __forceinline__ void bf16_bytes(uint32_t w, uint32_t& lo, uint32_t& hi) {
-    lo = bf16_pair(ub<0>(w), ub<1>(w));
-    hi = bf16_pair(ub<2>(w), ub<3>(w));
-}
 
 template <int T>
 __device__ __forceinline__ void raw32_bf16(const Raw32<T>& r, uint32_t k0, uint32_t (&bw)[16],

@@ -209,23 +209,28 @@ def test_staged_batched_widths(hip, port, gtype):
         wt.release()
 
 
-def test_mfma_batched_q4k_widths(hip, port):
-    """Five to eight vectors of Q4_K through the MFMA kernel: one block per
-    wave with two row tiles (2048 wide), two, three and four blocks per wave
-    with one tile (6144, 9216, 16384 wide: 12, 12 and 16 waves), row counts
-    that leave a partial tile; every vector against the CPU's linear."""
-    g = S.rng(313)
-    for rows, inn in ((1000, 2048), (777, 6144), (513, 9216), (300, 16384)):
-        w = S.quant_matrix(S.Q4_K, rows, inn, g)
-        wt = hip.upload(S.Q4_K, inn, rows, w)
+@pytest.mark.parametrize("gtype", (S.Q4_K, S.Q5_K, S.Q8_0, S.Q4_0))
+def test_mfma_batched_widths(hip, port, gtype):
+    """Five to eight vectors through the MFMA kernel: one 256-value range per
+    wave with two row tiles (2048 wide), two and three ranges per wave with
+    one tile (6144, 9216 wide: 12 waves), four (16384 wide, 16 waves; the
+    K-quants), row counts that leave a partial tile; every vector against the
+    CPU's linear."""
+    g = S.rng(313 + gtype)
+    shapes = [(1000, 2048), (777, 6144), (513, 9216)]
+    if gtype in (S.Q4_K, S.Q5_K):
+        shapes.append((300, 16384))
+    for rows, inn in shapes:
+        w = S.quant_matrix(gtype, rows, inn, g)
+        wt = hip.upload(gtype, inn, rows, w)
         for batch in (5, 8):
             x = S.normal_f32(g, batch * inn).reshape(batch, inn)
             gpu = hip.matvec(wt, x)
             for b in range(batch):
-                cpu = port.linear(S.Q4_K, w, inn, rows, x[b])
+                cpu = port.linear(gtype, w, inn, rows, x[b])
                 err = normwise_rel(gpu[b], cpu)
                 assert err <= TOL, (rows, inn, batch, b, err)
-            say("mfma batched matvec", rows, inn, batch, "ok")
+            say("mfma batched matvec", gtype, rows, inn, batch, "ok")
         wt.release()
 
 
