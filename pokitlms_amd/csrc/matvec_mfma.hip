@@ -47,6 +47,7 @@ template <> struct MmPart<T_Q4_K> { uint32_t h[4], q[8]; };           // q[2c..2
 template <> struct MmPart<T_Q5_K> { uint32_t h[4], q[8], qh[2]; };
 template <> struct MmPart<T_Q8_0> { uint32_t q[16], d[4]; };          // q[2i..2i+1]: block i
 template <> struct MmPart<T_Q4_0> { uint32_t q[16], d[4]; };
+template <> struct MmPart<T_Q6_K> { uint32_t ql[8], qh[4], sc[4], d; };  // ql[2r..2r+1]: run r
 
 __device__ __forceinline__ void ld2(const uint8_t* p, uint32_t* w) {
     const uint2 v = *reinterpret_cast<const uint2*>(__builtin_assume_aligned(p, 8));
@@ -73,6 +74,18 @@ __device__ __forceinline__ void mm_load(const QRow& r, uint32_t sb, uint32_t kq,
 #pragma unroll
         for (uint32_t c = 0; c < 4; ++c) ld2(qs + 32u * c, &p.q[2u * c]);
         if constexpr (T == T_Q5_K) ld2(blk + 16u + 8u * kq, p.qh);
+    } else if constexpr (T == T_Q6_K) {
+        // run r = 2h + (s & 1) of ql (64h + 32(s & 1)) and qh bytes 32h.. for
+        // the values 128h + 32s + 8kq .. (decode_q6_k's layout)
+        using L = Planar<T_Q6_K>;
+        const uint8_t* ql = field_ptr<L::QL, 128>(r, sb) + 8u * kq;
+        const uint8_t* qh = field_ptr<L::QH, 64>(r, sb) + 8u * kq;
+#pragma unroll
+        for (uint32_t run = 0; run < 4; ++run) ld2(ql + 32u * run, &p.ql[2u * run]);
+        ld2(qh, &p.qh[0]);
+        ld2(qh + 32u, &p.qh[2]);
+        ld4_16(field_ptr<L::SC, 16>(r, sb), p.sc);
+        p.d = ld_u16(field_ptr<L::D, 2>(r, sb));
     } else if constexpr (T == T_Q8_0) {
         using L = Planar<T_Q8_0>;
 #pragma unroll
@@ -168,6 +181,32 @@ __device__ __forceinline__ void mm_group(const MmPart<T>& p, uint32_t g, uint32_
     b = __builtin_bit_cast(mbf16x8, make_uint4(w[0], w[1], w[2], w[3]));
 }
 
+// Q6_K group g (0..7): 32 values of two 16-value scale groups, lanes kq < 2
+// holding the first.  The lane's fragment f (128 + the 6-bit field) goes to
+// two MFMAs, each with the other group's lanes zeroed; w = ds·(f - 32) =
+// ds·(128 + f) - 160·ds, and cb is that of the lane's own group.
+__device__ __forceinline__ void q6k_group(const MmPart<T_Q6_K>& p, uint32_t g, uint32_t kq,
+                                          mbf16x8& b0, mbf16x8& b1, float& ds0, float& ds1,
+                                          float& cb) {
+    const uint32_t h = g >> 2, s = g & 3u, run = 2u * h + (s & 1u);
+    uint32_t w[4];
+#pragma unroll
+    for (uint32_t i = 0; i < 2; ++i) {
+        const uint32_t nib = ((s < 2u ? p.ql[2u * run + i] : p.ql[2u * run + i] >> 4)) & 0x0f0f0f0fu;
+        const uint32_t hb = ((p.qh[2u * h + i] >> (2u * s)) & 0x03030303u) << 4;
+        bf16_bytes_b128(nib | hb, w[2u * i], w[2u * i + 1u]);
+    }
+    const uint4 z = make_uint4(0u, 0u, 0u, 0u), v = make_uint4(w[0], w[1], w[2], w[3]);
+    b0 = __builtin_bit_cast(mbf16x8, kq < 2u ? v : z);
+    b1 = __builtin_bit_cast(mbf16x8, kq < 2u ? z : v);
+    const float d = half_bits_to_float(p.d);
+    const uint32_t i0 = 8u * h + 2u * s;  // scale index of the first group
+    const uint32_t s2 = (p.sc[i0 >> 2] >> (8u * (i0 & 3u))) & 0xffffu;
+    ds0 = __fmul_rn(d, static_cast<float>(static_cast<int8_t>(s2 & 0xffu)));
+    ds1 = __fmul_rn(d, static_cast<float>(static_cast<int8_t>(s2 >> 8)));
+    cb = __fmul_rn(-160.0f, kq < 2u ? ds0 : ds1);
+}
+
 template <int T, int NT, int KB>
 __global__ __launch_bounds__(1024) void k_matvec_mfma(const uint8_t* W, uint32_t nb,
                                                      const float* x, float* __restrict__ y,
@@ -215,15 +254,33 @@ __global__ __launch_bounds__(1024) void k_matvec_mfma(const uint8_t* W, uint32_t
         const int j = gi / 8, g = gi % 8;
 #pragma unroll
         for (int t = 0; t < NT; ++t) {
-            mbf16x8 b;
-            float ds, cb;
-            mm_group<T>(part[t][j], g, kq, b, ds, cb);
-            mf32x4 P = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xf.lo, b, mf32x4{0.0f, 0.0f, 0.0f, 0.0f},
-                                                               0, 0, 0);
-            P = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xf.mid, b, P, 0, 0, 0);
-            P = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xf.hi, b, P, 0, 0, 0);
+            const mf32x4 zero = {0.0f, 0.0f, 0.0f, 0.0f};
+            float cb;
+            if constexpr (T == T_Q6_K) {
+                mbf16x8 b0, b1;
+                float ds0, ds1;
+                q6k_group(part[t][j], g, kq, b0, b1, ds0, ds1, cb);
+                mf32x4 P = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xf.lo, b0, zero, 0, 0, 0);
+                mf32x4 Q = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xf.lo, b1, zero, 0, 0, 0);
+                P = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xf.mid, b0, P, 0, 0, 0);
+                Q = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xf.mid, b1, Q, 0, 0, 0);
+                P = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xf.hi, b0, P, 0, 0, 0);
+                Q = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xf.hi, b1, Q, 0, 0, 0);
 #pragma unroll
-            for (int i = 0; i < 4; ++i) acc[t][i] = __builtin_fmaf(ds, P[i], acc[t][i]);
+                for (int i = 0; i < 4; ++i) {
+                    acc[t][i] = __builtin_fmaf(ds0, P[i], acc[t][i]);
+                    acc[t][i] = __builtin_fmaf(ds1, Q[i], acc[t][i]);
+                }
+            } else {
+                mbf16x8 b;
+                float ds;
+                mm_group<T>(part[t][j], g, kq, b, ds, cb);
+                mf32x4 P = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xf.lo, b, zero, 0, 0, 0);
+                P = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xf.mid, b, P, 0, 0, 0);
+                P = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xf.hi, b, P, 0, 0, 0);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) acc[t][i] = __builtin_fmaf(ds, P[i], acc[t][i]);
+            }
             acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(xf.part, cb, acc[t], 0, 0, 0);
         }
     }
@@ -277,12 +334,13 @@ hipError_t launch_t(uint32_t kb, const uint8_t* W, uint32_t nb, uint32_t rows, c
 // row, else the fewest (2..4, Q8_0/Q4_0 2..3) that leave at most 16 waves
 // (one tile per wave).  Batches of 5 to 8: at 4 vectors the register kernels are faster.
 uint32_t matvec_mfma_blocks_per_wave(uint32_t type, uint32_t in, uint32_t batch) {
-    if (type != T_Q4_K && type != T_Q5_K && type != T_Q8_0 && type != T_Q4_0) return 0;
+    if (type != T_Q4_K && type != T_Q5_K && type != T_Q6_K && type != T_Q8_0 && type != T_Q4_0)
+        return 0;
     if (batch < 5u || batch > 8u || in == 0 || in % 256u) return 0;
     const uint32_t nb = in / 256u;
     if (nb <= 8u) return 1;
-    // four ranges of 8 Q8_0/Q4_0 blocks would spill
-    const uint32_t max_kb = type == T_Q8_0 || type == T_Q4_0 ? 3u : 4u;
+    // four ranges of Q6_K, or of 8 Q8_0/Q4_0 blocks, would spill
+    const uint32_t max_kb = type == T_Q4_K || type == T_Q5_K ? 4u : 3u;
     for (uint32_t kb = 2; kb <= max_kb; ++kb)
         if (nb % kb == 0 && nb / kb <= 16u) return kb;
     return 0;
@@ -295,6 +353,7 @@ hipError_t launch_matvec_mfma(uint32_t type, const uint8_t* W, uint32_t rows, ui
     switch (type) {
         case T_Q4_K: return launch_t<T_Q4_K>(kb, W, nb, rows, x, y, batch, s);
         case T_Q5_K: return launch_t<T_Q5_K>(kb, W, nb, rows, x, y, batch, s);
+        case T_Q6_K: return launch_t<T_Q6_K>(kb, W, nb, rows, x, y, batch, s);
         case T_Q8_0: return launch_t<T_Q8_0>(kb, W, nb, rows, x, y, batch, s);
         case T_Q4_0: return launch_t<T_Q4_0>(kb, W, nb, rows, x, y, batch, s);
         default: return hipErrorInvalidValue;

@@ -209,7 +209,7 @@ def test_staged_batched_widths(hip, port, gtype):
         wt.release()
 
 
-@pytest.mark.parametrize("gtype", (S.Q4_K, S.Q5_K, S.Q8_0, S.Q4_0))
+@pytest.mark.parametrize("gtype", (S.Q4_K, S.Q5_K, S.Q6_K, S.Q8_0, S.Q4_0))
 def test_mfma_batched_widths(hip, port, gtype):
     """Five to eight vectors through the MFMA kernel: one 256-value range per
     wave with two row tiles (2048 wide), two and three ranges per wave with
