@@ -10,8 +10,9 @@ namespace pk {
 // formats fetch one extra dword); every device weight buffer is padded by it.
 constexpr uint64_t kWeightTailPad = 64;
 
-// Largest hidden (input) width the register-resident matvec supports, per
-// batch size; wider rows are reported unsupported.
+// Whether a kernel covers (type, in, batch): the register-resident kernels up
+// to a width per batch size, the MFMA kernel for 5-8 vectors at any width it
+// can split into at most 16 waves; wider rows are reported unsupported.
 bool matvec_supported(uint32_t type, uint32_t in, uint32_t batch);
 
 // y[b][r] = W[r] . x[b] for b < batch.  W: rows x row_bytes encoded GGUF rows
