@@ -220,6 +220,9 @@ __global__ __launch_bounds__(1024) void k_matvec_mfma(const uint8_t* W, uint32_t
     const uint32_t waves = blockDim.x >> 6;
     const uint32_t n = lane & 15u, kq = lane >> 4;
     const uint32_t r0 = blockIdx.x * 16u * NT;
+    // gridDim.y K halves: half blockIdx.y takes the ranges from
+    // blockIdx.y * waves * KB on, and adds into y (zeroed beforehand)
+    const uint32_t kbase = (blockIdx.y * waves + wave) * KB;
     const uint32_t in = nb * 256u;
     const bool live = n < batch;  // A operand row m = n of this lane
 
@@ -232,12 +235,12 @@ __global__ __launch_bounds__(1024) void k_matvec_mfma(const uint8_t* W, uint32_t
         const uint32_t row = r0 + 16u * t + n;
         const QRow qr{W, nblk, static_cast<uint64_t>(row < rows ? row : rows - 1u) * nb * kPer};
 #pragma unroll
-        for (int j = 0; j < KB; ++j) mm_load<T>(qr, wave * KB + j, kq, part[t][j]);
+        for (int j = 0; j < KB; ++j) mm_load<T>(qr, kbase + j, kq, part[t][j]);
     }
 
     // the x of the wave's first XD groups, then XD groups ahead of their use
     constexpr int NG = KB * 8, XD = NG < 4 ? NG : 4;
-    const uint32_t m = live ? n : 0u, kw = wave * KB * 256u;
+    const uint32_t m = live ? n : 0u, kw = kbase * 256u;
     XRaw xr[XD];
 #pragma unroll
     for (int i = 0; i < XD; ++i) x_load(x, in, m, kw + 32u * i, kq, xr[i]);
@@ -298,20 +301,40 @@ __global__ __launch_bounds__(1024) void k_matvec_mfma(const uint8_t* W, uint32_t
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const uint32_t m = 4u * kq + i;
-                if (m < batch && row < rows) y[static_cast<uint64_t>(m) * rows + row] = s[i];
+                if (m < batch && row < rows) {
+                    float* o = y + static_cast<uint64_t>(m) * rows + row;
+                    // two halves onto +0: 0 + a + b = a + b in either order
+                    if (gridDim.y == 1) *o = s[i];
+                    else __hip_atomic_fetch_add(o, s[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                }
             }
         }
     }
 }
 
+__global__ __launch_bounds__(256) void k_zero(float* y, uint32_t n) {
+    const uint32_t i = blockIdx.x * 256u + threadIdx.x;
+    if (i < n) y[i] = 0.0f;
+}
+
 template <int T, int NT, int KB>
 hipError_t launch_nt_kb(const uint8_t* W, uint32_t nb, uint32_t rows, const float* x, float* y,
                         uint32_t batch, hipStream_t s) {
-    const uint32_t waves = nb / KB;
+    uint32_t waves = nb / KB;
     const uint32_t blocks = (rows + 16u * NT - 1u) / (16u * NT);
+    // at most half as many workgroups as CUs: two per row group, each half of
+    // K (the kernel's VALU work then spreads over twice the CUs; the zeroing
+    // launch costs about 2 us, more than that gains at 192 workgroups)
+    uint32_t halves = 1;
+    if (blocks <= 128u && waves % 2u == 0 && waves >= 4u) {
+        halves = 2;
+        waves /= 2;
+        const uint32_t n = batch * rows;
+        hipLaunchKernelGGL(k_zero, dim3((n + 255u) / 256u), dim3(256), 0, s, y, n);
+    }
     const size_t lds = static_cast<size_t>(waves) * NT * 64u * sizeof(mf32x4);
-    hipLaunchKernelGGL((k_matvec_mfma<T, NT, KB>), dim3(blocks), dim3(64u * waves), lds, s, W, nb,
-                       x, y, rows, batch);
+    hipLaunchKernelGGL((k_matvec_mfma<T, NT, KB>), dim3(blocks, halves), dim3(64u * waves), lds, s,
+                       W, nb, x, y, rows, batch);
     return hipGetLastError();
 }
 
