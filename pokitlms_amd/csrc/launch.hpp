@@ -21,10 +21,11 @@ hipError_t launch_matvec(uint32_t type, const uint8_t* W, uint64_t row_bytes, ui
                          uint32_t in, const float* x, float* y, uint32_t batch,
                          hipStream_t stream);
 
-// Batched Q4_K matvecs on MFMA (matvec_mfma.hip): K blocks per wave for
+// Batched matvecs on MFMA (matvec_mfma.hip): 256-value K ranges per wave for
 // (type, in, batch), 0 where that kernel does not apply; launch_matvec takes
-// it where it applies.
+// it where matvec_mfma_takes says so.
 uint32_t matvec_mfma_blocks_per_wave(uint32_t type, uint32_t in, uint32_t batch);
+bool matvec_mfma_takes(uint32_t type, uint32_t in, uint32_t batch, uint32_t rows);
 hipError_t launch_matvec_mfma(uint32_t type, const uint8_t* W, uint32_t rows, uint32_t in,
                               const float* x, float* y, uint32_t batch, hipStream_t stream);
 

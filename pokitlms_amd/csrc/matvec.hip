@@ -516,7 +516,7 @@ hipError_t launch_matvec(uint32_t type, const uint8_t* W, uint64_t row_bytes, ui
                          uint32_t in, const float* x, float* y, uint32_t batch,
                          hipStream_t stream) {
     if (rows == 0) return hipSuccess;
-    if (matvec_mfma_blocks_per_wave(type, in, batch))
+    if (matvec_mfma_takes(type, in, batch, rows))
         return launch_matvec_mfma(type, W, rows, in, x, y, batch, stream);
     switch (type) {
         case T_F32: return dispatch_batch_f<T_F32>(batch, W, row_bytes, rows, x, in, y, stream);

@@ -354,12 +354,12 @@ hipError_t launch_t(uint32_t kb, const uint8_t* W, uint32_t nb, uint32_t rows, c
 }  // namespace
 
 // 256-value ranges of K per wave: one (two row tiles per wave) up to 8 per
-// row, else the fewest (2..4, Q8_0/Q4_0 2..3) that leave at most 16 waves
-// (one tile per wave).  Batches of 5 to 8: at 4 vectors the register kernels are faster.
-uint32_t matvec_mfma_blocks_per_wave(uint32_t type, uint32_t in, uint32_t batch) {
+// row, else the fewest (2..4, Q8_0/Q4_0/Q6_K 2..3) that leave at most 16
+// waves (one tile per wave); 0 where the kernel does not apply.
+uint32_t mfma_kb(uint32_t type, uint32_t in) {
     if (type != T_Q4_K && type != T_Q5_K && type != T_Q6_K && type != T_Q8_0 && type != T_Q4_0)
         return 0;
-    if (batch < 5u || batch > 8u || in == 0 || in % 256u) return 0;
+    if (in == 0 || in % 256u) return 0;
     const uint32_t nb = in / 256u;
     if (nb <= 8u) return 1;
     // four ranges of Q6_K, or of 8 Q8_0/Q4_0 blocks, would spill
@@ -369,9 +369,26 @@ uint32_t matvec_mfma_blocks_per_wave(uint32_t type, uint32_t in, uint32_t batch)
     return 0;
 }
 
+uint32_t matvec_mfma_blocks_per_wave(uint32_t type, uint32_t in, uint32_t batch) {
+    return batch >= 5u && batch <= 8u ? mfma_kb(type, in) : 0u;
+}
+
+// Batches of 5 to 8; 4 vectors of the nibble formats where the grid splits K
+// over two workgroups (at most 128 row groups): there the register kernels
+// trail by about 10%, and lead by 2% for Q8_0 and Q6_K.
+bool matvec_mfma_takes(uint32_t type, uint32_t in, uint32_t batch, uint32_t rows) {
+    if (batch >= 5u) return matvec_mfma_blocks_per_wave(type, in, batch) != 0;
+    if (batch != 4u || type == T_Q8_0 || type == T_Q6_K) return false;
+    const uint32_t kb = mfma_kb(type, in);
+    if (kb == 0) return false;
+    const uint32_t nt = kb == 1u ? 2u : 1u, waves = in / 256u / kb;
+    const uint32_t blocks = (rows + 16u * nt - 1u) / (16u * nt);
+    return blocks <= 128u && waves % 2u == 0 && waves >= 4u;
+}
+
 hipError_t launch_matvec_mfma(uint32_t type, const uint8_t* W, uint32_t rows, uint32_t in,
                               const float* x, float* y, uint32_t batch, hipStream_t s) {
-    const uint32_t kb = matvec_mfma_blocks_per_wave(type, in, batch);
+    const uint32_t kb = mfma_kb(type, in);
     const uint32_t nb = in / 256u;
     switch (type) {
         case T_Q4_K: return launch_t<T_Q4_K>(kb, W, nb, rows, x, y, batch, s);
