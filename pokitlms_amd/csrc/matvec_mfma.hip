@@ -26,9 +26,9 @@
 //    group the CPU's weight is ds·f + cb, so acc += ds · (x . f) + cb · sum(x).
 //  * x enters as three bf16 planes (hi, mid, lo: x = hi + mid + lo exactly),
 //    split by each lane from FP32 for its (vector m = lane % 16, kq) slot;
-//    vectors m >= batch are zero.  The group sums go in through one
-//    v_mfma_f32_16x16x4f32 per group whose K runs over the four kq partial
-//    sums of 8 values, against cb.
+//    rows m >= batch repeat vector 0 and their outputs are not stored.  The
+//    group sums go in through one v_mfma_f32_16x16x4f32 per group whose K
+//    runs over the four kq partial sums of 8 values, against cb.
 //
 // Results differ from the CPU's serial FP32 sum only in rounding order, like
 // the register kernels' (within 1e-4 normwise).
@@ -122,10 +122,8 @@ __device__ __forceinline__ void x_load(const float* x, uint32_t in, uint32_t m, 
     r.b = *reinterpret_cast<const float4*>(p + 4);
 }
 
-__device__ __forceinline__ void x_split(const XRaw& r, bool live, XFrag& f) {
-    float v[8] = {r.a.x, r.a.y, r.a.z, r.a.w, r.b.x, r.b.y, r.b.z, r.b.w};
-#pragma unroll
-    for (int e = 0; e < 8; ++e) v[e] = live ? v[e] : 0.0f;
+__device__ __forceinline__ void x_split(const XRaw& r, XFrag& f) {
+    const float v[8] = {r.a.x, r.a.y, r.a.z, r.a.w, r.b.x, r.b.y, r.b.z, r.b.w};
     uint32_t h[4], md[4], lo[4];
 #pragma unroll
     for (int e = 0; e < 8; e += 2) {
@@ -224,7 +222,6 @@ __global__ __launch_bounds__(1024) void k_matvec_mfma(const uint8_t* W, uint32_t
     // blockIdx.y * waves * KB on, and adds into y (zeroed beforehand)
     const uint32_t kbase = (blockIdx.y * waves + wave) * KB;
     const uint32_t in = nb * 256u;
-    const bool live = n < batch;  // A operand row m = n of this lane
 
     // nb: 256-value ranges per row
     constexpr uint32_t kPer = 256u / Fmt<T>::BE;  // GGUF blocks per 256 values
@@ -240,7 +237,9 @@ __global__ __launch_bounds__(1024) void k_matvec_mfma(const uint8_t* W, uint32_t
 
     // the x of the wave's first XD groups, then XD groups ahead of their use
     constexpr int NG = KB * 8, XD = NG < 4 ? NG : 4;
-    const uint32_t m = live ? n : 0u, kw = kbase * 256u;
+    // A operand row m = n of this lane; rows m >= batch repeat vector 0 and
+    // only feed output rows that are not stored
+    const uint32_t m = n < batch ? n : 0u, kw = kbase * 256u;
     XRaw xr[XD];
 #pragma unroll
     for (int i = 0; i < XD; ++i) x_load(x, in, m, kw + 32u * i, kq, xr[i]);
@@ -252,7 +251,7 @@ __global__ __launch_bounds__(1024) void k_matvec_mfma(const uint8_t* W, uint32_t
 #pragma unroll
     for (int gi = 0; gi < NG; ++gi) {
         XFrag xf;
-        x_split(xr[gi % XD], live, xf);
+        x_split(xr[gi % XD], xf);
         if (gi + XD < NG) x_load(x, in, m, kw + 32u * (gi + XD), kq, xr[gi % XD]);
         const int j = gi / 8, g = gi % 8;
 #pragma unroll
@@ -346,7 +345,9 @@ hipError_t launch_t(uint32_t kb, const uint8_t* W, uint32_t nb, uint32_t rows, c
         case 1: return launch_nt_kb<T, 2, 1>(W, nb, rows, x, y, batch, s);
         case 2: return launch_nt_kb<T, 1, 2>(W, nb, rows, x, y, batch, s);
         case 3: return launch_nt_kb<T, 1, 3>(W, nb, rows, x, y, batch, s);
-        case 4: return launch_nt_kb<T, 1, 4>(W, nb, rows, x, y, batch, s);
+        case 4:  // (mfma_kb gives 4 to Q4_K/Q5_K only)
+            if constexpr (T == T_Q4_K || T == T_Q5_K) return launch_nt_kb<T, 1, 4>(W, nb, rows, x, y, batch, s);
+            return hipErrorInvalidValue;
         default: return hipErrorInvalidValue;
     }
 }
