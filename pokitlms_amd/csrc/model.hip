@@ -251,6 +251,56 @@ __global__ __launch_bounds__(256) void k_add_rmsnorm(float* __restrict__ x, cons
     for (uint32_t i = threadIdx.x; i < n; i += blockDim.x) out[i] = x[i] * scale * w[i];
 }
 
+// The same for n % 4 == 0, n <= 1024·NI, 16-byte-aligned rows: each thread
+// loads its float4s of x, delta and w at once and keeps them in registers, so
+// the kernel waits for memory once (the loop above reloads x after storing
+// it, and loads w only after the sum).
+template <int NI>
+__global__ __launch_bounds__(256) void k_add_rmsnorm4(float* __restrict__ x,
+                                                      const float* __restrict__ delta,
+                                                      const float* __restrict__ w,
+                                                      float* __restrict__ out, uint32_t n,
+                                                      float eps) {
+    __shared__ float red[4];
+    const uint32_t n4 = n / 4u;
+    float4 v[NI], wv[NI];
+#pragma unroll
+    for (int i = 0; i < NI; ++i) {
+        const uint32_t c = threadIdx.x + 256u * i, cc = c < n4 ? c : 0u;
+        v[i] = reinterpret_cast<const float4*>(x)[cc];
+        wv[i] = reinterpret_cast<const float4*>(w)[cc];
+        if (delta) {
+            const float4 d = reinterpret_cast<const float4*>(delta)[cc];
+            v[i].x = v[i].x + d.x;
+            v[i].y = v[i].y + d.y;
+            v[i].z = v[i].z + d.z;
+            v[i].w = v[i].w + d.w;
+        }
+    }
+    float ss = 0.0f;
+#pragma unroll
+    for (int i = 0; i < NI; ++i) {
+        if (threadIdx.x + 256u * i < n4) {
+            ss += v[i].x * v[i].x;
+            ss += v[i].y * v[i].y;
+            ss += v[i].z * v[i].z;
+            ss += v[i].w * v[i].w;
+        }
+    }
+    const float total = block_sum(ss, red);
+    const float scale = 1.0f / sqrtf(total / static_cast<float>(n) + eps);
+#pragma unroll
+    for (int i = 0; i < NI; ++i) {
+        const uint32_t c = threadIdx.x + 256u * i;
+        if (c < n4) {
+            if (delta) reinterpret_cast<float4*>(x)[c] = v[i];
+            reinterpret_cast<float4*>(out)[c] =
+                make_float4(v[i].x * scale * wv[i].x, v[i].y * scale * wv[i].y,
+                            v[i].z * scale * wv[i].z, v[i].w * scale * wv[i].w);
+        }
+    }
+}
+
 // First-max argmax of the logits in two launches: each workgroup of
 // k_argmax_part the maximum of one 2048-logit chunk (larger value, then smaller
 // index: the first maximum), non-finite logits flagged; k_argmax the maximum
@@ -467,8 +517,23 @@ hipError_t launch_model_step(const ModelArgs& a, const ModelLayer* layers, bool 
     const uint32_t qd = a.heads * a.head_dim, kd = a.kv_heads * a.head_dim;
     const float* delta = nullptr;  // the residual the next RMSNorm adds first
     auto norm = [&](const float* d, const float* w) -> hipError_t {
-        hipLaunchKernelGGL(k_add_rmsnorm, dim3(1), dim3(256), 0, s, a.hidden_state, d, w, a.normed,
-                           a.hidden, a.rms_eps);
+        const auto al16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; };
+        const uint32_t ni = (a.hidden + 1023u) / 1024u;
+        if (a.hidden % 4u == 0 && ni <= 8u && al16(a.hidden_state) && al16(d) && al16(w) &&
+            al16(a.normed)) {
+            const dim3 g(1), b(256);
+            if (ni == 1u)
+                hipLaunchKernelGGL(k_add_rmsnorm4<1>, g, b, 0, s, a.hidden_state, d, w, a.normed, a.hidden, a.rms_eps);
+            else if (ni == 2u)
+                hipLaunchKernelGGL(k_add_rmsnorm4<2>, g, b, 0, s, a.hidden_state, d, w, a.normed, a.hidden, a.rms_eps);
+            else if (ni <= 4u)
+                hipLaunchKernelGGL(k_add_rmsnorm4<4>, g, b, 0, s, a.hidden_state, d, w, a.normed, a.hidden, a.rms_eps);
+            else
+                hipLaunchKernelGGL(k_add_rmsnorm4<8>, g, b, 0, s, a.hidden_state, d, w, a.normed, a.hidden, a.rms_eps);
+        } else {
+            hipLaunchKernelGGL(k_add_rmsnorm, dim3(1), dim3(256), 0, s, a.hidden_state, d, w, a.normed,
+                               a.hidden, a.rms_eps);
+        }
         return hipGetLastError();
     };
     auto matvec = [&](uint32_t type, const uint8_t* W, uint64_t row_bytes, uint32_t rows,
