@@ -1,5 +1,5 @@
-// matvec_mfma.hip -- batched matvecs (5 to 8 vectors) on bf16 MFMA, for
-// Q4_K, Q5_K, Q8_0 and Q4_0.
+// matvec_mfma.hip -- batched matvecs (5 to 8 vectors, and 4 where the grid
+// is small) on bf16 MFMA, for Q4_K, Q5_K, Q6_K, Q8_0 and Q4_0.
 //
 // The batched case of tensor_linear (src/tensor_linear.cpp:232-263 of the
 // reference, per-row linear_k / linear_quantized of
@@ -13,9 +13,13 @@
 //  * A wave owns 16·NT rows (NT tiles of 16, lane n = lane % 16 of each tile)
 //    and KB consecutive 256-value ranges of K; the waves of a workgroup own
 //    the same rows and consecutive K ranges, and their partial results are
-//    added through LDS in wave order (deterministic).
-//  * Every scale group of the formats here is 32 values, one MFMA K step,
-//    lane kq = lane / 16 holding values 8kq .. 8kq+7 of it.  Per 256 values
+//    added through LDS in wave order (deterministic).  A grid of at most 128
+//    row groups takes two workgroups per row group, one per half of K, that
+//    add into y zeroed beforehand (two terms onto +0: the same sum in either
+//    order).
+//  * A scale group of 32 values is one MFMA K step, lane kq = lane / 16
+//    holding values 8kq .. 8kq+7 of it (Q6_K's two 16-value groups per step:
+//    two MFMAs, each with the other group's lanes zeroed).  Per 256 values
 //    lane (n, kq) loads (Q4_K, Q5_K) the block header and bytes 8kq .. 8kq+7
 //    of each 32-byte nibble chunk (chunk c's low nibbles are group 2c, its
 //    high nibbles group 2c+1; Q5_K also bytes 8kq .. 8kq+7 of qh, bit g for
