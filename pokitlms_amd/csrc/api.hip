@@ -1218,6 +1218,7 @@ struct pk_hip_qwen3moe {
     DeviceBuffer<uint32_t> expf_slots;
     DeviceBuffer<double> row_sum, row_bound;
     DeviceBuffer<uint16_t> kv;
+    DeviceBuffer<uint8_t> qkv;  // fast mode: each layer's q, k and v rows back to back
     hipGraphExec_t step_logits = nullptr, step_plain = nullptr;
     hipEvent_t ev[2] = {};
 };
@@ -1279,6 +1280,7 @@ void release_model(pk_hip_qwen3moe* m) {
     m->row_sum.release();
     m->row_bound.release();
     m->kv.release();
+    m->qkv.release();
 }
 
 }  // namespace
@@ -1336,10 +1338,10 @@ pk_hip_status pk_hip_qwen3moe_create(pk_hip_ctx* ctx, const pk_hip_qwen3moe_conf
         a.normed = p; p += c.hidden;
         a.attn_out = p; p += c.hidden;
         a.hidden_alt = p; p += c.hidden;
-        a.q = p; p += qd;
-        a.att = p; p += qd;
+        a.q = p; p += qd;  // q, k, v back to back: one matvec fills all three
         a.k = p; p += kd;
         a.v = p; p += kd;
+        a.att = p; p += qd;
         a.logits = p; p += c.vocab;
         a.argmax_part = p;
         a.state = m->state.ptr;
@@ -1434,6 +1436,20 @@ pk_hip_status pk_hip_qwen3moe_create(pk_hip_ctx* ctx, const pk_hip_qwen3moe_conf
             D.k_row = L.k->row_bytes;
             D.v_row = L.v->row_bytes;
             D.o_row = L.o->row_bytes;
+            // fast mode, GGUF-form rows (planar types keep a plane per tensor):
+            // a copy of q, k and v back to back, so one launch computes all three
+            D.qkv = nullptr;
+            if (!exact && !pk::planar_type(D.attn_type) && D.k_row == D.q_row && D.v_row == D.q_row) {
+                const uint64_t qb = qd * D.q_row, kb = kd * D.q_row;
+                const uint64_t pitch = (qb + 2 * kb + pk::kWeightTailPad + 255) / 256 * 256;
+                if (l == 0) m->qkv.ensure(pitch * c.layers);
+                uint8_t* dst = m->qkv.ptr + pitch * l;
+                check(hipMemcpyAsync(dst, D.q, qb, hipMemcpyDeviceToDevice, ctx->stream), "copy q rows");
+                check(hipMemcpyAsync(dst + qb, D.k, kb, hipMemcpyDeviceToDevice, ctx->stream), "copy k rows");
+                check(hipMemcpyAsync(dst + qb + kb, D.v, kb, hipMemcpyDeviceToDevice, ctx->stream),
+                      "copy v rows");
+                D.qkv = dst;
+            }
             D.kcache = m->kv.ptr + 2ull * l * c.kv_capacity * kd;
             D.vcache = D.kcache + uint64_t(c.kv_capacity) * kd;
             pk::MoeDecodeArgs& g = D.moe;

@@ -117,6 +117,7 @@ struct ModelLayer {
     const uint8_t* q;         // [heads * head_dim] rows of [hidden]
     const uint8_t* k;         // [kv_heads * head_dim] rows
     const uint8_t* v;
+    const uint8_t* qkv;       // fast mode: q, k and v rows back to back, or null
     const uint8_t* o;         // [hidden] rows of [heads * head_dim]
     uint32_t attn_type;
     uint64_t q_row, k_row, v_row, o_row;

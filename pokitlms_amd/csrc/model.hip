@@ -543,9 +543,14 @@ hipError_t launch_model_step(const ModelArgs& a, const ModelLayer* layers, bool 
     for (uint32_t l = 0; l < a.layers; ++l) {
         const ModelLayer& L = layers[l];
         if ((err = norm(delta, L.attn_norm))) return err;
-        if ((err = matvec(L.attn_type, L.q, L.q_row, qd, a.hidden, a.normed, a.q))) return err;
-        if ((err = matvec(L.attn_type, L.k, L.k_row, kd, a.hidden, a.normed, a.k))) return err;
-        if ((err = matvec(L.attn_type, L.v, L.v_row, kd, a.hidden, a.normed, a.v))) return err;
+        if (L.qkv && a.k == a.q + qd && a.v == a.k + kd) {  // q, k and v in one launch
+            if ((err = matvec(L.attn_type, L.qkv, L.q_row, qd + 2u * kd, a.hidden, a.normed, a.q)))
+                return err;
+        } else {
+            if ((err = matvec(L.attn_type, L.q, L.q_row, qd, a.hidden, a.normed, a.q))) return err;
+            if ((err = matvec(L.attn_type, L.k, L.k_row, kd, a.hidden, a.normed, a.k))) return err;
+            if ((err = matvec(L.attn_type, L.v, L.v_row, kd, a.hidden, a.normed, a.v))) return err;
+        }
         if ((err = launch_ref_attention(a, L, s))) return err;  // the kernel of both modes
         if ((err = matvec(L.attn_type, L.o, L.o_row, a.hidden, qd, a.att, a.attn_out))) return err;
         if ((err = norm(a.attn_out, L.ffn_norm))) return err;
