@@ -905,8 +905,11 @@ __global__ __launch_bounds__(1024) void k_ref_rmsnorm(float* x, RefResidual res,
 // current position's k and v come from LDS, older ones from the ring: each
 // FP16 K row loaded whole (HD / 8 16-byte loads), V rows staged through LDS a
 // tile of positions at a time.
+// FAST (the bandwidth-optimised decode step): the device's expf instead of
+// the reference's (an FP64 exp and two table loads from global memory per
+// position, a memory round trip in the middle of the kernel).
 constexpr uint32_t kAttnTileBytes = 64u * 1024u;
-template <int HD>
+template <int HD, bool FAST>
 __global__ __launch_bounds__(256) void k_ref_attention(ModelArgs a, ModelLayer L) {
     extern __shared__ __attribute__((aligned(64))) float lds[];  // sc [chain_floats(capacity)], V tile
     __shared__ float qv[HD], kcur[HD], sqq[HD], sqk[HD];
@@ -1003,7 +1006,10 @@ __global__ __launch_bounds__(256) void k_ref_attention(ModelArgs a, ModelLayer L
     if ((tid & 63u) == 0u) red[tid >> 6] = m;
     __syncthreads();
     const float mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-    for (uint32_t i = tid; i < n; i += 256u) sc[i] = expf_libm(__fsub_rn(sc[i], mx), a.expf);
+    for (uint32_t i = tid; i < n; i += 256u) {
+        const float e = __fsub_rn(sc[i], mx);
+        sc[i] = FAST ? expf(e) : expf_libm(e, a.expf);
+    }
     __syncthreads();
     if (tid == 0) s_den = serial_sum(sc, n, 0.0f);
     __syncthreads();
@@ -1162,15 +1168,24 @@ bool ref_attention_supported(uint32_t head_dim, uint32_t capacity) {
            (chain_floats(capacity) * 4ull + kAttnTileBytes) <= 160ull * 1024u - 8192u;
 }
 
-hipError_t launch_ref_attention(const ModelArgs& a, const ModelLayer& L, hipStream_t s) {
+template <bool FAST>
+hipError_t launch_attention_t(const ModelArgs& a, const ModelLayer& L, hipStream_t s) {
     const size_t lds = chain_floats(a.capacity) * sizeof(float) + kAttnTileBytes;
     switch (a.head_dim) {
-        case 64: hipLaunchKernelGGL(k_ref_attention<64>, dim3(a.heads), dim3(256), lds, s, a, L); break;
-        case 128: hipLaunchKernelGGL(k_ref_attention<128>, dim3(a.heads), dim3(256), lds, s, a, L); break;
-        case 256: hipLaunchKernelGGL(k_ref_attention<256>, dim3(a.heads), dim3(256), lds, s, a, L); break;
+        case 64: hipLaunchKernelGGL((k_ref_attention<64, FAST>), dim3(a.heads), dim3(256), lds, s, a, L); break;
+        case 128: hipLaunchKernelGGL((k_ref_attention<128, FAST>), dim3(a.heads), dim3(256), lds, s, a, L); break;
+        case 256: hipLaunchKernelGGL((k_ref_attention<256, FAST>), dim3(a.heads), dim3(256), lds, s, a, L); break;
         default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
+}
+
+hipError_t launch_ref_attention(const ModelArgs& a, const ModelLayer& L, hipStream_t s) {
+    return launch_attention_t<false>(a, L, s);
+}
+
+hipError_t launch_fast_attention(const ModelArgs& a, const ModelLayer& L, hipStream_t s) {
+    return launch_attention_t<true>(a, L, s);
 }
 
 // Six launches per layer; the residual stream alternates between

@@ -269,6 +269,8 @@ constexpr uint32_t kMaxRefNormWidth = 4096;
 // q/k head norms, RoPE, KV append and attention of one layer in the
 // reference's order (both modes use it).
 hipError_t launch_ref_attention(const ModelArgs& a, const ModelLayer& L, hipStream_t stream);
+// The same attention with the device's expf (the fast step).
+hipError_t launch_fast_attention(const ModelArgs& a, const ModelLayer& L, hipStream_t stream);
 // The reference-order token step after the embedding (all layers, then the
 // head when logits).
 hipError_t launch_ref_step(const ModelArgs& a, const ModelLayer* layers, bool logits,

@@ -551,7 +551,7 @@ hipError_t launch_model_step(const ModelArgs& a, const ModelLayer* layers, bool 
             if ((err = matvec(L.attn_type, L.k, L.k_row, kd, a.hidden, a.normed, a.k))) return err;
             if ((err = matvec(L.attn_type, L.v, L.v_row, kd, a.hidden, a.normed, a.v))) return err;
         }
-        if ((err = launch_ref_attention(a, L, s))) return err;  // the kernel of both modes
+        if ((err = launch_fast_attention(a, L, s))) return err;
         if ((err = matvec(L.attn_type, L.o, L.o_row, a.hidden, qd, a.att, a.attn_out))) return err;
         if ((err = norm(a.attn_out, L.ffn_norm))) return err;
         err = launch_moe_decode(L.moe, s);  // normed -> moe_out
