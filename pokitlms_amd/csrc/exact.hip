@@ -1021,22 +1021,23 @@ __global__ __launch_bounds__(256) void k_ref_attention(ModelArgs a, ModelLayer L
         __syncthreads();  // previous tile consumed (and, first time, the weights written)
         // stage V rows t0 .. t0 + tn: HD / 8 16-byte pieces per row
         constexpr uint32_t PPR = HD / 8;
-        for (uint32_t base = 0; base < tn * PPR; base += 256u * 4u) {
-            u32x4_t pv[4];
+        // 8 pieces per thread, every global load unconditional (the current
+        // position reads a ring row and takes the LDS copy instead), so the
+        // pass waits for memory once
+        constexpr int KL = 8;
+        for (uint32_t base = 0; base < tn * PPR; base += 256u * KL) {
+            u32x4_t pv[KL];
 #pragma unroll
-            for (int k = 0; k < 4; ++k) {
+            for (int k = 0; k < KL; ++k) {
                 const uint32_t q = base + tid + 256u * k, qc = q < tn * PPR ? q : 0u;
                 const uint32_t i = t0 + qc / PPR;
-                if (i + 1u == n) {
-                    pv[k] = reinterpret_cast<const u32x4_t*>(vcur)[qc % PPR];
-                } else {
-                    const uint32_t slot = (first + i) % a.capacity;
-                    pv[k] = reinterpret_cast<const u32x4_t*>(L.vcache + slot * row_halves + kvh * HD)[qc % PPR];
-                }
+                const uint32_t slot = (first + i) % a.capacity;
+                pv[k] = reinterpret_cast<const u32x4_t*>(L.vcache + slot * row_halves + kvh * HD)[qc % PPR];
             }
 #pragma unroll
-            for (int k = 0; k < 4; ++k) {
-                const uint32_t q = base + tid + 256u * k;
+            for (int k = 0; k < KL; ++k) {
+                const uint32_t q = base + tid + 256u * k, qc = q < tn * PPR ? q : 0u;
+                if (t0 + qc / PPR + 1u == n) pv[k] = reinterpret_cast<const u32x4_t*>(vcur)[qc % PPR];
                 if (q < tn * PPR) reinterpret_cast<u32x4_t*>(vt)[q] = pv[k];
             }
         }
