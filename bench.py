@@ -51,6 +51,7 @@ def parse():
     ap.add_argument("--prefill-reps", type=int, default=40)
     ap.add_argument("--no-decode", action="store_true", help="skip the whole-model decode leg")
     ap.add_argument("--no-matvec", action="store_true", help="skip the C1/C2 matvec leg")
+    ap.add_argument("--no-floor", action="store_true", help="skip the plain-read floor leg")
     ap.add_argument("--matvec-reps", type=int, default=10)
     ap.add_argument("--decode-cpu-full", action="store_true",
                     help="only time the reference CPU runner on the full 48-layer model")
@@ -60,6 +61,24 @@ def parse():
                     help="first run a plain device copy of this many MiB three times "
                          "(the known-size kernel that scales rocprofv3 FETCH/WRITE_SIZE)")
     return ap.parse_args()
+
+
+def cpu_info() -> dict:
+    """The host CPU model (/proc/cpuinfo) and the threads this process may use."""
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    try:
+        usable = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        usable = os.cpu_count()
+    return {"cpu_model": model, "nproc": usable}
 
 
 def profiled_traffic(kernel: str):
@@ -120,7 +139,7 @@ PREFILL_GEMM_FLOPS = {"gate_up": PREFILL_TOKENS * 8 * 2 * 2 * 2048 * 768,
                       "down": PREFILL_TOKENS * 8 * 2 * 768 * 2048}
 
 
-def prefill_leg(torch, hip, layers, stream, reps: int, cpu_ms_per_token):
+def prefill_leg(torch, hip, layers, stream, reps: int, with_cpu: bool):
     """Batched prefill: 512 tokens through the config-3
     layer shape with a router fitted so the expert load follows Zipf(1.1).
     The rotated layers keep their expert weights; each gets the fitted router.
@@ -197,6 +216,14 @@ def prefill_leg(torch, hip, layers, stream, reps: int, cpu_ms_per_token):
                      "avg_us": round(phase_us["gate_up"], 2),
                      "algorithmic_flops": PREFILL_GEMM_FLOPS["gate_up"]},
         "phase_us": {k: round(v, 2) for k, v in phase_us.items()},
+        # the roofline as flat fields too (nested objects are not kept by every reader)
+        "gate_up_tflops": round(gu_tflops, 2),
+        "gate_up_frac_of_bf16_peak": round(gu_tflops / MFMA_BF16_PEAK_TFLOPS, 4),
+        "gate_up_us": round(phase_us["gate_up"], 2),
+        "down_us": round(phase_us["down"], 2),
+        "route_us": round(phase_us["route"], 2),
+        "ids_equal_decode": ids_ok,
+        "normwise_vs_decode": worst,
         "router_fallbacks_per_batch": st["router_fallbacks"] / n,
         "router_candidates_per_batch": st["router_candidates"] / n,
         "expert_load": {"max": int(counts.max()), "touched": int((counts > 0).sum()),
@@ -204,14 +231,82 @@ def prefill_leg(torch, hip, layers, stream, reps: int, cpu_ms_per_token):
         "parity_vs_decode": {"ids_equal": ids_ok, "normwise_rel": worst, "tokens": 128},
         "layers_rotated": len(zl),
     }
-    if cpu_ms_per_token:
-        cpu_tps = 1e3 / cpu_ms_per_token
-        out["cpu_baseline"] = {"tokens_per_s": round(cpu_tps, 2),
-                               "sample": "512 sequential single-token MoE blocks, from the "
-                                         "single-token pass time of the decode baseline"}
-        out["speedup_vs_cpu"] = round(out["tokens_per_s"] / cpu_tps, 1)
+    if with_cpu:
+        log("prefill cpu baseline (512 single-token reference MoE blocks) ...")
+        cpu = prefill_cpu_baseline()
+        out["cpu_baseline"] = cpu
+        out["cpu_tokens_per_s"] = cpu["tokens_per_s"]
+        out["speedup_vs_cpu"] = round(out["tokens_per_s"] / cpu["tokens_per_s"], 1)
     r.release()
     return out
+
+
+# Plain-read floors: the whole config-3 step's routed bytes, each of its two
+# expert kernels' bytes, and config 1's matrix.
+FLOOR_BYTES = {"step": 25_526_272, "gate_up": 14_188_544, "down": 10_354_688,
+               "c1": 9_437_184}
+
+
+def floor_leg(torch, hip, stream, reps: int = 20):
+    """What a plain streaming read (pk_hip_read_floor_async: 16-byte
+    nontemporal loads over the whole chip) takes for each byte count, timed
+    like the MoE step: a HIP graph of one launch per distinct copy (at least
+    640 MB of copies, so nothing is served from the 256 MB MALL), replayed
+    `reps` times; per-launch time = graph time / launches."""
+    dev = torch.device("cuda:0")
+    out = {}
+    sink = torch.zeros(4, dtype=torch.int32, device=dev)
+    for name, nbytes in FLOOR_BYTES.items():
+        copies = max(4, -(-(640 << 20) // nbytes))
+        buf = torch.randint(0, 256, (copies * nbytes,), dtype=torch.uint8, device=dev)
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=stream):
+            cs = torch.cuda.current_stream().cuda_stream
+            for c in range(copies):
+                hip.read_floor_async(buf.data_ptr() + c * nbytes, nbytes, sink.data_ptr(), cs)
+        with torch.cuda.stream(stream):
+            g.replay()
+            torch.cuda.synchronize()
+            ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            ev0.record(stream)
+            for _ in range(reps):
+                g.replay()
+            ev1.record(stream)
+            ev1.synchronize()
+        us = ev0.elapsed_time(ev1) * 1e3 / (reps * copies)
+        out[name] = {"bytes": nbytes, "us": round(us, 3), "gbs": round(nbytes / us / 1e3, 1),
+                     "frac": round(nbytes / us / 1e3 / HBM_PEAK_GBS, 4), "copies": copies}
+        log(f"read floor {name} {nbytes} B: {us:.3f} us/launch, {nbytes / us / 1e3:.0f} GB/s")
+        del g, buf
+        torch.cuda.synchronize()
+    return out
+
+
+def prefill_cpu_baseline(kind_pref: str = "reference"):
+    """The reference MoE block (oracle/_ref, its row pool; the port when the
+    reference library is absent) run on the 512 config-4 tokens one at a time,
+    as the reference prefills (src/qwen3_moe_runner.cpp:785-790), through a
+    config-3 layer with the fitted Zipf router: total wall seconds."""
+    import oracle
+    from pokitlms_amd import synth as S
+    kind = kind_pref if oracle.available(kind_pref) else "port"
+    cpu = oracle.Oracle(kind)
+    layer = S.moe_layer(seed=3)
+    router, _ = S.zipf_router(128, 2048, 8, seed=404)
+    layer.router = router
+    blk = cpu.moe(layer)
+    x = S.zipf_tokens(404, PREFILL_TOKENS, 2048)
+    blk.forward(x[0])  # warm-up
+    t0 = time.perf_counter()
+    for t in range(PREFILL_TOKENS):
+        blk.forward(x[t])
+    secs = time.perf_counter() - t0
+    cores = cpu.lib.pkref_row_workers() if kind == "reference" else 1
+    return {"tokens_per_s": round(PREFILL_TOKENS / secs, 2), "seconds": round(secs, 3),
+            "cores": int(cores), "kind": kind, **cpu_info(),
+            "sample": f"{PREFILL_TOKENS} config-4 tokens through the reference MoE block one "
+                      f"at a time (Zipf router fitted as the GPU leg's), row pool of {cores}"}
 
 
 MATVEC_COPIES = 64  # distinct weight copies per case (at most; > 2x the 256 MB MALL)
@@ -231,7 +326,28 @@ def matvec_cases():
     return cases
 
 
-def matvec_leg(torch, hip, stream, reps: int, only=None):
+def matvec_cpu_us(cpu, gtype, rows, inn, batch, seed, reps: int = 5):
+    """The reference tensor_linear (oracle/_ref, row pool of min(6, max(2,
+    nproc - 1)) workers, src/tensor_linear.cpp:20-128,196-227) on one random
+    matrix of the case's format and shape: `batch` calls per timed rep (the
+    reference has no batched matvec), median of `reps` reps after one warm-up
+    call, in microseconds per rep."""
+    import numpy as np
+
+    from pokitlms_amd import synth as S
+    g = S.rng(seed)
+    w = S.quant_matrix(gtype, rows, inn, g)
+    x = S.normal_f32(g, inn)
+    cpu.linear_repeat(gtype, w, inn, rows, x, 1)
+    times = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        cpu.linear_repeat(gtype, w, inn, rows, x, batch)
+        times.append(time.perf_counter() - t0)
+    return float(np.median(times)) * 1e6
+
+
+def matvec_leg(torch, hip, stream, reps: int, only=None, with_cpu: bool = True):
     """K-quant matvec throughput (configs[0..1]).  Each case's weights are one
     expert tensor of MATVEC_COPIES distinct random matrices made on the GPU;
     a HIP graph launches the matvec once per copy, so the weights stream from
@@ -243,6 +359,11 @@ def matvec_leg(torch, hip, stream, reps: int, only=None):
     from pokitlms_amd import synth as S
     dev = torch.device("cuda:0")
     out = []
+    cpu = None
+    if with_cpu:
+        import oracle
+        if oracle.available("reference"):
+            cpu = oracle.Oracle("reference")
     for name, gtype, rows, inn, batch in matvec_cases():
         if only and (S.TYPE_NAMES[gtype], rows, inn, batch) not in only:
             continue
@@ -280,15 +401,21 @@ def matvec_leg(torch, hip, stream, reps: int, only=None):
         st = hip.stats()
         us_event = st["matvec_ns"] / st["matvec_launches"] / 1e3
         nbytes = S.matrix_bytes(gtype, inn, rows) + 4 * batch * (inn + rows)
-        out.append({"config": name, "type": S.TYPE_NAMES[gtype], "out": rows, "in": inn,
-                    "batch": batch, "bytes": nbytes, "copies": copies,
-                    "us_graph": round(us_graph, 3), "us_event": round(us_event, 3),
-                    "gbs_graph": round(nbytes / us_graph / 1e3, 1),
-                    "gbs_event": round(nbytes / us_event / 1e3, 1),
-                    "frac_event": round(nbytes / us_event / 1e3 / HBM_PEAK_GBS, 4)})
+        rec = {"config": name, "type": S.TYPE_NAMES[gtype], "out": rows, "in": inn,
+               "batch": batch, "bytes": nbytes, "copies": copies,
+               "us_graph": round(us_graph, 3), "us_event": round(us_event, 3),
+               "gbs_graph": round(nbytes / us_graph / 1e3, 1),
+               "gbs_event": round(nbytes / us_event / 1e3, 1),
+               "frac_event": round(nbytes / us_event / 1e3 / HBM_PEAK_GBS, 4)}
+        if cpu is not None:
+            cpu_us = matvec_cpu_us(cpu, gtype, rows, inn, batch, 7000 + gtype + rows // 2048)
+            rec["cpu_us"] = round(cpu_us, 1)
+            rec["speedup_vs_cpu"] = round(cpu_us / us_graph, 1)
+        out.append(rec)
         log(f"matvec {name} {S.TYPE_NAMES[gtype]} {rows}x{inn} B={batch}: "
             f"{us_graph:.2f} us/launch (graph), {us_event:.2f} us (event), "
-            f"{nbytes / us_graph / 1e3:.0f} GB/s")
+            f"{nbytes / us_graph / 1e3:.0f} GB/s"
+            + (f", cpu {rec['cpu_us']:.0f} us" if cpu is not None else ""))
         del g, X, Y
         w.release()
         torch.cuda.synchronize()
@@ -469,10 +596,16 @@ def decode_leg(torch, hip, with_cpu: bool):
         cpu = decode_cpu_full()
         if cpu is None:
             cpu = decode_cpu_baseline()
+        if cpu:
+            cpu.update(cpu_info())
         out["cpu_baseline"] = cpu
         if cpu:
-            for mode in ("reference_order", "fast"):
-                out[mode]["speedup_vs_cpu"] = round(out[mode]["forwards_per_s"] / cpu["value"], 1)
+            # token parity holds in reference order only; the fast kernels'
+            # tokens leave the reference's (see "fast"), so no speed-up is
+            # claimed for them
+            out["reference_order"]["speedup_vs_cpu"] = round(
+                out["reference_order"]["forwards_per_s"] / cpu["value"], 1)
+    out["fast"]["token_parity"] = False
     return out
 
 
@@ -502,6 +635,7 @@ def cpu_baseline(seconds: float):
     med = float(np.median(times))
     cores = cpu.lib.pkref_row_workers() if kind == "reference" else 1
     return {
+        **cpu_info(),
         "value": round(layer.routed_bytes() / med / 1e9, 3),
         "unit": "GB/s",
         "cores": int(cores),
@@ -511,6 +645,40 @@ def cpu_baseline(seconds: float):
                   f"wall time; reference row pool of {cores} workers, router single-threaded; "
                   f"host nproc {os.cpu_count()}",
     }
+
+
+def flatten_summary(out, floors, matvec, decode):
+    """The other configs' headline figures as flat scalar fields of the
+    `roofline` and `cpu_baseline` objects (readers that keep only scalar
+    fields of known objects still see them): config-1/2 matvec times and HBM
+    fractions with their reference CPU times, the plain-read floors, and the
+    config-5 decode's ms/forward, HBM fraction, token parity and CPU time."""
+    rl, cb = out["roofline"], out["cpu_baseline"]
+    rl["step_us"] = out["ms_per_step"] * 1e3
+    if floors:
+        for name, f in floors.items():
+            rl[f"floor_{name}_us"] = f["us"]
+            rl[f"floor_{name}_frac"] = f["frac"]
+        rl["step_vs_floor"] = round(floors["step"]["us"] / rl["step_us"], 4)
+    if matvec:
+        for m in matvec:
+            key = (f"c1" if m["config"] == "c1" else
+                   "head" if m["config"] == "c5_head" else
+                   f"c2_{m['type']}_{m['out']}x{m['in']}_b{m['batch']}")
+            rl[f"{key}_us"] = m["us_graph"]
+            rl[f"{key}_frac"] = round(m["gbs_graph"] / HBM_PEAK_GBS, 4)
+            if cb is not None and "cpu_us" in m:
+                cb[f"{key}_cpu_us"] = m["cpu_us"]
+    if decode:
+        ro = decode["reference_order"]
+        rl["c5_ms_per_forward"] = ro["ms_per_forward"]
+        rl["c5_hbm_frac"] = round(ro["weight_gbs"] / HBM_PEAK_GBS, 4)
+        rl["c5_token_parity"] = bool(decode["token_parity"])
+        rl["c5_fast_ms_per_forward"] = decode["fast"]["ms_per_forward"]
+        c5cpu = decode.get("cpu_baseline")
+        if cb is not None and c5cpu:
+            cb["c5_s_per_forward"] = c5cpu["s_per_forward"]
+            cb["c5_speedup"] = ro.get("speedup_vs_cpu")
 
 
 def main():
@@ -680,13 +848,17 @@ def main():
     prefill = None
     if not args.no_prefill:
         log("prefill leg ...")
-        prefill = prefill_leg(torch, hip, layers[:4], stream, args.prefill_reps,
-                              cpu["ms_per_token"] if cpu else None)
+        prefill = prefill_leg(torch, hip, layers[:4], stream, args.prefill_reps, not args.no_cpu)
+
+    floors = None
+    if not args.no_floor:
+        log("read-floor leg ...")
+        floors = floor_leg(torch, hip, stream)
 
     matvec = None
     if not args.no_matvec:
         log("matvec leg ...")
-        matvec = matvec_leg(torch, hip, stream, args.matvec_reps)
+        matvec = matvec_leg(torch, hip, stream, args.matvec_reps, with_cpu=not args.no_cpu)
 
     decode = None
     if not args.no_decode:
@@ -734,6 +906,8 @@ def main():
     }
     if cpu:
         out["speedup_vs_cpu"] = round(value / cpu["value"], 1)
+    out["floors"] = floors
+    flatten_summary(out, floors, matvec, decode)
     print(json.dumps(out), flush=True)
     for l in layers:
         l.release()

@@ -394,6 +394,52 @@ pk_hip_status pk_hip_expf_block_sums(pk_hip_ctx* ctx, const uint32_t* libm_expf_
                                      uint32_t block_size, uint32_t n_blocks, uint64_t* sums,
                                      char* error_buffer, size_t error_capacity);
 
+/* The fast decode step's residual add + RMSNorm kernel (no counterpart
+ * name in the reference; it computes the runner's `hidden += delta`
+ * followed by rms_norm(hidden, w), src/qwen3_moe_runner.cpp:630,692 and
+ * src/rms_norm.cpp:9-27, for each of `rows` rows of n values): hidden_out =
+ * hidden + delta (delta may be NULL), bit for bit; out = (hidden_out *
+ * scale) * w with scale = 1 / sqrt(sum / n + eps), the sum of squares
+ * reassociated as a block reduction (within FP32 reassociation error of the
+ * reference's serial sum).  Host buffers [rows][n], w [n]. */
+pk_hip_status pk_hip_add_rmsnorm(pk_hip_ctx* ctx, const float* hidden, const float* delta,
+                                 const float* w, uint32_t rows, uint32_t n, float eps,
+                                 float* hidden_out, float* out, char* error_buffer,
+                                 size_t error_capacity);
+
+/* Attention of one layer as the whole-model decode computes it. */
+typedef struct pk_hip_attention_config {
+    uint32_t heads, kv_heads, head_dim;  /* head_dim 64, 128 or 256 */
+    uint32_t capacity;                   /* KV ring positions */
+    float rms_eps, rope_theta;
+    /* 0: the fast mode's kernel (device expf); non-zero: reference order,
+     * which needs the host libm's expf exceptions (as pk_hip_qwen3moe_config) */
+    uint32_t reference_order;
+    const uint32_t* libm_expf_pairs;
+    uint64_t libm_expf_count;
+} pk_hip_attention_config;
+
+/* For positions t = 0 .. steps - 1 in turn, the decode's attention stage of
+ * one layer (src/qwen3_moe_runner.cpp:610-628): rms_norm of every q and k head
+ * (q_norm / k_norm [head_dim]), NeoX RoPE with prepare_qwen_rope's angles
+ * (:141-155), the FP16 KvCache::append of k and v and KvCache::attend over
+ * the last `capacity` positions (src/kv_cache.cpp:131-294).  q / out
+ * [steps][heads * head_dim], k / v [steps][kv_heads * head_dim] host buffers
+ * (the projections before the head norms). */
+pk_hip_status pk_hip_attention_steps(pk_hip_ctx* ctx, const pk_hip_attention_config* config,
+                                     const float* q_norm, const float* k_norm, uint32_t steps,
+                                     const float* q, const float* k, const float* v, float* out,
+                                     char* error_buffer, size_t error_capacity);
+
+/* A plain streaming read of `bytes` device bytes at `src` on `stream`
+ * (no counterpart in the reference: the measured floor of any kernel that
+ * reads that many bytes from HBM, for the benchmark).  16-byte-aligned src,
+ * bytes a multiple of 16; sink: one device word, written only for one
+ * particular XOR of the data. */
+pk_hip_status pk_hip_read_floor_async(pk_hip_ctx* ctx, const void* src, uint64_t bytes,
+                                      uint32_t* sink, void* stream, char* error_buffer,
+                                      size_t error_capacity);
+
 /* Waits for the context's work (and `stream`, if not NULL) and reports any
  * deferred router error. */
 pk_hip_status pk_hip_sync(pk_hip_ctx* ctx, void* stream, char* error_buffer,

@@ -55,6 +55,11 @@ def _fp(a: np.ndarray):
     return a.ctypes.data_as(_f32p)
 
 
+_ATTENTION_ARGS = [ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_uint32,
+                   ctypes.c_float, ctypes.c_float, _f32p, _f32p, ctypes.c_uint32, _f32p, _f32p,
+                   _f32p, _f32p]
+
+
 class Oracle:
     def __init__(self, kind: str = "port"):
         if kind not in ("port", "reference"):
@@ -73,6 +78,9 @@ class Oracle:
             L.pko_expf_block_sums.restype = None
             L.pko_rms_norm.argtypes = [_f32p, _f32p, ctypes.c_uint64, ctypes.c_uint64, ctypes.c_float,
                                        _f32p]
+            L.pko_add_rms_norm.argtypes = [_f32p, _f32p, _f32p, ctypes.c_uint64, ctypes.c_uint64,
+                                           ctypes.c_float, _f32p]
+            L.pko_attention_steps.argtypes = _ATTENTION_ARGS
             L.pko_linear.argtypes = [ctypes.c_uint32, _u8p, ctypes.c_uint64, ctypes.c_uint64,
                                      ctypes.c_uint64, _f32p, _f32p]
             L.pko_dequantize_row.argtypes = [ctypes.c_uint32, _u8p, ctypes.c_uint64, _f32p,
@@ -94,6 +102,7 @@ class Oracle:
             L.pkref_row_workers.restype = ctypes.c_uint
             L.pkref_rms_norm.argtypes = [_f32p, _f32p, ctypes.c_uint64, ctypes.c_uint64,
                                          ctypes.c_float, _f32p]
+            L.pkref_attention_steps.argtypes = _ATTENTION_ARGS
             L.pkref_tensor_linear.argtypes = [ctypes.c_uint32, ctypes.c_uint64, ctypes.c_uint64,
                                               _u8p, ctypes.c_uint64, _f32p, _f32p]
             L.pkref_tensor_linear_repeat.argtypes = [ctypes.c_uint32, ctypes.c_uint64,
@@ -176,6 +185,38 @@ class Oracle:
         rc = fn(_fp(xx), _fp(ww), rows, n, float(eps), _fp(out))
         if rc:
             raise OracleError(rc, "rms_norm")
+        return out
+
+    def add_rms_norm(self, hidden: np.ndarray, delta, w: np.ndarray, eps: float):
+        """Port only: (hidden + delta, rms_norm(hidden + delta, w)) per row."""
+        h = np.array(hidden, dtype=np.float32, copy=True)
+        rows, n = (1, h.size) if h.ndim == 1 else h.shape
+        d = None if delta is None else np.ascontiguousarray(delta, dtype=np.float32)
+        ww = np.ascontiguousarray(w, dtype=np.float32).reshape(-1)
+        out = np.empty_like(h)
+        rc = self.lib.pko_add_rms_norm(_fp(h), None if d is None else _fp(d), _fp(ww), rows, n,
+                                       float(eps), _fp(out))
+        if rc:
+            raise OracleError(rc, "add_rms_norm")
+        return h, out
+
+    def attention_steps(self, heads: int, kv_heads: int, head_dim: int, capacity: int,
+                        eps: float, theta: float, q_norm, k_norm, q, k, v) -> np.ndarray:
+        """One layer's q/k head norms, RoPE, FP16 KV ring and attention for
+        positions 0 .. steps - 1: out [steps][heads * head_dim]."""
+        qq = np.ascontiguousarray(q, dtype=np.float32)
+        kk = np.ascontiguousarray(k, dtype=np.float32)
+        vv = np.ascontiguousarray(v, dtype=np.float32)
+        steps = qq.shape[0]
+        out = np.zeros((steps, heads * head_dim), np.float32)
+        qn = np.ascontiguousarray(q_norm, dtype=np.float32)
+        kn = np.ascontiguousarray(k_norm, dtype=np.float32)
+        fn = (self.lib.pko_attention_steps if self.kind == "port"
+              else self.lib.pkref_attention_steps)
+        rc = fn(heads, kv_heads, head_dim, capacity, float(eps), float(theta), _fp(qn), _fp(kn),
+                steps, _fp(qq), _fp(kk), _fp(vv), _fp(out))
+        if rc:
+            raise OracleError(rc, "attention_steps")
         return out
 
     def dequantize_row(self, gtype: int, encoded: np.ndarray, count: int) -> np.ndarray:

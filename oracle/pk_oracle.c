@@ -661,3 +661,135 @@ int pko_rms_norm(const float* x, const float* w, uint64_t rows, uint64_t n, floa
     }
     return 0;
 }
+
+/* float_to_half of src/kv_cache.cpp:20-44: binary32 -> binary16, round to
+ * nearest even, NaN kept quiet with payload 0x200, overflow to infinity. */
+static uint16_t float_to_half_rne(float value) {
+    uint32_t bits;
+    memcpy(&bits, &value, 4);
+    const uint16_t sign = (uint16_t)((bits >> 16) & 0x8000u);
+    const uint32_t exponent = (bits >> 23) & 0xffu;
+    uint32_t mantissa = bits & 0x7fffffu;
+    if (exponent == 0xffu) return (uint16_t)(sign | 0x7c00u | (mantissa ? 0x0200u : 0u));
+    int half_exponent = (int)exponent - 127 + 15;
+    if (half_exponent >= 31) return (uint16_t)(sign | 0x7c00u);
+    if (half_exponent <= 0) {
+        if (half_exponent < -10) return sign;
+        mantissa |= 0x800000u;
+        const unsigned shift = (unsigned)(14 - half_exponent);
+        const uint32_t rounding = (1u << (shift - 1)) - 1u + ((mantissa >> shift) & 1u);
+        return (uint16_t)(sign | ((mantissa + rounding) >> shift));
+    }
+    mantissa += 0x0fffu + ((mantissa >> 13) & 1u);
+    if (mantissa & 0x800000u) {
+        mantissa = 0;
+        if (++half_exponent >= 31) return (uint16_t)(sign | 0x7c00u);
+    }
+    return (uint16_t)(sign | ((uint16_t)half_exponent << 10) | (uint16_t)(mantissa >> 13));
+}
+
+/* One layer's attention for positions 0 .. steps - 1, as the runner's token
+ * step does it (src/qwen3_moe_runner.cpp:610-628): rms_norm of every q and k
+ * head with the head norm weights (src/rms_norm.cpp:9-27), NeoX RoPE with the
+ * angles of prepare_qwen_rope (:141-155: angle = pos * powf(theta, -p / half),
+ * cosf, sinf) applied as rope_rotate_f32 (src/simd_kernels.hpp:88-108: a' = a c
+ * - b s, b' = b c + a s over the two halves), KvCache::append in FP16
+ * (src/kv_cache.cpp:131-168) and KvCache::attend (:170-294): per q head the
+ * serial dot with each cached key (decoded from FP16) times 1/sqrt(head_dim),
+ * the maximum, expf(score - max) and their serial sum in window order, then
+ * out += (score / sum) * value in window order.  The ring holds the last
+ * `capacity` positions.  q[t] [heads][head_dim], k[t] / v[t] [kv_heads][head_dim]
+ * are step t's projections before the head norms; out[t] [heads][head_dim]. */
+int pko_attention_steps(uint32_t heads, uint32_t kv_heads, uint32_t head_dim, uint32_t capacity,
+                        float eps, float theta, const float* q_norm, const float* k_norm,
+                        uint32_t steps, const float* q, const float* k, const float* v,
+                        float* out) {
+    if (!heads || !kv_heads || heads % kv_heads || !head_dim || head_dim % 2 || !capacity ||
+        !q_norm || !k_norm || !q || !k || !v || !out)
+        return 1;
+    const uint32_t half = head_dim / 2, group = heads / kv_heads;
+    const uint64_t qd = (uint64_t)heads * head_dim, kd = (uint64_t)kv_heads * head_dim;
+    uint16_t* kc = (uint16_t*)malloc(sizeof(uint16_t) * capacity * kd);
+    uint16_t* vc = (uint16_t*)malloc(sizeof(uint16_t) * capacity * kd);
+    float* qq = (float*)malloc(sizeof(float) * qd);
+    float* kk = (float*)malloc(sizeof(float) * kd);
+    float* cs = (float*)malloc(sizeof(float) * head_dim);
+    float* key = (float*)malloc(sizeof(float) * head_dim);
+    float* val = (float*)malloc(sizeof(float) * head_dim);
+    float* sc = (float*)malloc(sizeof(float) * (uint64_t)capacity * group);
+    float* mx = (float*)malloc(sizeof(float) * group);
+    float* den = (float*)malloc(sizeof(float) * group);
+    int rc = (kc && vc && qq && kk && cs && key && val && sc && mx && den) ? 0 : 2;
+    const float scale = 1.0f / sqrtf((float)head_dim);
+    for (uint32_t t = 0; t < steps && !rc; ++t) {
+        memcpy(qq, q + t * qd, sizeof(float) * qd);
+        memcpy(kk, k + t * kd, sizeof(float) * kd);
+        for (uint32_t h = 0; h < heads; ++h) pko_rms_norm(qq + h * head_dim, q_norm, 1, head_dim, eps, qq + h * head_dim);
+        for (uint32_t h = 0; h < kv_heads; ++h) pko_rms_norm(kk + h * head_dim, k_norm, 1, head_dim, eps, kk + h * head_dim);
+        for (uint32_t p = 0; p < half; ++p) {
+            const float angle = (float)t * powf(theta, -(float)p / (float)half);
+            cs[p] = cosf(angle);
+            cs[half + p] = sinf(angle);
+        }
+        for (uint32_t h = 0; h < heads + kv_heads; ++h) {
+            float* vec = h < heads ? qq + h * head_dim : kk + (h - heads) * head_dim;
+            for (uint32_t i = 0; i < half; ++i) {
+                const float a = vec[i], b = vec[half + i];
+                vec[i] = a * cs[i] - b * cs[half + i];
+                vec[half + i] = b * cs[i] + a * cs[half + i];
+            }
+        }
+        const uint32_t slot_now = t % capacity;
+        for (uint64_t i = 0; i < kd; ++i) {
+            kc[slot_now * kd + i] = float_to_half_rne(kk[i]);
+            vc[slot_now * kd + i] = float_to_half_rne(v[t * kd + i]);
+        }
+        const uint32_t size = t + 1 < capacity ? t + 1 : capacity, first = t + 1 - size;
+        for (uint32_t kh = 0; kh < kv_heads; ++kh) {
+            for (uint32_t g = 0; g < group; ++g) mx[g] = -INFINITY;
+            for (uint32_t i = 0; i < size; ++i) {
+                const uint32_t slot = (first + i) % capacity;
+                for (uint32_t d = 0; d < head_dim; ++d) key[d] = pko_half_to_float(kc[slot * kd + kh * head_dim + d]);
+                for (uint32_t g = 0; g < group; ++g) {
+                    float s = dot_f32(qq + (kh * group + g) * head_dim, key, head_dim);
+                    s *= scale;
+                    sc[g * capacity + i] = s;
+                    mx[g] = mx[g] < s ? s : mx[g];  /* std::max(current, score) */
+                }
+            }
+            for (uint32_t g = 0; g < group; ++g) {
+                float sum = 0.0f;
+                for (uint32_t i = 0; i < size; ++i) {
+                    float* s = sc + g * capacity + i;
+                    *s = expf(*s - mx[g]);
+                    sum += *s;
+                }
+                den[g] = sum;
+                memset(out + t * qd + (kh * group + g) * head_dim, 0, sizeof(float) * head_dim);
+            }
+            for (uint32_t i = 0; i < size; ++i) {
+                const uint32_t slot = (first + i) % capacity;
+                for (uint32_t d = 0; d < head_dim; ++d) val[d] = pko_half_to_float(vc[slot * kd + kh * head_dim + d]);
+                for (uint32_t g = 0; g < group; ++g) {
+                    const float prob = sc[g * capacity + i] / den[g];
+                    float* o = out + t * qd + (kh * group + g) * head_dim;
+                    for (uint32_t d = 0; d < head_dim; ++d) o[d] += prob * val[d];
+                }
+            }
+        }
+    }
+    free(kc); free(vc); free(qq); free(kk); free(cs); free(key); free(val); free(sc); free(mx); free(den);
+    return rc;
+}
+
+/* The fast decode's residual add and RMSNorm as the reference runner does
+ * them (src/qwen3_moe_runner.cpp:630,692 then src/rms_norm.cpp:9-27):
+ * hidden_i += delta_i (FP32), then out = rms_norm(hidden, w, eps).  Rows of
+ * n values; delta may be null (no add). */
+int pko_add_rms_norm(float* hidden, const float* delta, const float* w, uint64_t rows, uint64_t n,
+                     float eps, float* out) {
+    if (!hidden || !w || !out || n == 0) return 1;
+    if (delta)
+        for (uint64_t i = 0; i < rows * n; ++i) hidden[i] += delta[i];
+    return pko_rms_norm(hidden, w, rows, n, eps, out);
+}

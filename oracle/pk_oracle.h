@@ -124,6 +124,24 @@ int pko_rms_norm(const float* x, const float* w, uint64_t rows, uint64_t n, floa
 void pko_expf_block_sums(uint32_t first_bits, uint32_t block_size, uint32_t n_blocks,
                          uint64_t* sums, uint32_t threads);
 
+
+/* One layer's attention for positions 0 .. steps - 1 as the runner's token
+ * step (src/qwen3_moe_runner.cpp:610-628): q/k head rms_norm, NeoX RoPE
+ * (prepare_qwen_rope :141-155, rope_rotate_f32 src/simd_kernels.hpp:88-108),
+ * FP16 KvCache::append and KvCache::attend (src/kv_cache.cpp:131-294) over a
+ * ring of `capacity` positions.  q/out [steps][heads][head_dim], k/v
+ * [steps][kv_heads][head_dim] (projections before the head norms). */
+int pko_attention_steps(uint32_t heads, uint32_t kv_heads, uint32_t head_dim, uint32_t capacity,
+                        float eps, float theta, const float* q_norm, const float* k_norm,
+                        uint32_t steps, const float* q, const float* k, const float* v,
+                        float* out);
+
+/* hidden += delta (FP32, delta may be null), then out = rms_norm(hidden, w)
+ * per row: the runner's residual add followed by its next RMSNorm
+ * (src/qwen3_moe_runner.cpp:630,692; src/rms_norm.cpp:9-27). */
+int pko_add_rms_norm(float* hidden, const float* delta, const float* w, uint64_t rows, uint64_t n,
+                     float eps, float* out);
+
 #ifdef __cplusplus
 }
 #endif

@@ -287,4 +287,44 @@ int pkref_qwen3moe_forward_times(const char* path, const std::uint32_t* prompt,
     }
 }
 
+
+// One layer's attention for positions 0 .. steps - 1 with the reference's own
+// functions, in the order of the runner's token step (:610-628): rms_norm of
+// every q and k head, prepare_qwen_rope / apply_qwen_rope, KvCache::append
+// and KvCache::attend with an FP16 cache of `capacity` positions.
+int pkref_attention_steps(std::uint32_t heads, std::uint32_t kv_heads, std::uint32_t head_dim,
+                          std::uint32_t capacity, float eps, float theta, const float* q_norm,
+                          const float* k_norm, std::uint32_t steps, const float* q,
+                          const float* k, const float* v, float* out) {
+    try {
+        const std::size_t qd = std::size_t{heads} * head_dim, kd = std::size_t{kv_heads} * head_dim;
+        pokitlms::KvCache cache(capacity, kv_heads, head_dim, head_dim,
+                                pokitlms::KvCachePrecision::Float16, heads);
+        std::vector<float> query(qd), key(kd), cosine(head_dim / 2), sine(head_dim / 2);
+        const std::span<const float> qn(q_norm, head_dim), kn(k_norm, head_dim);
+        for (std::uint32_t t = 0; t < steps; ++t) {
+            std::copy_n(q + t * qd, qd, query.begin());
+            std::copy_n(k + t * kd, kd, key.begin());
+            for (std::size_t h = 0; h < heads; ++h) {
+                auto* b = query.data() + h * head_dim;
+                pokitlms::rms_norm(std::span<const float>(b, head_dim), qn,
+                                   std::span<float>(b, head_dim), eps);
+            }
+            for (std::size_t h = 0; h < kv_heads; ++h) {
+                auto* b = key.data() + h * head_dim;
+                pokitlms::rms_norm(std::span<const float>(b, head_dim), kn,
+                                   std::span<float>(b, head_dim), eps);
+            }
+            pokitlms::model::prepare_qwen_rope(t, head_dim, theta, cosine, sine);
+            pokitlms::model::apply_qwen_rope(query, head_dim, head_dim, cosine, sine);
+            pokitlms::model::apply_qwen_rope(key, head_dim, head_dim, cosine, sine);
+            cache.append(t, key.data(), kd, v + t * kd, kd);
+            cache.attend(query.data(), qd, out + t * qd, qd);
+        }
+        return 0;
+    } catch (...) {
+        return status_of_current_exception();
+    }
+}
+
 }  // extern "C"

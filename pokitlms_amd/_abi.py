@@ -32,7 +32,8 @@ EXPORTS = (
     "pk_hip_moe_prefill_async", "pk_hip_qwen3moe_create", "pk_hip_qwen3moe_destroy",
     "pk_hip_qwen3moe_generate", "pk_hip_synth_weight", "pk_hip_matvec_reference_order",
     "pk_hip_weight_download", "pk_hip_moe_decode_noalloc", "pk_hip_dequantize_rows",
-    "pk_hip_expf_block_sums", "pk_hip_rmsnorm",
+    "pk_hip_expf_block_sums", "pk_hip_rmsnorm", "pk_hip_add_rmsnorm", "pk_hip_attention_steps",
+    "pk_hip_read_floor_async",
 )
 
 
@@ -86,6 +87,14 @@ class Qwen3MoeWeights(ctypes.Structure):
                 ("output", ctypes.c_void_p), ("layers", ctypes.POINTER(Qwen3MoeLayer))]
 
 
+class AttentionConfig(ctypes.Structure):
+    _fields_ = [("heads", ctypes.c_uint32), ("kv_heads", ctypes.c_uint32),
+                ("head_dim", ctypes.c_uint32), ("capacity", ctypes.c_uint32),
+                ("rms_eps", ctypes.c_float), ("rope_theta", ctypes.c_float),
+                ("reference_order", ctypes.c_uint32), ("libm_expf_pairs", ctypes.c_void_p),
+                ("libm_expf_count", ctypes.c_uint64)]
+
+
 class GenerationStats(ctypes.Structure):
     _fields_ = [("prefill_ns", ctypes.c_uint64), ("decode_ns", ctypes.c_uint64),
                 ("prompt_tokens", ctypes.c_uint32), ("decode_forwards", ctypes.c_uint32)]
@@ -133,6 +142,13 @@ def lib() -> ctypes.CDLL:
     L.pk_hip_rmsnorm.restype = ctypes.c_int
     L.pk_hip_rmsnorm.argtypes = [vp, vp, vp, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_float, vp,
                                  ctypes.c_char_p, ctypes.c_size_t]
+    L.pk_hip_add_rmsnorm.restype = ctypes.c_int
+    L.pk_hip_add_rmsnorm.argtypes = [vp, vp, vp, vp, u32, u32, ctypes.c_float, vp, vp, cp, sz]
+    L.pk_hip_attention_steps.restype = ctypes.c_int
+    L.pk_hip_attention_steps.argtypes = [vp, ctypes.POINTER(AttentionConfig), vp, vp, u32, vp, vp,
+                                         vp, vp, cp, sz]
+    L.pk_hip_read_floor_async.restype = ctypes.c_int
+    L.pk_hip_read_floor_async.argtypes = [vp, vp, u64, vp, vp, cp, sz]
     L.pk_hip_weight_download.restype = ctypes.c_int
     L.pk_hip_weight_download.argtypes = [vp, vp, u64, ctypes.c_char_p, ctypes.c_size_t]
     L.pk_hip_matvec.restype = ctypes.c_int

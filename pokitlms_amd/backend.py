@@ -342,6 +342,60 @@ class HipBackend:
                                          float(eps), out.ctypes.data, err, _ERRBUF), err)
         return out
 
+    def add_rmsnorm(self, hidden: np.ndarray, delta, w: np.ndarray, eps: float):
+        """The fast decode's residual add + RMSNorm kernel on each row:
+        (hidden + delta, rms_norm(hidden + delta, w)); delta may be None."""
+        h = np.ascontiguousarray(hidden, dtype=np.float32)
+        rows, n = (1, h.size) if h.ndim == 1 else h.shape
+        d = None if delta is None else np.ascontiguousarray(delta, dtype=np.float32)
+        if d is not None and d.size != h.size:
+            raise ValueError("delta must have the hidden rows' shape")
+        w = np.ascontiguousarray(w, dtype=np.float32).reshape(-1)
+        if w.size != n:
+            raise ValueError("weight size must equal the row width")
+        h_out, out = np.empty_like(h), np.empty_like(h)
+        err = ctypes.create_string_buffer(_ERRBUF)
+        _raise(_abi.lib().pk_hip_add_rmsnorm(self.handle, h.ctypes.data,
+                                             None if d is None else d.ctypes.data, w.ctypes.data,
+                                             rows, n, float(eps), h_out.ctypes.data,
+                                             out.ctypes.data, err, _ERRBUF), err)
+        return h_out, out
+
+    def attention_steps(self, heads: int, kv_heads: int, head_dim: int, capacity: int,
+                        eps: float, theta: float, q_norm, k_norm, q, k, v,
+                        reference_order: bool = False, libm_expf_pairs=None) -> np.ndarray:
+        """The decode's attention stage of one layer for positions 0 .. steps-1
+        (pk_hip_attention_steps): out [steps][heads * head_dim]."""
+        qq = np.ascontiguousarray(q, dtype=np.float32)
+        kk = np.ascontiguousarray(k, dtype=np.float32)
+        vv = np.ascontiguousarray(v, dtype=np.float32)
+        steps = qq.shape[0]
+        if qq.shape != (steps, heads * head_dim) or kk.shape != (steps, kv_heads * head_dim) \
+                or vv.shape != kk.shape:
+            raise ValueError("q [steps][heads*head_dim], k and v [steps][kv_heads*head_dim]")
+        qn = np.ascontiguousarray(q_norm, dtype=np.float32)
+        kn = np.ascontiguousarray(k_norm, dtype=np.float32)
+        cfg = _abi.AttentionConfig(heads, kv_heads, head_dim, capacity, eps, theta,
+                                   1 if reference_order else 0)
+        pairs = None
+        if reference_order and libm_expf_pairs is not None:
+            pairs = np.ascontiguousarray(libm_expf_pairs, dtype=np.uint32)
+            cfg.libm_expf_pairs = pairs.ctypes.data
+            cfg.libm_expf_count = pairs.shape[0]
+        out = np.empty((steps, heads * head_dim), np.float32)
+        err = ctypes.create_string_buffer(_ERRBUF)
+        _raise(_abi.lib().pk_hip_attention_steps(self.handle, ctypes.byref(cfg), qn.ctypes.data,
+                                                 kn.ctypes.data, steps, qq.ctypes.data,
+                                                 kk.ctypes.data, vv.ctypes.data, out.ctypes.data,
+                                                 err, _ERRBUF), err)
+        return out
+
+    def read_floor_async(self, src_ptr: int, nbytes: int, sink_ptr: int, stream) -> None:
+        """A plain streaming read of nbytes device bytes (the HBM floor)."""
+        err = ctypes.create_string_buffer(_ERRBUF)
+        _raise(_abi.lib().pk_hip_read_floor_async(self.handle, src_ptr, nbytes, sink_ptr, stream,
+                                                  err, _ERRBUF), err)
+
     def expf_block_sums(self, pairs: np.ndarray, first_bits: int, block_size: int,
                         n_blocks: int) -> np.ndarray:
         """Checksums of the reference-order expf over float bit patterns

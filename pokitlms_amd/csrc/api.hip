@@ -1175,6 +1175,23 @@ pk_hip_status pk_hip_sync(pk_hip_ctx* ctx, void* stream, char* err, size_t cap) 
 // expf_libm: each half holds 1 << bits slots, at most a third of all slots
 // used; the hash multipliers are the first pair from a fixed list with which
 // every insertion settles (deterministic for a given table).
+// prepare_qwen_rope (src/qwen3_moe_runner.cpp:141-155) with this host's libm
+// for positions 0 .. positions - 1: per position cos [head_dim / 2], then sin.
+std::vector<float> rope_table_host(uint32_t positions, uint32_t head_dim, float theta) {
+    const uint32_t half = head_dim / 2;
+    std::vector<float> table(uint64_t(positions) * head_dim);
+    for (uint32_t pos = 0; pos < positions; ++pos) {
+        float* row = table.data() + uint64_t(pos) * head_dim;
+        for (uint32_t p = 0; p < half; ++p) {
+            const float angle = static_cast<float>(pos) *
+                std::pow(theta, -static_cast<float>(p) / static_cast<float>(half));
+            row[p] = std::cos(angle);
+            row[half + p] = std::sin(angle);
+        }
+    }
+    return table;
+}
+
 pk::LibmExpf build_expf_cuckoo(const uint32_t* pairs, uint64_t n, std::vector<uint32_t>& slots) {
     static const uint32_t kMul[] = {0x9E3779B1u, 0x85EBCA77u, 0xC2B2AE3Du, 0x27D4EB2Fu,
                                     0x165667B1u, 0xD3A2646Du, 0xFD7046C5u, 0xB55A4F09u};
@@ -1363,19 +1380,7 @@ pk_hip_status pk_hip_qwen3moe_create(pk_hip_ctx* ctx, const pk_hip_qwen3moe_conf
         m->moe_out.ensure(c.hidden);
         if (!pk::ref_attention_supported(c.head_dim, c.kv_capacity))
             throw Unsupported("attention covers head_dim 64/128/256");
-        // prepare_qwen_rope (src/qwen3_moe_runner.cpp:141-155) with this host's libm,
-        // for every position of the model context
-        const uint32_t half = c.head_dim / 2;
-        std::vector<float> table(uint64_t(c.context) * c.head_dim);
-        for (uint32_t pos = 0; pos < c.context; ++pos) {
-            float* row = table.data() + uint64_t(pos) * c.head_dim;
-            for (uint32_t p = 0; p < half; ++p) {
-                const float angle = static_cast<float>(pos) *
-                    std::pow(c.rope_theta, -static_cast<float>(p) / static_cast<float>(half));
-                row[p] = std::cos(angle);
-                row[half + p] = std::sin(angle);
-            }
-        }
+        const std::vector<float> table = rope_table_host(c.context, c.head_dim, c.rope_theta);
         m->rope_table.ensure(table.size());
         check(hipMemcpy(m->rope_table.ptr, table.data(), table.size() * sizeof(float),
                         hipMemcpyHostToDevice),
@@ -1406,6 +1411,25 @@ pk_hip_status pk_hip_qwen3moe_create(pk_hip_ctx* ctx, const pk_hip_qwen3moe_conf
             }
         }
         check(hipMemsetAsync(m->moe_status.ptr, 0, 4 * sizeof(uint32_t), ctx->stream), "clear status");
+        // fast mode, GGUF-form rows (planar types keep a plane per tensor): each
+        // layer's q, k and v rows are copied back to back, so one launch computes
+        // all three.  Layers may use different attention formats, so the offsets
+        // are a prefix sum of each eligible layer's own 256-byte-rounded size and
+        // the buffer is allocated once, before any copy.
+        std::vector<uint64_t> qkv_off(c.layers, ~0ull);
+        if (!exact) {
+            uint64_t total = 0;
+            for (uint32_t l = 0; l < c.layers; ++l) {
+                const pk_hip_qwen3moe_layer& L = w->layers[l];
+                if (!L.q || !L.k || !L.v || pk::planar_type(L.q->type)) continue;
+                if (L.k->type != L.q->type || L.v->type != L.q->type) continue;
+                if (L.k->row_bytes != L.q->row_bytes || L.v->row_bytes != L.q->row_bytes) continue;
+                const uint64_t bytes = uint64_t(qd + 2 * kd) * L.q->row_bytes + pk::kWeightTailPad;
+                qkv_off[l] = total;
+                total += (bytes + 255) / 256 * 256;
+            }
+            if (total) m->qkv.ensure(total);
+        }
         m->layers.resize(c.layers);
         for (uint32_t l = 0; l < c.layers; ++l) {
             const pk_hip_qwen3moe_layer& L = w->layers[l];
@@ -1436,14 +1460,10 @@ pk_hip_status pk_hip_qwen3moe_create(pk_hip_ctx* ctx, const pk_hip_qwen3moe_conf
             D.k_row = L.k->row_bytes;
             D.v_row = L.v->row_bytes;
             D.o_row = L.o->row_bytes;
-            // fast mode, GGUF-form rows (planar types keep a plane per tensor):
-            // a copy of q, k and v back to back, so one launch computes all three
             D.qkv = nullptr;
-            if (!exact && !pk::planar_type(D.attn_type) && D.k_row == D.q_row && D.v_row == D.q_row) {
+            if (qkv_off[l] != ~0ull) {
                 const uint64_t qb = qd * D.q_row, kb = kd * D.q_row;
-                const uint64_t pitch = (qb + 2 * kb + pk::kWeightTailPad + 255) / 256 * 256;
-                if (l == 0) m->qkv.ensure(pitch * c.layers);
-                uint8_t* dst = m->qkv.ptr + pitch * l;
+                uint8_t* dst = m->qkv.ptr + qkv_off[l];
                 check(hipMemcpyAsync(dst, D.q, qb, hipMemcpyDeviceToDevice, ctx->stream), "copy q rows");
                 check(hipMemcpyAsync(dst + qb, D.k, kb, hipMemcpyDeviceToDevice, ctx->stream), "copy k rows");
                 check(hipMemcpyAsync(dst + qb + kb, D.v, kb, hipMemcpyDeviceToDevice, ctx->stream),
@@ -1717,6 +1737,160 @@ pk_hip_status pk_hip_expf_block_sums(pk_hip_ctx* ctx, const uint32_t* pairs, uin
         }
         slots.release();
         dsums.release();
+    });
+}
+
+pk_hip_status pk_hip_add_rmsnorm(pk_hip_ctx* ctx, const float* hidden, const float* delta,
+                                 const float* w, uint32_t rows, uint32_t n, float eps,
+                                 float* hidden_out, float* out, char* err, size_t cap) {
+    return guarded(ctx, err, cap, [&] {
+        require_usable(ctx);
+        if (!hidden || !w || !hidden_out || !out) throw ArgError("hidden, weight and outputs are required");
+        if (rows == 0) return;
+        if (n == 0) throw ArgError("row width must be non-zero");
+        std::lock_guard lock(ctx->mutex);
+        ctx->set_device();
+        const size_t total = static_cast<size_t>(rows) * n;
+        DeviceBuffer<float> buf;
+        try {
+            // rows of x | delta | out, then w; 16-byte aligned when n % 4 == 0
+            buf.ensure(3 * total + n);
+            float* dx = buf.ptr;
+            float* dd = dx + total;
+            float* dout = dd + total;
+            float* dw = dout + total;
+            check(hipMemcpyAsync(dx, hidden, total * 4, hipMemcpyHostToDevice, ctx->stream), "copy rows");
+            if (delta)
+                check(hipMemcpyAsync(dd, delta, total * 4, hipMemcpyHostToDevice, ctx->stream), "copy delta");
+            check(hipMemcpyAsync(dw, w, n * 4, hipMemcpyHostToDevice, ctx->stream), "copy weight");
+            for (uint32_t r = 0; r < rows; ++r) {
+                const uint64_t o = uint64_t(r) * n;
+                launch_checked(pk::launch_fast_add_rmsnorm(dx + o, delta ? dd + o : nullptr, dw, dout + o,
+                                                           n, eps, ctx->stream),
+                               "add_rmsnorm launch");
+            }
+            check(hipMemcpyAsync(hidden_out, dx, total * 4, hipMemcpyDeviceToHost, ctx->stream), "copy hidden");
+            check(hipMemcpyAsync(out, dout, total * 4, hipMemcpyDeviceToHost, ctx->stream), "copy output");
+            check(hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
+        } catch (...) {
+            (void)hipStreamSynchronize(ctx->stream);
+            buf.release();
+            throw;
+        }
+        buf.release();
+    });
+}
+
+pk_hip_status pk_hip_attention_steps(pk_hip_ctx* ctx, const pk_hip_attention_config* cfg,
+                                     const float* q_norm, const float* k_norm, uint32_t steps,
+                                     const float* q, const float* k, const float* v, float* out,
+                                     char* err, size_t cap) {
+    return guarded(ctx, err, cap, [&] {
+        require_usable(ctx);
+        if (!cfg || !q_norm || !k_norm || !q || !k || !v || !out)
+            throw ArgError("config, norms, projections and output are required");
+        const pk_hip_attention_config& c = *cfg;
+        if (steps == 0) return;
+        if (c.heads == 0 || c.kv_heads == 0 || c.heads % c.kv_heads || c.capacity == 0)
+            throw ArgError("invalid head counts or KV window");
+        if (!(c.rms_eps > 0.0f) || !(c.rope_theta > 0.0f)) throw ArgError("invalid norm epsilon or RoPE base");
+        if (!pk::ref_attention_supported(c.head_dim, c.capacity))
+            throw Unsupported("attention covers head_dim 64/128/256 and windows whose scores fit LDS");
+        if (c.reference_order && c.libm_expf_count && !c.libm_expf_pairs)
+            throw ArgError("libm_expf_pairs: missing table");
+        std::lock_guard lock(ctx->mutex);
+        ctx->set_device();
+        const uint64_t qd = uint64_t(c.heads) * c.head_dim, kd = uint64_t(c.kv_heads) * c.head_dim;
+        const std::vector<float> table = rope_table_host(steps, c.head_dim, c.rope_theta);
+        std::vector<uint32_t> state(4ull * steps, 0u);
+        for (uint32_t t = 0; t < steps; ++t) state[4ull * t] = t;
+        DeviceBuffer<float> fbuf;
+        DeviceBuffer<uint32_t> sbuf, slots;
+        DeviceBuffer<uint16_t> kv;
+        try {
+            const uint64_t nf = 2 * steps * qd + 2 * steps * kd + table.size() + 2ull * c.head_dim;
+            fbuf.ensure(nf);
+            float* dq = fbuf.ptr;
+            float* dk = dq + steps * qd;
+            float* dv = dk + steps * kd;
+            float* datt = dv + steps * kd;
+            float* drope = datt + steps * qd;
+            float* dnorm = drope + table.size();
+            sbuf.ensure(state.size());
+            kv.ensure(2ull * c.capacity * kd);
+            check(hipMemcpyAsync(dq, q, steps * qd * 4, hipMemcpyHostToDevice, ctx->stream), "copy q");
+            check(hipMemcpyAsync(dk, k, steps * kd * 4, hipMemcpyHostToDevice, ctx->stream), "copy k");
+            check(hipMemcpyAsync(dv, v, steps * kd * 4, hipMemcpyHostToDevice, ctx->stream), "copy v");
+            check(hipMemcpyAsync(drope, table.data(), table.size() * 4, hipMemcpyHostToDevice, ctx->stream),
+                  "copy RoPE table");
+            check(hipMemcpyAsync(dnorm, q_norm, c.head_dim * 4, hipMemcpyHostToDevice, ctx->stream), "copy q_norm");
+            check(hipMemcpyAsync(dnorm + c.head_dim, k_norm, c.head_dim * 4, hipMemcpyHostToDevice, ctx->stream),
+                  "copy k_norm");
+            check(hipMemcpyAsync(sbuf.ptr, state.data(), state.size() * 4, hipMemcpyHostToDevice, ctx->stream),
+                  "copy positions");
+            pk::ModelArgs a{};
+            a.heads = c.heads;
+            a.kv_heads = c.kv_heads;
+            a.head_dim = c.head_dim;
+            a.capacity = c.capacity;
+            a.rms_eps = c.rms_eps;
+            a.rope_theta = c.rope_theta;
+            a.attn_scale = 1.0f / std::sqrt(static_cast<float>(c.head_dim));  // KvCache::attend default
+            a.rope_table = drope;
+            a.exact = c.reference_order ? 1u : 0u;
+            if (c.reference_order && c.libm_expf_count) {
+                std::vector<uint32_t> host;
+                a.expf = build_expf_cuckoo(c.libm_expf_pairs, c.libm_expf_count, host);
+                slots.ensure(host.size());
+                check(hipMemcpyAsync(slots.ptr, host.data(), host.size() * 4, hipMemcpyHostToDevice,
+                                     ctx->stream),
+                      "copy expf table");
+                a.expf.slots = slots.ptr;
+            }
+            pk::ModelLayer L{};
+            L.q_norm = dnorm;
+            L.k_norm = dnorm + c.head_dim;
+            L.kcache = kv.ptr;
+            L.vcache = kv.ptr + uint64_t(c.capacity) * kd;
+            for (uint32_t t = 0; t < steps; ++t) {
+                a.state = sbuf.ptr + 4ull * t;
+                a.q = dq + t * qd;
+                a.k = dk + t * kd;
+                a.v = dv + t * kd;
+                a.att = datt + t * qd;
+                launch_checked(c.reference_order ? pk::launch_ref_attention(a, L, ctx->stream)
+                                                 : pk::launch_fast_attention(a, L, ctx->stream),
+                               "attention launch");
+            }
+            check(hipMemcpyAsync(out, datt, steps * qd * 4, hipMemcpyDeviceToHost, ctx->stream), "copy output");
+            check(hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
+        } catch (...) {
+            (void)hipStreamSynchronize(ctx->stream);
+            fbuf.release();
+            sbuf.release();
+            slots.release();
+            kv.release();
+            throw;
+        }
+        fbuf.release();
+        sbuf.release();
+        slots.release();
+        kv.release();
+    });
+}
+
+pk_hip_status pk_hip_read_floor_async(pk_hip_ctx* ctx, const void* src, uint64_t bytes,
+                                      uint32_t* sink, void* stream, char* err, size_t cap) {
+    return guarded(ctx, err, cap, [&] {
+        require_usable(ctx);
+        if (!src || !sink) throw ArgError("source and sink are required");
+        if (bytes == 0 || bytes % 16u || (reinterpret_cast<uintptr_t>(src) & 15u))
+            throw ArgError("the read covers whole 16-byte pieces of a 16-byte aligned source");
+        std::lock_guard lock(ctx->mutex);
+        ctx->set_device();
+        launch_checked(pk::launch_read_floor(static_cast<const uint8_t*>(src), bytes, sink,
+                                             static_cast<hipStream_t>(stream)),
+                       "read floor launch");
     });
 }
 

@@ -162,6 +162,11 @@ struct ModelArgs {
     LibmExpf expf;            // reference order: the host libm's expf exceptions
 };
 bool model_supported(const ModelArgs& a);
+// The fast step's residual add + RMSNorm (one workgroup): x += d (d may be
+// null), out = (x * (1 / sqrt(sum(x^2) / n + eps))) * w with the sum of
+// squares reassociated (a block reduction).
+hipError_t launch_fast_add_rmsnorm(float* x, const float* d, const float* w, float* out, uint32_t n,
+                                   float eps, hipStream_t stream);
 // logits: run the final norm, head and argmax (else only advance the position).
 hipError_t launch_model_step(const ModelArgs& a, const ModelLayer* layers, bool logits,
                              hipStream_t stream);
@@ -279,6 +284,12 @@ hipError_t launch_ref_step(const ModelArgs& a, const ModelLayer* layers, bool lo
 inline uint64_t ref_scratch_floats(uint32_t top_k, uint32_t ffn, uint32_t hidden) {
     return kMaxExperts256 + 2ull * top_k * ffn + static_cast<uint64_t>(top_k) * hidden;
 }
+
+// A plain streaming read of `bytes` bytes (16-byte nontemporal loads spread
+// over the whole chip), the floor any kernel reading that many bytes from HBM
+// meets: the XOR of the data goes to *sink only if it equals a constant
+// (so no load can be dropped), 16-byte aligned src, bytes % 16 == 0.
+hipError_t launch_read_floor(const uint8_t* src, uint64_t bytes, uint32_t* sink, hipStream_t stream);
 
 // Individual stages (timing and tests).
 hipError_t launch_moe_router(const MoeDecodeArgs& a, hipStream_t stream);

@@ -488,6 +488,23 @@ hipError_t launch_synth_fill(uint8_t* dst, uint64_t nbytes, uint64_t key, uint32
     return hipGetLastError();
 }
 
+hipError_t launch_fast_add_rmsnorm(float* x, const float* d, const float* w, float* out, uint32_t n,
+                                   float eps, hipStream_t s) {
+    if (n == 0) return hipErrorInvalidValue;
+    const auto al16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; };
+    const uint32_t ni = (n + 1023u) / 1024u;
+    if (n % 4u == 0 && ni <= 8u && al16(x) && al16(d) && al16(w) && al16(out)) {
+        const dim3 g(1), b(256);
+        if (ni == 1u) hipLaunchKernelGGL(k_add_rmsnorm4<1>, g, b, 0, s, x, d, w, out, n, eps);
+        else if (ni == 2u) hipLaunchKernelGGL(k_add_rmsnorm4<2>, g, b, 0, s, x, d, w, out, n, eps);
+        else if (ni <= 4u) hipLaunchKernelGGL(k_add_rmsnorm4<4>, g, b, 0, s, x, d, w, out, n, eps);
+        else hipLaunchKernelGGL(k_add_rmsnorm4<8>, g, b, 0, s, x, d, w, out, n, eps);
+    } else {
+        hipLaunchKernelGGL(k_add_rmsnorm, dim3(1), dim3(256), 0, s, x, d, w, out, n, eps);
+    }
+    return hipGetLastError();
+}
+
 hipError_t launch_model_step(const ModelArgs& a, const ModelLayer* layers, bool logits,
                              hipStream_t s) {
     hipError_t err = hipSuccess;
@@ -517,24 +534,7 @@ hipError_t launch_model_step(const ModelArgs& a, const ModelLayer* layers, bool 
     const uint32_t qd = a.heads * a.head_dim, kd = a.kv_heads * a.head_dim;
     const float* delta = nullptr;  // the residual the next RMSNorm adds first
     auto norm = [&](const float* d, const float* w) -> hipError_t {
-        const auto al16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; };
-        const uint32_t ni = (a.hidden + 1023u) / 1024u;
-        if (a.hidden % 4u == 0 && ni <= 8u && al16(a.hidden_state) && al16(d) && al16(w) &&
-            al16(a.normed)) {
-            const dim3 g(1), b(256);
-            if (ni == 1u)
-                hipLaunchKernelGGL(k_add_rmsnorm4<1>, g, b, 0, s, a.hidden_state, d, w, a.normed, a.hidden, a.rms_eps);
-            else if (ni == 2u)
-                hipLaunchKernelGGL(k_add_rmsnorm4<2>, g, b, 0, s, a.hidden_state, d, w, a.normed, a.hidden, a.rms_eps);
-            else if (ni <= 4u)
-                hipLaunchKernelGGL(k_add_rmsnorm4<4>, g, b, 0, s, a.hidden_state, d, w, a.normed, a.hidden, a.rms_eps);
-            else
-                hipLaunchKernelGGL(k_add_rmsnorm4<8>, g, b, 0, s, a.hidden_state, d, w, a.normed, a.hidden, a.rms_eps);
-        } else {
-            hipLaunchKernelGGL(k_add_rmsnorm, dim3(1), dim3(256), 0, s, a.hidden_state, d, w, a.normed,
-                               a.hidden, a.rms_eps);
-        }
-        return hipGetLastError();
+        return launch_fast_add_rmsnorm(a.hidden_state, d, w, a.normed, a.hidden, a.rms_eps, s);
     };
     auto matvec = [&](uint32_t type, const uint8_t* W, uint64_t row_bytes, uint32_t rows,
                       uint32_t in, const float* x, float* y) -> hipError_t {

@@ -41,9 +41,12 @@ struct HipLinearOptions {
     // least-recently-used set of at most this many bytes, keyed by tensor
     // name, offset, type and shape.  An entry is reused only when the call's
     // bytes equal the bytes it was uploaded from (a host copy is kept for the
-    // comparison), so a hit never serves stale weights.  0 uploads every
-    // in-memory tensor for its call and releases it.
-    std::size_t transient_cache_bytes = std::size_t{1} << 30;
+    // comparison: the set costs up to this many bytes of host memory as well
+    // as of device memory), so a hit never serves stale weights.  0 (the
+    // default, as the Vulkan backend, which keeps no copy) uploads every
+    // in-memory tensor for its call and releases it; runners that hand over
+    // the same expert slices repeatedly opt in.
+    std::size_t transient_cache_bytes = 0;
 };
 
 // Counters in the style of VulkanLinearStats (vulkan_linear.hpp:41-67).

@@ -99,9 +99,10 @@ class Qwen3MoeModel:
         self.handle = h.value
 
     # ---- construction ---------------------------------------------------------------
-    @classmethod
-    def synthetic(cls, backend: HipBackend, shape: SM.Qwen3MoeShape, seed: int,
-                  reference_order: bool = True) -> "Qwen3MoeModel":
+    @staticmethod
+    def synthetic_weights(backend: HipBackend, shape: SM.Qwen3MoeShape,
+                          seed: int) -> dict[str, Weight]:
+        """Every tensor of the seeded model, generated in HBM, by GGUF name."""
         weights = {}
         L = _abi.lib()
         try:
@@ -114,6 +115,17 @@ class Qwen3MoeModel:
                                              _ERRBUF), err)
                 weights[name] = Weight(backend, h.value, gtype, inn, out, ne,
                                        gguf.payload_bytes(gtype, dims))
+            return weights
+        except BaseException:
+            for w in weights.values():
+                w.release()
+            raise
+
+    @classmethod
+    def synthetic(cls, backend: HipBackend, shape: SM.Qwen3MoeShape, seed: int,
+                  reference_order: bool = True) -> "Qwen3MoeModel":
+        weights = cls.synthetic_weights(backend, shape, seed)
+        try:
             return cls(backend, shape, weights, reference_order)
         except BaseException:
             for w in weights.values():

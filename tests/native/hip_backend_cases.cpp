@@ -378,9 +378,10 @@ void file_reload_cases(HipLinearBackend& hip) {
     report(ok, "file_reload", d);
 }
 
-// In-memory tensors: a repeat with the same bytes is served from the LRU set;
-// the same name, offset and shape with different bytes is uploaded again.
-void transient_cache_cases(HipLinearBackend& hip) {
+// In-memory tensors: with the LRU set opted in, a repeat with the same bytes is
+// served from it and the same name, offset and shape with different bytes is
+// uploaded again; by default (no set, as the Vulkan backend) every call uploads.
+void transient_cache_round(HipLinearBackend& hip, bool opted_in) {
     Rng g(0x5eed0015);
     const std::size_t rows = 48, in = 1024;
     std::vector<float> x(in), cpu(rows), gpu(rows);
@@ -408,11 +409,24 @@ void transient_cache_cases(HipLinearBackend& hip) {
         ok = ok && e.harness_ok && e.normwise <= 1e-4;
     }
     const auto after = hip.stats();
-    ok = ok && after.transient_hits == before.transient_hits + 1 &&
-         after.transient_uploads == before.transient_uploads + 2;
+    const std::uint64_t hits = opted_in ? 1 : 0, uploads = opted_in ? 2 : 3;
+    ok = ok && after.transient_hits == before.transient_hits + hits &&
+         after.transient_uploads == before.transient_uploads + uploads &&
+         (opted_in || after.transient_bytes == 0);
     char d[160];
-    std::snprintf(d, sizeof d, "Q5_K in-memory: 2 uploads, 1 hit, max_normwise=%.3g", worst);
-    report(ok, "transient_cache", d);
+    std::snprintf(d, sizeof d, "Q5_K in-memory, %s: %llu uploads, %llu hits, max_normwise=%.3g",
+                  opted_in ? "LRU set of 1 GiB" : "default (no set)",
+                  static_cast<unsigned long long>(uploads), static_cast<unsigned long long>(hits),
+                  worst);
+    report(ok, opted_in ? "transient_cache" : "transient_default", d);
+}
+
+void transient_cache_cases(HipLinearBackend& hip) {
+    transient_cache_round(hip, false);
+    HipLinearOptions options;
+    options.transient_cache_bytes = std::size_t{1} << 30;
+    HipLinearBackend cached(options);
+    transient_cache_round(cached, true);
 }
 
 // The reference runner driven through the backend (tests/vulkan_linear_test.cpp:9-36):

@@ -140,6 +140,50 @@ def test_full_model_fast_kernels_diverge_only_at_a_near_tie(hip, mg):
     assert gap <= 2.0 * err, (d, gap, err)
 
 
+def _generate_borrowed(hip, shape, weights, prompt, n_new, reference_order):
+    """generate() on a model over weights it does not own (they stay alive)."""
+    from pokitlms_amd import _abi
+    from pokitlms_amd.model import Qwen3MoeModel
+    model = Qwen3MoeModel(hip, shape, weights, reference_order)
+    try:
+        return model.generate(prompt, n_new, want_logits=True)
+    finally:
+        _abi.lib().pk_hip_qwen3moe_destroy(model.handle)
+        model.handle, model.weights = None, {}
+
+
+@pytest.mark.parametrize("first,second", ((S.Q5_K, S.Q4_K), (S.Q4_K, S.Q5_K),
+                                          (S.Q6_K, S.Q4_K), (S.Q4_K, S.Q6_K)))
+def test_fast_mode_layers_with_different_attention_formats(hip, first, second):
+    """Each layer may store its attention weights in its own format (one format
+    within a layer).  The fast kernels' fused q/k/v copies are laid out per
+    layer by each layer's own size (a larger-block or a planar format in layer
+    0 must not size or skip the later layers' copies), so the fast logits stay
+    within the fast kernels' tolerance of the reference-order logits of the
+    same mixed model, whose matvecs read the tensors themselves."""
+    from pokitlms_amd.model import Qwen3MoeModel
+    shapes = [SM.Qwen3MoeShape(layers=2, vocab=4096, experts=16, top_k=4, context=1024,
+                               attn_type=t) for t in (first, second)]
+    sets = [Qwen3MoeModel.synthetic_weights(hip, m, 71) for m in shapes]
+    try:
+        mixed = dict(sets[0])
+        for name in ("attn_q", "attn_k", "attn_v", "attn_output"):
+            key = f"blk.1.{name}.weight"
+            mixed[key] = sets[1][key]
+        prompt = SM.prompt_tokens(71, 24, 4096)
+        tr, lr, _ = _generate_borrowed(hip, shapes[0], mixed, prompt, 4, True)
+        tf, lf, _ = _generate_borrowed(hip, shapes[0], mixed, prompt, 4, False)
+    finally:
+        for ws in sets:
+            for w in ws.values():
+                w.release()
+    err = normwise_rel(lf, lr)
+    say("attention formats", S.TYPE_NAMES[first], S.TYPE_NAMES[second], "fast vs reference order",
+        err, "tokens", tf, tr)
+    assert err <= 1e-3, err
+    assert tf[0] == tr[0]
+
+
 def test_gguf_file_loads_like_the_generator(hip, tmp_path):
     """A GGUF file written by synth_model and loaded through the GGUF reader
     decodes to the same tokens and logits, bit for bit, as the model generated

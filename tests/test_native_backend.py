@@ -58,6 +58,6 @@ def test_native_backend_cases():
     assert sum(l.startswith("PASS try_linear_unsupported") for l in lines) == 1
     assert sum(l.startswith("PASS moe_block_parity") for l in lines) == 2
     assert sum(l.startswith("PASS moe35_block_parity") for l in lines) == 1
-    for name in ("file_reload", "transient_cache", "expert_cache_stats"):
+    for name in ("file_reload", "transient_cache", "transient_default", "expert_cache_stats"):
         assert sum(l.startswith("PASS " + name) for l in lines) == 1, name
     assert sum(l.startswith("PASS runner_parity") for l in lines) == 2

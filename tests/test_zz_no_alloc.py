@@ -24,6 +24,9 @@ def _run(hip, handles, x, noalloc):
     IDS = torch.full((k,), -1, dtype=torch.int32, device=dev)
     P = torch.full((k,), float("nan"), device=dev)
     fn = hip.moe_decode_noalloc if noalloc else hip.moe_decode_async
+    # the fills above run on torch's stream, the call on the library's: let
+    # them land first so a late fill cannot overwrite the call's outputs
+    torch.cuda.synchronize()
     fn(handles, X.data_ptr(), Y.data_ptr(), IDS.data_ptr(), P.data_ptr())
     hip.sync()
     torch.cuda.synchronize()
