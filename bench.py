@@ -52,6 +52,8 @@ def parse():
     ap.add_argument("--no-decode", action="store_true", help="skip the whole-model decode leg")
     ap.add_argument("--no-matvec", action="store_true", help="skip the C1/C2 matvec leg")
     ap.add_argument("--no-floor", action="store_true", help="skip the plain-read floor leg")
+    ap.add_argument("--timeline", action="store_true",
+                    help="only the per-phase timeline of a step (prints JSON and a table)")
     ap.add_argument("--matvec-reps", type=int, default=10)
     ap.add_argument("--decode-cpu-full", action="store_true",
                     help="only time the reference CPU runner on the full 48-layer model")
@@ -647,6 +649,58 @@ def cpu_baseline(seconds: float):
     }
 
 
+TRACE_SLOTS = {"router": ("start", "inputs in", "done"),
+               "gate_up": ("start", "ranked", "routes shared", "loads issued", "done"),
+               "down": ("start", "loads issued", "dots done", "partials shared", "done")}
+
+
+def timeline_leg(torch, hip, step_args, stream, steps: int = 30, reps: int = 7):
+    """Per-phase times of one MoE-layer step from the kernels' own stamps
+    (pk_hip_moe_decode_traced_async: the 100 MHz s_memrealtime counter read by
+    every wave at fixed points).  A graph of `steps` traced steps (the timed
+    run's layers and tokens) is replayed `reps` times; the trace then holds the
+    last step, whose phases are given in microseconds after the first router
+    wave's start: the 10th percentile, median and 90th percentile over the
+    kernel's waves, pooled over the replays."""
+    import numpy as np
+    from pokitlms_amd import _abi
+    dev = torch.device("cuda:0")
+    trace = torch.zeros(_abi.TRACE_WORDS, dtype=torch.int64, device=dev)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=stream):
+        cs = torch.cuda.current_stream().cuda_stream
+        for i in range(steps):
+            layer, x, y, ids, p = step_args(i)
+            hip.moe_decode_traced_async(layer, x, y, ids, p, trace.data_ptr(), cs)
+    pooled = {k: [[] for _ in v] for k, v in TRACE_SLOTS.items()}
+    for _ in range(reps):
+        trace.zero_()
+        with torch.cuda.stream(stream):
+            g.replay()
+        torch.cuda.synchronize()
+        t = trace.cpu().numpy().reshape(3, 8192, 8)
+        t0 = t[0, :, 0][t[0, :, 0] > 0].min()
+        for k, (name, slots) in enumerate(TRACE_SLOTS.items()):
+            live = t[k, :, 0] > 0
+            for j in range(len(slots)):
+                pooled[name][j].extend(((t[k, live, j] - t0) / 100.0).tolist())
+    out = {}
+    for name, slots in TRACE_SLOTS.items():
+        out[name] = {slot: [round(float(np.percentile(v, q)), 2) for q in (10, 50, 90)]
+                     for slot, v in zip(slots, pooled[name])}
+        out[name]["waves"] = len(pooled[name][0]) // reps
+    return out
+
+
+def timeline_markdown(tl) -> str:
+    rows = ["| Kernel | Point | p10 µs | median µs | p90 µs |", "|---|---|---:|---:|---:|"]
+    for name, slots in TRACE_SLOTS.items():
+        for slot in slots:
+            a, b, c = tl[name][slot]
+            rows.append(f"| {name} ({tl[name]['waves']} waves) | {slot} | {a:.2f} | {b:.2f} | {c:.2f} |")
+    return "\n".join(rows)
+
+
 def flatten_summary(out, floors, matvec, decode):
     """The other configs' headline figures as flat scalar fields of the
     `roofline` and `cpu_baseline` objects (readers that keep only scalar
@@ -727,10 +781,26 @@ def main():
     stream = torch.cuda.Stream()
     torch.cuda.synchronize()
 
-    def step(i, s):
+    def step_args(i):
         t = i % args.tokens
-        hip.moe_decode_async(layers[i % args.layers], X[t].data_ptr(), Y[t].data_ptr(),
-                             IDS[t].data_ptr(), P[t].data_ptr(), s)
+        return layers[i % args.layers], X[t].data_ptr(), Y[t].data_ptr(), IDS[t].data_ptr(), \
+            P[t].data_ptr()
+
+    def step(i, s):
+        hip.moe_decode_async(*step_args(i), s)
+
+    if args.timeline:
+        with torch.cuda.stream(stream):
+            for i in range(args.warmup):
+                step(i, stream.cuda_stream)
+        hip.sync(stream.cuda_stream)
+        tl = timeline_leg(torch, hip, step_args, stream)
+        print(timeline_markdown(tl), file=sys.stderr, flush=True)
+        print(json.dumps({"timeline": tl}), flush=True)
+        for l in layers:
+            l.release()
+        hip.close()
+        return
 
     with torch.cuda.stream(stream):
         s = stream.cuda_stream

@@ -193,6 +193,22 @@ pk_hip_status pk_hip_moe_decode_async(pk_hip_ctx* ctx, const pk_hip_moe_layer* l
                                       uint32_t* device_ids, float* device_probs, void* stream,
                                       char* error_buffer, size_t error_capacity);
 
+/* pk_hip_moe_decode_async that also records its phase times (no
+ * counterpart in the reference; a trace of the reference runner's MoE block
+ * step for performance work): every wave's lane 0 reads the 100 MHz
+ * s_memrealtime counter at fixed points of each kernel into `device_trace`,
+ * PK_HIP_TRACE_WORDS uint64 words, word (kernel * 8192 + wave) * 8 + slot with
+ * kernel 0 router (slots: start, inputs in, done), 1 gate/up (start, ranked,
+ * routes shared, weight loads issued, done), 2 down (start, loads issued,
+ * dots done, partials shared, done) and wave = workgroup * waves per
+ * workgroup + wave.  Words of waves that do not exist keep their contents. */
+#define PK_HIP_TRACE_WORDS (3u * 8192u * 8u)
+pk_hip_status pk_hip_moe_decode_traced_async(pk_hip_ctx* ctx, const pk_hip_moe_layer* layer,
+                                             const float* device_x, float* device_y,
+                                             uint32_t* device_ids, float* device_probs,
+                                             uint64_t* device_trace, void* stream,
+                                             char* error_buffer, size_t error_capacity);
+
 /* As pk_hip_moe_decode_async, allocating nothing: no counterpart in the
  * reference; for callers that cannot allocate device memory (code under HIP
  * graph capture, tight serving loops, harnesses that forbid hipMalloc).  The

@@ -315,6 +315,17 @@ class HipBackend:
                                                   device_x, device_y, device_ids, device_probs,
                                                   stream or None, err, _ERRBUF), err)
 
+    def moe_decode_traced_async(self, layer: MoeLayerHandles, device_x: int, device_y: int,
+                                device_ids: int, device_probs: int, device_trace: int,
+                                stream: int = 0) -> None:
+        """moe_decode_async that records its phase times into device_trace
+        (_abi.TRACE_WORDS uint64 words; layout in include/pokit_hip.h)."""
+        err = ctypes.create_string_buffer(_ERRBUF)
+        _raise(_abi.lib().pk_hip_moe_decode_traced_async(self.handle, ctypes.byref(layer.desc),
+                                                         device_x, device_y, device_ids,
+                                                         device_probs, device_trace,
+                                                         stream or None, err, _ERRBUF), err)
+
     def dequantize_rows(self, w: Weight, first_row: int = 0, rows: int | None = None,
                         expert: int | None = None) -> np.ndarray:
         """Rows of a resident weight as FP32 (the reference's

@@ -483,9 +483,11 @@ MoeScratch context_scratch(pk_hip_ctx* c, const MoeShape& m, uint32_t top_k) {
 
 void enqueue_moe(pk_hip_ctx* c, const pk_hip_moe_layer* L, const MoeShape& m, const float* dx,
                  float* dy, uint32_t* dids, float* dprobs, hipStream_t s,
-                 const pk_hip_moe35_layer* shared = nullptr, const MoeScratch* scratch = nullptr) {
+                 const pk_hip_moe35_layer* shared = nullptr, const MoeScratch* scratch = nullptr,
+                 uint64_t* trace = nullptr) {
     const MoeScratch sc = scratch ? *scratch : context_scratch(c, m, L->top_k);
     pk::MoeDecodeArgs a{};
+    a.trace = trace;
     if (shared) {
         a.variant = 1;
         a.shared_router = reinterpret_cast<const float*>(shared->shared_router->dptr);
@@ -862,6 +864,22 @@ pk_hip_status pk_hip_moe_decode_async(pk_hip_ctx* ctx, const pk_hip_moe_layer* l
             check(hipStreamSynchronize(s), "hipStreamSynchronize");
             collect_timing_moe(ctx);
         }
+    });
+}
+
+pk_hip_status pk_hip_moe_decode_traced_async(pk_hip_ctx* ctx, const pk_hip_moe_layer* layer,
+                                             const float* dx, float* dy, uint32_t* dids,
+                                             float* dprobs, uint64_t* dtrace, void* stream,
+                                             char* err, size_t cap) {
+    return guarded(ctx, err, cap, [&] {
+        require_usable(ctx);
+        if (!dx || !dy || !dids || !dprobs || !dtrace) throw ArgError("device buffers are required");
+        std::lock_guard lock(ctx->mutex);
+        const MoeShape m = check_decode_layer(ctx, layer);
+        ctx->set_device();
+        hipStream_t s = stream ? static_cast<hipStream_t>(stream) : ctx->stream;
+        const CaptureScope capture(s);
+        enqueue_moe(ctx, layer, m, dx, dy, dids, dprobs, s, nullptr, nullptr, dtrace);
     });
 }
 

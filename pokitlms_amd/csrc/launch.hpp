@@ -59,7 +59,17 @@ struct MoeDecodeArgs {
     double* row_bound;       // [n_experts + variant]
     float* act;              // [top_k + variant][ffn]
     uint32_t* status;        // [4]: error flag, serial-fallback count, candidates, spare
+    // optional phase times (null: off): see kTraceWaves
+    uint64_t* trace;
 };
+
+// Phase times of a traced decode step: the 100 MHz s_memrealtime counter
+// read by lane 0 of every wave at fixed points, trace[(kernel * kTraceWaves
+// + wave) * kTraceSlots + slot] with kernel 0 router, 1 gate/up, 2 down and
+// wave = blockIdx.x * (waves per workgroup) + wave in the workgroup.
+constexpr uint32_t kTraceWaves = 8192;
+constexpr uint32_t kTraceSlots = 8;
+constexpr uint64_t kTraceWords = 3ull * kTraceWaves * kTraceSlots;
 
 bool moe_decode_supported(uint32_t gate_type, uint32_t up_type, uint32_t down_type,
                           uint32_t hidden, uint32_t ffn, uint32_t n_experts, uint32_t top_k,

@@ -48,6 +48,7 @@ constexpr uint32_t kDownPasses = 2;    // row passes per down workgroup
 
 template <int C>  // hidden = 256 * C: 4 * C consecutive products per lane
 __global__ __launch_bounds__(64) void k_router(MoeDecodeArgs a) {
+    trace_stamp(a.trace, 0, 0);
     const uint32_t e = blockIdx.x;  // row n_experts: the shared expert's gate (variant 1)
     const uint32_t lane = threadIdx.x;
     const float* row = e < a.n_experts ? a.router + static_cast<uint64_t>(e) * a.hidden : a.shared_router;
@@ -81,6 +82,7 @@ __global__ __launch_bounds__(64) void k_router(MoeDecodeArgs a) {
         router_lane_load<C>(a.x, lane, x);
         __builtin_amdgcn_sched_barrier(0);  // every load out before the first is waited for
     }
+    trace_stamp(a.trace, 0, 1);
     RouterLane<C> r;
     double total, bound;
     router_lane_sums<C>(w, x, r);
@@ -89,6 +91,7 @@ __global__ __launch_bounds__(64) void k_router(MoeDecodeArgs a) {
         a.row_sum[e] = total;
         a.row_bound[e] = bound;
     }
+    trace_stamp(a.trace, 0, 2);
 }
 
 // ---------------------------------------------------------------------------
@@ -107,6 +110,7 @@ __global__ __launch_bounds__(256) void k_gate_up(MoeDecodeArgs a, uint32_t units
     extern __shared__ __attribute__((aligned(16))) float xs[];  // [hidden]
     __shared__ FallbackShared<128> fb;
     __shared__ SharedRoutes sr;
+    trace_stamp(a.trace, 1, 0);
     const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
     const bool first_wave = blockIdx.x == 0 && wave == 0;
     // x and (wave 0) the routing data go out together; x is stored first
@@ -149,7 +153,9 @@ __global__ __launch_bounds__(256) void k_gate_up(MoeDecodeArgs a, uint32_t units
             sr.lo_min_sel = w.lo_min_sel;
         }
     }
+    trace_stamp(a.trace, 1, 1);
     __syncthreads();
+    trace_stamp(a.trace, 1, 2);
     const uint32_t state = sr.state;  // uniform
     if (state == 2u) {
         if (first_wave) flag_router_error(a);
@@ -195,6 +201,7 @@ __global__ __launch_bounds__(256) void k_gate_up(MoeDecodeArgs a, uint32_t units
             unit_load<T, UB>(ur, pos[k], ru[q][k]);
         }
     }
+    trace_stamp(a.trace, 1, 3);
     UnitX<T, UB, 1> ux[NU];
 #pragma unroll
     for (int k = 0; k < NU; ++k) load_unit_x<T, UB, 1>(xs, 0, pos[k], valid[k], ux[k]);
@@ -217,6 +224,7 @@ __global__ __launch_bounds__(256) void k_gate_up(MoeDecodeArgs a, uint32_t units
         if (live && ul == G - 1u)
             a.act[item[q]] = a.variant ? silu(gs) * us : (gs / (1.0f + expf(-gs))) * us;
     }
+    trace_stamp(a.trace, 1, 4);
 }
 
 
@@ -230,6 +238,7 @@ __global__ __launch_bounds__(64 * (kMaxTopK + (SHARED ? 1 : 0))) void k_down(Moe
                                                                             uint32_t units,
                                                                             uint32_t glog2) {
     extern __shared__ float part[];  // [top_k + variant][kDownPasses * RPP]
+    trace_stamp(a.trace, 2, 0);
     const uint32_t lane = threadIdx.x & 63u, k = threadIdx.x >> 6;
     const uint32_t G = 1u << glog2, RPP = 64u >> glog2;
     const uint32_t sub = lane >> glog2, ul = lane & (G - 1u);
@@ -259,6 +268,7 @@ __global__ __launch_bounds__(64 * (kMaxTopK + (SHARED ? 1 : 0))) void k_down(Moe
 #pragma unroll
         for (int q = 0; q < NU; ++q) unit_load<T, UB>(qr, pos[q], raw[p][q]);
     }
+    trace_stamp(a.trace, 2, 1);
     UnitX<T, UB, 1> ux[NU];
     const float* act = a.act + k * a.ffn;
 #pragma unroll
@@ -279,7 +289,9 @@ __global__ __launch_bounds__(64 * (kMaxTopK + (SHARED ? 1 : 0))) void k_down(Moe
     // variant 1: mixer_output = moe_result + sigmoid(shared gate) * shared output
     // (src/qwen35_runner.cpp:752-761)
     const float shared_scale = SHARED ? sigmoid35(static_cast<float>(a.row_sum[a.n_experts])) : 0.0f;
+    trace_stamp(a.trace, 2, 2);
     __syncthreads();
+    trace_stamp(a.trace, 2, 3);
     for (uint32_t i = threadIdx.x; i < RB; i += blockDim.x) {
         const uint32_t orow = row0 + i;
         if (orow < rows) {
@@ -290,6 +302,7 @@ __global__ __launch_bounds__(64 * (kMaxTopK + (SHARED ? 1 : 0))) void k_down(Moe
             a.y[orow] = y;
         }
     }
+    trace_stamp(a.trace, 2, 4);
 }
 
 uint32_t ceil_div(uint32_t a, uint32_t b) { return (a + b - 1u) / b; }

@@ -34,6 +34,16 @@ __device__ __forceinline__ float sigmoid35(float v) {
 }
 __device__ __forceinline__ float silu(float v) { return v * sigmoid35(v); }
 
+// Phase stamp of a traced step (MoeDecodeArgs::trace; a uniform branch when off).
+__device__ __forceinline__ void trace_stamp(uint64_t* trace, uint32_t kernel, uint32_t slot) {
+    if (trace) {
+        const uint32_t w = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+        const uint64_t t = __builtin_amdgcn_s_memrealtime();
+        if ((threadIdx.x & 63u) == 0u && w < kTraceWaves)
+            trace[(static_cast<uint64_t>(kernel) * kTraceWaves + w) * kTraceSlots + slot] = t;
+    }
+}
+
 // route_experts' sorted-insertion order: larger logit first, then smaller id.
 __device__ __forceinline__ bool key_before(double av, uint32_t aid, double bv, uint32_t bid) {
     return av > bv || (av == bv && aid < bid);
