@@ -185,6 +185,30 @@ pk_hip_status pk_hip_moe_decode(pk_hip_ctx* ctx, const pk_hip_moe_layer* layer, 
                                 float* y, uint32_t* ids, float* probs, char* error_buffer,
                                 size_t error_capacity);
 
+/* The host libm's expf results where they differ from the correctly
+ * rounded exponential, as (input bits, result bits) pairs with increasing
+ * inputs (the file libm_expf.bin the build writes beside the library: "PKEXPF01",
+ * a uint32 count, then the pairs), for the context's reference-order kernels
+ * (pk_hip_moe_decode_reference_order).  count 0 clears the table; without
+ * one, those kernels' expf is the correctly rounded exponential. */
+pk_hip_status pk_hip_set_libm_expf(pk_hip_ctx* ctx, const uint32_t* libm_expf_pairs,
+                                   uint64_t pair_count, char* error_buffer,
+                                   size_t error_capacity);
+
+/* pk_hip_moe_decode in the reference's own operation order (the MoE block of
+ * src/qwen3_moe_runner.cpp:644-691 with route_experts :267-305): the router
+ * logits as linear's serial FP32 sums, route_experts' ranking and FP64
+ * softmax, linear_k / linear_quantized's block-order sums for gate, up and
+ * down, g / (1 + expf(-g)) * u with the host libm's expf (pk_hip_set_libm_expf),
+ * and moe_result += p * expert_output in route order from zero -- bit for bit
+ * the reference's outputs.  Qwen3-MoE layers (scale 1) up to 256 experts,
+ * top-16 and rows of 8192; others return UNSUPPORTED.  Host buffers;
+ * synchronous. */
+pk_hip_status pk_hip_moe_decode_reference_order(pk_hip_ctx* ctx, const pk_hip_moe_layer* layer,
+                                                const float* x, float* y, uint32_t* ids,
+                                                float* probs, char* error_buffer,
+                                                size_t error_capacity);
+
 /* Device-buffer variant, enqueued on `stream` without synchronising.  A
  * router error is reported by the next pk_hip_sync.  Scratch and stream
  * capture as for pk_hip_moe_prefill_async. */

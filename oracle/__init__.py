@@ -37,7 +37,7 @@ def build(reference: bool = True) -> None:
         # the C++ backend parity program links the product library
         hiplib = os.path.join(os.path.dirname(HERE), "pokitlms_amd", "libpokit_hip.so")
         if os.path.exists(hiplib):
-            targets.append("cases")
+            targets += ["cases", "runner"]
     subprocess.run(["make", "-s", "-C", HERE, "-j8", *targets], check=True)
 
 

@@ -33,7 +33,8 @@ EXPORTS = (
     "pk_hip_qwen3moe_generate", "pk_hip_synth_weight", "pk_hip_matvec_reference_order",
     "pk_hip_weight_download", "pk_hip_moe_decode_noalloc", "pk_hip_dequantize_rows",
     "pk_hip_expf_block_sums", "pk_hip_rmsnorm", "pk_hip_add_rmsnorm", "pk_hip_attention_steps",
-    "pk_hip_read_floor_async", "pk_hip_moe_decode_traced_async",
+    "pk_hip_read_floor_async", "pk_hip_moe_decode_traced_async", "pk_hip_set_libm_expf",
+    "pk_hip_moe_decode_reference_order",
 )
 TRACE_WORDS = 3 * 8192 * 8
 
@@ -168,6 +169,11 @@ def lib() -> ctypes.CDLL:
     L.pk_hip_moe_decode_async.restype = ctypes.c_int
     L.pk_hip_moe_decode_async.argtypes = [vp, ctypes.POINTER(MoeLayerDesc), vp, vp, vp, vp, vp,
                                           cp, sz]
+    L.pk_hip_set_libm_expf.restype = ctypes.c_int
+    L.pk_hip_set_libm_expf.argtypes = [vp, vp, u64, cp, sz]
+    L.pk_hip_moe_decode_reference_order.restype = ctypes.c_int
+    L.pk_hip_moe_decode_reference_order.argtypes = [vp, ctypes.POINTER(MoeLayerDesc), fp, fp, up,
+                                                    fp, cp, sz]
     L.pk_hip_moe_decode_traced_async.restype = ctypes.c_int
     L.pk_hip_moe_decode_traced_async.argtypes = [vp, ctypes.POINTER(MoeLayerDesc), vp, vp, vp, vp,
                                                  vp, vp, cp, sz]

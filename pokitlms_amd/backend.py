@@ -315,6 +315,27 @@ class HipBackend:
                                                   device_x, device_y, device_ids, device_probs,
                                                   stream or None, err, _ERRBUF), err)
 
+    def set_libm_expf(self, pairs) -> None:
+        """The host libm's expf exceptions (uint32 [n, 2]) for the reference-order
+        kernels of this context; None or empty clears them."""
+        p = np.ascontiguousarray(pairs if pairs is not None else np.zeros((0, 2)), dtype=np.uint32)
+        err = ctypes.create_string_buffer(_ERRBUF)
+        _raise(_abi.lib().pk_hip_set_libm_expf(self.handle, p.ctypes.data if p.size else None,
+                                               p.size // 2, err, _ERRBUF), err)
+
+    def moe_decode_reference_order(self, layer: MoeLayerHandles, x: np.ndarray):
+        """The MoE block in the reference's operation order: (moe_result,
+        ids, probs), bit for bit the reference's with the libm expf table set."""
+        xx = np.ascontiguousarray(x, dtype=np.float32)
+        y = np.empty(layer.hidden, np.float32)
+        ids = np.empty(layer.top_k, np.uint32)
+        probs = np.empty(layer.top_k, np.float32)
+        err = ctypes.create_string_buffer(_ERRBUF)
+        _raise(_abi.lib().pk_hip_moe_decode_reference_order(
+            self.handle, ctypes.byref(layer.desc), _f32p(xx), _f32p(y),
+            ids.ctypes.data_as(ctypes.POINTER(ctypes.c_uint32)), _f32p(probs), err, _ERRBUF), err)
+        return y, ids, probs
+
     def moe_decode_traced_async(self, layer: MoeLayerHandles, device_x: int, device_y: int,
                                 device_ids: int, device_probs: int, device_trace: int,
                                 stream: int = 0) -> None:

@@ -173,6 +173,11 @@ struct pk_hip_ctx {
     DeviceBuffer<uint32_t> pids, poffsets, ptiles, pperm;
     DeviceBuffer<uint16_t> pxparts, paparts;
     DeviceBuffer<double> prow_sum, prow_bound;
+    // reference-order MoE block: its scratch and the host libm's expf
+    // exceptions (pk_hip_set_libm_expf)
+    DeviceBuffer<float> ref_scratch;
+    DeviceBuffer<uint32_t> expf_slots;
+    pk::LibmExpf expf{nullptr, 0, 0, 0};
     hipEvent_t ev[10] = {};
     int wall_rate_khz = 100000;  // wall_clock64() rate
 
@@ -638,6 +643,8 @@ void pk_hip_destroy(pk_hip_ctx* c) {
     c->paparts.release();
     c->prow_sum.release();
     c->prow_bound.release();
+    c->ref_scratch.release();
+    c->expf_slots.release();
     for (auto& e : c->ev)
         if (e) (void)hipEventDestroy(e);
     if (c->stream) (void)hipStreamDestroy(c->stream);
@@ -845,6 +852,98 @@ pk_hip_status pk_hip_moe_decode(pk_hip_ctx* ctx, const pk_hip_moe_layer* layer, 
               "copy probabilities");
         sync_and_check(ctx, ctx->stream);
         collect_timing_moe(ctx);
+    });
+}
+
+pk::LibmExpf build_expf_cuckoo(const uint32_t* pairs, uint64_t n, std::vector<uint32_t>& slots);
+
+pk_hip_status pk_hip_set_libm_expf(pk_hip_ctx* ctx, const uint32_t* pairs, uint64_t count,
+                                   char* err, size_t cap) {
+    return guarded(ctx, err, cap, [&] {
+        require_usable(ctx);
+        if (count && !pairs) throw ArgError("libm_expf_pairs: missing table");
+        if (count > (1ull << 24)) throw ArgError("libm_expf_pairs: oversized table");
+        for (uint64_t i = 0; i < count; ++i)
+            if (pairs[2 * i] == pk::kExpfEmpty || (i && pairs[2 * i] <= pairs[2 * i - 2]))
+                throw ArgError("libm_expf_pairs: inputs not increasing");
+        std::lock_guard lock(ctx->mutex);
+        ctx->set_device();
+        check(hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
+        ctx->expf_slots.release();
+        ctx->expf = pk::LibmExpf{nullptr, 0, 0, 0};
+        if (!count) return;
+        std::vector<uint32_t> host;
+        const pk::LibmExpf t = build_expf_cuckoo(pairs, count, host);
+        ctx->expf_slots.ensure(host.size());
+        check(hipMemcpy(ctx->expf_slots.ptr, host.data(), host.size() * 4, hipMemcpyHostToDevice),
+              "copy expf table");
+        ctx->expf = t;
+        ctx->expf.slots = ctx->expf_slots.ptr;
+    });
+}
+
+pk_hip_status pk_hip_moe_decode_reference_order(pk_hip_ctx* ctx, const pk_hip_moe_layer* layer,
+                                                const float* x, float* y, uint32_t* ids,
+                                                float* probs, char* err, size_t cap) {
+    return guarded(ctx, err, cap, [&] {
+        require_usable(ctx);
+        if (!x || !y || !ids || !probs) throw ArgError("input and output buffers are required");
+        std::lock_guard lock(ctx->mutex);
+        const MoeShape m = check_layer(ctx, layer);
+        pk::MoeDecodeArgs a{};
+        a.router = reinterpret_cast<const float*>(layer->router->dptr);
+        a.gate = layer->gate->dptr;
+        a.up = layer->up->dptr;
+        a.down = layer->down->dptr;
+        a.gate_type = layer->gate->type;
+        a.up_type = layer->up->type;
+        a.down_type = layer->down->type;
+        a.gate_slice = layer->gate->slice_pitch;
+        a.up_slice = layer->up->slice_pitch;
+        a.down_slice = layer->down->slice_pitch;
+        a.gate_row = layer->gate->row_bytes;
+        a.up_row = layer->up->row_bytes;
+        a.down_row = layer->down->row_bytes;
+        a.hidden = m.hidden;
+        a.ffn = m.ffn;
+        a.n_experts = m.experts;
+        a.top_k = layer->top_k;
+        a.normalize = layer->normalize ? 1u : 0u;
+        a.scale = layer->scale;
+        if (a.scale != 1.0f || !pk::ref_moe_block_supported(a))
+            throw Unsupported("MoE shape not covered by the reference-order kernels");
+        ctx->set_device();
+        ctx->x.ensure(m.hidden);
+        ctx->y.ensure(m.hidden);
+        ctx->ids.ensure(16);
+        ctx->probs.ensure(16);
+        ctx->ref_scratch.ensure(pk::ref_scratch_floats(a.top_k, m.ffn, m.hidden));
+        a.x = ctx->x.ptr;
+        a.y = ctx->y.ptr;
+        a.ids = ctx->ids.ptr;
+        a.probs = ctx->probs.ptr;
+        a.status = status_words(ctx);
+        check(hipMemcpyAsync(ctx->x.ptr, x, m.hidden * sizeof(float), hipMemcpyHostToDevice,
+                             ctx->stream),
+              "copy input");
+        launch_checked(pk::launch_ref_moe_block(a, ctx->ref_scratch.ptr, ctx->expf, ctx->stream),
+                       "reference-order MoE launch");
+        check(hipMemcpyAsync(y, ctx->y.ptr, m.hidden * sizeof(float), hipMemcpyDeviceToHost,
+                             ctx->stream),
+              "copy output");
+        check(hipMemcpyAsync(ids, ctx->ids.ptr, layer->top_k * sizeof(uint32_t),
+                             hipMemcpyDeviceToHost, ctx->stream),
+              "copy ids");
+        check(hipMemcpyAsync(probs, ctx->probs.ptr, layer->top_k * sizeof(float),
+                             hipMemcpyDeviceToHost, ctx->stream),
+              "copy probabilities");
+        sync_and_check(ctx, ctx->stream);
+        ++ctx->stats.moe_decode_calls;
+        ctx->stats.expert_hits += layer->top_k;
+        ctx->stats.weight_bytes += layer->router->nbytes +
+                                   static_cast<uint64_t>(layer->top_k) *
+                                       (layer->gate->slice_bytes + layer->up->slice_bytes +
+                                        layer->down->slice_bytes);
     });
 }
 
@@ -1189,10 +1288,6 @@ pk_hip_status pk_hip_sync(pk_hip_ctx* ctx, void* stream, char* err, size_t cap) 
 // ---------------------------------------------------------------------------
 // Whole-model greedy decode (Qwen3MoeRunner on the device).
 
-// Two-choice cuckoo table of (input bits, libm result bits) for the device's
-// expf_libm: each half holds 1 << bits slots, at most a third of all slots
-// used; the hash multipliers are the first pair from a fixed list with which
-// every insertion settles (deterministic for a given table).
 // prepare_qwen_rope (src/qwen3_moe_runner.cpp:141-155) with this host's libm
 // for positions 0 .. positions - 1: per position cos [head_dim / 2], then sin.
 std::vector<float> rope_table_host(uint32_t positions, uint32_t head_dim, float theta) {
@@ -1210,6 +1305,10 @@ std::vector<float> rope_table_host(uint32_t positions, uint32_t head_dim, float 
     return table;
 }
 
+// Two-choice cuckoo table of (input bits, libm result bits) for the device's
+// expf_libm: each half holds 1 << bits slots, at most a third of all slots
+// used; the hash multipliers are the first pair from a fixed list with which
+// every insertion settles (deterministic for a given table).
 pk::LibmExpf build_expf_cuckoo(const uint32_t* pairs, uint64_t n, std::vector<uint32_t>& slots) {
     static const uint32_t kMul[] = {0x9E3779B1u, 0x85EBCA77u, 0xC2B2AE3Du, 0x27D4EB2Fu,
                                     0x165667B1u, 0xD3A2646Du, 0xFD7046C5u, 0xB55A4F09u};

@@ -1287,6 +1287,20 @@ hipError_t launch_ref_step(const ModelArgs& a, const ModelLayer* layers, bool lo
 
 namespace {
 
+// moe_result = ((0 + p0 * o0) + p1 * o1) + ... in route order
+// (src/qwen3_moe_runner.cpp:652,688-690: the zero-filled result, then
+// moe_result[i] += probability * expert_output[i] per route).
+__global__ __launch_bounds__(256) void k_ref_combine(const float* __restrict__ parts,
+                                                     const float* __restrict__ probs, uint32_t K,
+                                                     uint32_t n, float* __restrict__ y) {
+    const uint32_t i = blockIdx.x * 256u + threadIdx.x;
+    if (i >= n) return;
+    float acc = 0.0f;
+    for (uint32_t r = 0; r < K; ++r)
+        acc = __fadd_rn(acc, __fmul_rn(probs[r], parts[static_cast<uint64_t>(r) * n + i]));
+    y[i] = acc;
+}
+
 __global__ __launch_bounds__(256) void k_expf_block_sums(LibmExpf t, uint32_t first_bits,
                                                          uint32_t block_size,
                                                          unsigned long long* sums) {
@@ -1306,6 +1320,74 @@ __global__ __launch_bounds__(256) void k_expf_block_sums(LibmExpf t, uint32_t fi
 }
 
 }  // namespace
+
+bool ref_moe_block_supported(const MoeDecodeArgs& m) {
+    return m.variant == 0 && m.n_experts >= 1 && m.n_experts <= kMaxExperts256 && m.top_k >= 1 &&
+           m.top_k <= kMaxRefTopK && m.top_k <= m.n_experts &&
+           ref_matvec_supported(T_F32, m.hidden) && ref_matvec_supported(m.gate_type, m.hidden) &&
+           ref_matvec_supported(m.up_type, m.hidden) && ref_matvec_supported(m.down_type, m.ffn) &&
+           m.gate_type != T_F32 && m.up_type != T_F32 && m.down_type != T_F32;
+}
+
+// The MoE block in the reference's order: the router rows, routing and
+// gate/up (with the SwiGLU activations where the pairing covers the width),
+// down, then the route-order combine -- stages 4-6 of launch_ref_step without
+// the RMSNorm, on a caller's normalised x.
+hipError_t launch_ref_moe_block(const MoeDecodeArgs& m, float* scratch, const LibmExpf& expf,
+                                hipStream_t s) {
+    if (!ref_moe_block_supported(m)) return hipErrorInvalidValue;
+    float* rl = scratch;
+    float* g = rl + kMaxExperts256;
+    float* u = g + static_cast<uint64_t>(m.top_k) * m.ffn;
+    float* out = u + static_cast<uint64_t>(m.top_k) * m.ffn;
+    hipError_t err;
+    RefMatvecArgs router{};
+    router.W = reinterpret_cast<const uint8_t*>(m.router);
+    router.row_bytes = static_cast<uint64_t>(m.hidden) * 4u;
+    router.rows = m.n_experts;
+    router.in = m.hidden;
+    router.x = m.x;
+    router.y = rl;
+    if ((err = launch_ref_matvec(T_F32, router, 1, s))) return err;
+    RefMatvecArgs gu{};
+    gu.in = m.hidden;
+    gu.x = m.x;
+    gu.y_stride = m.ffn;
+    gu.route = RefRouteIn{rl, m.n_experts, m.top_k, m.normalize, m.ids, m.probs, m.status};
+    const RefSeg gu_segs[2] = {{m.gate, m.gate_row, m.gate_slice, m.ffn, 0, g},
+                               {m.up, m.up_row, m.up_slice, m.ffn, 0, u}};
+    const bool paired = m.gate_type == m.up_type && ref_gate_up_act_supported(m.gate_type, m.hidden);
+    if (paired) {
+        gu.act = g;
+        gu.expf = expf;
+        if ((err = launch_ref_gate_up_act(m.gate_type, gu, gu_segs[0], gu_segs[1], m.top_k, s)))
+            return err;
+    } else if (m.gate_type == m.up_type) {
+        if ((err = launch_ref_matvec_multi(m.gate_type, gu, gu_segs, 2, m.top_k, s))) return err;
+    } else {
+        if ((err = launch_ref_matvec_multi(m.gate_type, gu, gu_segs, 1, m.top_k, s))) return err;
+        gu.route.logits = nullptr;  // the ids are written by now
+        gu.ids = m.ids;
+        if ((err = launch_ref_matvec_multi(m.up_type, gu, gu_segs + 1, 1, m.top_k, s))) return err;
+    }
+    RefMatvecArgs d{};
+    d.ids = m.ids;
+    d.W = m.down;
+    d.row_bytes = m.down_row;
+    d.slice_bytes = m.down_slice;
+    d.rows = m.hidden;
+    d.in = m.ffn;
+    d.x = g;
+    d.x_up = paired ? nullptr : u;
+    d.x_stride = m.ffn;
+    d.expf = expf;
+    d.y = out;
+    d.y_stride = m.hidden;
+    if ((err = launch_ref_matvec(m.down_type, d, m.top_k, s))) return err;
+    hipLaunchKernelGGL(k_ref_combine, dim3((m.hidden + 255u) / 256u), dim3(256), 0, s, out, m.probs,
+                       m.top_k, m.hidden, m.y);
+    return hipGetLastError();
+}
 
 hipError_t launch_expf_block_sums(const LibmExpf& t, uint32_t first_bits, uint32_t block_size,
                                   uint32_t n_blocks, unsigned long long* sums, hipStream_t s) {

@@ -290,6 +290,14 @@ hipError_t launch_fast_attention(const ModelArgs& a, const ModelLayer& L, hipStr
 // head when logits).
 hipError_t launch_ref_step(const ModelArgs& a, const ModelLayer* layers, bool logits,
                            hipStream_t stream);
+// The MoE block of one token in the reference's operation order (router rows,
+// route_experts, gate/up, SwiGLU with the given expf, down, route-order
+// combine; variant 0 only): m.x normalised input, m.y moe_result, m.ids /
+// m.probs the routes, m.status the non-finite flag; scratch holds
+// ref_scratch_floats(top_k, ffn, hidden) floats.
+bool ref_moe_block_supported(const MoeDecodeArgs& m);
+hipError_t launch_ref_moe_block(const MoeDecodeArgs& m, float* scratch, const LibmExpf& expf,
+                                hipStream_t stream);
 // floats of ModelArgs::ref_scratch for one layer shape
 inline uint64_t ref_scratch_floats(uint32_t top_k, uint32_t ffn, uint32_t hidden) {
     return kMaxExperts256 + 2ull * top_k * ffn + static_cast<uint64_t>(top_k) * hidden;

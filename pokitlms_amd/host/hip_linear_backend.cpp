@@ -12,8 +12,11 @@
 
 #include "pokit_hip.h"
 
+#include <dlfcn.h>
+
 #include <array>
 #include <cstring>
+#include <fstream>
 #include <iterator>
 #include <limits>
 #include <list>
@@ -62,6 +65,30 @@ bool block_aligned(std::uint32_t type, std::uint64_t in) {
     }
 }
 
+// The (input bits, result bits) pairs of a libm_expf.bin file ("PKEXPF01",
+// a uint32 count, then the pairs); an empty path selects the file beside the
+// loaded libpokit_hip.so.
+std::vector<std::uint32_t> read_libm_expf(std::string path) {
+    if (path.empty()) {
+        Dl_info info{};
+        if (!dladdr(reinterpret_cast<const void*>(&pk_hip_create), &info) || !info.dli_fname)
+            throw std::runtime_error("HIP backend: cannot locate libpokit_hip.so");
+        path = info.dli_fname;
+        path = path.substr(0, path.find_last_of('/') + 1) + "libm_expf.bin";
+    }
+    std::ifstream in(path, std::ios::binary);
+    char magic[8] = {};
+    std::uint32_t count = 0;
+    if (!in.read(magic, 8) || std::memcmp(magic, "PKEXPF01", 8) != 0 ||
+        !in.read(reinterpret_cast<char*>(&count), 4))
+        throw std::runtime_error("HIP backend: " + path + " is not an expf exception table");
+    std::vector<std::uint32_t> pairs(2ull * count);
+    if (!in.read(reinterpret_cast<char*>(pairs.data()),
+                 static_cast<std::streamsize>(pairs.size() * 4)))
+        throw std::runtime_error("HIP backend: " + path + " is truncated");
+    return pairs;
+}
+
 struct WeightDeleter {
     void operator()(pk_hip_weight* w) const noexcept { pk_hip_weight_release(w); }
 };
@@ -73,6 +100,7 @@ class HipLinearBackend::Impl {
 public:
     explicit Impl(const HipLinearOptions& options)
         : cache_file_tensors(options.cache_file_tensors),
+          reference_order(options.reference_order),
           transient_budget(options.transient_cache_bytes) {
         pk_hip_options opts{};
         opts.struct_size = sizeof(opts);
@@ -81,6 +109,18 @@ public:
         const auto st = pk_hip_create(options.device_index, &opts, &ctx, err.data(), kErrorCapacity);
         if (st == PK_HIP_STATUS_INVALID_ARGUMENT) throw std::invalid_argument(err.str());
         if (st != PK_HIP_STATUS_OK) throw std::runtime_error("HIP backend: " + err.str());
+        if (reference_order) {
+            try {
+                const auto pairs = read_libm_expf(options.libm_expf_table);
+                const auto ts = pk_hip_set_libm_expf(ctx, pairs.data(), pairs.size() / 2, err.data(),
+                                                     kErrorCapacity);
+                if (ts != PK_HIP_STATUS_OK) throw std::runtime_error("HIP backend: " + err.str());
+            } catch (...) {
+                pk_hip_destroy(ctx);
+                ctx = nullptr;
+                throw;
+            }
+        }
     }
     ~Impl() {
         resident.clear();  // weights before the context that owns them
@@ -211,6 +251,7 @@ public:
 
     pk_hip_ctx* ctx = nullptr;
     bool cache_file_tensors = true;
+    bool reference_order = false;
     std::size_t transient_budget = 0;
     std::size_t transient_held = 0;
     bool failed = false;
@@ -276,8 +317,11 @@ bool HipLinearBackend::try_linear(const model::TensorReader& weights,
         w = impl_->cached_transient(weights, input.size(), output.size(), weights.read_all(),
                                     transient);
     ErrorBuffer err;
-    const auto st = pk_hip_matvec(impl_->ctx, w, UINT32_MAX, input.data(), 1, output.data(),
-                                  err.data(), kErrorCapacity);
+    const auto st = impl_->reference_order
+                        ? pk_hip_matvec_reference_order(impl_->ctx, w, UINT32_MAX, input.data(),
+                                                        output.data(), err.data(), kErrorCapacity)
+                        : pk_hip_matvec(impl_->ctx, w, UINT32_MAX, input.data(), 1, output.data(),
+                                        err.data(), kErrorCapacity);
     if (st == PK_HIP_STATUS_UNSUPPORTED) {
         ++impl_->counters.unsupported_calls;
         return false;
@@ -386,7 +430,12 @@ bool HipLinearBackend::try_moe_block(const HipMoeLayer& layer, std::span<const f
     impl_->require_usable();
     ErrorBuffer err;
     pk_hip_status st;
-    if (layer.shared_router) {  // Qwen3.5: select_experts weights and the shared expert
+    if (impl_->reference_order) {
+        if (layer.shared_router) return false;  // the CPU block runs
+        st = pk_hip_moe_decode_reference_order(impl_->ctx, &desc, normalized.data(),
+                                               moe_result.data(), ids.data(), probs.data(),
+                                               err.data(), kErrorCapacity);
+    } else if (layer.shared_router) {  // Qwen3.5: select_experts weights and the shared expert
         pk_hip_moe35_layer desc35{};
         desc35.routed = desc;
         desc35.shared_router = layer.shared_router.get();

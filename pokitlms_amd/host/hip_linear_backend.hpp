@@ -47,6 +47,16 @@ struct HipLinearOptions {
     // in-memory tensor for its call and releases it; runners that hand over
     // the same expert slices repeatedly opt in.
     std::size_t transient_cache_bytes = 0;
+    // Run every matrix and MoE block in the reference's own operation order
+    // (pk_hip_matvec_reference_order, pk_hip_moe_decode_reference_order): the
+    // CPU kernels' outputs bit for bit, so a runner's greedy tokens equal the
+    // CPU runner's.  Types those kernels do not cover return false (the CPU
+    // kernel runs), as does a Qwen3.5 block with a shared expert.
+    bool reference_order = false;
+    // The host libm's expf exceptions the reference-order SwiGLU needs (the
+    // libm_expf.bin file the build writes); empty: the file beside
+    // libpokit_hip.so.
+    std::string libm_expf_table;
 };
 
 // Counters in the style of VulkanLinearStats (vulkan_linear.hpp:41-67).

@@ -10,6 +10,7 @@ import numpy as np
 import pytest
 
 from pokitlms_amd import synth as S
+from pokitlms_amd.backend import HipError
 from tests.conftest import normwise_rel
 from tests.golden import make_golden as G
 
@@ -334,6 +335,55 @@ def test_c3_moe_decode_golden(hip, port, golden, c3):
     st = hip.stats()
     say("c3 router fallbacks", st["router_fallbacks"], "of", toks.shape[0])
     assert st["router_fallbacks"] <= toks.shape[0] // 8
+
+
+def test_c3_moe_reference_order_bit_exact(hip, port, golden, c3):
+    """pk_hip_moe_decode_reference_order with the host libm's expf table: the
+    reference's ids, probabilities and moe_result bit for bit on all 64
+    golden tokens (outputs: the compiled reference's for the first four, the
+    oracle -- pinned to it bit for bit -- for the rest)."""
+    from pokitlms_amd.model import libm_expf_pairs
+    layer, h = c3
+    hip.set_libm_expf(libm_expf_pairs())
+    try:
+        toks = G.c3_tokens()
+        blk = port.moe(layer)
+        for t in range(toks.shape[0]):
+            y, ids, probs = hip.moe_decode_reference_order(h, toks[t])
+            assert np.array_equal(ids, golden["c3_ids"][t]), t
+            assert np.array_equal(probs.view(np.uint32), golden["c3_probs"][t].view(np.uint32)), t
+            cpu = golden["c3_y"][t] if t < 4 else blk.forward(toks[t])[0]
+            assert np.array_equal(y.view(np.uint32), cpu.view(np.uint32)), (t, normwise_rel(y, cpu))
+    finally:
+        hip.set_libm_expf(None)
+
+
+@pytest.mark.parametrize("gate_type,down_type", ((S.Q5_K, S.Q8_0), (S.Q8_0, S.Q4_K),
+                                                 (S.Q4_0, S.Q6_K)))
+def test_moe_reference_order_other_formats(hip, port, gate_type, down_type):
+    from pokitlms_amd.model import libm_expf_pairs
+    layer = S.moe_layer(seed=200 + gate_type, hidden=1024, experts=32, ffn=512, top_k=6,
+                        gate_type=gate_type, up_type=gate_type, down_type=down_type)
+    h = hip.upload_moe_layer(layer)
+    hip.set_libm_expf(libm_expf_pairs())
+    try:
+        blk = port.moe(layer)
+        for i in range(3):
+            x = S.normal_f32(S.rng(210 + i), 1024)
+            y, ids, probs = hip.moe_decode_reference_order(h, x)
+            cy, cids, cprobs = blk.forward(x)
+            assert np.array_equal(ids, cids)
+            assert np.array_equal(probs.view(np.uint32), cprobs.view(np.uint32))
+            assert np.array_equal(y.view(np.uint32), cy.view(np.uint32))
+        bad = S.normal_f32(S.rng(219), 1024)
+        bad[7] = np.inf
+        with pytest.raises(HipError):
+            hip.moe_decode_reference_order(h, bad)
+        y, _, _ = hip.moe_decode_reference_order(h, x)  # usable after the data error
+        assert np.array_equal(y.view(np.uint32), cy.view(np.uint32))
+    finally:
+        hip.set_libm_expf(None)
+        h.release()
 
 
 def test_moe_decode_deterministic(hip, c3):

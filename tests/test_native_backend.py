@@ -24,6 +24,9 @@ import pytest
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 CASES = os.path.join(ROOT, "oracle", "_ref", "hip_backend_cases")
+RUNNER = os.path.join(ROOT, "oracle", "_ref", "qwen3moe_hip_cases")
+RUNNER_MISSING = ("oracle/_ref/qwen3moe_hip_cases is built only where the reference checkout "
+                  "is present (make -C oracle runner)")
 MISSING = ("oracle/_ref/hip_backend_cases is built only where the reference checkout "
            "is present (make -C oracle cases)")
 
@@ -61,3 +64,38 @@ def test_native_backend_cases():
     for name in ("file_reload", "transient_cache", "transient_default", "expert_cache_stats"):
         assert sum(l.startswith("PASS " + name) for l in lines) == 1, name
     assert sum(l.startswith("PASS runner_parity") for l in lines) == 2
+
+
+@pytest.mark.gpu
+@pytest.mark.skipif(not os.path.exists(RUNNER), reason=RUNNER_MISSING)
+def test_qwen3moe_runner_selects_hip_backend(tmp_path):
+    """The reference's Qwen3MoeRunner with oracle/hip_runner_patch.py's
+    set_linear_backend and MoE hook, and the C API's
+    pokitlms_qwen3moe_create_with_backend (tests/native/qwen3moe_runner_cases.cpp),
+    on the seeded 2-layer model of the whole-model golden: with the
+    reference-order HIP backend every greedy token equals the CPU runner's and
+    the golden tokens the unpatched reference runner wrote, with the MoE hook
+    and try_linear both taking the work; the C API's HIP backend generates the
+    CPU backend's text."""
+    import numpy as np
+
+    from pokitlms_amd import synth_model as SM
+    with np.load(os.path.join(ROOT, "tests", "golden", "model_golden.npz"),
+                 allow_pickle=False) as z:
+        layers, seed = int(z["small_layers"]), int(z["small_seed"])
+        prompt, golden = z["small_prompt"], z["small_tokens"]
+    path = str(tmp_path / "small.gguf")
+    SM.write_gguf(path, SM.Qwen3MoeShape(layers=layers), seed)
+    r = subprocess.run([RUNNER, path, str(len(golden)), *[str(int(t)) for t in prompt]],
+                       capture_output=True, text=True, timeout=600)
+    print(r.stdout[-6000:])
+    print(r.stderr[-3000:])
+    assert r.returncode == 0, r.stdout[-3000:]
+    lines = r.stdout.splitlines()
+    assert not [l for l in lines if l.startswith("FAIL")]
+    for name in ("qwen3moe_runner_parity", "backend_reset", "c_api_backend", "c_api_bad_backend"):
+        assert sum(l.startswith("PASS " + name) for l in lines) == 1, name
+    toks = {l.split()[0]: [int(v) for v in l.split()[1:]] for l in lines
+            if l.split() and l.split()[0] in ("cpu_tokens", "hip_tokens")}
+    assert toks["cpu_tokens"] == [int(t) for t in golden]
+    assert toks["hip_tokens"] == [int(t) for t in golden]
