@@ -71,16 +71,19 @@ def test_small_model_matches_reference(hip, mg):
 
 
 def test_small_model_fast_kernels_within_tolerance(hip, mg):
-    """The bandwidth-optimised kernels: the prompt's logits within 1e-3
-    normwise of the CPU's (reassociation noise, amplified by FP16 KV
-    rounding) and the first greedy token equal."""
+    """The bandwidth-optimised kernels on the 2-layer golden model: the
+    prompt's logits within 2e-4 normwise of the CPU's (measured 9.3e-5) and
+    the first greedy token equal.  The 1e-4 bar holds for each kernel on its
+    own (tests/test_gpu_fast_kernels.py: 1e-6 to 4e-6); these logits come
+    out of 2 layers of a dozen such operations each over a 32-position FP16
+    KV history, and the errors of the chain add up."""
     from pokitlms_amd.model import Qwen3MoeModel
     m = SM.Qwen3MoeShape(layers=int(mg["small_layers"]))
     with Qwen3MoeModel.synthetic(hip, m, int(mg["small_seed"]), reference_order=False) as model:
         tokens, logits, _ = model.generate(mg["small_prompt"], 4, want_logits=True)
     err = normwise_rel(logits, mg["small_logits"])
     say("small model, fast kernels: logits normwise", err)
-    assert err <= 1e-3
+    assert err <= 2e-4
     assert tokens[0] == mg["small_tokens"][0]
 
 
@@ -100,44 +103,34 @@ def test_full_model_greedy_tokens_match_reference(hip, mg):
                         mg["full_tokens"][max(first_diff - 2, 0):first_diff + 3])
 
 
-def test_full_model_fast_kernels_diverge_only_at_a_near_tie(hip, mg):
-    """The bandwidth-optimised kernels on the 48-layer model: where their
-    greedy tokens first leave the golden ones, the golden top-2 logit gap must
-    be within what the fast logits' error at that step can move (each of the
-    two logits by up to the largest error, in opposite directions), i.e.
-    reassociation noise deciding a near-tie.  A wider gap would be a kernel
-    error.  The golden logits of that step come from the reference-order
-    kernels, whose tokens and logits equal the CPU runner's.  (At one or two
-    layers the fast logits stay within about 1e-4 normwise of the reference
-    for every prompt length; with depth the difference grows in an
-    input-dependent way -- a routing decision near a tie turns reassociation
-    noise into a different expert set -- so by layer 48 the logits differ
-    widely and the first greedy token after the prompt's is already
-    different.)"""
-    if "full_tokens" not in mg:
-        pytest.skip("full-model golden not generated (make_model_golden.py without --skip-full)")
+@pytest.mark.parametrize("layers", (1, 2, 4, 8))
+def test_fast_mode_tracks_reference_order_by_depth(hip, layers):
+    """The bandwidth-optimised kernels against the reference-order ones (whose
+    logits are the CPU runner's) on the seeded model's first `layers` layers:
+    after a 32-token prompt and after 8 greedy steps the fast logits stay
+    within 1e-3 normwise of the reference-order logits (measured: 1e-6 at one
+    layer, growing to about 2e-4 at eight: FP32 reassociation noise carried
+    through the residual stream and the FP16 KV ring) and the greedy tokens are
+    the same.  A wrong index, scale or row in any fast kernel moves the logits
+    by O(1).  (With more layers a router decision within that noise can pick
+    another expert set, after which the two runs are different computations, so
+    the fast mode claims no token parity on the 48-layer model.)"""
     from pokitlms_amd.model import Qwen3MoeModel
-    m = SM.Qwen3MoeShape(layers=int(mg["full_layers"]))
-    golden, prompt = mg["full_tokens"], mg["full_prompt"]
-    with Qwen3MoeModel.synthetic(hip, m, int(mg["full_seed"]), reference_order=False) as model:
-        tokens, _, _ = model.generate(prompt, len(golden))
-        same = tokens == golden
-        if same.all():
-            say("full model, fast kernels: all", len(golden), "tokens equal the golden ones")
-            return
-        d = int(np.argmin(same))
-        ctx = np.concatenate([prompt, golden[:d]]).astype(np.uint32)
-        fast = model.generate(ctx, 1, want_logits=True)[1]
-    with Qwen3MoeModel.synthetic(hip, m, int(mg["full_seed"])) as model:
-        ref = model.generate(ctx, 1, want_logits=True)[1]
-    assert int(np.argmax(ref)) == int(golden[d])
-    t1, t2 = (int(i) for i in np.argsort(ref)[::-1][:2])
-    gap = float(ref[t1]) - float(ref[t2])
-    err = float(np.max(np.abs(fast.astype(np.float64) - ref.astype(np.float64))))
-    say("full model, fast kernels: first mismatch at token", d, "golden top-2", (t1, t2),
-        "gap", gap, "fast max abs logit error", err, "fast argmax", int(np.argmax(fast)),
-        "normwise", err / float(np.max(np.abs(ref))))
-    assert gap <= 2.0 * err, (d, gap, err)
+    m = SM.Qwen3MoeShape(layers=layers)
+    prompt = SM.prompt_tokens(1234, 32, m.vocab)
+    outs = {}
+    for ref in (True, False):
+        with Qwen3MoeModel.synthetic(hip, m, 1234, reference_order=ref) as model:
+            t, l0, _ = model.generate(prompt, 8, want_logits=True)
+            ctx = np.concatenate([prompt, t[:7]]).astype(np.uint32)
+            _, l8, _ = model.generate(ctx, 1, want_logits=True)
+            outs[ref] = (t, l0, l8)
+    e0 = normwise_rel(outs[False][1], outs[True][1])
+    e8 = normwise_rel(outs[False][2], outs[True][2])
+    say("fast vs reference order,", layers, "layers: logits normwise", e0, "after the prompt,",
+        e8, "after 8 steps; tokens", outs[False][0], outs[True][0])
+    assert e0 <= 1e-3 and e8 <= 1e-3, (e0, e8)
+    assert np.array_equal(outs[False][0], outs[True][0])
 
 
 def _generate_borrowed(hip, shape, weights, prompt, n_new, reference_order):
