@@ -122,6 +122,33 @@ __device__ __forceinline__ void kq_scale_min(const uint32_t (&h)[4], uint32_t j,
     m = static_cast<float>(j < 4 ? m_lo : m_hi);
 }
 
+// Pairs 2c and 2c + 1 (c = 0..3) of a Q4_K/Q5_K block at once, without
+// branches: both sit in the low-index form (c < 2: six bits of byte j of
+// h[1] / h[2]) or both in the high-index form (c >= 2: a nibble of byte j & 3
+// of h[3] and two bits of h[1] / h[2]); a zero-width extract drops the top
+// bits of the low-index form.
+__device__ __forceinline__ void kq_scale_min_pair(const uint32_t (&h)[4], uint32_t c, uint32_t& s0,
+                                                  uint32_t& m0, uint32_t& s1, uint32_t& m1) {
+    const bool lo = c < 2u;
+    const uint32_t o0 = 16u * (c & 1u), o1 = o0 + 8u;
+    const uint32_t hs = lo ? h[1] : h[3], hm = lo ? h[2] : h[3];
+    const uint32_t w = lo ? 6u : 4u, wt = lo ? 0u : 2u, om = lo ? 0u : 4u;
+    s0 = __builtin_amdgcn_ubfe(hs, o0, w) | (__builtin_amdgcn_ubfe(h[1], o0 + 6u, wt) << 4);
+    s1 = __builtin_amdgcn_ubfe(hs, o1, w) | (__builtin_amdgcn_ubfe(h[1], o1 + 6u, wt) << 4);
+    m0 = __builtin_amdgcn_ubfe(hm, o0 + om, w) | (__builtin_amdgcn_ubfe(h[2], o0 + 6u, wt) << 4);
+    m1 = __builtin_amdgcn_ubfe(hm, o1 + om, w) | (__builtin_amdgcn_ubfe(h[2], o1 + 6u, wt) << 4);
+}
+
+// The fp16 value of the low / high half of a word, widened to fp32.  Used on
+// masked quant words, whose halves are fp16 subnormals (small integers times
+// 2^-24): an FMA on the result compiles to one v_fma_mix_f32.
+__device__ __forceinline__ float half_lo(uint32_t w) {
+    return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(w)));
+}
+__device__ __forceinline__ float half_hi(uint32_t w) {
+    return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(w >> 16)));
+}
+
 // Bits 0..3 of b to bit 4 of bytes 0..3 (the Q5_0/Q5_1 fifth bits).
 __device__ __forceinline__ uint32_t spread4(uint32_t b) {
     return ((b & 1u) << 4) | ((b & 2u) << 11) | ((b & 4u) << 18) | ((b & 8u) << 25);
@@ -349,7 +376,47 @@ __device__ __forceinline__ void unit_compute(const UnitRaw<T, UB>& r, const Unit
 #pragma unroll
     for (int b = 0; b < B; ++b) dot0[b] = dot1[b] = 0.0f;
 
-    if constexpr (T == T_Q4_K || T == T_Q5_K) {
+    if constexpr (T == T_Q4_K) {
+        // Element pairs (0, 2) and (1, 3) of each quant word sit in the two
+        // halves of a masked word: a nibble q there is the fp16 subnormal
+        // q * 2^-24 (16 q * 2^-24 for the high nibbles, masked in place), which
+        // v_fma_mix_f32 widens exactly inside the FMA.  The sums are the exact
+        // 2^-24 / 2^-20 multiples of the plain q.x sums (same order, same
+        // roundings), and the scales carry the factors back.
+        const uint32_t c = p.k0 / 32u;
+#pragma unroll
+        for (int t = 0; t < NW; ++t) {
+            const uint32_t q = r.q[t], s = q >> 8;
+            const uint32_t l02 = q & 0x000f000fu, l13 = s & 0x000f000fu;
+            const uint32_t h02 = q & 0x00f000f0u, h13 = s & 0x00f000f0u;
+#pragma unroll
+            for (int b = 0; b < B; ++b) {
+                const float* x0 = &ux.v[b][4 * t];
+                const float* x1 = &ux.v[b][UB + 4 * t];
+                dot0[b] = __builtin_fmaf(half_lo(l02), x0[0], dot0[b]);
+                dot0[b] = __builtin_fmaf(half_lo(l13), x0[1], dot0[b]);
+                dot0[b] = __builtin_fmaf(half_hi(l02), x0[2], dot0[b]);
+                dot0[b] = __builtin_fmaf(half_hi(l13), x0[3], dot0[b]);
+                dot1[b] = __builtin_fmaf(half_lo(h02), x1[0], dot1[b]);
+                dot1[b] = __builtin_fmaf(half_lo(h13), x1[1], dot1[b]);
+                dot1[b] = __builtin_fmaf(half_hi(h02), x1[2], dot1[b]);
+                dot1[b] = __builtin_fmaf(half_hi(h13), x1[3], dot1[b]);
+            }
+        }
+        uint32_t s0, m0, s1, m1;
+        kq_scale_min_pair(r.h, c, s0, m0, s1, m1);
+        const float d = half_bits_to_float(r.h[0] & 0xffffu);
+        const float dmin = half_bits_to_float(r.h[0] >> 16);
+        const float ds0 = (d * 0x1p24f) * static_cast<float>(s0);
+        const float ds1 = (d * 0x1p20f) * static_cast<float>(s1);
+        const float dm0 = dmin * static_cast<float>(m0), dm1 = dmin * static_cast<float>(m1);
+#pragma unroll
+        for (int b = 0; b < B; ++b) {
+            const float t0 = __builtin_fmaf(ds0, dot0[b], -dm0 * ux.s[b][0]);
+            const float t1 = __builtin_fmaf(ds1, dot1[b], -dm1 * ux.s[b][1]);
+            acc[b] += t0 + t1;
+        }
+    } else if constexpr (T == T_Q5_K) {
         const uint32_t c = p.k0 / 32u;
 #pragma unroll
         for (int t = 0; t < NW; ++t) {

@@ -25,9 +25,9 @@ constexpr int kMaxS = 12;  // waves per K-split group
 template <int B> constexpr int passes_for() { return B > 4 ? 1 : 2; }
 template <int B> constexpr int max_threads_for() { return B > 4 ? 768 : 512; }
 
-template <int T, int B, int UB, int NU, bool PIPE>
+template <int T, int B, int UB, int NU, bool PIPE, int P = passes_for<B>()>
 struct MvState {
-    static constexpr int kPasses = passes_for<B>();
+    static constexpr int kPasses = P;
     static constexpr int kBufs = PIPE ? 2 : 1;
     UnitPos pos[NU];
     bool valid[NU];
@@ -173,14 +173,14 @@ __global__ __launch_bounds__(max_threads_for<B>()) void k_matvec_q(
 // order).  W and x are not __restrict__ here: loads the compiler may not take
 // for invariant keep that program order around the barrier.
 
-template <int T, int B, int UB, int NU, int XG>
+template <int T, int B, int UB, int NU, int XG, int P>
 __global__ __launch_bounds__(512) void k_matvec_q_staged(
     const uint8_t* W, uint32_t nb, const float* x, float* y, uint32_t rows, uint32_t units,
     uint32_t slice_units, uint32_t S) {
     // vector b of x starts at b * nb * BE, of y at b * rows
     // staged x [S][NU][B][Q][64], then partial [waves][kPasses][B] when S > 1
     extern __shared__ xf32x4 smem[];
-    constexpr int kPasses = passes_for<B>(), Q = x_pieces<T, UB>(), QB = Q * B, XP = NU * QB / XG;
+    constexpr int kPasses = P, Q = x_pieces<T, UB>(), QB = Q * B, XP = NU * QB / XG;
     static_assert(XP * XG == NU * QB, "pieces split evenly over the waves of a slice");
     const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
     const uint32_t group = wave / S, slice = wave % S;
@@ -190,7 +190,7 @@ __global__ __launch_bounds__(512) void k_matvec_q_staged(
     uint32_t p0 = blockIdx.x * XG * kPasses;
     if (p0 >= rows) return;  // uniform per workgroup
 
-    MvState<T, B, UB, NU, false> st;
+    MvState<T, B, UB, NU, false, P> st;
 #pragma unroll
     for (int k = 0; k < NU; ++k) {
         const uint32_t local = lane + 64u * k;
@@ -373,6 +373,21 @@ bool plan_for(uint32_t in, uint32_t batch, int ub, Plan& p) {
     return p.nu <= kMaxUnitsPerLane;
 }
 
+// XG row streams of P rows each per workgroup, every stream split over the
+// plan's S waves; the activations (xl bytes) staged once per workgroup.
+template <int T, int B, int UB, int NU, int XG, int P>
+hipError_t run_staged(const Plan& pl, const uint8_t* W, uint32_t nb, uint32_t rows,
+                      const float* x, float* y, uint32_t xl, hipStream_t stream) {
+    const uint32_t waves = XG * pl.S;
+    uint32_t blocks = ceil_div(rows, XG * P);
+    const uint32_t max_blocks = 256u * 16u / waves;
+    if (blocks > max_blocks) blocks = max_blocks;
+    const size_t lds = xl + (pl.S > 1 ? static_cast<size_t>(waves) * P * B * sizeof(float) : 0);
+    hipLaunchKernelGGL((k_matvec_q_staged<T, B, UB, NU, XG, P>), dim3(blocks), dim3(64u * waves),
+                       lds, stream, W, nb, x, y, rows, pl.units, pl.slice_units, pl.S);
+    return hipGetLastError();
+}
+
 template <int T, int B, int UB, int NU>
 hipError_t run_q(const Plan& pl, const uint8_t* W, uint32_t nb, uint32_t rows,
                  const float* x, uint32_t in, float* y, hipStream_t stream) {
@@ -399,29 +414,28 @@ hipError_t run_q(const Plan& pl, const uint8_t* W, uint32_t nb, uint32_t rows,
         }
     }
     // up to four vectors (one for Q2_K/Q3_K, whose batches would spill), rows
-    // on 64 lanes, two or four row streams per workgroup sharing a slice: the
-    // activations staged once in LDS (at most 32 KB)
+    // on 64 lanes, two, four or eight row streams per workgroup sharing a
+    // slice: the activations staged once in LDS (at most 32 KB)
     if constexpr (B == 1 || (B <= 4 && T != T_Q2_K && T != T_Q3_K)) {
         // (each wave of a slice stages the same number of pieces)
         constexpr int kPieces = NU * x_pieces<T, UB>() * B;
         const uint32_t xl = pl.S * kPieces * 64u * 16u;
         if (pl.glog2 == 6u && xl <= 32768u) {
-            const dim3 grid(blocks), block(64u * pl.waves_per_block);
+            // one vector over one K-slice: eight one-row streams (a wave's dots
+            // follow its single row's loads sooner); otherwise the plan's
+            // streams, two rows each
+            const bool one = B == 1 && pl.S == 1u;
+            if constexpr (B == 1 && kPieces % 8 == 0) {
+                if (one && groups == 4u)
+                    return run_staged<T, B, UB, NU, 8, 1>(pl, W, nb, rows, x, y, xl, stream);
+            }
             if constexpr (kPieces % 4 == 0) {
-                if (groups == 4u) {
-                    hipLaunchKernelGGL((k_matvec_q_staged<T, B, UB, NU, 4>), grid, block, xl + lds,
-                                       stream, W, nb, x, y, rows, pl.units, pl.slice_units,
-                                       pl.S);
-                    return hipGetLastError();
-                }
+                if (groups == 4u)
+                    return run_staged<T, B, UB, NU, 4, 2>(pl, W, nb, rows, x, y, xl, stream);
             }
             if constexpr (kPieces % 2 == 0) {
-                if (groups == 2u) {
-                    hipLaunchKernelGGL((k_matvec_q_staged<T, B, UB, NU, 2>), grid, block, xl + lds,
-                                       stream, W, nb, x, y, rows, pl.units, pl.slice_units,
-                                       pl.S);
-                    return hipGetLastError();
-                }
+                if (groups == 2u)
+                    return run_staged<T, B, UB, NU, 2, 2>(pl, W, nb, rows, x, y, xl, stream);
             }
         }
     }
