@@ -118,19 +118,27 @@ __host__ __device__ constexpr uint32_t xpad_floats(uint32_t n) { return n + (n +
 __device__ float serial_sum(const float* p, uint32_t n, float s) {
     const f32x16* v = reinterpret_cast<const f32x16*>(p);
     const uint32_t nb = n / 16u;
-    f32x16 a = v[0], b = v[1];
+    // two register sets, each refilled right after its 32 values are added,
+    // so the reads of one run under the adds of the other and no set is
+    // copied (the scheduler would otherwise sink the reads next to their use,
+    // or move each loaded set into the one the loop carries)
+    f32x16 a0 = v[0], a1 = v[1];
     uint32_t k = 0;
-    for (; k + 2u <= nb; k += 2u) {
-        const f32x16 na = v[k + 2u], nb2 = v[k + 3u];
-        // keep the next 32 reads ahead of the 32 adds: the scheduler would
-        // otherwise sink them next to their use and expose the LDS latency
+    for (; k + 4u <= nb; k += 4u) {
+        const f32x16 b0 = v[k + 2u], b1 = v[k + 3u];
         __builtin_amdgcn_sched_barrier(0);
-        s = add16(s, a);
-        s = add16(s, b);
-        a = na;
-        b = nb2;
+        s = add16(s, a0);
+        s = add16(s, a1);
+        a0 = v[k + 4u];
+        a1 = v[k + 5u];
+        __builtin_amdgcn_sched_barrier(0);
+        s = add16(s, b0);
+        s = add16(s, b1);
     }
-    if (k < nb) s = add16(s, a);
+    // a0, a1 hold blocks k, k + 1 (read within the pad); up to three remain
+    if (k < nb) s = add16(s, a0);
+    if (k + 1u < nb) s = add16(s, a1);
+    if (k + 2u < nb) s = add16(s, v[k + 2u]);
     for (uint32_t i = 16u * nb; i < n; ++i) s = __fadd_rn(s, p[i]);
     return s;
 }
