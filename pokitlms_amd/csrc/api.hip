@@ -168,6 +168,7 @@ struct pk_hip_ctx {
     DeviceBuffer<float> x, y, act, probs;
     DeviceBuffer<uint32_t> ids, words;  // words: [1..4] status
     DeviceBuffer<double> row_sum, row_bound;
+    DeviceBuffer<float> mvpart;  // the K-sliced batched matvec's slice sums
     // prefill scratch (grown on demand)
     DeviceBuffer<float> px, py, pprobs, pout, pxsum, pasum;
     DeviceBuffer<uint32_t> pids, poffsets, ptiles, pperm;
@@ -391,11 +392,14 @@ void enqueue_matvec(pk_hip_ctx* c, const pk_hip_weight* w, uint32_t expert, cons
     }
     if (!pk::matvec_supported(w->type, static_cast<uint32_t>(w->in), batch))
         throw Unsupported("matrix width/batch not covered by the HIP matvec kernels");
+    const size_t part = pk::matvec_partial_floats(w->type, static_cast<uint32_t>(w->in), batch,
+                                                  static_cast<uint32_t>(w->out));
+    if (part) c->mvpart.ensure(part);
     if (c->time_kernels) hold_stream(c, s);
     begin_timing(c, s, 0);
     launch_checked(pk::launch_matvec(w->type, w->dptr + offset, w->row_bytes,
                                      static_cast<uint32_t>(w->out), static_cast<uint32_t>(w->in),
-                                     dx, dy, batch, s),
+                                     dx, dy, batch, s, part ? c->mvpart.ptr : nullptr),
                    "matvec launch");
     begin_timing(c, s, 1);
     ++c->stats.matvec_calls;
@@ -636,6 +640,7 @@ void pk_hip_destroy(pk_hip_ctx* c) {
     c->words.release();
     c->row_sum.release();
     c->row_bound.release();
+    c->mvpart.release();
     for (auto* b : {&c->px, &c->py, &c->pprobs, &c->pout, &c->pxsum, &c->pasum})
         b->release();
     for (auto* b : {&c->pids, &c->poffsets, &c->ptiles, &c->pperm}) b->release();
@@ -671,6 +676,13 @@ static pk_hip_status upload_impl(pk_hip_ctx* ctx, uint32_t type, uint64_t in, ui
             (void)hipFree(w->dptr);
             delete w;
             throw;
+        }
+        // the batched matvec's slice sums for this shape, reserved now (an
+        // allocation cannot happen later inside a captured graph)
+        if (in <= UINT32_MAX && out <= UINT32_MAX) {
+            const size_t part = pk::matvec_partial_floats(type, static_cast<uint32_t>(in), 8u,
+                                                          static_cast<uint32_t>(out));
+            if (part) ctx->mvpart.ensure(part);
         }
         ctx->stats.resident_bytes += nbytes;
         ctx->stats.uploaded_bytes += nbytes;

@@ -17,17 +17,22 @@ bool matvec_supported(uint32_t type, uint32_t in, uint32_t batch);
 
 // y[b][r] = W[r] . x[b] for b < batch.  W: rows x row_bytes encoded GGUF rows
 // (device), x: batch x in floats (device, rows 16-byte aligned), y: batch x rows.
+// `partial`: device scratch of matvec_partial_floats(type, in, batch, rows)
+// floats (K-sliced batched kernels; may be null where that count is 0).
 hipError_t launch_matvec(uint32_t type, const uint8_t* W, uint64_t row_bytes, uint32_t rows,
                          uint32_t in, const float* x, float* y, uint32_t batch,
-                         hipStream_t stream);
+                         hipStream_t stream, float* partial = nullptr);
+size_t matvec_partial_floats(uint32_t type, uint32_t in, uint32_t batch, uint32_t rows);
 
 // Batched matvecs on MFMA (matvec_mfma.hip): 256-value K ranges per wave for
 // (type, in, batch), 0 where that kernel does not apply; launch_matvec takes
 // it where matvec_mfma_takes says so.
 uint32_t matvec_mfma_blocks_per_wave(uint32_t type, uint32_t in, uint32_t batch);
 bool matvec_mfma_takes(uint32_t type, uint32_t in, uint32_t batch, uint32_t rows);
+size_t matvec_mfma_partial_floats(uint32_t type, uint32_t in, uint32_t batch, uint32_t rows);
 hipError_t launch_matvec_mfma(uint32_t type, const uint8_t* W, uint32_t rows, uint32_t in,
-                              const float* x, float* y, uint32_t batch, hipStream_t stream);
+                              const float* x, float* y, uint32_t batch, hipStream_t stream,
+                              float* partial);
 
 // One single-token routed-MoE layer (router -> top-k -> gate/up SwiGLU ->
 // down -> weighted combine).  Device pointers throughout.

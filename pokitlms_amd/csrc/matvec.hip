@@ -526,12 +526,17 @@ bool matvec_supported(uint32_t type, uint32_t in, uint32_t batch) {
     }
 }
 
+size_t matvec_partial_floats(uint32_t type, uint32_t in, uint32_t batch, uint32_t rows) {
+    if (rows == 0 || !matvec_mfma_takes(type, in, batch, rows)) return 0;
+    return matvec_mfma_partial_floats(type, in, batch, rows);
+}
+
 hipError_t launch_matvec(uint32_t type, const uint8_t* W, uint64_t row_bytes, uint32_t rows,
                          uint32_t in, const float* x, float* y, uint32_t batch,
-                         hipStream_t stream) {
+                         hipStream_t stream, float* partial) {
     if (rows == 0) return hipSuccess;
     if (matvec_mfma_takes(type, in, batch, rows))
-        return launch_matvec_mfma(type, W, rows, in, x, y, batch, stream);
+        return launch_matvec_mfma(type, W, rows, in, x, y, batch, stream, partial);
     switch (type) {
         case T_F32: return dispatch_batch_f<T_F32>(batch, W, row_bytes, rows, x, in, y, stream);
         case T_F16: return dispatch_batch_f<T_F16>(batch, W, row_bytes, rows, x, in, y, stream);

@@ -13,10 +13,10 @@
 //  * A wave owns 16·NT rows (NT tiles of 16, lane n = lane % 16 of each tile)
 //    and KB consecutive 256-value ranges of K; the waves of a workgroup own
 //    the same rows and consecutive K ranges, and their partial results are
-//    added through LDS in wave order (deterministic).  A grid of at most 128
-//    row groups takes two workgroups per row group, one per half of K, that
-//    add into y zeroed beforehand (two terms onto +0: the same sum in either
-//    order).
+//    added through LDS in wave order (deterministic).  Where that grid has
+//    at most 128 row groups, k_matvec_mfma_ks (below) takes the matrix
+//    instead: 64 rows and a K slice per workgroup, partial sums per slice
+//    added in slice order by a second launch.
 //  * A scale group of 32 values is one MFMA K step, lane kq = lane / 16
 //    holding values 8kq .. 8kq+7 of it (Q6_K's two 16-value groups per step:
 //    two MFMAs, each with the other group's lanes zeroed).  Per 256 values
@@ -222,9 +222,7 @@ __global__ __launch_bounds__(1024) void k_matvec_mfma(const uint8_t* W, uint32_t
     const uint32_t waves = blockDim.x >> 6;
     const uint32_t n = lane & 15u, kq = lane >> 4;
     const uint32_t r0 = blockIdx.x * 16u * NT;
-    // gridDim.y K halves: half blockIdx.y takes the ranges from
-    // blockIdx.y * waves * KB on, and adds into y (zeroed beforehand)
-    const uint32_t kbase = (blockIdx.y * waves + wave) * KB;
+    const uint32_t kbase = wave * KB;
     const uint32_t in = nb * 256u;
 
     // nb: 256-value ranges per row
@@ -304,43 +302,178 @@ __global__ __launch_bounds__(1024) void k_matvec_mfma(const uint8_t* W, uint32_t
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const uint32_t m = 4u * kq + i;
-                if (m < batch && row < rows) {
-                    float* o = y + static_cast<uint64_t>(m) * rows + row;
-                    // two halves onto +0: 0 + a + b = a + b in either order
-                    if (gridDim.y == 1) *o = s[i];
-                    else __hip_atomic_fetch_add(o, s[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                }
+                if (m < batch && row < rows) y[static_cast<uint64_t>(m) * rows + row] = s[i];
             }
         }
     }
 }
 
-__global__ __launch_bounds__(256) void k_zero(float* y, uint32_t n) {
+// K-sliced layout for small row counts.  In the kernel above every 16-row
+// tile reads and splits all of x (at 2048x6144 and 8 vectors, 25 MB of x
+// reads for 7 MB of weights, and the split is about half the VALU work).
+// Here a workgroup owns 64 rows (four tiles, one per wave column) and KR
+// consecutive 256-value ranges of K (one per wave row): it splits only its
+// K slice of x, once, into LDS (the 32 distinct A fragments per 32-value
+// group: vectors 0..7 x kq; lanes of rows m >= 8 read vector m - 8's, their
+// outputs are never stored), every wave reads its fragments from there, the
+// waves of a tile add their K ranges through LDS in range order, and the
+// slice's sums go to partial[slice][b][row].  k_mm_reduce adds the slices in
+// slice order (deterministic).  One slice (nb <= 4) writes y directly.
+constexpr uint32_t kKsTiles = 4;  // 16-row tiles per workgroup
+
+template <int T, int KR>
+__global__ __launch_bounds__(1024) void k_matvec_mfma_ks(const uint8_t* W, uint32_t nb,
+                                                        const float* x, float* out, uint32_t rows,
+                                                        uint32_t batch) {
+    constexpr uint32_t G = 8u * KR;  // 32-value groups of the slice
+    // [hi | mid | lo][G][32 slots] fragments, then the slots' 8-value sums
+    extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+    mbf16x8* ah = reinterpret_cast<mbf16x8*>(smem);
+    mbf16x8* am = ah + G * 32u;
+    mbf16x8* al = am + G * 32u;
+    float* ap = reinterpret_cast<float*>(al + G * 32u);
+    const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
+    const uint32_t tile = wave % kKsTiles, kr = wave / kKsTiles;
+    const uint32_t n = lane & 15u, kq = lane >> 4;
+    const uint32_t row = (blockIdx.x * kKsTiles + tile) * 16u + n;
+    constexpr uint32_t kPer = 256u / Fmt<T>::BE;  // GGUF blocks per 256 values
+    const uint64_t nblk = static_cast<uint64_t>(rows) * nb * kPer;
+    // the weight loads first (HBM), then the slice's x (L2)
+    MmPart<T> part;
+    const QRow qr{W, nblk, static_cast<uint64_t>(row < rows ? row : rows - 1u) * nb * kPer};
+    mm_load<T>(qr, blockIdx.y * KR + kr, kq, part);
+    const uint32_t in = nb * 256u, k0 = blockIdx.y * KR * 256u;
+    for (uint32_t i = tid; i < G * 32u; i += blockDim.x) {  // G * 32 is a multiple of blockDim
+        const uint32_t gi = i / 32u, slot = i % 32u, m = slot & 7u;
+        XRaw xr;
+        x_load(x, in, m < batch ? m : 0u, k0 + 32u * gi, slot >> 3, xr);
+        XFrag f;
+        x_split(xr, f);
+        ah[i] = f.hi;
+        am[i] = f.mid;
+        al[i] = f.lo;
+        ap[i] = f.part;
+    }
+    __syncthreads();
+    mf32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+    const uint32_t slot = (n & 7u) + 8u * kq;
+#pragma unroll
+    for (uint32_t g = 0; g < 8u; ++g) {
+        const uint32_t i = (kr * 8u + g) * 32u + slot;
+        const mbf16x8 xh = ah[i], xm = am[i], xl = al[i];
+        const float xp = ap[i];
+        const mf32x4 zero = {0.0f, 0.0f, 0.0f, 0.0f};
+        float cb;
+        if constexpr (T == T_Q6_K) {
+            mbf16x8 b0, b1;
+            float ds0, ds1;
+            q6k_group(part, g, kq, b0, b1, ds0, ds1, cb);
+            mf32x4 P = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xl, b0, zero, 0, 0, 0);
+            mf32x4 Q = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xl, b1, zero, 0, 0, 0);
+            P = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xm, b0, P, 0, 0, 0);
+            Q = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xm, b1, Q, 0, 0, 0);
+            P = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xh, b0, P, 0, 0, 0);
+            Q = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xh, b1, Q, 0, 0, 0);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                acc[j] = __builtin_fmaf(ds0, P[j], acc[j]);
+                acc[j] = __builtin_fmaf(ds1, Q[j], acc[j]);
+            }
+        } else {
+            mbf16x8 b;
+            float ds;
+            mm_group<T>(part, g, kq, b, ds, cb);
+            mf32x4 P = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xl, b, zero, 0, 0, 0);
+            P = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xm, b, P, 0, 0, 0);
+            P = __builtin_amdgcn_mfma_f32_16x16x32_bf16(xh, b, P, 0, 0, 0);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) acc[j] = __builtin_fmaf(ds, P[j], acc[j]);
+        }
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(xp, cb, acc, 0, 0, 0);
+    }
+    // the tile's K ranges in range order (the fragments are dead: reuse LDS)
+    __syncthreads();
+    mf32x4* red = reinterpret_cast<mf32x4*>(smem);  // [kr][tile][lane]
+    red[(kr * kKsTiles + tile) * 64u + lane] = acc;
+    __syncthreads();
+    if (kr == 0u) {
+        mf32x4 sum = red[tile * 64u + lane];
+        for (uint32_t k = 1; k < KR; ++k) sum += red[(k * kKsTiles + tile) * 64u + lane];
+        // lane holds vectors 4kq .. 4kq+3 of its row
+        float* o = out + static_cast<uint64_t>(blockIdx.y) * batch * rows;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const uint32_t m = 4u * kq + j;
+            if (m < batch && row < rows) o[static_cast<uint64_t>(m) * rows + row] = sum[j];
+        }
+    }
+}
+
+// y[i] = partial[0][i] + partial[1][i] + ... in slice order.
+__global__ __launch_bounds__(256) void k_mm_reduce(const float* __restrict__ partial,
+                                                   float* __restrict__ y, uint32_t n,
+                                                   uint32_t slices) {
     const uint32_t i = blockIdx.x * 256u + threadIdx.x;
-    if (i < n) y[i] = 0.0f;
+    if (i >= n) return;
+    float v = partial[i];
+    for (uint32_t s = 1; s < slices; ++s) v += partial[static_cast<uint64_t>(s) * n + i];
+    y[i] = v;
+}
+
+// K ranges per workgroup (KR) and slices for the K-sliced kernel: the
+// largest KR <= 4 dividing nb that still gives at least 256 workgroups, else
+// the smallest divisor; 0 where the kernel does not apply.
+uint32_t ks_ranges(uint32_t nb, uint32_t rows) {
+    const uint32_t groups = (rows + 16u * kKsTiles - 1u) / (16u * kKsTiles);
+    uint32_t best = 0;
+    for (uint32_t kr = 1; kr <= 4u; ++kr) {
+        if (nb % kr) continue;
+        if (best == 0 || groups * (nb / kr) >= 256u) best = kr;
+    }
+    return best;
+}
+
+template <int T, int KR>
+hipError_t launch_ks(const uint8_t* W, uint32_t nb, uint32_t rows, const float* x, float* y,
+                     uint32_t batch, float* partial, hipStream_t s) {
+    const uint32_t slices = nb / KR;
+    const uint32_t groups = (rows + 16u * kKsTiles - 1u) / (16u * kKsTiles);
+    float* out = slices > 1u ? partial : y;
+    if (!out) return hipErrorInvalidValue;
+    constexpr size_t kFrag = 8u * KR * 32u * (3u * sizeof(mbf16x8) + sizeof(float));
+    constexpr size_t kRed = KR * kKsTiles * 64u * sizeof(mf32x4);
+    const size_t lds = kFrag > kRed ? kFrag : kRed;
+    hipLaunchKernelGGL((k_matvec_mfma_ks<T, KR>), dim3(groups, slices), dim3(64u * kKsTiles * KR),
+                       lds, s, W, nb, x, out, rows, batch);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess || slices == 1u) return e;
+    const uint32_t n = batch * rows;
+    hipLaunchKernelGGL(k_mm_reduce, dim3((n + 255u) / 256u), dim3(256), 0, s, partial, y, n, slices);
+    return hipGetLastError();
+}
+
+template <int T>
+hipError_t launch_ks_t(const uint8_t* W, uint32_t nb, uint32_t rows, const float* x, float* y,
+                       uint32_t batch, float* partial, hipStream_t s) {
+    switch (ks_ranges(nb, rows)) {
+        case 1: return launch_ks<T, 1>(W, nb, rows, x, y, batch, partial, s);
+        case 2: return launch_ks<T, 2>(W, nb, rows, x, y, batch, partial, s);
+        case 3: return launch_ks<T, 3>(W, nb, rows, x, y, batch, partial, s);
+        case 4: return launch_ks<T, 4>(W, nb, rows, x, y, batch, partial, s);
+        default: return hipErrorInvalidValue;
+    }
 }
 
 template <int T, int NT, int KB>
 hipError_t launch_nt_kb(const uint8_t* W, uint32_t nb, uint32_t rows, const float* x, float* y,
                         uint32_t batch, hipStream_t s) {
-    uint32_t waves = nb / KB;
+    const uint32_t waves = nb / KB;
     const uint32_t blocks = (rows + 16u * NT - 1u) / (16u * NT);
-    // at most half as many workgroups as CUs: two per row group, each half of
-    // K (the kernel's VALU work then spreads over twice the CUs; the zeroing
-    // launch costs about 2 us, more than that gains at 192 workgroups)
-    uint32_t halves = 1;
-    if (blocks <= 128u && waves % 2u == 0 && waves >= 4u) {
-        halves = 2;
-        waves /= 2;
-        const uint32_t n = batch * rows;
-        hipLaunchKernelGGL(k_zero, dim3((n + 255u) / 256u), dim3(256), 0, s, y, n);
-    }
     const size_t lds = static_cast<size_t>(waves) * NT * 64u * sizeof(mf32x4);
-    hipLaunchKernelGGL((k_matvec_mfma<T, NT, KB>), dim3(blocks, halves), dim3(64u * waves), lds, s,
-                       W, nb, x, y, rows, batch);
+    hipLaunchKernelGGL((k_matvec_mfma<T, NT, KB>), dim3(blocks), dim3(64u * waves), lds, s, W, nb,
+                       x, y, rows, batch);
     return hipGetLastError();
 }
-
 
 template <int T>
 hipError_t launch_t(uint32_t kb, const uint8_t* W, uint32_t nb, uint32_t rows, const float* x,
@@ -378,23 +511,43 @@ uint32_t matvec_mfma_blocks_per_wave(uint32_t type, uint32_t in, uint32_t batch)
     return batch >= 5u && batch <= 8u ? mfma_kb(type, in) : 0u;
 }
 
-// Batches of 5 to 8; 4 vectors of the nibble formats where the grid splits K
-// over two workgroups (at most 128 row groups): there the register kernels
-// trail by about 10%, and lead by 2% for Q8_0 and Q6_K.
-bool matvec_mfma_takes(uint32_t type, uint32_t in, uint32_t batch, uint32_t rows) {
-    if (batch >= 5u) return matvec_mfma_blocks_per_wave(type, in, batch) != 0;
-    if (batch != 4u || type == T_Q8_0 || type == T_Q6_K) return false;
+// Grids of at most 128 row groups of the one-pass kernel (half the CUs:
+// 2048-row matrices) take the K-sliced kernel instead; 4 vectors go to MFMA
+// only there (the staged register kernel leads elsewhere: 6.7 against 11.1 us
+// at 6144x2048).
+bool ks_takes(uint32_t type, uint32_t in, uint32_t rows) {
     const uint32_t kb = mfma_kb(type, in);
     if (kb == 0) return false;
-    const uint32_t nt = kb == 1u ? 2u : 1u, waves = in / 256u / kb;
-    const uint32_t blocks = (rows + 16u * nt - 1u) / (16u * nt);
-    return blocks <= 128u && waves % 2u == 0 && waves >= 4u;
+    const uint32_t nt = kb == 1u ? 2u : 1u;
+    return (rows + 16u * nt - 1u) / (16u * nt) <= 128u && ks_ranges(in / 256u, rows) != 0;
+}
+
+bool matvec_mfma_takes(uint32_t type, uint32_t in, uint32_t batch, uint32_t rows) {
+    if (batch >= 5u) return matvec_mfma_blocks_per_wave(type, in, batch) != 0;
+    return batch == 4u && ks_takes(type, in, rows);
+}
+
+size_t matvec_mfma_partial_floats(uint32_t type, uint32_t in, uint32_t batch, uint32_t rows) {
+    if (!ks_takes(type, in, rows)) return 0;
+    const uint32_t nb = in / 256u, slices = nb / ks_ranges(nb, rows);
+    return slices > 1u ? static_cast<size_t>(slices) * batch * rows : 0u;
 }
 
 hipError_t launch_matvec_mfma(uint32_t type, const uint8_t* W, uint32_t rows, uint32_t in,
-                              const float* x, float* y, uint32_t batch, hipStream_t s) {
+                              const float* x, float* y, uint32_t batch, hipStream_t s,
+                              float* partial) {
     const uint32_t kb = mfma_kb(type, in);
     const uint32_t nb = in / 256u;
+    if (ks_takes(type, in, rows)) {
+        switch (type) {
+            case T_Q4_K: return launch_ks_t<T_Q4_K>(W, nb, rows, x, y, batch, partial, s);
+            case T_Q5_K: return launch_ks_t<T_Q5_K>(W, nb, rows, x, y, batch, partial, s);
+            case T_Q6_K: return launch_ks_t<T_Q6_K>(W, nb, rows, x, y, batch, partial, s);
+            case T_Q8_0: return launch_ks_t<T_Q8_0>(W, nb, rows, x, y, batch, partial, s);
+            case T_Q4_0: return launch_ks_t<T_Q4_0>(W, nb, rows, x, y, batch, partial, s);
+            default: return hipErrorInvalidValue;
+        }
+    }
     switch (type) {
         case T_Q4_K: return launch_t<T_Q4_K>(kb, W, nb, rows, x, y, batch, s);
         case T_Q5_K: return launch_t<T_Q5_K>(kb, W, nb, rows, x, y, batch, s);

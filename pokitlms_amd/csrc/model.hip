@@ -538,7 +538,7 @@ hipError_t launch_model_step(const ModelArgs& a, const ModelLayer* layers, bool 
     };
     auto matvec = [&](uint32_t type, const uint8_t* W, uint64_t row_bytes, uint32_t rows,
                       uint32_t in, const float* x, float* y) -> hipError_t {
-        return launch_matvec(type, W, row_bytes, rows, in, x, y, 1, s);
+        return launch_matvec(type, W, row_bytes, rows, in, x, y, 1, s, nullptr);
     };
     for (uint32_t l = 0; l < a.layers; ++l) {
         const ModelLayer& L = layers[l];

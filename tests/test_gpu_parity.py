@@ -235,6 +235,63 @@ def test_mfma_batched_widths(hip, port, gtype):
         wt.release()
 
 
+@pytest.mark.parametrize("gtype", (S.Q4_K, S.Q5_K, S.Q6_K, S.Q8_0, S.Q4_0))
+def test_mfma_k_sliced_shapes(hip, port, gtype):
+    """The K-sliced MFMA kernel (grids of at most 128 row groups) with two,
+    three and four 256-value ranges per workgroup (2000x4096, 2048x6144,
+    2048x8192: 8, 8 and 8 K slices added in slice order by the reduce
+    launch), a partial last row group, and 4, 5 and 8 vectors; every vector
+    against the CPU's linear."""
+    g = S.rng(911 + gtype)
+    for rows, inn in ((2000, 4096), (2048, 6144), (2048, 8192)):
+        w = S.quant_matrix(gtype, rows, inn, g)
+        wt = hip.upload(gtype, inn, rows, w)
+        for batch in (4, 5, 8):
+            x = S.normal_f32(g, batch * inn).reshape(batch, inn)
+            gpu = hip.matvec(wt, x)
+            for b in range(batch):
+                cpu = port.linear(gtype, w, inn, rows, x[b])
+                err = normwise_rel(gpu[b], cpu)
+                assert err <= TOL, (rows, inn, batch, b, err)
+            say("k-sliced matvec", gtype, rows, inn, batch, "ok")
+        wt.release()
+
+
+def test_k_sliced_matvec_in_a_graph(hip):
+    """A batched matvec on the K-sliced kernel captured into a HIP graph
+    straight after the upload (its partial-sum scratch was reserved then, so
+    the capture allocates nothing): every replay, with eager work and host
+    synchronisations between them, equals the eager result bit for bit."""
+    import torch
+    g = S.rng(4242)
+    rows, inn, batch = 2048, 6144, 8
+    w = S.quant_matrix(S.Q4_K, rows, inn, g)
+    wt = hip.upload(S.Q4_K, inn, rows, w)
+    dev = torch.device("cuda:0")
+    x = torch.from_numpy(S.normal_f32(g, batch * inn).reshape(batch, inn)).to(dev)
+    y = torch.full((batch, rows), float("nan"), device=dev)
+    stream = torch.cuda.Stream()
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        hip.matvec_async(wt, x.data_ptr(), batch, y.data_ptr(), torch.cuda.current_stream().cuda_stream)
+    eager = torch.empty_like(y)
+    with torch.cuda.stream(stream):
+        hip.matvec_async(wt, x.data_ptr(), batch, eager.data_ptr(), stream.cuda_stream)
+    torch.cuda.synchronize()
+    want = eager.cpu().numpy()
+    for _ in range(3):
+        y.fill_(float("nan"))
+        torch.cuda.synchronize()
+        with torch.cuda.stream(stream):
+            graph.replay()
+        torch.cuda.synchronize()
+        got = y.cpu().numpy()
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    del graph
+    wt.release()
+
+
 @pytest.mark.parametrize("gtype", (S.Q4_K, S.Q6_K, S.Q8_0))
 def test_long_matvec_pipelined_rows(hip, port, gtype):
     """Rows enough that every wave walks several row passes (the pipelined
