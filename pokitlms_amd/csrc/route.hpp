@@ -97,19 +97,23 @@ __device__ __forceinline__ uint32_t order_key(float f) {
     return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
 }
 
+// v of the lane CTRL selects, 0 (the identity of an unsigned maximum) in
+// lanes outside ROW_MASK: with that identity the compiler folds the move into
+// the maximum (one v_max_u32_dpp per step instead of a copy, a DPP move and a
+// maximum on the ranking's dependent chain).
 template <int CTRL, int ROW_MASK = 0xf>
-__device__ __forceinline__ uint32_t dpp_keep_u(uint32_t v) {
-    return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(
-        static_cast<int>(v), static_cast<int>(v), CTRL, ROW_MASK, 0xf, false));
+__device__ __forceinline__ uint32_t dpp_u0max(uint32_t v) {
+    return static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0, static_cast<int>(v), CTRL, ROW_MASK,
+                                                             0xf, ROW_MASK == 0xf));
 }
 
 __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
-    v = max(v, dpp_keep_u<0xb1>(v));
-    v = max(v, dpp_keep_u<0x4e>(v));
-    v = max(v, dpp_keep_u<0x141>(v));
-    v = max(v, dpp_keep_u<0x140>(v));
-    v = max(v, dpp_keep_u<0x142, 0xa>(v));
-    v = max(v, dpp_keep_u<0x143, 0xc>(v));
+    v = max(v, dpp_u0max<0xb1>(v));
+    v = max(v, dpp_u0max<0x4e>(v));
+    v = max(v, dpp_u0max<0x141>(v));
+    v = max(v, dpp_u0max<0x140>(v));
+    v = max(v, dpp_u0max<0x142, 0xa>(v));
+    v = max(v, dpp_u0max<0x143, 0xc>(v));
     return static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(v), 63));
 }
 
