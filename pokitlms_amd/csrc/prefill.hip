@@ -996,6 +996,12 @@ __global__ __launch_bounds__(256, 2) void k_expert_gemm(MoePrefillArgs a) {
     gemm_epilogue<TW, DUAL>(a, tr, n0, oslot, acc, acc2);
 }
 
+// Activation stages in flight in k_expert_gemm_w: four register sets (246
+// VGPRs, still two waves per SIMD) took the Zipf batch's gate/up GEMM from
+// 200.6-203.8 to 196.2-197.1 us and down from 140.2-141.5 to 136.6-137.4 us
+// against two sets on one box; eight spill.
+constexpr uint32_t kActSets = 4;
+
 // Q4_K and Q6_K weights: the same tiles and results as k_expert_gemm, with
 // each wave's weight rows in registers (half-block units, one unit ahead) and
 // only the activation planes staged through LDS (two stages; their global
@@ -1053,28 +1059,30 @@ __global__ __launch_bounds__(256, 2) void k_expert_gemm_w(MoePrefillArgs a) {
     gemm_src_w<TW, DUAL>(src, w0, parts, plane, kdim, sums, arow);
     const uint32_t nst = kdim / C::KC, last = nst - 1u;  // a multiple of 8 (kdim % 256 == 0)
     auto stage_k = [&](uint32_t s) { return (s < last ? s : last) * C::KC; };  // tail: harmless reloads
-    GemmPrefetch<TW, DUAL> f0, f1;
-    gemm_load_act_w<TW, DUAL>(f0, src, 0u);
-    gemm_load_act_w<TW, DUAL>(f1, src, stage_k(1u));
-    gemm_store_a<TW, DUAL>(st[0], f0, src);
-    gemm_load_act_w<TW, DUAL>(f0, src, stage_k(2u));
+    // kActSets register sets of activation loads in flight: stage s's live in
+    // f[s % kActSets]; step s computes stage s, stores stage s + 1 and loads
+    // stage s + 1 + kActSets into the set it freed.
+    GemmPrefetch<TW, DUAL> f[kActSets];
+#pragma unroll
+    for (uint32_t i = 0; i < kActSets; ++i) gemm_load_act_w<TW, DUAL>(f[i], src, stage_k(i));
+    gemm_store_a<TW, DUAL>(st[0], f[0], src);
+    gemm_load_act_w<TW, DUAL>(f[0], src, stage_k(kActSets));
     __syncthreads();
     f32x16 acc = {}, acc2 = {};
     BiasPrev bp{0.0f, 0.0f, 0.0f};
-    // Stage s's activations live in f(s % 2); step s computes stage s, stores
-    // stage s + 1 and loads stage s + 3.  Steps 0-3 of an iteration use units
-    // a, steps 4-7 units b; each buffer reloads (two units on) after its last
-    // step, four steps before its next use.
+    // Steps 0-3 of an iteration use units a, steps 4-7 units b; each buffer
+    // reloads (two units on) after its last step, four steps before its next
+    // use.
     for (uint32_t s0 = 0; s0 < nst; s0 += 8u) {
         const uint32_t u0 = s0 / 4u;
 #pragma unroll
         for (uint32_t t = 0; t < 8u; ++t) {
             const uint32_t s = s0 + t;
-            GemmPrefetch<TW, DUAL>& f = (t & 1u) ? f0 : f1;
+            GemmPrefetch<TW, DUAL>& fs = f[(t + 1u) % kActSets];
             if (t < 4u) gemm_compute_w<TW, DUAL>(st[s & 1u], ua0, ua1, 0u, t, acc, acc2, bp);
             else gemm_compute_w<TW, DUAL>(st[s & 1u], ub0, ub1, 1u, t - 4u, acc, acc2, bp);
-            gemm_store_a<TW, DUAL>(st[(s + 1u) & 1u], f, src);
-            gemm_load_act_w<TW, DUAL>(f, src, stage_k(s + 3u));
+            gemm_store_a<TW, DUAL>(st[(s + 1u) & 1u], fs, src);
+            gemm_load_act_w<TW, DUAL>(fs, src, stage_k(s + 1u + kActSets));
             if (t == 3u) {
                 const uint32_t un = u0 + 2u < lastu ? u0 + 2u : lastu;
                 wunit_load<TW>(w0, un, kq, ua0);
