@@ -293,6 +293,80 @@ __device__ __forceinline__ void load_unit_x_staged(const xf32x4* slot, uint32_t 
     }
 }
 
+// Activation pieces of one unit as loaded, before they become a UnitX: a
+// wave issues them ahead of its weight loads and converts them after, since
+// the first use of a load waits for every load issued before it.  NP = Q
+// (every piece of the unit) or Q / 2 (one half of a wave whose two 32-lane
+// halves hold the same units, lane l and lane l + 32 dotting two rows
+// against one vector).
+template <int NP>
+struct XRaw {
+    xf32x4 v[NP];
+};
+
+template <int T, int UB>
+__device__ __forceinline__ void load_x_pieces(const float* x, const UnitPos& p,
+                                              XRaw<x_pieces<T, UB>()>& r) {
+#pragma unroll
+    for (int q = 0; q < x_pieces<T, UB>(); ++q)
+        r.v[q] = *reinterpret_cast<const xf32x4*>(x + piece_col<T, UB>(p, q));
+}
+
+// Half h of the wave loads pieces [h Q/2, (h + 1) Q/2) of its lane's unit.
+template <int T, int UB>
+__device__ __forceinline__ void load_x_half(const float* x, const UnitPos& p, uint32_t h,
+                                            XRaw<x_pieces<T, UB>() / 2>& r) {
+    constexpr int H = x_pieces<T, UB>() / 2;
+    static_assert(x_pieces<T, UB>() % 2 == 0, "pieces split evenly between the halves");
+#pragma unroll
+    for (int i = 0; i < H; ++i) r.v[i] = *reinterpret_cast<const xf32x4*>(x + piece_col<T, UB>(p, h * H + i));
+}
+
+// The UnitX of load_unit_x (same values, same sums) from loaded pieces.
+template <int T, int UB>
+__device__ __forceinline__ void unit_x_sums(UnitX<T, UB, 1>& ux) {
+#pragma unroll
+    for (int r = 0; r < Fmt<T>::RUNS; ++r) {
+        float sum = 0.0f;
+#pragma unroll
+        for (int i = 0; i < UB; i += 4)
+            sum += (ux.v[0][r * UB + i] + ux.v[0][r * UB + i + 1]) +
+                   (ux.v[0][r * UB + i + 2] + ux.v[0][r * UB + i + 3]);
+        ux.s[0][r] = sum;
+    }
+}
+
+template <int T, int UB>
+__device__ __forceinline__ void unit_x_from_pieces(const XRaw<x_pieces<T, UB>()>& r, bool valid,
+                                                   UnitX<T, UB, 1>& ux) {
+#pragma unroll
+    for (int q = 0; q < x_pieces<T, UB>(); ++q)
+#pragma unroll
+        for (int c = 0; c < 4; ++c) ux.v[0][4 * q + c] = valid ? r.v[q][c] : 0.0f;
+    unit_x_sums<T, UB>(ux);
+}
+
+// From the two halves' pieces: v_permlane32_swap exchanges lanes 32..63 of
+// its first operand with lanes 0..31 of its second; with both operands the
+// same register, the first result is half 0's value and the second half 1's,
+// in every lane.  Every activation float so passes the vector load path once
+// per wave instead of twice.
+template <int T, int UB>
+__device__ __forceinline__ void unit_x_from_halves(const XRaw<x_pieces<T, UB>() / 2>& r, bool valid,
+                                                   UnitX<T, UB, 1>& ux) {
+    constexpr int H = x_pieces<T, UB>() / 2;
+#pragma unroll
+    for (int i = 0; i < H; ++i)
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            const uint32_t w = valid ? __float_as_uint(r.v[i][c]) : 0u;
+            const auto sw = __builtin_amdgcn_permlane32_swap(w, w, false, false);
+            ux.v[0][4 * i + c] = __uint_as_float(sw[0]);
+            ux.v[0][4 * H + 4 * i + c] = __uint_as_float(sw[1]);
+        }
+    unit_x_sums<T, UB>(ux);
+}
+
 // ---------------------------------------------------------------------------
 // Unit decode in two phases, so a wave can issue the loads of several rows
 // before it consumes any of them.

@@ -233,19 +233,18 @@ __global__ __launch_bounds__(256) void k_gate_up(MoeDecodeArgs a, uint32_t units
 // (variant 1: wave top_k the shared expert); the workgroup covers
 // kDownPasses * RPP output rows.
 
-template <int T, int UB, int NU, int kDownPasses, bool SHARED>
+template <int T, int UB, int NU, int kDownPasses, bool SHARED, bool HALVES>
 __global__ __launch_bounds__(64 * (kMaxTopK + (SHARED ? 1 : 0))) void k_down(MoeDecodeArgs a,
                                                                             uint32_t units,
                                                                             uint32_t glog2) {
     extern __shared__ float part[];  // [top_k + variant][kDownPasses * RPP]
     trace_stamp(a.trace, 2, 0);
-    const uint32_t lane = threadIdx.x & 63u, k = threadIdx.x >> 6;
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t k = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // a scalar: ids[k] is one s_load
     const uint32_t G = 1u << glog2, RPP = 64u >> glog2;
     const uint32_t sub = lane >> glog2, ul = lane & (G - 1u);
     const bool shared = SHARED && k >= a.top_k;
     uint64_t e = shared ? 0u : a.ids[k];
-    const bool ok = shared || e < a.n_experts;  // router error: ids are invalid, output unused
-    if (!ok) e = 0;
     UnitPos pos[NU];
     bool valid[NU];
 #pragma unroll
@@ -254,6 +253,19 @@ __global__ __launch_bounds__(64 * (kMaxTopK + (SHARED ? 1 : 0))) void k_down(Moe
         valid[q] = u < units;
         pos[q] = unit_pos<T, UB>(valid[q] ? u : 0u);
     }
+    // the route's activations first: they do not depend on its expert id, so
+    // they are in flight while the id arrives, and they come back before the
+    // weights (unconditional loads; absent units are zeroed afterwards)
+    const float* act = a.act + k * a.ffn;
+    constexpr int XP = x_pieces<T, UB>() / (HALVES ? 2 : 1);
+    XRaw<XP> xr[NU];
+#pragma unroll
+    for (int q = 0; q < NU; ++q) {
+        if constexpr (HALVES) load_x_half<T, UB>(act, pos[q], sub, xr[q]);
+        else load_x_pieces<T, UB>(act, pos[q], xr[q]);
+    }
+    const bool ok = shared || e < a.n_experts;  // router error: ids are invalid, output unused
+    if (!ok) e = 0;
     const uint8_t* base = shared ? a.shared_down : a.down + e * a.down_slice;
     const uint32_t rows = a.hidden;
     const uint32_t nb = a.ffn / Fmt<T>::BE;  // blocks per down row
@@ -270,9 +282,11 @@ __global__ __launch_bounds__(64 * (kMaxTopK + (SHARED ? 1 : 0))) void k_down(Moe
     }
     trace_stamp(a.trace, 2, 1);
     UnitX<T, UB, 1> ux[NU];
-    const float* act = a.act + k * a.ffn;
 #pragma unroll
-    for (int q = 0; q < NU; ++q) load_unit_x<T, UB, 1>(act, 0, pos[q], valid[q], ux[q]);
+    for (int q = 0; q < NU; ++q) {
+        if constexpr (HALVES) unit_x_from_halves<T, UB>(xr[q], valid[q], ux[q]);
+        else unit_x_from_pieces<T, UB>(xr[q], valid[q], ux[q]);
+    }
     const uint32_t RB = kDownPasses * RPP;
 #pragma unroll
     for (int p = 0; p < kDownPasses; ++p) {
@@ -364,13 +378,18 @@ hipError_t down_t(const MoeDecodeArgs& a, hipStream_t s) {
     const uint32_t blocks = ceil_div(a.hidden, kDownPasses * RPP);
     const uint32_t waves = a.top_k + a.variant;
     const size_t lds = static_cast<size_t>(waves) * kDownPasses * RPP * sizeof(float);
-#define PK_DN(N, SH)                                                                          \
-    hipLaunchKernelGGL((k_down<T, UB, N, kDownPasses, SH>), dim3(blocks), dim3(64u * waves), lds, s, \
-                       a, units, glog2)
-    if (nu == 1 && !a.variant) PK_DN(1, false);
-    else if (nu == 2 && !a.variant) PK_DN(2, false);
-    else if (nu == 1) PK_DN(1, true);
-    else if (nu == 2) PK_DN(2, true);
+#define PK_DN(N, SH, HV)                                                                          \
+    hipLaunchKernelGGL((k_down<T, UB, N, kDownPasses, SH, HV>), dim3(blocks), dim3(64u * waves), lds, \
+                       s, a, units, glog2)
+    const bool halves = glog2 == 5u;  // nu == 1: lanes l and l + 32 hold the same unit
+    if (nu == 1 && !a.variant) {
+        if (halves) PK_DN(1, false, true);
+        else PK_DN(1, false, false);
+    } else if (nu == 2 && !a.variant) PK_DN(2, false, false);
+    else if (nu == 1) {
+        if (halves) PK_DN(1, true, true);
+        else PK_DN(1, true, false);
+    } else if (nu == 2) PK_DN(2, true, false);
     else return hipErrorInvalidValue;
 #undef PK_DN
     return hipGetLastError();
