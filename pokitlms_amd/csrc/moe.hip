@@ -8,8 +8,9 @@
 //     rigorous bound B on how far the CPU's serial, unfused FP32 sum
 //     (src/linear.cpp:26-30, src/simd_kernels.hpp:22) can be from S:
 //         |serial - S| <= u * sum_i |T_i| / (1 - n u),  T_i = exact prefix sums.
-//  2. k_gate_up: wave 0 of every workgroup ranks the experts by S and shares
-//     the result through LDS.  When the intervals [S-B, S+B] prove the
+//  2. k_gate_up: the four waves of every workgroup rank the experts by S
+//     (each expert's rank counted as the number of larger keys) and share
+//     the routed ones through LDS.  When the intervals [S-B, S+B] prove the
 //     top-k set and order, that ranking is the CPU's; otherwise the
 //     workgroup recomputes every expert that could still enter the top-k
 //     with the CPU's exact serial FP32 recurrence and ranks those bit-exact
@@ -98,25 +99,27 @@ __global__ __launch_bounds__(64) void k_router(MoeDecodeArgs a) {
 // 2. Routing + gate/up + SwiGLU.  All (route, row) items share the input x,
 // so one unit mapping (and one register copy of x per lane) serves them all.
 
-// The ranking wave 0 hands to the workgroup.
-struct SharedRoutes {
-    uint32_t sel[kMaxTopK];
-    uint32_t state;  // 0 certified, 1 needs the exact path, 2 a logit is not finite
-    double lo_min_sel;
-};
+// x pieces per thread (float4s of a 256-thread workgroup) for the widest
+// hidden that NU units per lane cover
+template <int T, int UB, int NU>
+constexpr uint32_t gate_up_x_pieces() {
+    constexpr int per_unit = Fmt<T>::BE * UB / Fmt<T>::PRIM;  // elements per unit
+    constexpr int xp = NU * 64 * per_unit / 1024;
+    return xp < 1 ? 1u : xp > static_cast<int>(kXPieces) ? kXPieces : static_cast<uint32_t>(xp);
+}
 
-template <int T, int UB, int NU, int NP, int NS>
+template <int T, int UB, int NU, int NP, int NS, uint32_t XP = gate_up_x_pieces<T, UB, NU>()>
 __global__ __launch_bounds__(256) void k_gate_up(MoeDecodeArgs a, uint32_t units, uint32_t glog2) {
     extern __shared__ __attribute__((aligned(16))) float xs[];  // [hidden]
     __shared__ FallbackShared<128> fb;
-    __shared__ SharedRoutes sr;
+    __shared__ SharedRank<NS> sr;
     trace_stamp(a.trace, 1, 0);
     const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
     const bool first_wave = blockIdx.x == 0 && wave == 0;
-    // x and (wave 0) the routing data go out together; x is stored first
-    const XRegs xr = load_x_regs(a.x, a.hidden);
-    RouteData<NS> rd;
-    if (wave == 0) rd = load_route_data<NS>(a);
+    // x and the routing data go out together; x is stored first
+    const XRegs<XP> xr = load_x_regs<XP>(a.x, a.hidden);
+    const RouteData<NS> rd = load_route_data<NS>(a);
+    const RankData<NS> rk = load_rank_data<NS>(a);
     // everything about this wave's items but the experts, while the loads fly
     const uint32_t G = 1u << glog2, RPP = 64u >> glog2;
     const uint32_t sub = lane >> glog2, ul = lane & (G - 1u);
@@ -143,27 +146,19 @@ __global__ __launch_bounds__(256) void k_gate_up(MoeDecodeArgs a, uint32_t units
         blk0[q] = static_cast<uint64_t>(it % a.ffn) * nb;
     }
     store_x_regs(xs, xr, a.hidden);
-    WaveRoutes<NS> w;
-    if (wave == 0) {
-        w = wave_route<NS>(a, rd);
-        if (lane == 0) {
-#pragma unroll
-            for (uint32_t r = 0; r < kMaxTopK; ++r) sr.sel[r] = w.sel[r];
-            sr.state = !w.finite ? 2u : w.certified ? 0u : 1u;
-            sr.lo_min_sel = w.lo_min_sel;
-        }
-    }
+    wg_rank<NS>(a, rd, rk, sr);
     trace_stamp(a.trace, 1, 1);
     __syncthreads();
+    WaveRoutes<NS> w = wg_certify<NS>(a, rd, sr);
     trace_stamp(a.trace, 1, 2);
-    const uint32_t state = sr.state;  // uniform
+    const uint32_t state = !w.finite ? 2u : w.certified ? 0u : 1u;  // the same in every wave
     if (state == 2u) {
         if (first_wave) flag_router_error(a);
         return;
     }
     uint32_t sel[kMaxTopK];
     if (state == 1u) {  // rare: exact serial logits of the candidates
-        exact_routes<4, 128>(a, sr.lo_min_sel, xs, fb, blockIdx.x == 0);
+        exact_routes<4, 128>(a, w.lo_min_sel, xs, fb, blockIdx.x == 0);
         if (fb.bad) {  // uniform
             if (first_wave) flag_router_error(a);
             return;
@@ -178,7 +173,7 @@ __global__ __launch_bounds__(256) void k_gate_up(MoeDecodeArgs a, uint32_t units
         }
     } else {
 #pragma unroll
-        for (uint32_t r = 0; r < kMaxTopK; ++r) sel[r] = sr.sel[r];
+        for (uint32_t r = 0; r < kMaxTopK; ++r) sel[r] = w.sel[r];
     }
     if (first_wave) write_routes<NS>(a, sel, w.logit);
 

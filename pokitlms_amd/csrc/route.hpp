@@ -97,6 +97,17 @@ __device__ __forceinline__ uint32_t order_key(float f) {
     return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
 }
 
+// Ranking key of expert e (e < 256) with logit f: the top 23 bits of the
+// FP32 order key, then 255 - e in the low byte, so keys are distinct and a
+// larger key means a larger logit or, between logits equal in those bits, a
+// smaller id.  The key only proposes an order: certification checks it
+// against the exact intervals [S - B, S + B], so an order the truncated key
+// gets wrong is never certified and goes to the exact path.  Keys have 31
+// bits, so k > mine is the sign bit of mine - k.
+__device__ __forceinline__ uint32_t route_key(float f, uint32_t e) {
+    return ((order_key(f) >> 1) & ~0xffu) | (255u - e);
+}
+
 // v of the lane CTRL selects, 0 (the identity of an unsigned maximum) in
 // lanes outside ROW_MASK: with that identity the compiler folds the move into
 // the maximum (one v_max_u32_dpp per step instead of a copy, a DPP move and a
@@ -117,6 +128,10 @@ __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
     return static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(v), 63));
 }
 
+// Experts sit in the lane/slot layout e = lane + 64 * slot: NS slots per lane
+// cover up to 64 * NS experts.
+constexpr int slots_for(uint32_t experts) { return experts <= 64 ? 1 : experts <= 128 ? 2 : 4; }
+
 __device__ __forceinline__ double readlane_d(double v, uint32_t lane) {
     const int2 p = __builtin_bit_cast(int2, v);
     int2 r;
@@ -124,10 +139,6 @@ __device__ __forceinline__ double readlane_d(double v, uint32_t lane) {
     r.y = __builtin_amdgcn_readlane(p.y, static_cast<int>(lane));
     return __builtin_bit_cast(double, r);
 }
-
-// Experts sit in the lane/slot layout e = lane + 64 * slot: NS slots per lane
-// cover up to 64 * NS experts.
-constexpr int slots_for(uint32_t experts) { return experts <= 64 ? 1 : experts <= 128 ? 2 : 4; }
 
 // Expert e's entry (e uniform) of a per-lane slot array.
 template <int NS>
@@ -177,13 +188,10 @@ __device__ __forceinline__ RouteData<NS> load_route_data(const MoeDecodeArgs& a)
     return d;
 }
 
-// Top-k by (S desc, id asc) using 32-bit keys (FP32 value with its low byte
-// replaced by 255 - id).  The key only proposes an order: certification
-// below checks it against the exact intervals [S - B, S + B], so an ordering
-// the truncated key gets wrong is never certified and goes to the exact
-// path.  top_k selection rounds (a uniform condition per unrolled round),
-// each taking the winner's interval by readlane; then one wave maximum of
-// the unselected experts' upper bounds.
+// Top-k by (S desc, id asc) using route_key, by one wave: top_k selection
+// rounds (a uniform condition per unrolled round), each taking the winner's
+// interval by readlane; then one wave maximum of the unselected experts'
+// upper bounds.
 template <int NS>
 __device__ __forceinline__ WaveRoutes<NS> wave_route(const MoeDecodeArgs& a, const RouteData<NS>& d) {
     const uint32_t lane = threadIdx.x & 63u;
@@ -198,7 +206,7 @@ __device__ __forceinline__ WaveRoutes<NS> wave_route(const MoeDecodeArgs& a, con
         const bool present = e < E;
         const float f = static_cast<float>(d.S[m]);
         fin = fin && (!present || isfinite(f));
-        key[m] = present ? (order_key(f) & ~0xffu) | (255u - e) : 0u;
+        key[m] = present ? route_key(f, e) : 0u;
         lo[m] = d.S[m] - d.B[m];
         hi[m] = d.S[m] + d.B[m];
         w.logit[m] = present ? f : -INFINITY;
@@ -241,6 +249,130 @@ __device__ __forceinline__ WaveRoutes<NS> wave_route(const MoeDecodeArgs& a, con
         after = fmax(after, hi_r[r]);
     }
     w.certified = ok;
+    w.lo_min_sel = lmin;
+    return w;
+}
+
+// The same ranking and certification by a workgroup of four waves, as
+// counts instead of top_k dependent wave maxima: the rank of expert e is the
+// number of experts whose key exceeds its key.  Wave w ranks experts
+// 32 w + (lane & 31) + 128 p; each 32-lane half of the wave compares against
+// half of the keys, read back from the wave's own LDS row (written and read
+// by one wave, so no workgroup barrier), and v_permlane32_swap adds the two
+// halves' counts.  A routed expert's lanes (rank < top_k) store its id, key
+// and interval by rank; after the workgroup's barrier every wave certifies
+// the same ranking from those and its own copy of the routing data.
+template <int NS>
+constexpr int rank_passes() { return NS > 2 ? NS / 2 : 1; }
+
+template <int NS>
+struct SharedRank {
+    alignas(16) uint32_t keys[4][64 * NS];
+    uint32_t sel[kMaxTopK];
+    uint32_t key[kMaxTopK];
+    double lo[kMaxTopK], hi[kMaxTopK];
+};
+
+// S and B of the experts this lane ranks (absent experts re-read expert 0).
+template <int NS>
+struct RankData {
+    double S[rank_passes<NS>()], B[rank_passes<NS>()];
+};
+
+__device__ __forceinline__ uint32_t rank_expert(uint32_t p) {
+    return 128u * p + 32u * (threadIdx.x >> 6) + (threadIdx.x & 31u);
+}
+
+template <int NS>
+__device__ __forceinline__ RankData<NS> load_rank_data(const MoeDecodeArgs& a) {
+    RankData<NS> d;
+#pragma unroll
+    for (int p = 0; p < rank_passes<NS>(); ++p) {
+        const uint32_t e = rank_expert(p);
+        d.S[p] = a.row_sum[e < a.n_experts ? e : 0u];
+        d.B[p] = a.row_bound[e < a.n_experts ? e : 0u];
+    }
+    return d;
+}
+
+// Before the workgroup barrier: this wave's ranks; routed experts into sr.
+template <int NS>
+__device__ __forceinline__ void wg_rank(const MoeDecodeArgs& a, const RouteData<NS>& d,
+                                        const RankData<NS>& rk, SharedRank<NS>& sr) {
+    constexpr uint32_t HK = 32u * NS;  // keys per half
+    const uint32_t lane = threadIdx.x & 63u, E = a.n_experts, K = a.top_k;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    uint32_t* kw = sr.keys[wave];
+#pragma unroll
+    for (int m = 0; m < NS; ++m) {
+        const uint32_t e = lane + 64u * m;
+        kw[e] = e < E ? route_key(static_cast<float>(d.S[m]), e) : 0u;
+    }
+    // the wave reads what its other lanes wrote: LDS keeps one wave's
+    // accesses in order, the fences keep the compiler from reordering them
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    const uint32_t* kh = kw + HK * (lane >> 5);
+#pragma unroll
+    for (int p = 0; p < rank_passes<NS>(); ++p) {
+        const uint32_t e = rank_expert(p);
+        const bool present = e < E;
+        const uint32_t mine = present ? route_key(static_cast<float>(rk.S[p]), e) : 0u;
+        uint32_t cnt = 0u;
+#pragma unroll
+        for (uint32_t i = 0; i < HK; i += 4u) {
+            const u32x4_t k4 = *reinterpret_cast<const u32x4_t*>(kh + i);  // one address per half
+            cnt += ((mine - k4.x) >> 31) + ((mine - k4.y) >> 31);
+            cnt += ((mine - k4.z) >> 31) + ((mine - k4.w) >> 31);
+        }
+        const auto both = __builtin_amdgcn_permlane32_swap(cnt, cnt, false, false);
+        const uint32_t rank = both[0] + both[1];
+        if (lane < 32u && present && rank < K) {
+            sr.sel[rank] = e;
+            sr.key[rank] = mine;
+            sr.lo[rank] = rk.S[p] - rk.B[p];
+            sr.hi[rank] = rk.S[p] + rk.B[p];
+        }
+    }
+}
+
+// After the barrier, in every wave: the routes and their certification, as
+// wave_route gives them.  Rank r is certain when its lower bound clears the
+// upper bound of every expert ranked after it: of the routed ones after it
+// (a chain over the top_k stored intervals), and of every unrouted expert
+// (key below the top_k-th key), which must stay below the smallest routed
+// lower bound.
+template <int NS>
+__device__ __forceinline__ WaveRoutes<NS> wg_certify(const MoeDecodeArgs& a, const RouteData<NS>& d,
+                                                     const SharedRank<NS>& sr) {
+    const uint32_t lane = threadIdx.x & 63u, E = a.n_experts, K = a.top_k;
+    WaveRoutes<NS> w;
+    double after = -INFINITY, lmin = INFINITY;
+    bool ok = true;
+#pragma unroll
+    for (int r = kMaxTopK - 1; r >= 0; --r) {
+        const bool routed = static_cast<uint32_t>(r) < K;
+        w.sel[r] = routed ? sr.sel[r] : 0u;
+        const double lo = routed ? sr.lo[r] : INFINITY, hi = routed ? sr.hi[r] : -INFINITY;
+        ok = ok && (!routed || lo > after);
+        lmin = fmin(lmin, lo);
+        after = fmax(after, hi);
+    }
+    const uint32_t kth = sr.key[K - 1u];
+    bool fin = true, below = true;
+#pragma unroll
+    for (int m = 0; m < NS; ++m) {
+        const uint32_t e = lane + 64u * m;
+        const bool present = e < E;
+        const float f = static_cast<float>(d.S[m]);
+        fin = fin && (!present || isfinite(f));
+        const bool unrouted = present && route_key(f, e) < kth;
+        below = below && (!unrouted || d.S[m] + d.B[m] < lmin);
+        w.logit[m] = present ? f : -INFINITY;
+    }
+    w.finite = __all(fin);
+    w.certified = ok && __all(below);
     w.lo_min_sel = lmin;
     return w;
 }
@@ -517,8 +649,9 @@ __device__ __forceinline__ void flag_router_error(const MoeDecodeArgs& a) {
 // i * blockDim + threadIdx, i < kXPieces (hidden <= 4 * 256 * kXPieces).  All
 // loads are issued before any is used.
 constexpr uint32_t kXPieces = 8;  // hidden <= 8192, the widest router (32 * 256)
+template <uint32_t XP = kXPieces>  // pieces per thread: hidden <= 1024 * XP
 struct XRegs {
-    float4 v[kXPieces];
+    float4 v[XP];
 };
 
 // Pieces past the end load and store the last piece again (the same values
@@ -530,17 +663,19 @@ __device__ __forceinline__ uint32_t x_piece(uint32_t i, uint32_t n) {
     return k < n ? k : n - 4u;
 }
 
-__device__ __forceinline__ XRegs load_x_regs(const float* x, uint32_t n) {
-    XRegs r;
+template <uint32_t XP = kXPieces>
+__device__ __forceinline__ XRegs<XP> load_x_regs(const float* x, uint32_t n) {
+    XRegs<XP> r;
 #pragma unroll
-    for (uint32_t i = 0; i < kXPieces; ++i)
+    for (uint32_t i = 0; i < XP; ++i)
         r.v[i] = *reinterpret_cast<const float4*>(x + x_piece(i, n));
     return r;
 }
 
-__device__ __forceinline__ void store_x_regs(float* xs, const XRegs& r, uint32_t n) {
+template <uint32_t XP>
+__device__ __forceinline__ void store_x_regs(float* xs, const XRegs<XP>& r, uint32_t n) {
 #pragma unroll
-    for (uint32_t i = 0; i < kXPieces; ++i) *reinterpret_cast<float4*>(xs + x_piece(i, n)) = r.v[i];
+    for (uint32_t i = 0; i < XP; ++i) *reinterpret_cast<float4*>(xs + x_piece(i, n)) = r.v[i];
 }
 
 }  // namespace
