@@ -108,7 +108,9 @@ constexpr uint32_t gate_up_x_pieces() {
     return xp < 1 ? 1u : xp > static_cast<int>(kXPieces) ? kXPieces : static_cast<uint32_t>(xp);
 }
 
-template <int T, int UB, int NU, int NP, int NS, uint32_t XP = gate_up_x_pieces<T, UB, NU>()>
+// G64: every row on the 64 lanes of a wave (glog2 == 6), so the row sums are
+// straight-line DPP code the compiler can interleave.
+template <int T, int UB, int NU, int NP, int NS, bool G64, uint32_t XP = gate_up_x_pieces<T, UB, NU>()>
 __global__ __launch_bounds__(256) void k_gate_up(MoeDecodeArgs a, uint32_t units, uint32_t glog2) {
     extern __shared__ __attribute__((aligned(16))) float xs[];  // [hidden]
     __shared__ FallbackShared<128> fb;
@@ -121,6 +123,7 @@ __global__ __launch_bounds__(256) void k_gate_up(MoeDecodeArgs a, uint32_t units
     const RouteData<NS> rd = load_route_data<NS>(a);
     const RankData<NS> rk = load_rank_data<NS>(a);
     // everything about this wave's items but the experts, while the loads fly
+    if constexpr (G64) glog2 = 6u;
     const uint32_t G = 1u << glog2, RPP = 64u >> glog2;
     const uint32_t sub = lane >> glog2, ul = lane & (G - 1u);
     UnitPos pos[NU];
@@ -214,8 +217,8 @@ __global__ __launch_bounds__(256) void k_gate_up(MoeDecodeArgs a, uint32_t units
                 }
             }
         }
-        const float gs = group_sum_dyn(g[0], G);
-        const float us = group_sum_dyn(u[0], G);
+        const float gs = G64 ? group_sum<64>(g[0]) : group_sum_dyn(g[0], G);
+        const float us = G64 ? group_sum<64>(u[0]) : group_sum_dyn(u[0], G);
         if (live && ul == G - 1u)
             a.act[item[q]] = a.variant ? silu(gs) * us : (gs / (1.0f + expf(-gs))) * us;
     }
@@ -235,7 +238,8 @@ __global__ __launch_bounds__(64 * (kMaxTopK + (SHARED ? 1 : 0))) void k_down(Moe
     extern __shared__ float part[];  // [top_k + variant][kDownPasses * RPP]
     trace_stamp(a.trace, 2, 0);
     const uint32_t lane = threadIdx.x & 63u;
-    const uint32_t k = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // a scalar: ids[k] is one s_load
+    const uint32_t k = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform: scalar bases
+    if constexpr (HALVES) glog2 = 5u;
     const uint32_t G = 1u << glog2, RPP = 64u >> glog2;
     const uint32_t sub = lane >> glog2, ul = lane & (G - 1u);
     const bool shared = SHARED && k >= a.top_k;
@@ -292,7 +296,7 @@ __global__ __launch_bounds__(64 * (kMaxTopK + (SHARED ? 1 : 0))) void k_down(Moe
             for (int q = 0; q < NU; ++q)
                 if (valid[q]) unit_compute<T, UB, 1>(raw[p][q], pos[q], ux[q], acc);
         }
-        const float v = group_sum_dyn(acc[0], G);
+        const float v = HALVES ? group_sum<32>(acc[0]) : group_sum_dyn(acc[0], G);
         if (ul == G - 1u) part[k * RB + p * RPP + sub] = v;
     }
     // variant 1: mixer_output = moe_result + sigmoid(shared gate) * shared output
@@ -349,16 +353,23 @@ hipError_t gate_up_t(const MoeDecodeArgs& a, hipStream_t s) {
     const uint32_t passes = ceil_div((a.top_k + a.variant) * a.ffn, RPP);
     const uint32_t blocks = ceil_div(passes, 4u * kGateUpPasses);
     const size_t lds = a.hidden * sizeof(float);
-#define PK_GU(N, NS)                                                                            \
-    hipLaunchKernelGGL((k_gate_up<T, UB, N, kGateUpPasses, NS>), dim3(blocks), dim3(256), lds, s, a, \
-                       units, glog2)
+#define PK_GU(N, NS, G64)                                                                        \
+    hipLaunchKernelGGL((k_gate_up<T, UB, N, kGateUpPasses, NS, G64>), dim3(blocks), dim3(256), lds, s, \
+                       a, units, glog2)
     const int ns = slots_for(a.n_experts);
-    if (nu == 1 && ns == 1) PK_GU(1, 1);
-    else if (nu == 1 && ns == 2) PK_GU(1, 2);
-    else if (nu == 1 && ns == 4) PK_GU(1, 4);
-    else if (nu == 2 && ns == 1) PK_GU(2, 1);
-    else if (nu == 2 && ns == 2) PK_GU(2, 2);
-    else if (nu == 2 && ns == 4) PK_GU(2, 4);
+    const bool g64 = glog2 == 6u;  // always when nu == 2
+    if (nu == 1 && ns == 1) {
+        if (g64) PK_GU(1, 1, true);
+        else PK_GU(1, 1, false);
+    } else if (nu == 1 && ns == 2) {
+        if (g64) PK_GU(1, 2, true);
+        else PK_GU(1, 2, false);
+    } else if (nu == 1 && ns == 4) {
+        if (g64) PK_GU(1, 4, true);
+        else PK_GU(1, 4, false);
+    } else if (nu == 2 && ns == 1) PK_GU(2, 1, true);
+    else if (nu == 2 && ns == 2) PK_GU(2, 2, true);
+    else if (nu == 2 && ns == 4) PK_GU(2, 4, true);
     else return hipErrorInvalidValue;
 #undef PK_GU
     return hipGetLastError();
