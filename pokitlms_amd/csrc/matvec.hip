@@ -49,8 +49,9 @@ struct Buf {
 // head): two register sets, the next passes' loads issued before the current
 // ones are consumed; past the last pass the extra issue re-reads the current
 // rows (cache hits), so every issue is unconditional and the load counts stay
-// static.
-template <int T, int B, int UB, int NU, bool PIPE>
+// static.  G64: every row on the 64 lanes of a wave (glog2 == 6), so the row
+// sums are straight-line DPP code.
+template <int T, int B, int UB, int NU, bool PIPE, bool G64 = false>
 __global__ __launch_bounds__(max_threads_for<B>()) void k_matvec_q(
     const uint8_t* __restrict__ W, uint32_t nb, const float* __restrict__ x,
     uint32_t x_stride, float* __restrict__ y, uint32_t y_stride, uint32_t rows, uint32_t units,
@@ -61,6 +62,7 @@ __global__ __launch_bounds__(max_threads_for<B>()) void k_matvec_q(
     const uint32_t waves = blockDim.x >> 6;
     const uint32_t groups = waves / S;               // independent row streams per block
     const uint32_t group = wave / S, slice = wave % S;
+    if constexpr (G64) glog2 = 6u;
     const uint32_t G = 1u << glog2, RPP = 64u >> glog2;
     const uint32_t sub = lane >> glog2, ul = lane & (G - 1u);
     const uint64_t nblk = static_cast<uint64_t>(rows) * nb;
@@ -100,7 +102,7 @@ __global__ __launch_bounds__(max_threads_for<B>()) void k_matvec_q(
             for (int k = 0; k < NU; ++k)
                 if (st.valid[k]) unit_compute<T, UB, B>(st.raw[bi][q][k], st.pos[k], st.ux[k], acc);
 #pragma unroll
-            for (int b = 0; b < B; ++b) acc[b] = group_sum_dyn(acc[b], G);
+            for (int b = 0; b < B; ++b) acc[b] = G64 ? group_sum<64>(acc[b]) : group_sum_dyn(acc[b], G);
             if (ul == G - 1u) {
                 if (S == 1) {
                     if (st.live[bi][q]) {
@@ -407,9 +409,14 @@ hipError_t run_q(const Plan& pl, const uint8_t* W, uint32_t nb, uint32_t rows,
     // the overlap gains; Q2_K/Q3_K batches would spill)
     if constexpr (T != T_Q2_K && T != T_Q3_K) {
         if (passes >= 3u * blocks * groups * kPasses && (B == 1 || pl.S >= 8u)) {
-            hipLaunchKernelGGL((k_matvec_q<T, B, UB, NU, true>), dim3(blocks),
-                               dim3(64u * pl.waves_per_block), lds, stream, W, nb, x, in, y, rows,
-                               rows, pl.units, pl.slice_units, pl.S, pl.glog2);
+            if (pl.glog2 == 6u)
+                hipLaunchKernelGGL((k_matvec_q<T, B, UB, NU, true, true>), dim3(blocks),
+                                   dim3(64u * pl.waves_per_block), lds, stream, W, nb, x, in, y, rows,
+                                   rows, pl.units, pl.slice_units, pl.S, pl.glog2);
+            else
+                hipLaunchKernelGGL((k_matvec_q<T, B, UB, NU, true>), dim3(blocks),
+                                   dim3(64u * pl.waves_per_block), lds, stream, W, nb, x, in, y, rows,
+                                   rows, pl.units, pl.slice_units, pl.S, pl.glog2);
             return hipGetLastError();
         }
     }
@@ -439,9 +446,14 @@ hipError_t run_q(const Plan& pl, const uint8_t* W, uint32_t nb, uint32_t rows,
             }
         }
     }
-    hipLaunchKernelGGL((k_matvec_q<T, B, UB, NU, false>), dim3(blocks), dim3(64u * pl.waves_per_block),
-                       lds, stream, W, nb, x, in, y, rows, rows, pl.units, pl.slice_units, pl.S,
-                       pl.glog2);
+    if (pl.glog2 == 6u)
+        hipLaunchKernelGGL((k_matvec_q<T, B, UB, NU, false, true>), dim3(blocks),
+                           dim3(64u * pl.waves_per_block), lds, stream, W, nb, x, in, y, rows, rows,
+                           pl.units, pl.slice_units, pl.S, pl.glog2);
+    else
+        hipLaunchKernelGGL((k_matvec_q<T, B, UB, NU, false>), dim3(blocks), dim3(64u * pl.waves_per_block),
+                           lds, stream, W, nb, x, in, y, rows, rows, pl.units, pl.slice_units, pl.S,
+                           pl.glog2);
     return hipGetLastError();
 }
 
