@@ -18,7 +18,8 @@
 //     probabilities, FP32 renormalisation, as route_experts).  Every (route,
 //     ffn row) pair then dots the gate and up rows of the selected expert
 //     with the register-resident input and stores the SwiGLU activation
-//     g / (1 + expf(-g)) * u (:682-684).
+//     g / (1 + expf(-g)) * u (:682-684; here with the hardware exp2 and
+//     reciprocal).
 //  3. k_down: a workgroup of top_k waves computes one down-row dot per route
 //     and combines them in route order, y = ((0 + p0*o0) + p1*o1) + ...
 //     (:688-690), deterministically and without atomics.
@@ -219,8 +220,11 @@ __global__ __launch_bounds__(256) void k_gate_up(MoeDecodeArgs a, uint32_t units
         }
         const float gs = G64 ? group_sum<64>(g[0]) : group_sum_dyn(g[0], G);
         const float us = G64 ? group_sum<64>(u[0]) : group_sum_dyn(u[0], G);
+        // SwiGLU g / (1 + exp(-g)) * u with the hardware exp2 and reciprocal
+        // (a few ulps from the libm form, inside the fast path's tolerance; the
+        // reference-order kernels keep the CPU's expf and division)
         if (live && ul == G - 1u)
-            a.act[item[q]] = a.variant ? silu(gs) * us : (gs / (1.0f + expf(-gs))) * us;
+            a.act[item[q]] = a.variant ? silu(gs) * us : (gs * __builtin_amdgcn_rcpf(1.0f + __expf(-gs))) * us;
     }
     trace_stamp(a.trace, 1, 4);
 }
