@@ -442,6 +442,44 @@ __device__ __forceinline__ void unit_load(const QRow& r, const UnitPos& p, UnitR
     }
 }
 
+// The two nibble runs of a unit's quant words (low nibbles: run 0, high:
+// run 1) dotted with the activations in element order.  One vector: element
+// pairs (0, 2) and (1, 3) of each word sit in the two halves of a masked word,
+// and a nibble q there is the fp16 subnormal q * 2^-24 (16 q * 2^-24 for the
+// high nibbles, masked in place), which v_fma_mix_f32 widens exactly inside
+// the FMA: the dots are the exact 2^-24 / 2^-20 multiples of the plain q.x
+// sums (same order, same roundings), and the caller scales them back.
+// Several vectors: bytes converted once (dot4) and shared by the vectors.
+template <int UB, int B, int T>
+__device__ __forceinline__ void nibble_dots(const uint32_t (&q)[UB / 4], const UnitX<T, UB, B>& ux,
+                                            float (&dot0)[B], float (&dot1)[B]) {
+#pragma unroll
+    for (int t = 0; t < UB / 4; ++t) {
+        if constexpr (B == 1) {
+            const uint32_t s = q[t] >> 8;
+            const uint32_t l02 = q[t] & 0x000f000fu, l13 = s & 0x000f000fu;
+            const uint32_t h02 = q[t] & 0x00f000f0u, h13 = s & 0x00f000f0u;
+            const float* x0 = &ux.v[0][4 * t];
+            const float* x1 = &ux.v[0][UB + 4 * t];
+            dot0[0] = __builtin_fmaf(half_lo(l02), x0[0], dot0[0]);
+            dot0[0] = __builtin_fmaf(half_lo(l13), x0[1], dot0[0]);
+            dot0[0] = __builtin_fmaf(half_hi(l02), x0[2], dot0[0]);
+            dot0[0] = __builtin_fmaf(half_hi(l13), x0[3], dot0[0]);
+            dot1[0] = __builtin_fmaf(half_lo(h02), x1[0], dot1[0]);
+            dot1[0] = __builtin_fmaf(half_lo(h13), x1[1], dot1[0]);
+            dot1[0] = __builtin_fmaf(half_hi(h02), x1[2], dot1[0]);
+            dot1[0] = __builtin_fmaf(half_hi(h13), x1[3], dot1[0]);
+        } else {
+            const uint32_t lo = q[t] & 0x0f0f0f0fu, hi = (q[t] >> 4) & 0x0f0f0f0fu;
+#pragma unroll
+            for (int b = 0; b < B; ++b) {
+                dot0[b] = dot4(lo, &ux.v[b][4 * t], dot0[b]);
+                dot1[b] = dot4(hi, &ux.v[b][UB + 4 * t], dot1[b]);
+            }
+        }
+    }
+}
+
 template <int T, int UB, int B>
 __device__ __forceinline__ void unit_compute(const UnitRaw<T, UB>& r, const UnitPos& p,
                                              const UnitX<T, UB, B>& ux, float (&acc)[B]) {
@@ -451,38 +489,15 @@ __device__ __forceinline__ void unit_compute(const UnitRaw<T, UB>& r, const Unit
     for (int b = 0; b < B; ++b) dot0[b] = dot1[b] = 0.0f;
 
     if constexpr (T == T_Q4_K) {
-        // Element pairs (0, 2) and (1, 3) of each quant word sit in the two
-        // halves of a masked word: a nibble q there is the fp16 subnormal
-        // q * 2^-24 (16 q * 2^-24 for the high nibbles, masked in place), which
-        // v_fma_mix_f32 widens exactly inside the FMA.  The sums are the exact
-        // 2^-24 / 2^-20 multiples of the plain q.x sums (same order, same
-        // roundings), and the scales carry the factors back.
+        // the scales carry nibble_dots' 2^24 / 2^20 factors back (one vector)
         const uint32_t c = p.k0 / 32u;
-#pragma unroll
-        for (int t = 0; t < NW; ++t) {
-            const uint32_t q = r.q[t], s = q >> 8;
-            const uint32_t l02 = q & 0x000f000fu, l13 = s & 0x000f000fu;
-            const uint32_t h02 = q & 0x00f000f0u, h13 = s & 0x00f000f0u;
-#pragma unroll
-            for (int b = 0; b < B; ++b) {
-                const float* x0 = &ux.v[b][4 * t];
-                const float* x1 = &ux.v[b][UB + 4 * t];
-                dot0[b] = __builtin_fmaf(half_lo(l02), x0[0], dot0[b]);
-                dot0[b] = __builtin_fmaf(half_lo(l13), x0[1], dot0[b]);
-                dot0[b] = __builtin_fmaf(half_hi(l02), x0[2], dot0[b]);
-                dot0[b] = __builtin_fmaf(half_hi(l13), x0[3], dot0[b]);
-                dot1[b] = __builtin_fmaf(half_lo(h02), x1[0], dot1[b]);
-                dot1[b] = __builtin_fmaf(half_lo(h13), x1[1], dot1[b]);
-                dot1[b] = __builtin_fmaf(half_hi(h02), x1[2], dot1[b]);
-                dot1[b] = __builtin_fmaf(half_hi(h13), x1[3], dot1[b]);
-            }
-        }
+        nibble_dots<UB, B>(r.q, ux, dot0, dot1);
         uint32_t s0, m0, s1, m1;
         kq_scale_min_pair(r.h, c, s0, m0, s1, m1);
         const float d = half_bits_to_float(r.h[0] & 0xffffu);
         const float dmin = half_bits_to_float(r.h[0] >> 16);
-        const float ds0 = (d * 0x1p24f) * static_cast<float>(s0);
-        const float ds1 = (d * 0x1p20f) * static_cast<float>(s1);
+        const float ds0 = (B == 1 ? d * 0x1p24f : d) * static_cast<float>(s0);
+        const float ds1 = (B == 1 ? d * 0x1p20f : d) * static_cast<float>(s1);
         const float dm0 = dmin * static_cast<float>(m0), dm1 = dmin * static_cast<float>(m1);
 #pragma unroll
         for (int b = 0; b < B; ++b) {
@@ -647,22 +662,13 @@ __device__ __forceinline__ void unit_compute(const UnitRaw<T, UB>& r, const Unit
         for (int b = 0; b < B; ++b)
             acc[b] += __builtin_fmaf(d, dot0[b] + dot1[b], m * (ux.s[b][0] + ux.s[b][1]));
     } else {  // Q4_0
-#pragma unroll
-        for (int t = 0; t < NW; ++t) {
-            const uint32_t q = r.q[t];
-            const uint32_t lo = q & 0x0f0f0f0fu;
-            const uint32_t hi = (q >> 4) & 0x0f0f0f0fu;
-#pragma unroll
-            for (int b = 0; b < B; ++b) {
-                dot0[b] = dot4(lo, &ux.v[b][4 * t], dot0[b]);
-                dot1[b] = dot4(hi, &ux.v[b][UB + 4 * t], dot1[b]);
-            }
-        }
+        nibble_dots<UB, B>(r.q, ux, dot0, dot1);
         const float d = half_bits_to_float(r.d);
+        constexpr float f0 = B == 1 ? 0x1p24f : 1.0f, f1 = B == 1 ? 0x1p20f : 1.0f;
 #pragma unroll
         for (int b = 0; b < B; ++b) {
-            const float t0 = __builtin_fmaf(-8.0f, ux.s[b][0], dot0[b]);
-            const float t1 = __builtin_fmaf(-8.0f, ux.s[b][1], dot1[b]);
+            const float t0 = __builtin_fmaf(-8.0f, ux.s[b][0], dot0[b] * f0);
+            const float t1 = __builtin_fmaf(-8.0f, ux.s[b][1], dot1[b] * f1);
             acc[b] += d * (t0 + t1);
         }
     }
