@@ -367,6 +367,34 @@ __device__ __forceinline__ void unit_x_from_halves(const XRaw<x_pieces<T, UB>() 
     unit_x_sums<T, UB>(ux);
 }
 
+// As load_unit_x_staged, with the run sums from piece sums staged beside the
+// pieces: ps holds this lane's Q piece sums of vector 0 ((v.x + v.y) + (v.z +
+// v.w) of each piece), vector b's 64 * Q floats later.  The run sum adds them
+// in piece order from zero, the same additions as load_unit_x_staged, so the
+// same bits, without every wave repeating them.
+template <int T, int UB, int B = 1>
+__device__ __forceinline__ void load_unit_x_staged_ps(const xf32x4* slot, uint32_t G, const float* ps,
+                                                      UnitX<T, UB, B>& ux) {
+    constexpr int R = Fmt<T>::RUNS, Q = x_pieces<T, UB>();
+#pragma unroll
+    for (int b = 0; b < B; ++b) {
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+            float sum = 0.0f;
+#pragma unroll
+            for (int i = 0; i < UB; i += 4) {
+                const xf32x4 v = slot[(b * Q + r * (UB / 4) + i / 4) * G];
+                ux.v[b][r * UB + i + 0] = v.x;
+                ux.v[b][r * UB + i + 1] = v.y;
+                ux.v[b][r * UB + i + 2] = v.z;
+                ux.v[b][r * UB + i + 3] = v.w;
+                sum += ps[b * 64 * Q + r * (UB / 4) + i / 4];
+            }
+            ux.s[b][r] = sum;
+        }
+    }
+}
+
 // ---------------------------------------------------------------------------
 // Unit decode in two phases, so a wave can issue the loads of several rows
 // before it consumes any of them.

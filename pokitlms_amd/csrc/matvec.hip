@@ -180,15 +180,19 @@ __global__ __launch_bounds__(512) void k_matvec_q_staged(
     const uint8_t* W, uint32_t nb, const float* x, float* y, uint32_t rows, uint32_t units,
     uint32_t slice_units, uint32_t S) {
     // vector b of x starts at b * nb * BE, of y at b * rows
-    // staged x [S][NU][B][Q][64], then partial [waves][kPasses][B] when S > 1
+    // staged x [S][NU][B][Q][64], with one vector its piece sums [S][NU][64][Q]
+    // (batches: the LDS they would take costs occupancy), then partial
+    // [waves][kPasses][B] when S > 1
     extern __shared__ xf32x4 smem[];
+    constexpr bool PS = B == 1;
     constexpr int kPasses = P, Q = x_pieces<T, UB>(), QB = Q * B, XP = NU * QB / XG;
     static_assert(XP * XG == NU * QB, "pieces split evenly over the waves of a slice");
     const uint32_t lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;
     const uint32_t group = wave / S, slice = wave % S;
     const uint64_t nblk = static_cast<uint64_t>(rows) * nb;
     const uint32_t stride = gridDim.x * XG * kPasses;
-    float* partial = reinterpret_cast<float*>(smem + S * NU * QB * 64u);
+    float* psum = reinterpret_cast<float*>(smem + S * NU * QB * 64u);
+    float* partial = psum + (PS ? S * NU * QB * 64u : 0u);
     uint32_t p0 = blockIdx.x * XG * kPasses;
     if (p0 >= rows) return;  // uniform per workgroup
 
@@ -277,12 +281,24 @@ __global__ __launch_bounds__(512) void k_matvec_q_staged(
     // dequantisation of the weights is scheduled, and waited for, above it)
     if (wave < (blockDim.x >> 6)) {
 #pragma unroll
-        for (int j = 0; j < XP; ++j) smem[(slice * (NU * QB) + group * XP + j) * 64u + lane] = xv[j];
+        for (int j = 0; j < XP; ++j) {
+            const uint32_t piece = group * XP + j;  // (k * B + b) * Q + q
+            smem[(slice * (NU * QB) + piece) * 64u + lane] = xv[j];
+            if constexpr (PS)
+                psum[((slice * NU * B + piece / Q) * 64u + lane) * Q + piece % Q] =
+                    (xv[j].x + xv[j].y) + (xv[j].z + xv[j].w);
+        }
         __syncthreads();
     }
 #pragma unroll
-    for (int k = 0; k < NU; ++k)
-        load_unit_x_staged<T, UB, B>(smem + (slice * NU + k) * QB * 64u + lane, 64u, st.ux[k]);
+    for (int k = 0; k < NU; ++k) {
+        const xf32x4* slot = smem + (slice * NU + k) * QB * 64u + lane;
+        if constexpr (PS)
+            load_unit_x_staged_ps<T, UB, B>(slot, 64u, psum + ((slice * NU + k) * B * 64u + lane) * Q,
+                                            st.ux[k]);
+        else
+            load_unit_x_staged<T, UB, B>(slot, 64u, st.ux[k]);
+    }
     finish(p0);
     for (p0 += stride; p0 < rows; p0 += stride) {
         issue(p0);
@@ -384,7 +400,10 @@ hipError_t run_staged(const Plan& pl, const uint8_t* W, uint32_t nb, uint32_t ro
     uint32_t blocks = ceil_div(rows, XG * P);
     const uint32_t max_blocks = 256u * 16u / waves;
     if (blocks > max_blocks) blocks = max_blocks;
-    const size_t lds = xl + (pl.S > 1 ? static_cast<size_t>(waves) * P * B * sizeof(float) : 0);
+    // x pieces, with one vector their sums (a float per 16-byte piece), the
+    // slices' partials
+    const size_t lds = xl + (B == 1 ? xl / 4u : 0u) +
+                       (pl.S > 1 ? static_cast<size_t>(waves) * P * B * sizeof(float) : 0);
     hipLaunchKernelGGL((k_matvec_q_staged<T, B, UB, NU, XG, P>), dim3(blocks), dim3(64u * waves),
                        lds, stream, W, nb, x, y, rows, pl.units, pl.slice_units, pl.S);
     return hipGetLastError();
