@@ -247,7 +247,10 @@ __global__ __launch_bounds__(64 * (kMaxTopK + (SHARED ? 1 : 0))) void k_down(Moe
     const uint32_t G = 1u << glog2, RPP = 64u >> glog2;
     const uint32_t sub = lane >> glog2, ul = lane & (G - 1u);
     const bool shared = SHARED && k >= a.top_k;
-    uint64_t e = shared ? 0u : a.ids[k];
+    // the route's expert id through the scalar cache (constant address space:
+    // written by the previous launch, read-only here)
+    using cu32 = const __attribute__((address_space(4))) uint32_t;
+    uint64_t e = shared ? 0u : ((cu32*)(a.ids))[k];
     UnitPos pos[NU];
     bool valid[NU];
 #pragma unroll
@@ -267,6 +270,7 @@ __global__ __launch_bounds__(64 * (kMaxTopK + (SHARED ? 1 : 0))) void k_down(Moe
         if constexpr (HALVES) load_x_half<T, UB>(act, pos[q], sub, xr[q]);
         else load_x_pieces<T, UB>(act, pos[q], xr[q]);
     }
+    __builtin_amdgcn_sched_barrier(0);  // the activation loads out before the id is waited for
     const bool ok = shared || e < a.n_experts;  // router error: ids are invalid, output unused
     if (!ok) e = 0;
     const uint8_t* base = shared ? a.shared_down : a.down + e * a.down_slice;
