@@ -726,7 +726,10 @@ __global__ __launch_bounds__(256) void k_ref_matvec(RefMatvecArgs a) {
         const uint64_t expert = ref_route_block(a.route, r, leader, rsh);
         ref_load<T>(QRow{W + expert * slice_bytes, nblk, qrow.blk0}, b, raw);
     } else {
-        const uint64_t expert = a.ids ? a.ids[r] : 0u;
+        // the id of an earlier launch, read through the scalar cache (constant
+        // address space: read-only here)
+        using cu32 = const __attribute__((address_space(4))) uint32_t;
+        const uint64_t expert = a.ids ? ((cu32*)(a.ids))[r] : 0u;
         ref_load<T>(QRow{W + expert * slice_bytes, nblk, qrow.blk0}, b, raw);
     }
     const float* x = a.x + static_cast<uint64_t>(r) * a.x_stride;
