@@ -201,6 +201,8 @@ def prefill_leg(torch, hip, layers, stream, reps: int, with_cpu: bool):
         worst = max(worst, float(np.max(np.abs(dy - y[t])) / np.max(np.abs(dy))))
     counts = np.bincount(ids.ravel().astype(np.int64), minlength=128)
     gu_tflops = PREFILL_GEMM_FLOPS["gate_up"] / (phase_us["gate_up"] * 1e-6) / 1e12
+    # rows the 32-row tiles issue per assignment (partly filled last tiles)
+    tile_padding = float(np.sum(32 * ((counts + 31) // 32))) / float(counts.sum())
     whole_tflops = PREFILL_FLOPS / (ms * 1e-3) / 1e12
     out = {
         "workload": "512 tokens x ~ N(0,1) (one direction pinned) through the config-3 layer; "
@@ -213,7 +215,9 @@ def prefill_leg(torch, hip, layers, stream, reps: int, with_cpu: bool):
                      "kernel": "k_expert_gemm<Q4_K, gate/up> (v_mfma_f32_32x32x16_bf16)",
                      "achieved": round(gu_tflops, 2), "peak": MFMA_BF16_PEAK_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(gu_tflops / MFMA_BF16_PEAK_TFLOPS, 4),
-                     "mfma_issued_tflops": round(SPLIT_PASSES * gu_tflops, 2),
+                     # issued = algorithmic x three bf16 planes x tile padding
+                     "mfma_issued_tflops": round(SPLIT_PASSES * tile_padding * gu_tflops, 2),
+                     "tile_padding": round(tile_padding, 3),
                      "frac_of_fp32_mfma_peak": round(gu_tflops / MFMA_F32_PEAK_TFLOPS, 4),
                      "avg_us": round(phase_us["gate_up"], 2),
                      "algorithmic_flops": PREFILL_GEMM_FLOPS["gate_up"]},
