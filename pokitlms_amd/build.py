@@ -25,9 +25,14 @@ EXPF_TABLE = os.path.join(HERE, "libm_expf.bin")
 # -ffp-contract=off: every fused multiply-add is written out (fmaf), so the
 # bit-exact router recurrence and the reference's unfused orders stay intact.
 # The target-feature switch keeps hipcc from emitting packed-FP32 VALU ops.
+# Kernel-argument preloading: the leading scalar and pointer arguments of a
+# kernel arrive in SGPRs with the wave instead of through a load of the
+# argument block (the code object keeps the loading path for firmware that
+# does not preload).
 HIP_FLAGS = [
     "--offload-arch=gfx950", "-O3", "-std=c++20", "-fPIC", "-ffp-contract=off",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-mllvm", "-amdgpu-kernarg-preload-count=16",
     "-Wall", "-Wno-unused-function", "-Wno-unknown-pragmas",
 ]
 

@@ -236,9 +236,18 @@ __global__ __launch_bounds__(256) void k_gate_up(MoeDecodeArgs a, uint32_t units
 // kDownPasses * RPP output rows.
 
 template <int T, int UB, int NU, int kDownPasses, bool SHARED, bool HALVES>
-__global__ __launch_bounds__(64 * (kMaxTopK + (SHARED ? 1 : 0))) void k_down(MoeDecodeArgs a,
-                                                                            uint32_t units,
-                                                                            uint32_t glog2) {
+__global__ __launch_bounds__(64 * (kMaxTopK + (SHARED ? 1 : 0))) void k_down(
+    const uint32_t* ids, const float* act_in, const uint8_t* down, uint64_t down_slice, uint32_t ffn,
+    uint32_t n_experts, uint32_t units, uint32_t glog2, MoeDecodeArgs a) {
+    // The fields the first loads need lead the argument list: they arrive in
+    // SGPRs with the waves (kernel-argument preloading), not after a load of
+    // the argument block.
+    a.ids = const_cast<uint32_t*>(ids);
+    a.act = const_cast<float*>(act_in);
+    a.down = down;
+    a.down_slice = down_slice;
+    a.ffn = ffn;
+    a.n_experts = n_experts;
     extern __shared__ float part[];  // [top_k + variant][kDownPasses * RPP]
     trace_stamp(a.trace, 2, 0);
     const uint32_t lane = threadIdx.x & 63u;
@@ -394,7 +403,7 @@ hipError_t down_t(const MoeDecodeArgs& a, hipStream_t s) {
     const size_t lds = static_cast<size_t>(waves) * kDownPasses * RPP * sizeof(float);
 #define PK_DN(N, SH, HV)                                                                          \
     hipLaunchKernelGGL((k_down<T, UB, N, kDownPasses, SH, HV>), dim3(blocks), dim3(64u * waves), lds, \
-                       s, a, units, glog2)
+                       s, a.ids, a.act, a.down, a.down_slice, a.ffn, a.n_experts, units, glog2, a)
     const bool halves = glog2 == 5u;  // nu == 1: lanes l and l + 32 hold the same unit
     if (nu == 1 && !a.variant) {
         if (halves) PK_DN(1, false, true);
