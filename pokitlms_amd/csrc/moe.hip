@@ -237,13 +237,13 @@ __global__ __launch_bounds__(256) void k_gate_up(MoeDecodeArgs a, uint32_t units
 
 template <int T, int UB, int NU, int kDownPasses, bool SHARED, bool HALVES>
 __global__ __launch_bounds__(64 * (kMaxTopK + (SHARED ? 1 : 0))) void k_down(
-    const uint32_t* ids, const float* act_in, const uint8_t* down, uint64_t down_slice, uint32_t ffn,
+    uint32_t* ids, float* act_in, const uint8_t* down, uint64_t down_slice, uint32_t ffn,
     uint32_t n_experts, uint32_t units, uint32_t glog2, MoeDecodeArgs a) {
     // The fields the first loads need lead the argument list: they arrive in
     // SGPRs with the waves (kernel-argument preloading), not after a load of
     // the argument block.
-    a.ids = const_cast<uint32_t*>(ids);
-    a.act = const_cast<float*>(act_in);
+    a.ids = ids;
+    a.act = act_in;
     a.down = down;
     a.down_slice = down_slice;
     a.ffn = ffn;
