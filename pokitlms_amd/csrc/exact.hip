@@ -916,11 +916,8 @@ __global__ __launch_bounds__(1024) void k_ref_rmsnorm(float* x, RefResidual res,
 // current position's k and v come from LDS, older ones from the ring: each
 // FP16 K row loaded whole (HD / 8 16-byte loads), V rows staged through LDS a
 // tile of positions at a time.
-// FAST (the bandwidth-optimised decode step): the device's expf instead of
-// the reference's (an FP64 exp and two table loads from global memory per
-// position, a memory round trip in the middle of the kernel).
 constexpr uint32_t kAttnTileBytes = 64u * 1024u;
-template <int HD, bool FAST>
+template <int HD>
 __global__ __launch_bounds__(256) void k_ref_attention(ModelArgs a, ModelLayer L) {
     extern __shared__ __attribute__((aligned(64))) float lds[];  // sc [chain_floats(capacity)], V tile
     __shared__ float qv[HD], kcur[HD], sqq[HD], sqk[HD];
@@ -1019,7 +1016,7 @@ __global__ __launch_bounds__(256) void k_ref_attention(ModelArgs a, ModelLayer L
     const float mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
     for (uint32_t i = tid; i < n; i += 256u) {
         const float e = __fsub_rn(sc[i], mx);
-        sc[i] = FAST ? expf(e) : expf_libm(e, a.expf);
+        sc[i] = expf_libm(e, a.expf);
     }
     __syncthreads();
     if (tid == 0) s_den = serial_sum(sc, n, 0.0f);
@@ -1062,6 +1059,187 @@ __global__ __launch_bounds__(256) void k_ref_attention(ModelArgs a, ModelLayer L
     }
     if (tid < HD) a.att[h * HD + tid] = o;
 }
+
+// Fast-mode attention (no parity claim; within 1e-4 of the reference's
+// KvCache::attend, src/kv_cache.cpp:185-294): the same q/k head norms, RoPE
+// and FP16 KV ring as k_ref_attention, with every sum reassociated into
+// parallel partial sums except the norms' sums of squares, kept serial so
+// that the FP16 k of the ring rounds as the reference's.  One workgroup of
+// four waves per q head:
+//  * scores: one position per thread, four interleaved partial dots;
+//  * maximum and denominator: workgroup reductions;
+//  * output: interleaved position streams with 16-byte V loads, their
+//    partial sums added through LDS.
+__device__ __forceinline__ float wave_sum_f(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+    return v;
+}
+__device__ __forceinline__ float wave_max_f(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+    return v;
+}
+
+template <int HD>
+__global__ __launch_bounds__(256) void k_fast_attention(ModelArgs a, ModelLayer L) {
+    extern __shared__ __attribute__((aligned(64))) float lds[];  // scores [capacity]
+    __shared__ float qv[HD], kcur[HD], sq[2][HD], part[4u * (64u / (HD / 8))][HD], red[2][4];
+    __shared__ __attribute__((aligned(16))) uint16_t vcur[HD];
+    constexpr uint32_t HALF = HD / 2u;
+    const uint32_t h = blockIdx.x, tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
+    const uint32_t group = a.heads / a.kv_heads, kvh = h / group;
+    const uint32_t pos = a.state[0], slot_now = pos % a.capacity;
+    const uint32_t n = pos + 1u < a.capacity ? pos + 1u : a.capacity;
+    const uint32_t first = pos + 1u - n;
+    const uint64_t row_halves = static_cast<uint64_t>(a.kv_heads) * HD;
+    float* sc = lds;
+    const uint32_t d = tid < HD ? tid : 0u, dp = d % HALF;
+    const float* cs = a.rope_table + static_cast<uint64_t>(pos) * HD;
+    const float qx = a.q[h * HD + d], kx = a.k[kvh * HD + d], vx = a.v[kvh * HD + d];
+    const float qw = L.q_norm[d], kw = L.k_norm[d], c0 = cs[dp], s0 = cs[HALF + dp];
+    // the sums of squares in the reference's serial order (two threads at
+    // once): the FP16 rounding of this position's k then matches the
+    // reference's, and the ring holds the same k for later positions
+    if (tid < HD) {
+        sq[0][tid] = __fmul_rn(qx, qx);
+        sq[1][tid] = __fmul_rn(kx, kx);
+    }
+    __syncthreads();
+    if (tid == 0u || tid == 64u) {
+        const float* v = sq[tid == 0u ? 0 : 1];
+        float sum = 0.0f;
+        for (uint32_t i = 0; i < HD; ++i) sum = __fadd_rn(sum, v[i]);
+        red[tid == 0u ? 0 : 1][0] = sum;
+    }
+    __syncthreads();
+    const float qs = 1.0f / sqrtf(red[0][0] / static_cast<float>(HD) + a.rms_eps);
+    const float ks = 1.0f / sqrtf(red[1][0] / static_cast<float>(HD) + a.rms_eps);
+    __syncthreads();  // the squares read before the normed values replace them
+    if (tid < HD) {
+        sq[0][tid] = qx * qs * qw;
+        sq[1][tid] = kx * ks * kw;
+    }
+    __syncthreads();
+    if (tid < HD) {  // RoPE on (d, d + HD / 2) pairs, the current position's FP16 k and v
+        float rq, rk;
+        if (tid < HALF) {
+            rq = sq[0][tid] * c0 - sq[0][tid + HALF] * s0;
+            rk = sq[1][tid] * c0 - sq[1][tid + HALF] * s0;
+        } else {
+            rq = sq[0][tid] * c0 + sq[0][dp] * s0;
+            rk = sq[1][tid] * c0 + sq[1][dp] * s0;
+        }
+        const uint16_t kb = __half_as_ushort(__float2half_rn(rk));
+        const uint16_t vb = __half_as_ushort(__float2half_rn(vx));
+        qv[tid] = rq;
+        kcur[tid] = __half2float(__ushort_as_half(kb));
+        vcur[tid] = vb;
+        if (h % group == 0u) {
+            L.kcache[static_cast<uint64_t>(slot_now) * row_halves + kvh * HD + tid] = kb;
+            L.vcache[static_cast<uint64_t>(slot_now) * row_halves + kvh * HD + tid] = vb;
+        }
+    }
+    __syncthreads();
+    // scores, one position per thread (four partial dots), and their maximum
+    float m = -INFINITY;
+    for (uint32_t i = tid; i < n; i += 256u) {
+        float p0 = 0.0f, p1 = 0.0f, p2 = 0.0f, p3 = 0.0f;
+        if (i + 1u == n) {
+#pragma unroll 8
+            for (uint32_t e = 0; e < HD; e += 4u) {
+                p0 = __builtin_fmaf(qv[e], kcur[e], p0);
+                p1 = __builtin_fmaf(qv[e + 1u], kcur[e + 1u], p1);
+                p2 = __builtin_fmaf(qv[e + 2u], kcur[e + 2u], p2);
+                p3 = __builtin_fmaf(qv[e + 3u], kcur[e + 3u], p3);
+            }
+        } else {
+            const uint32_t slot = (first + i) % a.capacity;
+            const u32x4_t* kr = reinterpret_cast<const u32x4_t*>(L.kcache + slot * row_halves + kvh * HD);
+            u32x4_t kwv[HD / 8];
+#pragma unroll
+            for (int j = 0; j < HD / 8; ++j) kwv[j] = kr[j];
+#pragma unroll
+            for (int j = 0; j < HD / 8; ++j) {
+                const uint32_t w4[4] = {kwv[j].x, kwv[j].y, kwv[j].z, kwv[j].w};
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const float k0 = __half2float(__ushort_as_half(static_cast<uint16_t>(w4[e] & 0xffffu)));
+                    const float k1 = __half2float(__ushort_as_half(static_cast<uint16_t>(w4[e] >> 16)));
+                    if (e & 1) {
+                        p2 = __builtin_fmaf(qv[8 * j + 2 * e], k0, p2);
+                        p3 = __builtin_fmaf(qv[8 * j + 2 * e + 1], k1, p3);
+                    } else {
+                        p0 = __builtin_fmaf(qv[8 * j + 2 * e], k0, p0);
+                        p1 = __builtin_fmaf(qv[8 * j + 2 * e + 1], k1, p1);
+                    }
+                }
+            }
+        }
+        const float sv = ((p0 + p1) + (p2 + p3)) * a.attn_scale;
+        sc[i] = sv;
+        m = fmaxf(m, sv);
+    }
+    m = wave_max_f(m);
+    if (lane == 0u) red[0][wave] = m;
+    __syncthreads();
+    const float mx = fmaxf(fmaxf(red[0][0], red[0][1]), fmaxf(red[0][2], red[0][3]));
+    float den = 0.0f;
+    for (uint32_t i = tid; i < n; i += 256u) {
+        const float e = expf(sc[i] - mx);
+        sc[i] = e;
+        den += e;
+    }
+    den = wave_sum_f(den);
+    __syncthreads();  // every score exponentiated, and red[0] read
+    if (lane == 0u) red[1][wave] = den;
+    __syncthreads();
+    const float inv = 1.0f / (red[1][0] + red[1][1] + red[1][2] + red[1][3]);
+    // output: LP = HD / 8 lanes hold one position's row (8 dimensions, one
+    // 16-byte load each), so a wave reads 64 / LP positions per load and the
+    // workgroup runs S = 4 * 64 / LP interleaved position streams; batches of
+    // U positions per stream have every load issued (unconditional, clamped
+    // to a valid row) before any is used; the streams' sums meet in LDS.
+    constexpr uint32_t LP = HD / 8, S = 4u * (64u / LP), U = 8;
+    const uint32_t stream = tid / LP, d0 = 8u * (tid % LP);
+    float acc[8];
+#pragma unroll
+    for (uint32_t j = 0; j < 8; ++j) acc[j] = 0.0f;
+    const uint16_t* vbase = L.vcache + kvh * HD + d0;
+    for (uint32_t i0 = stream; i0 < n; i0 += S * U) {
+        u32x4_t raw[U];
+#pragma unroll
+        for (uint32_t u = 0; u < U; ++u) {
+            const uint32_t i = i0 + S * u, ic = i < n ? i : i0;
+            raw[u] = *reinterpret_cast<const u32x4_t*>(vbase + ((first + ic) % a.capacity) * row_halves);
+        }
+#pragma unroll
+        for (uint32_t u = 0; u < U; ++u) {
+            const uint32_t i = i0 + S * u;
+            if (i < n) {
+                const float p = sc[i];
+                const bool now = i + 1u == n;  // the current position: its LDS copy
+                const u32x4_t w = now ? *reinterpret_cast<const u32x4_t*>(vcur + d0) : raw[u];
+                const uint32_t w4[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+                for (uint32_t j = 0; j < 8; ++j) {
+                    const uint16_t b = static_cast<uint16_t>(w4[j / 2] >> (16 * (j % 2)));
+                    acc[j] = __builtin_fmaf(p, __half2float(__ushort_as_half(b)), acc[j]);
+                }
+            }
+        }
+    }
+#pragma unroll
+    for (uint32_t j = 0; j < 8; ++j) part[stream][d0 + j] = acc[j];
+    __syncthreads();
+    if (tid < HD) {
+        float o = 0.0f;
+#pragma unroll
+        for (uint32_t t = 0; t < S; ++t) o += part[t][tid];
+        a.att[h * HD + tid] = o * inv;
+    }
+}
+
 
 uint32_t ref_block_elems(uint32_t type) {
     return type == T_Q8_0 || type == T_Q4_0 || type == T_Q4_1 || type == T_Q5_0 ||
@@ -1180,24 +1358,26 @@ bool ref_attention_supported(uint32_t head_dim, uint32_t capacity) {
            (chain_floats(capacity) * 4ull + kAttnTileBytes) <= 160ull * 1024u - 8192u;
 }
 
-template <bool FAST>
-hipError_t launch_attention_t(const ModelArgs& a, const ModelLayer& L, hipStream_t s) {
+hipError_t launch_ref_attention(const ModelArgs& a, const ModelLayer& L, hipStream_t s) {
     const size_t lds = chain_floats(a.capacity) * sizeof(float) + kAttnTileBytes;
     switch (a.head_dim) {
-        case 64: hipLaunchKernelGGL((k_ref_attention<64, FAST>), dim3(a.heads), dim3(256), lds, s, a, L); break;
-        case 128: hipLaunchKernelGGL((k_ref_attention<128, FAST>), dim3(a.heads), dim3(256), lds, s, a, L); break;
-        case 256: hipLaunchKernelGGL((k_ref_attention<256, FAST>), dim3(a.heads), dim3(256), lds, s, a, L); break;
+        case 64: hipLaunchKernelGGL(k_ref_attention<64>, dim3(a.heads), dim3(256), lds, s, a, L); break;
+        case 128: hipLaunchKernelGGL(k_ref_attention<128>, dim3(a.heads), dim3(256), lds, s, a, L); break;
+        case 256: hipLaunchKernelGGL(k_ref_attention<256>, dim3(a.heads), dim3(256), lds, s, a, L); break;
         default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
 }
 
-hipError_t launch_ref_attention(const ModelArgs& a, const ModelLayer& L, hipStream_t s) {
-    return launch_attention_t<false>(a, L, s);
-}
-
 hipError_t launch_fast_attention(const ModelArgs& a, const ModelLayer& L, hipStream_t s) {
-    return launch_attention_t<true>(a, L, s);
+    const size_t lds = static_cast<size_t>(a.capacity) * sizeof(float);
+    switch (a.head_dim) {
+        case 64: hipLaunchKernelGGL(k_fast_attention<64>, dim3(a.heads), dim3(256), lds, s, a, L); break;
+        case 128: hipLaunchKernelGGL(k_fast_attention<128>, dim3(a.heads), dim3(256), lds, s, a, L); break;
+        case 256: hipLaunchKernelGGL(k_fast_attention<256>, dim3(a.heads), dim3(256), lds, s, a, L); break;
+        default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
 }
 
 // Six launches per layer; the residual stream alternates between
