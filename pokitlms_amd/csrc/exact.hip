@@ -1018,38 +1018,45 @@ __global__ __launch_bounds__(256) void k_ref_attention(ModelArgs a, ModelLayer L
         const float e = __fsub_rn(sc[i], mx);
         sc[i] = expf_libm(e, a.expf);
     }
-    __syncthreads();
-    if (tid == 0) s_den = serial_sum(sc, n, 0.0f);
-    __syncthreads();
-    const float den = s_den;
-    for (uint32_t i = tid; i < n; i += 256u) sc[i] = __fdiv_rn(sc[i], den);
-    float o = 0.0f;
-    for (uint32_t t0 = 0; t0 < n; t0 += TILE) {
-        const uint32_t tn = n - t0 < TILE ? n - t0 : TILE;
-        __syncthreads();  // previous tile consumed (and, first time, the weights written)
-        // stage V rows t0 .. t0 + tn: HD / 8 16-byte pieces per row
-        constexpr uint32_t PPR = HD / 8;
-        // 8 pieces per thread, every global load unconditional (the current
-        // position reads a ring row and takes the LDS copy instead), so the
-        // pass waits for memory once
+    // stage V rows t0 .. t0 + tn (HD / 8 16-byte pieces per row) with threads
+    // t0th .. t0th + nt - 1: 8 pieces per thread, every global load
+    // unconditional (the current position reads a ring row and takes the LDS
+    // copy instead), so a pass waits for memory once
+    constexpr uint32_t PPR = HD / 8;
+    auto stage = [&](uint32_t t0, uint32_t tn, uint32_t t, uint32_t nt) {
         constexpr int KL = 8;
-        for (uint32_t base = 0; base < tn * PPR; base += 256u * KL) {
+        for (uint32_t base = 0; base < tn * PPR; base += nt * KL) {
             u32x4_t pv[KL];
 #pragma unroll
             for (int k = 0; k < KL; ++k) {
-                const uint32_t q = base + tid + 256u * k, qc = q < tn * PPR ? q : 0u;
+                const uint32_t q = base + t + nt * k, qc = q < tn * PPR ? q : 0u;
                 const uint32_t i = t0 + qc / PPR;
                 const uint32_t slot = (first + i) % a.capacity;
                 pv[k] = reinterpret_cast<const u32x4_t*>(L.vcache + slot * row_halves + kvh * HD)[qc % PPR];
             }
 #pragma unroll
             for (int k = 0; k < KL; ++k) {
-                const uint32_t q = base + tid + 256u * k, qc = q < tn * PPR ? q : 0u;
+                const uint32_t q = base + t + nt * k, qc = q < tn * PPR ? q : 0u;
                 if (t0 + qc / PPR + 1u == n) pv[k] = reinterpret_cast<const u32x4_t*>(vcur)[qc % PPR];
                 if (q < tn * PPR) reinterpret_cast<u32x4_t*>(vt)[q] = pv[k];
             }
         }
-        __syncthreads();
+    };
+    __syncthreads();
+    // the serial denominator by thread 0 while waves 1-3 stage the first V tile
+    if (tid == 0) s_den = serial_sum(sc, n, 0.0f);
+    else if (tid >= 64u) stage(0u, n < TILE ? n : TILE, tid - 64u, 192u);
+    __syncthreads();
+    const float den = s_den;
+    for (uint32_t i = tid; i < n; i += 256u) sc[i] = __fdiv_rn(sc[i], den);
+    float o = 0.0f;
+    for (uint32_t t0 = 0; t0 < n; t0 += TILE) {
+        const uint32_t tn = n - t0 < TILE ? n - t0 : TILE;
+        __syncthreads();  // the weights written (first tile), or the previous tile consumed
+        if (t0 > 0u) {    // uniform
+            stage(t0, tn, tid, 256u);
+            __syncthreads();
+        }
         if (tid < HD) {
             for (uint32_t i = 0; i < tn; ++i) {
                 const float v = __half2float(__ushort_as_half(vt[i * HD + tid]));
