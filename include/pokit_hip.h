@@ -447,6 +447,21 @@ pk_hip_status pk_hip_add_rmsnorm(pk_hip_ctx* ctx, const float* hidden, const flo
                                  float* hidden_out, float* out, char* error_buffer,
                                  size_t error_capacity);
 
+/* The fast decode step's q/k/v projection with the attention norm in its
+ * staging (no counterpart name in the reference; it computes the runner's
+ * `hidden += delta`, rms_norm(hidden, norm_w) and the projection that reads
+ * it, src/qwen3_moe_runner.cpp:614-620,692 and src/rms_norm.cpp:9-27, in one
+ * launch): hidden_out = hidden + delta (delta may be NULL), bit for bit; y =
+ * W . ((hidden_out * scale) * norm_w) with the sum of squares reassociated
+ * as in pk_hip_add_rmsnorm.  Host buffers of the weight's width (hidden,
+ * delta, norm_w, hidden_out) and height (y); a plain matrix.  Returns
+ * PK_HIP_STATUS_UNSUPPORTED where the one-launch kernel does not cover the
+ * type or width (widths up to 4096, a multiple of 4). */
+pk_hip_status pk_hip_matvec_add_rmsnorm(pk_hip_ctx* ctx, const pk_hip_weight* weight,
+                                        const float* hidden, const float* delta,
+                                        const float* norm_w, float eps, float* hidden_out,
+                                        float* y, char* error_buffer, size_t error_capacity);
+
 /* Attention of one layer as the whole-model decode computes it. */
 typedef struct pk_hip_attention_config {
     uint32_t heads, kv_heads, head_dim;  /* head_dim 64, 128 or 256 */

@@ -32,7 +32,7 @@ EXPORTS = (
     "pk_hip_moe_prefill_async", "pk_hip_qwen3moe_create", "pk_hip_qwen3moe_destroy",
     "pk_hip_qwen3moe_generate", "pk_hip_synth_weight", "pk_hip_matvec_reference_order",
     "pk_hip_weight_download", "pk_hip_moe_decode_noalloc", "pk_hip_dequantize_rows",
-    "pk_hip_expf_block_sums", "pk_hip_rmsnorm", "pk_hip_add_rmsnorm", "pk_hip_attention_steps",
+    "pk_hip_expf_block_sums", "pk_hip_rmsnorm", "pk_hip_add_rmsnorm", "pk_hip_matvec_add_rmsnorm", "pk_hip_attention_steps",
     "pk_hip_read_floor_async", "pk_hip_moe_decode_traced_async", "pk_hip_set_libm_expf",
     "pk_hip_moe_decode_reference_order",
 )
@@ -146,6 +146,8 @@ def lib() -> ctypes.CDLL:
                                  ctypes.c_char_p, ctypes.c_size_t]
     L.pk_hip_add_rmsnorm.restype = ctypes.c_int
     L.pk_hip_add_rmsnorm.argtypes = [vp, vp, vp, vp, u32, u32, ctypes.c_float, vp, vp, cp, sz]
+    L.pk_hip_matvec_add_rmsnorm.restype = ctypes.c_int
+    L.pk_hip_matvec_add_rmsnorm.argtypes = [vp, vp, vp, vp, vp, ctypes.c_float, vp, vp, cp, sz]
     L.pk_hip_attention_steps.restype = ctypes.c_int
     L.pk_hip_attention_steps.argtypes = [vp, ctypes.POINTER(AttentionConfig), vp, vp, u32, vp, vp,
                                          vp, vp, cp, sz]

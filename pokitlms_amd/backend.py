@@ -393,6 +393,24 @@ class HipBackend:
                                              out.ctypes.data, err, _ERRBUF), err)
         return h_out, out
 
+    def matvec_add_rmsnorm(self, w: Weight, hidden: np.ndarray, delta, norm_w: np.ndarray,
+                           eps: float):
+        """The fast decode's projection with the norm in its staging:
+        (hidden + delta, W . rms_norm(hidden + delta, norm_w)); delta may be None."""
+        h = np.ascontiguousarray(hidden, dtype=np.float32).reshape(-1)
+        d = None if delta is None else np.ascontiguousarray(delta, dtype=np.float32).reshape(-1)
+        nw = np.ascontiguousarray(norm_w, dtype=np.float32).reshape(-1)
+        if h.size != w.in_features or nw.size != h.size or (d is not None and d.size != h.size):
+            raise ValueError("hidden, delta and norm weight must have the matrix's width")
+        h_out = np.empty_like(h)
+        y = np.empty(w.out_features, dtype=np.float32)
+        err = ctypes.create_string_buffer(_ERRBUF)
+        _raise(_abi.lib().pk_hip_matvec_add_rmsnorm(self.handle, w.handle, h.ctypes.data,
+                                                    None if d is None else d.ctypes.data,
+                                                    nw.ctypes.data, float(eps), h_out.ctypes.data,
+                                                    y.ctypes.data, err, _ERRBUF), err)
+        return h_out, y
+
     def attention_steps(self, heads: int, kv_heads: int, head_dim: int, capacity: int,
                         eps: float, theta: float, q_norm, k_norm, q, k, v,
                         reference_order: bool = False, libm_expf_pairs=None) -> np.ndarray:

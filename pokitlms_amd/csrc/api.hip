@@ -1910,6 +1910,49 @@ pk_hip_status pk_hip_add_rmsnorm(pk_hip_ctx* ctx, const float* hidden, const flo
     });
 }
 
+pk_hip_status pk_hip_matvec_add_rmsnorm(pk_hip_ctx* ctx, const pk_hip_weight* w, const float* hidden,
+                                        const float* delta, const float* norm_w, float eps,
+                                        float* hidden_out, float* y, char* err, size_t cap) {
+    return guarded(ctx, err, cap, [&] {
+        require_usable(ctx);
+        if (!w || !hidden || !norm_w || !hidden_out || !y)
+            throw ArgError("weight, hidden, norm weight and outputs are required");
+        if (w->n_experts) throw ArgError("not a plain matrix");
+        std::lock_guard lock(ctx->mutex);
+        ctx->set_device();
+        const size_t n = w->in;
+        DeviceBuffer<float> buf;
+        try {
+            // hidden | delta | norm weight | hidden_out, 16-byte aligned when n % 4 == 0
+            buf.ensure(4 * n);
+            float* dh = buf.ptr;
+            float* dd = dh + n;
+            float* dw = dd + n;
+            float* dho = dw + n;
+            ctx->y.ensure(w->out);
+            check(hipMemcpyAsync(dh, hidden, n * 4, hipMemcpyHostToDevice, ctx->stream), "copy hidden");
+            if (delta)
+                check(hipMemcpyAsync(dd, delta, n * 4, hipMemcpyHostToDevice, ctx->stream), "copy delta");
+            check(hipMemcpyAsync(dw, norm_w, n * 4, hipMemcpyHostToDevice, ctx->stream), "copy weight");
+            const pk::MatvecNorm nm{delta ? dd : nullptr, dw, dho, eps};
+            const hipError_t e = pk::launch_matvec_norm(w->type, w->dptr, static_cast<uint32_t>(w->out),
+                                                        static_cast<uint32_t>(n), dh, nm, ctx->y.ptr,
+                                                        ctx->stream);
+            if (e == hipErrorNotSupported)
+                throw Unsupported("type/width not covered by the one-launch norm + matvec kernel");
+            launch_checked(e, "matvec_add_rmsnorm launch");
+            check(hipMemcpyAsync(hidden_out, dho, n * 4, hipMemcpyDeviceToHost, ctx->stream), "copy hidden");
+            check(hipMemcpyAsync(y, ctx->y.ptr, w->out * 4, hipMemcpyDeviceToHost, ctx->stream), "copy output");
+            check(hipStreamSynchronize(ctx->stream), "hipStreamSynchronize");
+        } catch (...) {
+            (void)hipStreamSynchronize(ctx->stream);
+            buf.release();
+            throw;
+        }
+        buf.release();
+    });
+}
+
 pk_hip_status pk_hip_attention_steps(pk_hip_ctx* ctx, const pk_hip_attention_config* cfg,
                                      const float* q_norm, const float* k_norm, uint32_t steps,
                                      const float* q, const float* k, const float* v, float* out,

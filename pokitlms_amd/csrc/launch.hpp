@@ -24,6 +24,22 @@ hipError_t launch_matvec(uint32_t type, const uint8_t* W, uint64_t row_bytes, ui
                          hipStream_t stream, float* partial = nullptr);
 size_t matvec_partial_floats(uint32_t type, uint32_t in, uint32_t batch, uint32_t rows);
 
+// One vector whose x is the RMSNorm of h + delta, computed by every workgroup
+// of the matvec in its staging: x = (v * scale) * w with v = h + delta (delta
+// null: v = h) and scale = 1 / sqrt(mean(v^2) + eps); v is written to h_out
+// (device, may be null; not h or delta).  in a multiple of 4, at most 4096.
+struct MatvecNorm {
+    const float* delta;
+    const float* w;
+    float* h_out;
+    float eps;
+};
+// hipErrorNotSupported (nothing launched) where the staged one-vector kernel
+// does not cover (type, in): the caller norms and multiplies separately.
+hipError_t launch_matvec_norm(uint32_t type, const uint8_t* W, uint32_t rows, uint32_t in,
+                              const float* h, const MatvecNorm& nm, float* y,
+                              hipStream_t stream);
+
 // Batched matvecs on MFMA (matvec_mfma.hip): 256-value K ranges per wave for
 // (type, in, batch), 0 where that kernel does not apply; launch_matvec takes
 // it where matvec_mfma_takes says so.
@@ -177,11 +193,11 @@ struct ModelArgs {
     LibmExpf expf;            // reference order: the host libm's expf exceptions
 };
 bool model_supported(const ModelArgs& a);
-// The fast step's residual add + RMSNorm (one workgroup): x += d (d may be
-// null), out = (x * (1 / sqrt(sum(x^2) / n + eps))) * w with the sum of
-// squares reassociated (a block reduction).
+// The fast step's residual add + RMSNorm (one workgroup): v = x + d (d may be
+// null) into xo (null: x itself), out = (v * (1 / sqrt(sum(v^2) / n + eps))) * w
+// with the sum of squares reassociated (a block reduction).
 hipError_t launch_fast_add_rmsnorm(float* x, const float* d, const float* w, float* out, uint32_t n,
-                                   float eps, hipStream_t stream);
+                                   float eps, hipStream_t stream, float* xo = nullptr);
 // logits: run the final norm, head and argmax (else only advance the position).
 hipError_t launch_model_step(const ModelArgs& a, const ModelLayer* layers, bool logits,
                              hipStream_t stream);

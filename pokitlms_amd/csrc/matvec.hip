@@ -175,10 +175,19 @@ __global__ __launch_bounds__(max_threads_for<B>()) void k_matvec_q(
 // order).  W and x are not __restrict__ here: loads the compiler may not take
 // for invariant keep that program order around the barrier.
 
-template <int T, int B, int UB, int NU, int XG, int P>
+//
+// With NORM (one vector, one slice) x is the RMSNorm of h + d instead: every
+// workgroup loads h, d and the norm weights w coalesced, one float4 of each
+// per thread and pass, issues its first weight loads, then sums the squares
+// over the workgroup, writes (v * scale) * w into an LDS row from which the
+// waves take their pieces, and workgroup 0 writes v = h + d to h_out (d null:
+// v = h).  n = nb * BE elements, at most 4096, a multiple of four.
+
+template <int T, int B, int UB, int NU, int XG, int P, bool NORM = false>
 __global__ __launch_bounds__(512) void k_matvec_q_staged(
     const uint8_t* W, uint32_t nb, const float* x, float* y, uint32_t rows, uint32_t units,
-    uint32_t slice_units, uint32_t S) {
+    uint32_t slice_units, uint32_t S, const float* nd, const float* nw, float* h_out,
+    float eps) {
     // vector b of x starts at b * nb * BE, of y at b * rows
     // staged x [S][NU][B][Q][64], with one vector its piece sums [S][NU][64][Q]
     // (batches: the LDS they would take costs occupancy), then partial
@@ -193,6 +202,9 @@ __global__ __launch_bounds__(512) void k_matvec_q_staged(
     const uint32_t stride = gridDim.x * XG * kPasses;
     float* psum = reinterpret_cast<float*>(smem + S * NU * QB * 64u);
     float* partial = psum + (PS ? S * NU * QB * 64u : 0u);
+    static_assert(!NORM || (B == 1 && XG * 64 == 512), "the norm: one vector, 512 threads");
+    constexpr int kNormPasses = NORM ? 2 : 0;  // float4s of h per thread (n <= 4096)
+    float* xs = partial;                       // NORM: the normed row [n] (S == 1: no partials)
     uint32_t p0 = blockIdx.x * XG * kPasses;
     if (p0 >= rows) return;  // uniform per workgroup
 
@@ -262,9 +274,57 @@ __global__ __launch_bounds__(512) void k_matvec_q_staged(
         }
     };
 
+    xf32x4 xv[XP];
+    if constexpr (NORM) {
+        const uint32_t n4 = nb * (Fmt<T>::BE / 4u);
+        xf32x4 hv[kNormPasses], wv[kNormPasses];
+#pragma unroll
+        for (int i = 0; i < kNormPasses; ++i) {
+            const uint32_t c = threadIdx.x + 512u * i, cc = c < n4 ? c : 0u;
+            hv[i] = reinterpret_cast<const xf32x4*>(x)[cc];
+            wv[i] = reinterpret_cast<const xf32x4*>(nw)[cc];
+            if (nd) hv[i] = hv[i] + reinterpret_cast<const xf32x4*>(nd)[cc];
+        }
+        issue(p0);
+        __builtin_amdgcn_sched_barrier(0);
+        float ss = 0.0f;
+#pragma unroll
+        for (int i = 0; i < kNormPasses; ++i) {
+            if (threadIdx.x + 512u * i < n4) {
+                ss += hv[i].x * hv[i].x;
+                ss += hv[i].y * hv[i].y;
+                ss += hv[i].z * hv[i].z;
+                ss += hv[i].w * hv[i].w;
+            }
+        }
+        ss = group_sum<64>(ss);  // the wave's sum in lane 63
+        __shared__ float red[8];
+        if (lane == 63u) red[wave] = ss;
+        __syncthreads();
+        float total = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) total += red[i];
+        const float scale = 1.0f / sqrtf(total / static_cast<float>(4u * n4) + eps);
+#pragma unroll
+        for (int i = 0; i < kNormPasses; ++i) {
+            const uint32_t c = threadIdx.x + 512u * i;
+            if (c < n4) {
+                if (blockIdx.x == 0 && h_out) reinterpret_cast<xf32x4*>(h_out)[c] = hv[i];
+                reinterpret_cast<xf32x4*>(xs)[c] = (hv[i] * scale) * wv[i];
+            }
+        }
+        __syncthreads();
+#pragma unroll
+        for (int j = 0; j < XP; ++j) {
+            const uint32_t piece = group * XP + j, k = piece / Q, q = piece % Q;
+            const uint32_t local = lane + 64u * k;
+            const bool valid = local < slice_units && local < units;
+            xv[j] = *reinterpret_cast<const xf32x4*>(
+                xs + piece_col<T, UB>(unit_pos<T, UB>(valid ? local : 0u), q));
+        }
+    } else {
     // staging loads: unconditional (an absent unit reads unit 0's
     // activations, which no lane uses)
-    xf32x4 xv[XP];
 #pragma unroll
     for (int j = 0; j < XP; ++j) {
         const uint32_t piece = group * XP + j;  // (k, vector, q) of this lane's units
@@ -277,6 +337,7 @@ __global__ __launch_bounds__(512) void k_matvec_q_staged(
     }
     issue(p0);
     __builtin_amdgcn_sched_barrier(0);
+    }
     // (always true: a block of its own ends at the barrier, so no
     // dequantisation of the weights is scheduled, and waited for, above it)
     if (wave < (blockDim.x >> 6)) {
@@ -393,19 +454,23 @@ bool plan_for(uint32_t in, uint32_t batch, int ub, Plan& p) {
 
 // XG row streams of P rows each per workgroup, every stream split over the
 // plan's S waves; the activations (xl bytes) staged once per workgroup.
-template <int T, int B, int UB, int NU, int XG, int P>
+template <int T, int B, int UB, int NU, int XG, int P, bool NORM = false>
 hipError_t run_staged(const Plan& pl, const uint8_t* W, uint32_t nb, uint32_t rows,
-                      const float* x, float* y, uint32_t xl, hipStream_t stream) {
+                      const float* x, float* y, uint32_t xl, hipStream_t stream,
+                      const MatvecNorm* nm = nullptr) {
     const uint32_t waves = XG * pl.S;
     uint32_t blocks = ceil_div(rows, XG * P);
     const uint32_t max_blocks = 256u * 16u / waves;
     if (blocks > max_blocks) blocks = max_blocks;
     // x pieces, with one vector their sums (a float per 16-byte piece), the
-    // slices' partials
+    // slices' partials (with the norm: the normed row)
     const size_t lds = xl + (B == 1 ? xl / 4u : 0u) +
-                       (pl.S > 1 ? static_cast<size_t>(waves) * P * B * sizeof(float) : 0);
-    hipLaunchKernelGGL((k_matvec_q_staged<T, B, UB, NU, XG, P>), dim3(blocks), dim3(64u * waves),
-                       lds, stream, W, nb, x, y, rows, pl.units, pl.slice_units, pl.S);
+                       (pl.S > 1 ? static_cast<size_t>(waves) * P * B * sizeof(float) : 0) +
+                       (NORM ? static_cast<size_t>(nb) * Fmt<T>::BE * sizeof(float) : 0);
+    hipLaunchKernelGGL((k_matvec_q_staged<T, B, UB, NU, XG, P, NORM>), dim3(blocks),
+                       dim3(64u * waves), lds, stream, W, nb, x, y, rows, pl.units, pl.slice_units,
+                       pl.S, NORM ? nm->delta : nullptr, NORM ? nm->w : nullptr,
+                       NORM ? nm->h_out : nullptr, NORM ? nm->eps : 0.0f);
     return hipGetLastError();
 }
 
@@ -530,6 +595,34 @@ hipError_t dispatch_batch_f(uint32_t batch, const uint8_t* W, uint64_t rb, uint3
 #undef PK_F
 }
 
+template <int T, int UB, int NU>
+hipError_t run_norm(const Plan& pl, const uint8_t* W, uint32_t nb, uint32_t rows, const float* h,
+                    const MatvecNorm& nm, float* y, hipStream_t s) {
+    constexpr int kPieces = NU * x_pieces<T, UB>();
+    if constexpr (kPieces % 8 == 0) {
+        const uint32_t xl = kPieces * 64u * 16u;
+        if (xl <= 32768u) return run_staged<T, 1, UB, NU, 8, 1, true>(pl, W, nb, rows, h, y, xl, s, &nm);
+    }
+    return hipErrorNotSupported;
+}
+
+template <int T>
+hipError_t dispatch_norm(const uint8_t* W, uint32_t rows, const float* h, uint32_t in,
+                         const MatvecNorm& nm, float* y, hipStream_t s) {
+    constexpr int UB = unit_bytes_for(1, Fmt<T>::MAXUB, Fmt<T>::RUNS);
+    Plan pl;
+    if (!plan_for<T>(in, 1, UB, pl)) return hipErrorNotSupported;
+    // the staged kernel's one-vector case: one K-slice, eight one-row streams
+    if (pl.glog2 != 6u || pl.S != 1u || pl.waves_per_block != 4u) return hipErrorNotSupported;
+    const uint32_t nb = in / Fmt<T>::BE;
+    if constexpr (Fmt<T>::RUNS * UB > 32) {
+        return run_norm<T, UB, 1>(pl, W, nb, rows, h, nm, y, s);
+    } else {
+        if (pl.nu == 1) return run_norm<T, UB, 1>(pl, W, nb, rows, h, nm, y, s);
+        return run_norm<T, UB, 2>(pl, W, nb, rows, h, nm, y, s);
+    }
+}
+
 template <int T>
 bool supported_q(uint32_t in, uint32_t batch) {
     Plan pl;
@@ -583,6 +676,24 @@ hipError_t launch_matvec(uint32_t type, const uint8_t* W, uint64_t row_bytes, ui
         case T_Q5_K: return dispatch_batch_q<T_Q5_K>(batch, W, row_bytes, rows, x, in, y, stream);
         case T_Q6_K: return dispatch_batch_q<T_Q6_K>(batch, W, row_bytes, rows, x, in, y, stream);
         default: return hipErrorInvalidValue;
+    }
+}
+
+hipError_t launch_matvec_norm(uint32_t type, const uint8_t* W, uint32_t rows, uint32_t in,
+                              const float* h, const MatvecNorm& nm, float* y,
+                              hipStream_t stream) {
+    if (rows == 0 || in == 0 || in % 4u || in > 4096u) return hipErrorNotSupported;
+    if (nm.h_out && (nm.h_out == h || nm.h_out == nm.delta)) return hipErrorInvalidValue;
+    switch (type) {
+        case T_Q4_0: return dispatch_norm<T_Q4_0>(W, rows, h, in, nm, y, stream);
+        case T_Q4_1: return dispatch_norm<T_Q4_1>(W, rows, h, in, nm, y, stream);
+        case T_Q5_0: return dispatch_norm<T_Q5_0>(W, rows, h, in, nm, y, stream);
+        case T_Q5_1: return dispatch_norm<T_Q5_1>(W, rows, h, in, nm, y, stream);
+        case T_Q8_0: return dispatch_norm<T_Q8_0>(W, rows, h, in, nm, y, stream);
+        case T_Q4_K: return dispatch_norm<T_Q4_K>(W, rows, h, in, nm, y, stream);
+        case T_Q5_K: return dispatch_norm<T_Q5_K>(W, rows, h, in, nm, y, stream);
+        case T_Q6_K: return dispatch_norm<T_Q6_K>(W, rows, h, in, nm, y, stream);
+        default: return hipErrorNotSupported;
     }
 }
 

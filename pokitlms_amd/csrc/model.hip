@@ -255,12 +255,13 @@ __global__ __launch_bounds__(256) void k_add_rmsnorm(float* __restrict__ x, cons
 // loads its float4s of x, delta and w at once and keeps them in registers, so
 // the kernel waits for memory once (the loop above reloads x after storing
 // it, and loads w only after the sum).
+// x + delta goes to xo (x itself, or a buffer of its own).
 template <int NI>
-__global__ __launch_bounds__(256) void k_add_rmsnorm4(float* __restrict__ x,
+__global__ __launch_bounds__(256) void k_add_rmsnorm4(const float* x,
                                                       const float* __restrict__ delta,
                                                       const float* __restrict__ w,
                                                       float* __restrict__ out, uint32_t n,
-                                                      float eps) {
+                                                      float eps, float* xo) {
     __shared__ float red[4];
     const uint32_t n4 = n / 4u;
     float4 v[NI], wv[NI];
@@ -293,7 +294,7 @@ __global__ __launch_bounds__(256) void k_add_rmsnorm4(float* __restrict__ x,
     for (int i = 0; i < NI; ++i) {
         const uint32_t c = threadIdx.x + 256u * i;
         if (c < n4) {
-            if (delta) reinterpret_cast<float4*>(x)[c] = v[i];
+            if (delta || xo != x) reinterpret_cast<float4*>(xo)[c] = v[i];
             reinterpret_cast<float4*>(out)[c] =
                 make_float4(v[i].x * scale * wv[i].x, v[i].y * scale * wv[i].y,
                             v[i].z * scale * wv[i].z, v[i].w * scale * wv[i].w);
@@ -488,18 +489,26 @@ hipError_t launch_synth_fill(uint8_t* dst, uint64_t nbytes, uint64_t key, uint32
     return hipGetLastError();
 }
 
+// x + d into xo (default: x), its RMSNorm into out.
 hipError_t launch_fast_add_rmsnorm(float* x, const float* d, const float* w, float* out, uint32_t n,
-                                   float eps, hipStream_t s) {
+                                   float eps, hipStream_t s, float* xo) {
     if (n == 0) return hipErrorInvalidValue;
     const auto al16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; };
     const uint32_t ni = (n + 1023u) / 1024u;
-    if (n % 4u == 0 && ni <= 8u && al16(x) && al16(d) && al16(w) && al16(out)) {
+    if (n % 4u == 0 && ni <= 8u && al16(x) && al16(d) && al16(w) && al16(out) && al16(xo)) {
+        float* o = xo ? xo : x;
         const dim3 g(1), b(256);
-        if (ni == 1u) hipLaunchKernelGGL(k_add_rmsnorm4<1>, g, b, 0, s, x, d, w, out, n, eps);
-        else if (ni == 2u) hipLaunchKernelGGL(k_add_rmsnorm4<2>, g, b, 0, s, x, d, w, out, n, eps);
-        else if (ni <= 4u) hipLaunchKernelGGL(k_add_rmsnorm4<4>, g, b, 0, s, x, d, w, out, n, eps);
-        else hipLaunchKernelGGL(k_add_rmsnorm4<8>, g, b, 0, s, x, d, w, out, n, eps);
+        if (ni == 1u) hipLaunchKernelGGL(k_add_rmsnorm4<1>, g, b, 0, s, x, d, w, out, n, eps, o);
+        else if (ni == 2u) hipLaunchKernelGGL(k_add_rmsnorm4<2>, g, b, 0, s, x, d, w, out, n, eps, o);
+        else if (ni <= 4u) hipLaunchKernelGGL(k_add_rmsnorm4<4>, g, b, 0, s, x, d, w, out, n, eps, o);
+        else hipLaunchKernelGGL(k_add_rmsnorm4<8>, g, b, 0, s, x, d, w, out, n, eps, o);
     } else {
+        if (xo && xo != x) {  // the plain kernel adds in place: copy x to xo first
+            hipError_t err = hipMemcpyAsync(xo, x, static_cast<size_t>(n) * sizeof(float),
+                                            hipMemcpyDeviceToDevice, s);
+            if (err != hipSuccess) return err;
+            x = xo;
+        }
         hipLaunchKernelGGL(k_add_rmsnorm, dim3(1), dim3(256), 0, s, x, d, w, out, n, eps);
     }
     return hipGetLastError();
@@ -542,18 +551,39 @@ hipError_t launch_model_step(const ModelArgs& a, const ModelLayer* layers, bool 
     };
     for (uint32_t l = 0; l < a.layers; ++l) {
         const ModelLayer& L = layers[l];
-        if ((err = norm(delta, L.attn_norm))) return err;
-        if (L.qkv && a.k == a.q + qd && a.v == a.k + kd) {  // q, k and v in one launch
-            if ((err = matvec(L.attn_type, L.qkv, L.q_row, qd + 2u * kd, a.hidden, a.normed, a.q)))
-                return err;
-        } else {
-            if ((err = matvec(L.attn_type, L.q, L.q_row, qd, a.hidden, a.normed, a.q))) return err;
-            if ((err = matvec(L.attn_type, L.k, L.k_row, kd, a.hidden, a.normed, a.k))) return err;
-            if ((err = matvec(L.attn_type, L.v, L.v_row, kd, a.hidden, a.normed, a.v))) return err;
+        const bool qkv = L.qkv && a.k == a.q + qd && a.v == a.k + kd;  // q, k and v in one launch
+        // The attention RMSNorm inside the q/k/v matvec's staging: hidden_state
+        // + delta goes to hidden_alt, and the FFN norm brings hidden_alt +
+        // attn_out back to hidden_state (every workgroup reads hidden_state
+        // while one writes the sum, so the sum needs a buffer of its own).
+        bool fused = false;
+        if (qkv) {
+            const MatvecNorm nm{delta, L.attn_norm, a.hidden_alt, a.rms_eps};
+            err = launch_matvec_norm(L.attn_type, L.qkv, qd + 2u * kd, a.hidden, a.hidden_state, nm,
+                                     a.q, s);
+            if (err != hipSuccess && err != hipErrorNotSupported) return err;
+            fused = err == hipSuccess;
+        }
+        if (!fused) {
+            if ((err = norm(delta, L.attn_norm))) return err;
+            if (qkv) {
+                if ((err = matvec(L.attn_type, L.qkv, L.q_row, qd + 2u * kd, a.hidden, a.normed, a.q)))
+                    return err;
+            } else {
+                if ((err = matvec(L.attn_type, L.q, L.q_row, qd, a.hidden, a.normed, a.q))) return err;
+                if ((err = matvec(L.attn_type, L.k, L.k_row, kd, a.hidden, a.normed, a.k))) return err;
+                if ((err = matvec(L.attn_type, L.v, L.v_row, kd, a.hidden, a.normed, a.v))) return err;
+            }
         }
         if ((err = launch_fast_attention(a, L, s))) return err;
         if ((err = matvec(L.attn_type, L.o, L.o_row, a.hidden, qd, a.att, a.attn_out))) return err;
-        if ((err = norm(a.attn_out, L.ffn_norm))) return err;
+        if (fused) {
+            if ((err = launch_fast_add_rmsnorm(a.hidden_alt, a.attn_out, L.ffn_norm, a.normed,
+                                               a.hidden, a.rms_eps, s, a.hidden_state)))
+                return err;
+        } else if ((err = norm(a.attn_out, L.ffn_norm))) {
+            return err;
+        }
         err = launch_moe_decode(L.moe, s);  // normed -> moe_out
         if (err != hipSuccess) return err;
         delta = L.moe.y;

@@ -7,6 +7,9 @@ shapes (hidden 2048, 32 q heads / 4 kv heads of 128, Q4_K attention rows):
 * the fused q/k/v projection: the q, k and v rows of one layer back to back
   as one 5,120-row matrix in one matvec launch, each part within 1e-4 of the
   oracle's tensor_linear on that part;
+* the same projection with the residual add and attention RMSNorm in its
+  staging (pk_hip_matvec_add_rmsnorm): the residual bit for bit, the
+  projection within 1e-4 of tensor_linear on pko_add_rms_norm's row;
 * the attention stage (q/k head norms, RoPE, FP16 KV ring, attention): the
   fast kernel within 1e-4 normwise of pko_attention_steps (pinned bit for bit
   to the reference's KvCache::attend) at every position, the reference-order
@@ -59,6 +62,47 @@ def test_fused_qkv_projection(hip, port, gtype):
         say("fused qkv", S.TYPE_NAMES[gtype], name, "normwise", err)
         assert err <= 1e-4, (name, err)
         off += rows
+
+
+@pytest.mark.parametrize("gtype,hidden,rows", ((S.Q4_K, 2048, 5120), (S.Q5_K, 2048, 5120),
+                                               (S.Q6_K, 2048, 5120), (S.Q8_0, 2048, 5120),
+                                               (S.Q4_K, 4096, 2048)))
+def test_fused_norm_projection(hip, port, gtype, hidden, rows):
+    """The q/k/v projection with the residual add and attention RMSNorm in its
+    staging: the updated residual bit for bit, the projection within 1e-4
+    normwise of the oracle's tensor_linear of pko_add_rms_norm's row."""
+    g = S.rng(400 + gtype + hidden)
+    enc = S.quant_matrix(gtype, rows, hidden, g)
+    h = S.normal_f32(g, hidden) * np.float32(4)
+    d = S.normal_f32(g, hidden)
+    nw = (1 + 0.125 * np.random.default_rng(hidden).random(hidden)).astype(np.float32)
+    w = hip.upload(gtype, hidden, rows, enc)
+    try:
+        for delta in (d, None):
+            gh, gy = hip.matvec_add_rmsnorm(w, h, delta, nw, 1e-6)
+            ch, cn = port.add_rms_norm(h.reshape(1, -1), None if delta is None else delta.reshape(1, -1),
+                                       nw, 1e-6)
+            assert np.array_equal(gh.view(np.uint32), ch[0].view(np.uint32))
+            err = normwise_rel(gy, port.linear(gtype, enc, hidden, rows, cn[0]))
+            say("fused norm projection", S.TYPE_NAMES[gtype], hidden, rows, "delta",
+                delta is not None, "normwise", err)
+            assert err <= 1e-4, err
+    finally:
+        w.release()
+
+
+def test_fused_norm_projection_unsupported_width(hip):
+    """Widths the one-launch kernel does not cover are refused, not run."""
+    from pokitlms_amd.backend import Unsupported
+    g = S.rng(77)
+    hidden, rows = 8192, 64
+    w = hip.upload(S.Q4_K, hidden, rows, S.quant_matrix(S.Q4_K, rows, hidden, g))
+    try:
+        x = S.normal_f32(g, hidden)
+        with pytest.raises(Unsupported):
+            hip.matvec_add_rmsnorm(w, x, None, np.ones(hidden, np.float32), 1e-6)
+    finally:
+        w.release()
 
 
 ATTN = (  # heads, kv_heads, head_dim, capacity, steps
